@@ -1,0 +1,38 @@
+// Drop-in for the Gated DeltaNet kernels of include/gdn.hpp of the reference
+// (sahan974/qwen-3.5-cuda, :9-27 and :58-67), hipStream_t in place of
+// cudaStream_t.
+#ifndef QWEN35_GDN_HPP
+#define QWEN35_GDN_HPP
+
+#include <hip/hip_runtime_api.h>
+
+namespace qwen {
+
+// One decode step of the causal depthwise conv + SiLU; history [channels x
+// (kernel-1)] shifted in place.  ref: include/gdn.hpp:9-17
+void gdn_conv_step(const float* input, const float* weight, float* history, float* output, int channels,
+                   int kernel, hipStream_t stream);
+
+// Per-head L2 norm of q and k in place, q also scaled by 1/sqrt(dim).
+// ref: include/gdn.hpp:20-27
+void gdn_qk_normalize(float* q, float* k, int heads, int dim, float eps, hipStream_t stream);
+
+// out = norm(x) * weight * silu(z) per head.  ref: include/gdn.hpp:58-67
+void gdn_norm_gate(const float* x, const float* z, const float* weight, float* out, int heads, int dim,
+                   float eps, hipStream_t stream);
+
+// ---- row-batched and fused forms
+
+// `rows` conv steps + the q/k L2 norm of every row in one pass
+// (src/layer_gdn.cpp:89-97); hist_out may equal hist_in.
+void gdn_frontend_rows(const float* x, const float* weight, const float* hist_in, float* hist_out, float* y,
+                       int rows, int channels, int kernel, int k_heads, int key_dim, float eps,
+                       hipStream_t stream);
+
+// gdn_norm_gate over rows x heads x dim.
+void gdn_norm_gate_rows(const float* x, const float* z, const float* weight, float* out, int rows, int heads,
+                        int dim, float eps, hipStream_t stream);
+
+}  // namespace qwen
+
+#endif  // QWEN35_GDN_HPP

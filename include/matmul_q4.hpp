@@ -1,0 +1,29 @@
+// Drop-in for the dequant entry points of include/matmul_q4.hpp of the
+// reference (sahan974/qwen-3.5-cuda, :10 and :24-30), hipStream_t in place of
+// cudaStream_t. dequantize_row throws std::runtime_error with the reference's
+// messages ("cannot dequantize tensor '<name>'", "row is outside tensor '<name>'").
+#ifndef QWEN35_MATMUL_Q4_HPP
+#define QWEN35_MATMUL_Q4_HPP
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+
+#include "quantized.hpp"
+
+namespace qwen {
+
+// True for F32, F16, BF16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K.  ref: include/matmul_q4.hpp:10
+bool matmul_type_supported(GgmlType type);
+
+// out[i] = element (row * cols + i) of `tensor`.  ref: include/matmul_q4.hpp:24-30
+void dequantize_row(const QuantTensor& tensor, float* out, int row, int cols, hipStream_t stream = nullptr);
+
+// Batched embedding gather: out[t] = dequantize_row(tensor, ids[t], cols) for
+// t < n_ids; ids is a device int32 array. Ids outside the table give NaN rows.
+void dequant_gather_rows(const QuantTensor& tensor, const int32_t* ids, int n_ids, int cols, float* out,
+                         hipStream_t stream = nullptr);
+
+}  // namespace qwen
+
+#endif  // QWEN35_MATMUL_Q4_HPP

@@ -1,0 +1,185 @@
+/*
+ * qwen35_hip.h -- C ABI of the MI355X (gfx950) fused per-layer kernels.
+ *
+ * Plain pointers and sizes only. Every pointer argument that names a tensor is a
+ * device pointer owned by the caller; `stream` is a hipStream_t (NULL = the
+ * default stream). Every function validates its arguments on the host before
+ * anything is enqueued, enqueues asynchronously, never allocates, frees or
+ * synchronises, and returns a qwen_status. It never throws. On failure,
+ * qwen_last_error() returns a message for the calling thread.
+ *
+ * Citations "ref: file:line" name the reference interface (sahan974/qwen-3.5-cuda)
+ * that each entry point replaces. The C++ drop-in headers (ops.hpp, rope.hpp,
+ * gdn.hpp, matmul_q4.hpp, layer_kernels.hpp) wrap these in namespace qwen with
+ * the reference signatures and its exception behaviour.
+ *
+ * Layouts: "rows" are tokens. A [rows x n] tensor is row-major and contiguous.
+ * bf16 tensors are uint16_t holding the top half of an IEEE binary32.
+ * The vectorised paths use 16-byte loads when every pointer is 16-byte aligned
+ * and the row length is a multiple of 4 (fp32) or 8 (bf16); other shapes take a
+ * scalar path with the same results.
+ */
+#ifndef QWEN35_HIP_H
+#define QWEN35_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum qwen_status {
+    QWEN_STATUS_OK = 0,
+    QWEN_STATUS_INVALID_ARGUMENT = 1, /* bad pointer, size or parameter       */
+    QWEN_STATUS_UNSUPPORTED_TYPE = 2, /* GGML type without a dequant path     */
+    QWEN_STATUS_OUT_OF_RANGE = 3,     /* row/element range outside the tensor */
+    QWEN_STATUS_LAUNCH_FAILED = 4     /* the HIP runtime rejected the launch  */
+};
+
+/* ABI version of this header (bumped on any signature change). */
+int qwen_abi_version(void);
+/* Message describing the calling thread's most recent failure ("" if none). */
+const char* qwen_last_error(void);
+/* Constant name of a status code. */
+const char* qwen_status_name(int status);
+
+/* ===================================================================== norms
+ * out = (x * r) * w, r = rsqrtf(sum(x^2)/n + eps), per row.
+ * ref: include/ops.hpp:11-18 (rmsnorm_forward), src/cuda/ops.cu:25-65,143-154 */
+int qwen_rmsnorm_forward(const float* x, const float* weight, float* out, int n, float eps,
+                         void* stream);
+/* Row-batched form of the above: x, out [rows x n]. */
+int qwen_rmsnorm_rows(const float* x, const float* weight, float* out, int rows, int n, float eps,
+                      void* stream);
+
+/* out = ((x * r) * w) * silu(gate), full-row r.
+ * ref: include/ops.hpp:21-29 (rmsnorm_gated_forward), src/cuda/ops.cu:68-109 */
+int qwen_rmsnorm_gated_forward(const float* x, const float* gate, const float* weight, float* out,
+                               int n, float eps, void* stream);
+int qwen_rmsnorm_gated_rows(const float* x, const float* gate, const float* weight, float* out,
+                            int rows, int n, float eps, void* stream);
+
+/* out = x1 + x2.  ref: include/ops.hpp:32-38, src/cuda/ops.cu:115-125,170-181 */
+int qwen_residual_add(const float* x1, const float* x2, float* out, int size, void* stream);
+
+/* Fused residual add + RMSNorm: resid = x + branch; normed = rmsnorm(resid) * w.
+ * Replaces the pair residual_add (src/model.cpp:205) + rmsnorm_forward
+ * (src/model.cpp:208); both outputs are written. */
+int qwen_residual_rmsnorm_rows_f32(const float* x, const float* branch, const float* weight,
+                                   float* resid, float* normed, int rows, int n, float eps,
+                                   void* stream);
+/* bf16 storage, fp32 math: resid = bf16(x + branch); the norm reads the rounded
+ * resid back, so the result equals the unfused pair run on bf16 buffers. */
+int qwen_residual_rmsnorm_rows_bf16(const uint16_t* x, const uint16_t* branch, const float* weight,
+                                    uint16_t* resid, uint16_t* normed, int rows, int n, float eps,
+                                    void* stream);
+
+/* out = table[token_id * d_model : +d_model] (fp32 rows). token_id is not range
+ * checked (the reference has no vocabulary bound here either).
+ * ref: include/ops.hpp:41-47 (encoder_forward), src/cuda/ops.cu:128-138 */
+int qwen_encoder_forward(int token_id, const float* table, float* out, int d_model, void* stream);
+
+/* ================================================================ attention
+ * Per-head RMSNorm in place: x = x * (r * w), w shared by all heads [dim].
+ * ref: src/layer_attn.cpp:11 (attn_head_norm decl), src/cuda/attn_kernels.cu:34-68 */
+int qwen_attn_head_norm(float* x, const float* weight, int heads, int dim, float eps, void* stream);
+
+/* Split-half partial RoPE in place on the first rope_dim dims of every head:
+ * theta_i = pos / powf(theta, 2i/rope_dim); (a, b) -> (a c - b s, b c + a s).
+ * Rejects (INVALID_ARGUMENT) exactly what the reference throws on.
+ * ref: include/rope.hpp:13-21 (rope_forward), src/cuda/rope.cu:9-47 */
+int qwen_rope_forward(float* x, int pos, int heads, int head_dim, int rope_dim, float theta,
+                      void* stream);
+
+/* Fused Q/K per-head RMSNorm + partial RoPE over `rows` tokens, in place:
+ * q [rows x q_heads x head_dim] with q_weight [head_dim], k [rows x k_heads x
+ * head_dim] with k_weight [head_dim]. Row t uses position pos[t] (device int32
+ * array) or, when pos is NULL, pos0 + t. rope_dim 0 skips the rotation.
+ * Replaces src/layer_attn.cpp:91-96 (two attn_head_norm + two rope_forward). */
+int qwen_attn_qk_norm_rope_rows(float* q, float* k, const float* q_weight, const float* k_weight,
+                                const int32_t* pos, int pos0, int rows, int q_heads, int k_heads,
+                                int head_dim, int rope_dim, float theta, float eps, void* stream);
+
+/* ========================================================= Gated DeltaNet
+ * One decode step of the causal depthwise conv + SiLU; history [channels x
+ * (kernel-1)] is shifted in place.
+ * ref: include/gdn.hpp:9-17 (gdn_conv_step), src/cuda/gdn.cu:9-32 */
+int qwen_gdn_conv_step(const float* input, const float* weight, float* history, float* output,
+                       int channels, int kernel, void* stream);
+
+/* Per-head L2 norm in place; q is also scaled by rsqrtf(dim); eps on the sum.
+ * ref: include/gdn.hpp:20-27 (gdn_qk_normalize), src/cuda/gdn.cu:36-86 */
+int qwen_gdn_qk_normalize(float* q, float* k, int heads, int dim, float eps, void* stream);
+
+/* Fused GDN front end over `rows` tokens: y = silu(causal depthwise conv(x))
+ * with weights [channels x kernel] and history hist_in [channels x (kernel-1)];
+ * then the L2 norm of gdn_qk_normalize on q = channels [0, k_heads*key_dim) and
+ * k = [k_heads*key_dim, 2*k_heads*key_dim) of every row. hist_out receives the
+ * history after the last row (hist_out may equal hist_in). k_heads 0 skips the
+ * norm. Equals `rows` sequential gdn_conv_step calls followed by
+ * gdn_qk_normalize on each row (src/layer_gdn.cpp:89-97). */
+int qwen_gdn_frontend_rows(const float* x, const float* weight, const float* hist_in,
+                           float* hist_out, float* y, int rows, int channels, int kernel,
+                           int k_heads, int key_dim, float eps, void* stream);
+
+/* Gated per-head RMSNorm: out = ((x * r) * w) * silu(z), r per head of `dim`.
+ * ref: include/gdn.hpp:58-67 (gdn_norm_gate), src/cuda/gdn.cu:176-215 */
+int qwen_gdn_norm_gate(const float* x, const float* z, const float* weight, float* out, int heads,
+                       int dim, float eps, void* stream);
+/* Row-batched form: x, z, out [rows x heads x dim]. */
+int qwen_gdn_norm_gate_rows(const float* x, const float* z, const float* weight, float* out,
+                            int rows, int heads, int dim, float eps, void* stream);
+
+/* ====================================================================== MoE
+ * h = silu(g) * u (fp32).  ref: src/layer_moe.cpp:10 (moe_silu_mul decl),
+ * src/cuda/moe.cu:61-72 */
+int qwen_moe_silu_mul(const float* gate, const float* up, float* hidden, int n, void* stream);
+
+/* accum += x * sigmoid(gate[0]); gate is a device scalar.
+ * ref: src/layer_moe.cpp:12 (moe_shared_add decl), src/cuda/moe.cu:90-101 */
+int qwen_moe_shared_add(float* accum, const float* shared_out, const float* gate, int n,
+                        void* stream);
+/* Row-batched: accum, shared_out [rows x n], gate [rows] (one logit per token). */
+int qwen_moe_shared_add_rows(float* accum, const float* shared_out, const float* gate, int rows,
+                             int n, void* stream);
+
+/* SwiGLU on bf16 storage with fp32 math: h = bf16(silu(g) * u), n elements
+ * (e.g. [tokens x experts x moe_dim] flattened). Batched moe_silu_mul
+ * (src/layer_moe.cpp:135). */
+int qwen_swiglu_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* hidden, int64_t n,
+                     void* stream);
+/* Shared expert SwiGLU with its sigmoid gate folded in:
+ * h[t] = bf16((silu(g[t]) * u[t]) * sigmoid(logits[t])), rows x dim.
+ * Equals moe_silu_mul (layer_moe.cpp:149) followed by moe_shared_add's scale
+ * (layer_moe.cpp:153) moved before the (linear) down projection. */
+int qwen_shared_swiglu_sigmoid_rows_bf16(const uint16_t* gate, const uint16_t* up,
+                                         const float* logits, uint16_t* hidden, int rows, int dim,
+                                         void* stream);
+
+/* ================================================================== dequant
+ * GGML type ids as in include/quantized.hpp:12-35 (F32 0, F16 1, Q4_0 2,
+ * Q5_0 6, Q8_0 8, Q4_K 12, Q5_K 13, Q6_K 14, BF16 30).
+ * Returns 1 if `type` has a dequant path.
+ * ref: include/matmul_q4.hpp:10 (matmul_type_supported), src/cuda/matmul_q4.cu:179-183 */
+int qwen_type_supported(int type);
+
+/* out[i] = element (row*cols + i) of the tensor, i < cols.
+ * Errors: data NULL or type unsupported -> UNSUPPORTED_TYPE (reference message
+ * "cannot dequantize tensor"); row < 0, cols <= 0 or the span past
+ * num_elements -> OUT_OF_RANGE ("row is outside tensor").
+ * ref: include/matmul_q4.hpp:24-30 (dequantize_row), src/cuda/matmul_q4.cu:209-227 */
+int qwen_dequantize_row(const void* data, int type, uint64_t num_elements, float* out, int row,
+                        int cols, void* stream);
+
+/* Embedding gather: out[t] = dequantize_row(table, ids[t], cols) for t < n_ids,
+ * ids a device int32 array. A table of num_elements holds num_elements/cols
+ * rows; an id outside [0, rows) yields a row of quiet NaNs instead of a read
+ * outside the table. Batched form of src/model.cpp:190. */
+int qwen_dequant_gather_rows(const void* table, int type, uint64_t num_elements,
+                             const int32_t* ids, int n_ids, int cols, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN35_HIP_H */

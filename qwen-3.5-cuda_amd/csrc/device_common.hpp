@@ -1,0 +1,80 @@
+// Device-side building blocks shared by every kernel: wave64 reductions over
+// DPP, bf16 packing, and the SiLU / sigmoid forms the reference uses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qk {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- reductions
+// DPP row-local move (gfx9 encodings): quad_perm, row_half_mirror, row_mirror.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float read_lane(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Sum over aligned groups of G lanes (G a power of two, 1..64). Every lane of a
+// group ends with the same bits: each step adds a lane and its partner, and both
+// partners evaluate the same commutative sum.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "group");
+    if constexpr (G >= 2) v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+    if constexpr (G >= 4) v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+    if constexpr (G >= 8) v += dpp_move<0x141>(v);  // row_half_mirror: 8-lane halves
+    if constexpr (G >= 16) v += dpp_move<0x140>(v); // row_mirror: 16-lane rows
+    if constexpr (G == 32) {
+        // ds_swizzle bit mode, and_mask 0x1f, xor_mask 0x10: lane ^ 16 within 32.
+        v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+    }
+    if constexpr (G == 64) {
+        // Four 16-lane row sums, combined in scalar registers: wave-uniform.
+        v = (read_lane(v, 0) + read_lane(v, 16)) + (read_lane(v, 32) + read_lane(v, 48));
+    }
+    return v;
+}
+
+// Value of `v` held by lane `src` (any lane of the wave).
+__device__ __forceinline__ float lane_fetch(float v, int src) {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(v)));
+}
+
+// ---------------------------------------------------------------- activations
+// The reference's SiLU, x / (1 + expf(-x)) (src/cuda/ops.cu:9-11), with IEEE
+// division and the accurate expf.
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// 1 / (1 + expf(-x)) (src/cuda/moe.cu:94).
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// ---------------------------------------------------------------- bf16
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 pair (lo in bits 0..15), round to nearest even
+// (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    float2_t f = {lo, hi};
+    bf16x2_t b = __builtin_convertvector(f, bf16x2_t);
+    return __builtin_bit_cast(uint32_t, b);
+}
+
+// ---------------------------------------------------------------- memory
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+
+__device__ __forceinline__ float sumsq4(float4 v) { return (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w); }
+
+}  // namespace qk

@@ -1,0 +1,192 @@
+// MoE expert activations on gfx950: SwiGLU h = silu(g) * u (fp32 and bf16
+// storage), the sigmoid-gated shared expert, and the shared-expert accumulate.
+//
+// Reference semantics: silu_mul_kernel (src/cuda/moe.cu:61-67) and shared_kernel
+// (src/cuda/moe.cu:90-96, out += x * sigmoid(gate[0])). The reference runs one
+// launch per expert per token with 4-byte accesses; here a launch covers every
+// token and expert, each thread moves 16-byte vectors and keeps U vectors in
+// flight, and the bf16 forms do the math in fp32 with one round-to-nearest-even
+// at the store.
+#include <algorithm>
+
+#include "capi_common.hpp"
+#include "device_common.hpp"
+
+namespace qk {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;  // 16-byte vectors in flight per thread
+
+// ------------------------------------------------------------ bf16 SwiGLU
+// Chunk i = 8 bf16 (16 bytes). Block b, step u covers chunks
+// (b*kUnroll + u)*kBlock + [0, kBlock): every load instruction is coalesced.
+__device__ __forceinline__ uint32_t swiglu_pair(uint32_t g, uint32_t u, float scale, bool scaled) {
+    float lo = silu(bf16_lo(g)) * bf16_lo(u);
+    float hi = silu(bf16_hi(g)) * bf16_hi(u);
+    if (scaled) {
+        lo *= scale;
+        hi *= scale;
+    }
+    return pack_bf16(lo, hi);
+}
+
+__global__ __launch_bounds__(kBlock) void swiglu_bf16_v8(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+                                                         uint16_t* __restrict__ h, int64_t n8) {
+    uint4 gv[kUnroll], uv[kUnroll];
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * kUnroll * kBlock + threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+        const int64_t i = first + k * kBlock;
+        if (i < n8) {
+            gv[k] = ld16(g + 8 * i);
+            uv[k] = ld16(u + 8 * i);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+        const int64_t i = first + k * kBlock;
+        if (i < n8) {
+            st16(h + 8 * i, make_uint4(swiglu_pair(gv[k].x, uv[k].x, 1.f, false), swiglu_pair(gv[k].y, uv[k].y, 1.f, false),
+                                       swiglu_pair(gv[k].z, uv[k].z, 1.f, false), swiglu_pair(gv[k].w, uv[k].w, 1.f, false)));
+        }
+    }
+}
+
+// Shared expert: rows x dim with one logit per row (dim % 8 == 0, so a chunk
+// never straddles two rows).
+__global__ __launch_bounds__(kBlock) void shared_swiglu_bf16_v8(const uint16_t* __restrict__ g,
+                                                                const uint16_t* __restrict__ u,
+                                                                const float* __restrict__ logits,
+                                                                uint16_t* __restrict__ h, int64_t n8, int dim8) {
+    uint4 gv[kUnroll], uv[kUnroll];
+    float lg[kUnroll];
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * kUnroll * kBlock + threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+        const int64_t i = first + k * kBlock;
+        if (i < n8) {
+            gv[k] = ld16(g + 8 * i);
+            uv[k] = ld16(u + 8 * i);
+            lg[k] = logits[i / dim8];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+        const int64_t i = first + k * kBlock;
+        if (i < n8) {
+            const float sc = sigmoid(lg[k]);
+            st16(h + 8 * i, make_uint4(swiglu_pair(gv[k].x, uv[k].x, sc, true), swiglu_pair(gv[k].y, uv[k].y, sc, true),
+                                       swiglu_pair(gv[k].z, uv[k].z, sc, true), swiglu_pair(gv[k].w, uv[k].w, sc, true)));
+        }
+    }
+}
+
+__device__ __forceinline__ float bf16_at(const uint16_t* p) { return __uint_as_float(static_cast<uint32_t>(*p) << 16); }
+
+__global__ __launch_bounds__(kBlock) void swiglu_bf16_any(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+                                                          const float* __restrict__ logits, uint16_t* __restrict__ h,
+                                                          int64_t n, int dim) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kBlock) {
+        float v = silu(bf16_at(g + i)) * bf16_at(u + i);
+        if (logits) v *= sigmoid(logits[i / dim]);
+        h[i] = static_cast<uint16_t>(pack_bf16(v, 0.f) & 0xffffu);
+    }
+}
+
+// ------------------------------------------------------------ fp32 forms
+__global__ __launch_bounds__(kBlock) void silu_mul_v4(const float* __restrict__ g, const float* __restrict__ u,
+                                                      float* __restrict__ h, int64_t n4) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n4;
+         i += static_cast<int64_t>(gridDim.x) * kBlock) {
+        const float4 a = ld4(g + 4 * i);
+        const float4 b = ld4(u + 4 * i);
+        st4(h + 4 * i, make_float4(silu(a.x) * b.x, silu(a.y) * b.y, silu(a.z) * b.z, silu(a.w) * b.w));
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void silu_mul_any(const float* __restrict__ g, const float* __restrict__ u,
+                                                       float* __restrict__ h, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kBlock)
+        h[i] = silu(g[i]) * u[i];
+}
+
+// accum[t, i] += x[t, i] * sigmoid(gate[t]); one block row-strip per row.
+__global__ __launch_bounds__(kBlock) void shared_add_rows(float* __restrict__ accum, const float* __restrict__ x,
+                                                          const float* __restrict__ gate, int dim) {
+    const float sc = sigmoid(gate[blockIdx.y]);
+    const size_t base = static_cast<size_t>(blockIdx.y) * dim;
+    for (int i = blockIdx.x * kBlock + threadIdx.x; i < dim; i += gridDim.x * kBlock)
+        accum[base + i] += x[base + i] * sc;
+}
+
+unsigned stride_grid(int64_t items) { return static_cast<unsigned>(std::min<int64_t>(blocks_for(items, kBlock), 8192)); }
+
+int swiglu_common(const uint16_t* g, const uint16_t* u, const float* logits, uint16_t* h, int64_t n, int dim,
+                  hipStream_t s, const char* what) {
+    const bool vec = n % 8 == 0 && (!logits || dim % 8 == 0) && aligned16(g) && aligned16(u) && aligned16(h);
+    if (vec) {
+        const int64_t n8 = n / 8;
+        const unsigned grid = blocks_for(n8, static_cast<int64_t>(kUnroll) * kBlock);
+        if (logits)
+            shared_swiglu_bf16_v8<<<grid, kBlock, 0, s>>>(g, u, logits, h, n8, dim / 8);
+        else
+            swiglu_bf16_v8<<<grid, kBlock, 0, s>>>(g, u, h, n8);
+    } else {
+        swiglu_bf16_any<<<stride_grid(n), kBlock, 0, s>>>(g, u, logits, h, n, dim);
+    }
+    return check_launch(what);
+}
+
+}  // namespace
+}  // namespace qk
+
+using namespace qk;
+
+extern "C" {
+
+int qwen_swiglu_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* hidden, int64_t n, void* stream) {
+    QK_REQUIRE(n >= 0, "swiglu_bf16: negative size");
+    if (n == 0) return ok();
+    QK_REQUIRE(gate && up && hidden, "swiglu_bf16: null pointer");
+    return swiglu_common(gate, up, nullptr, hidden, n, 1, as_stream(stream), "swiglu_bf16");
+}
+
+int qwen_shared_swiglu_sigmoid_rows_bf16(const uint16_t* gate, const uint16_t* up, const float* logits,
+                                         uint16_t* hidden, int rows, int dim, void* stream) {
+    QK_REQUIRE(rows >= 0 && dim >= 0, "shared_swiglu_sigmoid: negative size");
+    if (rows == 0 || dim == 0) return ok();
+    QK_REQUIRE(gate && up && logits && hidden, "shared_swiglu_sigmoid: null pointer");
+    return swiglu_common(gate, up, logits, hidden, static_cast<int64_t>(rows) * dim, dim, as_stream(stream),
+                         "shared_swiglu_sigmoid");
+}
+
+int qwen_moe_silu_mul(const float* gate, const float* up, float* hidden, int n, void* stream) {
+    QK_REQUIRE(n >= 0, "moe_silu_mul: negative size");
+    if (n == 0) return ok();
+    QK_REQUIRE(gate && up && hidden, "moe_silu_mul: null pointer");
+    hipStream_t s = as_stream(stream);
+    if (n % 4 == 0 && aligned16(gate) && aligned16(up) && aligned16(hidden))
+        silu_mul_v4<<<stride_grid(n / 4), kBlock, 0, s>>>(gate, up, hidden, n / 4);
+    else
+        silu_mul_any<<<stride_grid(n), kBlock, 0, s>>>(gate, up, hidden, n);
+    return check_launch("moe_silu_mul");
+}
+
+int qwen_moe_shared_add_rows(float* accum, const float* shared_out, const float* gate, int rows, int n, void* stream) {
+    QK_REQUIRE(rows >= 0 && n >= 0, "moe_shared_add: negative size");
+    if (rows == 0 || n == 0) return ok();
+    QK_REQUIRE(accum && shared_out && gate, "moe_shared_add: null pointer");
+    QK_REQUIRE(rows <= 65535, "moe_shared_add: %d rows exceed one launch (65535)", rows);
+    const dim3 grid(std::min<unsigned>(blocks_for(n, kBlock), 64u), static_cast<unsigned>(rows));
+    shared_add_rows<<<grid, kBlock, 0, as_stream(stream)>>>(accum, shared_out, gate, n);
+    return check_launch("moe_shared_add");
+}
+
+int qwen_moe_shared_add(float* accum, const float* shared_out, const float* gate, int n, void* stream) {
+    return qwen_moe_shared_add_rows(accum, shared_out, gate, 1, n, stream);
+}
+
+}  // extern "C"

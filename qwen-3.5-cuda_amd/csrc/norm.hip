@@ -1,0 +1,397 @@
+// RMSNorm family on gfx950: plain / gated RMSNorm rows, fused residual add +
+// RMSNorm (fp32 and bf16 storage), residual add and the fp32 embedding copy.
+//
+// Reference semantics: src/cuda/ops.cu:25-138 (rmsnorm_kernel,
+// rmsnorm_gated_kernel, residual_add_kernel, encoder_kernel). The reference
+// launches one 256-thread block per call and re-reads x for the second pass;
+// here one wave64 owns a row, holds the row in VGPRs between the reduction and
+// the scale (x is read from HBM once), reduces with DPP row ops plus four
+// readlanes, and moves data in 16-byte vectors.
+#include <algorithm>
+
+#include "capi_common.hpp"
+#include "device_common.hpp"
+
+namespace qk {
+namespace {
+
+constexpr int kBlock = 256;
+
+// Waves per block: spread small row counts one wave per workgroup so they land
+// on different CUs; pack four rows per workgroup otherwise.
+inline int waves_per_block(int rows) { return rows >= 1024 ? 4 : 1; }
+
+// ------------------------------------------------------------- fp32 rows
+// One wave per row; lane l holds float4 chunks l, l+64, ... (up to MAXC).
+template <int MAXC, bool GATED>
+__global__ __launch_bounds__(kBlock) void rmsnorm_rows_v4(const float* __restrict__ x, const float* __restrict__ gate,
+                                                          const float* __restrict__ w, float* __restrict__ out, int rows,
+                                                          int n, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int n4 = n >> 2;
+    const size_t base = static_cast<size_t>(row) * n;
+    float4 v[MAXC];
+    float4 g[GATED ? MAXC : 1];
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        const int i = c * kWave + lane;
+        v[c] = (i < n4) ? ld4(x + base + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (GATED) g[c] = (i < n4) ? ld4(gate + base + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) ss += sumsq4(v[c]);
+    ss = group_sum<kWave>(ss);
+    const float r = rsqrtf(ss / static_cast<float>(n) + eps);
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        const int i = c * kWave + lane;
+        if (i < n4) {
+            const float4 wv = ld4(w + 4 * i);
+            float4 o;
+            o.x = v[c].x * r * wv.x;
+            o.y = v[c].y * r * wv.y;
+            o.z = v[c].z * r * wv.z;
+            o.w = v[c].w * r * wv.w;
+            if constexpr (GATED) {
+                o.x *= silu(g[c].x);
+                o.y *= silu(g[c].y);
+                o.z *= silu(g[c].z);
+                o.w *= silu(g[c].w);
+            }
+            st4(out + base + 4 * i, o);
+        }
+    }
+}
+
+// Cross-wave sum for a block of kBlock threads: wave sums meet in LDS.
+__device__ __forceinline__ float block_sum(float v, float* lds) {
+    v = group_sum<kWave>(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < kBlock / kWave; ++i) t += lds[i];
+    return t;
+}
+
+// Any n, any alignment: one block per row, two passes (the second pass re-reads
+// x, which the first pass left in cache).
+template <bool GATED>
+__global__ __launch_bounds__(kBlock) void rmsnorm_rows_any(const float* __restrict__ x, const float* __restrict__ gate,
+                                                           const float* __restrict__ w, float* __restrict__ out, int n,
+                                                           float eps) {
+    __shared__ float lds[kBlock / kWave];
+    const size_t base = static_cast<size_t>(blockIdx.x) * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += kBlock) ss += x[base + i] * x[base + i];
+    ss = block_sum(ss, lds);
+    const float r = rsqrtf(ss / static_cast<float>(n) + eps);
+    for (int i = threadIdx.x; i < n; i += kBlock) {
+        float o = x[base + i] * r * w[i];
+        if constexpr (GATED) o *= silu(gate[base + i]);
+        out[base + i] = o;
+    }
+}
+
+// ------------------------------------------------- fused residual + RMSNorm, fp32
+template <int MAXC>
+__global__ __launch_bounds__(kBlock) void residual_rmsnorm_f32_v4(const float* __restrict__ x,
+                                                                  const float* __restrict__ b,
+                                                                  const float* __restrict__ w,
+                                                                  float* __restrict__ resid,
+                                                                  float* __restrict__ normed, int rows, int n,
+                                                                  float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int n4 = n >> 2;
+    const size_t base = static_cast<size_t>(row) * n;
+    float4 v[MAXC];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        const int i = c * kWave + lane;
+        if (i < n4) {
+            const float4 a = ld4(x + base + 4 * i);
+            const float4 d = ld4(b + base + 4 * i);
+            v[c] = make_float4(a.x + d.x, a.y + d.y, a.z + d.z, a.w + d.w);
+            st4(resid + base + 4 * i, v[c]);
+        } else {
+            v[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        ss += sumsq4(v[c]);
+    }
+    ss = group_sum<kWave>(ss);
+    const float r = rsqrtf(ss / static_cast<float>(n) + eps);
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        const int i = c * kWave + lane;
+        if (i < n4) {
+            const float4 wv = ld4(w + 4 * i);
+            st4(normed + base + 4 * i,
+                make_float4(v[c].x * r * wv.x, v[c].y * r * wv.y, v[c].z * r * wv.z, v[c].w * r * wv.w));
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void residual_rmsnorm_f32_any(const float* __restrict__ x,
+                                                                   const float* __restrict__ b,
+                                                                   const float* __restrict__ w,
+                                                                   float* __restrict__ resid,
+                                                                   float* __restrict__ normed, int n, float eps) {
+    __shared__ float lds[kBlock / kWave];
+    const size_t base = static_cast<size_t>(blockIdx.x) * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += kBlock) {
+        const float s = x[base + i] + b[base + i];
+        resid[base + i] = s;
+        ss += s * s;
+    }
+    ss = block_sum(ss, lds);
+    const float r = rsqrtf(ss / static_cast<float>(n) + eps);
+    // Each thread re-reads only the elements it wrote itself.
+    for (int i = threadIdx.x; i < n; i += kBlock) normed[base + i] = resid[base + i] * r * w[i];
+}
+
+// ------------------------------------------------- fused residual + RMSNorm, bf16
+// 8 bf16 per 16-byte chunk; lane l holds chunks l, l+64, ... The rounded sum is
+// what the norm reads, so the result equals the unfused pair on bf16 buffers.
+template <int MAXC>
+__global__ __launch_bounds__(kBlock) void residual_rmsnorm_bf16_v8(const uint16_t* __restrict__ x,
+                                                                   const uint16_t* __restrict__ b,
+                                                                   const float* __restrict__ w,
+                                                                   uint16_t* __restrict__ resid,
+                                                                   uint16_t* __restrict__ normed, int rows, int n,
+                                                                   float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int n8 = n >> 3;
+    const size_t base = static_cast<size_t>(row) * n;
+    uint4 xa[MAXC], ba[MAXC];
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        const int i = c * kWave + lane;
+        if (i < n8) {
+            xa[c] = ld16(x + base + 8 * i);
+            ba[c] = ld16(b + base + 8 * i);
+        } else {
+            xa[c] = make_uint4(0, 0, 0, 0);
+            ba[c] = make_uint4(0, 0, 0, 0);
+        }
+    }
+    uint4 s[MAXC];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        const uint32_t xs[4] = {xa[c].x, xa[c].y, xa[c].z, xa[c].w};
+        const uint32_t bs[4] = {ba[c].x, ba[c].y, ba[c].z, ba[c].w};
+        uint32_t ps[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            ps[k] = pack_bf16(bf16_lo(xs[k]) + bf16_lo(bs[k]), bf16_hi(xs[k]) + bf16_hi(bs[k]));
+            const float lo = bf16_lo(ps[k]);
+            const float hi = bf16_hi(ps[k]);
+            ss += lo * lo + hi * hi;
+        }
+        s[c] = make_uint4(ps[0], ps[1], ps[2], ps[3]);
+        const int i = c * kWave + lane;
+        if (i < n8) st16(resid + base + 8 * i, s[c]);
+    }
+    ss = group_sum<kWave>(ss);
+    const float r = rsqrtf(ss / static_cast<float>(n) + eps);
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        const int i = c * kWave + lane;
+        if (i < n8) {
+            const float4 w0 = ld4(w + 8 * i);
+            const float4 w1 = ld4(w + 8 * i + 4);
+            const uint4 o = make_uint4(pack_bf16(bf16_lo(s[c].x) * r * w0.x, bf16_hi(s[c].x) * r * w0.y),
+                                       pack_bf16(bf16_lo(s[c].y) * r * w0.z, bf16_hi(s[c].y) * r * w0.w),
+                                       pack_bf16(bf16_lo(s[c].z) * r * w1.x, bf16_hi(s[c].z) * r * w1.y),
+                                       pack_bf16(bf16_lo(s[c].w) * r * w1.z, bf16_hi(s[c].w) * r * w1.w));
+            st16(normed + base + 8 * i, o);
+        }
+    }
+}
+
+__device__ __forceinline__ uint16_t to_bf16(float f) { return static_cast<uint16_t>(pack_bf16(f, 0.f) & 0xffffu); }
+__device__ __forceinline__ float from_bf16(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
+
+__global__ __launch_bounds__(kBlock) void residual_rmsnorm_bf16_any(const uint16_t* __restrict__ x,
+                                                                    const uint16_t* __restrict__ b,
+                                                                    const float* __restrict__ w,
+                                                                    uint16_t* __restrict__ resid,
+                                                                    uint16_t* __restrict__ normed, int n, float eps) {
+    __shared__ float lds[kBlock / kWave];
+    const size_t base = static_cast<size_t>(blockIdx.x) * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += kBlock) {
+        const uint16_t s = to_bf16(from_bf16(x[base + i]) + from_bf16(b[base + i]));
+        resid[base + i] = s;
+        const float f = from_bf16(s);
+        ss += f * f;
+    }
+    ss = block_sum(ss, lds);
+    const float r = rsqrtf(ss / static_cast<float>(n) + eps);
+    for (int i = threadIdx.x; i < n; i += kBlock) normed[base + i] = to_bf16(from_bf16(resid[base + i]) * r * w[i]);
+}
+
+// ------------------------------------------------------------- elementwise
+__global__ __launch_bounds__(kBlock) void add_v4(const float* __restrict__ a, const float* __restrict__ b,
+                                                 float* __restrict__ out, int n4) {
+    for (int i = blockIdx.x * kBlock + threadIdx.x; i < n4; i += gridDim.x * kBlock) {
+        const float4 p = ld4(a + 4 * static_cast<size_t>(i));
+        const float4 q = ld4(b + 4 * static_cast<size_t>(i));
+        st4(out + 4 * static_cast<size_t>(i), make_float4(p.x + q.x, p.y + q.y, p.z + q.z, p.w + q.w));
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void add_any(const float* __restrict__ a, const float* __restrict__ b,
+                                                  float* __restrict__ out, int n) {
+    for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) out[i] = a[i] + b[i];
+}
+
+__global__ __launch_bounds__(kBlock) void copy_row(const float* __restrict__ src, float* __restrict__ dst, int n) {
+    for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) dst[i] = src[i];
+}
+
+// ------------------------------------------------------------- launchers
+template <bool GATED>
+int launch_rmsnorm(const float* x, const float* gate, const float* w, float* out, int rows, int n, float eps,
+                   hipStream_t s) {
+    const int n4 = n / 4;
+    const bool vec = (n % 4 == 0) && aligned16(x) && aligned16(w) && aligned16(out) && (!GATED || aligned16(gate));
+    if (vec && n4 <= 16 * kWave) {
+        const int wpb = waves_per_block(rows);
+        const dim3 grid(blocks_for(rows, wpb)), block(wpb * kWave);
+        if (n4 <= kWave)
+            rmsnorm_rows_v4<1, GATED><<<grid, block, 0, s>>>(x, gate, w, out, rows, n, eps);
+        else if (n4 <= 2 * kWave)
+            rmsnorm_rows_v4<2, GATED><<<grid, block, 0, s>>>(x, gate, w, out, rows, n, eps);
+        else if (n4 <= 4 * kWave)
+            rmsnorm_rows_v4<4, GATED><<<grid, block, 0, s>>>(x, gate, w, out, rows, n, eps);
+        else if (n4 <= 8 * kWave)
+            rmsnorm_rows_v4<8, GATED><<<grid, block, 0, s>>>(x, gate, w, out, rows, n, eps);
+        else
+            rmsnorm_rows_v4<16, GATED><<<grid, block, 0, s>>>(x, gate, w, out, rows, n, eps);
+    } else {
+        rmsnorm_rows_any<GATED><<<rows, kBlock, 0, s>>>(x, gate, w, out, n, eps);
+    }
+    return check_launch(GATED ? "rmsnorm_gated" : "rmsnorm");
+}
+
+}  // namespace
+}  // namespace qk
+
+using namespace qk;
+
+extern "C" {
+
+int qwen_rmsnorm_rows(const float* x, const float* weight, float* out, int rows, int n, float eps, void* stream) {
+    QK_REQUIRE(rows >= 0 && n >= 0, "rmsnorm: negative size (rows=%d, n=%d)", rows, n);
+    if (rows == 0 || n == 0) return ok();
+    QK_REQUIRE(x && weight && out, "rmsnorm: null pointer");
+    return launch_rmsnorm<false>(x, nullptr, weight, out, rows, n, eps, as_stream(stream));
+}
+
+int qwen_rmsnorm_forward(const float* x, const float* weight, float* out, int n, float eps, void* stream) {
+    return qwen_rmsnorm_rows(x, weight, out, 1, n, eps, stream);
+}
+
+int qwen_rmsnorm_gated_rows(const float* x, const float* gate, const float* weight, float* out, int rows, int n,
+                            float eps, void* stream) {
+    QK_REQUIRE(rows >= 0 && n >= 0, "rmsnorm_gated: negative size (rows=%d, n=%d)", rows, n);
+    if (rows == 0 || n == 0) return ok();
+    QK_REQUIRE(x && gate && weight && out, "rmsnorm_gated: null pointer");
+    return launch_rmsnorm<true>(x, gate, weight, out, rows, n, eps, as_stream(stream));
+}
+
+int qwen_rmsnorm_gated_forward(const float* x, const float* gate, const float* weight, float* out, int n, float eps,
+                               void* stream) {
+    return qwen_rmsnorm_gated_rows(x, gate, weight, out, 1, n, eps, stream);
+}
+
+int qwen_residual_add(const float* x1, const float* x2, float* out, int size, void* stream) {
+    QK_REQUIRE(size >= 0, "residual_add: negative size %d", size);
+    if (size == 0) return ok();
+    QK_REQUIRE(x1 && x2 && out, "residual_add: null pointer");
+    hipStream_t s = as_stream(stream);
+    if (size % 4 == 0 && aligned16(x1) && aligned16(x2) && aligned16(out)) {
+        const int n4 = size / 4;
+        add_v4<<<std::min<unsigned>(blocks_for(n4, kBlock), 4096u), kBlock, 0, s>>>(x1, x2, out, n4);
+    } else {
+        add_any<<<std::min<unsigned>(blocks_for(size, kBlock), 4096u), kBlock, 0, s>>>(x1, x2, out, size);
+    }
+    return check_launch("residual_add");
+}
+
+int qwen_residual_rmsnorm_rows_f32(const float* x, const float* branch, const float* weight, float* resid,
+                                   float* normed, int rows, int n, float eps, void* stream) {
+    QK_REQUIRE(rows >= 0 && n >= 0, "residual_rmsnorm_f32: negative size (rows=%d, n=%d)", rows, n);
+    if (rows == 0 || n == 0) return ok();
+    QK_REQUIRE(x && branch && weight && resid && normed, "residual_rmsnorm_f32: null pointer");
+    hipStream_t s = as_stream(stream);
+    const int n4 = n / 4;
+    const bool vec = n % 4 == 0 && aligned16(x) && aligned16(branch) && aligned16(weight) && aligned16(resid) &&
+                     aligned16(normed);
+    if (vec && n4 <= 16 * kWave) {
+        const int wpb = waves_per_block(rows);
+        const dim3 grid(blocks_for(rows, wpb)), block(wpb * kWave);
+        if (n4 <= kWave)
+            residual_rmsnorm_f32_v4<1><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+        else if (n4 <= 2 * kWave)
+            residual_rmsnorm_f32_v4<2><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+        else if (n4 <= 4 * kWave)
+            residual_rmsnorm_f32_v4<4><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+        else if (n4 <= 8 * kWave)
+            residual_rmsnorm_f32_v4<8><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+        else
+            residual_rmsnorm_f32_v4<16><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+    } else {
+        residual_rmsnorm_f32_any<<<rows, kBlock, 0, s>>>(x, branch, weight, resid, normed, n, eps);
+    }
+    return check_launch("residual_rmsnorm_f32");
+}
+
+int qwen_residual_rmsnorm_rows_bf16(const uint16_t* x, const uint16_t* branch, const float* weight, uint16_t* resid,
+                                    uint16_t* normed, int rows, int n, float eps, void* stream) {
+    QK_REQUIRE(rows >= 0 && n >= 0, "residual_rmsnorm_bf16: negative size (rows=%d, n=%d)", rows, n);
+    if (rows == 0 || n == 0) return ok();
+    QK_REQUIRE(x && branch && weight && resid && normed, "residual_rmsnorm_bf16: null pointer");
+    hipStream_t s = as_stream(stream);
+    const int n8 = n / 8;
+    const bool vec = n % 8 == 0 && aligned16(x) && aligned16(branch) && aligned16(weight) && aligned16(resid) &&
+                     aligned16(normed);
+    if (vec && n8 <= 8 * kWave) {
+        const int wpb = waves_per_block(rows);
+        const dim3 grid(blocks_for(rows, wpb)), block(wpb * kWave);
+        if (n8 <= kWave)
+            residual_rmsnorm_bf16_v8<1><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+        else if (n8 <= 2 * kWave)
+            residual_rmsnorm_bf16_v8<2><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+        else if (n8 <= 4 * kWave)
+            residual_rmsnorm_bf16_v8<4><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+        else
+            residual_rmsnorm_bf16_v8<8><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+    } else {
+        residual_rmsnorm_bf16_any<<<rows, kBlock, 0, s>>>(x, branch, weight, resid, normed, n, eps);
+    }
+    return check_launch("residual_rmsnorm_bf16");
+}
+
+int qwen_encoder_forward(int token_id, const float* table, float* out, int d_model, void* stream) {
+    QK_REQUIRE(d_model >= 0 && token_id >= 0, "encoder_forward: bad token %d or d_model %d", token_id, d_model);
+    if (d_model == 0) return ok();
+    QK_REQUIRE(table && out, "encoder_forward: null pointer");
+    hipStream_t s = as_stream(stream);
+    copy_row<<<blocks_for(d_model, kBlock), kBlock, 0, s>>>(table + static_cast<size_t>(token_id) * d_model, out,
+                                                            d_model);
+    return check_launch("encoder_forward");
+}
+
+}  // extern "C"

@@ -1,0 +1,147 @@
+// C++ drop-in layer (namespace qwen) over the C ABI: the reference's function
+// names and signatures (with hipStream_t), throwing std::runtime_error where the
+// reference throws. Each function forwards to its qwen_* C entry point.
+#include <stdexcept>
+#include <string>
+
+#include "gdn.hpp"
+#include "layer_kernels.hpp"
+#include "matmul_q4.hpp"
+#include "ops.hpp"
+#include "qwen35_hip.h"
+#include "rope.hpp"
+
+namespace qwen {
+namespace {
+
+void* st(hipStream_t s) { return reinterpret_cast<void*>(s); }
+
+// Throws the C ABI's message for a failed call.
+void check(int status) {
+    if (status != QWEN_STATUS_OK) throw std::runtime_error(qwen_last_error());
+}
+
+}  // namespace
+
+// ---- ops.hpp
+void rmsnorm_forward(const float* x, const float* weight, float* out, int N, float eps, hipStream_t stream) {
+    check(qwen_rmsnorm_forward(x, weight, out, N, eps, st(stream)));
+}
+
+void rmsnorm_gated_forward(const float* x, const float* gate, const float* weight, float* out, int N, float eps,
+                           hipStream_t stream) {
+    check(qwen_rmsnorm_gated_forward(x, gate, weight, out, N, eps, st(stream)));
+}
+
+void residual_add(const float* x1, const float* x2, float* out, int size, hipStream_t stream) {
+    check(qwen_residual_add(x1, x2, out, size, st(stream)));
+}
+
+void encoder_forward(int token_id, const float* embed_table, float* out, int d_model, hipStream_t stream) {
+    check(qwen_encoder_forward(token_id, embed_table, out, d_model, st(stream)));
+}
+
+void rmsnorm_rows(const float* x, const float* weight, float* out, int rows, int N, float eps, hipStream_t stream) {
+    check(qwen_rmsnorm_rows(x, weight, out, rows, N, eps, st(stream)));
+}
+
+void residual_rmsnorm_rows(const float* x, const float* branch, const float* weight, float* resid, float* normed,
+                           int rows, int N, float eps, hipStream_t stream) {
+    check(qwen_residual_rmsnorm_rows_f32(x, branch, weight, resid, normed, rows, N, eps, st(stream)));
+}
+
+void residual_rmsnorm_rows_bf16(const uint16_t* x, const uint16_t* branch, const float* weight, uint16_t* resid,
+                                uint16_t* normed, int rows, int N, float eps, hipStream_t stream) {
+    check(qwen_residual_rmsnorm_rows_bf16(x, branch, weight, resid, normed, rows, N, eps, st(stream)));
+}
+
+// ---- rope.hpp
+void rope_forward(float* q_or_k, int pos, int num_heads, int head_dim, int partial_rope_dim, float rope_theta,
+                  hipStream_t stream) {
+    // The C ABI reports the reference's own message, "invalid RoPE arguments".
+    check(qwen_rope_forward(q_or_k, pos, num_heads, head_dim, partial_rope_dim, rope_theta, st(stream)));
+}
+
+void attn_qk_norm_rope_rows(float* q, float* k, const float* q_weight, const float* k_weight, const int32_t* pos,
+                            int pos0, int rows, int q_heads, int k_heads, int head_dim, int partial_rope_dim,
+                            float rope_theta, float eps, hipStream_t stream) {
+    check(qwen_attn_qk_norm_rope_rows(q, k, q_weight, k_weight, pos, pos0, rows, q_heads, k_heads, head_dim,
+                                      partial_rope_dim, rope_theta, eps, st(stream)));
+}
+
+// ---- gdn.hpp
+void gdn_conv_step(const float* input, const float* weight, float* history, float* output, int channels, int kernel,
+                   hipStream_t stream) {
+    check(qwen_gdn_conv_step(input, weight, history, output, channels, kernel, st(stream)));
+}
+
+void gdn_qk_normalize(float* q, float* k, int heads, int dim, float eps, hipStream_t stream) {
+    check(qwen_gdn_qk_normalize(q, k, heads, dim, eps, st(stream)));
+}
+
+void gdn_norm_gate(const float* x, const float* z, const float* weight, float* out, int heads, int dim, float eps,
+                   hipStream_t stream) {
+    check(qwen_gdn_norm_gate(x, z, weight, out, heads, dim, eps, st(stream)));
+}
+
+void gdn_frontend_rows(const float* x, const float* weight, const float* hist_in, float* hist_out, float* y, int rows,
+                       int channels, int kernel, int k_heads, int key_dim, float eps, hipStream_t stream) {
+    check(qwen_gdn_frontend_rows(x, weight, hist_in, hist_out, y, rows, channels, kernel, k_heads, key_dim, eps,
+                                 st(stream)));
+}
+
+void gdn_norm_gate_rows(const float* x, const float* z, const float* weight, float* out, int rows, int heads, int dim,
+                        float eps, hipStream_t stream) {
+    check(qwen_gdn_norm_gate_rows(x, z, weight, out, rows, heads, dim, eps, st(stream)));
+}
+
+// ---- layer_kernels.hpp
+void attn_head_norm(float* x, const float* weight, int heads, int dim, float eps, hipStream_t stream) {
+    check(qwen_attn_head_norm(x, weight, heads, dim, eps, st(stream)));
+}
+
+void moe_silu_mul(const float* gate, const float* up, float* hidden, int dim, hipStream_t stream) {
+    check(qwen_moe_silu_mul(gate, up, hidden, dim, st(stream)));
+}
+
+void moe_shared_add(float* accum, const float* shared_out, const float* sgate, int dim, hipStream_t stream) {
+    check(qwen_moe_shared_add(accum, shared_out, sgate, dim, st(stream)));
+}
+
+void moe_shared_add_rows(float* accum, const float* shared_out, const float* sgate, int rows, int dim,
+                         hipStream_t stream) {
+    check(qwen_moe_shared_add_rows(accum, shared_out, sgate, rows, dim, st(stream)));
+}
+
+void swiglu_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* hidden, int64_t n, hipStream_t stream) {
+    check(qwen_swiglu_bf16(gate, up, hidden, n, st(stream)));
+}
+
+void shared_swiglu_sigmoid_rows_bf16(const uint16_t* gate, const uint16_t* up, const float* logits, uint16_t* hidden,
+                                     int rows, int dim, hipStream_t stream) {
+    check(qwen_shared_swiglu_sigmoid_rows_bf16(gate, up, logits, hidden, rows, dim, st(stream)));
+}
+
+// ---- matmul_q4.hpp
+bool matmul_type_supported(GgmlType type) { return qwen_type_supported(static_cast<int>(type)) != 0; }
+
+void dequantize_row(const QuantTensor& tensor, float* out, int row, int cols, hipStream_t stream) {
+    const int status = qwen_dequantize_row(tensor.device_ptr, static_cast<int>(tensor.type), tensor.num_elements, out,
+                                           row, cols, st(stream));
+    // Reference messages, src/cuda/matmul_q4.cu:210-217.
+    if (status == QWEN_STATUS_UNSUPPORTED_TYPE)
+        throw std::runtime_error("cannot dequantize tensor '" + tensor.name + "'");
+    if (status == QWEN_STATUS_OUT_OF_RANGE) throw std::runtime_error("row is outside tensor '" + tensor.name + "'");
+    check(status);
+}
+
+void dequant_gather_rows(const QuantTensor& tensor, const int32_t* ids, int n_ids, int cols, float* out,
+                         hipStream_t stream) {
+    const int status = qwen_dequant_gather_rows(tensor.device_ptr, static_cast<int>(tensor.type), tensor.num_elements,
+                                                ids, n_ids, cols, out, st(stream));
+    if (status == QWEN_STATUS_UNSUPPORTED_TYPE)
+        throw std::runtime_error("cannot dequantize tensor '" + tensor.name + "'");
+    check(status);
+}
+
+}  // namespace qwen

@@ -1,0 +1,279 @@
+"""Tensor-level entry points over the C ABI.
+
+Each function checks on the host that every tensor is a contiguous device
+tensor of the dtype and shape the kernel assumes (the C ABI can only check
+sizes, not buffer extents), then enqueues the kernel on `stream` (default: the
+current torch stream) and returns the output tensor(s). Nothing here computes on
+the CPU: the work is done by libqwen35_hip.so or not at all.
+
+torch is used for device memory and streams only.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ._lib import check, load
+
+BF16 = torch.bfloat16  # bf16 storage (fp32 math inside the kernels)
+
+GGML_TYPES = {"F32": 0, "F16": 1, "Q4_0": 2, "Q5_0": 6, "Q8_0": 8, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "BF16": 30}
+
+
+def _stream(stream) -> ctypes.c_void_p:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _p(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
+
+
+def _dev(*ts: torch.Tensor, dtype=None) -> None:
+    for t in ts:
+        if not isinstance(t, torch.Tensor) or not t.is_cuda:
+            raise ValueError("expected a device tensor")
+        if not t.is_contiguous():
+            raise ValueError("expected a contiguous tensor")
+        if dtype is not None and t.dtype != dtype:
+            raise ValueError(f"expected dtype {dtype}, got {t.dtype}")
+
+
+def _same(shape, *ts: torch.Tensor) -> None:
+    for t in ts:
+        if tuple(t.shape) != tuple(shape):
+            raise ValueError(f"shape {tuple(t.shape)} != {tuple(shape)}")
+
+
+def _rows(x: torch.Tensor) -> tuple[int, int]:
+    if x.dim() < 1:
+        raise ValueError("expected at least one dimension")
+    n = x.shape[-1]
+    return (x.numel() // n if n else 0), n
+
+
+# ------------------------------------------------------------------ norms
+def rmsnorm_rows(x, weight, out=None, eps=1e-6, stream=None):
+    _dev(x, weight, dtype=torch.float32)
+    rows, n = _rows(x)
+    _same((n,), weight)
+    out = torch.empty_like(x) if out is None else out
+    _dev(out, dtype=torch.float32)
+    _same(x.shape, out)
+    check(load().qwen_rmsnorm_rows(_p(x), _p(weight), _p(out), rows, n, eps, _stream(stream)))
+    return out
+
+
+def rmsnorm_gated_rows(x, gate, weight, out=None, eps=1e-6, stream=None):
+    _dev(x, gate, weight, dtype=torch.float32)
+    rows, n = _rows(x)
+    _same(x.shape, gate)
+    _same((n,), weight)
+    out = torch.empty_like(x) if out is None else out
+    _dev(out, dtype=torch.float32)
+    _same(x.shape, out)
+    check(load().qwen_rmsnorm_gated_rows(_p(x), _p(gate), _p(weight), _p(out), rows, n, eps, _stream(stream)))
+    return out
+
+
+def residual_add(x1, x2, out=None, stream=None):
+    _dev(x1, x2, dtype=torch.float32)
+    _same(x1.shape, x2)
+    out = torch.empty_like(x1) if out is None else out
+    _dev(out, dtype=torch.float32)
+    _same(x1.shape, out)
+    check(load().qwen_residual_add(_p(x1), _p(x2), _p(out), x1.numel(), _stream(stream)))
+    return out
+
+
+def residual_rmsnorm_rows(x, branch, weight, resid=None, normed=None, eps=1e-6, stream=None):
+    """resid = x + branch; normed = rmsnorm(resid) * weight. fp32 or bf16 storage."""
+    dt = x.dtype
+    if dt not in (torch.float32, BF16):
+        raise ValueError("x must be float32 or bfloat16")
+    _dev(x, branch, dtype=dt)
+    _dev(weight, dtype=torch.float32)
+    rows, n = _rows(x)
+    _same(x.shape, branch)
+    _same((n,), weight)
+    resid = torch.empty_like(x) if resid is None else resid
+    normed = torch.empty_like(x) if normed is None else normed
+    _dev(resid, normed, dtype=dt)
+    _same(x.shape, resid, normed)
+    fn = load().qwen_residual_rmsnorm_rows_f32 if dt == torch.float32 else load().qwen_residual_rmsnorm_rows_bf16
+    check(fn(_p(x), _p(branch), _p(weight), _p(resid), _p(normed), rows, n, eps, _stream(stream)))
+    return resid, normed
+
+
+def encoder_forward(token_id: int, table, out=None, stream=None):
+    _dev(table, dtype=torch.float32)
+    vocab, d = table.shape
+    if not 0 <= token_id < vocab:
+        raise ValueError(f"token {token_id} outside the table of {vocab} rows")
+    out = torch.empty(d, dtype=torch.float32, device=table.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    _same((d,), out)
+    check(load().qwen_encoder_forward(token_id, _p(table), _p(out), d, _stream(stream)))
+    return out
+
+
+# ------------------------------------------------------------------ attention
+def attn_head_norm(x, weight, eps=1e-6, stream=None):
+    """In place on x [..., heads, dim]."""
+    _dev(x, weight, dtype=torch.float32)
+    heads, dim = _rows(x)
+    _same((dim,), weight)
+    check(load().qwen_attn_head_norm(_p(x), _p(weight), heads, dim, eps, _stream(stream)))
+    return x
+
+
+def rope_forward(x, pos: int, rope_dim=64, theta=1e6, stream=None):
+    """In place on x [heads, head_dim] (one token)."""
+    _dev(x, dtype=torch.float32)
+    heads, hd = _rows(x)
+    check(load().qwen_rope_forward(_p(x), pos, heads, hd, rope_dim, theta, _stream(stream)))
+    return x
+
+
+def attn_qk_norm_rope_rows(q, k, q_weight, k_weight, pos=None, pos0=0, rope_dim=64, theta=1e7, eps=1e-6,
+                           stream=None):
+    """In place: q [rows, q_heads, hd], k [rows, k_heads, hd]; pos int32 [rows] or None."""
+    _dev(q, k, q_weight, k_weight, dtype=torch.float32)
+    if q.dim() != 3 or k.dim() != 3 or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise ValueError("q, k must be [rows, heads, head_dim] with equal rows and head_dim")
+    rows, qh, hd = q.shape
+    kh = k.shape[1]
+    _same((hd,), q_weight, k_weight)
+    if pos is not None:
+        _dev(pos, dtype=torch.int32)
+        _same((rows,), pos)
+    check(load().qwen_attn_qk_norm_rope_rows(_p(q), _p(k), _p(q_weight), _p(k_weight), _p(pos), pos0, rows, qh, kh,
+                                             hd, rope_dim, theta, eps, _stream(stream)))
+    return q, k
+
+
+# ------------------------------------------------------------------ Gated DeltaNet
+def gdn_frontend_rows(x, weight, hist_in, hist_out=None, y=None, k_heads=16, key_dim=128, eps=1e-6, stream=None):
+    """x [rows, C], weight [C, K], hist [C, K-1] -> (y [rows, C], hist_out)."""
+    _dev(x, weight, hist_in, dtype=torch.float32)
+    rows, c = _rows(x)
+    if weight.dim() != 2 or weight.shape[0] != c:
+        raise ValueError("weight must be [channels, kernel]")
+    kernel = weight.shape[1]
+    _same((c, kernel - 1), hist_in)
+    hist_out = torch.empty_like(hist_in) if hist_out is None else hist_out
+    y = torch.empty_like(x) if y is None else y
+    _dev(hist_out, y, dtype=torch.float32)
+    _same(hist_in.shape, hist_out)
+    _same(x.shape, y)
+    check(load().qwen_gdn_frontend_rows(_p(x), _p(weight), _p(hist_in), _p(hist_out), _p(y), rows, c, kernel, k_heads,
+                                        key_dim, eps, _stream(stream)))
+    return y, hist_out
+
+
+def gdn_conv_step(x, weight, history, y=None, stream=None):
+    """One token: x [C], weight [C, K], history [C, K-1] (updated in place)."""
+    _dev(x, weight, history, dtype=torch.float32)
+    c = x.numel()
+    kernel = weight.shape[1]
+    _same((c, kernel), weight)
+    _same((c, kernel - 1), history)
+    y = torch.empty_like(x) if y is None else y
+    _dev(y, dtype=torch.float32)
+    _same(x.shape, y)
+    check(load().qwen_gdn_conv_step(_p(x), _p(weight), _p(history), _p(y), c, kernel, _stream(stream)))
+    return y
+
+
+def gdn_qk_normalize(q, k, eps=1e-6, stream=None):
+    """In place on q, k [heads, dim]."""
+    _dev(q, k, dtype=torch.float32)
+    heads, dim = _rows(q)
+    _same(q.shape, k)
+    check(load().qwen_gdn_qk_normalize(_p(q), _p(k), heads, dim, eps, _stream(stream)))
+    return q, k
+
+
+def gdn_norm_gate_rows(x, z, weight, out=None, eps=1e-6, stream=None):
+    """x, z [..., heads, dim]; weight [dim]."""
+    _dev(x, z, weight, dtype=torch.float32)
+    heads_total, dim = _rows(x)
+    _same(x.shape, z)
+    _same((dim,), weight)
+    out = torch.empty_like(x) if out is None else out
+    _dev(out, dtype=torch.float32)
+    _same(x.shape, out)
+    check(load().qwen_gdn_norm_gate_rows(_p(x), _p(z), _p(weight), _p(out), heads_total, 1, dim, eps,
+                                         _stream(stream)))
+    return out
+
+
+# ------------------------------------------------------------------ MoE
+def moe_silu_mul(g, u, out=None, stream=None):
+    _dev(g, u, dtype=torch.float32)
+    _same(g.shape, u)
+    out = torch.empty_like(g) if out is None else out
+    _dev(out, dtype=torch.float32)
+    _same(g.shape, out)
+    check(load().qwen_moe_silu_mul(_p(g), _p(u), _p(out), g.numel(), _stream(stream)))
+    return out
+
+
+def moe_shared_add_rows(accum, shared_out, gate, stream=None):
+    """accum [rows, n] += shared_out * sigmoid(gate[rows]) in place."""
+    _dev(accum, shared_out, gate, dtype=torch.float32)
+    rows, n = _rows(accum)
+    _same(accum.shape, shared_out)
+    _same((rows,), gate)
+    check(load().qwen_moe_shared_add_rows(_p(accum), _p(shared_out), _p(gate), rows, n, _stream(stream)))
+    return accum
+
+
+def swiglu_bf16(g, u, out=None, stream=None):
+    _dev(g, u, dtype=BF16)
+    _same(g.shape, u)
+    out = torch.empty_like(g) if out is None else out
+    _dev(out, dtype=BF16)
+    _same(g.shape, out)
+    check(load().qwen_swiglu_bf16(_p(g), _p(u), _p(out), g.numel(), _stream(stream)))
+    return out
+
+
+def shared_swiglu_sigmoid_rows_bf16(g, u, logits, out=None, stream=None):
+    _dev(g, u, dtype=BF16)
+    _dev(logits, dtype=torch.float32)
+    rows, dim = _rows(g)
+    _same(g.shape, u)
+    _same((rows,), logits)
+    out = torch.empty_like(g) if out is None else out
+    _dev(out, dtype=BF16)
+    _same(g.shape, out)
+    check(load().qwen_shared_swiglu_sigmoid_rows_bf16(_p(g), _p(u), _p(logits), _p(out), rows, dim, _stream(stream)))
+    return out
+
+
+# ------------------------------------------------------------------ dequant
+def dequant_gather_rows(table, ggml_type, num_elements: int, ids, cols: int, out=None, stream=None):
+    """table: uint8 device tensor of GGML blocks; ids int32 [n]; -> float32 [n, cols]."""
+    _dev(table, dtype=torch.uint8)
+    _dev(ids, dtype=torch.int32)
+    t = GGML_TYPES[ggml_type] if isinstance(ggml_type, str) else int(ggml_type)
+    n = ids.numel()
+    out = torch.empty((n, cols), dtype=torch.float32, device=table.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    _same((n, cols), out)
+    check(load().qwen_dequant_gather_rows(_p(table), t, num_elements, _p(ids), n, cols, _p(out), _stream(stream)))
+    return out
+
+
+def dequantize_row(table, ggml_type, num_elements: int, row: int, cols: int, out=None, stream=None):
+    _dev(table, dtype=torch.uint8)
+    t = GGML_TYPES[ggml_type] if isinstance(ggml_type, str) else int(ggml_type)
+    out = torch.empty(cols, dtype=torch.float32, device=table.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    _same((cols,), out)
+    check(load().qwen_dequantize_row(_p(table), t, num_elements, _p(out), row, cols, _stream(stream)))
+    return out

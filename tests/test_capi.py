@@ -1,0 +1,133 @@
+"""C ABI checks that need no GPU: the library loads, exports every function the
+header declares, and rejects bad arguments on the host before any launch (the
+reference's throw conditions, src/cuda/rope.cu:33-43 and
+src/cuda/matmul_q4.cu:210-217, map to status codes). Zero-size calls return OK
+without touching the device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+
+import pytest
+
+from qwen35_hip import _lib
+
+NULL = None
+ST = None  # default stream; never reached by these calls
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def msg(lib) -> str:
+    return lib.qwen_last_error().decode()
+
+
+def test_exports_every_declared_function(lib):
+    declared = _lib.header_functions()
+    assert len(declared) >= 27
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    missing = [f for f in declared if f not in exported]
+    assert not missing, missing
+    assert set(declared) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_cxx_dropin_symbols_exported():
+    out = subprocess.run(["nm", "-DC", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    for sig in [
+        "qwen::rmsnorm_forward(float const*, float const*, float*, int, float, ihipStream_t*)",
+        "qwen::rmsnorm_gated_forward(float const*, float const*, float const*, float*, int, float, ihipStream_t*)",
+        "qwen::residual_add(float const*, float const*, float*, int, ihipStream_t*)",
+        "qwen::encoder_forward(int, float const*, float*, int, ihipStream_t*)",
+        "qwen::rope_forward(float*, int, int, int, int, float, ihipStream_t*)",
+        "qwen::attn_head_norm(float*, float const*, int, int, float, ihipStream_t*)",
+        "qwen::gdn_conv_step(float const*, float const*, float*, float*, int, int, ihipStream_t*)",
+        "qwen::gdn_qk_normalize(float*, float*, int, int, float, ihipStream_t*)",
+        "qwen::gdn_norm_gate(float const*, float const*, float const*, float*, int, int, float, ihipStream_t*)",
+        "qwen::moe_silu_mul(float const*, float const*, float*, int, ihipStream_t*)",
+        "qwen::moe_shared_add(float*, float const*, float const*, int, ihipStream_t*)",
+        "qwen::dequantize_row(qwen::QuantTensor const&, float*, int, int, ihipStream_t*)",
+        "qwen::matmul_type_supported(qwen::GgmlType)",
+    ]:
+        assert sig in out, sig
+
+
+def test_status_names(lib):
+    assert lib.qwen_abi_version() == 1
+    names = [lib.qwen_status_name(i).decode() for i in range(5)]
+    assert names == ["QWEN_STATUS_OK", "QWEN_STATUS_INVALID_ARGUMENT", "QWEN_STATUS_UNSUPPORTED_TYPE",
+                     "QWEN_STATUS_OUT_OF_RANGE", "QWEN_STATUS_LAUNCH_FAILED"]
+
+
+FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails validation first
+
+
+@pytest.mark.parametrize("args", [
+    (NULL, 3, 2, 8, 4, 100.0),        # null pointer
+    (FAKE, -1, 2, 8, 4, 100.0),       # negative position
+    (FAKE, 3, 0, 8, 4, 100.0),        # no heads
+    (FAKE, 3, 2, 0, 4, 100.0),        # head_dim 0
+    (FAKE, 3, 2, 8, 0, 100.0),        # rope_dim 0
+    (FAKE, 3, 2, 8, 10, 100.0),       # rope_dim > head_dim
+    (FAKE, 3, 2, 8, 3, 100.0),        # odd rope_dim
+    (FAKE, 3, 2, 4096, 2050, 100.0),  # rope_dim / 2 > 1024
+    (FAKE, 3, 2, 8, 4, 0.0),          # theta <= 0
+    (FAKE, 3, 2, 8, 4, float("nan")),  # theta not > 0
+])
+def test_rope_rejects_reference_conditions(lib, args):
+    assert lib.qwen_rope_forward(*args, ST) == _lib.STATUS_INVALID_ARGUMENT
+    assert msg(lib) == "invalid RoPE arguments"
+
+
+def test_dequantize_row_errors(lib):
+    Q4_K, Q4_1 = 12, 3
+    assert lib.qwen_dequantize_row(NULL, Q4_K, 256, FAKE, 0, 256, ST) == _lib.STATUS_UNSUPPORTED_TYPE
+    assert msg(lib) == "cannot dequantize tensor"
+    assert lib.qwen_dequantize_row(FAKE, Q4_1, 256, FAKE, 0, 256, ST) == _lib.STATUS_UNSUPPORTED_TYPE
+    for row, cols, n in [(-1, 256, 512), (0, 0, 512), (0, -5, 512), (1, 256, 256), (2, 256, 767)]:
+        assert lib.qwen_dequantize_row(FAKE, Q4_K, n, FAKE, row, cols, ST) == _lib.STATUS_OUT_OF_RANGE
+        assert msg(lib) == "row is outside tensor"
+    assert lib.qwen_dequantize_row(FAKE, Q4_K, 512, NULL, 1, 256, ST) == _lib.STATUS_INVALID_ARGUMENT
+    assert lib.qwen_dequant_gather_rows(FAKE, 3, 512, FAKE, 1, 256, FAKE, ST) == _lib.STATUS_UNSUPPORTED_TYPE
+    assert lib.qwen_dequant_gather_rows(FAKE, Q4_K, 512, FAKE, -1, 256, FAKE, ST) == _lib.STATUS_INVALID_ARGUMENT
+    assert lib.qwen_dequant_gather_rows(FAKE, Q4_K, 512, NULL, 4, 256, FAKE, ST) == _lib.STATUS_INVALID_ARGUMENT
+    assert lib.qwen_dequant_gather_rows(FAKE, Q4_K, 512, FAKE, 0, 256, FAKE, ST) == _lib.STATUS_OK
+
+
+def test_type_supported(lib):
+    for t in range(40):
+        assert lib.qwen_type_supported(t) == (1 if t in (0, 1, 2, 6, 8, 12, 13, 14, 30) else 0)
+
+
+def test_size_and_pointer_validation(lib):
+    INV, OK = _lib.STATUS_INVALID_ARGUMENT, _lib.STATUS_OK
+    assert lib.qwen_rmsnorm_rows(FAKE, FAKE, FAKE, -1, 8, 1e-6, ST) == INV
+    assert lib.qwen_rmsnorm_rows(NULL, FAKE, FAKE, 2, 8, 1e-6, ST) == INV
+    assert lib.qwen_rmsnorm_rows(NULL, NULL, NULL, 0, 8, 1e-6, ST) == OK  # nothing to do
+    assert lib.qwen_rmsnorm_forward(NULL, NULL, NULL, 0, 1e-6, ST) == OK
+    assert lib.qwen_rmsnorm_gated_rows(FAKE, NULL, FAKE, FAKE, 1, 8, 1e-6, ST) == INV
+    assert lib.qwen_residual_add(FAKE, FAKE, FAKE, -4, ST) == INV
+    assert lib.qwen_residual_rmsnorm_rows_bf16(FAKE, FAKE, NULL, FAKE, FAKE, 1, 8, 1e-6, ST) == INV
+    assert lib.qwen_encoder_forward(-1, FAKE, FAKE, 16, ST) == INV
+    assert lib.qwen_attn_head_norm(NULL, FAKE, 2, 8, 1e-6, ST) == INV
+    assert lib.qwen_attn_qk_norm_rope_rows(FAKE, FAKE, FAKE, FAKE, NULL, 0, 4, 2, 1, 8, 10, 1e7, 1e-6, ST) == INV
+    assert lib.qwen_attn_qk_norm_rope_rows(FAKE, FAKE, FAKE, FAKE, NULL, -1, 4, 2, 1, 8, 4, 1e7, 1e-6, ST) == INV
+    assert lib.qwen_attn_qk_norm_rope_rows(FAKE, NULL, FAKE, NULL, NULL, 0, 4, 2, 1, 8, 4, 1e7, 1e-6, ST) == INV
+    assert lib.qwen_attn_qk_norm_rope_rows(FAKE, FAKE, FAKE, FAKE, NULL, 0, 4, 2, 1, 8, 4, 0.0, 1e-6, ST) == INV
+    assert lib.qwen_gdn_frontend_rows(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 1, 0, 0, 1e-6, ST) == INV
+    assert lib.qwen_gdn_frontend_rows(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 4, 1, 64, 1e-6, ST) == INV
+    assert lib.qwen_gdn_frontend_rows(FAKE, FAKE, NULL, FAKE, FAKE, 4, 64, 4, 0, 0, 1e-6, ST) == INV
+    assert lib.qwen_gdn_qk_normalize(FAKE, NULL, 2, 8, 1e-6, ST) == INV
+    assert lib.qwen_gdn_norm_gate_rows(FAKE, FAKE, FAKE, FAKE, 1, -2, 8, 1e-6, ST) == INV
+    assert lib.qwen_moe_silu_mul(FAKE, NULL, FAKE, 8, ST) == INV
+    assert lib.qwen_moe_shared_add_rows(FAKE, FAKE, FAKE, 70000, 8, ST) == INV
+    assert lib.qwen_swiglu_bf16(FAKE, FAKE, FAKE, -1, ST) == INV
+    assert lib.qwen_shared_swiglu_sigmoid_rows_bf16(FAKE, FAKE, NULL, FAKE, 2, 8, ST) == INV
+    assert "null" in msg(lib)

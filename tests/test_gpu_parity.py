@@ -1,0 +1,343 @@
+"""GPU parity: every C entry point against the CPU oracle on identical inputs.
+
+Bars: fp32 within 1e-5 relative (row-rms floor for cancelling sums), bf16
+within 1 ulp, dequant-gather bit-exact. Inputs are the seeded BASELINE configs
+(qwen35_hip.synth) at full size plus edge shapes that route through the
+scalar / generic paths (odd lengths, unaligned pointers, other head sizes,
+kernel sizes and GGML types).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_bf16_close, assert_bits_equal, assert_f32_close
+from qwen35_hip import ops, synth
+
+pytestmark = pytest.mark.gpu
+THREADS = 16
+F32 = np.float32
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda().view(torch.bfloat16)
+    return torch.from_numpy(a).cuda()
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    torch.cuda.synchronize()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+    return t.cpu().numpy()
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ------------------------------------------------------------------ RMSNorm family
+def test_rmsnorm_config_c1(oracle):
+    c = synth.c1_rmsnorm()
+    got = host(ops.rmsnorm_rows(dev(c["x"]), dev(c["w"]), eps=c["eps"]))
+    assert_f32_close(got, oracle.rmsnorm_rows(c["x"], c["w"], c["eps"]), what="C1")
+
+
+@pytest.mark.parametrize("rows,n", [(1, 2), (3, 7), (5, 64), (2, 1000), (9, 1001), (4, 4096), (3, 8192), (1100, 512)])
+def test_rmsnorm_shapes(oracle, rows, n):
+    r = rng(rows * 100003 + n)
+    x = r.standard_normal((rows, n)).astype(F32)
+    w = (1 + 0.1 * r.standard_normal(n)).astype(F32)
+    got = host(ops.rmsnorm_rows(dev(x), dev(w)))
+    assert_f32_close(got, oracle.rmsnorm_rows(x, w), what=f"rmsnorm {rows}x{n}")
+
+
+def test_rmsnorm_unaligned_and_reference_fixture(oracle):
+    r = rng(5)
+    buf = dev(r.standard_normal(2049).astype(F32))
+    x = buf[1:]  # 4-byte aligned only: the scalar path
+    w = dev((1 + 0.1 * r.standard_normal(2048)).astype(F32))
+    got = host(ops.rmsnorm_rows(x.view(1, 2048), w))
+    assert_f32_close(got, oracle.rmsnorm_rows(host(x).reshape(1, 2048), host(w)), what="unaligned")
+    # tests/kernel_tests.cu:301-325 through the single-row entry point
+    xf, wf = dev(np.array([3.0, 4.0], F32)), dev(np.array([2.0, 0.5], F32))
+    out = torch.empty(2, device="cuda")
+    ops.check(ops.load().qwen_rmsnorm_forward(ops._p(xf), ops._p(wf), ops._p(out), 2, 1e-6, ops._stream(None)))
+    r_ = 1.0 / np.sqrt(np.float32(12.5) + np.float32(1e-6))
+    assert np.max(np.abs(host(out) - np.array([3 * r_ * 2, 4 * r_ * 0.5], F32))) < 1e-5
+
+
+@pytest.mark.parametrize("rows,n", [(36, 2048), (3, 1001), (8, 8192)])
+def test_rmsnorm_gated(oracle, rows, n):
+    r = rng(n)
+    x = r.standard_normal((rows, n)).astype(F32)
+    g = (2 * r.standard_normal((rows, n))).astype(F32)
+    w = (1 + 0.1 * r.standard_normal(n)).astype(F32)
+    got = host(ops.rmsnorm_gated_rows(dev(x), dev(g), dev(w)))
+    assert_f32_close(got, oracle.rmsnorm_gated_rows(x, g, w), what="gated")
+
+
+@pytest.mark.parametrize("n", [2048, 1001, 1 << 20])
+def test_residual_add(oracle, n):
+    r = rng(n)
+    a, b = r.standard_normal(n).astype(F32), r.standard_normal(n).astype(F32)
+    assert_bits_equal(host(ops.residual_add(dev(a), dev(b))), oracle.residual_add(a, b))
+
+
+def test_residual_rmsnorm_bf16_config_c3a(oracle):
+    c = synth.c3_residual()
+    resid, normed = ops.residual_rmsnorm_rows(dev(c["x"]), dev(c["branch"]), dev(c["w"]), eps=c["eps"])
+    r_ref, n_ref = oracle.residual_rmsnorm_rows(c["x"], c["branch"], c["w"], c["eps"], threads=THREADS)
+    assert np.array_equal(host(resid), r_ref), "resid must be the exact RNE of the fp32 sum"
+    assert_bf16_close(host(normed), n_ref, what="C3a normed")
+
+
+@pytest.mark.parametrize("rows,n", [(7, 2048), (3, 1000), (2, 6000), (64, 4096)])
+def test_residual_rmsnorm_shapes(oracle, rows, n):
+    r = rng(rows + n)
+    x, b = r.standard_normal((rows, n)).astype(F32), r.standard_normal((rows, n)).astype(F32)
+    w = (1 + 0.1 * r.standard_normal(n)).astype(F32)
+    resid, normed = ops.residual_rmsnorm_rows(dev(x), dev(b), dev(w))
+    r_ref, n_ref = oracle.residual_rmsnorm_rows(x, b, w)
+    assert_bits_equal(host(resid), r_ref)
+    assert_f32_close(host(normed), n_ref, what="f32 normed")
+    xb, bb = synth.to_bf16_bits(x), synth.to_bf16_bits(b)
+    resid, normed = ops.residual_rmsnorm_rows(dev(xb), dev(bb), dev(w))
+    r_ref, n_ref = oracle.residual_rmsnorm_rows(xb, bb, w)
+    assert np.array_equal(host(resid), r_ref)
+    assert_bf16_close(host(normed), n_ref, what="bf16 normed")
+
+
+def test_encoder_forward(oracle):
+    table = rng(9).standard_normal((100, 2048)).astype(F32)
+    t = dev(table)
+    for tok in (0, 57, 99):
+        assert_bits_equal(host(ops.encoder_forward(tok, t)), table[tok])
+
+
+# ------------------------------------------------------------------ attention
+def test_qk_norm_rope_config_c2(oracle):
+    c = synth.c2_qk_rope()
+    q, k = dev(c["q"]), dev(c["k"])
+    ops.attn_qk_norm_rope_rows(q, k, dev(c["qw"]), dev(c["kw"]), pos=dev(c["pos"]), rope_dim=c["rope_dim"],
+                               theta=c["theta"], eps=c["eps"])
+    rq, rk = oracle.qk_norm_rope_rows(c["q"], c["k"], c["qw"], c["kw"], pos=c["pos"], rope_dim=c["rope_dim"],
+                                      theta=c["theta"], eps=c["eps"], threads=THREADS)
+    assert_f32_close(host(q), rq, group=256, what="C2 q")
+    assert_f32_close(host(k), rk, group=256, what="C2 k")
+
+
+@pytest.mark.parametrize("hd,rd,qh,kh", [(128, 64, 4, 2), (128, 128, 3, 1), (64, 32, 5, 3), (256, 256, 2, 1),
+                                         (256, 0, 2, 2), (96, 32, 2, 1), (256, 60, 2, 1)])
+def test_qk_norm_rope_shapes(oracle, hd, rd, qh, kh):
+    r = rng(hd * 7 + rd)
+    rows = 33
+    q, k = r.standard_normal((rows, qh, hd)).astype(F32), r.standard_normal((rows, kh, hd)).astype(F32)
+    qw, kw = (1 + 0.1 * r.standard_normal(hd)).astype(F32), (1 + 0.1 * r.standard_normal(hd)).astype(F32)
+    pos = r.integers(0, 40000, size=rows).astype(np.int32)
+    dq, dk = dev(q), dev(k)
+    ops.attn_qk_norm_rope_rows(dq, dk, dev(qw), dev(kw), pos=dev(pos), rope_dim=rd, theta=1e6)
+    rq, rk = oracle.qk_norm_rope_rows(q, k, qw, kw, pos=pos, rope_dim=rd, theta=1e6)
+    assert_f32_close(host(dq), rq, group=hd, what="q")
+    assert_f32_close(host(dk), rk, group=hd, what="k")
+
+
+def test_rope_forward_reference_fixture_and_drop_in(oracle):
+    import json
+    from pathlib import Path
+
+    fx = json.loads((Path(__file__).parent / "golden" / "reference_fixtures.json").read_text())["rope"]
+    x = dev(np.array(fx["x"], F32).reshape(fx["heads"], fx["head_dim"]))
+    ops.rope_forward(x, fx["pos"], rope_dim=fx["rope_dim"], theta=fx["theta"])
+    assert np.max(np.abs(host(x).ravel() - np.array(fx["expected"], F32))) < fx["tol"]
+    # the production shape: 16 heads x 256, rope 64, theta 1e7, pos 511
+    v = rng(3).standard_normal((16, 256)).astype(F32)
+    d = dev(v)
+    ops.rope_forward(d, 511, rope_dim=64, theta=1e7)
+    assert_f32_close(host(d), oracle.rope_rows(v[None], pos0=511, rope_dim=64, theta=1e7)[0], group=256)
+
+
+@pytest.mark.parametrize("heads,dim", [(16, 256), (2, 256), (3, 100)])
+def test_attn_head_norm(oracle, heads, dim):
+    r = rng(heads * dim)
+    x, w = r.standard_normal((heads, dim)).astype(F32), (1 + 0.1 * r.standard_normal(dim)).astype(F32)
+    d = dev(x)
+    ops.attn_head_norm(d, dev(w))
+    assert_f32_close(host(d), oracle.head_norm_rows(x, w), what="head_norm")
+
+
+# ------------------------------------------------------------------ Gated DeltaNet
+@pytest.mark.parametrize("random_history", [False, True])
+def test_gdn_frontend_config_c4a(oracle, random_history):
+    c = synth.c4_frontend(random_history=random_history)
+    hist = dev(c["hist"])
+    y, h = ops.gdn_frontend_rows(dev(c["x"]), dev(c["w"]), hist, hist_out=hist, k_heads=c["k_heads"],
+                                 key_dim=c["key_dim"], eps=c["eps"])
+    ry, rh = oracle.gdn_frontend_rows(c["x"], c["w"], c["hist"], c["k_heads"], c["key_dim"], c["eps"],
+                                      threads=THREADS)
+    assert_f32_close(host(y), ry, group=128, what="C4a y")
+    assert_bits_equal(host(h), rh, "C4a history")
+
+
+@pytest.mark.parametrize("rows,channels,kernel,heads,dim", [
+    (1, 8192, 4, 16, 128), (2, 1024, 4, 2, 128), (65, 1024, 4, 2, 128), (200, 640, 4, 1, 64),
+    (130, 768, 4, 3, 128), (50, 8192, 4, 0, 0), (40, 1000, 4, 2, 100), (70, 512, 3, 2, 64), (9, 255, 5, 1, 32)])
+def test_gdn_frontend_shapes(oracle, rows, channels, kernel, heads, dim):
+    r = rng(rows * 31 + channels + kernel)
+    x = r.standard_normal((rows, channels)).astype(F32)
+    w = (0.5 * r.standard_normal((channels, kernel))).astype(F32)
+    hist = r.standard_normal((channels, kernel - 1)).astype(F32)
+    y, h = ops.gdn_frontend_rows(dev(x), dev(w), dev(hist), k_heads=heads, key_dim=dim)
+    ry, rh = oracle.gdn_frontend_rows(x, w, hist, heads, dim)
+    assert_f32_close(host(y), ry, group=channels, what="y")
+    assert_bits_equal(host(h), rh, "history")
+
+
+def test_gdn_frontend_chunked_equals_one_shot(oracle):
+    c = synth.c4_frontend(rows=300, channels=1024, random_history=True)
+    x, w = dev(c["x"]), dev(c["w"])
+    hist = dev(c["hist"])
+    y1, _ = ops.gdn_frontend_rows(x[:100], w, hist, hist_out=hist, k_heads=2, key_dim=128)
+    y2, _ = ops.gdn_frontend_rows(x[100:], w, hist, hist_out=hist, k_heads=2, key_dim=128)
+    y, h = ops.gdn_frontend_rows(x, w, dev(c["hist"]), k_heads=2, key_dim=128)
+    assert_bits_equal(torch.cat([y1, y2]).cpu().numpy(), host(y))
+    assert_bits_equal(host(hist), host(h))
+
+
+def test_gdn_conv_step_sequence_and_qk_normalize(oracle):
+    r = rng(77)
+    C, T = 8192, 5
+    x = r.standard_normal((T, C)).astype(F32)
+    w = (0.5 * r.standard_normal((C, 4))).astype(F32)
+    hist = dev(np.zeros((C, 3), F32))
+    dw = dev(w)
+    ys = [host(ops.gdn_conv_step(dev(x[t]), dw, hist)) for t in range(T)]
+    ry, rh = oracle.conv_rows(x, w, np.zeros((C, 3), F32))
+    assert_f32_close(np.stack(ys), ry, group=C)
+    assert_bits_equal(host(hist), rh)
+    q = r.standard_normal((16, 128)).astype(F32)
+    k = r.standard_normal((16, 128)).astype(F32)
+    dq, dk = dev(q), dev(k)
+    ops.gdn_qk_normalize(dq, dk)
+    rq, rk = oracle.qk_l2_rows(q[None], k[None])
+    assert_f32_close(host(dq), rq[0])
+    assert_f32_close(host(dk), rk[0])
+
+
+def test_gdn_norm_gate_config_c4b(oracle):
+    c = synth.c4_norm_gate()
+    got = host(ops.gdn_norm_gate_rows(dev(c["x"]), dev(c["z"]), dev(c["w"]), eps=c["eps"]))
+    assert_f32_close(got, oracle.norm_gate_rows(c["x"], c["z"], c["w"], c["eps"], threads=THREADS), what="C4b")
+
+
+@pytest.mark.parametrize("shape", [(1, 32, 128), (3, 7, 64), (5, 3, 256), (2, 4, 100)])
+def test_gdn_norm_gate_shapes(oracle, shape):
+    r = rng(sum(shape))
+    x, z = r.standard_normal(shape).astype(F32), r.standard_normal(shape).astype(F32)
+    w = (1 + 0.1 * r.standard_normal(shape[-1])).astype(F32)
+    got = host(ops.gdn_norm_gate_rows(dev(x), dev(z), dev(w)))
+    assert_f32_close(got, oracle.norm_gate_rows(x, z, w), what="norm_gate")
+
+
+# ------------------------------------------------------------------ MoE
+def test_swiglu_config_c3b(oracle):
+    c = synth.c3_swiglu()
+    got = host(ops.swiglu_bf16(dev(c["g"]), dev(c["u"])))
+    assert_bf16_close(got, oracle.swiglu_bf16(c["g"], c["u"], threads=THREADS), what="C3b")
+
+
+def test_shared_swiglu_config_c3c(oracle):
+    c = synth.c3_shared()
+    got = host(ops.shared_swiglu_sigmoid_rows_bf16(dev(c["g"]), dev(c["u"]), dev(c["logits"])))
+    assert_bf16_close(got, oracle.shared_swiglu_sigmoid_bf16(c["g"], c["u"], c["logits"]), what="C3c")
+
+
+def test_swiglu_exhaustive_and_odd(oracle):
+    g = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    u = np.full_like(g, 0x3F80)
+    assert_bf16_close(host(ops.swiglu_bf16(dev(g), dev(u))), oracle.swiglu_bf16(g, u), what="all bf16 g")
+    r = rng(4)
+    g2 = synth.to_bf16_bits(2 * r.standard_normal((3, 37)).astype(F32))
+    u2 = synth.to_bf16_bits(2 * r.standard_normal((3, 37)).astype(F32))
+    lg = r.standard_normal(3).astype(F32)
+    assert_bf16_close(host(ops.swiglu_bf16(dev(g2), dev(u2))), oracle.swiglu_bf16(g2, u2))
+    assert_bf16_close(host(ops.shared_swiglu_sigmoid_rows_bf16(dev(g2), dev(u2), dev(lg))),
+                      oracle.shared_swiglu_sigmoid_bf16(g2, u2, lg))
+
+
+@pytest.mark.parametrize("n", [512, 2047, 1 << 20])
+def test_moe_silu_mul(oracle, n):
+    r = rng(n)
+    g, u = (2 * r.standard_normal(n)).astype(F32), (2 * r.standard_normal(n)).astype(F32)
+    assert_f32_close(host(ops.moe_silu_mul(dev(g), dev(u))), oracle.silu_mul(g, u))
+
+
+@pytest.mark.parametrize("rows,n", [(1, 2048), (4096, 2048), (3, 1001)])
+def test_moe_shared_add(oracle, rows, n):
+    r = rng(rows + n)
+    acc, x = r.standard_normal((rows, n)).astype(F32), r.standard_normal((rows, n)).astype(F32)
+    gate = r.standard_normal(rows).astype(F32)
+    got = host(ops.moe_shared_add_rows(dev(acc), dev(x), dev(gate)))
+    assert_f32_close(got, oracle.shared_add_rows(acc, x, gate), group=n)
+
+
+# ------------------------------------------------------------------ dequant gather
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
+def test_gather_config_c5(oracle, kind):
+    vocab, cols = 248320, 2048
+    table = synth.q4k_table(vocab, cols) if kind == "Q4_K" else synth.q6k_table(vocab, cols)
+    ids = synth.token_ids(8192, vocab)
+    t = ops.GGML_TYPES[kind]
+    got = host(ops.dequant_gather_rows(dev(table), kind, vocab * cols, dev(ids), cols))
+    assert_bits_equal(got, oracle.dequant_gather(table, t, ids, cols, threads=THREADS), f"C5 {kind}")
+
+
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K", "Q4_0", "Q5_0", "Q8_0", "Q5_K", "F16", "BF16", "F32"])
+@pytest.mark.parametrize("cols", [2048, 768, 256])
+def test_gather_types(oracle, kind, cols):
+    import ggml_blocks
+
+    t = ops.GGML_TYPES[kind]
+    r = rng(t * 1000 + cols)
+    vocab = 300
+    if t in ggml_blocks.BLOCK:
+        elems = ggml_blocks.BLOCK[t][0]
+        table = ggml_blocks.random_blocks(r, t, vocab * cols // elems)
+    else:
+        width = 4 if kind == "F32" else 2
+        table = r.integers(0, 256, size=vocab * cols * width, dtype=np.uint8)
+        if kind != "BF16":  # keep floats finite
+            table = (r.standard_normal(vocab * cols).astype(np.float32 if kind == "F32" else np.float16)).view(np.uint8)
+    ids = r.integers(0, vocab, size=77).astype(np.int32)
+    got = host(ops.dequant_gather_rows(dev(table), t, vocab * cols, dev(ids), cols))
+    ref = oracle.dequant_gather(table, t, ids, cols)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert_bits_equal(np.where(nan, 0, got), np.where(nan, 0, ref), f"{kind} cols {cols}")
+
+
+def test_gather_out_of_range_ids_give_nan(oracle):
+    table = synth.q4k_table(16, 2048)
+    ids = np.array([3, -1, 16, 15, 1 << 30], dtype=np.int32)
+    got = host(ops.dequant_gather_rows(dev(table), "Q4_K", 16 * 2048, dev(ids), 2048))
+    assert np.isnan(got[[1, 2, 4]]).all()
+    assert_bits_equal(got[[0, 3]], oracle.dequant_gather(table, 12, ids[[0, 3]], 2048))
+
+
+@pytest.mark.parametrize("kind,cols,row", [("Q4_K", 2048, 5), ("Q6_K", 2048, 0), ("Q4_K", 100, 7), ("Q6_K", 300, 3),
+                                           ("Q8_0", 50, 9), ("F16", 33, 4)])
+def test_dequantize_row(oracle, kind, cols, row):
+    import ggml_blocks
+
+    t = ops.GGML_TYPES[kind]
+    r = rng(cols + row)
+    n_el = 16 * 2048
+    if t in ggml_blocks.BLOCK:
+        table = ggml_blocks.random_blocks(r, t, n_el // ggml_blocks.BLOCK[t][0])
+    else:
+        table = r.standard_normal(n_el).astype(np.float16).view(np.uint8)
+    got = host(ops.dequantize_row(dev(table), kind, n_el, row, cols))
+    assert_bits_equal(got, oracle.dequant_span(table, t, row * cols, cols), f"{kind} row {row}")
