@@ -12,17 +12,22 @@ inputs resident in HBM:
   C4b GDN gated per-head RMSNorm, fp32 [4096 x 32 x 128]
   C5  Q4_K and Q6_K embedding dequant-gather, 8192 ids from 248320 x 2048
 
-The timed region replays the step as one HIP graph (the nine launches with no
-host work between them), K times, bracketed by torch.cuda.synchronize();
-value = algorithmic bytes per step / wall time per step.
+Timed region (the contract): the step captured as one HIP graph (nine launches,
+no host work between them) replayed K times, bracketed by
+torch.cuda.synchronize(); value = algorithmic bytes per step / wall time per step.
+One step touches ~830 MB, more than the 256 MB MALL, so every call reads its
+inputs from HBM and pays for writing its outputs back.
 
-Per-kernel figures (the metric's "GB/s and us/call per kernel"): each kernel is
-timed on its own stream with HIP events around single launches, each launch
-preceded by a 512 MiB read of an unrelated buffer so that neither L2 nor the
-256 MB MALL holds the kernel's inputs (a cold, HBM-bound call), and a spin
-kernel ahead of each batch so all launches are queued before the GPU reaches
-them. Algorithmic bytes count every input read once and every output written
-once. The roofline object reports the kernel with the largest time per step.
+Per-kernel figures (the metric's "GB/s and us/call per kernel"), steady state:
+each kernel gets enough copies of its buffers that consecutive launches touch
+>= 1 GiB of distinct memory (4x the MALL); the rotating launches are captured in
+a graph and timed with HIP events around R replays on the launching stream;
+us/call = elapsed / launches. The same measurement of a plain 16-byte-vector
+copy of the same byte count is reported beside each kernel as the box's
+practical ceiling. Algorithmic bytes count every input read once and every
+output written once. The roofline object reports the kernel with the largest
+time per step; its "traffic" comes from the committed rocprofv3 counter runs
+(profiles/traffic.json) when present.
 
 CPU baseline: the oracle (oracle/liboracle.so, a C++ restatement of the
 reference kernels) timed on this host on a bounded sample of each config.
@@ -31,9 +36,9 @@ reference kernels) timed on this host on a bounded sample of each config.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
-import statistics
 import sys
 import time
 from pathlib import Path
@@ -45,19 +50,20 @@ sys.path.insert(0, str(ROOT / "qwen-3.5-cuda_amd"))
 
 METRIC = "achieved HBM GB/s (% of MI355X peak) + µs/call per fused norm/RoPE/act kernel"
 PEAK_GBPS = 8000.0  # MI355X HBM3E
-FLUSH_BYTES = 512 << 20
+ROTATE_BYTES = 1 << 30
 
 
 class Kernel:
-    def __init__(self, name, config, nbytes, launch, cpu=None):
-        self.name, self.config, self.bytes, self.launch, self.cpu = name, config, nbytes, launch, cpu
+    """A config: `make(i)` returns a launch closure bound to buffer set i
+    (set 0 = the base buffers; i > 0 = fresh copies)."""
+
+    def __init__(self, name, config, nbytes, footprint, make):
+        self.name, self.config, self.bytes, self.footprint, self.make = name, config, nbytes, footprint, make
         self.us = None
-        self.us_warm = None
+        self.copy_us = None
 
 
-def build_workload(torch, ops, synth, with_host: bool):
-    """Returns [Kernel] with device buffers bound into each launch closure, and
-    the host inputs needed by the CPU baseline."""
+def build_workload(torch, ops, synth):
     dev = torch.device("cuda:0")
 
     def d(a):
@@ -66,60 +72,90 @@ def build_workload(torch, ops, synth, with_host: bool):
             return torch.from_numpy(a.view(np.int16)).to(dev).view(torch.bfloat16)
         return torch.from_numpy(a).to(dev)
 
+    def cp(t, i):
+        return t if i == 0 else t.clone()
+
+    def new(t, i, keep):
+        return keep if i == 0 else torch.empty_like(t)
+
     ks: list[Kernel] = []
     host = {}
 
     c = synth.c1_rmsnorm()
-    x, w = d(c["x"]), d(c["w"])
-    out = torch.empty_like(x)
-    nb = 2 * x.numel() * 4 + w.numel() * 4
-    ks.append(Kernel("rmsnorm", "C1 f32 [36x2048]", nb, lambda x=x, w=w, out=out: ops.rmsnorm_rows(x, w, out)))
     host["rmsnorm"] = c
+    x1, w1 = d(c["x"]), d(c["w"])
+    o1 = torch.empty_like(x1)
+
+    def mk_rms(i, x=x1, w=w1, o=o1):
+        xx, oo = cp(x, i), new(o, i, o)
+        return lambda: ops.rmsnorm_rows(xx, w, oo)
+    nb = 2 * x1.numel() * 4 + w1.numel() * 4
+    ks.append(Kernel("rmsnorm", "C1 f32 [36x2048] eps 1e-6", nb, nb, mk_rms))
 
     c = synth.c2_qk_rope()
-    q, k, qw, kw, pos = d(c["q"]), d(c["k"]), d(c["qw"]), d(c["kw"]), d(c["pos"])
-    nb = 2 * (q.numel() + k.numel()) * 4 + (qw.numel() + kw.numel()) * 4 + pos.numel() * 4
-    ks.append(Kernel("qk_norm_rope", "C2 f32 Q[512x16x256] K[512x2x256] rd64 theta1e7", nb,
-                     lambda: ops.attn_qk_norm_rope_rows(q, k, qw, kw, pos=pos, rope_dim=64, theta=1e7)))
     host["qk_norm_rope"] = c
+    q2, k2, qw2, kw2, pos2 = d(c["q"]), d(c["k"]), d(c["qw"]), d(c["kw"]), d(c["pos"])
+
+    def mk_rope(i):
+        qq, kk = cp(q2, i), cp(k2, i)
+        return lambda: ops.attn_qk_norm_rope_rows(qq, kk, qw2, kw2, pos=pos2, rope_dim=64, theta=1e7)
+    nb = 2 * (q2.numel() + k2.numel()) * 4 + (qw2.numel() + kw2.numel()) * 4 + pos2.numel() * 4
+    ks.append(Kernel("qk_norm_rope", "C2 f32 Q[512x16x256] K[512x2x256] rope 64 theta 1e7", nb, nb, mk_rope))
 
     c = synth.c3_residual()
-    xr, br, wr = d(c["x"]), d(c["branch"]), d(c["w"])
-    resid, normed = torch.empty_like(xr), torch.empty_like(xr)
-    nb = 4 * xr.numel() * 2 + wr.numel() * 4
-    ks.append(Kernel("residual_rmsnorm_bf16", "C3a bf16 [4096x2048]", nb,
-                     lambda: ops.residual_rmsnorm_rows(xr, br, wr, resid, normed)))
     host["residual_rmsnorm_bf16"] = c
+    x3, b3, w3 = d(c["x"]), d(c["branch"]), d(c["w"])
+    r3, n3 = torch.empty_like(x3), torch.empty_like(x3)
+
+    def mk_res(i):
+        xx, bb, rr, nn = cp(x3, i), cp(b3, i), new(r3, i, r3), new(n3, i, n3)
+        return lambda: ops.residual_rmsnorm_rows(xx, bb, w3, rr, nn)
+    nb = 4 * x3.numel() * 2 + w3.numel() * 4
+    ks.append(Kernel("residual_rmsnorm_bf16", "C3a bf16 [4096x2048]", nb, nb, mk_res))
 
     c = synth.c3_swiglu()
-    g, u = d(c["g"]), d(c["u"])
-    h = torch.empty_like(g)
-    nb = 3 * g.numel() * 2
-    ks.append(Kernel("swiglu_bf16", "C3b bf16 [4096x8x512]", nb, lambda: ops.swiglu_bf16(g, u, h)))
     host["swiglu_bf16"] = c
+    g4, u4 = d(c["g"]), d(c["u"])
+    h4 = torch.empty_like(g4)
+
+    def mk_sw(i):
+        gg, uu, hh = cp(g4, i), cp(u4, i), new(h4, i, h4)
+        return lambda: ops.swiglu_bf16(gg, uu, hh)
+    nb = 3 * g4.numel() * 2
+    ks.append(Kernel("swiglu_bf16", "C3b bf16 [4096x8x512]", nb, nb, mk_sw))
 
     c = synth.c3_shared()
-    gs, us_, lg = d(c["g"]), d(c["u"]), d(c["logits"])
-    hs = torch.empty_like(gs)
-    nb = 3 * gs.numel() * 2 + lg.numel() * 4
-    ks.append(Kernel("shared_swiglu_sigmoid_bf16", "C3c bf16 [4096x512] + logits", nb,
-                     lambda: ops.shared_swiglu_sigmoid_rows_bf16(gs, us_, lg, hs)))
     host["shared_swiglu_sigmoid_bf16"] = c
+    g5, u5, l5 = d(c["g"]), d(c["u"]), d(c["logits"])
+    h5 = torch.empty_like(g5)
+
+    def mk_sh(i):
+        gg, uu, ll, hh = cp(g5, i), cp(u5, i), cp(l5, i), new(h5, i, h5)
+        return lambda: ops.shared_swiglu_sigmoid_rows_bf16(gg, uu, ll, hh)
+    nb = 3 * g5.numel() * 2 + l5.numel() * 4
+    ks.append(Kernel("shared_swiglu_sigmoid_bf16", "C3c bf16 [4096x512] + logits [4096]", nb, nb, mk_sh))
 
     c = synth.c4_frontend()
-    xc, wc, hin = d(c["x"]), d(c["w"]), d(c["hist"])
-    hout, yc = torch.empty_like(hin), torch.empty_like(xc)
-    nb = 2 * xc.numel() * 4 + wc.numel() * 4 + 2 * hin.numel() * 4
-    ks.append(Kernel("gdn_frontend", "C4a f32 [4096x8192] k4, 16 key heads x128", nb,
-                     lambda: ops.gdn_frontend_rows(xc, wc, hin, hout, yc, k_heads=16, key_dim=128)))
     host["gdn_frontend"] = c
+    x6, w6, hi6 = d(c["x"]), d(c["w"]), d(c["hist"])
+    ho6, y6 = torch.empty_like(hi6), torch.empty_like(x6)
+
+    def mk_fe(i):
+        xx, hi, ho, yy = cp(x6, i), cp(hi6, i), new(ho6, i, ho6), new(y6, i, y6)
+        return lambda: ops.gdn_frontend_rows(xx, w6, hi, ho, yy, k_heads=16, key_dim=128)
+    nb = 2 * x6.numel() * 4 + w6.numel() * 4 + 2 * hi6.numel() * 4
+    ks.append(Kernel("gdn_frontend", "C4a f32 [4096x8192] kernel 4, 16 key heads x 128", nb, nb, mk_fe))
 
     c = synth.c4_norm_gate()
-    xg, zg, wg = d(c["x"]), d(c["z"]), d(c["w"])
-    og = torch.empty_like(xg)
-    nb = 3 * xg.numel() * 4 + wg.numel() * 4
-    ks.append(Kernel("gdn_norm_gate", "C4b f32 [4096x32x128]", nb, lambda: ops.gdn_norm_gate_rows(xg, zg, wg, og)))
     host["gdn_norm_gate"] = c
+    x7, z7, w7 = d(c["x"]), d(c["z"]), d(c["w"])
+    o7 = torch.empty_like(x7)
+
+    def mk_ng(i):
+        xx, zz, oo = cp(x7, i), cp(z7, i), new(o7, i, o7)
+        return lambda: ops.gdn_norm_gate_rows(xx, zz, w7, oo)
+    nb = 3 * x7.numel() * 4 + w7.numel() * 4
+    ks.append(Kernel("gdn_norm_gate", "C4b f32 [4096x32x128]", nb, nb, mk_ng))
 
     vocab, cols = 248320, 2048
     ids_h = synth.token_ids(8192, vocab)
@@ -127,12 +163,15 @@ def build_workload(torch, ops, synth, with_host: bool):
     for kind, make, bpr in (("Q4_K", synth.q4k_table, 1152), ("Q6_K", synth.q6k_table, 1680)):
         tab_h = make(vocab, cols)
         tab = d(tab_h)
-        o = torch.empty((8192, cols), dtype=torch.float32, device=dev)
-        nb = 8192 * bpr + ids.numel() * 4 + o.numel() * 4
+        out = torch.empty((8192, cols), dtype=torch.float32, device=dev)
         name = f"dequant_gather_{kind.lower()}"
-        ks.append(Kernel(name, f"C5 {kind} 248320x2048, 8192 ids", nb,
-                         lambda tab=tab, kind=kind, o=o: ops.dequant_gather_rows(tab, kind, vocab * cols, ids, cols, o)))
-        host[name] = {"table": tab_h if with_host else None, "ids": ids_h, "type": ops.GGML_TYPES[kind]}
+        host[name] = {"table": tab_h, "ids": ids_h, "type": ops.GGML_TYPES[kind]}
+
+        def mk_ga(i, tab=tab, kind=kind, out=out):
+            ii, oo = cp(ids, i), new(out, i, out)
+            return lambda: ops.dequant_gather_rows(tab, kind, vocab * cols, ii, cols, oo)
+        nb = 8192 * bpr + ids.numel() * 4 + out.numel() * 4
+        ks.append(Kernel(name, f"C5 {kind} table 248320x2048, 8192 ids -> f32", nb, nb, mk_ga))
     return ks, host
 
 
@@ -146,44 +185,80 @@ def spin_cycles_per_ms(torch) -> float:
     return 2_000_000 / max(s.elapsed_time(e), 1e-3)
 
 
-def time_kernel(torch, k: Kernel, flush, spin, reps: int, batch: int, cold: bool) -> float:
-    """Median event-timed duration (us) of single launches of k."""
-    times = []
-    done = 0
-    while done < reps:
-        n = min(batch, reps - done)
-        torch.cuda._sleep(spin)
-        evs = []
-        for _ in range(n):
-            if cold:
-                flush()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            k.launch()
-            e1.record()
-            evs.append((e0, e1))
-        torch.cuda.synchronize()
-        times += [a.elapsed_time(b) * 1e3 for a, b in evs]
-        done += n
-    return statistics.median(times)
+def steady_state_us(torch, launches, replays: int, spin: int) -> float:
+    """us per launch of `launches` (one per buffer set), captured as one graph
+    and replayed; events bracket all replays on the capturing stream."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for f in launches:
+            f()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in launches:
+            f()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(spin)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (replays * len(launches))
+    del g
+    return us
+
+
+def n_sets(footprint: int) -> int:
+    return max(2, min(2048, -(-ROTATE_BYTES // footprint)))
+
+
+def measure_kernel(torch, k: Kernel, spin: int, min_launches: int) -> float:
+    sets = n_sets(k.footprint)
+    launches = [k.make(i) for i in range(sets)]
+    replays = max(1, -(-min_launches // sets))
+    us = steady_state_us(torch, launches, replays, spin)
+    del launches
+    torch.cuda.empty_cache()
+    return us
+
+
+def measure_copy(torch, bench_lib, nbytes: int, spin: int, min_launches: int) -> float:
+    half = (nbytes // 2 + 15) // 16 * 16
+    sets = n_sets(2 * half)
+    bufs = [(torch.empty(half, dtype=torch.uint8, device="cuda:0"), torch.empty(half, dtype=torch.uint8, device="cuda:0"))
+            for _ in range(sets)]
+
+    def launcher(src, dst):
+        def f():
+            rc = bench_lib.qwen_bench_copy(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), half,
+                                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            if rc:
+                raise RuntimeError("qwen_bench_copy failed")
+        return f
+    us = steady_state_us(torch, [launcher(s, d) for s, d in bufs], max(1, -(-min_launches // sets)), spin)
+    del bufs
+    torch.cuda.empty_cache()
+    return us
 
 
 def cpu_baseline(host, kernels, threads: int, budget_s: float):
     """Times the oracle on a bounded sample of every config; returns per-kernel
-    (GB/s, sample description) and the aggregate."""
+    results and the aggregate GB/s (full-step bytes / extrapolated full-step time)."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import pyoracle as orc
 
     orc.lib()
-    by = {k.name: k for k in kernels}
-    frac_rows = {  # sample size per config
-        "rmsnorm": 36, "qk_norm_rope": 64, "residual_rmsnorm_bf16": 512, "swiglu_bf16": 512,
-        "shared_swiglu_sigmoid_bf16": 4096, "gdn_frontend": 256, "gdn_norm_gate": 512,
-        "dequant_gather_q4_k": 1024, "dequant_gather_q6_k": 1024,
-    }
-    full_rows = {"rmsnorm": 36, "qk_norm_rope": 512, "residual_rmsnorm_bf16": 4096, "swiglu_bf16": 4096,
-                 "shared_swiglu_sigmoid_bf16": 4096, "gdn_frontend": 4096, "gdn_norm_gate": 4096,
-                 "dequant_gather_q4_k": 8192, "dequant_gather_q6_k": 8192}
+    sample = {"rmsnorm": 36, "qk_norm_rope": 64, "residual_rmsnorm_bf16": 512, "swiglu_bf16": 512,
+              "shared_swiglu_sigmoid_bf16": 4096, "gdn_frontend": 256, "gdn_norm_gate": 512,
+              "dequant_gather_q4_k": 1024, "dequant_gather_q6_k": 1024}
+    full = {"rmsnorm": 36, "qk_norm_rope": 512, "residual_rmsnorm_bf16": 4096, "swiglu_bf16": 4096,
+            "shared_swiglu_sigmoid_bf16": 4096, "gdn_frontend": 4096, "gdn_norm_gate": 4096,
+            "dequant_gather_q4_k": 8192, "dequant_gather_q6_k": 8192}
 
     def runner(name, rows, th):
         c = host[name]
@@ -205,25 +280,23 @@ def cpu_baseline(host, kernels, threads: int, budget_s: float):
         return lambda: orc.dequant_gather(c["table"], c["type"], c["ids"][:rows], 2048, threads=th)
 
     per, tot_b, tot_t = {}, 0.0, 0.0
-    per_budget = budget_s / len(by)
-    for name, k in by.items():
-        rows = frac_rows[name]
-        fn = runner(name, rows, threads)
-        fn()  # warm
+    budget = budget_s / len(kernels)
+    for k in kernels:
+        rows = sample[k.name]
+        fn = runner(k.name, rows, threads)
+        fn()
         t0 = time.perf_counter()
         n = 0
         while True:
             fn()
             n += 1
             el = time.perf_counter() - t0
-            if el > per_budget or n >= 200:
+            if el > budget or n >= 200:
                 break
-        sec = el / n
-        b = k.bytes * rows / full_rows[name]
-        per[name] = {"gbps": b / sec / 1e9, "us_per_call_full": sec * full_rows[name] / rows * 1e6,
-                     "sample_rows": rows}
+        sec_full = el / n * full[k.name] / rows
+        per[k.name] = {"gbps": k.bytes / sec_full / 1e9, "us_per_call": sec_full * 1e6, "sample_rows": rows}
         tot_b += k.bytes
-        tot_t += sec * full_rows[name] / rows
+        tot_t += sec_full
     return per, tot_b / tot_t / 1e9
 
 
@@ -238,111 +311,105 @@ def cpu_model() -> str:
 
 
 def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap = argparse.ArgumentParser(description="Fused per-layer kernels on one MI355X")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--reps", type=int, default=40, help="event-timed launches per kernel")
-    ap.add_argument("--kernels", default="", help="comma list: only these kernels (profiling)")
+    ap.add_argument("--launches", type=int, default=64, help="min launches per kernel for the per-kernel timing")
+    ap.add_argument("--kernels", default="", help="comma list: only these kernels (profiling runs)")
+    ap.add_argument("--no-per-kernel", action="store_true", help="skip the per-kernel and copy measurements")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
-    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph replay")
     ap.add_argument("--json-out", default="", help="also write the JSON line to this file")
     args = ap.parse_args()
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(every kernel is row-local and the multi-GPU path is not built)", file=sys.stderr)
+              "(every kernel is row-local; the multi-GPU path is not built)", file=sys.stderr)
         return 2
 
     import torch
 
-    from qwen35_hip import load, ops, synth
+    from qwen35_hip import PACKAGE_DIR, load, ops, synth
 
     load()  # fail loudly if the HIP library is missing
+    bench_lib = ctypes.CDLL(str(PACKAGE_DIR / "libqwen35_benchutil.so"))
+    bench_lib.qwen_bench_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
     torch.cuda.set_device(0)
     t_setup = time.perf_counter()
-    kernels, host = build_workload(torch, ops, synth, with_host=not args.no_cpu)
+    kernels, host = build_workload(torch, ops, synth)
     if args.kernels:
         keep = set(args.kernels.split(","))
         kernels = [k for k in kernels if k.name in keep]
     torch.cuda.synchronize()
     print(f"# setup {time.perf_counter() - t_setup:.1f}s, {len(kernels)} kernels", file=sys.stderr, flush=True)
+    spin = int(spin_cycles_per_ms(torch) * 2.0)
 
-    flush_buf = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device="cuda:0")
-    flush_out = torch.empty((), dtype=torch.float32, device="cuda:0")
-
-    def flush():
-        torch.sum(flush_buf, dtype=torch.float32, out=flush_out)
-
-    spin = int(spin_cycles_per_ms(torch) * 4.0)  # ~4 ms of spin ahead of each batch
-
-    for k in kernels:  # warm-up: first launches load code objects
-        k.launch()
+    # ---- the step: K graph replays (the contract)
+    base = [k.make(0) for k in kernels]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for f in base:
+            f()
+    torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-
-    # ---- per-kernel cold-cache timing
-    for k in kernels:
-        k.us = time_kernel(torch, k, flush, spin, args.reps, 10, cold=True)
-        k.us_warm = time_kernel(torch, k, flush, spin, max(args.reps // 2, 5), 20, cold=False)
-        print(f"# {k.name:28s} {k.us:9.2f} us cold ({k.bytes / k.us / 1e3:7.1f} GB/s, "
-              f"{k.bytes / k.us / 1e3 / PEAK_GBPS:6.1%}), {k.us_warm:9.2f} us warm", file=sys.stderr, flush=True)
-
-    # ---- timed steps (the contract): K graph replays of the whole step
-    graph = None
-    if not args.eager:
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            for k in kernels:
-                k.launch()
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for k in kernels:
-                k.launch()
-
-    def step():
-        if graph is not None:
-            graph.replay()
-        else:
-            for k in kernels:
-                k.launch()
-
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for f in base:
+            f()
     for _ in range(args.warmup):
-        step()
+        graph.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        graph.replay()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall / args.steps * 1e3
     bytes_step = sum(k.bytes for k in kernels)
     value = bytes_step / (ms_per_step * 1e-3) / 1e9
     print(f"# step: {ms_per_step * 1e3:.1f} us, {value:.1f} GB/s aggregate", file=sys.stderr, flush=True)
+    del graph
+
+    # ---- per-kernel steady state and the copy ceiling at the same bytes
+    if not args.no_per_kernel:
+        for k in kernels:
+            k.us = measure_kernel(torch, k, spin, args.launches)
+            k.copy_us = measure_copy(torch, bench_lib, k.bytes, spin, args.launches)
+            print(f"# {k.name:28s} {k.us:9.2f} us  {k.bytes / k.us / 1e3:7.1f} GB/s ({k.bytes / k.us / 1e3 / PEAK_GBPS:6.1%})"
+                  f"   copy of same bytes {k.copy_us:8.2f} us {k.bytes / k.copy_us / 1e3:7.1f} GB/s",
+                  file=sys.stderr, flush=True)
+        big = 1 << 30
+        copy_big = measure_copy(torch, bench_lib, big, spin, 16)
+        print(f"# copy 1 GiB: {big / copy_big / 1e3:.1f} GB/s", file=sys.stderr, flush=True)
 
     # ---- roofline of the dominant kernel
-    dom = max(kernels, key=lambda k: k.us)
-    traffic = None
-    tf = ROOT / "profiles" / "traffic.json"
-    if tf.exists():
-        traffic = json.loads(tf.read_text()).get(dom.name, {}).get("bytes_per_launch")
-    roofline = {"kernel": dom.name, "bound": "hbm", "achieved": round(dom.bytes / dom.us / 1e3, 1),
-                "peak": PEAK_GBPS, "unit": "GB/s", "frac": round(dom.bytes / dom.us / 1e3 / PEAK_GBPS, 4),
-                "traffic": traffic, "algorithmic_bytes": dom.bytes, "us_per_call": round(dom.us, 3)}
+    roofline = None
+    if not args.no_per_kernel:
+        dom = max(kernels, key=lambda k: k.us)
+        traffic = None
+        tf = ROOT / "profiles" / "traffic.json"
+        if tf.exists():
+            traffic = json.loads(tf.read_text()).get(dom.name, {}).get("bytes_per_launch")
+        roofline = {"kernel": dom.name, "bound": "hbm", "achieved": round(dom.bytes / dom.us / 1e3, 1),
+                    "peak": PEAK_GBPS, "unit": "GB/s", "frac": round(dom.bytes / dom.us / 1e3 / PEAK_GBPS, 4),
+                    "traffic": traffic, "algorithmic_bytes": dom.bytes, "us_per_call": round(dom.us, 3),
+                    "copy_same_bytes_gbps": round(dom.bytes / dom.copy_us / 1e3, 1),
+                    "copy_1gib_gbps": round(big / copy_big / 1e3, 1)}
 
     # ---- CPU baseline
     cpu = None
     if not args.no_cpu and not args.kernels:
         threads = max(1, min(16, os.cpu_count() or 1))
         per, agg = cpu_baseline(host, kernels, threads, args.cpu_seconds)
+        rows_desc = ", ".join(f"{n} {p['sample_rows']}" for n, p in per.items())
         cpu = {"value": round(agg, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-               "sample": ("oracle/liboracle.so (C++ restatement of the reference kernels, -O2) on the first rows "
-                          "of each config: " + ", ".join(f"{n} {p['sample_rows']}" for n, p in per.items())
-                          + f"; row-parallel std::threads; host CPU {cpu_model()}"),
-               "per_kernel_gbps": {n: round(p["gbps"], 3) for n, p in per.items()}}
+               "sample": ("oracle/liboracle.so (C++ restatement of the reference kernels, -O2, row-parallel "
+                          "std::threads) on the first rows of each config (" + rows_desc + "), "
+                          f"extrapolated to the full step; host CPU {cpu_model()}"),
+               "per_kernel": {n: {"gbps": round(p["gbps"], 3), "us_per_call": round(p["us_per_call"], 1)}
+                              for n, p in per.items()}}
 
     line = {
         "metric": METRIC,
@@ -357,14 +424,13 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: splitmix64 + Box-Muller inputs, seeds 0x5EED0000+k, BASELINE.json configs C1-C5",
-        "config": {"workload": "one call of each of the 9 fused kernels at BASELINE configs C1-C5 "
-                               "(HIP graph replay; storage f32/bf16/Q4_K/Q6_K, math f32)",
-                   "bytes_per_step": bytes_step, "parallelism": "single GPU",
-                   "graph": graph is not None},
-        "kernels": {k.name: {"config": k.config, "bytes": k.bytes, "us_per_call": round(k.us, 3),
-                             "gbps": round(k.bytes / k.us / 1e3, 1),
-                             "frac_peak": round(k.bytes / k.us / 1e3 / PEAK_GBPS, 4),
-                             "us_per_call_warm_cache": round(k.us_warm, 3)} for k in kernels},
+        "config": {"workload": "one call of each of the 9 fused kernels at BASELINE configs C1-C5 as one HIP graph "
+                               "(storage f32/bf16/Q4_K/Q6_K, math f32)",
+                   "bytes_per_step": bytes_step, "parallelism": "single GPU"},
+        "kernels": None if args.no_per_kernel else {
+            k.name: {"config": k.config, "bytes": k.bytes, "us_per_call": round(k.us, 3),
+                     "gbps": round(k.bytes / k.us / 1e3, 1), "frac_peak": round(k.bytes / k.us / 1e3 / PEAK_GBPS, 4),
+                     "copy_same_bytes_us": round(k.copy_us, 3)} for k in kernels},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

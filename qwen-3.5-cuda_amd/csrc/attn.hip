@@ -62,25 +62,26 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_v4(float* __restrict__ q,
     if (wave * HPW >= total) return;  // wave-uniform
     const int64_t slot = wave * HPW + lane / LPH;
     const bool active = slot < total;
+    const int64_t sl = active ? slot : total - 1;  // clamped: loads never branch
+    const int t = static_cast<int>(sl / hpr);
+    const int h = static_cast<int>(sl % hpr);
+    float* p = (h < q_heads) ? q + (static_cast<size_t>(t) * q_heads + h) * HD
+                             : k + (static_cast<size_t>(t) * k_heads + (h - q_heads)) * HD;
+    const float* wt = (h < q_heads) ? qw : kw;
+    const int half = rope_dim >> 1;
 
-    int t = 0;
-    float* p = nullptr;
-    const float* wt = nullptr;
-    if (active) {
-        t = static_cast<int>(slot / hpr);
-        const int h = static_cast<int>(slot % hpr);
-        if (h < q_heads) {
-            p = q + (static_cast<size_t>(t) * q_heads + h) * HD;
-            wt = qw;
-        } else {
-            p = k + (static_cast<size_t>(t) * k_heads + (h - q_heads)) * HD;
-            wt = kw;
-        }
+    // Rotation angles of this group's head: pairs lg and lg + LPH. They do not
+    // depend on x, so they are computed while the row is in flight.
+    float c0 = 1.f, s0 = 0.f, c1 = 1.f, s1 = 0.f;
+    if constexpr (ROPE) {
+        const float fp = static_cast<float>(pos ? pos[t] : pos0 + t);
+        if (lg < half) sincosf(fp / den.den[lg], &s0, &c0);
+        if (lg + LPH < half) sincosf(fp / den.den[lg + LPH], &s1, &c1);
     }
-    float4 v = active ? ld4(p + 4 * lg) : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 v = ld4_nt(p + 4 * lg);
 
     if constexpr (NORM) {
-        const float4 wv = active ? ld4(wt + 4 * lg) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 wv = ld4(wt + 4 * lg);
         const float ss = group_sum<LPH>(sumsq4(v));
         const float r = rsqrtf(ss / static_cast<float>(HD) + eps);
         v.x = v.x * (r * wv.x);
@@ -90,17 +91,9 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_v4(float* __restrict__ q,
     }
 
     if constexpr (ROPE) {
-        const int half = rope_dim >> 1;
-        const int pp = active ? (pos ? pos[t] : pos0 + t) : 0;
-        const float fp = static_cast<float>(pp);
-        // Angles of pairs lg and lg + LPH of this group's head.
-        float c0 = 1.f, s0 = 0.f, c1 = 1.f, s1 = 0.f;
-        if (lg < half) sincosf(fp / den.den[lg], &s0, &c0);
-        if (lg + LPH < half) sincosf(fp / den.den[lg + LPH], &s1, &c1);
-
         const int d0 = 4 * lg;
-        const bool first = d0 < half;                     // dims i..i+3, partner i+half
-        const bool second = !first && d0 < rope_dim;      // dims i+half.., partner i
+        const bool first = d0 < half;                 // dims i..i+3, partner i+half
+        const bool second = !first && d0 < rope_dim;  // dims i+half.., partner i
         const int plg = first ? lg + (half >> 2) : (second ? lg - (half >> 2) : lg);
         const int src = gbase + plg;
         float4 pv;
@@ -113,8 +106,7 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_v4(float* __restrict__ q,
         float cs[4], sn[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int i = i0 + j;
-            const int from = gbase + (i % LPH);
+            const int from = gbase + ((i0 + j) % LPH);
             cs[j] = lane_fetch(c0, from);
             sn[j] = lane_fetch(s0, from);
         }
@@ -144,7 +136,7 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_v4(float* __restrict__ q,
         }
         v = make_float4(o[0], o[1], o[2], o[3]);
     }
-    if (active) st4(p + 4 * lg, v);
+    if (active) st4_nt(p + 4 * lg, v);
 }
 
 // ------------------------------------------------------------ generic kernels

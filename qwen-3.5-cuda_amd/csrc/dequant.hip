@@ -160,13 +160,13 @@ __device__ __forceinline__ int stage_row(const uint8_t* __restrict__ table, int6
     const int off = static_cast<int>(start - a);
     const int chunks = (off + row_bytes + 15) >> 4;
     const uint4* src = reinterpret_cast<const uint4*>(table + a);
-    for (int j = lane; j < chunks; j += kWave) slot[j] = src[j];
+    for (int j = lane; j < chunks; j += kWave) slot[j] = ld16_nt(src + j);
     return off;
 }
 
 __device__ __forceinline__ void fill_nan(float* orow, int nb, int lane) {
     const float q = __builtin_nanf("");
-    for (int k = 0; k < nb; ++k) st4(orow + k * 256 + 4 * lane, make_float4(q, q, q, q));
+    for (int k = 0; k < nb; ++k) st4_nt(orow + k * 256 + 4 * lane, make_float4(q, q, q, q));
 }
 
 // Q4_K: 144-byte blocks = d, dmin (fp16), scales[12], qs[128]. Rows are whole
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(kBlock) void gather_q4k(const uint8_t* __restrict__
         o.y = A * static_cast<float>(byte_of(nib, 1)) - B;
         o.z = A * static_cast<float>(byte_of(nib, 2)) - B;
         o.w = A * static_cast<float>(byte_of(nib, 3)) - B;
-        st4(orow + k * 256 + 4 * lane, o);
+        st4_nt(orow + k * 256 + 4 * lane, o);
     }
 }
 
@@ -269,7 +269,7 @@ __global__ __launch_bounds__(kBlock) void gather_q6k(const uint8_t* __restrict__
         o.y = A * static_cast<float>(static_cast<int>(byte_of(q, 1)) - 32);
         o.z = A * static_cast<float>(static_cast<int>(byte_of(q, 2)) - 32);
         o.w = A * static_cast<float>(static_cast<int>(byte_of(q, 3)) - 32);
-        st4(orow + k * 256 + 4 * lane, o);
+        st4_nt(orow + k * 256 + 4 * lane, o);
     }
 }
 

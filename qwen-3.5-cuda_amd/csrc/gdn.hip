@@ -43,11 +43,16 @@ __device__ __forceinline__ float conv4(float h0, float h1, float h2, float xv, f
 }
 
 // ---------------------------------------------------- front end, kernel size 4
+// Wave = 256 channels (float4 per lane) x kConvTile tokens. The token loop is
+// software-pipelined: the next kConvUnroll rows are in flight while the current
+// ones are convolved, normalised and stored. Lanes past the last channel
+// address a clamped channel and skip their stores, so loads never branch.
 template <int LPH>
 __global__ __launch_bounds__(kBlock) void gdn_frontend_k4(const float* __restrict__ x, const float* __restrict__ w,
                                                           const float* hist_in, float* hist_out, float* __restrict__ y,
                                                           int rows, int C, int q_ch, int qk_ch, float eps, float qscale,
                                                           int n_ctiles, int n_ttiles) {
+    constexpr int U = kConvUnroll;
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * (kBlock / kWave) + (threadIdx.x >> 6);
     if (wave >= n_ctiles * n_ttiles) return;  // wave-uniform
@@ -56,45 +61,51 @@ __global__ __launch_bounds__(kBlock) void gdn_frontend_k4(const float* __restric
     const int t1 = min(t0 + kConvTile, rows);
     const int c = cbase + 4 * lane;
     const bool on = c < C;
+    const int cc = on ? c : C - 4;         // clamped channel for addressing
     const bool norm_wave = cbase < qk_ch;  // wave-uniform
     const bool is_q = c < q_ch;
     const bool is_qk = c < qk_ch;
 
-    float4 w0 = make_float4(0.f, 0.f, 0.f, 0.f), w1 = w0, w2 = w0, w3 = w0;  // taps of channels c..c+3
-    float4 h0 = w0, h1 = w0, h2 = w0;                                         // x[t-3], x[t-2], x[t-1]
-    if (on) {
-        w0 = ld4(w + 4 * static_cast<size_t>(c));
-        w1 = ld4(w + 4 * static_cast<size_t>(c) + 4);
-        w2 = ld4(w + 4 * static_cast<size_t>(c) + 8);
-        w3 = ld4(w + 4 * static_cast<size_t>(c) + 12);
-        if (t0 == 0) {
-            const float4 a = ld4(hist_in + 3 * static_cast<size_t>(c));
-            const float4 b = ld4(hist_in + 3 * static_cast<size_t>(c) + 4);
-            const float4 d = ld4(hist_in + 3 * static_cast<size_t>(c) + 8);
-            // [ch0: j0 j1 j2 | ch1: j0 j1 j2 | ch2 ... | ch3 ...]
-            h0 = make_float4(a.x, a.w, b.z, d.y);
-            h1 = make_float4(a.y, b.x, b.w, d.z);
-            h2 = make_float4(a.z, b.y, d.x, d.w);
-        } else {
-            h0 = ld4(x + static_cast<size_t>(t0 - 3) * C + c);
-            h1 = ld4(x + static_cast<size_t>(t0 - 2) * C + c);
-            h2 = ld4(x + static_cast<size_t>(t0 - 1) * C + c);
-        }
+    // taps of channels c..c+3, and the window x[t-3], x[t-2], x[t-1]
+    const float4 w0 = ld4(w + 4 * static_cast<size_t>(cc));
+    const float4 w1 = ld4(w + 4 * static_cast<size_t>(cc) + 4);
+    const float4 w2 = ld4(w + 4 * static_cast<size_t>(cc) + 8);
+    const float4 w3 = ld4(w + 4 * static_cast<size_t>(cc) + 12);
+    float4 h0, h1, h2;
+    if (t0 == 0) {
+        const float4 a = ld4(hist_in + 3 * static_cast<size_t>(cc));
+        const float4 b = ld4(hist_in + 3 * static_cast<size_t>(cc) + 4);
+        const float4 d = ld4(hist_in + 3 * static_cast<size_t>(cc) + 8);
+        // [ch0: j0 j1 j2 | ch1: j0 j1 j2 | ch2 ... | ch3 ...]
+        h0 = make_float4(a.x, a.w, b.z, d.y);
+        h1 = make_float4(a.y, b.x, b.w, d.z);
+        h2 = make_float4(a.z, b.y, d.x, d.w);
+    } else {
+        h0 = ld4(x + static_cast<size_t>(t0 - 3) * C + cc);
+        h1 = ld4(x + static_cast<size_t>(t0 - 2) * C + cc);
+        h2 = ld4(x + static_cast<size_t>(t0 - 1) * C + cc);
+    }
+    // Loads issue (and return) in order: the small reused operands above go
+    // first so the first row's math waits only for them and its own row.
+    auto xrow = [&](int t) { return x + static_cast<size_t>(min(t, t1 - 1)) * C + cc; };
+    float4 cur[U], nxt[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        cur[u] = ld4_nt(xrow(t0 + u));
+        nxt[u] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
 
-    for (int t = t0; t < t1; t += kConvUnroll) {
-        float4 xv[kConvUnroll];
+    for (int t = t0; t < t1; t += U) {
+        if (t + U < t1) {  // wave-uniform: prefetch the next rows
 #pragma unroll
-        for (int u = 0; u < kConvUnroll; ++u)
-            xv[u] = (on && t + u < t1) ? ld4(x + static_cast<size_t>(t + u) * C + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int u = 0; u < U; ++u) nxt[u] = ld4_nt(xrow(t + U + u));
+        }
 #pragma unroll
-        for (int u = 0; u < kConvUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
             if (t + u >= t1) break;  // wave-uniform
-            float4 v;
-            v.x = silu(conv4(h0.x, h1.x, h2.x, xv[u].x, w0));
-            v.y = silu(conv4(h0.y, h1.y, h2.y, xv[u].y, w1));
-            v.z = silu(conv4(h0.z, h1.z, h2.z, xv[u].z, w2));
-            v.w = silu(conv4(h0.w, h1.w, h2.w, xv[u].w, w3));
+            const float4 xv = cur[u];
+            float4 v = silu4(make_float4(conv4(h0.x, h1.x, h2.x, xv.x, w0), conv4(h0.y, h1.y, h2.y, xv.y, w1),
+                                         conv4(h0.z, h1.z, h2.z, xv.z, w2), conv4(h0.w, h1.w, h2.w, xv.w, w3)));
             if (norm_wave) {
                 const float ss = group_sum<LPH>(sumsq4(v));
                 const float r = rsqrtf(ss + eps);
@@ -106,11 +117,13 @@ __global__ __launch_bounds__(kBlock) void gdn_frontend_k4(const float* __restric
                     v.w *= sc;
                 }
             }
-            if (on) st4(y + static_cast<size_t>(t + u) * C + c, v);
+            if (on) st4_nt(y + static_cast<size_t>(t + u) * C + c, v);
             h0 = h1;
             h1 = h2;
-            h2 = xv[u];
+            h2 = xv;
         }
+#pragma unroll
+        for (int u = 0; u < U; ++u) cur[u] = nxt[u];
     }
 
     // The wave of the first time tile owns the history: it read hist_in first
@@ -200,6 +213,8 @@ __global__ __launch_bounds__(kBlock) void qk_l2_any(float* q, float* k, int64_t 
 }
 
 // ---------------------------------------------------- gated per-head RMSNorm
+// Lane groups of LPH lanes per head (dim = 4*LPH); a wave handles kGateUnroll
+// consecutive head groups with every x and z load issued before any math.
 template <int LPH>
 __global__ __launch_bounds__(kBlock) void norm_gate_v4(const float* __restrict__ x, const float* __restrict__ z,
                                                        const float* __restrict__ w, float* __restrict__ out,
@@ -215,22 +230,22 @@ __global__ __launch_bounds__(kBlock) void norm_gate_v4(const float* __restrict__
     float4 xv[kGateUnroll], zv[kGateUnroll];
 #pragma unroll
     for (int u = 0; u < kGateUnroll; ++u) {
-        const int64_t h = h_first + u * HPW + lane / LPH;
-        const bool act = h < heads_total;
-        xv[u] = act ? ld4(x + h * D + 4 * lg) : make_float4(0.f, 0.f, 0.f, 0.f);
-        zv[u] = act ? ld4(z + h * D + 4 * lg) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int64_t h = min(h_first + u * HPW + lane / LPH, heads_total - 1);
+        xv[u] = ld4_nt(x + h * D + 4 * lg);
+        zv[u] = ld4_nt(z + h * D + 4 * lg);
     }
 #pragma unroll
     for (int u = 0; u < kGateUnroll; ++u) {
         const int64_t h = h_first + u * HPW + lane / LPH;
         const float ss = group_sum<LPH>(sumsq4(xv[u]));
         const float r = rsqrtf(ss / static_cast<float>(D) + eps);
+        const float4 sz = silu4(zv[u]);
         float4 o;
-        o.x = xv[u].x * r * wv.x * silu(zv[u].x);
-        o.y = xv[u].y * r * wv.y * silu(zv[u].y);
-        o.z = xv[u].z * r * wv.z * silu(zv[u].z);
-        o.w = xv[u].w * r * wv.w * silu(zv[u].w);
-        if (h < heads_total) st4(out + h * D + 4 * lg, o);
+        o.x = xv[u].x * r * wv.x * sz.x;
+        o.y = xv[u].y * r * wv.y * sz.y;
+        o.z = xv[u].z * r * wv.z * sz.z;
+        o.w = xv[u].w * r * wv.w * sz.w;
+        if (h < heads_total) st4_nt(out + h * D + 4 * lg, o);
     }
 }
 
@@ -285,7 +300,10 @@ extern "C" {
 int qwen_gdn_frontend_rows(const float* x, const float* weight, const float* hist_in, float* hist_out, float* y,
                            int rows, int channels, int kernel, int k_heads, int key_dim, float eps, void* stream) {
     QK_REQUIRE(rows >= 0 && channels >= 0, "gdn_frontend: negative size (rows=%d, channels=%d)", rows, channels);
-    QK_REQUIRE(kernel >= 2, "gdn_frontend: kernel size %d must be at least 2", kernel);
+    // kernel - 1 <= kConvTile keeps every history read inside the first time
+    // tile, whose thread alone writes hist_out (in-place safety).
+    QK_REQUIRE(kernel >= 2 && kernel <= kConvTile + 1, "gdn_frontend: kernel size %d outside [2, %d]", kernel,
+               kConvTile + 1);
     QK_REQUIRE(k_heads >= 0 && (k_heads == 0 || key_dim > 0), "gdn_frontend: bad k_heads %d / key_dim %d", k_heads,
                key_dim);
     QK_REQUIRE(static_cast<int64_t>(2) * k_heads * key_dim <= channels,

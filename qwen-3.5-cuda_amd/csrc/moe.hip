@@ -19,65 +19,62 @@ constexpr int kBlock = 256;
 constexpr int kUnroll = 4;  // 16-byte vectors in flight per thread
 
 // ------------------------------------------------------------ bf16 SwiGLU
-// Chunk i = 8 bf16 (16 bytes). Block b, step u covers chunks
-// (b*kUnroll + u)*kBlock + [0, kBlock): every load instruction is coalesced.
-__device__ __forceinline__ uint32_t swiglu_pair(uint32_t g, uint32_t u, float scale, bool scaled) {
-    float lo = silu(bf16_lo(g)) * bf16_lo(u);
-    float hi = silu(bf16_hi(g)) * bf16_hi(u);
-    if (scaled) {
-        lo *= scale;
-        hi *= scale;
+// Eight bf16 pairs (one 16-byte chunk of g and of u) -> eight bf16 outputs,
+// h = (silu(g) * u) [* scale], fp32 math, one rounding per output.
+template <bool SCALED>
+__device__ __forceinline__ uint4 swiglu8(uint4 g, uint4 u, float scale) {
+    const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
+    const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+    float s[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        s[2 * k] = bf16_lo(gw[k]);
+        s[2 * k + 1] = bf16_hi(gw[k]);
     }
-    return pack_bf16(lo, hi);
+    silu_n<8>(s);
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        float lo = s[2 * k] * bf16_lo(uw[k]);
+        float hi = s[2 * k + 1] * bf16_hi(uw[k]);
+        if (SCALED) {
+            lo *= scale;
+            hi *= scale;
+        }
+        o[k] = pack_bf16(lo, hi);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
-__global__ __launch_bounds__(kBlock) void swiglu_bf16_v8(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
-                                                         uint16_t* __restrict__ h, int64_t n8) {
-    uint4 gv[kUnroll], uv[kUnroll];
-    const int64_t first = static_cast<int64_t>(blockIdx.x) * kUnroll * kBlock + threadIdx.x;
-#pragma unroll
-    for (int k = 0; k < kUnroll; ++k) {
-        const int64_t i = first + k * kBlock;
-        if (i < n8) {
-            gv[k] = ld16(g + 8 * i);
-            uv[k] = ld16(u + 8 * i);
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < kUnroll; ++k) {
-        const int64_t i = first + k * kBlock;
-        if (i < n8) {
-            st16(h + 8 * i, make_uint4(swiglu_pair(gv[k].x, uv[k].x, 1.f, false), swiglu_pair(gv[k].y, uv[k].y, 1.f, false),
-                                       swiglu_pair(gv[k].z, uv[k].z, 1.f, false), swiglu_pair(gv[k].w, uv[k].w, 1.f, false)));
-        }
-    }
-}
-
-// Shared expert: rows x dim with one logit per row (dim % 8 == 0, so a chunk
+// Chunk i = 8 bf16 (16 bytes). Block b covers chunks b*kUnroll*kBlock + k*kBlock
+// + threadIdx.x, k < kUnroll, so each load instruction of a wave reads 1 KB of
+// contiguous memory. Every block but the last takes the unconditional path: all
+// 2*kUnroll streaming loads are issued before any math. SCALED: the shared
+// expert's rows x dim layout with one logit per row (dim % 8 == 0, so a chunk
 // never straddles two rows).
-__global__ __launch_bounds__(kBlock) void shared_swiglu_bf16_v8(const uint16_t* __restrict__ g,
-                                                                const uint16_t* __restrict__ u,
-                                                                const float* __restrict__ logits,
-                                                                uint16_t* __restrict__ h, int64_t n8, int dim8) {
-    uint4 gv[kUnroll], uv[kUnroll];
-    float lg[kUnroll];
+template <bool SCALED>
+__global__ __launch_bounds__(kBlock) void swiglu_bf16_v8(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+                                                         const float* __restrict__ logits, uint16_t* __restrict__ h,
+                                                         int64_t n8, int dim8) {
     const int64_t first = static_cast<int64_t>(blockIdx.x) * kUnroll * kBlock + threadIdx.x;
+    uint4 gv[kUnroll], uv[kUnroll];
+    float sc[kUnroll];
+    if (static_cast<int64_t>(blockIdx.x + 1) * kUnroll * kBlock <= n8) {  // block-uniform
 #pragma unroll
-    for (int k = 0; k < kUnroll; ++k) {
-        const int64_t i = first + k * kBlock;
-        if (i < n8) {
-            gv[k] = ld16(g + 8 * i);
-            uv[k] = ld16(u + 8 * i);
-            lg[k] = logits[i / dim8];
+        for (int k = 0; k < kUnroll; ++k) {
+            gv[k] = ld16_nt(g + 8 * (first + k * kBlock));
+            uv[k] = ld16_nt(u + 8 * (first + k * kBlock));
+            if (SCALED) sc[k] = logits[(first + k * kBlock) / dim8];
         }
-    }
 #pragma unroll
-    for (int k = 0; k < kUnroll; ++k) {
-        const int64_t i = first + k * kBlock;
-        if (i < n8) {
-            const float sc = sigmoid(lg[k]);
-            st16(h + 8 * i, make_uint4(swiglu_pair(gv[k].x, uv[k].x, sc, true), swiglu_pair(gv[k].y, uv[k].y, sc, true),
-                                       swiglu_pair(gv[k].z, uv[k].z, sc, true), swiglu_pair(gv[k].w, uv[k].w, sc, true)));
+        for (int k = 0; k < kUnroll; ++k)
+            st16_nt(h + 8 * (first + k * kBlock), swiglu8<SCALED>(gv[k], uv[k], SCALED ? sigmoid(sc[k]) : 1.0f));
+    } else {
+        for (int k = 0; k < kUnroll; ++k) {
+            const int64_t i = first + k * kBlock;
+            if (i < n8)
+                st16_nt(h + 8 * i, swiglu8<SCALED>(ld16_nt(g + 8 * i), ld16_nt(u + 8 * i),
+                                                   SCALED ? sigmoid(logits[i / dim8]) : 1.0f));
         }
     }
 }
@@ -100,9 +97,10 @@ __global__ __launch_bounds__(kBlock) void silu_mul_v4(const float* __restrict__ 
                                                       float* __restrict__ h, int64_t n4) {
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n4;
          i += static_cast<int64_t>(gridDim.x) * kBlock) {
-        const float4 a = ld4(g + 4 * i);
-        const float4 b = ld4(u + 4 * i);
-        st4(h + 4 * i, make_float4(silu(a.x) * b.x, silu(a.y) * b.y, silu(a.z) * b.z, silu(a.w) * b.w));
+        const float4 a = ld4_nt(g + 4 * i);
+        const float4 b = ld4_nt(u + 4 * i);
+        const float4 s = silu4(a);
+        st4_nt(h + 4 * i, make_float4(s.x * b.x, s.y * b.y, s.z * b.z, s.w * b.w));
     }
 }
 
@@ -131,9 +129,9 @@ int swiglu_common(const uint16_t* g, const uint16_t* u, const float* logits, uin
         const int64_t n8 = n / 8;
         const unsigned grid = blocks_for(n8, static_cast<int64_t>(kUnroll) * kBlock);
         if (logits)
-            shared_swiglu_bf16_v8<<<grid, kBlock, 0, s>>>(g, u, logits, h, n8, dim / 8);
+            swiglu_bf16_v8<true><<<grid, kBlock, 0, s>>>(g, u, logits, h, n8, dim / 8);
         else
-            swiglu_bf16_v8<<<grid, kBlock, 0, s>>>(g, u, h, n8);
+            swiglu_bf16_v8<false><<<grid, kBlock, 0, s>>>(g, u, nullptr, h, n8, 1);
     } else {
         swiglu_bf16_any<<<stride_grid(n), kBlock, 0, s>>>(g, u, logits, h, n, dim);
     }

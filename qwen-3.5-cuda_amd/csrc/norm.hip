@@ -23,6 +23,9 @@ inline int waves_per_block(int rows) { return rows >= 1024 ? 4 : 1; }
 
 // ------------------------------------------------------------- fp32 rows
 // One wave per row; lane l holds float4 chunks l, l+64, ... (up to MAXC).
+// Lanes past the row end load a clamped in-row address and use zeros, so every
+// load is issued unconditionally; the weights are loaded with the row, ahead
+// of the reduction, so the second pass waits on nothing.
 template <int MAXC, bool GATED>
 __global__ __launch_bounds__(kBlock) void rmsnorm_rows_v4(const float* __restrict__ x, const float* __restrict__ gate,
                                                           const float* __restrict__ w, float* __restrict__ out, int rows,
@@ -32,13 +35,17 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_v4(const float* __restric
     if (row >= rows) return;
     const int n4 = n >> 2;
     const size_t base = static_cast<size_t>(row) * n;
-    float4 v[MAXC];
+    float4 v[MAXC], wv[MAXC];
     float4 g[GATED ? MAXC : 1];
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
         const int i = c * kWave + lane;
-        v[c] = (i < n4) ? ld4(x + base + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
-        if constexpr (GATED) g[c] = (i < n4) ? ld4(gate + base + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int ic = min(i, n4 - 1);
+        v[c] = ld4_nt(x + base + 4 * ic);
+        wv[c] = ld4(w + 4 * ic);
+        if constexpr (GATED) g[c] = ld4_nt(gate + base + 4 * ic);
+        if (i >= n4) v[c] = zero;
     }
     float ss = 0.f;
 #pragma unroll
@@ -48,21 +55,19 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_v4(const float* __restric
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
         const int i = c * kWave + lane;
-        if (i < n4) {
-            const float4 wv = ld4(w + 4 * i);
-            float4 o;
-            o.x = v[c].x * r * wv.x;
-            o.y = v[c].y * r * wv.y;
-            o.z = v[c].z * r * wv.z;
-            o.w = v[c].w * r * wv.w;
-            if constexpr (GATED) {
-                o.x *= silu(g[c].x);
-                o.y *= silu(g[c].y);
-                o.z *= silu(g[c].z);
-                o.w *= silu(g[c].w);
-            }
-            st4(out + base + 4 * i, o);
+        float4 o;
+        o.x = v[c].x * r * wv[c].x;
+        o.y = v[c].y * r * wv[c].y;
+        o.z = v[c].z * r * wv[c].z;
+        o.w = v[c].w * r * wv[c].w;
+        if constexpr (GATED) {
+            const float4 sg = silu4(g[c]);
+            o.x *= sg.x;
+            o.y *= sg.y;
+            o.z *= sg.z;
+            o.w *= sg.w;
         }
+        if (i < n4) st4_nt(out + base + 4 * i, o);
     }
 }
 
@@ -110,31 +115,32 @@ __global__ __launch_bounds__(kBlock) void residual_rmsnorm_f32_v4(const float* _
     if (row >= rows) return;
     const int n4 = n >> 2;
     const size_t base = static_cast<size_t>(row) * n;
-    float4 v[MAXC];
+    float4 v[MAXC], wv[MAXC];
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        const int ic = min(c * kWave + lane, n4 - 1);
+        const float4 a = ld4_nt(x + base + 4 * ic);
+        const float4 d = ld4_nt(b + base + 4 * ic);
+        wv[c] = ld4(w + 4 * ic);
+        v[c] = make_float4(a.x + d.x, a.y + d.y, a.z + d.z, a.w + d.w);
+    }
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
         const int i = c * kWave + lane;
         if (i < n4) {
-            const float4 a = ld4(x + base + 4 * i);
-            const float4 d = ld4(b + base + 4 * i);
-            v[c] = make_float4(a.x + d.x, a.y + d.y, a.z + d.z, a.w + d.w);
-            st4(resid + base + 4 * i, v[c]);
-        } else {
-            v[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+            st4_nt(resid + base + 4 * i, v[c]);
+            ss += sumsq4(v[c]);
         }
-        ss += sumsq4(v[c]);
     }
     ss = group_sum<kWave>(ss);
     const float r = rsqrtf(ss / static_cast<float>(n) + eps);
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
         const int i = c * kWave + lane;
-        if (i < n4) {
-            const float4 wv = ld4(w + 4 * i);
-            st4(normed + base + 4 * i,
-                make_float4(v[c].x * r * wv.x, v[c].y * r * wv.y, v[c].z * r * wv.z, v[c].w * r * wv.w));
-        }
+        if (i < n4)
+            st4_nt(normed + base + 4 * i, make_float4(v[c].x * r * wv[c].x, v[c].y * r * wv[c].y,
+                                                      v[c].z * r * wv[c].z, v[c].w * r * wv[c].w));
     }
 }
 
@@ -173,16 +179,14 @@ __global__ __launch_bounds__(kBlock) void residual_rmsnorm_bf16_v8(const uint16_
     const int n8 = n >> 3;
     const size_t base = static_cast<size_t>(row) * n;
     uint4 xa[MAXC], ba[MAXC];
+    float4 w0[MAXC], w1[MAXC];
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
-        const int i = c * kWave + lane;
-        if (i < n8) {
-            xa[c] = ld16(x + base + 8 * i);
-            ba[c] = ld16(b + base + 8 * i);
-        } else {
-            xa[c] = make_uint4(0, 0, 0, 0);
-            ba[c] = make_uint4(0, 0, 0, 0);
-        }
+        const int ic = min(c * kWave + lane, n8 - 1);
+        xa[c] = ld16_nt(x + base + 8 * ic);
+        ba[c] = ld16_nt(b + base + 8 * ic);
+        w0[c] = ld4(w + 8 * ic);
+        w1[c] = ld4(w + 8 * ic + 4);
     }
     uint4 s[MAXC];
     float ss = 0.f;
@@ -191,16 +195,20 @@ __global__ __launch_bounds__(kBlock) void residual_rmsnorm_bf16_v8(const uint16_
         const uint32_t xs[4] = {xa[c].x, xa[c].y, xa[c].z, xa[c].w};
         const uint32_t bs[4] = {ba[c].x, ba[c].y, ba[c].z, ba[c].w};
         uint32_t ps[4];
+        float part = 0.f;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             ps[k] = pack_bf16(bf16_lo(xs[k]) + bf16_lo(bs[k]), bf16_hi(xs[k]) + bf16_hi(bs[k]));
             const float lo = bf16_lo(ps[k]);
             const float hi = bf16_hi(ps[k]);
-            ss += lo * lo + hi * hi;
+            part += lo * lo + hi * hi;
         }
         s[c] = make_uint4(ps[0], ps[1], ps[2], ps[3]);
         const int i = c * kWave + lane;
-        if (i < n8) st16(resid + base + 8 * i, s[c]);
+        if (i < n8) {
+            st16_nt(resid + base + 8 * i, s[c]);
+            ss += part;
+        }
     }
     ss = group_sum<kWave>(ss);
     const float r = rsqrtf(ss / static_cast<float>(n) + eps);
@@ -208,13 +216,11 @@ __global__ __launch_bounds__(kBlock) void residual_rmsnorm_bf16_v8(const uint16_
     for (int c = 0; c < MAXC; ++c) {
         const int i = c * kWave + lane;
         if (i < n8) {
-            const float4 w0 = ld4(w + 8 * i);
-            const float4 w1 = ld4(w + 8 * i + 4);
-            const uint4 o = make_uint4(pack_bf16(bf16_lo(s[c].x) * r * w0.x, bf16_hi(s[c].x) * r * w0.y),
-                                       pack_bf16(bf16_lo(s[c].y) * r * w0.z, bf16_hi(s[c].y) * r * w0.w),
-                                       pack_bf16(bf16_lo(s[c].z) * r * w1.x, bf16_hi(s[c].z) * r * w1.y),
-                                       pack_bf16(bf16_lo(s[c].w) * r * w1.z, bf16_hi(s[c].w) * r * w1.w));
-            st16(normed + base + 8 * i, o);
+            const uint4 o = make_uint4(pack_bf16(bf16_lo(s[c].x) * r * w0[c].x, bf16_hi(s[c].x) * r * w0[c].y),
+                                       pack_bf16(bf16_lo(s[c].y) * r * w0[c].z, bf16_hi(s[c].y) * r * w0[c].w),
+                                       pack_bf16(bf16_lo(s[c].z) * r * w1[c].x, bf16_hi(s[c].z) * r * w1[c].y),
+                                       pack_bf16(bf16_lo(s[c].w) * r * w1[c].z, bf16_hi(s[c].w) * r * w1[c].w));
+            st16_nt(normed + base + 8 * i, o);
         }
     }
 }

@@ -5,6 +5,6 @@ device tensors; `qwen35_hip.synth` builds the deterministic synthetic inputs of
 the benchmark configurations.
 """
 
-from ._lib import LIB_PATH, QwenError, load  # noqa: F401
+from ._lib import LIB_PATH, PACKAGE_DIR, QwenError, load  # noqa: F401
 
-__all__ = ["LIB_PATH", "QwenError", "load"]
+__all__ = ["LIB_PATH", "PACKAGE_DIR", "QwenError", "load"]
