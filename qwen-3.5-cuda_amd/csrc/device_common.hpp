@@ -16,13 +16,12 @@ __device__ __forceinline__ float dpp_move(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-__device__ __forceinline__ float read_lane(float v, int lane) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
-
 // Sum over aligned groups of G lanes (G a power of two, 1..64). Every lane of a
 // group ends with the same bits: each step adds a lane and its partner, and both
-// partners evaluate the same commutative sum.
+// partners evaluate the same sum with the same operand order (or a commutative
+// pair). Everything stays in the VALU: DPP within 16-lane rows, then gfx950's
+// v_permlane16_swap / v_permlane32_swap, which with both operands = v return
+// (even row, odd row) and (lower half, upper half) values in every lane.
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
     static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "group");
@@ -30,13 +29,13 @@ __device__ __forceinline__ float group_sum(float v) {
     if constexpr (G >= 4) v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
     if constexpr (G >= 8) v += dpp_move<0x141>(v);  // row_half_mirror: 8-lane halves
     if constexpr (G >= 16) v += dpp_move<0x140>(v); // row_mirror: 16-lane rows
-    if constexpr (G == 32) {
-        // ds_swizzle bit mode, and_mask 0x1f, xor_mask 0x10: lane ^ 16 within 32.
-        v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+    if constexpr (G >= 32) {                        // rows (0,1) and (2,3)
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
     }
-    if constexpr (G == 64) {
-        // Four 16-lane row sums, combined in scalar registers: wave-uniform.
-        v = (read_lane(v, 0) + read_lane(v, 16)) + (read_lane(v, 32) + read_lane(v, 48));
+    if constexpr (G >= 64) {                        // halves (0..31) and (32..63)
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
     }
     return v;
 }

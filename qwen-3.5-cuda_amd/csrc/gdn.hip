@@ -25,8 +25,9 @@ namespace qk {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kConvTile = 64;    // tokens per wave tile (front end)
-constexpr int kConvUnroll = 8;   // token loads in flight per lane
+constexpr int kConvTile = 64;    // tokens per thread tile (generic front end)
+constexpr int kConvRows = 4;     // rows per wave (vector front end)
+constexpr int kConvWaves = 8;    // waves per workgroup (vector front end)
 constexpr int kGateUnroll = 4;   // head groups in flight per wave (norm_gate)
 
 // Exactly-rounded 1/sqrt(n) for the q scale, so the device multiplies by the
@@ -43,22 +44,24 @@ __device__ __forceinline__ float conv4(float h0, float h1, float h2, float xv, f
 }
 
 // ---------------------------------------------------- front end, kernel size 4
-// Wave = 256 channels (float4 per lane) x kConvTile tokens. The token loop is
-// software-pipelined: the next kConvUnroll rows are in flight while the current
-// ones are convolved, normalised and stored. Lanes past the last channel
-// address a clamped channel and skip their stores, so loads never branch.
-template <int LPH>
-__global__ __launch_bounds__(kBlock) void gdn_frontend_k4(const float* __restrict__ x, const float* __restrict__ w,
+// Workgroup = 256 channels (float4 per lane) x W waves x R rows: wave v owns
+// rows T0 + v*R .. +R-1 and issues all R row loads at once. The three rows
+// before a wave's first row are the previous wave's last three, handed over
+// through LDS, so only wave 0 reads rows outside its tile (the rows before T0,
+// or the history when T0 == 0). Lanes past the last channel address a clamped
+// channel and skip their stores, so loads never branch.
+template <int LPH, int R, int W>
+__global__ __launch_bounds__(W * kWave) void gdn_frontend_k4(const float* __restrict__ x, const float* __restrict__ w,
                                                           const float* hist_in, float* hist_out, float* __restrict__ y,
                                                           int rows, int C, int q_ch, int qk_ch, float eps, float qscale,
-                                                          int n_ctiles, int n_ttiles) {
-    constexpr int U = kConvUnroll;
+                                                          int n_ctiles) {
+    static_assert(R >= 3, "a wave hands its last three rows to the next wave");
+    __shared__ float4 halo[W][3][kWave];
     const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * (kBlock / kWave) + (threadIdx.x >> 6);
-    if (wave >= n_ctiles * n_ttiles) return;  // wave-uniform
-    const int cbase = (wave % n_ctiles) * (4 * kWave);
-    const int t0 = (wave / n_ctiles) * kConvTile;
-    const int t1 = min(t0 + kConvTile, rows);
+    const int wv = threadIdx.x >> 6;
+    const int cbase = (blockIdx.x % n_ctiles) * (4 * kWave);
+    const int T0 = (blockIdx.x / n_ctiles) * (W * R);       // first row of the workgroup
+    const int t0 = T0 + wv * R;                             // first row of this wave
     const int c = cbase + 4 * lane;
     const bool on = c < C;
     const int cc = on ? c : C - 4;         // clamped channel for addressing
@@ -66,70 +69,69 @@ __global__ __launch_bounds__(kBlock) void gdn_frontend_k4(const float* __restric
     const bool is_q = c < q_ch;
     const bool is_qk = c < qk_ch;
 
-    // taps of channels c..c+3, and the window x[t-3], x[t-2], x[t-1]
-    const float4 w0 = ld4(w + 4 * static_cast<size_t>(cc));
+    // Loads return in order: the small reused operands first, then the rows.
+    const float4 w0 = ld4(w + 4 * static_cast<size_t>(cc));  // taps of channels c..c+3
     const float4 w1 = ld4(w + 4 * static_cast<size_t>(cc) + 4);
     const float4 w2 = ld4(w + 4 * static_cast<size_t>(cc) + 8);
     const float4 w3 = ld4(w + 4 * static_cast<size_t>(cc) + 12);
-    float4 h0, h1, h2;
-    if (t0 == 0) {
-        const float4 a = ld4(hist_in + 3 * static_cast<size_t>(cc));
-        const float4 b = ld4(hist_in + 3 * static_cast<size_t>(cc) + 4);
-        const float4 d = ld4(hist_in + 3 * static_cast<size_t>(cc) + 8);
-        // [ch0: j0 j1 j2 | ch1: j0 j1 j2 | ch2 ... | ch3 ...]
-        h0 = make_float4(a.x, a.w, b.z, d.y);
-        h1 = make_float4(a.y, b.x, b.w, d.z);
-        h2 = make_float4(a.z, b.y, d.x, d.w);
-    } else {
-        h0 = ld4(x + static_cast<size_t>(t0 - 3) * C + cc);
-        h1 = ld4(x + static_cast<size_t>(t0 - 2) * C + cc);
-        h2 = ld4(x + static_cast<size_t>(t0 - 1) * C + cc);
+    float4 h0 = make_float4(0.f, 0.f, 0.f, 0.f), h1 = h0, h2 = h0;  // x[t-3], x[t-2], x[t-1]
+    if (wv == 0) {
+        if (T0 == 0) {
+            const float4 a = ld4(hist_in + 3 * static_cast<size_t>(cc));
+            const float4 b = ld4(hist_in + 3 * static_cast<size_t>(cc) + 4);
+            const float4 d = ld4(hist_in + 3 * static_cast<size_t>(cc) + 8);
+            // [ch0: j0 j1 j2 | ch1: j0 j1 j2 | ch2 ... | ch3 ...]
+            h0 = make_float4(a.x, a.w, b.z, d.y);
+            h1 = make_float4(a.y, b.x, b.w, d.z);
+            h2 = make_float4(a.z, b.y, d.x, d.w);
+        } else {
+            h0 = ld4(x + static_cast<size_t>(T0 - 3) * C + cc);
+            h1 = ld4(x + static_cast<size_t>(T0 - 2) * C + cc);
+            h2 = ld4(x + static_cast<size_t>(T0 - 1) * C + cc);
+        }
     }
-    // Loads issue (and return) in order: the small reused operands above go
-    // first so the first row's math waits only for them and its own row.
-    auto xrow = [&](int t) { return x + static_cast<size_t>(min(t, t1 - 1)) * C + cc; };
-    float4 cur[U], nxt[U];
+    float4 xv[R];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        cur[u] = ld4_nt(xrow(t0 + u));
-        nxt[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int u = 0; u < R; ++u) xv[u] = ld4_nt(x + static_cast<size_t>(min(t0 + u, rows - 1)) * C + cc);
+
+    // Hand the last three rows to the next wave. A wave whose rows run past the
+    // end publishes clamped rows, read only by waves with no rows at all.
+    halo[wv][0][lane] = xv[R - 3];
+    halo[wv][1][lane] = xv[R - 2];
+    halo[wv][2][lane] = xv[R - 1];
+    __syncthreads();
+    if (wv > 0) {
+        h0 = halo[wv - 1][0][lane];
+        h1 = halo[wv - 1][1][lane];
+        h2 = halo[wv - 1][2][lane];
     }
 
-    for (int t = t0; t < t1; t += U) {
-        if (t + U < t1) {  // wave-uniform: prefetch the next rows
 #pragma unroll
-            for (int u = 0; u < U; ++u) nxt[u] = ld4_nt(xrow(t + U + u));
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (t + u >= t1) break;  // wave-uniform
-            const float4 xv = cur[u];
-            float4 v = silu4(make_float4(conv4(h0.x, h1.x, h2.x, xv.x, w0), conv4(h0.y, h1.y, h2.y, xv.y, w1),
-                                         conv4(h0.z, h1.z, h2.z, xv.z, w2), conv4(h0.w, h1.w, h2.w, xv.w, w3)));
-            if (norm_wave) {
-                const float ss = group_sum<LPH>(sumsq4(v));
-                const float r = rsqrtf(ss + eps);
-                const float sc = is_q ? r * qscale : r;  // q *= rq * scale; k *= rk
-                if (is_qk) {
-                    v.x *= sc;
-                    v.y *= sc;
-                    v.z *= sc;
-                    v.w *= sc;
-                }
+    for (int u = 0; u < R; ++u) {
+        if (t0 + u >= rows) break;  // wave-uniform
+        float4 v = silu4(make_float4(conv4(h0.x, h1.x, h2.x, xv[u].x, w0), conv4(h0.y, h1.y, h2.y, xv[u].y, w1),
+                                     conv4(h0.z, h1.z, h2.z, xv[u].z, w2), conv4(h0.w, h1.w, h2.w, xv[u].w, w3)));
+        if (norm_wave) {
+            const float ss = group_sum<LPH>(sumsq4(v));
+            const float r = rsqrtf(ss + eps);
+            const float sc = is_q ? r * qscale : r;  // q *= rq * scale; k *= rk
+            if (is_qk) {
+                v.x *= sc;
+                v.y *= sc;
+                v.z *= sc;
+                v.w *= sc;
             }
-            if (on) st4_nt(y + static_cast<size_t>(t + u) * C + c, v);
-            h0 = h1;
-            h1 = h2;
-            h2 = xv;
         }
-#pragma unroll
-        for (int u = 0; u < U; ++u) cur[u] = nxt[u];
+        if (on) st4_nt(y + static_cast<size_t>(t0 + u) * C + c, v);
+        h0 = h1;
+        h1 = h2;
+        h2 = xv[u];
     }
 
-    // The wave of the first time tile owns the history: it read hist_in first
-    // and writes hist_out last, so hist_out may alias hist_in.
-    if (t0 == 0 && on) {
-        if (n_ttiles > 1) {  // rows > kConvTile: the last three inputs
+    // Wave 0 of the first workgroup in time owns the history: it read hist_in
+    // first and writes hist_out last, so hist_out may alias hist_in.
+    if (T0 == 0 && wv == 0 && on) {
+        if (rows > R) {  // the last three inputs (when rows <= R the window already holds them)
             h0 = ld4(x + static_cast<size_t>(rows - 3) * C + c);
             h1 = ld4(x + static_cast<size_t>(rows - 2) * C + c);
             h2 = ld4(x + static_cast<size_t>(rows - 1) * C + c);
@@ -318,18 +320,20 @@ int qwen_gdn_frontend_rows(const float* x, const float* weight, const float* his
                      aligned16(hist_in) && aligned16(hist_out) && aligned16(y);
     const int n_ttiles = (rows + kConvTile - 1) / kConvTile;
     if (vec) {
+        constexpr int R = kConvRows, W = kConvWaves;
         const int n_ctiles = (channels + 4 * kWave - 1) / (4 * kWave);
-        const unsigned grid = blocks_for(static_cast<int64_t>(n_ctiles) * n_ttiles, kBlock / kWave);
+        const int n_wtiles = (rows + W * R - 1) / (W * R);
+        const unsigned grid = static_cast<unsigned>(n_ctiles) * n_wtiles;
         const float qscale = k_heads > 0 ? host_rsqrt(key_dim) : 1.0f;
         if (lph == 64)
-            gdn_frontend_k4<64><<<grid, kBlock, 0, s>>>(x, weight, hist_in, hist_out, y, rows, channels, q_ch, qk_ch, eps,
-                                                       qscale, n_ctiles, n_ttiles);
+            gdn_frontend_k4<64, R, W><<<grid, W * kWave, 0, s>>>(x, weight, hist_in, hist_out, y, rows, channels, q_ch,
+                                                                qk_ch, eps, qscale, n_ctiles);
         else if (lph == 32)
-            gdn_frontend_k4<32><<<grid, kBlock, 0, s>>>(x, weight, hist_in, hist_out, y, rows, channels, q_ch, qk_ch, eps,
-                                                       qscale, n_ctiles, n_ttiles);
+            gdn_frontend_k4<32, R, W><<<grid, W * kWave, 0, s>>>(x, weight, hist_in, hist_out, y, rows, channels, q_ch,
+                                                                qk_ch, eps, qscale, n_ctiles);
         else
-            gdn_frontend_k4<16><<<grid, kBlock, 0, s>>>(x, weight, hist_in, hist_out, y, rows, channels, q_ch, qk_ch, eps,
-                                                       qscale, n_ctiles, n_ttiles);
+            gdn_frontend_k4<16, R, W><<<grid, W * kWave, 0, s>>>(x, weight, hist_in, hist_out, y, rows, channels, q_ch,
+                                                                qk_ch, eps, qscale, n_ctiles);
     } else {
         const int64_t threads = static_cast<int64_t>(channels) * n_ttiles;
         gdn_conv_any<<<blocks_for(threads, kBlock), kBlock, 0, s>>>(x, weight, hist_in, hist_out, y, rows, channels,
