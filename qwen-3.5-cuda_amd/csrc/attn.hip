@@ -45,7 +45,20 @@ RopeDen make_den(int lo, int count, int rope_dim, float theta) {
 }
 
 // ------------------------------------------------------------ vector kernel
-template <int LPH, bool NORM, bool ROPE>
+// R64: the production shape (head_dim 256, rope_dim 64), where every value the
+// rotation needs moves through VALU cross-lane ops instead of ds_bpermute:
+// lane 16r + m evaluates the angle of pair 4*(m % 8) + r, so rotary lane m
+// (m < 16) finds its four pairs at lanes m, m+16, m+32, m+48 (gathered with
+// v_permlane16_swap / v_permlane32_swap), and its partner 8 lanes away in the
+// same 16-lane row (DPP row_ror:8).
+__device__ __forceinline__ float pl16_hi(float v) {  // lane m (even row) <- lane m + 16
+    return __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)[1]);
+}
+__device__ __forceinline__ float pl32_hi(float v) {  // lane m (< 32) <- lane m + 32
+    return __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false)[1]);
+}
+
+template <int LPH, bool NORM, bool ROPE, bool R64>
 __global__ __launch_bounds__(kBlock) void qk_norm_rope_v4(float* __restrict__ q, float* __restrict__ k,
                                                           const float* __restrict__ qw, const float* __restrict__ kw,
                                                           const int32_t* __restrict__ pos, int pos0, int rows,
@@ -75,8 +88,12 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_v4(float* __restrict__ q,
     float c0 = 1.f, s0 = 0.f, c1 = 1.f, s1 = 0.f;
     if constexpr (ROPE) {
         const float fp = static_cast<float>(pos ? pos[t] : pos0 + t);
-        if (lg < half) sincosf(fp / den.den[lg], &s0, &c0);
-        if (lg + LPH < half) sincosf(fp / den.den[lg + LPH], &s1, &c1);
+        if constexpr (R64) {
+            sincosf(fp / den.den[4 * (lane & 7) + (lane >> 4)], &s0, &c0);
+        } else {
+            if (lg < half) sincosf(fp / den.den[lg], &s0, &c0);
+            if (lg + LPH < half) sincosf(fp / den.den[lg + LPH], &s1, &c1);
+        }
     }
     float4 v = ld4_nt(p + 4 * lg);
 
@@ -90,7 +107,27 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_v4(float* __restrict__ q,
         v.w = v.w * (r * wv.w);
     }
 
-    if constexpr (ROPE) {
+    if constexpr (ROPE && R64) {
+        const bool first = lane < 8, second = lane >= 8 && lane < 16;
+        const float pv[4] = {dpp_move<0x128>(v.x), dpp_move<0x128>(v.y), dpp_move<0x128>(v.z),
+                             dpp_move<0x128>(v.w)};
+        const float c01 = pl16_hi(c0), s01 = pl16_hi(s0);
+        const float cs[4] = {c0, c01, pl32_hi(c0), pl32_hi(c01)};
+        const float sn[4] = {s0, s01, pl32_hi(s0), pl32_hi(s01)};
+        const float a[4] = {v.x, v.y, v.z, v.w};
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (first)
+                o[j] = a[j] * cs[j] - pv[j] * sn[j];  // x[i]      = a c - b s
+            else if (second)
+                o[j] = a[j] * cs[j] + pv[j] * sn[j];  // x[i+half] = b c + a s
+            else
+                o[j] = a[j];
+        }
+        v = make_float4(o[0], o[1], o[2], o[3]);
+    }
+    if constexpr (ROPE && !R64) {
         const int d0 = 4 * lg;
         const bool first = d0 < half;                 // dims i..i+3, partner i+half
         const bool second = !first && d0 < rope_dim;  // dims i+half.., partner i
@@ -181,12 +218,18 @@ void launch_vec(int lph, float* q, float* k, const float* qw, const float* kw, c
     const int hpw = kWave / lph;
     const int64_t waves = (heads + hpw - 1) / hpw;
     const dim3 grid(blocks_for(waves, kBlock / kWave)), block(kBlock);
-    if (lph == 64)
-        qk_norm_rope_v4<64, NORM, ROPE><<<grid, block, 0, s>>>(q, k, qw, kw, pos, pos0, rows, qh, kh, rope_dim, den, eps);
+    if (lph == 64 && ROPE && rope_dim == 64)
+        qk_norm_rope_v4<64, NORM, ROPE, true><<<grid, block, 0, s>>>(q, k, qw, kw, pos, pos0, rows, qh, kh, rope_dim, den,
+                                                                    eps);
+    else if (lph == 64)
+        qk_norm_rope_v4<64, NORM, ROPE, false><<<grid, block, 0, s>>>(q, k, qw, kw, pos, pos0, rows, qh, kh, rope_dim,
+                                                                     den, eps);
     else if (lph == 32)
-        qk_norm_rope_v4<32, NORM, ROPE><<<grid, block, 0, s>>>(q, k, qw, kw, pos, pos0, rows, qh, kh, rope_dim, den, eps);
+        qk_norm_rope_v4<32, NORM, ROPE, false><<<grid, block, 0, s>>>(q, k, qw, kw, pos, pos0, rows, qh, kh, rope_dim,
+                                                                     den, eps);
     else
-        qk_norm_rope_v4<16, NORM, ROPE><<<grid, block, 0, s>>>(q, k, qw, kw, pos, pos0, rows, qh, kh, rope_dim, den, eps);
+        qk_norm_rope_v4<16, NORM, ROPE, false><<<grid, block, 0, s>>>(q, k, qw, kw, pos, pos0, rows, qh, kh, rope_dim,
+                                                                     den, eps);
 }
 
 // Common path of the three entry points. Pointers of a tensor with 0 heads are
