@@ -321,6 +321,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
     ap.add_argument("--json-out", default="", help="also write the JSON line to this file")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="also run the reference copy of BYTES (read) + BYTES (write) three times, for "
+                         "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE against known traffic")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -371,6 +374,19 @@ def main() -> int:
     value = bytes_step / (ms_per_step * 1e-3) / 1e9
     print(f"# step: {ms_per_step * 1e3:.1f} us, {value:.1f} GB/s aggregate", file=sys.stderr, flush=True)
     del graph
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy // 16 * 16
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+        for _ in range(3):
+            if bench_lib.qwen_bench_copy(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), n,
+                                         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)):
+                raise RuntimeError("qwen_bench_copy failed")
+            torch.cuda.synchronize()
+        print(f"# calibration copy: {n} bytes read + {n} bytes written per launch, 3 launches", file=sys.stderr,
+              flush=True)
+        del src, dst
 
     # ---- per-kernel steady state and the copy ceiling at the same bytes
     if not args.no_per_kernel:

@@ -1,0 +1,141 @@
+"""Summarise rocprofv3 outputs of bench.py runs into the profile tables.
+
+  python -m qwen35_hip.rocprof_summary stats   KERNEL_STATS.csv
+      per-kernel dispatch count and average / min / max duration (us)
+  python -m qwen35_hip.rocprof_summary traffic FETCH.csv WRITE.csv COPY_BYTES [--json OUT]
+      per-kernel FETCH_SIZE / WRITE_SIZE (KiB per dispatch, from two --pmc runs),
+      scaled to bytes by the factor that makes the reference copy of COPY_BYTES
+      read + COPY_BYTES written read exactly its known traffic, next to each
+      kernel's algorithmic bytes
+
+Kernel symbols are mapped to the bench.py kernel names; the reference copy is
+"copy16" (libqwen35_benchutil.so).
+"""
+
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import sys
+from collections import defaultdict
+
+# symbol substring -> bench.py kernel name (first match wins)
+NAMES = [
+    ("gdn_frontend_k4", "gdn_frontend"),
+    ("norm_gate_v4", "gdn_norm_gate"),
+    ("swiglu_bf16_v8ILb1", "shared_swiglu_sigmoid_bf16"),
+    ("swiglu_bf16_v8ILb0", "swiglu_bf16"),
+    ("swiglu_bf16_v8<true>", "shared_swiglu_sigmoid_bf16"),
+    ("swiglu_bf16_v8<false>", "swiglu_bf16"),
+    ("gather_q4k", "dequant_gather_q4_k"),
+    ("gather_q6k", "dequant_gather_q6_k"),
+    ("residual_rmsnorm_bf16_v8", "residual_rmsnorm_bf16"),
+    ("qk_norm_rope_v4", "qk_norm_rope"),
+    ("rmsnorm_rows_v4", "rmsnorm"),
+    ("copy16", "copy"),
+]
+
+# algorithmic bytes per call at the BASELINE configs (bench.py computes the same)
+ALGORITHMIC = {
+    "rmsnorm": 598016, "qk_norm_rope": 18878464, "residual_rmsnorm_bf16": 67117056, "swiglu_bf16": 100663296,
+    "shared_swiglu_sigmoid_bf16": 12599296, "gdn_frontend": 268763136, "gdn_norm_gate": 201327104,
+    "dequant_gather_q4_k": 76578816, "dequant_gather_q6_k": 80904192,
+}
+
+
+def kernel_name(symbol: str) -> str | None:
+    for key, name in NAMES:
+        if key in symbol:
+            return name
+    return None
+
+
+def stats(path: str) -> dict:
+    out = {}
+    for r in csv.DictReader(open(path)):
+        name = kernel_name(r["Name"])
+        if name is None:
+            continue
+        out.setdefault(name, []).append(r)
+    table = {}
+    for name, rs in out.items():
+        calls = sum(int(r["Calls"]) for r in rs)
+        total = sum(float(r["TotalDurationNs"]) for r in rs)
+        table[name] = {"calls": calls, "avg_us": total / calls / 1e3, "min_us": min(float(r["MinNs"]) for r in rs) / 1e3,
+                       "max_us": max(float(r["MaxNs"]) for r in rs) / 1e3}
+    return table
+
+
+def counter_means(path: str, counter: str) -> dict:
+    """Mean counter value per dispatch, per kernel name (copy16 split by grid size)."""
+    acc = defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        if r.get("Counter_Name") != counter:
+            continue
+        name = kernel_name(r["Kernel_Name"])
+        if name is None:
+            continue
+        if name == "copy":
+            name = f"copy:{r.get('Grid_Size', '')}"
+        acc[name].append(float(r["Counter_Value"]))
+    return {k: sum(v) / len(v) for k, v in acc.items()}
+
+
+def traffic(fetch_csv: str, write_csv: str, copy_bytes: int) -> dict:
+    fetch = counter_means(fetch_csv, "FETCH_SIZE")
+    write = counter_means(write_csv, "WRITE_SIZE")
+    # the calibration copy is the largest copy16 dispatch
+    ck = max((k for k in fetch if k.startswith("copy:")), key=lambda k: fetch[k])
+    f_scale = copy_bytes / (fetch[ck] * 1024.0)
+    w_scale = copy_bytes / (write[ck] * 1024.0)
+    out = {"_calibration": {"copy_bytes_each_way": copy_bytes, "copy_fetch_kib": fetch[ck], "copy_write_kib": write[ck],
+                            "fetch_bytes_per_kib": f_scale * 1024.0, "write_bytes_per_kib": w_scale * 1024.0}}
+    for name, alg in ALGORITHMIC.items():
+        if name not in fetch or name not in write:
+            continue
+        fb = fetch[name] * 1024.0 * f_scale
+        wb = write[name] * 1024.0 * w_scale
+        out[name] = {"fetch_kib": fetch[name], "write_kib": write[name], "fetch_bytes": round(fb),
+                     "write_bytes": round(wb), "bytes_per_launch": round(fb + wb), "algorithmic_bytes": alg,
+                     "traffic_over_algorithmic": round((fb + wb) / alg, 4)}
+    return out
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    a = sub.add_parser("stats")
+    a.add_argument("csv")
+    b = sub.add_parser("traffic")
+    b.add_argument("fetch_csv")
+    b.add_argument("write_csv")
+    b.add_argument("copy_bytes", type=int)
+    b.add_argument("--json", default="")
+    args = ap.parse_args(argv)
+    if args.cmd == "stats":
+        t = stats(args.csv)
+        print(f"{'kernel':30s} {'calls':>6s} {'avg us':>9s} {'min us':>9s} {'max us':>9s} {'GB/s (avg)':>11s}")
+        for name, r in sorted(t.items(), key=lambda kv: -kv[1]["avg_us"]):
+            gbps = ALGORITHMIC.get(name, 0) / r["avg_us"] / 1e3 if name in ALGORITHMIC else float("nan")
+            print(f"{name:30s} {r['calls']:6d} {r['avg_us']:9.2f} {r['min_us']:9.2f} {r['max_us']:9.2f} {gbps:11.1f}")
+        return 0
+    t = traffic(args.fetch_csv, args.write_csv, args.copy_bytes)
+    cal = t["_calibration"]
+    print(f"calibration: copy of {cal['copy_bytes_each_way']} B each way read as FETCH {cal['copy_fetch_kib']:.0f} KiB, "
+          f"WRITE {cal['copy_write_kib']:.0f} KiB -> {cal['fetch_bytes_per_kib']:.1f} / {cal['write_bytes_per_kib']:.1f} "
+          "bytes per counter KiB")
+    print(f"{'kernel':30s} {'fetch B':>12s} {'write B':>12s} {'total B':>12s} {'algorithmic':>12s} {'ratio':>7s}")
+    for name, r in t.items():
+        if name.startswith("_"):
+            continue
+        print(f"{name:30s} {r['fetch_bytes']:12d} {r['write_bytes']:12d} {r['bytes_per_launch']:12d} "
+              f"{r['algorithmic_bytes']:12d} {r['traffic_over_algorithmic']:7.3f}")
+    if args.json:
+        with open(args.json, "w") as f:
+            json.dump(t, f, indent=1)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
