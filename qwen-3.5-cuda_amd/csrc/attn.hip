@@ -69,36 +69,54 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_v4(float* __restrict__ q,
     const int lane = threadIdx.x & 63;
     const int lg = lane % LPH;
     const int gbase = lane - lg;
+    // 32-bit index math (the host checks rows * heads < 2^31); the wave index is
+    // made explicitly uniform so that, with one head per wave, the head and
+    // position arithmetic and the position load stay scalar.
     const int hpr = q_heads + k_heads;
-    const int64_t total = static_cast<int64_t>(rows) * hpr;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int total = rows * hpr;
+    const int wave = static_cast<int>(blockIdx.x) * (kBlock / kWave) + wave_in_block();
     if (wave * HPW >= total) return;  // wave-uniform
-    const int64_t slot = wave * HPW + lane / LPH;
+    const int slot = wave * HPW + (HPW > 1 ? lane / LPH : 0);  // wave-uniform when HPW == 1
     const bool active = slot < total;
-    const int64_t sl = active ? slot : total - 1;  // clamped: loads never branch
-    const int t = static_cast<int>(sl / hpr);
-    const int h = static_cast<int>(sl % hpr);
+    const int sl = active ? slot : total - 1;  // clamped: loads never branch
+    const int t = sl / hpr;
+    const int h = sl - t * hpr;
     float* p = (h < q_heads) ? q + (static_cast<size_t>(t) * q_heads + h) * HD
                              : k + (static_cast<size_t>(t) * k_heads + (h - q_heads)) * HD;
     const float* wt = (h < q_heads) ? qw : kw;
     const int half = rope_dim >> 1;
 
-    // Rotation angles of this group's head: pairs lg and lg + LPH. They do not
-    // depend on x, so they are computed while the row is in flight.
-    float c0 = 1.f, s0 = 0.f, c1 = 1.f, s1 = 0.f;
+    // Issue order matters (vector loads return in order): the denominators
+    // first, then the row and its weights, then the angle math, which only
+    // waits for the denominators and so overlaps the row's flight. The
+    // position is a scalar load when a wave holds one head.
+    float fp = 0.f, dn0 = 1.f, dn1 = 1.f;
     if constexpr (ROPE) {
-        const float fp = static_cast<float>(pos ? pos[t] : pos0 + t);
+        fp = static_cast<float>(pos ? pos[t] : pos0 + t);
         if constexpr (R64) {
-            sincosf(fp / den.den[4 * (lane & 7) + (lane >> 4)], &s0, &c0);
+            // lane 16r + m evaluates pair 4*(m % 8) + r
+            dn0 = den.den[4 * (lane & 7) + (lane >> 4)];
         } else {
-            if (lg < half) sincosf(fp / den.den[lg], &s0, &c0);
-            if (lg + LPH < half) sincosf(fp / den.den[lg + LPH], &s1, &c1);
+            dn0 = den.den[min(lg, kMaxDen - 1)];
+            dn1 = den.den[min(lg + LPH, kMaxDen - 1)];
         }
     }
     float4 v = ld4_nt(p + 4 * lg);
+    const float4 wv = NORM ? ld4(wt + 4 * lg) : make_float4(1.f, 1.f, 1.f, 1.f);
+
+    // Rotation angles of this group's head (pairs lg and lg + LPH, or the R64
+    // assignment above).
+    float c0 = 1.f, s0 = 0.f, c1 = 1.f, s1 = 0.f;
+    if constexpr (ROPE) {
+        if constexpr (R64) {
+            sincosf(fp / dn0, &s0, &c0);
+        } else {
+            if (lg < half) sincosf(fp / dn0, &s0, &c0);
+            if (lg + LPH < half) sincosf(fp / dn1, &s1, &c1);
+        }
+    }
 
     if constexpr (NORM) {
-        const float4 wv = ld4(wt + 4 * lg);
         const float ss = group_sum<LPH>(sumsq4(v));
         const float r = rsqrtf(ss / static_cast<float>(HD) + eps);
         v.x = v.x * (r * wv.x);
@@ -307,6 +325,8 @@ int qwen_attn_qk_norm_rope_rows(float* q, float* k, const float* q_weight, const
                "attn_qk_norm_rope: rope_dim %d invalid for head_dim %d", rope_dim, head_dim);
     QK_REQUIRE(rope_dim == 0 || theta > 0.0f, "attn_qk_norm_rope: theta must be positive");
     QK_REQUIRE(pos != nullptr || pos0 >= 0, "attn_qk_norm_rope: negative pos0 %d", pos0);
+    QK_REQUIRE(static_cast<int64_t>(rows) * (static_cast<int64_t>(q_heads) + k_heads) < (int64_t{1} << 31),
+               "attn_qk_norm_rope: rows x heads exceeds 2^31");
     if (rows == 0 || q_heads + k_heads == 0) return ok();
     QK_REQUIRE(q_heads == 0 || (q && q_weight), "attn_qk_norm_rope: null q or q_weight");
     QK_REQUIRE(k_heads == 0 || (k && k_weight), "attn_qk_norm_rope: null k or k_weight");

@@ -176,7 +176,7 @@ __global__ __launch_bounds__(kBlock) void gather_q4k(const uint8_t* __restrict__
                                                      int slot_chunks, float* __restrict__ out) {
     extern __shared__ uint4 stage[];
     const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
+    const int w = wave_in_block();
     const int t = blockIdx.x * kWavesPerBlock + w;
     const bool live = t < n_ids;  // wave-uniform
     const int64_t id = live ? (ids ? ids[t] : fixed_row) : 0;
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(kBlock) void gather_q6k(const uint8_t* __restrict__
                                                      int slot_chunks, float* __restrict__ out) {
     extern __shared__ uint4 stage[];
     const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
+    const int w = wave_in_block();
     const int t = blockIdx.x * kWavesPerBlock + w;
     const bool live = t < n_ids;
     const int64_t id = live ? (ids ? ids[t] : fixed_row) : 0;

@@ -9,6 +9,12 @@ namespace qk {
 
 constexpr int kWave = 64;
 
+// Index of the calling wave inside its workgroup, as a wave-uniform (scalar)
+// value: the compiler cannot prove threadIdx.x / 64 uniform by itself, and
+// without this the row / head arithmetic and the per-wave loads that depend on
+// it are done per lane (vector ALU, vector loads) instead of once per wave.
+__device__ __forceinline__ int wave_in_block() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 // ---------------------------------------------------------------- reductions
 // DPP row-local move (gfx9 encodings): quad_perm, row_half_mirror, row_mirror.
 template <int CTRL>
@@ -98,9 +104,14 @@ __device__ __forceinline__ float4 silu4(float4 x) {
     return make_float4(v[0], v[1], v[2], v[3]);
 }
 
-// 1 / (1 + expf(-x)) (src/cuda/moe.cu:94); evaluated once per row, so the
-// accurate form is kept.
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+// Sigmoid, 1 / (1 + expf(-x)) in the reference (src/cuda/moe.cu:94): the same
+// fast form and guard as silu (rcp(1 + 2^(-x log2 e)); the reference formula
+// below kSiluFastMin, where the reciprocal would approach the denormal range).
+__device__ __forceinline__ float sigmoid(float x) {
+    float r = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
+    if (x < kSiluFastMin) r = 1.0f / (1.0f + expf(-x));
+    return r;
+}
 
 // ---------------------------------------------------------------- bf16
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }

@@ -58,7 +58,7 @@ __global__ __launch_bounds__(W * kWave) void gdn_frontend_k4(const float* __rest
     static_assert(R >= 3, "a wave hands its last three rows to the next wave");
     __shared__ float4 halo[W][3][kWave];
     const int lane = threadIdx.x & 63;
-    const int wv = threadIdx.x >> 6;
+    const int wv = wave_in_block();
     const int cbase = (blockIdx.x % n_ctiles) * (4 * kWave);
     const int T0 = (blockIdx.x / n_ctiles) * (W * R);       // first row of the workgroup
     const int t0 = T0 + wv * R;                             // first row of this wave
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kBlock) void qk_l2_v4(float* q, float* k, int64_t s
     const int lane = threadIdx.x & 63;
     const int lg = lane % LPH;
     const int64_t total = static_cast<int64_t>(rows) * heads * 2;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + (threadIdx.x >> 6);
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave_in_block();
     if (wave * HPW >= total) return;
     const int64_t slot = wave * HPW + lane / LPH;
     const bool active = slot < total;
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(kBlock) void norm_gate_v4(const float* __restrict__
     constexpr int D = 4 * LPH;
     const int lane = threadIdx.x & 63;
     const int lg = lane % LPH;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + (threadIdx.x >> 6);
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave_in_block();
     const int64_t h_first = wave * (HPW * kGateUnroll);
     if (h_first >= heads_total) return;
     const float4 wv = ld4(w + 4 * lg);

@@ -16,7 +16,7 @@ namespace qk {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;  // 16-byte vectors in flight per thread
+constexpr int kUnroll = 2;  // 16-byte chunks of each input in flight per thread (best of 1/2/4/8 on gfx950)
 
 // ------------------------------------------------------------ bf16 SwiGLU
 // Eight bf16 pairs (one 16-byte chunk of g and of u) -> eight bf16 outputs,
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(kBlock) void swiglu_bf16_v8(const uint16_t* __restr
         for (int k = 0; k < kUnroll; ++k) {
             gv[k] = ld16_nt(g + 8 * (first + k * kBlock));
             uv[k] = ld16_nt(u + 8 * (first + k * kBlock));
-            if (SCALED) sc[k] = logits[(first + k * kBlock) / dim8];
+            if (SCALED) sc[k] = logits[static_cast<int>(first + k * kBlock) / dim8];  // n8 < 2^31 (host check)
         }
 #pragma unroll
         for (int k = 0; k < kUnroll; ++k)
@@ -124,7 +124,8 @@ unsigned stride_grid(int64_t items) { return static_cast<unsigned>(std::min<int6
 
 int swiglu_common(const uint16_t* g, const uint16_t* u, const float* logits, uint16_t* h, int64_t n, int dim,
                   hipStream_t s, const char* what) {
-    const bool vec = n % 8 == 0 && (!logits || dim % 8 == 0) && aligned16(g) && aligned16(u) && aligned16(h);
+    const bool vec = n % 8 == 0 && n / 8 < (int64_t{1} << 31) && (!logits || dim % 8 == 0) && aligned16(g) &&
+                     aligned16(u) && aligned16(h);
     if (vec) {
         const int64_t n8 = n / 8;
         const unsigned grid = blocks_for(n8, static_cast<int64_t>(kUnroll) * kBlock);

@@ -8,6 +8,7 @@
 // the scale (x is read from HBM once), reduces with DPP row ops plus four
 // readlanes, and moves data in 16-byte vectors.
 #include <algorithm>
+#include <type_traits>
 
 #include "capi_common.hpp"
 #include "device_common.hpp"
@@ -17,24 +18,38 @@ namespace {
 
 constexpr int kBlock = 256;
 
-// Waves per block: spread small row counts one wave per workgroup so they land
-// on different CUs; pack four rows per workgroup otherwise.
-inline int waves_per_block(int rows) { return rows >= 1024 ? 4 : 1; }
+// Launch shape. Few rows: one wave (one row) per workgroup, so rows land on
+// different CUs, each wave loading its own weights. Many rows: kStageWaves rows
+// per workgroup sharing one copy of the weight row in LDS, loaded once per
+// workgroup instead of once per wave (the per-wave reload is as many L2 bytes
+// as half a bf16 row's HBM traffic).
+constexpr int kStageWaves = 8;
+inline bool stage_weights(int rows) { return rows >= 1024; }
+
+// Cooperative copy of n4 float4 weights into LDS, then a barrier. Every wave of
+// the workgroup must call it (no early return before).
+__device__ __forceinline__ void stage_rows_weights(float4* wl, const float* __restrict__ w, int n4) {
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) wl[i] = ld4(w + 4 * i);
+    __syncthreads();
+}
 
 // ------------------------------------------------------------- fp32 rows
 // One wave per row; lane l holds float4 chunks l, l+64, ... (up to MAXC).
 // Lanes past the row end load a clamped in-row address and use zeros, so every
-// load is issued unconditionally; the weights are loaded with the row, ahead
-// of the reduction, so the second pass waits on nothing.
-template <int MAXC, bool GATED>
-__global__ __launch_bounds__(kBlock) void rmsnorm_rows_v4(const float* __restrict__ x, const float* __restrict__ gate,
-                                                          const float* __restrict__ w, float* __restrict__ out, int rows,
-                                                          int n, float eps) {
+// load is issued unconditionally; the weights are loaded with the row (or, when
+// staged, read from LDS after it), ahead of the reduction, so the second pass
+// waits on nothing. Waves past the last row clamp to it and leave after the
+// staging barrier.
+template <int MAXC, bool GATED, bool STAGE>
+__global__ __launch_bounds__(STAGE ? kStageWaves * kWave : kWave) void rmsnorm_rows_v4(
+    const float* __restrict__ x, const float* __restrict__ gate, const float* __restrict__ w, float* __restrict__ out,
+    int rows, int n, float eps) {
+    extern __shared__ float4 wl[];
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= rows) return;
+    const int row = blockIdx.x * (blockDim.x >> 6) + wave_in_block();
+    const bool live = row < rows;  // wave-uniform
     const int n4 = n >> 2;
-    const size_t base = static_cast<size_t>(row) * n;
+    const size_t base = static_cast<size_t>(live ? row : rows - 1) * n;
     float4 v[MAXC], wv[MAXC];
     float4 g[GATED ? MAXC : 1];
     const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -43,10 +58,16 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_v4(const float* __restric
         const int i = c * kWave + lane;
         const int ic = min(i, n4 - 1);
         v[c] = ld4_nt(x + base + 4 * ic);
-        wv[c] = ld4(w + 4 * ic);
+        if constexpr (!STAGE) wv[c] = ld4(w + 4 * ic);
         if constexpr (GATED) g[c] = ld4_nt(gate + base + 4 * ic);
         if (i >= n4) v[c] = zero;
     }
+    if constexpr (STAGE) {
+        stage_rows_weights(wl, w, n4);
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) wv[c] = wl[min(c * kWave + lane, n4 - 1)];
+    }
+    if (!live) return;
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) ss += sumsq4(v[c]);
@@ -103,27 +124,31 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_any(const float* __restri
 }
 
 // ------------------------------------------------- fused residual + RMSNorm, fp32
-template <int MAXC>
-__global__ __launch_bounds__(kBlock) void residual_rmsnorm_f32_v4(const float* __restrict__ x,
-                                                                  const float* __restrict__ b,
-                                                                  const float* __restrict__ w,
-                                                                  float* __restrict__ resid,
-                                                                  float* __restrict__ normed, int rows, int n,
-                                                                  float eps) {
+template <int MAXC, bool STAGE>
+__global__ __launch_bounds__(STAGE ? kStageWaves * kWave : kWave) void residual_rmsnorm_f32_v4(
+    const float* __restrict__ x, const float* __restrict__ b, const float* __restrict__ w, float* __restrict__ resid,
+    float* __restrict__ normed, int rows, int n, float eps) {
+    extern __shared__ float4 wl[];
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= rows) return;
+    const int row = blockIdx.x * (blockDim.x >> 6) + wave_in_block();
+    const bool live = row < rows;  // wave-uniform
     const int n4 = n >> 2;
-    const size_t base = static_cast<size_t>(row) * n;
+    const size_t base = static_cast<size_t>(live ? row : rows - 1) * n;
     float4 v[MAXC], wv[MAXC];
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
         const int ic = min(c * kWave + lane, n4 - 1);
         const float4 a = ld4_nt(x + base + 4 * ic);
         const float4 d = ld4_nt(b + base + 4 * ic);
-        wv[c] = ld4(w + 4 * ic);
+        if constexpr (!STAGE) wv[c] = ld4(w + 4 * ic);
         v[c] = make_float4(a.x + d.x, a.y + d.y, a.z + d.z, a.w + d.w);
     }
+    if constexpr (STAGE) {
+        stage_rows_weights(wl, w, n4);
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) wv[c] = wl[min(c * kWave + lane, n4 - 1)];
+    }
+    if (!live) return;
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
@@ -166,18 +191,16 @@ __global__ __launch_bounds__(kBlock) void residual_rmsnorm_f32_any(const float* 
 // ------------------------------------------------- fused residual + RMSNorm, bf16
 // 8 bf16 per 16-byte chunk; lane l holds chunks l, l+64, ... The rounded sum is
 // what the norm reads, so the result equals the unfused pair on bf16 buffers.
-template <int MAXC>
-__global__ __launch_bounds__(kBlock) void residual_rmsnorm_bf16_v8(const uint16_t* __restrict__ x,
-                                                                   const uint16_t* __restrict__ b,
-                                                                   const float* __restrict__ w,
-                                                                   uint16_t* __restrict__ resid,
-                                                                   uint16_t* __restrict__ normed, int rows, int n,
-                                                                   float eps) {
+template <int MAXC, bool STAGE>
+__global__ __launch_bounds__(STAGE ? kStageWaves * kWave : kWave) void residual_rmsnorm_bf16_v8(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ b, const float* __restrict__ w,
+    uint16_t* __restrict__ resid, uint16_t* __restrict__ normed, int rows, int n, float eps) {
+    extern __shared__ float4 wl[];
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= rows) return;
+    const int row = blockIdx.x * (blockDim.x >> 6) + wave_in_block();
+    const bool live = row < rows;  // wave-uniform
     const int n8 = n >> 3;
-    const size_t base = static_cast<size_t>(row) * n;
+    const size_t base = static_cast<size_t>(live ? row : rows - 1) * n;
     uint4 xa[MAXC], ba[MAXC];
     float4 w0[MAXC], w1[MAXC];
 #pragma unroll
@@ -185,9 +208,21 @@ __global__ __launch_bounds__(kBlock) void residual_rmsnorm_bf16_v8(const uint16_
         const int ic = min(c * kWave + lane, n8 - 1);
         xa[c] = ld16_nt(x + base + 8 * ic);
         ba[c] = ld16_nt(b + base + 8 * ic);
-        w0[c] = ld4(w + 8 * ic);
-        w1[c] = ld4(w + 8 * ic + 4);
+        if constexpr (!STAGE) {
+            w0[c] = ld4(w + 8 * ic);
+            w1[c] = ld4(w + 8 * ic + 4);
+        }
     }
+    if constexpr (STAGE) {
+        stage_rows_weights(wl, w, 2 * n8);
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) {
+            const int ic = min(c * kWave + lane, n8 - 1);
+            w0[c] = wl[2 * ic];
+            w1[c] = wl[2 * ic + 1];
+        }
+    }
+    if (!live) return;
     uint4 s[MAXC];
     float ss = 0.f;
 #pragma unroll
@@ -267,24 +302,35 @@ __global__ __launch_bounds__(kBlock) void copy_row(const float* __restrict__ src
 }
 
 // ------------------------------------------------------------- launchers
+// Calls launch(stage, grid, block, lds_bytes) with the row-kernel launch shape
+// for `rows`; stage is std::true_type / std::false_type (the kernel's STAGE).
+template <typename L>
+void launch_row_shape(int rows, size_t weight_bytes, L&& launch) {
+    if (stage_weights(rows))
+        launch(std::true_type{}, dim3(blocks_for(rows, kStageWaves)), dim3(kStageWaves * kWave), weight_bytes);
+    else
+        launch(std::false_type{}, dim3(rows), dim3(kWave), size_t{0});
+}
+
 template <bool GATED>
 int launch_rmsnorm(const float* x, const float* gate, const float* w, float* out, int rows, int n, float eps,
                    hipStream_t s) {
     const int n4 = n / 4;
     const bool vec = (n % 4 == 0) && aligned16(x) && aligned16(w) && aligned16(out) && (!GATED || aligned16(gate));
     if (vec && n4 <= 16 * kWave) {
-        const int wpb = waves_per_block(rows);
-        const dim3 grid(blocks_for(rows, wpb)), block(wpb * kWave);
-        if (n4 <= kWave)
-            rmsnorm_rows_v4<1, GATED><<<grid, block, 0, s>>>(x, gate, w, out, rows, n, eps);
-        else if (n4 <= 2 * kWave)
-            rmsnorm_rows_v4<2, GATED><<<grid, block, 0, s>>>(x, gate, w, out, rows, n, eps);
-        else if (n4 <= 4 * kWave)
-            rmsnorm_rows_v4<4, GATED><<<grid, block, 0, s>>>(x, gate, w, out, rows, n, eps);
-        else if (n4 <= 8 * kWave)
-            rmsnorm_rows_v4<8, GATED><<<grid, block, 0, s>>>(x, gate, w, out, rows, n, eps);
-        else
-            rmsnorm_rows_v4<16, GATED><<<grid, block, 0, s>>>(x, gate, w, out, rows, n, eps);
+        launch_row_shape(rows, size_t(n4) * 16, [&](auto stage, dim3 grid, dim3 block, size_t lds) {
+            constexpr bool S = decltype(stage)::value;
+            if (n4 <= kWave)
+                rmsnorm_rows_v4<1, GATED, S><<<grid, block, lds, s>>>(x, gate, w, out, rows, n, eps);
+            else if (n4 <= 2 * kWave)
+                rmsnorm_rows_v4<2, GATED, S><<<grid, block, lds, s>>>(x, gate, w, out, rows, n, eps);
+            else if (n4 <= 4 * kWave)
+                rmsnorm_rows_v4<4, GATED, S><<<grid, block, lds, s>>>(x, gate, w, out, rows, n, eps);
+            else if (n4 <= 8 * kWave)
+                rmsnorm_rows_v4<8, GATED, S><<<grid, block, lds, s>>>(x, gate, w, out, rows, n, eps);
+            else
+                rmsnorm_rows_v4<16, GATED, S><<<grid, block, lds, s>>>(x, gate, w, out, rows, n, eps);
+        });
     } else {
         rmsnorm_rows_any<GATED><<<rows, kBlock, 0, s>>>(x, gate, w, out, n, eps);
     }
@@ -346,18 +392,19 @@ int qwen_residual_rmsnorm_rows_f32(const float* x, const float* branch, const fl
     const bool vec = n % 4 == 0 && aligned16(x) && aligned16(branch) && aligned16(weight) && aligned16(resid) &&
                      aligned16(normed);
     if (vec && n4 <= 16 * kWave) {
-        const int wpb = waves_per_block(rows);
-        const dim3 grid(blocks_for(rows, wpb)), block(wpb * kWave);
-        if (n4 <= kWave)
-            residual_rmsnorm_f32_v4<1><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
-        else if (n4 <= 2 * kWave)
-            residual_rmsnorm_f32_v4<2><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
-        else if (n4 <= 4 * kWave)
-            residual_rmsnorm_f32_v4<4><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
-        else if (n4 <= 8 * kWave)
-            residual_rmsnorm_f32_v4<8><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
-        else
-            residual_rmsnorm_f32_v4<16><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+        launch_row_shape(rows, size_t(n4) * 16, [&](auto stage, dim3 grid, dim3 block, size_t lds) {
+            constexpr bool S = decltype(stage)::value;
+            if (n4 <= kWave)
+                residual_rmsnorm_f32_v4<1, S><<<grid, block, lds, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+            else if (n4 <= 2 * kWave)
+                residual_rmsnorm_f32_v4<2, S><<<grid, block, lds, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+            else if (n4 <= 4 * kWave)
+                residual_rmsnorm_f32_v4<4, S><<<grid, block, lds, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+            else if (n4 <= 8 * kWave)
+                residual_rmsnorm_f32_v4<8, S><<<grid, block, lds, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+            else
+                residual_rmsnorm_f32_v4<16, S><<<grid, block, lds, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+        });
     } else {
         residual_rmsnorm_f32_any<<<rows, kBlock, 0, s>>>(x, branch, weight, resid, normed, n, eps);
     }
@@ -374,16 +421,17 @@ int qwen_residual_rmsnorm_rows_bf16(const uint16_t* x, const uint16_t* branch, c
     const bool vec = n % 8 == 0 && aligned16(x) && aligned16(branch) && aligned16(weight) && aligned16(resid) &&
                      aligned16(normed);
     if (vec && n8 <= 8 * kWave) {
-        const int wpb = waves_per_block(rows);
-        const dim3 grid(blocks_for(rows, wpb)), block(wpb * kWave);
-        if (n8 <= kWave)
-            residual_rmsnorm_bf16_v8<1><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
-        else if (n8 <= 2 * kWave)
-            residual_rmsnorm_bf16_v8<2><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
-        else if (n8 <= 4 * kWave)
-            residual_rmsnorm_bf16_v8<4><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
-        else
-            residual_rmsnorm_bf16_v8<8><<<grid, block, 0, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+        launch_row_shape(rows, size_t(n8) * 32, [&](auto stage, dim3 grid, dim3 block, size_t lds) {
+            constexpr bool S = decltype(stage)::value;
+            if (n8 <= kWave)
+                residual_rmsnorm_bf16_v8<1, S><<<grid, block, lds, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+            else if (n8 <= 2 * kWave)
+                residual_rmsnorm_bf16_v8<2, S><<<grid, block, lds, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+            else if (n8 <= 4 * kWave)
+                residual_rmsnorm_bf16_v8<4, S><<<grid, block, lds, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+            else
+                residual_rmsnorm_bf16_v8<8, S><<<grid, block, lds, s>>>(x, branch, weight, resid, normed, rows, n, eps);
+        });
     } else {
         residual_rmsnorm_bf16_any<<<rows, kBlock, 0, s>>>(x, branch, weight, resid, normed, n, eps);
     }

@@ -70,7 +70,8 @@ def test_rmsnorm_unaligned_and_reference_fixture(oracle):
     assert np.max(np.abs(host(out) - np.array([3 * r_ * 2, 4 * r_ * 0.5], F32))) < 1e-5
 
 
-@pytest.mark.parametrize("rows,n", [(36, 2048), (3, 1001), (8, 8192)])
+# 1031 rows: the weight-staging launch shape with a partly filled last workgroup
+@pytest.mark.parametrize("rows,n", [(36, 2048), (3, 1001), (8, 8192), (1031, 2048)])
 def test_rmsnorm_gated(oracle, rows, n):
     r = rng(n)
     x = r.standard_normal((rows, n)).astype(F32)
@@ -95,7 +96,9 @@ def test_residual_rmsnorm_bf16_config_c3a(oracle):
     assert_bf16_close(host(normed), n_ref, what="C3a normed")
 
 
-@pytest.mark.parametrize("rows,n", [(7, 2048), (3, 1000), (2, 6000), (64, 4096)])
+# 1025 / 1030 rows: the weight-staging launch shape with a partly filled last workgroup
+@pytest.mark.parametrize("rows,n", [(7, 2048), (3, 1000), (2, 6000), (64, 4096), (1025, 4096), (1030, 1000),
+                                    (1027, 256)])
 def test_residual_rmsnorm_shapes(oracle, rows, n):
     r = rng(rows + n)
     x, b = r.standard_normal((rows, n)).astype(F32), r.standard_normal((rows, n)).astype(F32)
