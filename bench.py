@@ -172,7 +172,51 @@ def build_workload(torch, ops, synth):
             return lambda: ops.dequant_gather_rows(tab, kind, vocab * cols, ii, cols, oo)
         nb = 8192 * bpr + ids.numel() * 4 + out.numel() * 4
         ks.append(Kernel(name, f"C5 {kind} table 248320x2048, 8192 ids -> f32", nb, nb, mk_ga))
+        host[name]["device_table"] = tab
     return ks, host
+
+
+def build_next_rows(torch, ops, synth, host):
+    """Decode-step GEMVs (matmul_dispatch) at the model's real shapes
+    (include/config.hpp:40-60 of the reference: d_model 2048, vocab 248320, GDN
+    conv dim 8192, value dim 4096, 256 experts x 512): one token's x [K] f32 ->
+    y [M] f32. Bytes = weight bytes + 4K + 4M. Not part of the step."""
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(2048)
+    ks: list[Kernel] = []
+
+    def add(name, config, kind, tab, n_el, M, K, offsets, bpb, host_tab):
+        x = torch.from_numpy(rng.standard_normal(K).astype(np.float32)).to(dev)
+        y = torch.empty(M, dtype=torch.float32, device=dev)
+        wbytes = M * (K // 256) * bpb
+        nb = wbytes + 4 * K + 4 * M
+        copies = {}
+
+        def mk(i):
+            # launch i reads weight slice offsets[i % len] of copy i // len
+            c, o = divmod(i, len(offsets))
+            if c not in copies:
+                copies[c] = tab if c == 0 else tab.clone()
+            t, yy = copies[c], (y if i == 0 else torch.empty_like(y))
+            return lambda: ops.matmul_dispatch(t, kind, n_el, x, M, K, element_offset=offsets[o], out=yy)
+        k = Kernel(name, config, nb, nb, mk)
+        k.gemv = {"type": ops.GGML_TYPES[kind], "table": host_tab, "M": M, "K": K, "x": x.cpu().numpy()}
+        ks.append(k)
+
+    q6 = host["dequant_gather_q6_k"]
+    add("gemv_lm_head_q6_k", "Q6_K [248320 x 2048] x f32 [2048] (model.cpp:216 LM head)", "Q6_K",
+        q6["device_table"], 248320 * 2048, 248320, 2048, [0], 210, q6["table"])
+    t = synth.q4k_table(8192, 2048, seed_tensor=16)
+    add("gemv_qkv_q4_k", "Q4_K [8192 x 2048] x f32 [2048] (layer_gdn.cpp:83 qkv projection)", "Q4_K",
+        torch.from_numpy(t).to(dev), 8192 * 2048, 8192, 2048, [0], 144, t)
+    t = synth.q4k_table(2048, 4096, seed_tensor=20)
+    add("gemv_out_q4_k", "Q4_K [2048 x 4096] x f32 [4096] (layer_gdn.cpp:112 output projection)", "Q4_K",
+        torch.from_numpy(t).to(dev), 2048 * 4096, 2048, 4096, [0], 144, t)
+    t = synth.q4k_table(256 * 512, 2048, seed_tensor=24)
+    add("gemv_expert_q4_k", "Q4_K expert e of [256 x 512 x 2048] x f32 [2048] (layer_moe.cpp:131 gate, "
+        "element offset e*512*2048)", "Q4_K", torch.from_numpy(t).to(dev), 256 * 512 * 2048, 512, 2048,
+        [e * 512 * 2048 for e in range(256)], 144, t)
+    return ks
 
 
 def spin_cycles_per_ms(torch) -> float:
@@ -246,7 +290,7 @@ def measure_copy(torch, bench_lib, nbytes: int, spin: int, min_launches: int) ->
     return us
 
 
-def cpu_baseline(host, kernels, threads: int, budget_s: float):
+def cpu_baseline(host, kernels, threads: int, budget_s: float, gemv=None):
     """Times the oracle on a bounded sample of every config; returns per-kernel
     results and the aggregate GB/s (full-step bytes / extrapolated full-step time)."""
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -256,11 +300,18 @@ def cpu_baseline(host, kernels, threads: int, budget_s: float):
     sample = {"rmsnorm": 36, "qk_norm_rope": 64, "residual_rmsnorm_bf16": 512, "swiglu_bf16": 512,
               "shared_swiglu_sigmoid_bf16": 4096, "gdn_frontend": 256, "gdn_norm_gate": 512,
               "dequant_gather_q4_k": 1024, "dequant_gather_q6_k": 1024}
+    gemv = gemv or {}
+    for name, g in gemv.items():
+        sample[name] = min(g["M"], 4096)
     full = {"rmsnorm": 36, "qk_norm_rope": 512, "residual_rmsnorm_bf16": 4096, "swiglu_bf16": 4096,
             "shared_swiglu_sigmoid_bf16": 4096, "gdn_frontend": 4096, "gdn_norm_gate": 4096,
             "dequant_gather_q4_k": 8192, "dequant_gather_q6_k": 8192}
+    full.update({name: g["M"] for name, g in gemv.items()})
 
     def runner(name, rows, th):
+        if name.startswith("gemv_"):
+            g = gemv[name]
+            return lambda: orc.gemv(g["table"], g["type"], g["x"], rows, g["K"], threads=th)
         c = host[name]
         if name == "rmsnorm":
             return lambda: orc.rmsnorm_rows(c["x"][:rows], c["w"], threads=th)
@@ -319,6 +370,7 @@ def main() -> int:
     ap.add_argument("--kernels", default="", help="comma list: only these kernels (profiling runs)")
     ap.add_argument("--no-per-kernel", action="store_true", help="skip the per-kernel and copy measurements")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-next", action="store_true", help="skip the decode GEMV measurements (not part of the step)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
     ap.add_argument("--json-out", default="", help="also write the JSON line to this file")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
@@ -349,31 +401,32 @@ def main() -> int:
     spin = int(spin_cycles_per_ms(torch) * 2.0)
 
     # ---- the step: K graph replays (the contract)
-    base = [k.make(0) for k in kernels]
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        for f in base:
-            f()
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for f in base:
-            f()
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        graph.replay()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_per_step = wall / args.steps * 1e3
-    bytes_step = sum(k.bytes for k in kernels)
-    value = bytes_step / (ms_per_step * 1e-3) / 1e9
-    print(f"# step: {ms_per_step * 1e3:.1f} us, {value:.1f} GB/s aggregate", file=sys.stderr, flush=True)
-    del graph
+    ms_per_step, value, bytes_step = 0.0, 0.0, sum(k.bytes for k in kernels)
+    if kernels:  # (empty only in a profiling run of the decode GEMVs)
+        base = [k.make(0) for k in kernels]
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for f in base:
+                f()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for f in base:
+                f()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms_per_step = wall / args.steps * 1e3
+        value = bytes_step / (ms_per_step * 1e-3) / 1e9
+        print(f"# step: {ms_per_step * 1e3:.1f} us, {value:.1f} GB/s aggregate", file=sys.stderr, flush=True)
+        del graph
 
     if args.calibrate_copy:
         n = args.calibrate_copy // 16 * 16
@@ -400,9 +453,22 @@ def main() -> int:
         copy_big = measure_copy(torch, bench_lib, big, spin, 16)
         print(f"# copy 1 GiB: {big / copy_big / 1e3:.1f} GB/s", file=sys.stderr, flush=True)
 
+    # ---- decode GEMVs (matmul_dispatch): measured alone, not part of the step
+    nxt = []
+    if not args.no_next and not args.no_per_kernel:
+        nxt = build_next_rows(torch, ops, synth, host)
+        if args.kernels:
+            nxt = [k for k in nxt if k.name in keep]
+        for k in nxt:
+            k.us = measure_kernel(torch, k, spin, args.launches)
+            k.copy_us = measure_copy(torch, bench_lib, k.bytes, spin, args.launches)
+            print(f"# {k.name:28s} {k.us:9.2f} us  {k.bytes / k.us / 1e3:7.1f} GB/s ({k.bytes / k.us / 1e3 / PEAK_GBPS:6.1%})"
+                  f"   copy of same bytes {k.copy_us:8.2f} us {k.bytes / k.copy_us / 1e3:7.1f} GB/s",
+                  file=sys.stderr, flush=True)
+
     # ---- roofline of the dominant kernel
     roofline = None
-    if not args.no_per_kernel:
+    if not args.no_per_kernel and kernels:
         dom = max(kernels, key=lambda k: k.us)
         traffic = None
         tf = ROOT / "profiles" / "traffic.json"
@@ -427,6 +493,19 @@ def main() -> int:
                "per_kernel": {n: {"gbps": round(p["gbps"], 3), "us_per_call": round(p["us_per_call"], 1)}
                               for n, p in per.items()}}
 
+    next_rows = None
+    if nxt:
+        cpu_next = {}
+        if not args.no_cpu:
+            threads = max(1, min(16, os.cpu_count() or 1))
+            cpu_next, _ = cpu_baseline(host, nxt, threads, args.cpu_seconds / 3, gemv={k.name: k.gemv for k in nxt})
+        next_rows = {
+            k.name: {"config": k.config, "bytes": k.bytes, "us_per_call": round(k.us, 3),
+                     "gbps": round(k.bytes / k.us / 1e3, 1), "frac_peak": round(k.bytes / k.us / 1e3 / PEAK_GBPS, 4),
+                     "copy_same_bytes_us": round(k.copy_us, 3),
+                     "cpu_gbps": round(cpu_next[k.name]["gbps"], 3) if k.name in cpu_next else None}
+            for k in nxt}
+
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -449,6 +528,7 @@ def main() -> int:
                      "copy_same_bytes_us": round(k.copy_us, 3)} for k in kernels},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "next_rows": next_rows,
     }
     text = json.dumps(line)
     print(text, flush=True)

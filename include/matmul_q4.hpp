@@ -1,7 +1,9 @@
-// Drop-in for the dequant entry points of include/matmul_q4.hpp of the
-// reference (sahan974/qwen-3.5-cuda, :10 and :24-30), hipStream_t in place of
-// cudaStream_t. dequantize_row throws std::runtime_error with the reference's
-// messages ("cannot dequantize tensor '<name>'", "row is outside tensor '<name>'").
+// Drop-in for include/matmul_q4.hpp of the reference (sahan974/qwen-3.5-cuda,
+// :10-30), hipStream_t in place of cudaStream_t. matmul_dispatch and
+// dequantize_row throw std::runtime_error with the reference's messages
+// ("tensor '<name>' is not loaded", "unsupported GGML type for tensor '<name>'",
+// "GEMV shape exceeds tensor '<name>'"; "cannot dequantize tensor '<name>'",
+// "row is outside tensor '<name>'").
 #ifndef QWEN35_MATMUL_Q4_HPP
 #define QWEN35_MATMUL_Q4_HPP
 
@@ -15,6 +17,11 @@ namespace qwen {
 
 // True for F32, F16, BF16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K.  ref: include/matmul_q4.hpp:10
 bool matmul_type_supported(GgmlType type);
+
+// y[m] = sum_k W[element_offset + m*K + k] * x[k], m < M (x, y device fp32).
+// ref: include/matmul_q4.hpp:13-21
+void matmul_dispatch(const QuantTensor& weight, const float* x, float* y, int M, int K, hipStream_t stream = nullptr,
+                     uint64_t element_offset = 0);
 
 // out[i] = element (row * cols + i) of `tensor`.  ref: include/matmul_q4.hpp:24-30
 void dequantize_row(const QuantTensor& tensor, float* out, int row, int cols, hipStream_t stream = nullptr);

@@ -178,6 +178,24 @@ int qwen_dequantize_row(const void* data, int type, uint64_t num_elements, float
 int qwen_dequant_gather_rows(const void* table, int type, uint64_t num_elements,
                              const int32_t* ids, int n_ids, int cols, float* out, void* stream);
 
+/* ================================================================== quantized GEMV
+ * ref: include/matmul_q4.hpp:10-21, src/cuda/matmul_q4.cu:140-167 (gemv_kernel), :179-207 */
+
+/* Returns 1 if `type` has a GEMV path (the dequant types).
+ * ref: include/matmul_q4.hpp:10 (matmul_type_supported), src/cuda/matmul_q4.cu:179-183 */
+int qwen_matmul_type_supported(int type);
+
+/* y[m] = sum_{k<K} W[element_offset + m*K + k] * x[k] for m < M: weight is the
+ * device pointer of a GGML tensor of `type` holding num_elements elements
+ * (row-major, K elements per row), x fp32 [K], y fp32 [M], fp32 accumulation.
+ * Statuses, in the reference's order of checks: weight NULL ->
+ * QWEN_STATUS_INVALID_ARGUMENT ("tensor is not loaded"); type without a path ->
+ * QWEN_STATUS_UNSUPPORTED_TYPE; M <= 0, K <= 0 or element_offset + M*K past
+ * num_elements -> QWEN_STATUS_OUT_OF_RANGE ("GEMV shape exceeds tensor").
+ * ref: include/matmul_q4.hpp:13-21 (matmul_dispatch), src/cuda/matmul_q4.cu:185-207 */
+int qwen_matmul_dispatch(const void* weight, int type, uint64_t num_elements, const float* x,
+                         float* y, int M, int K, uint64_t element_offset, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -517,4 +517,26 @@ void or_dequant_span(const uint8_t* data, int type, uint64_t start, int count, f
     for (int i = 0; i < count; ++i) out[i] = or_dequant(data, type, start + static_cast<uint64_t>(i));
 }
 
+// ---------------------------------------------------------------- quantized GEMV
+
+// y[m] = sum_k dequant(W, element_offset + m*K + k) * x[k], m < M
+//                                                    -- src/cuda/matmul_q4.cu:140-167,185-207
+// The reference sums fp32 products in an order fixed by its launch shape
+// (256 strided partial sums, then a shuffle tree); the oracle takes every
+// product exactly (a float times a float fits a double), sums in double and
+// rounds once.
+void or_gemv(const uint8_t* w, int type, const float* x, float* y, int M, int K, uint64_t element_offset,
+             int threads) {
+    parallel_for(M, threads, [&](int64_t lo, int64_t hi) {
+        for (int64_t m = lo; m < hi; ++m) {
+            const uint64_t base = element_offset + static_cast<uint64_t>(m) * static_cast<uint64_t>(K);
+            double s = 0.0;
+            for (int k = 0; k < K; ++k)
+                s += static_cast<double>(or_dequant(w, type, base + static_cast<uint64_t>(k))) *
+                     static_cast<double>(x[k]);
+            y[m] = static_cast<float>(s);
+        }
+    });
+}
+
 }  // extern "C"

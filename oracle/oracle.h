@@ -97,6 +97,10 @@ void or_dequant_gather(const uint8_t* table, int type, const int32_t* ids, int n
                        int cols, float* out, int threads);                /* matmul_q4.cu:169-173,209-227 */
 void or_dequant_span(const uint8_t* data, int type, uint64_t start, int count, float* out);
 
+/* ---- quantized GEMV ---- */
+void or_gemv(const uint8_t* w, int type, const float* x, float* y, int M, int K,
+             uint64_t element_offset, int threads);             /* matmul_q4.cu:140-167,185-207 */
+
 #ifdef __cplusplus
 }
 #endif

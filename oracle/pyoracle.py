@@ -56,6 +56,7 @@ _SIGS = {
     "or_type_supported": ([_I], _I),
     "or_dequant_gather": ([_P, _I, _P, _I, _I, _P, _I], None),
     "or_dequant_span": ([_P, _I, _U64, _I, _P], None),
+    "or_gemv": ([_P, _I, _P, _P, _I, _I, _U64, _I], None),
 }
 
 _lib = None
@@ -281,3 +282,13 @@ def dequant_span(data, ggml_type: int, start: int, count: int):
     out = np.empty(count, dtype=F32)
     lib().or_dequant_span(_p(data), ggml_type, start, count, _p(out))
     return out
+
+
+# ---------------------------------------------------------------- quantized GEMV
+def gemv(weight, ggml_type: int, x, M: int, K: int, element_offset: int = 0, threads=1):
+    """y[m] = sum_k W[element_offset + m*K + k] * x[k] (exact products, double sum)."""
+    weight, x = _c(weight, U8), _c(x, F32)
+    assert x.size >= K
+    y = np.empty(M, dtype=F32)
+    lib().or_gemv(_p(weight), ggml_type, _p(x), _p(y), M, K, element_offset, threads)
+    return y

@@ -103,6 +103,26 @@ void cpu_checks() {
                  "dequantize_row negative row");
     expect(qwen::matmul_type_supported(qwen::GgmlType::Q6_K) && !qwen::matmul_type_supported(qwen::GgmlType::Q2_K),
            "matmul_type_supported");
+
+    // matmul_dispatch validation, in the reference's order (src/cuda/matmul_q4.cu:187-195)
+    qwen::QuantTensor wq;
+    wq.name = "blk.0.attn_q.weight";
+    wq.type = qwen::GgmlType::Q4_K;
+    wq.num_elements = 4 * 512;
+    wq.device_ptr = nullptr;
+    expect_throw([&] { qwen::matmul_dispatch(wq, dummy.data(), dummy.data(), 4, 512); },
+                 "tensor 'blk.0.attn_q.weight' is not loaded", "matmul_dispatch unloaded tensor");
+    wq.device_ptr = dummy.data();
+    wq.type = qwen::GgmlType::Q4_1;
+    expect_throw([&] { qwen::matmul_dispatch(wq, dummy.data(), dummy.data(), 4, 512); },
+                 "unsupported GGML type for tensor 'blk.0.attn_q.weight'", "matmul_dispatch unsupported type");
+    wq.type = qwen::GgmlType::Q4_K;
+    expect_throw([&] { qwen::matmul_dispatch(wq, dummy.data(), dummy.data(), 5, 512); },
+                 "GEMV shape exceeds tensor 'blk.0.attn_q.weight'", "matmul_dispatch rows past the end");
+    expect_throw([&] { qwen::matmul_dispatch(wq, dummy.data(), dummy.data(), 2, 512, nullptr, 1024 + 256); },
+                 "GEMV shape exceeds tensor 'blk.0.attn_q.weight'", "matmul_dispatch offset past the end");
+    expect_throw([&] { qwen::matmul_dispatch(wq, dummy.data(), dummy.data(), 0, 512); },
+                 "GEMV shape exceeds tensor 'blk.0.attn_q.weight'", "matmul_dispatch M = 0");
     expect(qwen::calculate_tensor_bytes(qwen::GgmlType::Q4_K, 2048) == 8 * 144 &&
                qwen::calculate_tensor_bytes(qwen::GgmlType::Q6_K, 100) == 0,
            "calculate_tensor_bytes");
@@ -143,6 +163,20 @@ void check_block(qwen::GgmlType type, const char* name, const std::vector<uint8_
     qwen::dequantize_row(t, out, 0, static_cast<int>(expected.size()));
     const std::vector<float> got = to_host(out, expected.size());
     expect(max_abs_diff(got, expected) < 1e-6f, std::string("dequantize_row ") + name + " fixture");
+    // matmul_dispatch over the same block as one row: x = 1, 2, 1, 2, ... gives
+    // y = sum(w) + sum(w at odd k).
+    std::vector<float> x(expected.size());
+    double ref = 0.0, mag = 0.0;
+    for (size_t k = 0; k < x.size(); ++k) {
+        x[k] = (k & 1) ? 2.0f : 1.0f;
+        ref += static_cast<double>(expected[k]) * x[k];
+        mag += std::fabs(static_cast<double>(expected[k]) * x[k]);
+    }
+    float* dx = to_device(x);
+    qwen::matmul_dispatch(t, dx, out, 1, static_cast<int>(x.size()));
+    const float y = to_host(out, 1)[0];
+    expect(std::fabs(y - ref) <= 1e-5 * mag, std::string("matmul_dispatch ") + name + " fixture row");
+    (void)hipFree(dx);
     (void)hipFree(out);
     (void)hipFree(t.device_ptr);
 }

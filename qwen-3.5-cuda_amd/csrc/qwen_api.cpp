@@ -123,7 +123,20 @@ void shared_swiglu_sigmoid_rows_bf16(const uint16_t* gate, const uint16_t* up, c
 }
 
 // ---- matmul_q4.hpp
-bool matmul_type_supported(GgmlType type) { return qwen_type_supported(static_cast<int>(type)) != 0; }
+bool matmul_type_supported(GgmlType type) { return qwen_matmul_type_supported(static_cast<int>(type)) != 0; }
+
+void matmul_dispatch(const QuantTensor& w, const float* x, float* y, int M, int K, hipStream_t stream,
+                     uint64_t element_offset) {
+    const int status = qwen_matmul_dispatch(w.device_ptr, static_cast<int>(w.type), w.num_elements, x, y, M, K,
+                                            element_offset, st(stream));
+    // Reference messages, src/cuda/matmul_q4.cu:187-195.
+    if (status == QWEN_STATUS_INVALID_ARGUMENT && !w.device_ptr)
+        throw std::runtime_error("tensor '" + w.name + "' is not loaded");
+    if (status == QWEN_STATUS_UNSUPPORTED_TYPE)
+        throw std::runtime_error("unsupported GGML type for tensor '" + w.name + "'");
+    if (status == QWEN_STATUS_OUT_OF_RANGE) throw std::runtime_error("GEMV shape exceeds tensor '" + w.name + "'");
+    check(status);
+}
 
 void dequantize_row(const QuantTensor& tensor, float* out, int row, int cols, hipStream_t stream) {
     const int status = qwen_dequantize_row(tensor.device_ptr, static_cast<int>(tensor.type), tensor.num_elements, out,

@@ -54,6 +54,8 @@ SIGNATURES: dict[str, list] = {
     "qwen_type_supported": [_I],
     "qwen_dequantize_row": [_P, _I, _U64, _P, _I, _I, _P],
     "qwen_dequant_gather_rows": [_P, _I, _U64, _P, _I, _I, _P, _P],
+    "qwen_matmul_type_supported": [_I],
+    "qwen_matmul_dispatch": [_P, _I, _U64, _P, _P, _I, _I, _U64, _P],
 }
 
 _RESTYPES = {"qwen_last_error": ctypes.c_char_p, "qwen_status_name": ctypes.c_char_p}

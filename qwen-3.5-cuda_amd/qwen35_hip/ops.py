@@ -277,3 +277,22 @@ def dequantize_row(table, ggml_type, num_elements: int, row: int, cols: int, out
     _same((cols,), out)
     check(load().qwen_dequantize_row(_p(table), t, num_elements, _p(out), row, cols, _stream(stream)))
     return out
+
+
+# ------------------------------------------------------------------ quantized GEMV
+def matmul_dispatch(weight, ggml_type, num_elements: int, x, M: int, K: int, element_offset: int = 0, out=None,
+                    stream=None):
+    """weight: uint8 device tensor of GGML blocks; x float32 [K] -> y float32 [M],
+    y[m] = sum_k W[element_offset + m*K + k] * x[k]."""
+    _dev(weight, dtype=torch.uint8)
+    _dev(x, dtype=torch.float32)
+    if x.numel() < K:
+        raise ValueError(f"x has {x.numel()} elements, K = {K}")
+    t = GGML_TYPES[ggml_type] if isinstance(ggml_type, str) else int(ggml_type)
+    out = torch.empty(M, dtype=torch.float32, device=x.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    if out.numel() < M:
+        raise ValueError(f"out has {out.numel()} elements, M = {M}")
+    check(load().qwen_matmul_dispatch(_p(weight), t, num_elements, _p(x), _p(out), M, K, element_offset,
+                                      _stream(stream)))
+    return out

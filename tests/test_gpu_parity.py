@@ -344,3 +344,71 @@ def test_dequantize_row(oracle, kind, cols, row):
         table = r.standard_normal(n_el).astype(np.float16).view(np.uint8)
     got = host(ops.dequantize_row(dev(table), kind, n_el, row, cols))
     assert_bits_equal(got, oracle.dequant_span(table, t, row * cols, cols), f"{kind} row {row}")
+
+
+# ------------------------------------------------------------------ quantized GEMV
+def _gemv_weight(kind: str, rows: int, cols: int, r) -> np.ndarray:
+    """GGML bytes of a rows x cols tensor: the C5 table generators for Q4_K/Q6_K
+    (fp16 d, dmin ~ U(0, 0.01)), random finite blocks or floats otherwise."""
+    import ggml_blocks
+
+    t = ops.GGML_TYPES[kind]
+    if kind == "Q4_K" and cols % 256 == 0:
+        return synth.q4k_table(rows, cols, seed_tensor=cols % 7)
+    if kind == "Q6_K" and cols % 256 == 0:
+        return synth.q6k_table(rows, cols, seed_tensor=cols % 5)
+    if t in ggml_blocks.BLOCK:
+        return ggml_blocks.random_blocks(r, t, rows * cols // ggml_blocks.BLOCK[t][0])
+    dt = {"F32": np.float32, "F16": np.float16}.get(kind)
+    if dt is not None:
+        return r.standard_normal(rows * cols).astype(dt).view(np.uint8)
+    return synth.to_bf16_bits(r.standard_normal(rows * cols).astype(np.float32)).view(np.uint8)
+
+
+# (type, tensor rows, K, M, first row): fast-path launch shapes (8/4/2/1 units
+# per wave, 2 slices per row, 2/4/8 rows per unit with ragged tails, an expert
+# slice by element offset) and the generic path (K not a multiple of 2048 or a
+# divisor of it, Q6_K offsets off the 8-block grid, the other GGML types).
+GEMV_CASES = [
+    ("Q4_K", 40000, 2048, 40000, 0), ("Q4_K", 20000, 2048, 20000, 0), ("Q4_K", 9000, 2048, 9000, 0),
+    ("Q4_K", 2048, 4096, 2048, 0), ("Q4_K", 1001, 512, 1001, 0), ("Q4_K", 37, 256, 37, 0),
+    ("Q4_K", 513, 1024, 513, 0), ("Q4_K", 4 * 512, 2048, 512, 2 * 512),
+    ("Q6_K", 40000, 2048, 40000, 0), ("Q6_K", 4096, 4096, 4096, 0), ("Q6_K", 4 * 512, 512, 512, 3 * 512),
+    ("Q6_K", 1008, 512, 1001, 0), ("Q6_K", 64, 256, 61, 0), ("Q6_K", 200, 1024, 100, 1),
+    ("Q4_K", 64, 768, 64, 0), ("Q6_K", 64, 1280, 64, 0),
+    ("Q8_0", 300, 2048, 300, 0), ("Q4_0", 100, 1024, 100, 0), ("Q5_0", 100, 512, 100, 0),
+    ("Q5_K", 64, 2048, 64, 0), ("F32", 256, 2048, 256, 0), ("F16", 100, 1000, 100, 0), ("BF16", 77, 2048, 77, 0),
+]
+
+
+@pytest.mark.parametrize("kind,rows,K,M,row0", GEMV_CASES)
+def test_matmul_dispatch(oracle, kind, rows, K, M, row0):
+    t = ops.GGML_TYPES[kind]
+    r = rng(rows * 7 + K + M)
+    w = _gemv_weight(kind, rows, K, r)
+    x = r.standard_normal(K).astype(F32)
+    n_el, off = rows * K, row0 * K
+    got = host(ops.matmul_dispatch(dev(w), t, n_el, dev(x), M, K, element_offset=off))
+    ref = oracle.gemv(w, t, x, M, K, element_offset=off, threads=THREADS)
+    assert_f32_close(got, ref, group=M, what=f"{kind} {M}x{K} @ row {row0}")
+
+
+def test_matmul_dispatch_reuses_x_and_checks_shapes(oracle):
+    """Output rows past M stay untouched; bad shapes and types are rejected with
+    the reference's conditions (src/cuda/matmul_q4.cu:187-195)."""
+    from qwen35_hip._lib import QwenError
+
+    rows, K = 48, 2048
+    w = synth.q4k_table(rows, K)
+    x = rng(3).standard_normal(K).astype(F32)
+    out = torch.full((rows + 5,), 7.0, device="cuda")
+    ops.matmul_dispatch(dev(w), "Q4_K", rows * K, dev(x), rows, K, out=out)
+    got = host(out)
+    assert_f32_close(got[:rows], oracle.gemv(w, 12, x, rows, K), group=rows)
+    assert np.all(got[rows:] == 7.0)
+    dw, dx = dev(w), dev(x)
+    for kw in (dict(M=rows + 1), dict(M=0), dict(M=rows, element_offset=K)):
+        with pytest.raises(QwenError):
+            ops.matmul_dispatch(dw, "Q4_K", rows * K, dx, kw.get("M", rows), K, element_offset=kw.get("element_offset", 0))
+    with pytest.raises(QwenError):
+        ops.matmul_dispatch(dw, 3, rows * K, dx, rows, K)  # Q4_1: no path

@@ -106,6 +106,54 @@ def test_dequant_gather_indexing(oracle, ggml_type):
     assert_bits_equal(oracle.dequant_gather(raw, ggml_type, ids, cols, threads=4), full[ids], "gather mt")
 
 
+# ------------------------------------------------------------------ quantized GEMV
+def _gemv_tensor(rng, ggml_type, n_el):
+    """Raw GGML bytes of n_el elements and the same tensor dequantized by ggml's loops."""
+    if ggml_type == 0:
+        dense = rng.standard_normal(n_el).astype(F32)
+        return dense.view(np.uint8), dense
+    elems = ggml_blocks.BLOCK[ggml_type][0]
+    raw = ggml_blocks.random_blocks(rng, ggml_type, n_el // elems)
+    return raw, ggml_blocks.DEQUANT[ggml_type](raw)
+
+
+@pytest.mark.parametrize("ggml_type", [12, 14, 8, 2, 0])
+def test_gemv_matches_float64_matmul(oracle, ggml_type):
+    """W (ggml block loops) @ x by numpy in float64: the oracle's single rounding
+    of the exact sum must land within one float ulp of it."""
+    rng = np.random.default_rng(100 + ggml_type)
+    M, K = 24, 512
+    raw, dense = _gemv_tensor(rng, ggml_type, M * K)
+    x = rng.standard_normal(K).astype(F32)
+    exact = dense.reshape(M, K).astype(np.float64) @ x.astype(np.float64)
+    got = oracle.gemv(raw, ggml_type, x, M, K)
+    ulp = np.spacing(np.abs(exact).astype(F32)).astype(np.float64)
+    assert np.all(np.abs(got.astype(np.float64) - exact) <= ulp), ggml_type
+    assert np.array_equal(oracle.gemv(raw, ggml_type, x, M, K, threads=4), got)
+
+
+@pytest.mark.parametrize("ggml_type", [12, 14])
+def test_gemv_one_hot_columns_and_offset(oracle, ggml_type):
+    """x = e_j reads column j of W exactly; element_offset selects whole rows
+    (src/layer_moe.cpp:131-138 slices experts by element offset)."""
+    rng = np.random.default_rng(7 + ggml_type)
+    E, M, K = 3, 8, 512
+    raw, dense = _gemv_tensor(rng, ggml_type, E * M * K)
+    W = dense.reshape(E, M, K)
+    for j in (0, 1, 31, 32, 255, 256, 511):
+        x = np.zeros(K, dtype=F32)
+        x[j] = 1.0
+        got = oracle.gemv(raw, ggml_type, x, E * M, K)
+        assert np.array_equal(got, W.reshape(E * M, K)[:, j]), j
+    x = rng.standard_normal(K).astype(F32)
+    full = oracle.gemv(raw, ggml_type, x, E * M, K)
+    for e in range(E):
+        part = oracle.gemv(raw, ggml_type, x, M, K, element_offset=e * M * K)
+        assert_bits_equal(part, full[e * M:(e + 1) * M], f"expert {e}")
+    # linearity in x: W(2x) = 2 Wx exactly (scaling by 2 is exact throughout)
+    assert_bits_equal(oracle.gemv(raw, ggml_type, 2 * x, E * M, K), 2 * full, "2x")
+
+
 def test_type_supported(oracle):
     for t in range(40):
         assert oracle.type_supported(t) == (t in (0, 1, 2, 6, 8, 12, 13, 14, 30))
