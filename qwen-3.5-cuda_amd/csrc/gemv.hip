@@ -279,10 +279,9 @@ void launch_kquant(const uint8_t* w, const float* x, float* y, int M, int nb, ui
 template <int TYPE>
 void dispatch_kquant(const uint8_t* w, const float* x, float* y, int M, int nb, uint64_t ub0, int groups,
                      uint64_t tensor_bytes, hipStream_t s) {
-    // Units per wave: enough waves to fill 256 CUs several times over.
-    if (groups >= 8 * 4096)
-        launch_kquant<TYPE, 8>(w, x, y, M, nb, ub0, groups, tensor_bytes, s);
-    else if (groups >= 4 * 4096)
+    // Units per wave: enough waves to fill 256 CUs several times over. More than
+    // 4 units per wave measured slower (fewer waves per SIMD to hide latency).
+    if (groups >= 4 * 4096)
         launch_kquant<TYPE, 4>(w, x, y, M, nb, ub0, groups, tensor_bytes, s);
     else if (groups >= 2 * 4096)
         launch_kquant<TYPE, 2>(w, x, y, M, nb, ub0, groups, tensor_bytes, s);

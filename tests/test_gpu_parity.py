@@ -378,6 +378,10 @@ GEMV_CASES = [
     ("Q4_K", 64, 768, 64, 0), ("Q6_K", 64, 1280, 64, 0),
     ("Q8_0", 300, 2048, 300, 0), ("Q4_0", 100, 1024, 100, 0), ("Q5_0", 100, 512, 100, 0),
     ("Q5_K", 64, 2048, 64, 0), ("F32", 256, 2048, 256, 0), ("F16", 100, 1000, 100, 0), ("BF16", 77, 2048, 77, 0),
+    ("Q8_0", 50, 96, 50, 0), ("F32", 33, 7, 33, 0),  # K < 256
+    # persistent-grid shapes: 2 / 4 rows per tile, 2 slices held in VGPRs, x reloaded (K > 4096)
+    ("Q4_K", 5000, 2048, 5000, 0), ("Q4_K", 9000, 4096, 9000, 0), ("Q4_K", 300, 8192, 300, 0),
+    ("Q6_K", 5000, 2048, 5000, 0), ("Q6_K", 9000, 4096, 9000, 0), ("Q6_K", 300, 8192, 300, 0),
 ]
 
 
