@@ -177,7 +177,9 @@ def build_workload(torch, ops, synth):
 
 
 def build_next_rows(torch, ops, synth, host):
-    """Decode-step GEMVs (matmul_dispatch) at the model's real shapes
+    """The next rows of the path, measured alone (not part of the step). GDN
+    recurrent state update at the Qwen3.5 GDN shape; decode-step GEMVs
+    (matmul_dispatch) at the model's real shapes
     (include/config.hpp:40-60 of the reference: d_model 2048, vocab 248320, GDN
     conv dim 8192, value dim 4096, 256 experts x 512): one token's x [K] f32 ->
     y [M] f32. Bytes = weight bytes + 4K + 4M. Not part of the step."""
@@ -212,6 +214,34 @@ def build_next_rows(torch, ops, synth, host):
     t = synth.q4k_table(2048, 4096, seed_tensor=20)
     add("gemv_out_q4_k", "Q4_K [2048 x 4096] x f32 [4096] (layer_gdn.cpp:112 output projection)", "Q4_K",
         torch.from_numpy(t).to(dev), 2048 * 4096, 2048, 4096, [0], 144, t)
+    # GDN recurrent state (gdn.cu:108-172): 16 key / 32 value heads of 128, state 2 MB.
+    kh, vh, dk, dv = 16, 32, 128, 128
+    c = host["gdn_frontend"]
+    for rows in (1, 4096):
+        # Front-end-shaped rows [rows x 8192]: q | k scaled to about unit norm per
+        # head so that the recurrence stays bounded over 4096 steps.
+        qkv_h = np.array(c["x"][:rows], dtype=np.float32)
+        qkv_h[:, :2 * kh * dk] *= dk ** -0.5
+        qkv = torch.from_numpy(np.ascontiguousarray(qkv_h)).to(dev)
+        beta = torch.full((rows, vh), 0.5, device=dev)
+        decay = torch.full((rows, vh), 0.95, device=dev)
+        st0 = torch.from_numpy((0.1 * rng.standard_normal(vh * dk * dv)).astype(np.float32)).to(dev)
+        o = torch.empty((rows, vh * dv), dtype=torch.float32, device=dev)
+        nb = 2 * st0.numel() * 4 + rows * (2 * kh * dk + 2 * vh * dv + 2 * vh) * 4
+
+        def mk_gdn(i, qkv=qkv, beta=beta, decay=decay, st0=st0, o=o, rows=rows):
+            ss = st0 if i == 0 else st0.clone()
+            qq = qkv if i == 0 or rows == 1 else qkv.clone()
+            oo = o if i == 0 else torch.empty_like(o)
+            return lambda: ops.gdn_recurrent_rows(ss, qq, beta, decay, kh, vh, dk, dv, oo)
+        name = "gdn_recurrent_step" if rows == 1 else "gdn_recurrent_rows_4096"
+        desc = ("one decode step, state [32 x 128 x 128] f32 (layer_gdn.cpp:100)" if rows == 1 else
+                "4096 sequential steps in one launch over front-end rows [4096 x 8192] f32")
+        k = Kernel(name, desc, nb, nb, mk_gdn)
+        k.gdn = {"rows": rows, "qkv": qkv_h, "beta": np.full((rows, vh), 0.5, np.float32),
+                 "decay": np.full((rows, vh), 0.95, np.float32), "state": st0.cpu().numpy()}
+        ks.append(k)
+
     t = synth.q4k_table(256 * 512, 2048, seed_tensor=24)
     add("gemv_expert_q4_k", "Q4_K expert e of [256 x 512 x 2048] x f32 [2048] (layer_moe.cpp:131 gate, "
         "element offset e*512*2048)", "Q4_K", torch.from_numpy(t).to(dev), 256 * 512 * 2048, 512, 2048,
@@ -302,16 +332,21 @@ def cpu_baseline(host, kernels, threads: int, budget_s: float, gemv=None):
               "dequant_gather_q4_k": 1024, "dequant_gather_q6_k": 1024}
     gemv = gemv or {}
     for name, g in gemv.items():
-        sample[name] = min(g["M"], 4096)
+        sample[name] = min(g["M"], 4096) if "M" in g else min(g["rows"], 4)
     full = {"rmsnorm": 36, "qk_norm_rope": 512, "residual_rmsnorm_bf16": 4096, "swiglu_bf16": 4096,
             "shared_swiglu_sigmoid_bf16": 4096, "gdn_frontend": 4096, "gdn_norm_gate": 4096,
             "dequant_gather_q4_k": 8192, "dequant_gather_q6_k": 8192}
-    full.update({name: g["M"] for name, g in gemv.items()})
+    full.update({name: g["M"] if "M" in g else g["rows"] for name, g in gemv.items()})
 
     def runner(name, rows, th):
         if name.startswith("gemv_"):
             g = gemv[name]
             return lambda: orc.gemv(g["table"], g["type"], g["x"], rows, g["K"], threads=th)
+        if name.startswith("gdn_recurrent"):
+            g = gemv[name]
+            st = g["state"].copy()
+            return lambda: orc.gdn_recurrent_rows(st, g["qkv"][:rows], g["beta"][:rows], g["decay"][:rows],
+                                                  16, 32, 128, 128)
         c = host[name]
         if name == "rmsnorm":
             return lambda: orc.rmsnorm_rows(c["x"][:rows], c["w"], threads=th)
@@ -498,7 +533,8 @@ def main() -> int:
         cpu_next = {}
         if not args.no_cpu:
             threads = max(1, min(16, os.cpu_count() or 1))
-            cpu_next, _ = cpu_baseline(host, nxt, threads, args.cpu_seconds / 3, gemv={k.name: k.gemv for k in nxt})
+            cpu_next, _ = cpu_baseline(host, nxt, threads, args.cpu_seconds / 3,
+                                       gemv={k.name: getattr(k, "gemv", None) or k.gdn for k in nxt})
         next_rows = {
             k.name: {"config": k.config, "bytes": k.bytes, "us_per_call": round(k.us, 3),
                      "gbps": round(k.bytes / k.us / 1e3, 1), "frac_peak": round(k.bytes / k.us / 1e3 / PEAK_GBPS, 4),

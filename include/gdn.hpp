@@ -1,10 +1,11 @@
 // Drop-in for the Gated DeltaNet kernels of include/gdn.hpp of the reference
-// (sahan974/qwen-3.5-cuda, :9-27 and :58-67), hipStream_t in place of
-// cudaStream_t.
+// (sahan974/qwen-3.5-cuda, :9-67), hipStream_t in place of cudaStream_t.
 #ifndef QWEN35_GDN_HPP
 #define QWEN35_GDN_HPP
 
 #include <hip/hip_runtime_api.h>
+
+#include <cstdint>
 
 namespace qwen {
 
@@ -17,6 +18,18 @@ void gdn_conv_step(const float* input, const float* weight, float* history, floa
 // ref: include/gdn.hpp:20-27
 void gdn_qk_normalize(float* q, float* k, int heads, int dim, float eps, hipStream_t stream);
 
+// beta = sigmoid(beta_raw); decay = exp(a * softplus(alpha_raw + dt_bias)) per
+// value head.  ref: include/gdn.hpp:29-38
+void gdn_gate_values(const float* beta_raw, const float* alpha_raw, const float* a, const float* dt_bias,
+                     float* beta, float* decay, int heads, hipStream_t stream);
+
+// One delta-rule step of the [value_heads x key_dim x value_dim] state, in
+// place; throws "GDN value dimension exceeds kernel limit" for value_dim > 256.
+// ref: include/gdn.hpp:41-54
+void gdn_recurrent_step(float* state, const float* q, const float* k, const float* v, const float* beta,
+                        const float* decay, float* out, int key_heads, int value_heads, int key_dim, int value_dim,
+                        hipStream_t stream);
+
 // out = norm(x) * weight * silu(z) per head.  ref: include/gdn.hpp:58-67
 void gdn_norm_gate(const float* x, const float* z, const float* weight, float* out, int heads, int dim,
                    float eps, hipStream_t stream);
@@ -28,6 +41,16 @@ void gdn_norm_gate(const float* x, const float* z, const float* weight, float* o
 void gdn_frontend_rows(const float* x, const float* weight, const float* hist_in, float* hist_out, float* y,
                        int rows, int channels, int kernel, int k_heads, int key_dim, float eps,
                        hipStream_t stream);
+
+// gdn_gate_values over rows x heads (a, dt_bias per head).
+void gdn_gate_values_rows(const float* beta_raw, const float* alpha_raw, const float* a, const float* dt_bias,
+                          float* beta, float* decay, int rows, int heads, hipStream_t stream);
+
+// `rows` consecutive recurrent steps in one launch; token t reads q, k, v at
+// t * qkv_stride and beta, decay at t * value_heads, writes out at t * out_stride.
+void gdn_recurrent_rows(float* state, const float* q, const float* k, const float* v, const float* beta,
+                        const float* decay, float* out, int rows, int key_heads, int value_heads, int key_dim,
+                        int value_dim, int64_t qkv_stride, int64_t out_stride, hipStream_t stream);
 
 // gdn_norm_gate over rows x heads x dim.
 void gdn_norm_gate_rows(const float* x, const float* z, const float* weight, float* out, int rows, int heads,

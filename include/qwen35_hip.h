@@ -130,6 +130,35 @@ int qwen_gdn_norm_gate(const float* x, const float* z, const float* weight, floa
 int qwen_gdn_norm_gate_rows(const float* x, const float* z, const float* weight, float* out,
                             int rows, int heads, int dim, float eps, void* stream);
 
+/* Gates of the delta rule: beta = 1/(1+expf(-beta_raw)),
+ * decay = expf(a * softplus(alpha_raw + dt_bias)), softplus(x) = x > 20 ? x : log1p(exp(x)).
+ * beta_raw, alpha_raw, beta, decay [heads]; a, dt_bias [heads].
+ * ref: include/gdn.hpp:29-38 (gdn_gate_values), src/cuda/gdn.cu:90-104 */
+int qwen_gdn_gate_values(const float* beta_raw, const float* alpha_raw, const float* a,
+                         const float* dt_bias, float* beta, float* decay, int heads, void* stream);
+/* Row-batched form: beta_raw, alpha_raw, beta, decay [rows x heads]; a, dt_bias [heads]. */
+int qwen_gdn_gate_values_rows(const float* beta_raw, const float* alpha_raw, const float* a,
+                              const float* dt_bias, float* beta, float* decay, int rows, int heads,
+                              void* stream);
+
+/* One delta-rule step per value head h (key head h % key_heads), state
+ * [value_heads x key_dim x value_dim] updated in place:
+ *   S *= decay[h]; delta = (v - k^T S) * beta[h]; S += k delta^T; out = q^T S.
+ * q, k [key_heads x key_dim]; v, out [value_heads x value_dim]; beta, decay [value_heads].
+ * value_dim > 256 -> QWEN_STATUS_INVALID_ARGUMENT ("GDN value dimension exceeds kernel limit").
+ * ref: include/gdn.hpp:41-54 (gdn_recurrent_step), src/cuda/gdn.cu:108-172 */
+int qwen_gdn_recurrent_step(float* state, const float* q, const float* k, const float* v,
+                            const float* beta, const float* decay, float* out, int key_heads,
+                            int value_heads, int key_dim, int value_dim, void* stream);
+/* `rows` consecutive steps in one launch (the reference's per-token loop,
+ * src/layer_gdn.cpp:97-103): token t reads q, k, v at t * qkv_stride elements
+ * (e.g. the q | k | v slices of the GDN front end's output rows), beta and decay
+ * at t * value_heads, and writes out at t * out_stride. */
+int qwen_gdn_recurrent_rows(float* state, const float* q, const float* k, const float* v,
+                            const float* beta, const float* decay, float* out, int rows,
+                            int key_heads, int value_heads, int key_dim, int value_dim,
+                            int64_t qkv_stride, int64_t out_stride, void* stream);
+
 /* ====================================================================== MoE
  * h = silu(g) * u (fp32).  ref: src/layer_moe.cpp:10 (moe_silu_mul decl),
  * src/cuda/moe.cu:61-72 */

@@ -461,6 +461,18 @@ void or_gdn_recurrent_step(float* state, const float* q, const float* k, const f
     }
 }
 
+// T consecutive recurrent steps (the reference calls gdn_recurrent_step once
+// per token, src/layer_gdn.cpp:100-103): token t reads q, k, v at
+// t * qkv_stride, beta / decay at t * value_heads, writes out at t * out_stride.
+void or_gdn_recurrent_rows(float* state, const float* q, const float* k, const float* v, const float* beta,
+                           const float* decay, float* out, int rows, int key_heads, int value_heads, int key_dim,
+                           int value_dim, int64_t qkv_stride, int64_t out_stride) {
+    for (int t = 0; t < rows; ++t)
+        or_gdn_recurrent_step(state, q + t * qkv_stride, k + t * qkv_stride, v + t * qkv_stride,
+                              beta + static_cast<int64_t>(t) * value_heads, decay + static_cast<int64_t>(t) * value_heads,
+                              out + t * out_stride, key_heads, value_heads, key_dim, value_dim);
+}
+
 // ---------------------------------------------------------------- MoE activations
 
 // h = silu(g) * u                                    -- src/cuda/moe.cu:61-67

@@ -83,6 +83,10 @@ void or_gdn_gate_values(const float* b, const float* alpha, const float* a, cons
 void or_gdn_recurrent_step(float* state, const float* q, const float* k, const float* v,
                            const float* beta, const float* decay, float* out, int key_heads,
                            int value_heads, int key_dim, int value_dim); /* gdn.cu:108-151 */
+void or_gdn_recurrent_rows(float* state, const float* q, const float* k, const float* v,
+                           const float* beta, const float* decay, float* out, int rows,
+                           int key_heads, int value_heads, int key_dim, int value_dim,
+                           int64_t qkv_stride, int64_t out_stride);  /* layer_gdn.cpp:100-103 */
 
 /* ---- MoE activations ---- */
 void or_silu_mul_f32(const float* g, const float* u, float* h, int64_t n, int threads); /* moe.cu:61-67 */

@@ -49,6 +49,7 @@ _SIGS = {
     "or_norm_gate_rows": ([_P, _P, _P, _P, _I, _I, _I, _F, _I], None),
     "or_gdn_gate_values": ([_P, _P, _P, _P, _P, _P, _I], None),
     "or_gdn_recurrent_step": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I], None),
+    "or_gdn_recurrent_rows": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I64, _I64], None),
     "or_silu_mul_f32": ([_P, _P, _P, _I64, _I], None),
     "or_swiglu_bf16": ([_P, _P, _P, _I64, _I], None),
     "or_shared_swiglu_sigmoid_bf16": ([_P, _P, _P, _P, _I, _I, _I], None),
@@ -231,6 +232,30 @@ def gdn_recurrent_step(state, q, k, v, beta, decay, key_heads, value_heads, key_
     out = np.empty(value_heads * value_dim, dtype=F32)
     lib().or_gdn_recurrent_step(_p(state), _p(q), _p(k), _p(v), _p(beta), _p(decay), _p(out), key_heads,
                                 value_heads, key_dim, value_dim)
+    return out
+
+
+def gdn_gate_values_rows(b, alpha, a, dt):
+    """b, alpha [rows, heads]; a, dt [heads] -> beta, decay [rows, heads]."""
+    b, alpha = _c(b, F32), _c(alpha, F32)
+    rows, heads = b.shape
+    beta, decay = gdn_gate_values(b.reshape(-1), alpha.reshape(-1), np.tile(_c(a, F32), rows), np.tile(_c(dt, F32), rows))
+    return beta.reshape(rows, heads), decay.reshape(rows, heads)
+
+
+def gdn_recurrent_rows(state, qkv, beta, decay, key_heads, value_heads, key_dim, value_dim):
+    """qkv [rows, 2*key_heads*key_dim + value_heads*value_dim] (q | k | v per token, the
+    GDN front end's output layout); beta, decay [rows, value_heads]. Updates `state` in
+    place; returns out [rows, value_heads * value_dim]."""
+    assert state.dtype == F32 and state.flags.c_contiguous
+    qkv, beta, decay = _c(qkv, F32), _c(beta, F32), _c(decay, F32)
+    rows, stride = qkv.shape
+    kd = key_heads * key_dim
+    out = np.empty((rows, value_heads * value_dim), dtype=F32)
+    base = qkv.ctypes.data
+    lib().or_gdn_recurrent_rows(_p(state), ctypes.c_void_p(base), ctypes.c_void_p(base + 4 * kd),
+                                ctypes.c_void_p(base + 8 * kd), _p(beta), _p(decay), _p(out), rows, key_heads,
+                                value_heads, key_dim, value_dim, stride, value_heads * value_dim)
     return out
 
 

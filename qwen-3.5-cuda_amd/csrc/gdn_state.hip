@@ -1,0 +1,253 @@
+// Gated DeltaNet gates and recurrent state update on gfx950.
+//
+// Reference semantics (src/cuda/gdn.cu):
+//   gates_kernel :90-99      beta = 1 / (1 + expf(-b));
+//                            decay = expf(a * softplus(alpha + dt)),
+//                            softplus(x) = x > 20 ? x : log1pf(expf(x))
+//   recurrent_kernel :108-151, per value head h (key head h % key_heads) and
+//   value column j:
+//       S[i][j] *= decay[h];  mem += k[i] * S[i][j]          (i < key_dim)
+//       delta = (v[j] - mem) * beta[h]
+//       S[i][j] += k[i] * delta
+//       out[j] = sum_i q[i] * S[i][j]
+// called once per token per GDN layer (src/layer_gdn.cpp:97-103). The
+// reference walks the state three times per token (one thread per column, a
+// block per head, 32 blocks).
+//
+// Here the state (value_heads x key_dim x value_dim fp32, 2 MB per layer at
+// 32 x 128 x 128) is read once and written once per call: one wave owns 4
+// value columns of one head, lane L holds rows L, L+64, ... of those columns
+// as float4 in VGPRs, the column sums over rows are wave reductions (DPP +
+// permlane), and the updated rows go back with 16-byte stores. The multi-token
+// entry point keeps the state slice in VGPRs across all tokens of the call
+// (the reference's per-token loop, one launch), reading each token's q, k, v
+// straight from the GDN front end's output rows.
+#include <algorithm>
+#include <cmath>
+
+#include "capi_common.hpp"
+#include "device_common.hpp"
+
+namespace qk {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / kWave;
+constexpr int kMaxValueDim = 256;  // src/cuda/gdn.cu:167-169
+
+// softplus with the reference's threshold; log1p(exp(x)) evaluated with the
+// accurate device expf / log1pf.
+__device__ __forceinline__ float softplus20(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+__global__ __launch_bounds__(kBlock) void gates_kernel(const float* __restrict__ b, const float* __restrict__ alpha,
+                                                       const float* __restrict__ a, const float* __restrict__ dt,
+                                                       float* __restrict__ beta, float* __restrict__ decay,
+                                                       int64_t n, int heads) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kBlock) {
+        const int h = static_cast<int>(i % heads);
+        beta[i] = 1.0f / (1.0f + expf(-b[i]));
+        decay[i] = expf(a[h] * softplus20(alpha[i] + dt[h]));
+    }
+}
+
+// One wave per (value head, 4 value columns); RPL rows of the state per lane
+// (key_dim = 64 * RPL). Tokens t < rows run in order, the state slice staying
+// in VGPRs; q/k/v of token t sit at t * qkv_stride, beta/decay at
+// t * value_heads, out at t * out_stride. The inputs of token t + kPrefetch
+// are loaded while token t is computed (a ring of kPrefetch register slots;
+// loads past the last token re-read it and are never used).
+constexpr int kPrefetch = 4;
+
+template <int RPL>
+__global__ __launch_bounds__(kBlock) void gdn_recurrent_v4(float* __restrict__ S, const float* __restrict__ q,
+                                                           const float* __restrict__ k, const float* __restrict__ v,
+                                                           const float* __restrict__ beta,
+                                                           const float* __restrict__ decay, float* __restrict__ out,
+                                                           int rows, int key_heads, int value_heads, int value_dim,
+                                                           int64_t qkv_stride, int64_t out_stride) {
+    constexpr int DK = 64 * RPL;
+    constexpr int P = kPrefetch;
+    const int cblocks = value_dim >> 2;
+    const int wave = blockIdx.x * kWaves + wave_in_block();
+    if (wave >= value_heads * cblocks) return;  // wave-uniform
+    const int lane = threadIdx.x & 63;
+    const int h = wave / cblocks;
+    const int j0 = 4 * (wave - h * cblocks);
+    const int src = h % key_heads;  // value heads tile as [subgroup][key head]
+    float* Sh = S + static_cast<size_t>(h) * DK * value_dim + j0;
+
+    float kr[P][RPL], qr[P][RPL], bt[P], dc[P];
+    float4 vv[P];
+    auto fetch = [&](int slot, int t) {
+        t = min(t, rows - 1);
+        const float* qt = q + t * qkv_stride + src * DK;
+        const float* kt = k + t * qkv_stride + src * DK;
+#pragma unroll
+        for (int r = 0; r < RPL; ++r) {
+            kr[slot][r] = kt[lane + 64 * r];
+            qr[slot][r] = qt[lane + 64 * r];
+        }
+        vv[slot] = ld4(v + t * qkv_stride + static_cast<size_t>(h) * value_dim + j0);
+        bt[slot] = beta[static_cast<int64_t>(t) * value_heads + h];
+        dc[slot] = decay[static_cast<int64_t>(t) * value_heads + h];
+    };
+#pragma unroll
+    for (int p = 0; p < P; ++p) fetch(p, p);
+
+    float4 s[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) s[r] = ld4_nt(Sh + static_cast<size_t>(lane + 64 * r) * value_dim);
+
+    for (int t0 = 0; t0 < rows; t0 += P) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const int t = t0 + p;
+            if (t >= rows) break;  // wave-uniform
+            // S *= decay; mem = sum_i k_i S_i  (per column)
+            const float d = dc[p];
+            float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int r = 0; r < RPL; ++r) {
+                s[r].x *= d;
+                s[r].y *= d;
+                s[r].z *= d;
+                s[r].w *= d;
+                m.x = __builtin_fmaf(kr[p][r], s[r].x, m.x);
+                m.y = __builtin_fmaf(kr[p][r], s[r].y, m.y);
+                m.z = __builtin_fmaf(kr[p][r], s[r].z, m.z);
+                m.w = __builtin_fmaf(kr[p][r], s[r].w, m.w);
+            }
+            m.x = group_sum<64>(m.x);
+            m.y = group_sum<64>(m.y);
+            m.z = group_sum<64>(m.z);
+            m.w = group_sum<64>(m.w);
+            const float b = bt[p];
+            const float4 dl = make_float4((vv[p].x - m.x) * b, (vv[p].y - m.y) * b, (vv[p].z - m.z) * b,
+                                          (vv[p].w - m.w) * b);
+            // S += k_i * delta; o = sum_i q_i S_i
+            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int r = 0; r < RPL; ++r) {
+                s[r].x = __builtin_fmaf(kr[p][r], dl.x, s[r].x);
+                s[r].y = __builtin_fmaf(kr[p][r], dl.y, s[r].y);
+                s[r].z = __builtin_fmaf(kr[p][r], dl.z, s[r].z);
+                s[r].w = __builtin_fmaf(kr[p][r], dl.w, s[r].w);
+                o.x = __builtin_fmaf(qr[p][r], s[r].x, o.x);
+                o.y = __builtin_fmaf(qr[p][r], s[r].y, o.y);
+                o.z = __builtin_fmaf(qr[p][r], s[r].z, o.z);
+                o.w = __builtin_fmaf(qr[p][r], s[r].w, o.w);
+            }
+            o.x = group_sum<64>(o.x);
+            o.y = group_sum<64>(o.y);
+            o.z = group_sum<64>(o.z);
+            o.w = group_sum<64>(o.w);
+            if (lane == 0) st4(out + t * out_stride + static_cast<size_t>(h) * value_dim + j0, o);
+            fetch(p, t + P);
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) st4_nt(Sh + static_cast<size_t>(lane + 64 * r) * value_dim, s[r]);
+}
+
+// Any key / value dim (value_dim <= 256): one block per value head, thread j
+// owns column j and walks the rows, as the reference does.
+__global__ __launch_bounds__(kMaxValueDim) void gdn_recurrent_any(
+    float* __restrict__ S, const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ beta, const float* __restrict__ decay, float* __restrict__ out, int rows, int key_heads,
+    int value_heads, int key_dim, int value_dim, int64_t qkv_stride, int64_t out_stride) {
+    const int h = blockIdx.x;
+    const int j = threadIdx.x;
+    if (j >= value_dim) return;
+    const int src = h % key_heads;
+    float* Sh = S + static_cast<size_t>(h) * key_dim * value_dim + j;
+    for (int t = 0; t < rows; ++t) {
+        const float* qt = q + t * qkv_stride + static_cast<size_t>(src) * key_dim;
+        const float* kt = k + t * qkv_stride + static_cast<size_t>(src) * key_dim;
+        const float dc = decay[static_cast<int64_t>(t) * value_heads + h];
+        float mem = 0.f;
+        for (int i = 0; i < key_dim; ++i) {
+            float c = Sh[static_cast<size_t>(i) * value_dim] * dc;
+            Sh[static_cast<size_t>(i) * value_dim] = c;
+            mem = __builtin_fmaf(kt[i], c, mem);
+        }
+        const float dl = (v[t * qkv_stride + static_cast<size_t>(h) * value_dim + j] - mem) *
+                         beta[static_cast<int64_t>(t) * value_heads + h];
+        float o = 0.f;
+        for (int i = 0; i < key_dim; ++i) {
+            const float c = __builtin_fmaf(kt[i], dl, Sh[static_cast<size_t>(i) * value_dim]);
+            Sh[static_cast<size_t>(i) * value_dim] = c;
+            o = __builtin_fmaf(qt[i], c, o);
+        }
+        out[t * out_stride + static_cast<size_t>(h) * value_dim + j] = o;
+    }
+}
+
+int launch_recurrent(float* state, const float* q, const float* k, const float* v, const float* beta,
+                     const float* decay, float* out, int rows, int key_heads, int value_heads, int key_dim,
+                     int value_dim, int64_t qkv_stride, int64_t out_stride, hipStream_t s, const char* what) {
+    const bool vec = value_dim % 4 == 0 && (key_dim == 64 || key_dim == 128) && aligned16(state) && aligned16(v) &&
+                     aligned16(out) && qkv_stride % 4 == 0 && out_stride % 4 == 0;
+    if (vec) {
+        const int waves = value_heads * (value_dim / 4);
+        const unsigned grid = blocks_for(waves, kWaves);
+        if (key_dim == 64)
+            gdn_recurrent_v4<1><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
+                                                        value_heads, value_dim, qkv_stride, out_stride);
+        else
+            gdn_recurrent_v4<2><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
+                                                        value_heads, value_dim, qkv_stride, out_stride);
+    } else {
+        gdn_recurrent_any<<<value_heads, kMaxValueDim, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
+                                                               value_heads, key_dim, value_dim, qkv_stride,
+                                                               out_stride);
+    }
+    return check_launch(what);
+}
+
+}  // namespace
+}  // namespace qk
+
+using namespace qk;
+
+extern "C" {
+
+int qwen_gdn_gate_values_rows(const float* beta_raw, const float* alpha_raw, const float* a, const float* dt_bias,
+                              float* beta, float* decay, int rows, int heads, void* stream) {
+    QK_REQUIRE(rows >= 0 && heads >= 0, "gdn_gate_values: negative size (rows=%d, heads=%d)", rows, heads);
+    if (rows == 0 || heads == 0) return ok();
+    QK_REQUIRE(beta_raw && alpha_raw && a && dt_bias && beta && decay, "gdn_gate_values: null pointer");
+    const int64_t n = static_cast<int64_t>(rows) * heads;
+    gates_kernel<<<std::min<unsigned>(blocks_for(n, kBlock), 4096u), kBlock, 0, as_stream(stream)>>>(
+        beta_raw, alpha_raw, a, dt_bias, beta, decay, n, heads);
+    return check_launch("gdn_gate_values");
+}
+
+int qwen_gdn_gate_values(const float* beta_raw, const float* alpha_raw, const float* a, const float* dt_bias,
+                         float* beta, float* decay, int heads, void* stream) {
+    return qwen_gdn_gate_values_rows(beta_raw, alpha_raw, a, dt_bias, beta, decay, 1, heads, stream);
+}
+
+int qwen_gdn_recurrent_rows(float* state, const float* q, const float* k, const float* v, const float* beta,
+                            const float* decay, float* out, int rows, int key_heads, int value_heads, int key_dim,
+                            int value_dim, int64_t qkv_stride, int64_t out_stride, void* stream) {
+    QK_REQUIRE(rows >= 0 && key_heads >= 0 && value_heads >= 0 && key_dim >= 0 && value_dim >= 0,
+               "gdn_recurrent: negative size");
+    QK_REQUIRE(value_dim <= kMaxValueDim, "GDN value dimension exceeds kernel limit");
+    if (rows == 0 || value_heads == 0 || value_dim == 0) return ok();
+    QK_REQUIRE(key_heads > 0 && key_dim > 0, "gdn_recurrent: key_heads and key_dim must be positive");
+    QK_REQUIRE(state && q && k && v && beta && decay && out, "gdn_recurrent: null pointer");
+    QK_REQUIRE(rows == 1 || (qkv_stride > 0 && out_stride > 0), "gdn_recurrent: non-positive row stride");
+    return launch_recurrent(state, q, k, v, beta, decay, out, rows, key_heads, value_heads, key_dim, value_dim,
+                            qkv_stride, out_stride, as_stream(stream), "gdn_recurrent");
+}
+
+int qwen_gdn_recurrent_step(float* state, const float* q, const float* k, const float* v, const float* beta,
+                            const float* decay, float* out, int key_heads, int value_heads, int key_dim,
+                            int value_dim, void* stream) {
+    return qwen_gdn_recurrent_rows(state, q, k, v, beta, decay, out, 1, key_heads, value_heads, key_dim, value_dim,
+                                   0, 0, stream);
+}
+
+}  // extern "C"

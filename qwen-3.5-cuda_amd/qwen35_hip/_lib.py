@@ -54,6 +54,10 @@ SIGNATURES: dict[str, list] = {
     "qwen_type_supported": [_I],
     "qwen_dequantize_row": [_P, _I, _U64, _P, _I, _I, _P],
     "qwen_dequant_gather_rows": [_P, _I, _U64, _P, _I, _I, _P, _P],
+    "qwen_gdn_gate_values": [_P] * 6 + [_I, _P],
+    "qwen_gdn_gate_values_rows": [_P] * 6 + [_I, _I, _P],
+    "qwen_gdn_recurrent_step": [_P] * 7 + [_I, _I, _I, _I, _P],
+    "qwen_gdn_recurrent_rows": [_P] * 7 + [_I, _I, _I, _I, _I, _I64, _I64, _P],
     "qwen_matmul_type_supported": [_I],
     "qwen_matmul_dispatch": [_P, _I, _U64, _P, _P, _I, _I, _U64, _P],
 }

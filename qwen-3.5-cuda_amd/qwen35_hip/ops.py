@@ -211,6 +211,65 @@ def gdn_norm_gate_rows(x, z, weight, out=None, eps=1e-6, stream=None):
     return out
 
 
+def gdn_gate_values_rows(beta_raw, alpha_raw, a, dt_bias, beta=None, decay=None, stream=None):
+    """beta_raw, alpha_raw [rows, heads] (or [heads]); a, dt_bias [heads] -> beta, decay."""
+    _dev(beta_raw, alpha_raw, a, dt_bias, dtype=torch.float32)
+    heads = a.numel()
+    _same((heads,), dt_bias)
+    _same(beta_raw.shape, alpha_raw)
+    if beta_raw.numel() % max(heads, 1):
+        raise ValueError("beta_raw must hold whole rows of `heads` values")
+    rows = beta_raw.numel() // max(heads, 1)
+    beta = torch.empty_like(beta_raw) if beta is None else beta
+    decay = torch.empty_like(beta_raw) if decay is None else decay
+    _dev(beta, decay, dtype=torch.float32)
+    _same(beta_raw.shape, beta, decay)
+    check(load().qwen_gdn_gate_values_rows(_p(beta_raw), _p(alpha_raw), _p(a), _p(dt_bias), _p(beta), _p(decay), rows,
+                                           heads, _stream(stream)))
+    return beta, decay
+
+
+def gdn_recurrent_step(state, q, k, v, beta, decay, key_heads, value_heads, key_dim, value_dim, out=None,
+                       stream=None):
+    """state [value_heads, key_dim, value_dim] updated in place; q, k [key_heads * key_dim];
+    v [value_heads * value_dim]; beta, decay [value_heads] -> out [value_heads * value_dim]."""
+    _dev(state, q, k, v, beta, decay, dtype=torch.float32)
+    if state.numel() != value_heads * key_dim * value_dim:
+        raise ValueError("state shape does not match the head sizes")
+    for t, n in ((q, key_heads * key_dim), (k, key_heads * key_dim), (v, value_heads * value_dim),
+                 (beta, value_heads), (decay, value_heads)):
+        if t.numel() < n:
+            raise ValueError(f"input of {t.numel()} elements, need {n}")
+    out = torch.empty(value_heads * value_dim, dtype=torch.float32, device=state.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    check(load().qwen_gdn_recurrent_step(_p(state), _p(q), _p(k), _p(v), _p(beta), _p(decay), _p(out), key_heads,
+                                         value_heads, key_dim, value_dim, _stream(stream)))
+    return out
+
+
+def gdn_recurrent_rows(state, qkv, beta, decay, key_heads, value_heads, key_dim, value_dim, out=None, stream=None):
+    """qkv [rows, 2*key_heads*key_dim + value_heads*value_dim] (q | k | v per token, the GDN
+    front end's output rows); beta, decay [rows, value_heads]; state updated in place
+    -> out [rows, value_heads * value_dim]."""
+    _dev(state, qkv, beta, decay, dtype=torch.float32)
+    rows, stride = qkv.shape
+    kd = key_heads * key_dim
+    if stride < 2 * kd + value_heads * value_dim:
+        raise ValueError("qkv rows too short for q | k | v")
+    if state.numel() != value_heads * key_dim * value_dim:
+        raise ValueError("state shape does not match the head sizes")
+    _same((rows, value_heads), beta, decay)
+    out = torch.empty((rows, value_heads * value_dim), dtype=torch.float32, device=qkv.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    _same((rows, value_heads * value_dim), out)
+    base = qkv.data_ptr()
+    check(load().qwen_gdn_recurrent_rows(_p(state), ctypes.c_void_p(base), ctypes.c_void_p(base + 4 * kd),
+                                         ctypes.c_void_p(base + 8 * kd), _p(beta), _p(decay), _p(out), rows,
+                                         key_heads, value_heads, key_dim, value_dim, stride, value_heads * value_dim,
+                                         _stream(stream)))
+    return out
+
+
 # ------------------------------------------------------------------ MoE
 def moe_silu_mul(g, u, out=None, stream=None):
     _dev(g, u, dtype=torch.float32)

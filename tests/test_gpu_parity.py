@@ -346,6 +346,110 @@ def test_dequantize_row(oracle, kind, cols, row):
     assert_bits_equal(got, oracle.dequant_span(table, t, row * cols, cols), f"{kind} row {row}")
 
 
+# ------------------------------------------------------------------ GDN gates + recurrent state
+def _gdn_inputs(r, rows, kh, vh, dk, dv, extra=0):
+    """Front-end-like rows (unit-norm k, q scaled by dk^-1/2, v ~ N(0,1)), gates from raw
+    projections through the oracle's gate formula, and a random state."""
+    kd = kh * dk
+    qkv = r.standard_normal((rows, 2 * kd + vh * dv + extra)).astype(F32)
+    for t in range(rows):
+        for part, scale in ((0, dk ** -0.5), (kd, 1.0)):
+            seg = qkv[t, part:part + kd].reshape(kh, dk)
+            seg /= np.linalg.norm(seg, axis=1, keepdims=True)
+            seg *= scale
+    b = r.standard_normal((rows, vh)).astype(F32)
+    alpha = (2 * r.standard_normal((rows, vh))).astype(F32)
+    a = -np.exp(r.standard_normal(vh)).astype(F32)
+    dt = r.uniform(-1, 1, vh).astype(F32)
+    state = (0.5 * r.standard_normal(vh * dk * dv)).astype(F32)
+    return qkv, b, alpha, a, dt, state
+
+
+def test_gdn_gate_values(oracle):
+    r = rng(31)
+    rows, heads = 64, 32
+    b = (4 * r.standard_normal((rows, heads))).astype(F32)
+    alpha = (8 * r.standard_normal((rows, heads))).astype(F32)
+    alpha[0, :4] = [25.0, 20.5, 19.5, -90.0]  # both sides of the softplus threshold
+    a = -np.exp(r.standard_normal(heads)).astype(F32)
+    dt = r.uniform(-1, 1, heads).astype(F32)
+    beta, decay = ops.gdn_gate_values_rows(dev(b), dev(alpha), dev(a), dev(dt))
+    rb, rd = oracle.gdn_gate_values_rows(b, alpha, a, dt)
+    assert_f32_close(host(beta), rb, what="beta")
+    assert_f32_close(host(decay), rd, what="decay")
+
+
+def test_gdn_recurrent_reference_fixture():
+    """tests/kernel_tests.cu:225-262 (kh=2, vh=4, dk=4, dv=3: the generic path), three steps."""
+    import json
+    from pathlib import Path
+
+    fx = json.loads((Path(__file__).resolve().parent / "golden" / "reference_fixtures.json").read_text())["gdn_recurrent"]
+    kh, vh, dk, dv = fx["key_heads"], fx["value_heads"], fx["key_dim"], fx["value_dim"]
+    state = torch.zeros(vh * dk * dv, dtype=torch.float32, device="cuda")
+    for st in fx["steps"]:
+        out = ops.gdn_recurrent_step(state, *(dev(np.array(st[n], dtype=F32)) for n in ("q", "k", "v", "beta", "decay")),
+                                     kh, vh, dk, dv)
+        assert np.max(np.abs(host(out) - np.array(st["expected"], dtype=F32))) < fx["tol"]
+
+
+@pytest.mark.parametrize("kh,vh,dk,dv,rows", [(16, 32, 128, 128, 1), (16, 32, 128, 128, 37), (4, 8, 64, 64, 9),
+                                              (2, 4, 96, 100, 5), (3, 6, 128, 256, 3)])
+def test_gdn_recurrent_rows(oracle, kh, vh, dk, dv, rows):
+    """Qwen3.5 GDN shape (16 key / 32 value heads of 128), a token count that is not a
+    multiple of the 4-deep prefetch, key dim 64, and generic shapes (dk 96, dv 100 / 256)."""
+    r = rng(kh * 1000 + rows)
+    qkv, b, alpha, a, dt, state = _gdn_inputs(r, rows, kh, vh, dk, dv, extra=8)
+    beta, decay = oracle.gdn_gate_values_rows(b, alpha, a, dt)
+    ds = dev(state)
+    out = host(ops.gdn_recurrent_rows(ds, dev(qkv), dev(beta), dev(decay), kh, vh, dk, dv))
+    # Oracle token by token, keeping each readout's condition scale sum_i |q_i| |S_ij|:
+    # out_j is a dot product that can cancel (a strongly decayed head reads ~1e-4 from
+    # terms ~4e-3), so its fp32 error is bounded relative to that scale, not to |out_j|.
+    ref_state = state.copy()
+    kd = kh * dk
+    ref = np.empty_like(out)
+    scale = np.empty(out.shape, dtype=np.float64)
+    src = np.arange(vh) % kh
+    for t in range(rows):
+        q, k, v = qkv[t, :kd], qkv[t, kd:2 * kd], qkv[t, 2 * kd:2 * kd + vh * dv]
+        ref[t] = oracle.gdn_recurrent_step(ref_state, q, k, v, beta[t], decay[t], kh, vh, dk, dv)
+        aq = np.abs(q.astype(np.float64)).reshape(kh, dk)[src]                       # [vh, dk]
+        aS = np.abs(ref_state.astype(np.float64)).reshape(vh, dk, dv)
+        scale[t] = np.einsum("hi,hij->hj", aq, aS).reshape(-1)
+    err = np.abs(out.astype(np.float64) - ref) / np.maximum(np.abs(ref.astype(np.float64)), scale)
+    worst = np.unravel_index(int(np.argmax(err)), err.shape)
+    assert err[worst] <= 1e-5, f"out rel err {err[worst]:.3e} at {worst}: got {out[worst]!r} ref {ref[worst]!r}"
+    assert_f32_close(host(ds), ref_state, group=dv, what="state")
+
+
+def test_gdn_recurrent_rows_equals_steps():
+    """One launch over T tokens leaves the same bits as T single-step launches."""
+    kh, vh, dk, dv, T = 16, 32, 128, 128, 6
+    r = rng(77)
+    qkv, b, alpha, a, dt, state = _gdn_inputs(r, T, kh, vh, dk, dv)
+    beta, decay = ops.gdn_gate_values_rows(dev(b), dev(alpha), dev(a), dev(dt))
+    s1, s2 = dev(state), dev(state)
+    dq = dev(qkv)
+    out = host(ops.gdn_recurrent_rows(s1, dq, beta, decay, kh, vh, dk, dv))
+    kd = kh * dk
+    for t in range(T):
+        o = ops.gdn_recurrent_step(s2, dq[t, :kd].contiguous(), dq[t, kd:2 * kd].contiguous(),
+                                   dq[t, 2 * kd:].contiguous(), beta[t].contiguous(), decay[t].contiguous(),
+                                   kh, vh, dk, dv)
+        assert_bits_equal(host(o), out[t], f"token {t}")
+    assert_bits_equal(host(s1), host(s2), "state")
+
+
+def test_gdn_recurrent_rejects_wide_values():
+    from qwen35_hip._lib import QwenError
+
+    s = torch.zeros(1 * 4 * 260, device="cuda")
+    x = torch.zeros(1040, device="cuda")
+    with pytest.raises(QwenError, match="GDN value dimension exceeds kernel limit"):
+        ops.gdn_recurrent_step(s, x, x, x, x, x, 1, 1, 4, 260)
+
+
 # ------------------------------------------------------------------ quantized GEMV
 def _gemv_weight(kind: str, rows: int, cols: int, r) -> np.ndarray:
     """GGML bytes of a rows x cols tensor: the C5 table generators for Q4_K/Q6_K

@@ -413,6 +413,57 @@ def test_gdn_recurrent_reference_fixture(oracle):
         assert np.max(np.abs(out - np.array(st["expected"], dtype=F32))) < fx["tol"]
 
 
+def _delta_rule_f64(S, q, k, v, beta, decay, kh, vh, dk, dv):
+    """The delta rule in matrix form, float64: S_h <- d S_h + k (beta (v - d S_h^T k))^T, out = S_h^T q."""
+    S = S.reshape(vh, dk, dv)
+    out = np.empty((vh, dv))
+    for h in range(vh):
+        src = h % kh
+        kk, qq = k[src * dk:(src + 1) * dk], q[src * dk:(src + 1) * dk]
+        Sd = decay[h] * S[h]
+        delta = beta[h] * (v[h * dv:(h + 1) * dv] - Sd.T @ kk)
+        S[h] = Sd + np.outer(kk, delta)
+        out[h] = S[h].T @ qq
+    return out.reshape(-1)
+
+
+def test_gdn_recurrent_matches_matrix_form(oracle):
+    """Independent float64 matrix form of the delta rule over 6 tokens, value heads
+    tiling key heads as h % key_heads (kh=2, vh=6)."""
+    kh, vh, dk, dv = 2, 6, 8, 5
+    rng = np.random.default_rng(21)
+    S32 = (0.3 * rng.standard_normal(vh * dk * dv)).astype(F32)
+    S64 = S32.astype(np.float64)
+    for _ in range(6):
+        q = rng.standard_normal(kh * dk).astype(F32)
+        k = (rng.standard_normal(kh * dk) / np.sqrt(dk)).astype(F32)
+        v = rng.standard_normal(vh * dv).astype(F32)
+        beta = rng.uniform(0.05, 0.95, vh).astype(F32)
+        decay = rng.uniform(0.5, 1.0, vh).astype(F32)
+        out = oracle.gdn_recurrent_step(S32, q, k, v, beta, decay, kh, vh, dk, dv)
+        ref = _delta_rule_f64(S64, *(t.astype(np.float64) for t in (q, k, v, beta, decay)), kh, vh, dk, dv)
+        assert_f32_close(out, ref, group=dv, rtol=1e-5, what="out")
+        assert_f32_close(S32, S64, group=dv, rtol=1e-5, what="state")
+
+
+def test_gdn_recurrent_rows_layout(oracle):
+    """The multi-token form reads q | k | v out of one front-end row per token and
+    equals the per-token calls."""
+    kh, vh, dk, dv, T = 2, 4, 8, 6, 5
+    rng = np.random.default_rng(5)
+    qkv = rng.standard_normal((T, 2 * kh * dk + vh * dv + 3)).astype(F32)  # 3 spare columns: a real stride
+    beta = rng.uniform(0.1, 0.9, (T, vh)).astype(F32)
+    decay = rng.uniform(0.6, 1.0, (T, vh)).astype(F32)
+    S0 = (0.2 * rng.standard_normal(vh * dk * dv)).astype(F32)
+    S1 = S0.copy()
+    out = oracle.gdn_recurrent_rows(S1, qkv, beta, decay, kh, vh, dk, dv)
+    S2 = S0.copy()
+    for t in range(T):
+        q, k, v = qkv[t, :kh * dk], qkv[t, kh * dk:2 * kh * dk], qkv[t, 2 * kh * dk:2 * kh * dk + vh * dv]
+        assert_bits_equal(out[t], oracle.gdn_recurrent_step(S2, q, k, v, beta[t], decay[t], kh, vh, dk, dv), f"t={t}")
+    assert_bits_equal(S1, S2, "state")
+
+
 def test_gdn_gate_values(oracle):
     b = np.array([0.0, 2.0, -3.0, 10.0], dtype=F32)
     alpha = np.array([0.0, 25.0, -1.0, 19.0], dtype=F32)
