@@ -242,6 +242,36 @@ def build_next_rows(torch, ops, synth, host):
                  "decay": np.full((rows, vh), 0.95, np.float32), "state": st0.cpu().numpy()}
         ks.append(k)
 
+    # Decode attention (attn_kernels.cu:72-195): 16 query / 2 kv heads of 256,
+    # 4096 cached keys, sigmoid gate; fused split-K path and the reference's
+    # staged launches (scores, softmax, values, gate) on the same inputs.
+    H, Hkv, D, pos = 16, 2, 256, 4095
+    qa = torch.from_numpy(rng.standard_normal(H * D).astype(np.float32)).to(dev)
+    ga = torch.from_numpy(rng.standard_normal(H * D).astype(np.float32)).to(dev)
+    kc0 = torch.from_numpy(rng.standard_normal((pos + 1) * Hkv * D).astype(np.float32)).to(dev)
+    vc0 = torch.from_numpy(rng.standard_normal((pos + 1) * Hkv * D).astype(np.float32)).to(dev)
+    ws = torch.empty(ops.attn_decode_workspace_bytes(H, Hkv, D, pos), dtype=torch.uint8, device=dev)
+    nb = 2 * kc0.numel() * 4 + 3 * H * D * 4
+    for name, staged in (("attn_decode_4096", False), ("attn_decode_staged_4096", True)):
+        def mk_att(i, staged=staged):
+            kc, vc = (kc0, vc0) if i == 0 else (kc0.clone(), vc0.clone())
+            o = torch.empty(H * D, dtype=torch.float32, device=dev)
+            sc = torch.empty(H * (pos + 1), dtype=torch.float32, device=dev)
+            if not staged:
+                return lambda: ops.attn_decode(qa, kc, vc, H, Hkv, D, pos, gate=ga, workspace=ws, out=o)
+
+            def run():
+                ops.attn_scores(qa, kc, H, Hkv, D, pos, out=sc)
+                ops.attn_softmax(sc, H, pos + 1)
+                ops.attn_values(sc, vc, H, Hkv, D, pos, out=o)
+                ops.attn_sigmoid_gate(o, ga, out=o)
+            return run
+        desc = ("fused split-K decode, q [16 x 256] vs K/V cache [4096 x 2 x 256] f32, sigmoid gate" if not staged else
+                "the reference's four launches (scores, softmax, values, gate) on the same inputs")
+        k = Kernel(name, desc, nb, nb, mk_att)
+        k.attn = {"q": qa.cpu().numpy(), "K": kc0.cpu().numpy(), "V": vc0.cpu().numpy(), "g": ga.cpu().numpy()}
+        ks.append(k)
+
     t = synth.q4k_table(256 * 512, 2048, seed_tensor=24)
     add("gemv_expert_q4_k", "Q4_K expert e of [256 x 512 x 2048] x f32 [2048] (layer_moe.cpp:131 gate, "
         "element offset e*512*2048)", "Q4_K", torch.from_numpy(t).to(dev), 256 * 512 * 2048, 512, 2048,
@@ -332,16 +362,20 @@ def cpu_baseline(host, kernels, threads: int, budget_s: float, gemv=None):
               "dequant_gather_q4_k": 1024, "dequant_gather_q6_k": 1024}
     gemv = gemv or {}
     for name, g in gemv.items():
-        sample[name] = min(g["M"], 4096) if "M" in g else min(g["rows"], 4)
+        sample[name] = min(g["M"], 4096) if "M" in g else min(g["rows"], 4) if "rows" in g else 4096
     full = {"rmsnorm": 36, "qk_norm_rope": 512, "residual_rmsnorm_bf16": 4096, "swiglu_bf16": 4096,
             "shared_swiglu_sigmoid_bf16": 4096, "gdn_frontend": 4096, "gdn_norm_gate": 4096,
             "dequant_gather_q4_k": 8192, "dequant_gather_q6_k": 8192}
-    full.update({name: g["M"] if "M" in g else g["rows"] for name, g in gemv.items()})
+    full.update({name: g["M"] if "M" in g else g["rows"] if "rows" in g else 4096 for name, g in gemv.items()})
 
     def runner(name, rows, th):
         if name.startswith("gemv_"):
             g = gemv[name]
             return lambda: orc.gemv(g["table"], g["type"], g["x"], rows, g["K"], threads=th)
+        if name.startswith("attn_decode"):
+            g = gemv[name]
+            n = min(rows, 4096)
+            return lambda: orc.attn_decode(g["q"], g["K"][:n * 512], g["V"][:n * 512], 16, 2, 256, n - 1, gate=g["g"])
         if name.startswith("gdn_recurrent"):
             g = gemv[name]
             st = g["state"].copy()
@@ -534,7 +568,8 @@ def main() -> int:
         if not args.no_cpu:
             threads = max(1, min(16, os.cpu_count() or 1))
             cpu_next, _ = cpu_baseline(host, nxt, threads, args.cpu_seconds / 3,
-                                       gemv={k.name: getattr(k, "gemv", None) or k.gdn for k in nxt})
+                                       gemv={k.name: getattr(k, "gemv", None) or getattr(k, "gdn", None) or k.attn
+                                             for k in nxt})
         next_rows = {
             k.name: {"config": k.config, "bytes": k.bytes, "us_per_call": round(k.us, 3),
                      "gbps": round(k.bytes / k.us / 1e3, 1), "frac_peak": round(k.bytes / k.us / 1e3 / PEAK_GBPS, 4),

@@ -8,6 +8,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <cstddef>
 #include <cstdint>
 
 namespace qwen {
@@ -15,13 +16,44 @@ namespace qwen {
 // Per-head RMSNorm in place, x = x * (r * w).  ref: src/layer_attn.cpp:11
 void attn_head_norm(float* x, const float* weight, int heads, int dim, float eps, hipStream_t stream);
 
+// q[h] = qg[h][0:dim], gate[h] = qg[h][dim:2*dim].  ref: src/layer_attn.cpp:10
+void attn_split_qg(const float* qg, float* q, float* gate, int heads, int dim, hipStream_t stream);
+
+// scores[h][t] = (q_h . k_cache[t][h / (heads / kv_heads)]) / sqrt(dim), t <= pos.
+// ref: src/layer_attn.cpp:12
+void attn_scores(const float* q, const float* k_cache, float* scores, int q_heads, int kv_heads, int dim, int pos,
+                 hipStream_t stream);
+
+// Row softmax of scores [heads x valid_len] in place.  ref: src/layer_attn.cpp:13
+void attn_softmax(float* scores, int heads, int valid_len, hipStream_t stream);
+
+// out[h][j] = sum_t scores[h][t] * v_cache[t][h / (heads / kv_heads)][j].  ref: src/layer_attn.cpp:14
+void attn_values(const float* scores, const float* v_cache, float* out, int q_heads, int kv_heads, int dim, int pos,
+                 hipStream_t stream);
+
+// out = attn / (1 + exp(-gate)).  ref: src/layer_attn.cpp:15
+void attn_sigmoid_gate(const float* attn, const float* gate, float* out, int dim, hipStream_t stream);
+
 // hidden = silu(gate) * up.  ref: src/layer_moe.cpp:10
 void moe_silu_mul(const float* gate, const float* up, float* hidden, int dim, hipStream_t stream);
 
 // accum += shared_out * sigmoid(sgate[0]) (sgate on the device).  ref: src/layer_moe.cpp:12
 void moe_shared_add(float* accum, const float* shared_out, const float* sgate, int dim, hipStream_t stream);
 
-// ---- row-batched forms
+// ---- row-batched and fused forms
+
+// Cache store of src/layer_attn.cpp:98-100: k, v [kv_dim] to row pos; throws
+// "attention position exceeds configured context" unless 0 <= pos < max_seq_len.
+void attn_kv_store(const float* k, const float* v, float* k_cache, float* v_cache, int pos, int kv_dim,
+                   int max_seq_len, hipStream_t stream);
+
+// Bytes of workspace attn_decode needs for this shape.
+size_t attn_decode_workspace_bytes(int heads, int kv_heads, int dim, int pos);
+
+// scores -> softmax -> values -> (gate) of src/layer_attn.cpp:103-108 in one
+// split-K pass and a combine; gate may be null.
+void attn_decode(const float* q, const float* k_cache, const float* v_cache, const float* gate, float* out, int heads,
+                 int kv_heads, int dim, int pos, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 // moe_shared_add per row: accum, shared_out [rows x dim], sgate [rows].
 void moe_shared_add_rows(float* accum, const float* shared_out, const float* sgate, int rows, int dim,

@@ -22,6 +22,7 @@
 #ifndef QWEN35_HIP_H
 #define QWEN35_HIP_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -158,6 +159,51 @@ int qwen_gdn_recurrent_rows(float* state, const float* q, const float* k, const 
                             const float* beta, const float* decay, float* out, int rows,
                             int key_heads, int value_heads, int key_dim, int value_dim,
                             int64_t qkv_stride, int64_t out_stride, void* stream);
+
+/* ====================================================================== attention core (decode)
+ * One query position against the KV cache, rows [t][kv_heads][dim]; query head h
+ * reads kv head h / (heads / kv_heads) (heads a multiple of kv_heads). */
+
+/* q[h] = qg[h][0:dim], gate[h] = qg[h][dim:2*dim].
+ * ref: src/layer_attn.cpp:10 (attn_split_qg decl), src/cuda/attn_kernels.cu:16-31 */
+int qwen_attn_split_qg(const float* qg, float* q, float* gate, int heads, int dim, void* stream);
+
+/* scores[h][t] = (q_h . k_t) * (1/sqrt(dim)), t <= pos, scores [heads x (pos+1)].
+ * ref: src/layer_attn.cpp:12 (attn_scores decl), src/cuda/attn_kernels.cu:72-96 */
+int qwen_attn_scores(const float* q, const float* k_cache, float* scores, int heads, int kv_heads,
+                     int dim, int pos, void* stream);
+
+/* Row softmax in place: s = exp(s - max) / sum over valid_len entries per head.
+ * ref: src/layer_attn.cpp:13 (attn_softmax decl), src/cuda/attn_kernels.cu:99-158 */
+int qwen_attn_softmax(float* scores, int heads, int valid_len, void* stream);
+
+/* out[h][j] = sum_{t<=pos} scores[h][t] * v_cache[t][kv(h)][j].
+ * ref: src/layer_attn.cpp:14 (attn_values decl), src/cuda/attn_kernels.cu:162-181 */
+int qwen_attn_values(const float* scores, const float* v_cache, float* out, int heads, int kv_heads,
+                     int dim, int pos, void* stream);
+
+/* out = x / (1 + exp(-gate)) over n elements (out may equal x).
+ * ref: src/layer_attn.cpp:15 (attn_sigmoid_gate decl), src/cuda/attn_kernels.cu:185-195 */
+int qwen_attn_sigmoid_gate(const float* x, const float* gate, float* out, int n, void* stream);
+
+/* k, v [kv_dim] stored to row pos of the caches; pos outside [0, max_seq_len) ->
+ * QWEN_STATUS_OUT_OF_RANGE ("attention position exceeds configured context").
+ * ref: src/layer_attn.cpp:77-79 (check), :98-100 (cudaMemcpyAsync of k and v) */
+int qwen_attn_kv_store(const float* k, const float* v, float* k_cache, float* v_cache, int pos,
+                       int kv_dim, int max_seq_len, void* stream);
+
+/* Workspace bytes qwen_attn_decode needs for this shape (0 for an invalid shape). */
+size_t qwen_attn_decode_workspace_bytes(int heads, int kv_heads, int dim, int pos);
+
+/* scores -> softmax -> values -> sigmoid gate (gate may be NULL) in one call:
+ * out[h] = sum_t softmax_t(q_h . k_t / sqrt(dim)) v_t (* sigmoid(gate[h])).
+ * workspace: device memory of at least qwen_attn_decode_workspace_bytes, owned by
+ * the caller (the per-split partial results; the reference's scores buffer plays
+ * this role, src/layer_attn.cpp:57).
+ * ref: src/layer_attn.cpp:103-108 */
+int qwen_attn_decode(const float* q, const float* k_cache, const float* v_cache, const float* gate,
+                     float* out, int heads, int kv_heads, int dim, int pos, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 /* ====================================================================== MoE
  * h = silu(g) * u (fp32).  ref: src/layer_moe.cpp:10 (moe_silu_mul decl),

@@ -473,6 +473,79 @@ void or_gdn_recurrent_rows(float* state, const float* q, const float* k, const f
                               out + t * out_stride, key_heads, value_heads, key_dim, value_dim);
 }
 
+// ---------------------------------------------------------------- attention core (decode)
+
+// q[h][j] = in[h][j], g[h][j] = in[h][d + j] (rows of 2d)  -- src/cuda/attn_kernels.cu:16-31
+void or_attn_split_qg(const float* in, float* q, float* g, int heads, int dim) {
+    for (int64_t h = 0; h < heads; ++h)
+        for (int64_t j = 0; j < dim; ++j) {
+            q[h * dim + j] = in[h * 2 * dim + j];
+            g[h * dim + j] = in[h * 2 * dim + dim + j];
+        }
+}
+
+// scores[h][t] = (q_h . k_t) * rsqrt(D), t <= pos, kv head h / (H / Hkv)
+//                                                     -- src/cuda/attn_kernels.cu:72-96
+void or_attn_scores(const float* q, const float* k_cache, float* scores, int heads, int kv_heads, int dim, int pos) {
+    const int group = heads / kv_heads;
+    const float scale = or_rsqrt(static_cast<float>(dim));
+    for (int64_t h = 0; h < heads; ++h) {
+        const int64_t kv = h / group;
+        for (int64_t t = 0; t <= pos; ++t) {
+            double sum = 0.0;
+            const float* kt = k_cache + (t * kv_heads + kv) * dim;
+            for (int i = 0; i < dim; ++i) sum += static_cast<double>(q[h * dim + i]) * kt[i];
+            scores[h * (pos + 1) + t] = static_cast<float>(sum) * scale;
+        }
+    }
+}
+
+// Row softmax: r = expf(r - max) / sum               -- src/cuda/attn_kernels.cu:99-158
+void or_attn_softmax(float* scores, int heads, int n) {
+    for (int64_t h = 0; h < heads; ++h) {
+        float* r = scores + h * n;
+        float m = -INFINITY;
+        for (int i = 0; i < n; ++i) m = std::fmax(m, r[i]);
+        double sum = 0.0;
+        for (int i = 0; i < n; ++i) {
+            r[i] = exp_f(r[i] - m);
+            sum += r[i];
+        }
+        const float fs = static_cast<float>(sum);
+        for (int i = 0; i < n; ++i) r[i] /= fs;
+    }
+}
+
+// out[h][j] = sum_t s[h][t] * v[t][kv][j]            -- src/cuda/attn_kernels.cu:162-181
+void or_attn_values(const float* scores, const float* v_cache, float* out, int heads, int kv_heads, int dim, int pos) {
+    const int group = heads / kv_heads;
+    for (int64_t h = 0; h < heads; ++h) {
+        const int64_t kv = h / group;
+        for (int64_t j = 0; j < dim; ++j) {
+            double z = 0.0;
+            for (int64_t t = 0; t <= pos; ++t)
+                z += static_cast<double>(scores[h * (pos + 1) + t]) * v_cache[(t * kv_heads + kv) * dim + j];
+            out[h * dim + j] = static_cast<float>(z);
+        }
+    }
+}
+
+// out = x / (1 + expf(-g))                            -- src/cuda/attn_kernels.cu:185-195
+void or_attn_sigmoid_gate(const float* x, const float* g, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = x[i] / (1.0f + exp_f(-g[i]));
+}
+
+// The decode sequence of src/layer_attn.cpp:98-108 after the cache store:
+// scores, softmax over pos + 1 keys, values, then the sigmoid gate when gate
+// is non-null. scratch holds heads * (pos + 1) floats.
+void or_attn_decode(const float* q, const float* k_cache, const float* v_cache, const float* gate, float* out,
+                    float* scratch, int heads, int kv_heads, int dim, int pos) {
+    or_attn_scores(q, k_cache, scratch, heads, kv_heads, dim, pos);
+    or_attn_softmax(scratch, heads, pos + 1);
+    or_attn_values(scratch, v_cache, out, heads, kv_heads, dim, pos);
+    if (gate) or_attn_sigmoid_gate(out, gate, out, static_cast<int64_t>(heads) * dim);
+}
+
 // ---------------------------------------------------------------- MoE activations
 
 // h = silu(g) * u                                    -- src/cuda/moe.cu:61-67

@@ -88,6 +88,18 @@ void or_gdn_recurrent_rows(float* state, const float* q, const float* k, const f
                            int key_heads, int value_heads, int key_dim, int value_dim,
                            int64_t qkv_stride, int64_t out_stride);  /* layer_gdn.cpp:100-103 */
 
+/* ---- attention core (decode) ---- */
+void or_attn_split_qg(const float* in, float* q, float* g, int heads, int dim);  /* attn_kernels.cu:16-31 */
+void or_attn_scores(const float* q, const float* k_cache, float* scores, int heads, int kv_heads,
+                    int dim, int pos);                                  /* attn_kernels.cu:72-96 */
+void or_attn_softmax(float* scores, int heads, int n);                  /* attn_kernels.cu:99-158 */
+void or_attn_values(const float* scores, const float* v_cache, float* out, int heads, int kv_heads,
+                    int dim, int pos);                                  /* attn_kernels.cu:162-181 */
+void or_attn_sigmoid_gate(const float* x, const float* g, float* out, int64_t n); /* :185-195 */
+void or_attn_decode(const float* q, const float* k_cache, const float* v_cache, const float* gate,
+                    float* out, float* scratch, int heads, int kv_heads, int dim,
+                    int pos);                                           /* layer_attn.cpp:98-108 */
+
 /* ---- MoE activations ---- */
 void or_silu_mul_f32(const float* g, const float* u, float* h, int64_t n, int threads); /* moe.cu:61-67 */
 void or_swiglu_bf16(const uint16_t* g, const uint16_t* u, uint16_t* h, int64_t n, int threads);

@@ -58,6 +58,12 @@ _SIGS = {
     "or_dequant_gather": ([_P, _I, _P, _I, _I, _P, _I], None),
     "or_dequant_span": ([_P, _I, _U64, _I, _P], None),
     "or_gemv": ([_P, _I, _P, _P, _I, _I, _U64, _I], None),
+    "or_attn_split_qg": ([_P, _P, _P, _I, _I], None),
+    "or_attn_scores": ([_P, _P, _P, _I, _I, _I, _I], None),
+    "or_attn_softmax": ([_P, _I, _I], None),
+    "or_attn_values": ([_P, _P, _P, _I, _I, _I, _I], None),
+    "or_attn_sigmoid_gate": ([_P, _P, _P, _I64], None),
+    "or_attn_decode": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I], None),
 }
 
 _lib = None
@@ -317,3 +323,47 @@ def gemv(weight, ggml_type: int, x, M: int, K: int, element_offset: int = 0, thr
     y = np.empty(M, dtype=F32)
     lib().or_gemv(_p(weight), ggml_type, _p(x), _p(y), M, K, element_offset, threads)
     return y
+
+
+# ---------------------------------------------------------------- attention core (decode)
+def attn_split_qg(qg, heads, dim):
+    qg = _c(qg, F32)
+    q, g = np.empty(heads * dim, F32), np.empty(heads * dim, F32)
+    lib().or_attn_split_qg(_p(qg), _p(q), _p(g), heads, dim)
+    return q, g
+
+
+def attn_scores(q, k_cache, heads, kv_heads, dim, pos):
+    q, k_cache = _c(q, F32), _c(k_cache, F32)
+    s = np.empty(heads * (pos + 1), F32)
+    lib().or_attn_scores(_p(q), _p(k_cache), _p(s), heads, kv_heads, dim, pos)
+    return s
+
+
+def attn_softmax(scores, heads, n):
+    s = _c(scores, F32).copy()
+    lib().or_attn_softmax(_p(s), heads, n)
+    return s
+
+
+def attn_values(scores, v_cache, heads, kv_heads, dim, pos):
+    scores, v_cache = _c(scores, F32), _c(v_cache, F32)
+    out = np.empty(heads * dim, F32)
+    lib().or_attn_values(_p(scores), _p(v_cache), _p(out), heads, kv_heads, dim, pos)
+    return out
+
+
+def attn_sigmoid_gate(x, g):
+    x, g = _c(x, F32), _c(g, F32)
+    out = np.empty_like(x)
+    lib().or_attn_sigmoid_gate(_p(x), _p(g), _p(out), x.size)
+    return out
+
+
+def attn_decode(q, k_cache, v_cache, heads, kv_heads, dim, pos, gate=None):
+    q, k_cache, v_cache = _c(q, F32), _c(k_cache, F32), _c(v_cache, F32)
+    g = None if gate is None else _c(gate, F32)
+    out = np.empty(heads * dim, F32)
+    scratch = np.empty(heads * (pos + 1), F32)
+    lib().or_attn_decode(_p(q), _p(k_cache), _p(v_cache), _p(g), _p(out), _p(scratch), heads, kv_heads, dim, pos)
+    return out

@@ -1,0 +1,473 @@
+// Decode attention core on gfx950: one query position against the KV cache.
+//
+// Reference semantics (src/cuda/attn_kernels.cu, called from
+// src/layer_attn.cpp:82-109 once per token per full-attention layer):
+//   split_qg_kernel :16-31     q[h][j] = qg[h][j], g[h][j] = qg[h][d + j]
+//   score_kernel :72-96        s[h][t] = (q_h . k_t) * rsqrtf(D), t <= pos,
+//                              kv head h / (H / Hkv); cache rows [t][kv][D]
+//   softmax_kernel :99-158     s = expf(s - max) / sum, per head row
+//   value_kernel :162-181      out[h][j] = sum_t s[h][t] * v[t][kv][j]
+//   sigmoid_mul_kernel :185-195 out = x / (1 + expf(-g))
+// plus the cache store of layer_attn.cpp:98-100 (k, v copied to row pos).
+// The reference runs these as separate launches (scores with 32-thread
+// blocks per (head, key), values with one block per head).
+//
+// The separate entry points are kept as drop-ins. The fused decode path is a
+// split-K pass plus a combine: workgroup (split, kv head) takes the G = H/Hkv
+// (8 or 16) query heads that share kv head and 16 or 8 keys (4 lanes per
+// (head, key) for the scores, thread = value column for P.V), so every key and value row of
+// the cache is read from HBM once per call; it writes per-split softmax
+// statistics (max, sum of exp) and unnormalised P.V rows to a caller-provided
+// workspace, and the combine rescales the splits to the global max, divides by
+// the total and applies the sigmoid gate.
+#include <algorithm>
+#include <cmath>
+
+#include "capi_common.hpp"
+#include "device_common.hpp"
+
+namespace qk {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kMaxDim = 256;  // fused path: one thread per value column
+
+float host_rsqrt(int n) { return static_cast<float>(1.0 / std::sqrt(static_cast<double>(n))); }
+
+// ---------------------------------------------------------------- elementwise
+__global__ __launch_bounds__(kBlock) void split_qg_kernel(const float* __restrict__ in, float* __restrict__ q,
+                                                          float* __restrict__ g, int heads, int dim) {
+    const int64_t n = static_cast<int64_t>(heads) * dim;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kBlock) {
+        const int64_t h = i / dim, j = i - h * dim;
+        q[i] = in[h * 2 * dim + j];
+        g[i] = in[h * 2 * dim + dim + j];
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void sigmoid_gate_kernel(const float* x, const float* __restrict__ g,
+                                                              float* out, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kBlock)
+        out[i] = x[i] / (1.0f + expf(-g[i]));
+}
+
+__global__ __launch_bounds__(kBlock) void kv_store_kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                                          float* __restrict__ kc, float* __restrict__ vc, int n) {
+    for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) {
+        kc[i] = k[i];
+        vc[i] = v[i];
+    }
+}
+
+// ---------------------------------------------------------------- drop-in stages
+// One wave per (head, key): dot over dim, lanes strided.
+__global__ __launch_bounds__(kBlock) void scores_kernel(const float* __restrict__ q, const float* __restrict__ kc,
+                                                        float* __restrict__ s, int heads, int kv_heads, int dim,
+                                                        int n_keys, float scale) {
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kBlock / kWave) + wave_in_block();
+    if (wave >= static_cast<int64_t>(heads) * n_keys) return;
+    const int lane = threadIdx.x & 63;
+    const int h = static_cast<int>(wave / n_keys);
+    const int t = static_cast<int>(wave - static_cast<int64_t>(h) * n_keys);
+    const int kv = h / (heads / kv_heads);
+    const float* qh = q + static_cast<size_t>(h) * dim;
+    const float* kt = kc + (static_cast<size_t>(t) * kv_heads + kv) * dim;
+    float sum = 0.f;
+    for (int i = lane; i < dim; i += kWave) sum = __builtin_fmaf(qh[i], kt[i], sum);
+    sum = group_sum<64>(sum);
+    if (lane == 0) s[static_cast<size_t>(h) * n_keys + t] = sum * scale;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_move<0xB1>(v));
+    v = fmaxf(v, dpp_move<0x4E>(v));
+    v = fmaxf(v, dpp_move<0x141>(v));
+    v = fmaxf(v, dpp_move<0x140>(v));
+    v = fmaxf(v, __shfl_xor(v, 16));
+    return fmaxf(v, __shfl_xor(v, 32));
+}
+
+// One block per head row of n scores.
+__global__ __launch_bounds__(kBlock) void softmax_kernel(float* __restrict__ s, int n) {
+    __shared__ float red[kBlock / kWave];
+    float* r = s + static_cast<size_t>(blockIdx.x) * n;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    float m = -INFINITY;
+    for (int i = threadIdx.x; i < n; i += kBlock) m = fmaxf(m, r[i]);
+    m = wave_max(m);
+    if (lane == 0) red[w] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float sum = 0.f;
+    for (int i = threadIdx.x; i < n; i += kBlock) {
+        const float e = expf(r[i] - m);
+        r[i] = e;
+        sum += e;
+    }
+    sum = group_sum<64>(sum);
+    if (lane == 0) red[w] = sum;
+    __syncthreads();
+    sum = (red[0] + red[1]) + (red[2] + red[3]);
+    for (int i = threadIdx.x; i < n; i += kBlock) r[i] /= sum;
+}
+
+// out[h][j]: one thread per (head, column), keys in order.
+__global__ __launch_bounds__(kBlock) void values_kernel(const float* __restrict__ s, const float* __restrict__ vc,
+                                                        float* __restrict__ out, int heads, int kv_heads, int dim,
+                                                        int n_keys) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= static_cast<int64_t>(heads) * dim) return;
+    const int h = static_cast<int>(i / dim), j = static_cast<int>(i - static_cast<int64_t>(h) * dim);
+    const int kv = h / (heads / kv_heads);
+    const float* sh = s + static_cast<size_t>(h) * n_keys;
+    float z = 0.f;
+    for (int t = 0; t < n_keys; ++t) z = __builtin_fmaf(sh[t], vc[(static_cast<size_t>(t) * kv_heads + kv) * dim + j], z);
+    out[i] = z;
+}
+
+// ---------------------------------------------------------------- fused decode
+// Workgroup (split, kv head): G query heads x L keys; T = 4 lanes per (head,
+// key) pair take interleaved float4 chunks of the 256-wide dot product, so
+// the (G * L * 4)-thread workgroup keeps 4 waves per SIMD busy at Qwen3.5's
+// shape instead of one. All of the split's loads go out before the first wait
+// (a wait on one load waits for all loads issued before it). Keys go through
+// LDS (rows padded to kKeyStride floats: the 4 lanes of a pair and the L keys
+// of a head hit different banks); values stay in VGPRs, thread (half, column)
+// holding its column of one half of the keys; the two halves of P.V meet in
+// LDS. Workspace: acc [Hkv][splits][G][D], then m and l [Hkv][splits][G].
+constexpr int kKeyStride = kMaxDim + 4;
+constexpr int kPairLanes = 4;
+
+template <int G, int L>
+__global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
+    const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
+    float* __restrict__ ws_acc, float* __restrict__ ws_m, float* __restrict__ ws_l, int kv_heads, int n_keys,
+    int splits, float scale) {
+    constexpr int D = kMaxDim;                 // this path: head dim 256
+    constexpr int D4 = D / 4;
+    constexpr int NT = G * L * kPairLanes;
+    constexpr int HALVES = NT / D;             // P.V: key groups, one thread per (group, column)
+    constexpr int LH = L / HALVES;             // keys per group
+    constexpr int QCH = G * D4 / NT;           // float4 chunks of q per thread
+    constexpr int KCH = L * D4 / NT;           // float4 chunks of the key tile per thread
+    static_assert(NT % D == 0 && L % HALVES == 0 && (G * D4) % NT == 0 && (L * D4) % NT == 0 &&
+                  L * kPairLanes <= kWave && kWave % (L * kPairLanes) == 0, "decode_split shape");
+    __shared__ float4 q_lds[G][D4];
+    __shared__ __align__(16) float k_lds[L][kKeyStride];
+    __shared__ __align__(16) float p_lds[G][L];
+    __shared__ float acc_lds[HALVES > 1 ? HALVES - 1 : 1][G][D];
+    const int split = blockIdx.x, kv = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int t0 = split * L;
+    const size_t row_stride = static_cast<size_t>(kv_heads) * D;  // floats between consecutive keys
+    const float* kbase = kc + static_cast<size_t>(kv) * D;
+    const float* vbase = vc + static_cast<size_t>(kv) * D;
+    const int col = tid % D, half = tid / D;
+
+    float4 qr[QCH], kr[KCH];
+    float vcol[LH];
+#pragma unroll
+    for (int i = 0; i < QCH; ++i) qr[i] = ld4(q + static_cast<size_t>(kv) * G * D + 4 * (tid + i * NT));
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+        const int c = tid + i * NT;
+        kr[i] = ld4(kbase + static_cast<size_t>(min(t0 + c / D4, n_keys - 1)) * row_stride + 4 * (c % D4));
+    }
+#pragma unroll
+    for (int k2 = 0; k2 < LH; ++k2)  // rows past the end clamped (weight 0)
+        vcol[k2] = vbase[static_cast<size_t>(min(t0 + half * LH + k2, n_keys - 1)) * row_stride + col];
+#pragma unroll
+    for (int i = 0; i < QCH; ++i) {
+        const int c = tid + i * NT;
+        q_lds[c / D4][c % D4] = qr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+        const int c = tid + i * NT;
+        *reinterpret_cast<float4*>(&k_lds[c / D4][4 * (c % D4)]) = kr[i];
+    }
+    __syncthreads();
+
+    // scores: pair (hh, tt) = lanes 4*pair .. +3; lane r takes chunks r, r+4, ...
+    const int pair = tid / kPairLanes, r = tid % kPairLanes;
+    const int hh = pair / L, tt = pair % L;
+    const bool valid = t0 + tt < n_keys;
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll 4
+    for (int c = r; c < D4; c += 2 * kPairLanes) {
+        const float4 kk = *reinterpret_cast<const float4*>(&k_lds[tt][4 * c]);
+        const float4 qq = q_lds[hh][c];
+        const float4 k2 = *reinterpret_cast<const float4*>(&k_lds[tt][4 * (c + kPairLanes)]);
+        const float4 q2 = q_lds[hh][c + kPairLanes];
+        a0 = __builtin_fmaf(qq.x, kk.x, a0);
+        a1 = __builtin_fmaf(q2.x, k2.x, a1);
+        a0 = __builtin_fmaf(qq.y, kk.y, a0);
+        a1 = __builtin_fmaf(q2.y, k2.y, a1);
+        a0 = __builtin_fmaf(qq.z, kk.z, a0);
+        a1 = __builtin_fmaf(q2.z, k2.z, a1);
+        a0 = __builtin_fmaf(qq.w, kk.w, a0);
+        a1 = __builtin_fmaf(q2.w, k2.w, a1);
+    }
+    const float dot = group_sum<kPairLanes>(a0 + a1);
+    const float sc = valid ? dot * scale : -INFINITY;
+    // max and sum over the L keys of head hh: 4*L consecutive lanes
+    constexpr int HL = L * kPairLanes;
+    float m = sc;
+    if constexpr (HL >= 8) m = fmaxf(m, dpp_move<0x141>(m));
+    if constexpr (HL >= 16) m = fmaxf(m, dpp_move<0x140>(m));
+    if constexpr (HL >= 32) m = fmaxf(m, __shfl_xor(m, 16));
+    if constexpr (HL >= 64) m = fmaxf(m, __shfl_xor(m, 32));
+    const float p = valid ? expf(sc - m) : 0.0f;  // every split holds at least one valid key
+    const float l = group_sum<HL>(r == 0 ? p : 0.0f);
+    if (r == 0) p_lds[hh][tt] = p;
+    const size_t stat = (static_cast<size_t>(kv) * splits + split) * G + hh;
+    if (tt == 0 && r == 0) {
+        ws_m[stat] = m;
+        ws_l[stat] = l;
+    }
+    __syncthreads();
+
+    // P.V: thread = (key group `half`, column), all G heads
+    float acc[G];
+#pragma unroll
+    for (int h2 = 0; h2 < G; ++h2) acc[h2] = 0.f;
+#pragma unroll
+    for (int k4 = 0; k4 < LH; k4 += 4) {
+#pragma unroll
+        for (int h2 = 0; h2 < G; ++h2) {
+            const float4 pp = *reinterpret_cast<const float4*>(&p_lds[h2][half * LH + k4]);
+            acc[h2] = __builtin_fmaf(pp.x, vcol[k4], acc[h2]);
+            acc[h2] = __builtin_fmaf(pp.y, vcol[k4 + 1], acc[h2]);
+            acc[h2] = __builtin_fmaf(pp.z, vcol[k4 + 2], acc[h2]);
+            acc[h2] = __builtin_fmaf(pp.w, vcol[k4 + 3], acc[h2]);
+        }
+    }
+    if constexpr (HALVES > 1) {
+        if (half > 0) {
+#pragma unroll
+            for (int h2 = 0; h2 < G; ++h2) acc_lds[half - 1][h2][col] = acc[h2];
+        }
+        __syncthreads();
+        if (half > 0) return;
+#pragma unroll
+        for (int v = 0; v < HALVES - 1; ++v) {
+#pragma unroll
+            for (int h2 = 0; h2 < G; ++h2) acc[h2] += acc_lds[v][h2][col];
+        }
+    }
+#pragma unroll
+    for (int h2 = 0; h2 < G; ++h2) ws_acc[((static_cast<size_t>(kv) * splits + split) * G + h2) * D + col] = acc[h2];
+}
+
+// Workgroup (query head, 64 columns): wave w folds splits w, w+4, ... for the
+// 64 columns (lane = column) into a running (max, weight, sum) with the usual
+// online rescaling, kCombineBatch splits per memory round trip (the partials
+// were written by workgroups on every XCD, so they come from memory); the four
+// wave states merge in LDS, then divide by the total weight and apply the gate.
+constexpr int kCombineCols = 64;
+constexpr int kCombineBatch = 32;
+
+__global__ __launch_bounds__(kBlock) void decode_combine(const float* __restrict__ ws_acc,
+                                                         const float* __restrict__ ws_m,
+                                                         const float* __restrict__ ws_l,
+                                                         const float* __restrict__ gate, float* __restrict__ out,
+                                                         int group, int dim, int splits) {
+    constexpr int NW = kBlock / kWave;
+    __shared__ float zpart[NW][kCombineCols];
+    __shared__ float mpart[NW], tpart[NW];
+    const int h = blockIdx.x;
+    const int kv = h / group, hh = h - kv * group;
+    const int lane = threadIdx.x & 63, w = wave_in_block();
+    const int j = blockIdx.y * kCombineCols + lane;
+    const int jc = min(j, dim - 1);
+    const size_t s0 = static_cast<size_t>(kv) * splits * group + hh;  // stat of split s: s0 + s * group
+    const float* accp = ws_acc + (static_cast<size_t>(kv) * splits * group + hh) * dim + jc;  // split s: + s*group*dim
+    const size_t acc_split = static_cast<size_t>(group) * dim;
+    // Per batch: lane i < kCombineBatch loads the statistics of split
+    // base + i*NW (vector loads; as wave-uniform scalar loads they would queue
+    // behind the scalar cache's small limit of outstanding requests), every
+    // lane loads its column of all kCombineBatch partial rows.
+    float m = -INFINITY, z = 0.f, tot = 0.f;
+    for (int base = w; base < splits; base += NW * kCombineBatch) {
+        const int si = base + min(lane, kCombineBatch - 1) * NW;
+        const bool mine = lane < kCombineBatch && si < splits;
+        const float mi = mine ? ws_m[s0 + static_cast<size_t>(si) * group] : -INFINITY;
+        const float li = mine ? ws_l[s0 + static_cast<size_t>(si) * group] : 0.0f;
+        float a[kCombineBatch];
+#pragma unroll
+        for (int i = 0; i < kCombineBatch; ++i)
+            a[i] = accp[static_cast<size_t>(min(base + i * NW, splits - 1)) * acc_split];
+        const float mb = fmaxf(m, wave_max(mi));
+        const float r = expf(m - mb);  // 0 on the first batch (m = -inf)
+        const float ei = mine ? expf(mi - mb) : 0.0f;
+        tot = __builtin_fmaf(tot, r, group_sum<64>(ei * li));
+        z *= r;
+#pragma unroll
+        for (int i = 0; i < kCombineBatch; ++i)  // weight of split base + i*NW (0 past the end)
+            z = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ei), i)), a[i], z);
+        m = mb;
+    }
+    zpart[w][lane] = z;
+    if (lane == 0) {
+        mpart[w] = m;
+        tpart[w] = tot;
+    }
+    __syncthreads();
+    if (w == 0 && j < dim) {
+        const float M = fmaxf(fmaxf(mpart[0], mpart[1]), fmaxf(mpart[2], mpart[3]));
+        float zz = 0.f, tt = 0.f;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) {
+            if (mpart[v] == -INFINITY) continue;  // a wave with no split (splits < NW)
+            const float e = expf(mpart[v] - M);
+            zz = __builtin_fmaf(e, zpart[v][lane], zz);
+            tt = __builtin_fmaf(e, tpart[v], tt);
+        }
+        float o = zz / tt;
+        if (gate) o = o / (1.0f + expf(-gate[static_cast<size_t>(h) * dim + j]));
+        out[static_cast<size_t>(h) * dim + j] = o;
+    }
+}
+
+// Keys per split of the fused path: 16 for 8 query heads per kv head, 8 for 16
+// (512-thread workgroups either way).
+int split_keys(int group) { return group == 8 ? 16 : 8; }
+
+int fused_splits(int heads, int kv_heads, int n_keys) {
+    const int L = split_keys(heads / kv_heads);
+    return (n_keys + L - 1) / L;
+}
+
+// Shapes of the fused path: head dim 256, 8 or 16 query heads per kv head.
+bool fused_ok(int heads, int kv_heads, int dim, int n_keys) {
+    const int g = heads / kv_heads;
+    (void)n_keys;
+    return dim == kMaxDim && (g == 8 || g == 16);
+}
+
+size_t fused_workspace_bytes(int heads, int kv_heads, int dim, int n_keys) {
+    return static_cast<size_t>(fused_splits(heads, kv_heads, n_keys)) * heads * (dim + 2) * sizeof(float);
+}
+
+}  // namespace
+}  // namespace qk
+
+using namespace qk;
+
+extern "C" {
+
+int qwen_attn_split_qg(const float* qg, float* q, float* gate, int heads, int dim, void* stream) {
+    QK_REQUIRE(heads >= 0 && dim >= 0, "attn_split_qg: negative size");
+    if (heads == 0 || dim == 0) return ok();
+    QK_REQUIRE(qg && q && gate, "attn_split_qg: null pointer");
+    const int64_t n = static_cast<int64_t>(heads) * dim;
+    split_qg_kernel<<<std::min<unsigned>(blocks_for(n, kBlock), 4096u), kBlock, 0, as_stream(stream)>>>(qg, q, gate,
+                                                                                                       heads, dim);
+    return check_launch("attn_split_qg");
+}
+
+int qwen_attn_sigmoid_gate(const float* x, const float* gate, float* out, int n, void* stream) {
+    QK_REQUIRE(n >= 0, "attn_sigmoid_gate: negative size");
+    if (n == 0) return ok();
+    QK_REQUIRE(x && gate && out, "attn_sigmoid_gate: null pointer");
+    sigmoid_gate_kernel<<<std::min<unsigned>(blocks_for(n, kBlock), 4096u), kBlock, 0, as_stream(stream)>>>(x, gate,
+                                                                                                           out, n);
+    return check_launch("attn_sigmoid_gate");
+}
+
+int qwen_attn_kv_store(const float* k, const float* v, float* k_cache, float* v_cache, int pos, int kv_dim,
+                       int max_seq_len, void* stream) {
+    QK_REQUIRE(kv_dim >= 0, "attn_kv_store: negative size");
+    if (pos < 0 || pos >= max_seq_len)
+        return fail(QWEN_STATUS_OUT_OF_RANGE, "attention position exceeds configured context");
+    if (kv_dim == 0) return ok();
+    QK_REQUIRE(k && v && k_cache && v_cache, "attn_kv_store: null pointer");
+    const size_t off = static_cast<size_t>(pos) * kv_dim;
+    kv_store_kernel<<<std::min<unsigned>(blocks_for(kv_dim, kBlock), 1024u), kBlock, 0, as_stream(stream)>>>(
+        k, v, k_cache + off, v_cache + off, kv_dim);
+    return check_launch("attn_kv_store");
+}
+
+#define QK_ATTN_SHAPE(what)                                                                                     \
+    QK_REQUIRE(heads > 0 && kv_heads > 0 && dim > 0 && pos >= 0, what ": bad shape (heads=%d kv_heads=%d "      \
+               "dim=%d pos=%d)", heads, kv_heads, dim, pos);                                                    \
+    QK_REQUIRE(heads % kv_heads == 0, what ": heads %d not a multiple of kv_heads %d", heads, kv_heads)
+
+int qwen_attn_scores(const float* q, const float* k_cache, float* scores, int heads, int kv_heads, int dim, int pos,
+                     void* stream) {
+    QK_ATTN_SHAPE("attn_scores");
+    QK_REQUIRE(q && k_cache && scores, "attn_scores: null pointer");
+    const int64_t waves = static_cast<int64_t>(heads) * (pos + 1);
+    scores_kernel<<<blocks_for(waves, kBlock / kWave), kBlock, 0, as_stream(stream)>>>(q, k_cache, scores, heads,
+                                                                                      kv_heads, dim, pos + 1,
+                                                                                      host_rsqrt(dim));
+    return check_launch("attn_scores");
+}
+
+int qwen_attn_softmax(float* scores, int heads, int valid_len, void* stream) {
+    QK_REQUIRE(heads >= 0 && valid_len >= 0, "attn_softmax: negative size");
+    if (heads == 0 || valid_len == 0) return ok();
+    QK_REQUIRE(scores, "attn_softmax: null pointer");
+    softmax_kernel<<<heads, kBlock, 0, as_stream(stream)>>>(scores, valid_len);
+    return check_launch("attn_softmax");
+}
+
+int qwen_attn_values(const float* scores, const float* v_cache, float* out, int heads, int kv_heads, int dim, int pos,
+                     void* stream) {
+    QK_ATTN_SHAPE("attn_values");
+    QK_REQUIRE(scores && v_cache && out, "attn_values: null pointer");
+    const int64_t n = static_cast<int64_t>(heads) * dim;
+    values_kernel<<<blocks_for(n, kBlock), kBlock, 0, as_stream(stream)>>>(scores, v_cache, out, heads, kv_heads, dim,
+                                                                           pos + 1);
+    return check_launch("attn_values");
+}
+
+size_t qwen_attn_decode_workspace_bytes(int heads, int kv_heads, int dim, int pos) {
+    if (heads <= 0 || kv_heads <= 0 || dim <= 0 || pos < 0 || heads % kv_heads) return 0;
+    const size_t staged = static_cast<size_t>(heads) * (pos + 1) * sizeof(float);  // scores of the staged path
+    return fused_ok(heads, kv_heads, dim, pos + 1)
+               ? std::max(staged, fused_workspace_bytes(heads, kv_heads, dim, pos + 1))
+               : staged;
+}
+
+int qwen_attn_decode(const float* q, const float* k_cache, const float* v_cache, const float* gate, float* out,
+                     int heads, int kv_heads, int dim, int pos, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+    QK_ATTN_SHAPE("attn_decode");
+    QK_REQUIRE(q && k_cache && v_cache && out && workspace, "attn_decode: null pointer");
+    const size_t need = qwen_attn_decode_workspace_bytes(heads, kv_heads, dim, pos);
+    QK_REQUIRE(workspace_bytes >= need, "attn_decode: workspace of %zu bytes, need %zu", workspace_bytes, need);
+    hipStream_t s = as_stream(stream);
+    const int n_keys = pos + 1;
+    if (fused_ok(heads, kv_heads, dim, n_keys) && aligned16(q) && aligned16(k_cache)) {
+        const int g = heads / kv_heads;
+        const int splits = fused_splits(heads, kv_heads, n_keys);
+        float* acc = static_cast<float*>(workspace);
+        float* m = acc + static_cast<size_t>(splits) * heads * dim;
+        float* l = m + static_cast<size_t>(splits) * heads;
+        const dim3 grid(splits, kv_heads);
+        const float scale = host_rsqrt(dim);
+        if (g == 8)
+            decode_split<8, 16><<<grid, 8 * 16 * kPairLanes, 0, s>>>(q, k_cache, v_cache, acc, m, l, kv_heads, n_keys,
+                                                                    splits, scale);
+        else
+            decode_split<16, 8><<<grid, 16 * 8 * kPairLanes, 0, s>>>(q, k_cache, v_cache, acc, m, l, kv_heads,
+                                                                    n_keys, splits, scale);
+        int st = check_launch("attn_decode");
+        if (st) return st;
+        decode_combine<<<dim3(heads, (dim + kCombineCols - 1) / kCombineCols), kBlock, 0, s>>>(acc, m, l, gate, out, g,
+                                                                                            dim, splits);
+        return check_launch("attn_decode");
+    }
+    float* sc = static_cast<float*>(workspace);
+    int st = qwen_attn_scores(q, k_cache, sc, heads, kv_heads, dim, pos, stream);
+    if (!st) st = qwen_attn_softmax(sc, heads, n_keys, stream);
+    if (!st) st = qwen_attn_values(sc, v_cache, out, heads, kv_heads, dim, pos, stream);
+    if (!st && gate) st = qwen_attn_sigmoid_gate(out, gate, out, heads * dim, stream);
+    return st;
+}
+
+}  // extern "C"

@@ -124,6 +124,43 @@ void attn_head_norm(float* x, const float* weight, int heads, int dim, float eps
     check(qwen_attn_head_norm(x, weight, heads, dim, eps, st(stream)));
 }
 
+void attn_split_qg(const float* qg, float* q, float* gate, int heads, int dim, hipStream_t stream) {
+    check(qwen_attn_split_qg(qg, q, gate, heads, dim, st(stream)));
+}
+
+void attn_scores(const float* q, const float* k_cache, float* scores, int q_heads, int kv_heads, int dim, int pos,
+                 hipStream_t stream) {
+    check(qwen_attn_scores(q, k_cache, scores, q_heads, kv_heads, dim, pos, st(stream)));
+}
+
+void attn_softmax(float* scores, int heads, int valid_len, hipStream_t stream) {
+    check(qwen_attn_softmax(scores, heads, valid_len, st(stream)));
+}
+
+void attn_values(const float* scores, const float* v_cache, float* out, int q_heads, int kv_heads, int dim, int pos,
+                 hipStream_t stream) {
+    check(qwen_attn_values(scores, v_cache, out, q_heads, kv_heads, dim, pos, st(stream)));
+}
+
+void attn_sigmoid_gate(const float* attn, const float* gate, float* out, int dim, hipStream_t stream) {
+    check(qwen_attn_sigmoid_gate(attn, gate, out, dim, st(stream)));
+}
+
+void attn_kv_store(const float* k, const float* v, float* k_cache, float* v_cache, int pos, int kv_dim,
+                   int max_seq_len, hipStream_t stream) {
+    check(qwen_attn_kv_store(k, v, k_cache, v_cache, pos, kv_dim, max_seq_len, st(stream)));
+}
+
+size_t attn_decode_workspace_bytes(int heads, int kv_heads, int dim, int pos) {
+    return qwen_attn_decode_workspace_bytes(heads, kv_heads, dim, pos);
+}
+
+void attn_decode(const float* q, const float* k_cache, const float* v_cache, const float* gate, float* out, int heads,
+                 int kv_heads, int dim, int pos, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    check(qwen_attn_decode(q, k_cache, v_cache, gate, out, heads, kv_heads, dim, pos, workspace, workspace_bytes,
+                           st(stream)));
+}
+
 void moe_silu_mul(const float* gate, const float* up, float* hidden, int dim, hipStream_t stream) {
     check(qwen_moe_silu_mul(gate, up, hidden, dim, st(stream)));
 }

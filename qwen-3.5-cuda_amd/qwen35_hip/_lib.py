@@ -58,11 +58,20 @@ SIGNATURES: dict[str, list] = {
     "qwen_gdn_gate_values_rows": [_P] * 6 + [_I, _I, _P],
     "qwen_gdn_recurrent_step": [_P] * 7 + [_I, _I, _I, _I, _P],
     "qwen_gdn_recurrent_rows": [_P] * 7 + [_I, _I, _I, _I, _I, _I64, _I64, _P],
+    "qwen_attn_split_qg": [_P, _P, _P, _I, _I, _P],
+    "qwen_attn_scores": [_P, _P, _P, _I, _I, _I, _I, _P],
+    "qwen_attn_softmax": [_P, _I, _I, _P],
+    "qwen_attn_values": [_P, _P, _P, _I, _I, _I, _I, _P],
+    "qwen_attn_sigmoid_gate": [_P, _P, _P, _I, _P],
+    "qwen_attn_kv_store": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "qwen_attn_decode_workspace_bytes": [_I, _I, _I, _I],
+    "qwen_attn_decode": [_P] * 5 + [_I, _I, _I, _I, _P, ctypes.c_size_t, _P],
     "qwen_matmul_type_supported": [_I],
     "qwen_matmul_dispatch": [_P, _I, _U64, _P, _P, _I, _I, _U64, _P],
 }
 
-_RESTYPES = {"qwen_last_error": ctypes.c_char_p, "qwen_status_name": ctypes.c_char_p}
+_RESTYPES = {"qwen_last_error": ctypes.c_char_p, "qwen_status_name": ctypes.c_char_p,
+             "qwen_attn_decode_workspace_bytes": ctypes.c_size_t}
 
 _lib = None
 
@@ -73,7 +82,7 @@ def header_functions(header: Path | None = None) -> list[str]:
 
     header = header or PACKAGE_DIR.parent / "include" / "qwen35_hip.h"
     text = header.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(qwen_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(qwen_\w+)\s*\(", text, flags=re.M)))
 
 
 def load(path: os.PathLike | str | None = None) -> ctypes.CDLL:

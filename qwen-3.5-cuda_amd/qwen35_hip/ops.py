@@ -270,6 +270,87 @@ def gdn_recurrent_rows(state, qkv, beta, decay, key_heads, value_heads, key_dim,
     return out
 
 
+# ------------------------------------------------------------------ attention core (decode)
+def attn_split_qg(qg, heads, dim, stream=None):
+    _dev(qg, dtype=torch.float32)
+    if qg.numel() != 2 * heads * dim:
+        raise ValueError("qg must hold heads x 2 x dim values")
+    q = torch.empty(heads * dim, dtype=torch.float32, device=qg.device)
+    g = torch.empty_like(q)
+    check(load().qwen_attn_split_qg(_p(qg), _p(q), _p(g), heads, dim, _stream(stream)))
+    return q, g
+
+
+def _attn_check(q, cache, heads, kv_heads, dim, pos):
+    if q.numel() < heads * dim or cache.numel() < (pos + 1) * kv_heads * dim:
+        raise ValueError("q or cache too small for the shape")
+
+
+def attn_scores(q, k_cache, heads, kv_heads, dim, pos, out=None, stream=None):
+    _dev(q, k_cache, dtype=torch.float32)
+    _attn_check(q, k_cache, heads, kv_heads, dim, pos)
+    out = torch.empty(heads * (pos + 1), dtype=torch.float32, device=q.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    check(load().qwen_attn_scores(_p(q), _p(k_cache), _p(out), heads, kv_heads, dim, pos, _stream(stream)))
+    return out
+
+
+def attn_softmax(scores, heads, valid_len, stream=None):
+    _dev(scores, dtype=torch.float32)
+    if scores.numel() < heads * valid_len:
+        raise ValueError("scores too small")
+    check(load().qwen_attn_softmax(_p(scores), heads, valid_len, _stream(stream)))
+    return scores
+
+
+def attn_values(scores, v_cache, heads, kv_heads, dim, pos, out=None, stream=None):
+    _dev(scores, v_cache, dtype=torch.float32)
+    _attn_check(scores, v_cache, heads, kv_heads, 1, pos)
+    out = torch.empty(heads * dim, dtype=torch.float32, device=scores.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    check(load().qwen_attn_values(_p(scores), _p(v_cache), _p(out), heads, kv_heads, dim, pos, _stream(stream)))
+    return out
+
+
+def attn_sigmoid_gate(x, gate, out=None, stream=None):
+    _dev(x, gate, dtype=torch.float32)
+    _same(x.shape, gate)
+    out = torch.empty_like(x) if out is None else out
+    check(load().qwen_attn_sigmoid_gate(_p(x), _p(gate), _p(out), x.numel(), _stream(stream)))
+    return out
+
+
+def attn_kv_store(k, v, k_cache, v_cache, pos, max_seq_len, stream=None):
+    _dev(k, v, k_cache, v_cache, dtype=torch.float32)
+    _same(k.shape, v)
+    if k_cache.numel() < max_seq_len * k.numel() or v_cache.numel() < max_seq_len * k.numel():
+        raise ValueError("caches smaller than max_seq_len rows")
+    check(load().qwen_attn_kv_store(_p(k), _p(v), _p(k_cache), _p(v_cache), pos, k.numel(), max_seq_len,
+                                    _stream(stream)))
+
+
+def attn_decode_workspace_bytes(heads, kv_heads, dim, pos) -> int:
+    return int(load().qwen_attn_decode_workspace_bytes(heads, kv_heads, dim, pos))
+
+
+def attn_decode(q, k_cache, v_cache, heads, kv_heads, dim, pos, gate=None, workspace=None, out=None, stream=None):
+    """One query per head against cache rows 0..pos -> out [heads * dim] (x sigmoid(gate))."""
+    _dev(q, k_cache, v_cache, dtype=torch.float32)
+    _attn_check(q, k_cache, heads, kv_heads, dim, pos)
+    _attn_check(q, v_cache, heads, kv_heads, dim, pos)
+    if gate is not None:
+        _dev(gate, dtype=torch.float32)
+    nbytes = attn_decode_workspace_bytes(heads, kv_heads, dim, pos)
+    if workspace is None:
+        workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+    _dev(workspace)
+    out = torch.empty(heads * dim, dtype=torch.float32, device=q.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    check(load().qwen_attn_decode(_p(q), _p(k_cache), _p(v_cache), _p(gate), _p(out), heads, kv_heads, dim, pos,
+                                  _p(workspace), workspace.numel() * workspace.element_size(), _stream(stream)))
+    return out
+
+
 # ------------------------------------------------------------------ MoE
 def moe_silu_mul(g, u, out=None, stream=None):
     _dev(g, u, dtype=torch.float32)

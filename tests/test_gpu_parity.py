@@ -450,6 +450,104 @@ def test_gdn_recurrent_rejects_wide_values():
         ops.gdn_recurrent_step(s, x, x, x, x, x, 1, 1, 4, 260)
 
 
+# ------------------------------------------------------------------ attention core (decode)
+def _attn_inputs(r, heads, kv_heads, dim, n_keys):
+    q = r.standard_normal(heads * dim).astype(F32)
+    K = r.standard_normal((n_keys, kv_heads * dim)).astype(F32)
+    V = r.standard_normal((n_keys, kv_heads * dim)).astype(F32)
+    g = (2 * r.standard_normal(heads * dim)).astype(F32)
+    return q, K, V, g
+
+
+def _attn_scale(oracle, q, K, V, heads, kv_heads, dim, pos, gate=None):
+    """Condition scale of each output: sum_t p_t |v_tj| (times the gate's sigmoid)."""
+    p = oracle.attn_softmax(oracle.attn_scores(q, K, heads, kv_heads, dim, pos), heads, pos + 1)
+    Vh = np.abs(V.reshape(pos + 1, kv_heads, dim).astype(np.float64))
+    sc = np.stack([p.reshape(heads, -1)[h].astype(np.float64) @ Vh[:, h // (heads // kv_heads)]
+                   for h in range(heads)]).reshape(-1)
+    if gate is not None:
+        sc = sc / (1.0 + np.exp(-gate.astype(np.float64)))
+    return sc
+
+
+def _assert_scaled(got, ref, scale, what, rtol=1e-5):
+    err = np.abs(got.astype(np.float64) - ref) / np.maximum(np.abs(ref.astype(np.float64)), scale)
+    w = int(np.argmax(err))
+    assert err[w] <= rtol, f"{what}: rel err {err[w]:.3e} at {w}: got {got[w]!r} ref {ref[w]!r}"
+
+
+def test_attn_split_qg_gate_and_kv_store(oracle):
+    from qwen35_hip._lib import QwenError
+
+    r = rng(5)
+    heads, dim = 16, 256
+    qg = r.standard_normal(2 * heads * dim).astype(F32)
+    q, g = ops.attn_split_qg(dev(qg), heads, dim)
+    rq, rg = oracle.attn_split_qg(qg, heads, dim)
+    assert_bits_equal(host(q), rq)
+    assert_bits_equal(host(g), rg)
+    x = r.standard_normal(heads * dim).astype(F32)
+    assert_f32_close(host(ops.attn_sigmoid_gate(dev(x), g)), oracle.attn_sigmoid_gate(x, rg), what="gate")
+    kd, max_len = 512, 8
+    kc, vc = torch.zeros(max_len * kd, device="cuda"), torch.zeros(max_len * kd, device="cuda")
+    k, v = r.standard_normal(kd).astype(F32), r.standard_normal(kd).astype(F32)
+    ops.attn_kv_store(dev(k), dev(v), kc, vc, 5, max_len)
+    assert_bits_equal(host(kc).reshape(max_len, kd)[5], k)
+    assert_bits_equal(host(vc).reshape(max_len, kd)[5], v)
+    assert not host(kc).reshape(max_len, kd)[[4, 6]].any()
+    for bad in (-1, max_len):
+        with pytest.raises(QwenError, match="attention position exceeds configured context"):
+            ops.attn_kv_store(dev(k), dev(v), kc, vc, bad, max_len)
+
+
+@pytest.mark.parametrize("pos", [0, 40, 1000])
+def test_attn_stages(oracle, pos):
+    """The reference's three launches: scores, softmax, values (16 query / 2 kv heads of 256)."""
+    heads, kv, dim = 16, 2, 256
+    q, K, V, _ = _attn_inputs(rng(pos + 1), heads, kv, dim, pos + 1)
+    dq, dK, dV = dev(q), dev(K), dev(V)
+    s = ops.attn_scores(dq, dK, heads, kv, dim, pos)
+    rs = oracle.attn_scores(q, K, heads, kv, dim, pos)
+    # a score is a dot product: bound its error by sum |q_i k_i| / sqrt(D)
+    ks = np.abs(K.reshape(pos + 1, kv, dim).astype(np.float64))
+    sscale = np.stack([ks[:, h // 8] @ np.abs(q.reshape(heads, dim)[h]) for h in range(heads)]).reshape(-1) / 16.0
+    _assert_scaled(host(s), rs, sscale, "scores")
+    # softmax of the oracle's scores on both sides: probabilities to 1e-5 relative
+    p = ops.attn_softmax(dev(rs), heads, pos + 1)
+    rp = oracle.attn_softmax(rs, heads, pos + 1)
+    assert_f32_close(host(p), rp, what="softmax")
+    out = ops.attn_values(dev(rp), dV, heads, kv, dim, pos)
+    _assert_scaled(host(out), oracle.attn_values(rp, V, heads, kv, dim, pos),
+                   _attn_scale(oracle, q, K, V, heads, kv, dim, pos), "values")
+
+
+@pytest.mark.parametrize("heads,kv,dim,pos,gated", [
+    (16, 2, 256, 0, True), (16, 2, 256, 31, True), (16, 2, 256, 32, False), (16, 2, 256, 33, True),
+    (16, 2, 256, 1000, True), (16, 2, 256, 4095, True), (8, 2, 128, 200, True), (32, 2, 64, 77, False),
+    (6, 2, 256, 50, True), (16, 2, 100, 45, True), (4, 1, 512, 20, True)])
+def test_attn_decode(oracle, heads, kv, dim, pos, gated):
+    """Fused decode at the Qwen3.5 attention shape across split boundaries (32 keys per
+    split), groups of 4 and 16, and the staged fallback (group 3, dim 100, dim 512)."""
+    q, K, V, g = _attn_inputs(rng(heads * 7 + pos), heads, kv, dim, pos + 1)
+    gate = g if gated else None
+    got = host(ops.attn_decode(dev(q), dev(K), dev(V), heads, kv, dim, pos, gate=None if gate is None else dev(gate)))
+    ref = oracle.attn_decode(q, K, V, heads, kv, dim, pos, gate=gate)
+    _assert_scaled(got, ref, _attn_scale(oracle, q, K, V, heads, kv, dim, pos, gate), f"decode pos {pos}")
+
+
+def test_attn_decode_rejects_small_workspace():
+    from qwen35_hip._lib import QwenError
+
+    heads, kv, dim, pos = 16, 2, 256, 100
+    x = torch.zeros(heads * dim * (pos + 1), device="cuda")
+    need = ops.attn_decode_workspace_bytes(heads, kv, dim, pos)
+    assert need > 0
+    ws = torch.empty(need - 4, dtype=torch.uint8, device="cuda")
+    with pytest.raises(QwenError, match="workspace"):
+        ops.attn_decode(x, x, x, heads, kv, dim, pos, workspace=ws)
+    assert ops.attn_decode_workspace_bytes(6, 4, 64, 3) == 0  # heads not a multiple of kv_heads
+
+
 # ------------------------------------------------------------------ quantized GEMV
 def _gemv_weight(kind: str, rows: int, cols: int, r) -> np.ndarray:
     """GGML bytes of a rows x cols tensor: the C5 table generators for Q4_K/Q6_K

@@ -477,6 +477,76 @@ def test_gdn_gate_values(oracle):
     assert_f32_close(decay, np.exp(a * sp), rtol=2e-6)
 
 
+# ------------------------------------------------------------------ attention core (decode)
+def _attn_f64(q, K, V, heads, kv_heads, dim, gate=None):
+    """softmax(q K^T / sqrt(D)) V per head in float64, query head h reading kv head
+    h // (heads / kv_heads) (consecutive query heads share a kv head)."""
+    n = K.shape[0]
+    Kh = K.reshape(n, kv_heads, dim).astype(np.float64)
+    Vh = V.reshape(n, kv_heads, dim).astype(np.float64)
+    out = np.empty((heads, dim))
+    for h in range(heads):
+        kv = h // (heads // kv_heads)
+        s = Kh[:, kv] @ q.reshape(heads, dim)[h].astype(np.float64) / np.sqrt(dim)
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ Vh[:, kv]
+    out = out.reshape(-1)
+    if gate is not None:
+        out = out / (1.0 + np.exp(-gate.astype(np.float64)))
+    return out
+
+
+def test_attn_split_qg(oracle):
+    qg = np.arange(3 * 2 * 5, dtype=F32)
+    q, g = oracle.attn_split_qg(qg, 3, 5)
+    assert np.array_equal(q, qg.reshape(3, 2, 5)[:, 0].reshape(-1))
+    assert np.array_equal(g, qg.reshape(3, 2, 5)[:, 1].reshape(-1))
+
+
+def test_attn_scores_softmax_values_float64(oracle):
+    """Each stage against float64 numpy; 4 query heads over 2 kv heads, so mapping
+    query head h to kv head h % 2 instead of h // 2 fails."""
+    heads, kv_heads, dim, pos = 4, 2, 16, 9
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal(heads * dim).astype(F32)
+    K = rng.standard_normal((pos + 1, kv_heads * dim)).astype(F32)
+    V = rng.standard_normal((pos + 1, kv_heads * dim)).astype(F32)
+    s = oracle.attn_scores(q, K, heads, kv_heads, dim, pos)
+    s64 = np.stack([K.reshape(pos + 1, kv_heads, dim)[:, h // 2].astype(np.float64) @ q.reshape(heads, dim)[h]
+                    for h in range(heads)]) / np.sqrt(dim)
+    assert_f32_close(s, s64.reshape(-1), rtol=1e-6, what="scores")
+    p = oracle.attn_softmax(s, heads, pos + 1)
+    e = np.exp(s.reshape(heads, -1).astype(np.float64) - s.reshape(heads, -1).max(axis=1, keepdims=True))
+    assert_f32_close(p, (e / e.sum(axis=1, keepdims=True)).reshape(-1), rtol=1e-6, what="softmax")
+    assert np.allclose(p.reshape(heads, -1).sum(axis=1), 1.0, atol=1e-6)
+    out = oracle.attn_values(p, V, heads, kv_heads, dim, pos)
+    ref = np.stack([p.reshape(heads, -1)[h].astype(np.float64) @ V.reshape(pos + 1, kv_heads, dim)[:, h // 2]
+                    for h in range(heads)]).reshape(-1)
+    assert_f32_close(out, ref, group=dim, what="values")
+
+
+def test_attn_softmax_special_cases(oracle):
+    """Shift invariance, a dominant score gives a one-hot row, equal scores a uniform row."""
+    row = np.array([1.0, 2.0, 3.0, -5.0], dtype=F32)
+    a = oracle.attn_softmax(row, 1, 4)
+    b = oracle.attn_softmax(row + 100.0, 1, 4)
+    assert_f32_close(a, b, rtol=2e-6, what="shift")
+    assert np.array_equal(oracle.attn_softmax(np.array([0.0, 200.0, -3.0], dtype=F32), 1, 3), np.array([0, 1, 0], F32))
+    assert np.array_equal(oracle.attn_softmax(np.full(8, 0.7, F32), 1, 8), np.full(8, 0.125, F32))
+
+
+def test_attn_decode_end_to_end(oracle):
+    heads, kv_heads, dim, pos = 16, 2, 256, 40
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal(heads * dim).astype(F32)
+    K = rng.standard_normal((pos + 1, kv_heads * dim)).astype(F32)
+    V = rng.standard_normal((pos + 1, kv_heads * dim)).astype(F32)
+    g = rng.standard_normal(heads * dim).astype(F32)
+    got = oracle.attn_decode(q, K, V, heads, kv_heads, dim, pos, gate=g)
+    assert_f32_close(got, _attn_f64(q, K, V, heads, kv_heads, dim, gate=g), group=dim, what="decode")
+    assert_f32_close(oracle.attn_sigmoid_gate(q, g), q / (1 + np.exp(-g.astype(np.float64))), rtol=1e-6, what="gate")
+
+
 # ------------------------------------------------------------------ MoE
 def test_silu_scalars(oracle):
     assert oracle.silu(0.0) == 0.0
