@@ -272,10 +272,53 @@ def build_next_rows(torch, ops, synth, host):
         k.attn = {"q": qa.cpu().numpy(), "K": kc0.cpu().numpy(), "V": vc0.cpu().numpy(), "g": ga.cpu().numpy()}
         ks.append(k)
 
+    # MoE routing (moe.cu:7-86, layer_moe.cpp:98-140) with the routing kept on the device.
+    T, E, k_sel, Dm = 4096, 256, 8, 2048
+    lg = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32)).to(dev)
+    ti = torch.empty((T, k_sel), dtype=torch.int32, device=dev)
+    tw = torch.empty((T, k_sel), dtype=torch.float32, device=dev)
+
+    def mk_topk(i):
+        ll = lg if i == 0 else lg.clone()
+        return lambda: ops.moe_topk_rows(ll, k_sel, idx=ti, weights=tw)
+    nb = lg.numel() * 4 + 2 * ti.numel() * 4
+    k = Kernel("moe_topk_4096", "router logits [4096 x 256] f32 -> top-8 ids + softmax weights", nb, nb, mk_topk)
+    k.route = {"logits": lg.cpu().numpy()}
+    ks.append(k)
+    ye = torch.from_numpy(rng.standard_normal((T, k_sel, Dm)).astype(np.float32)).to(dev)
+    acc0 = torch.zeros((T, Dm), dtype=torch.float32, device=dev)
+    wts = torch.full((T, k_sel), 0.125, device=dev)
+
+    def mk_wsum(i):
+        yy, aa = (ye, acc0) if i == 0 else (ye.clone(), acc0.clone())
+        return lambda: ops.moe_weighted_sum_rows(aa, yy, wts)
+    nb = ye.numel() * 4 + 2 * acc0.numel() * 4 + wts.numel() * 4
+    k = Kernel("moe_weighted_sum_4096", "acc [4096 x 2048] += sum of 8 weighted expert rows [4096 x 8 x 2048] f32",
+               nb, nb, mk_wsum)
+    k.route = {"y": ye[:64].cpu().numpy(), "w": wts[:64].cpu().numpy()}
+    ks.append(k)
+
     t = synth.q4k_table(256 * 512, 2048, seed_tensor=24)
     add("gemv_expert_q4_k", "Q4_K expert e of [256 x 512 x 2048] x f32 [2048] (layer_moe.cpp:131 gate, "
         "element offset e*512*2048)", "Q4_K", torch.from_numpy(t).to(dev), 256 * 512 * 2048, 512, 2048,
         [e * 512 * 2048 for e in range(256)], 144, t)
+    # the 8 routed experts' gate projections of one token in one launch, ids on the device
+    qt = torch.from_numpy(t).to(dev)
+    ids8 = torch.from_numpy(np.array([3, 77, 141, 200, 9, 250, 31, 128], np.int32)).to(dev)
+    x8 = torch.from_numpy(rng.standard_normal(2048).astype(np.float32)).to(dev)
+    y8 = torch.empty((8, 512), dtype=torch.float32, device=dev)
+
+    def mk_ex(i):
+        # one 151 MB table; each buffer set picks other experts so the rotation still
+        # walks distinct weight bytes
+        ii = ids8 if i == 0 else (ids8 + 8 * i) % 256
+        return lambda: ops.moe_expert_matmul(qt, "Q4_K", 256 * 512 * 2048, 512 * 2048, 256, ii, x8, 0, 512, 2048,
+                                             out=y8)
+    nb = 8 * 512 * 8 * 144 + 2048 * 4 + 8 * 512 * 4
+    k = Kernel("moe_expert_gate_8", "8 routed experts' Q4_K gate projections [8 x 512 x 2048], ids on the device",
+               nb, nb, mk_ex)
+    k.gemv = {"type": 12, "table": t[:8 * 512 * 8 * 144], "M": 8 * 512, "K": 2048, "x": x8.cpu().numpy()}
+    ks.append(k)
     return ks
 
 
@@ -362,16 +405,23 @@ def cpu_baseline(host, kernels, threads: int, budget_s: float, gemv=None):
               "dequant_gather_q4_k": 1024, "dequant_gather_q6_k": 1024}
     gemv = gemv or {}
     for name, g in gemv.items():
-        sample[name] = min(g["M"], 4096) if "M" in g else min(g["rows"], 4) if "rows" in g else 4096
+        sample[name] = (min(g["M"], 4096) if "M" in g else min(g["rows"], 4) if "rows" in g else
+                        64 if "y" in g else 4096)
     full = {"rmsnorm": 36, "qk_norm_rope": 512, "residual_rmsnorm_bf16": 4096, "swiglu_bf16": 4096,
             "shared_swiglu_sigmoid_bf16": 4096, "gdn_frontend": 4096, "gdn_norm_gate": 4096,
             "dequant_gather_q4_k": 8192, "dequant_gather_q6_k": 8192}
     full.update({name: g["M"] if "M" in g else g["rows"] if "rows" in g else 4096 for name, g in gemv.items()})
 
     def runner(name, rows, th):
-        if name.startswith("gemv_"):
+        if name in gemv and "table" in gemv[name]:
             g = gemv[name]
             return lambda: orc.gemv(g["table"], g["type"], g["x"], rows, g["K"], threads=th)
+        if name == "moe_topk_4096":
+            g = gemv[name]
+            return lambda: orc.moe_topk_rows(g["logits"][:rows], 8)
+        if name == "moe_weighted_sum_4096":
+            g = gemv[name]
+            return lambda: orc.moe_weighted_sum_rows(np.zeros((rows, 2048), np.float32), g["y"][:rows], g["w"][:rows])
         if name.startswith("attn_decode"):
             g = gemv[name]
             n = min(rows, 4096)
@@ -568,8 +618,8 @@ def main() -> int:
         if not args.no_cpu:
             threads = max(1, min(16, os.cpu_count() or 1))
             cpu_next, _ = cpu_baseline(host, nxt, threads, args.cpu_seconds / 3,
-                                       gemv={k.name: getattr(k, "gemv", None) or getattr(k, "gdn", None) or k.attn
-                                             for k in nxt})
+                                       gemv={k.name: getattr(k, "gemv", None) or getattr(k, "gdn", None) or
+                                             getattr(k, "attn", None) or k.route for k in nxt})
         next_rows = {
             k.name: {"config": k.config, "bytes": k.bytes, "us_per_call": round(k.us, 3),
                      "gbps": round(k.bytes / k.us / 1e3, 1), "frac_peak": round(k.bytes / k.us / 1e3 / PEAK_GBPS, 4),

@@ -37,6 +37,13 @@ void attn_sigmoid_gate(const float* attn, const float* gate, float* out, int dim
 // hidden = silu(gate) * up.  ref: src/layer_moe.cpp:10
 void moe_silu_mul(const float* gate, const float* up, float* hidden, int dim, hipStream_t stream);
 
+// Top-k experts of the router logits and softmax weights over the picks
+// (idx[0] = -1, weight[0] = NaN for a non-finite logit).  ref: src/layer_moe.cpp:9
+void moe_topk(const float* router, int* top_idx, float* top_weight, int experts, int k, hipStream_t stream);
+
+// accum += weight * expert_out.  ref: src/layer_moe.cpp:11
+void moe_add(float* accum, const float* expert_out, float weight, int dim, hipStream_t stream);
+
 // accum += shared_out * sigmoid(sgate[0]) (sgate on the device).  ref: src/layer_moe.cpp:12
 void moe_shared_add(float* accum, const float* shared_out, const float* sgate, int dim, hipStream_t stream);
 
@@ -58,6 +65,14 @@ void attn_decode(const float* q, const float* k_cache, const float* v_cache, con
 // moe_shared_add per row: accum, shared_out [rows x dim], sgate [rows].
 void moe_shared_add_rows(float* accum, const float* shared_out, const float* sgate, int rows, int dim,
                          hipStream_t stream);
+
+// moe_topk per row: router [rows x experts] -> top_idx, top_weight [rows x k].
+void moe_topk_rows(const float* router, int* top_idx, float* top_weight, int rows, int experts, int k,
+                   hipStream_t stream);
+
+// accum[t] += sum_j weight[t][j] * expert_out[t][j] with the weights on the device.
+void moe_weighted_sum_rows(float* accum, const float* expert_out, const float* weight, int rows, int k, int dim,
+                           hipStream_t stream);
 
 // bf16 SwiGLU over n elements: hidden = bf16(silu(gate) * up).
 void swiglu_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* hidden, int64_t n, hipStream_t stream);

@@ -23,6 +23,13 @@ bool matmul_type_supported(GgmlType type);
 void matmul_dispatch(const QuantTensor& weight, const float* x, float* y, int M, int K, hipStream_t stream = nullptr,
                      uint64_t element_offset = 0);
 
+// n_sel expert GEMVs with the expert ids on the device: y[j] = W_{idx[j]} x_j,
+// expert e at element offset e * expert_stride, x_j = x + j * x_stride, y
+// [n_sel x M]; an invalid id gives a NaN row. Throws as matmul_dispatch.
+void moe_expert_matmul(const QuantTensor& weight, uint64_t expert_stride, int n_experts, const int32_t* idx,
+                       int n_sel, const float* x, int64_t x_stride, float* y, int M, int K,
+                       hipStream_t stream = nullptr);
+
 // out[i] = element (row * cols + i) of `tensor`.  ref: include/matmul_q4.hpp:24-30
 void dequantize_row(const QuantTensor& tensor, float* out, int row, int cols, hipStream_t stream = nullptr);
 

@@ -205,6 +205,38 @@ int qwen_attn_decode(const float* q, const float* k_cache, const float* v_cache,
                      float* out, int heads, int kv_heads, int dim, int pos, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* ====================================================================== MoE routing
+ * The reference picks experts on the device, copies them to the host and syncs
+ * (src/layer_moe.cpp:98-124); these entry points keep the routing on the device. */
+
+/* Top-k of n router logits, then softmax over the k picks: idx int32 [k] (strictly
+ * greater wins, ties to the lower index), weights [k]; a non-finite logit gives
+ * idx[0] = -1, weights[0] = NaN. 0 < k <= min(n, 64), n <= 1024.
+ * ref: src/layer_moe.cpp:9 (moe_topk decl), src/cuda/moe.cu:7-57 */
+int qwen_moe_topk(const float* logits, int32_t* idx, float* weights, int n, int k, void* stream);
+/* Row-batched form: logits [rows x n] -> idx, weights [rows x k]. */
+int qwen_moe_topk_rows(const float* logits, int32_t* idx, float* weights, int rows, int n, int k,
+                       void* stream);
+
+/* out += a * x over n elements (a from the host).
+ * ref: src/layer_moe.cpp:11 (moe_add decl), src/cuda/moe.cu:76-86 */
+int qwen_moe_add(float* out, const float* x, float a, int n, void* stream);
+
+/* out[t] += sum_j weights[t][j] * expert_out[t][j] for j < k (weights on the device):
+ * the layer's k moe_add calls per token, src/layer_moe.cpp:127-140.
+ * out [rows x dim], expert_out [rows x k x dim], weights [rows x k]. */
+int qwen_moe_weighted_sum_rows(float* out, const float* expert_out, const float* weights, int rows,
+                               int k, int dim, void* stream);
+
+/* n_sel expert GEMVs in one launch with the expert ids on the device:
+ * y[j] = W_e x_j, e = idx[j], W_e = the M x K rows at element offset e * expert_stride
+ * of a GGML tensor of n_experts experts; x_j = x + j * x_stride; y [n_sel x M]. An id
+ * outside [0, n_experts) gives a NaN row. Statuses as qwen_matmul_dispatch.
+ * ref: src/layer_moe.cpp:129-138 (matmul_dispatch at element offset e * stride) */
+int qwen_moe_expert_matmul(const void* weight, int type, uint64_t num_elements, uint64_t expert_stride,
+                           int n_experts, const int32_t* idx, int n_sel, const float* x,
+                           int64_t x_stride, float* y, int M, int K, void* stream);
+
 /* ====================================================================== MoE
  * h = silu(g) * u (fp32).  ref: src/layer_moe.cpp:10 (moe_silu_mul decl),
  * src/cuda/moe.cu:61-72 */

@@ -546,6 +546,76 @@ void or_attn_decode(const float* q, const float* k_cache, const float* v_cache, 
     if (gate) or_attn_sigmoid_gate(out, gate, out, static_cast<int64_t>(heads) * dim);
 }
 
+// ---------------------------------------------------------------- MoE routing
+
+// Top-k of n router logits by repeated selection (strictly greater wins, so
+// ties go to the lowest index), then a softmax over the k picks; a non-finite
+// logit gives idx[0] = -1, w[0] = NaN and leaves the rest untouched.
+//                                                     -- src/cuda/moe.cu:7-51
+void or_moe_topk(const float* x, int32_t* idx, float* w, int n, int k) {
+    for (int i = 0; i < n; ++i)
+        if (!std::isfinite(x[i])) {
+            idx[0] = -1;
+            w[0] = NAN;
+            return;
+        }
+    for (int j = 0; j < k; ++j) {
+        float best = -INFINITY;
+        int bi = -1;
+        for (int i = 0; i < n; ++i) {
+            bool used = false;
+            for (int p = 0; p < j; ++p) used |= (idx[p] == i);
+            if (!used && x[i] > best) {
+                best = x[i];
+                bi = i;
+            }
+        }
+        idx[j] = bi;
+        w[j] = best;
+    }
+    float mx = w[0];
+    for (int j = 1; j < k; ++j) mx = std::fmax(mx, w[j]);
+    double sum = 0.0;
+    for (int j = 0; j < k; ++j) {
+        w[j] = exp_f(w[j] - mx);
+        sum += w[j];
+    }
+    const float fs = static_cast<float>(sum);
+    for (int j = 0; j < k; ++j) w[j] /= fs;
+}
+
+void or_moe_topk_rows(const float* x, int32_t* idx, float* w, int rows, int n, int k) {
+    for (int64_t t = 0; t < rows; ++t) or_moe_topk(x + t * n, idx + t * k, w + t * k, n, k);
+}
+
+// out += a * x                                        -- src/cuda/moe.cu:76-86
+// (one fused multiply-add, as nvcc contracts `out[i] += a * x[i]`)
+void or_moe_add(float* out, const float* x, float a, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = std::fma(a, x[i], out[i]);
+}
+
+// out[t] += sum_j w[t][j] * y[t][j]: the layer's k moe_add calls per token
+// (src/layer_moe.cpp:127-140) with the weights read from device memory.
+void or_moe_weighted_sum_rows(float* out, const float* y, const float* w, int rows, int k, int dim) {
+    for (int64_t t = 0; t < rows; ++t)
+        for (int j = 0; j < k; ++j) or_moe_add(out + t * dim, y + (t * k + j) * dim, w[t * k + j], dim);
+}
+
+// y[j] = W[idx[j] * expert_stride ...] x[j * x_stride ...]: matmul_dispatch of
+// each selected expert (src/layer_moe.cpp:131-138, element offset
+// e * stride). An id outside [0, n_experts) gives a NaN row.
+void or_moe_expert_gemv(const uint8_t* w, int type, const int32_t* idx, int n_sel, int n_experts,
+                        uint64_t expert_stride, const float* x, int64_t x_stride, float* y, int M, int K) {
+    for (int j = 0; j < n_sel; ++j) {
+        float* yj = y + static_cast<int64_t>(j) * M;
+        if (idx[j] < 0 || idx[j] >= n_experts) {
+            for (int m = 0; m < M; ++m) yj[m] = NAN;
+            continue;
+        }
+        or_gemv(w, type, x + j * x_stride, yj, M, K, static_cast<uint64_t>(idx[j]) * expert_stride, 1);
+    }
+}
+
 // ---------------------------------------------------------------- MoE activations
 
 // h = silu(g) * u                                    -- src/cuda/moe.cu:61-67

@@ -100,6 +100,16 @@ void or_attn_decode(const float* q, const float* k_cache, const float* v_cache, 
                     float* out, float* scratch, int heads, int kv_heads, int dim,
                     int pos);                                           /* layer_attn.cpp:98-108 */
 
+/* ---- MoE routing ---- */
+void or_moe_topk(const float* x, int32_t* idx, float* w, int n, int k);   /* moe.cu:7-51 */
+void or_moe_topk_rows(const float* x, int32_t* idx, float* w, int rows, int n, int k);
+void or_moe_add(float* out, const float* x, float a, int64_t n);          /* moe.cu:76-86 */
+void or_moe_weighted_sum_rows(float* out, const float* y, const float* w, int rows, int k,
+                              int dim);                                  /* layer_moe.cpp:127-140 */
+void or_moe_expert_gemv(const uint8_t* w, int type, const int32_t* idx, int n_sel, int n_experts,
+                        uint64_t expert_stride, const float* x, int64_t x_stride, float* y, int M,
+                        int K);                                          /* layer_moe.cpp:131-138 */
+
 /* ---- MoE activations ---- */
 void or_silu_mul_f32(const float* g, const float* u, float* h, int64_t n, int threads); /* moe.cu:61-67 */
 void or_swiglu_bf16(const uint16_t* g, const uint16_t* u, uint16_t* h, int64_t n, int threads);

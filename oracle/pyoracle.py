@@ -59,6 +59,10 @@ _SIGS = {
     "or_dequant_span": ([_P, _I, _U64, _I, _P], None),
     "or_gemv": ([_P, _I, _P, _P, _I, _I, _U64, _I], None),
     "or_attn_split_qg": ([_P, _P, _P, _I, _I], None),
+    "or_moe_topk_rows": ([_P, _P, _P, _I, _I, _I], None),
+    "or_moe_add": ([_P, _P, ctypes.c_float, _I64], None),
+    "or_moe_weighted_sum_rows": ([_P, _P, _P, _I, _I, _I], None),
+    "or_moe_expert_gemv": ([_P, _I, _P, _I, _I, _U64, _P, _I64, _P, _I, _I], None),
     "or_attn_scores": ([_P, _P, _P, _I, _I, _I, _I], None),
     "or_attn_softmax": ([_P, _I, _I], None),
     "or_attn_values": ([_P, _P, _P, _I, _I, _I, _I], None),
@@ -367,3 +371,38 @@ def attn_decode(q, k_cache, v_cache, heads, kv_heads, dim, pos, gate=None):
     scratch = np.empty(heads * (pos + 1), F32)
     lib().or_attn_decode(_p(q), _p(k_cache), _p(v_cache), _p(g), _p(out), _p(scratch), heads, kv_heads, dim, pos)
     return out
+
+
+# ---------------------------------------------------------------- MoE routing
+def moe_topk_rows(x, k, idx=None, w=None):
+    """x [rows, n] -> idx int32 [rows, k], w [rows, k] (inputs idx / w give the
+    untouched entries of a non-finite row)."""
+    x = _c(x, F32)
+    rows, n = x.shape
+    idx = np.zeros((rows, k), np.int32) if idx is None else _c(idx, I32).copy()
+    w = np.zeros((rows, k), F32) if w is None else _c(w, F32).copy()
+    lib().or_moe_topk_rows(_p(x), _p(idx), _p(w), rows, n, k)
+    return idx, w
+
+
+def moe_add(out, x, a):
+    out = _c(out, F32).copy()
+    lib().or_moe_add(_p(out), _p(_c(x, F32)), a, out.size)
+    return out
+
+
+def moe_weighted_sum_rows(out, y, w):
+    """out [rows, dim] += sum_j w[rows, k] * y[rows, k, dim]."""
+    out = _c(out, F32).copy()
+    y, w = _c(y, F32), _c(w, F32)
+    rows, k, dim = y.shape
+    lib().or_moe_weighted_sum_rows(_p(out), _p(y), _p(w), rows, k, dim)
+    return out
+
+
+def moe_expert_gemv(weight, ggml_type, idx, n_experts, expert_stride, x, x_stride, M, K):
+    weight, idx, x = _c(weight, U8), _c(idx, I32), _c(x, F32)
+    y = np.empty((idx.size, M), F32)
+    lib().or_moe_expert_gemv(_p(weight), ggml_type, _p(idx), idx.size, n_experts, expert_stride, _p(x), x_stride,
+                             _p(y), M, K)
+    return y

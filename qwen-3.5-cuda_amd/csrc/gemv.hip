@@ -173,13 +173,39 @@ __device__ __forceinline__ float block_dot(const uint8_t* blk, const LaneX<TYPE>
     }
 }
 
+// Device-side expert selection (MoE): launch row blockIdx.y runs selected
+// expert idx[blockIdx.y] -- weight rows at element offset idx * stride -- on
+// x + blockIdx.y * x_stride, writing y + blockIdx.y * M. An id outside
+// [0, n_experts) gives a NaN row. idx == nullptr: a plain GEMV.
+struct Experts {
+    const int32_t* idx;
+    int n_experts;
+    uint64_t stride;  // elements between experts (a multiple of 256 on the fast path)
+    int64_t x_stride;
+};
+
+// Applies the selection of launch row blockIdx.y; false if the expert id is
+// invalid (the caller writes NaN rows).
+__device__ __forceinline__ bool select_expert(const Experts& ex, int M, int64_t& x_off, int64_t& y_off,
+                                              uint64_t& element_offset) {
+    x_off = y_off = 0;
+    if (!ex.idx) return true;
+    const int j = blockIdx.y;
+    const int e = ex.idx[j];
+    x_off = static_cast<int64_t>(j) * ex.x_stride;
+    y_off = static_cast<int64_t>(j) * M;
+    if (e < 0 || e >= ex.n_experts) return false;
+    element_offset += static_cast<uint64_t>(e) * ex.stride;
+    return true;
+}
+
 // Fast path. Row groups: when 8 | nb, group = one row and unit (row, slice s)
 // starts at block ub0 + row*nb + 8s; when nb | 8, group = 8/nb rows (P) and
 // unit u starts at block ub0 + 8u. A wave owns groups g0 .. g0+R-1.
 template <int TYPE, int R>
 __global__ __launch_bounds__(kGemvBlock) void gemv_kquant(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                           float* __restrict__ y, int M, int nb, uint64_t ub0,
-                                                          int groups, uint64_t tensor_bytes) {
+                                                          int groups, uint64_t tensor_bytes, Experts ex) {
     constexpr int BB = KQuant<TYPE>::kBlockBytes;
     constexpr int UB = 8 * BB;             // unit bytes
     constexpr int CPU = UB / 16;           // 16-byte chunks per unit
@@ -193,6 +219,16 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant(const uint8_t* __restr
     const bool packed = nb < 8;
     const int S = packed ? 1 : nb >> 3;
     const int P = packed ? 8 / nb : 1;     // rows per unit
+    uint64_t eoff = 0;
+    int64_t x_off, y_off;
+    const bool ok_e = select_expert(ex, M, x_off, y_off, eoff);
+    x += x_off;
+    y += y_off;
+    if (!ok_e) {  // uniform per workgroup: no barrier is reached
+        for (int r = g0 * P + lane; r < min((g0 + R) * P, M); r += kWave) y[r] = __builtin_nanf("");
+        return;
+    }
+    ub0 += eoff / 256;
 
     float acc[R];
 #pragma unroll
@@ -255,10 +291,18 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant(const uint8_t* __restr
 // decode.
 __global__ __launch_bounds__(kBlock) void gemv_any(const uint8_t* __restrict__ w, int type,
                                                    const float* __restrict__ x, float* __restrict__ y, int M, int K,
-                                                   uint64_t element_offset) {
+                                                   uint64_t element_offset, Experts ex) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * (kBlock / kWave) + wave_in_block();
     if (row >= M) return;
+    int64_t x_off, y_off;
+    const bool ok_e = select_expert(ex, M, x_off, y_off, element_offset);
+    x += x_off;
+    y += y_off;
+    if (!ok_e) {
+        if (lane == 0) y[row] = __builtin_nanf("");
+        return;
+    }
     const uint64_t base = element_offset + static_cast<uint64_t>(row) * K;
     float s = 0.f;
     for (int k = lane; k < K; k += kWave) s = __builtin_fmaf(dequant_elem(w, type, base + k), x[k], s);
@@ -268,25 +312,52 @@ __global__ __launch_bounds__(kBlock) void gemv_any(const uint8_t* __restrict__ w
 
 template <int TYPE, int R>
 void launch_kquant(const uint8_t* w, const float* x, float* y, int M, int nb, uint64_t ub0, int groups,
-                   uint64_t tensor_bytes, hipStream_t s) {
+                   uint64_t tensor_bytes, const Experts& ex, int n_sel, hipStream_t s) {
     constexpr int CPU = KQuant<TYPE>::kBlockBytes * 8 / 16;
     const size_t lds = static_cast<size_t>(kGemvWaves) * R * CPU * 16;
     const int waves = (groups + R - 1) / R;
-    gemv_kquant<TYPE, R><<<blocks_for(waves, kGemvWaves), kGemvBlock, lds, s>>>(w, x, y, M, nb, ub0, groups,
-                                                                               tensor_bytes);
+    gemv_kquant<TYPE, R><<<dim3(blocks_for(waves, kGemvWaves), n_sel), kGemvBlock, lds, s>>>(
+        w, x, y, M, nb, ub0, groups, tensor_bytes, ex);
 }
 
 template <int TYPE>
 void dispatch_kquant(const uint8_t* w, const float* x, float* y, int M, int nb, uint64_t ub0, int groups,
-                     uint64_t tensor_bytes, hipStream_t s) {
+                     uint64_t tensor_bytes, const Experts& ex, int n_sel, hipStream_t s) {
     // Units per wave: enough waves to fill 256 CUs several times over. More than
     // 4 units per wave measured slower (fewer waves per SIMD to hide latency).
-    if (groups >= 4 * 4096)
-        launch_kquant<TYPE, 4>(w, x, y, M, nb, ub0, groups, tensor_bytes, s);
-    else if (groups >= 2 * 4096)
-        launch_kquant<TYPE, 2>(w, x, y, M, nb, ub0, groups, tensor_bytes, s);
+    const int64_t all = static_cast<int64_t>(groups) * n_sel;
+    if (all >= 4 * 4096)
+        launch_kquant<TYPE, 4>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, n_sel, s);
+    else if (all >= 2 * 4096)
+        launch_kquant<TYPE, 2>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, n_sel, s);
     else
-        launch_kquant<TYPE, 1>(w, x, y, M, nb, ub0, groups, tensor_bytes, s);
+        launch_kquant<TYPE, 1>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, n_sel, s);
+}
+
+// One GEMV (ex.idx == nullptr, n_sel == 1) or n_sel expert GEMVs of one launch.
+// The caller has validated the shapes against the tensor.
+int launch_gemv(const uint8_t* w, int type, uint64_t num_elements, const float* x, float* y, int M, int K,
+                uint64_t element_offset, const Experts& ex, int n_sel, hipStream_t s, const char* what) {
+    const bool kquant = type == kQ4_K || type == kQ6_K;
+    const int nb = K / 256;
+    const uint64_t tensor_bytes = (num_elements / 256) * static_cast<uint64_t>(block_bytes(type));
+    const bool shape_ok = K % 256 == 0 && (nb % 8 == 0 || 8 % nb == 0) && element_offset % 256 == 0 &&
+                          num_elements % 256 == 0 && tensor_bytes % 16 == 0 && (!ex.idx || ex.stride % 256 == 0);
+    // Units start 16-byte aligned: always for 144-byte blocks, every 8 blocks for 210.
+    const bool aligned = aligned16(w) && aligned16(x) && (!ex.idx || ex.x_stride % 4 == 0) &&
+                         (type == kQ4_K || ((element_offset / 256) % 8 == 0 && (!ex.idx || (ex.stride / 256) % 8 == 0)));
+    if (kquant && shape_ok && aligned) {
+        const uint64_t ub0 = element_offset / 256;
+        const int groups = nb >= 8 ? M : (M + 8 / nb - 1) / (8 / nb);
+        if (type == kQ4_K)
+            dispatch_kquant<kQ4_K>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, n_sel, s);
+        else
+            dispatch_kquant<kQ6_K>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, n_sel, s);
+    } else {
+        gemv_any<<<dim3(blocks_for(M, kBlock / kWave), n_sel), kBlock, 0, s>>>(w, type, x, y, M, K, element_offset,
+                                                                             ex);
+    }
+    return check_launch(what);
 }
 
 }  // namespace
@@ -307,26 +378,26 @@ int qwen_matmul_dispatch(const void* weight, int type, uint64_t num_elements, co
         static_cast<uint64_t>(M) * static_cast<uint64_t>(K) > num_elements - element_offset)
         return fail(QWEN_STATUS_OUT_OF_RANGE, "GEMV shape exceeds tensor (M=%d, K=%d)", M, K);
     QK_REQUIRE(x && y, "matmul_dispatch: null pointer");
-    hipStream_t s = as_stream(stream);
-    const uint8_t* w = static_cast<const uint8_t*>(weight);
-    const bool kquant = type == kQ4_K || type == kQ6_K;
-    const int nb = K / 256;
-    const uint64_t tensor_bytes = (num_elements / 256) * static_cast<uint64_t>(block_bytes(type));
-    const bool shape_ok = K % 256 == 0 && (nb % 8 == 0 || 8 % nb == 0) && element_offset % 256 == 0 &&
-                          num_elements % 256 == 0 && tensor_bytes % 16 == 0;
-    // Units start 16-byte aligned: always for 144-byte blocks, every 8 blocks for 210.
-    const bool aligned = aligned16(w) && aligned16(x) && (type == kQ4_K || (element_offset / 256) % 8 == 0);
-    if (kquant && shape_ok && aligned) {
-        const uint64_t ub0 = element_offset / 256;
-        const int groups = nb >= 8 ? M : (M + 8 / nb - 1) / (8 / nb);
-        if (type == kQ4_K)
-            dispatch_kquant<kQ4_K>(w, x, y, M, nb, ub0, groups, tensor_bytes, s);
-        else
-            dispatch_kquant<kQ6_K>(w, x, y, M, nb, ub0, groups, tensor_bytes, s);
-    } else {
-        gemv_any<<<blocks_for(M, kBlock / kWave), kBlock, 0, s>>>(w, type, x, y, M, K, element_offset);
-    }
-    return check_launch("matmul_dispatch");
+    return launch_gemv(static_cast<const uint8_t*>(weight), type, num_elements, x, y, M, K, element_offset,
+                       Experts{nullptr, 0, 0, 0}, 1, as_stream(stream), "matmul_dispatch");
+}
+
+int qwen_moe_expert_matmul(const void* weight, int type, uint64_t num_elements, uint64_t expert_stride, int n_experts,
+                           const int32_t* idx, int n_sel, const float* x, int64_t x_stride, float* y, int M, int K,
+                           void* stream) {
+    if (!weight) return fail(QWEN_STATUS_INVALID_ARGUMENT, "tensor is not loaded");
+    if (!type_supported(type)) return fail(QWEN_STATUS_UNSUPPORTED_TYPE, "unsupported GGML type %d", type);
+    QK_REQUIRE(n_sel >= 0 && n_experts > 0 && x_stride >= 0, "moe_expert_matmul: bad n_sel %d / n_experts %d",
+               n_sel, n_experts);
+    if (M <= 0 || K <= 0 || static_cast<uint64_t>(M) * static_cast<uint64_t>(K) > expert_stride ||
+        expert_stride > num_elements / static_cast<uint64_t>(n_experts))
+        return fail(QWEN_STATUS_OUT_OF_RANGE, "GEMV shape exceeds tensor (M=%d, K=%d, %d experts)", M, K, n_experts);
+    if (n_sel == 0) return ok();
+    QK_REQUIRE(idx && x && y, "moe_expert_matmul: null pointer");
+    QK_REQUIRE(n_sel <= 65535, "moe_expert_matmul: n_sel %d too large", n_sel);
+    return launch_gemv(static_cast<const uint8_t*>(weight), type, num_elements, x, y, M, K, 0,
+                       Experts{idx, n_experts, expert_stride, x_stride}, n_sel, as_stream(stream),
+                       "moe_expert_matmul");
 }
 
 }  // extern "C"

@@ -1,0 +1,172 @@
+// MoE routing and weighted accumulate on gfx950.
+//
+// Reference semantics (src/cuda/moe.cu):
+//   topk_kernel :7-51   one thread: any non-finite logit -> idx[0] = -1,
+//                       w[0] = NaN (rest untouched); else k rounds of "largest
+//                       unused logit, strictly greater wins" (ties to the lower
+//                       index), then w = softmax over the k picks
+//   add_kernel :76-86   out += a * x
+// The layer (src/layer_moe.cpp:98-140) copies idx / w to the host, waits on
+// the stream, and launches k expert GEMV chains with host-side offsets and k
+// moe_add calls with host-side weights.
+//
+// Here top-k is one wave per token row: lane L holds logits L, L+64, ...; each
+// round is a wave arg-max (value, then lower index) and the winner's lane marks
+// it used; the softmax over the picks runs in the first k lanes. Routing stays
+// on the device: qwen_moe_expert_matmul (gemv.hip) reads the expert ids, and
+// qwen_moe_weighted_sum_rows reads the weights, so no host round trip is needed.
+#include <algorithm>
+#include <cmath>
+
+#include "capi_common.hpp"
+#include "device_common.hpp"
+
+namespace qk {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / kWave;
+constexpr int kMaxExperts = 16 * kWave;  // logits per row held in VGPRs (16 per lane)
+
+// Arg-max of (v, i) pairs over the wave: larger value wins, then lower index.
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const float ov = __shfl_xor(v, off);
+        const int oi = __shfl_xor(i, off);
+        if (ov > v || (ov == v && oi < i)) {
+            v = ov;
+            i = oi;
+        }
+    }
+}
+
+template <int VPL>
+__global__ __launch_bounds__(kBlock) void topk_rows_kernel(const float* __restrict__ x, int32_t* __restrict__ idx,
+                                                           float* __restrict__ w, int rows, int n, int k) {
+    const int row = blockIdx.x * kWaves + wave_in_block();
+    if (row >= rows) return;  // wave-uniform
+    const int lane = threadIdx.x & 63;
+    const float* xr = x + static_cast<size_t>(row) * n;
+    float v[VPL];
+    bool finite = true;
+#pragma unroll
+    for (int s = 0; s < VPL; ++s) {
+        const int i = lane + s * kWave;
+        v[s] = i < n ? xr[i] : -INFINITY;
+        if (i < n && !isfinite(v[s])) finite = false;
+    }
+    int32_t* ir = idx + static_cast<size_t>(row) * k;
+    float* wr = w + static_cast<size_t>(row) * k;
+    if (__any(!finite)) {
+        if (lane == 0) {
+            ir[0] = -1;
+            wr[0] = __builtin_nanf("");
+        }
+        return;
+    }
+    unsigned used = 0;      // bit s: logit lane + 64 s already picked
+    float pick_v = 0.f;     // lane j < k: value of pick j
+    int pick_i = -1;
+    for (int j = 0; j < k; ++j) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int s = 0; s < VPL; ++s) {
+            const int i = lane + s * kWave;
+            if (i < n && !((used >> s) & 1u) && (v[s] > bv || bi == 0x7fffffff)) {
+                bv = v[s];
+                bi = i;
+            }
+        }
+        wave_argmax(bv, bi);
+        if ((bi & (kWave - 1)) == lane) used |= 1u << (bi / kWave);
+        if (lane == j) {
+            pick_v = bv;
+            pick_i = bi;
+        }
+    }
+    // softmax over the picks (lanes < k); the first pick is the largest
+    const float mx = __shfl(pick_v, 0);
+    const float e = lane < k ? expf(pick_v - mx) : 0.0f;
+    const float sum = group_sum<64>(e);
+    if (lane < k) {
+        ir[lane] = pick_i;
+        wr[lane] = e / sum;
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void moe_add_kernel(float* __restrict__ out, const float* __restrict__ x,
+                                                         float a, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kBlock)
+        out[i] = __builtin_fmaf(a, x[i], out[i]);
+}
+
+// out[t][d] += sum_j w[t][j] * y[t][j][d], j in order (the reference's k
+// moe_add calls, each a fused multiply-add).
+__global__ __launch_bounds__(kBlock) void weighted_sum_kernel(float* __restrict__ out, const float* __restrict__ y,
+                                                              const float* __restrict__ w, int rows, int k, int dim) {
+    const int64_t n = static_cast<int64_t>(rows) * dim;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kBlock) {
+        const int64_t t = i / dim, d = i - t * dim;
+        float o = out[i];
+        for (int j = 0; j < k; ++j) o = __builtin_fmaf(w[t * k + j], y[(t * k + j) * dim + d], o);
+        out[i] = o;
+    }
+}
+
+}  // namespace
+}  // namespace qk
+
+using namespace qk;
+
+extern "C" {
+
+int qwen_moe_topk_rows(const float* logits, int32_t* idx, float* weights, int rows, int n, int k, void* stream) {
+    QK_REQUIRE(rows >= 0, "moe_topk: negative rows %d", rows);
+    QK_REQUIRE(n > 0 && n <= kMaxExperts && k > 0 && k <= n && k <= kWave,
+               "moe_topk: need 0 < k <= min(n, 64) and n <= %d (n=%d, k=%d)", kMaxExperts, n, k);
+    if (rows == 0) return ok();
+    QK_REQUIRE(logits && idx && weights, "moe_topk: null pointer");
+    hipStream_t s = as_stream(stream);
+    const unsigned grid = blocks_for(rows, kWaves);
+    const int vpl = (n + kWave - 1) / kWave;
+    if (vpl <= 1)
+        topk_rows_kernel<1><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
+    else if (vpl <= 2)
+        topk_rows_kernel<2><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
+    else if (vpl <= 4)
+        topk_rows_kernel<4><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
+    else if (vpl <= 8)
+        topk_rows_kernel<8><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
+    else
+        topk_rows_kernel<16><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
+    return check_launch("moe_topk");
+}
+
+int qwen_moe_topk(const float* logits, int32_t* idx, float* weights, int n, int k, void* stream) {
+    return qwen_moe_topk_rows(logits, idx, weights, 1, n, k, stream);
+}
+
+int qwen_moe_add(float* out, const float* x, float a, int n, void* stream) {
+    QK_REQUIRE(n >= 0, "moe_add: negative size %d", n);
+    if (n == 0) return ok();
+    QK_REQUIRE(out && x, "moe_add: null pointer");
+    moe_add_kernel<<<std::min<unsigned>(blocks_for(n, kBlock), 4096u), kBlock, 0, as_stream(stream)>>>(out, x, a, n);
+    return check_launch("moe_add");
+}
+
+int qwen_moe_weighted_sum_rows(float* out, const float* expert_out, const float* weights, int rows, int k, int dim,
+                               void* stream) {
+    QK_REQUIRE(rows >= 0 && k >= 0 && dim >= 0, "moe_weighted_sum: negative size");
+    if (rows == 0 || k == 0 || dim == 0) return ok();
+    QK_REQUIRE(out && expert_out && weights, "moe_weighted_sum: null pointer");
+    const int64_t n = static_cast<int64_t>(rows) * dim;
+    weighted_sum_kernel<<<std::min<unsigned>(blocks_for(n, kBlock), 8192u), kBlock, 0, as_stream(stream)>>>(
+        out, expert_out, weights, rows, k, dim);
+    return check_launch("moe_weighted_sum");
+}
+
+}  // extern "C"

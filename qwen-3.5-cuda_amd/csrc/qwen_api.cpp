@@ -161,6 +161,24 @@ void attn_decode(const float* q, const float* k_cache, const float* v_cache, con
                            st(stream)));
 }
 
+void moe_topk(const float* router, int* top_idx, float* top_weight, int experts, int k, hipStream_t stream) {
+    check(qwen_moe_topk(router, top_idx, top_weight, experts, k, st(stream)));
+}
+
+void moe_topk_rows(const float* router, int* top_idx, float* top_weight, int rows, int experts, int k,
+                   hipStream_t stream) {
+    check(qwen_moe_topk_rows(router, top_idx, top_weight, rows, experts, k, st(stream)));
+}
+
+void moe_add(float* accum, const float* expert_out, float weight, int dim, hipStream_t stream) {
+    check(qwen_moe_add(accum, expert_out, weight, dim, st(stream)));
+}
+
+void moe_weighted_sum_rows(float* accum, const float* expert_out, const float* weight, int rows, int k, int dim,
+                           hipStream_t stream) {
+    check(qwen_moe_weighted_sum_rows(accum, expert_out, weight, rows, k, dim, st(stream)));
+}
+
 void moe_silu_mul(const float* gate, const float* up, float* hidden, int dim, hipStream_t stream) {
     check(qwen_moe_silu_mul(gate, up, hidden, dim, st(stream)));
 }
@@ -191,6 +209,18 @@ void matmul_dispatch(const QuantTensor& w, const float* x, float* y, int M, int 
     const int status = qwen_matmul_dispatch(w.device_ptr, static_cast<int>(w.type), w.num_elements, x, y, M, K,
                                             element_offset, st(stream));
     // Reference messages, src/cuda/matmul_q4.cu:187-195.
+    if (status == QWEN_STATUS_INVALID_ARGUMENT && !w.device_ptr)
+        throw std::runtime_error("tensor '" + w.name + "' is not loaded");
+    if (status == QWEN_STATUS_UNSUPPORTED_TYPE)
+        throw std::runtime_error("unsupported GGML type for tensor '" + w.name + "'");
+    if (status == QWEN_STATUS_OUT_OF_RANGE) throw std::runtime_error("GEMV shape exceeds tensor '" + w.name + "'");
+    check(status);
+}
+
+void moe_expert_matmul(const QuantTensor& w, uint64_t expert_stride, int n_experts, const int32_t* idx, int n_sel,
+                       const float* x, int64_t x_stride, float* y, int M, int K, hipStream_t stream) {
+    const int status = qwen_moe_expert_matmul(w.device_ptr, static_cast<int>(w.type), w.num_elements, expert_stride,
+                                              n_experts, idx, n_sel, x, x_stride, y, M, K, st(stream));
     if (status == QWEN_STATUS_INVALID_ARGUMENT && !w.device_ptr)
         throw std::runtime_error("tensor '" + w.name + "' is not loaded");
     if (status == QWEN_STATUS_UNSUPPORTED_TYPE)

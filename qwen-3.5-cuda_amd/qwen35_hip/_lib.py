@@ -66,6 +66,11 @@ SIGNATURES: dict[str, list] = {
     "qwen_attn_kv_store": [_P, _P, _P, _P, _I, _I, _I, _P],
     "qwen_attn_decode_workspace_bytes": [_I, _I, _I, _I],
     "qwen_attn_decode": [_P] * 5 + [_I, _I, _I, _I, _P, ctypes.c_size_t, _P],
+    "qwen_moe_topk": [_P, _P, _P, _I, _I, _P],
+    "qwen_moe_topk_rows": [_P, _P, _P, _I, _I, _I, _P],
+    "qwen_moe_add": [_P, _P, _F, _I, _P],
+    "qwen_moe_weighted_sum_rows": [_P, _P, _P, _I, _I, _I, _P],
+    "qwen_moe_expert_matmul": [_P, _I, _U64, _U64, _I, _P, _I, _P, _I64, _P, _I, _I, _P],
     "qwen_matmul_type_supported": [_I],
     "qwen_matmul_dispatch": [_P, _I, _U64, _P, _P, _I, _I, _U64, _P],
 }

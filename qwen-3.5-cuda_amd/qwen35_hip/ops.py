@@ -351,6 +351,55 @@ def attn_decode(q, k_cache, v_cache, heads, kv_heads, dim, pos, gate=None, works
     return out
 
 
+# ------------------------------------------------------------------ MoE routing
+def moe_topk_rows(logits, k, idx=None, weights=None, stream=None):
+    """logits [rows, n] (or [n]) -> idx int32, weights float32 [rows, k]."""
+    _dev(logits, dtype=torch.float32)
+    n = logits.shape[-1]
+    rows = logits.numel() // n
+    idx = torch.empty((rows, k), dtype=torch.int32, device=logits.device) if idx is None else idx
+    weights = torch.empty((rows, k), dtype=torch.float32, device=logits.device) if weights is None else weights
+    _dev(idx, dtype=torch.int32)
+    _dev(weights, dtype=torch.float32)
+    _same((rows, k), idx, weights)
+    check(load().qwen_moe_topk_rows(_p(logits), _p(idx), _p(weights), rows, n, k, _stream(stream)))
+    return idx, weights
+
+
+def moe_add(out, x, a: float, stream=None):
+    _dev(out, x, dtype=torch.float32)
+    _same(out.shape, x)
+    check(load().qwen_moe_add(_p(out), _p(x), a, out.numel(), _stream(stream)))
+    return out
+
+
+def moe_weighted_sum_rows(out, expert_out, weights, stream=None):
+    """out [rows, dim] += sum_j weights[rows, k] * expert_out[rows, k, dim]."""
+    _dev(out, expert_out, weights, dtype=torch.float32)
+    rows, k, dim = expert_out.shape
+    _same((rows, dim), out)
+    _same((rows, k), weights)
+    check(load().qwen_moe_weighted_sum_rows(_p(out), _p(expert_out), _p(weights), rows, k, dim, _stream(stream)))
+    return out
+
+
+def moe_expert_matmul(weight, ggml_type, num_elements, expert_stride, n_experts, idx, x, x_stride, M, K, out=None,
+                      stream=None):
+    """y[j] = W_{idx[j]} x[j * x_stride : + K] for the n_sel = idx.numel() ids (device int32)."""
+    _dev(weight, dtype=torch.uint8)
+    _dev(idx, dtype=torch.int32)
+    _dev(x, dtype=torch.float32)
+    t = GGML_TYPES[ggml_type] if isinstance(ggml_type, str) else int(ggml_type)
+    n_sel = idx.numel()
+    if n_sel and x.numel() < (n_sel - 1) * x_stride + K:
+        raise ValueError("x too small for n_sel inputs")
+    out = torch.empty((n_sel, M), dtype=torch.float32, device=x.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    check(load().qwen_moe_expert_matmul(_p(weight), t, num_elements, expert_stride, n_experts, _p(idx), n_sel, _p(x),
+                                        x_stride, _p(out), M, K, _stream(stream)))
+    return out
+
+
 # ------------------------------------------------------------------ MoE
 def moe_silu_mul(g, u, out=None, stream=None):
     _dev(g, u, dtype=torch.float32)

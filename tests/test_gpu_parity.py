@@ -548,6 +548,65 @@ def test_attn_decode_rejects_small_workspace():
     assert ops.attn_decode_workspace_bytes(6, 4, 64, 3) == 0  # heads not a multiple of kv_heads
 
 
+# ------------------------------------------------------------------ MoE routing
+@pytest.mark.parametrize("rows,n,k", [(4096, 256, 8), (37, 100, 5), (3, 1024, 64), (5, 64, 1)])
+def test_moe_topk_rows(oracle, rows, n, k):
+    """Qwen3.5 routing (256 experts, top 8) over a token batch, plus ragged / wide /
+    k = 64 / k = 1 shapes; ties (a 3-way tie at the top, an all-equal row) and a
+    non-finite row that only writes idx[0] = -1, w[0] = NaN."""
+    r = rng(rows * n + k)
+    x = r.standard_normal((rows, n)).astype(F32)
+    x[0, [n // 3, n - 1, 1]] = 7.0
+    x[1, :] = 0.5
+    x[2, n // 2] = np.nan if rows > 2 else x[2, n // 2]
+    sent_i = np.full((rows, k), 1234, np.int32)
+    sent_w = np.full((rows, k), 0.125, F32)
+    di, dw = dev(sent_i), dev(sent_w)
+    ops.moe_topk_rows(dev(x), k, idx=di, weights=dw)
+    ri, rw = oracle.moe_topk_rows(x, k, idx=sent_i, w=sent_w)
+    gi, gw = host(di), host(dw)
+    assert np.array_equal(gi, ri), np.argwhere(gi != ri)[:5]
+    assert_f32_close(gw, rw, what="weights")
+
+
+def test_moe_add_and_weighted_sum(oracle):
+    r = rng(8)
+    rows, k, dim = 64, 8, 2048
+    y = r.standard_normal((rows, k, dim)).astype(F32)
+    w = r.uniform(0, 0.3, (rows, k)).astype(F32)
+    out0 = r.standard_normal((rows, dim)).astype(F32)
+    got = host(ops.moe_weighted_sum_rows(dev(out0), dev(y), dev(w)))
+    assert_bits_equal(got, oracle.moe_weighted_sum_rows(out0, y, w), "weighted sum")
+    a = float(np.float32(0.3719))
+    assert_bits_equal(host(ops.moe_add(dev(out0[0]), dev(y[0, 0]), a)), oracle.moe_add(out0[0], y[0, 0], a), "moe_add")
+
+
+@pytest.mark.parametrize("kind,M,K", [("Q4_K", 512, 2048), ("Q4_K", 2048, 512), ("Q6_K", 512, 2048), ("Q8_0", 96, 256)])
+def test_moe_expert_matmul(oracle, kind, M, K):
+    """Gate/up (512 x 2048) and down (2048 x 512, one input row per expert) projections
+    of the selected experts with the ids on the device; an invalid id gives a NaN row."""
+    import ggml_blocks
+
+    t = ops.GGML_TYPES[kind]
+    E = 12
+    r = rng(M + K + t)
+    n_el = E * M * K
+    table = (synth.q4k_table(E * M, K, seed_tensor=3) if kind == "Q4_K" else
+             synth.q6k_table(E * M, K, seed_tensor=3) if kind == "Q6_K" else
+             ggml_blocks.random_blocks(r, t, n_el // ggml_blocks.BLOCK[t][0]))
+    ids = np.array([7, 0, 11, 3, 12, 5, -1, 9], np.int32)
+    xs = r.standard_normal((ids.size, K)).astype(F32)
+    got = host(ops.moe_expert_matmul(dev(table), t, n_el, M * K, E, dev(ids), dev(xs), K, M, K))
+    ref = oracle.moe_expert_gemv(table, t, ids, E, M * K, xs, K, M, K)
+    bad = (ids < 0) | (ids >= E)
+    assert np.isnan(got[bad]).all()
+    assert_f32_close(got[~bad], ref[~bad], group=M, what=kind)
+    # one shared input row for all experts (x_stride 0), as the gate / up projections use
+    got0 = host(ops.moe_expert_matmul(dev(table), t, n_el, M * K, E, dev(ids[:3]), dev(xs[0]), 0, M, K))
+    ref0 = oracle.moe_expert_gemv(table, t, ids[:3], E, M * K, xs[0], 0, M, K)
+    assert_f32_close(got0, ref0, group=M, what=f"{kind} shared x")
+
+
 # ------------------------------------------------------------------ quantized GEMV
 def _gemv_weight(kind: str, rows: int, cols: int, r) -> np.ndarray:
     """GGML bytes of a rows x cols tensor: the C5 table generators for Q4_K/Q6_K

@@ -547,6 +547,55 @@ def test_attn_decode_end_to_end(oracle):
     assert_f32_close(oracle.attn_sigmoid_gate(q, g), q / (1 + np.exp(-g.astype(np.float64))), rtol=1e-6, what="gate")
 
 
+# ------------------------------------------------------------------ MoE routing
+def test_moe_topk_against_sort(oracle):
+    """Top-k = the k largest in descending order, ties to the lower index (a stable
+    sort of -x), then a float64 softmax over the picks."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((50, 256)).astype(F32)
+    x[3, [10, 200, 57]] = 9.0          # a three-way tie at the top
+    x[4, :] = 0.25                     # all equal: indices 0..k-1
+    idx, w = oracle.moe_topk_rows(x, 8)
+    order = np.argsort(-x, axis=1, kind="stable")[:, :8]
+    assert np.array_equal(idx, order)
+    assert list(idx[3, :3]) == [10, 57, 200]
+    assert list(idx[4]) == list(range(8))
+    sel = np.take_along_axis(x, order, axis=1).astype(np.float64)
+    e = np.exp(sel - sel.max(axis=1, keepdims=True))
+    assert_f32_close(w, e / e.sum(axis=1, keepdims=True), rtol=1e-6, what="weights")
+    assert np.allclose(w.sum(axis=1), 1.0, atol=1e-6)
+
+
+def test_moe_topk_non_finite(oracle):
+    x = np.zeros((2, 16), F32)
+    x[1, 5] = np.inf
+    idx, w = oracle.moe_topk_rows(x, 4, idx=np.full((2, 4), 7, np.int32), w=np.full((2, 4), 0.5, F32))
+    assert idx[1, 0] == -1 and np.isnan(w[1, 0])
+    assert list(idx[1, 1:]) == [7, 7, 7] and list(w[1, 1:]) == [0.5] * 3  # untouched, as the reference
+    assert list(idx[0]) == [0, 1, 2, 3]
+
+
+def test_moe_weighted_sum_and_expert_gemv(oracle):
+    rng = np.random.default_rng(12)
+    rows, k, dim = 3, 4, 10
+    y = rng.standard_normal((rows, k, dim)).astype(F32)
+    w = rng.uniform(0, 1, (rows, k)).astype(F32)
+    out0 = rng.standard_normal((rows, dim)).astype(F32)
+    got = oracle.moe_weighted_sum_rows(out0, y, w)
+    ref = out0.astype(np.float64) + np.einsum("tk,tkd->td", w.astype(np.float64), y.astype(np.float64))
+    assert_f32_close(got, ref, group=dim, what="weighted sum")
+    assert_bits_equal(oracle.moe_add(out0[0], y[0, 0], 0.5), out0[0] + np.float32(0.5) * y[0, 0], "moe_add")
+    # expert GEMV = matmul_dispatch at element offset e * stride, per selected expert
+    E, M, K = 5, 8, 512
+    raw = ggml_blocks.random_blocks(rng, 12, E * M * K // 256)
+    xs = rng.standard_normal((3, K)).astype(F32)
+    ids = np.array([4, 0, 9], np.int32)  # 9: no such expert -> NaN row
+    yy = oracle.moe_expert_gemv(raw, 12, ids, E, M * K, xs, K, M, K)
+    for j, e in enumerate(ids[:2]):
+        assert_bits_equal(yy[j], oracle.gemv(raw, 12, xs[j], M, K, element_offset=int(e) * M * K), f"expert {e}")
+    assert np.isnan(yy[2]).all()
+
+
 # ------------------------------------------------------------------ MoE
 def test_silu_scalars(oracle):
     assert oracle.silu(0.0) == 0.0
