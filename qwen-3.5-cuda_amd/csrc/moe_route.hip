@@ -28,17 +28,35 @@ constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
 constexpr int kMaxExperts = 16 * kWave;  // logits per row held in VGPRs (16 per lane)
 
-// Arg-max of (v, i) pairs over the wave: larger value wins, then lower index.
+// Wave max / min with DPP inside 16-lane rows, permlane swaps across rows.
+__device__ __forceinline__ float wave_maxf(float v) {
+    v = fmaxf(v, dpp_move<0xB1>(v));
+    v = fmaxf(v, dpp_move<0x4E>(v));
+    v = fmaxf(v, dpp_move<0x141>(v));
+    v = fmaxf(v, dpp_move<0x140>(v));
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
+__device__ __forceinline__ int wave_mini(int v) {
+    v = min(v, __float_as_int(dpp_move<0xB1>(__int_as_float(v))));
+    v = min(v, __float_as_int(dpp_move<0x4E>(__int_as_float(v))));
+    v = min(v, __float_as_int(dpp_move<0x141>(__int_as_float(v))));
+    v = min(v, __float_as_int(dpp_move<0x140>(__int_as_float(v))));
+    auto p = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+    v = min(static_cast<int>(p[0]), static_cast<int>(p[1]));
+    p = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+    return min(static_cast<int>(p[0]), static_cast<int>(p[1]));
+}
+
+// Arg-max of (v, i) pairs over the wave: larger value wins, then lower index
+// (the max value first, then the smallest index among the lanes holding it).
 __device__ __forceinline__ void wave_argmax(float& v, int& i) {
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const float ov = __shfl_xor(v, off);
-        const int oi = __shfl_xor(i, off);
-        if (ov > v || (ov == v && oi < i)) {
-            v = ov;
-            i = oi;
-        }
-    }
+    const float m = wave_maxf(v);
+    i = wave_mini(v == m ? i : 0x7fffffff);
+    v = m;
 }
 
 template <int VPL>
@@ -104,7 +122,28 @@ __global__ __launch_bounds__(kBlock) void moe_add_kernel(float* __restrict__ out
 }
 
 // out[t][d] += sum_j w[t][j] * y[t][j][d], j in order (the reference's k
-// moe_add calls, each a fused multiply-add).
+// moe_add calls, each a fused multiply-add). Vector form: 4 columns per
+// thread, the k expert rows streamed with 16-byte nontemporal loads.
+__global__ __launch_bounds__(kBlock) void weighted_sum_v4(float* __restrict__ out, const float* __restrict__ y,
+                                                          const float* __restrict__ w, int rows, int k, int dim4) {
+    const int64_t n = static_cast<int64_t>(rows) * dim4;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kBlock) {
+        const int64_t t = i / dim4, d4 = i - t * dim4;
+        float4 o = ld4_nt(out + 4 * i);
+        const float* yt = y + (t * k) * dim4 * 4 + 4 * d4;
+        for (int j = 0; j < k; ++j) {
+            const float4 yy = ld4_nt(yt + static_cast<int64_t>(j) * dim4 * 4);
+            const float a = w[t * k + j];
+            o.x = __builtin_fmaf(a, yy.x, o.x);
+            o.y = __builtin_fmaf(a, yy.y, o.y);
+            o.z = __builtin_fmaf(a, yy.z, o.z);
+            o.w = __builtin_fmaf(a, yy.w, o.w);
+        }
+        st4_nt(out + 4 * i, o);
+    }
+}
+
 __global__ __launch_bounds__(kBlock) void weighted_sum_kernel(float* __restrict__ out, const float* __restrict__ y,
                                                               const float* __restrict__ w, int rows, int k, int dim) {
     const int64_t n = static_cast<int64_t>(rows) * dim;
@@ -164,8 +203,14 @@ int qwen_moe_weighted_sum_rows(float* out, const float* expert_out, const float*
     if (rows == 0 || k == 0 || dim == 0) return ok();
     QK_REQUIRE(out && expert_out && weights, "moe_weighted_sum: null pointer");
     const int64_t n = static_cast<int64_t>(rows) * dim;
-    weighted_sum_kernel<<<std::min<unsigned>(blocks_for(n, kBlock), 8192u), kBlock, 0, as_stream(stream)>>>(
-        out, expert_out, weights, rows, k, dim);
+    if (dim % 4 == 0 && aligned16(out) && aligned16(expert_out)) {
+        const int64_t n4 = n / 4;
+        weighted_sum_v4<<<std::min<unsigned>(blocks_for(n4, kBlock), 16384u), kBlock, 0, as_stream(stream)>>>(
+            out, expert_out, weights, rows, k, dim / 4);
+    } else {
+        weighted_sum_kernel<<<std::min<unsigned>(blocks_for(n, kBlock), 8192u), kBlock, 0, as_stream(stream)>>>(
+            out, expert_out, weights, rows, k, dim);
+    }
     return check_launch("moe_weighted_sum");
 }
 
