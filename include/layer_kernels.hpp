@@ -49,7 +49,7 @@ void moe_shared_add(float* accum, const float* shared_out, const float* sgate, i
 
 // ---- row-batched and fused forms
 
-// Cache store of src/layer_attn.cpp:98-100: k, v [kv_dim] to row pos; throws
+// Cache store of src/layer_attn.cpp:99-100: k, v [kv_dim] to row pos; throws
 // "attention position exceeds configured context" unless 0 <= pos < max_seq_len.
 void attn_kv_store(const float* k, const float* v, float* k_cache, float* v_cache, int pos, int kv_dim,
                    int max_seq_len, hipStream_t stream);

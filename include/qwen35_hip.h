@@ -152,7 +152,7 @@ int qwen_gdn_recurrent_step(float* state, const float* q, const float* k, const 
                             const float* beta, const float* decay, float* out, int key_heads,
                             int value_heads, int key_dim, int value_dim, void* stream);
 /* `rows` consecutive steps in one launch (the reference's per-token loop,
- * src/layer_gdn.cpp:97-103): token t reads q, k, v at t * qkv_stride elements
+ * src/layer_gdn.cpp:100-106): token t reads q, k, v at t * qkv_stride elements
  * (e.g. the q | k | v slices of the GDN front end's output rows), beta and decay
  * at t * value_heads, and writes out at t * out_stride. */
 int qwen_gdn_recurrent_rows(float* state, const float* q, const float* k, const float* v,
@@ -188,7 +188,7 @@ int qwen_attn_sigmoid_gate(const float* x, const float* gate, float* out, int n,
 
 /* k, v [kv_dim] stored to row pos of the caches; pos outside [0, max_seq_len) ->
  * QWEN_STATUS_OUT_OF_RANGE ("attention position exceeds configured context").
- * ref: src/layer_attn.cpp:77-79 (check), :98-100 (cudaMemcpyAsync of k and v) */
+ * ref: src/layer_attn.cpp:76-78 (check), :99-100 (cudaMemcpyAsync of k and v) */
 int qwen_attn_kv_store(const float* k, const float* v, float* k_cache, float* v_cache, int pos,
                        int kv_dim, int max_seq_len, void* stream);
 
@@ -207,7 +207,7 @@ int qwen_attn_decode(const float* q, const float* k_cache, const float* v_cache,
 
 /* ====================================================================== MoE routing
  * The reference picks experts on the device, copies them to the host and syncs
- * (src/layer_moe.cpp:98-124); these entry points keep the routing on the device. */
+ * (src/layer_moe.cpp:98-106); these entry points keep the routing on the device. */
 
 /* Top-k of n router logits, then softmax over the k picks: idx int32 [k] (strictly
  * greater wins, ties to the lower index), weights [k]; a non-finite logit gives
@@ -223,7 +223,7 @@ int qwen_moe_topk_rows(const float* logits, int32_t* idx, float* weights, int ro
 int qwen_moe_add(float* out, const float* x, float a, int n, void* stream);
 
 /* out[t] += sum_j weights[t][j] * expert_out[t][j] for j < k (weights on the device):
- * the layer's k moe_add calls per token, src/layer_moe.cpp:127-140.
+ * the layer's k moe_add calls per token, src/layer_moe.cpp:127-142.
  * out [rows x dim], expert_out [rows x k x dim], weights [rows x k]. */
 int qwen_moe_weighted_sum_rows(float* out, const float* expert_out, const float* weights, int rows,
                                int k, int dim, void* stream);
@@ -232,7 +232,7 @@ int qwen_moe_weighted_sum_rows(float* out, const float* expert_out, const float*
  * y[j] = W_e x_j, e = idx[j], W_e = the M x K rows at element offset e * expert_stride
  * of a GGML tensor of n_experts experts; x_j = x + j * x_stride; y [n_sel x M]. An id
  * outside [0, n_experts) gives a NaN row. Statuses as qwen_matmul_dispatch.
- * ref: src/layer_moe.cpp:129-138 (matmul_dispatch at element offset e * stride) */
+ * ref: src/layer_moe.cpp:131-138 (matmul_dispatch at element offset e * stride) */
 int qwen_moe_expert_matmul(const void* weight, int type, uint64_t num_elements, uint64_t expert_stride,
                            int n_experts, const int32_t* idx, int n_sel, const float* x,
                            int64_t x_stride, float* y, int M, int K, void* stream);

@@ -462,7 +462,7 @@ void or_gdn_recurrent_step(float* state, const float* q, const float* k, const f
 }
 
 // T consecutive recurrent steps (the reference calls gdn_recurrent_step once
-// per token, src/layer_gdn.cpp:100-103): token t reads q, k, v at
+// per token, src/layer_gdn.cpp:100-106): token t reads q, k, v at
 // t * qkv_stride, beta / decay at t * value_heads, writes out at t * out_stride.
 void or_gdn_recurrent_rows(float* state, const float* q, const float* k, const float* v, const float* beta,
                            const float* decay, float* out, int rows, int key_heads, int value_heads, int key_dim,
@@ -535,7 +535,7 @@ void or_attn_sigmoid_gate(const float* x, const float* g, float* out, int64_t n)
     for (int64_t i = 0; i < n; ++i) out[i] = x[i] / (1.0f + exp_f(-g[i]));
 }
 
-// The decode sequence of src/layer_attn.cpp:98-108 after the cache store:
+// The decode sequence of src/layer_attn.cpp:103-108 after the cache store:
 // scores, softmax over pos + 1 keys, values, then the sigmoid gate when gate
 // is non-null. scratch holds heads * (pos + 1) floats.
 void or_attn_decode(const float* q, const float* k_cache, const float* v_cache, const float* gate, float* out,
@@ -595,7 +595,7 @@ void or_moe_add(float* out, const float* x, float a, int64_t n) {
 }
 
 // out[t] += sum_j w[t][j] * y[t][j]: the layer's k moe_add calls per token
-// (src/layer_moe.cpp:127-140) with the weights read from device memory.
+// (src/layer_moe.cpp:127-142) with the weights read from device memory.
 void or_moe_weighted_sum_rows(float* out, const float* y, const float* w, int rows, int k, int dim) {
     for (int64_t t = 0; t < rows; ++t)
         for (int j = 0; j < k; ++j) or_moe_add(out + t * dim, y + (t * k + j) * dim, w[t * k + j], dim);

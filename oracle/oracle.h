@@ -86,7 +86,7 @@ void or_gdn_recurrent_step(float* state, const float* q, const float* k, const f
 void or_gdn_recurrent_rows(float* state, const float* q, const float* k, const float* v,
                            const float* beta, const float* decay, float* out, int rows,
                            int key_heads, int value_heads, int key_dim, int value_dim,
-                           int64_t qkv_stride, int64_t out_stride);  /* layer_gdn.cpp:100-103 */
+                           int64_t qkv_stride, int64_t out_stride);  /* layer_gdn.cpp:100-106 */
 
 /* ---- attention core (decode) ---- */
 void or_attn_split_qg(const float* in, float* q, float* g, int heads, int dim);  /* attn_kernels.cu:16-31 */
@@ -98,14 +98,14 @@ void or_attn_values(const float* scores, const float* v_cache, float* out, int h
 void or_attn_sigmoid_gate(const float* x, const float* g, float* out, int64_t n); /* :185-195 */
 void or_attn_decode(const float* q, const float* k_cache, const float* v_cache, const float* gate,
                     float* out, float* scratch, int heads, int kv_heads, int dim,
-                    int pos);                                           /* layer_attn.cpp:98-108 */
+                    int pos);                                           /* layer_attn.cpp:99-108 */
 
 /* ---- MoE routing ---- */
 void or_moe_topk(const float* x, int32_t* idx, float* w, int n, int k);   /* moe.cu:7-51 */
 void or_moe_topk_rows(const float* x, int32_t* idx, float* w, int rows, int n, int k);
 void or_moe_add(float* out, const float* x, float a, int64_t n);          /* moe.cu:76-86 */
 void or_moe_weighted_sum_rows(float* out, const float* y, const float* w, int rows, int k,
-                              int dim);                                  /* layer_moe.cpp:127-140 */
+                              int dim);                                  /* layer_moe.cpp:127-142 */
 void or_moe_expert_gemv(const uint8_t* w, int type, const int32_t* idx, int n_sel, int n_experts,
                         uint64_t expert_stride, const float* x, int64_t x_stride, float* y, int M,
                         int K);                                          /* layer_moe.cpp:131-138 */

@@ -8,7 +8,7 @@
 //   softmax_kernel :99-158     s = expf(s - max) / sum, per head row
 //   value_kernel :162-181      out[h][j] = sum_t s[h][t] * v[t][kv][j]
 //   sigmoid_mul_kernel :185-195 out = x / (1 + expf(-g))
-// plus the cache store of layer_attn.cpp:98-100 (k, v copied to row pos).
+// plus the cache store of layer_attn.cpp:99-100 (k, v copied to row pos).
 // The reference runs these as separate launches (scores with 32-thread
 // blocks per (head, key), values with one block per head).
 //

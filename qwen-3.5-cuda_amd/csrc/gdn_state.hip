@@ -10,7 +10,7 @@
 //       delta = (v[j] - mem) * beta[h]
 //       S[i][j] += k[i] * delta
 //       out[j] = sum_i q[i] * S[i][j]
-// called once per token per GDN layer (src/layer_gdn.cpp:97-103). The
+// called once per token per GDN layer (src/layer_gdn.cpp:100-106). The
 // reference walks the state three times per token (one thread per column, a
 // block per head, 32 blocks).
 //

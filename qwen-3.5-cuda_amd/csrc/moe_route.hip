@@ -6,7 +6,7 @@
 //                       unused logit, strictly greater wins" (ties to the lower
 //                       index), then w = softmax over the k picks
 //   add_kernel :76-86   out += a * x
-// The layer (src/layer_moe.cpp:98-140) copies idx / w to the host, waits on
+// The layer (src/layer_moe.cpp:98-142) copies idx / w to the host, waits on
 // the stream, and launches k expert GEMV chains with host-side offsets and k
 // moe_add calls with host-side weights.
 //
