@@ -34,6 +34,18 @@ NAMES = [
     ("qk_norm_rope_v4", "qk_norm_rope"),
     ("rmsnorm_rows_v4", "rmsnorm"),
     ("copy16", "copy"),
+    # next rows (kernel symbols; several bench shapes can share one instantiation)
+    ("gemv_kquant<14, 4>", "gemv Q6_K, 4 units/wave (LM head)"),
+    ("gemv_kquant<12, 2>", "gemv Q4_K, 2 units/wave (GDN qkv)"),
+    ("gemv_kquant<12, 1>", "gemv Q4_K, 1 unit/wave (out proj, experts)"),
+    ("gdn_recurrent_v4", "gdn_recurrent (step and 4096-token form)"),
+    ("decode_split", "attn_decode split-K pass"),
+    ("decode_combine", "attn_decode combine"),
+    ("scores_kernel", "attn_scores (staged)"),
+    ("softmax_kernel", "attn_softmax (staged)"),
+    ("values_kernel", "attn_values (staged)"),
+    ("topk_rows_kernel", "moe_topk_rows"),
+    ("weighted_sum_v4", "moe_weighted_sum_rows"),
 ]
 
 # algorithmic bytes per call at the BASELINE configs (bench.py computes the same)
@@ -115,10 +127,11 @@ def main(argv=None) -> int:
     args = ap.parse_args(argv)
     if args.cmd == "stats":
         t = stats(args.csv)
-        print(f"{'kernel':30s} {'calls':>6s} {'avg us':>9s} {'min us':>9s} {'max us':>9s} {'GB/s (avg)':>11s}")
+        print(f"{'kernel':44s} {'calls':>6s} {'avg us':>9s} {'min us':>9s} {'max us':>9s} {'GB/s (avg)':>11s}")
         for name, r in sorted(t.items(), key=lambda kv: -kv[1]["avg_us"]):
             gbps = ALGORITHMIC.get(name, 0) / r["avg_us"] / 1e3 if name in ALGORITHMIC else float("nan")
-            print(f"{name:30s} {r['calls']:6d} {r['avg_us']:9.2f} {r['min_us']:9.2f} {r['max_us']:9.2f} {gbps:11.1f}")
+            print(f"{name[:44]:44s} {r['calls']:6d} {r['avg_us']:9.2f} {r['min_us']:9.2f} {r['max_us']:9.2f} "
+                  f"{gbps:11.1f}")
         return 0
     t = traffic(args.fetch_csv, args.write_csv, args.copy_bytes)
     cal = t["_calibration"]
