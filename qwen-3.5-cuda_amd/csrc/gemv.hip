@@ -9,7 +9,12 @@
 // weight element independently (header and 6-bit scales re-read per element).
 //
 // The op is bound by the weight bytes read from HBM (x is 8-16 KB and stays in
-// L2). Fast path (Q4_K, Q6_K): the weight is walked in units of 8 consecutive
+// L2). Two Q4_K / Q6_K kernels:
+//  * large matrices (the LM head): gemv_mfma below -- int8 MFMA on the raw
+//    quants against x in exact integer digits, LDS-staged tiles of 16 rows;
+//  * everything else: gemv_kquant, whose shorter per-wave latency wins at the
+//    per-layer sizes (<= 8192 rows in the model).
+// Per-row path (Q4_K, Q6_K): the weight is walked in units of 8 consecutive
 // 256-element blocks (2048 elements = 1152 B of Q4_K or 1680 B of Q6_K, both
 // multiples of 16 bytes). A row of K = 256*nb elements is nb/8 units when
 // 8 | nb; when nb | 8, 8/nb consecutive rows share one unit. A wave owns R
@@ -310,6 +315,432 @@ __global__ __launch_bounds__(kBlock) void gemv_any(const uint8_t* __restrict__ w
     if (lane == 0) y[row] = s;
 }
 
+// ------------------------------------------------------------------ MFMA path
+// Q4_K / Q6_K, K = 256*nb with nb = S*BPW (S in {1, 2, 4} k-slices of BPW in
+// 1..4 blocks, so K <= 4096): the dot products run on the matrix cores
+// (v_mfma_i32_16x16x64_i8, exact int8 x int8 -> int32).
+//
+// x is written in integer digits. Over a wave's k-slice, with
+// F = 26 - exponent(max |x|), X = rint(x * 2^F) is an integer of at most 27
+// bits, split into four signed base-128 digits
+//   X = D0*2^21 + D1*2^14 + D2*2^7 + D3,  D1..D3 in [-64, 63], |D0| <= 33.
+// The quants are small non-negative integers (Q4_K 0..15, Q6_K 0..63), so a
+// tile of 16 weight rows x 64 elements (a chunk) is an int8 B operand taken
+// straight from the nibbles, and the A operand holds the digits: A row 4g + i
+// is digit i of elements 16g .. 16g+15 of the chunk and zero elsewhere, so
+// C[4g+i][n] is the exact integer sum over the 16-element group g of row n,
+// digit i. In the 16x16 result layout lane L holds rows 4(L/16)..4(L/16)+3 of
+// column L%16: one (weight row n = L%16, group g = L/16) with its four digit
+// sums, and that is also the lane that reads row n's quants of group g for B
+// (the A and B layouts place element k of the chunk at the same (lane group,
+// byte) position, so the product pairs them whatever order the hardware sums
+// in). Per lane and chunk:
+//   P = sum_i (digit-i sum) * 2^(21-7i)   (the exact integer sum of q*X, one rounding)
+//   Q6_K: acc += (d*sc) * (P*2^-F - 32 * sum(X)*2^-F)            (q - 32)
+//   Q4_K: acc += (d*sc) * (P*2^-F) - (dmin*m) * sum(X)*2^-F
+// with the group sums of X computed once per wave. The only roundings are
+// x -> X (|dX| <= 2^-F / 2, at most 2^-26 of the slice's largest |x|), the
+// int32 -> fp32 steps and the fp32 sums, so the result matches the
+// reference's fp32 dot product to ~1e-7 of the row's sum of |w*x|. A
+// non-finite x switches the launch to the per-element form (the reference's
+// products).
+//
+// Work: a workgroup of 4 waves owns 4/S tile slots x S k-slices; wave
+// (slot, r) runs tiles_per_slot tiles of 16 rows over blocks
+// [r*BPW, (r+1)*BPW). It converts its slice of x once (digits in VGPRs as
+// the A operands of all its tiles). Each tile's quantized rows are copied to
+// the wave's LDS slot with coalesced 16-byte loads (a block of a row is 14 x
+// 16 B for Q6_K -- the last piece overlapping, since 210 B blocks are only
+// 2-byte aligned -- or 9 x 16 B for Q4_K; LDS rows padded by 16 B so the
+// per-lane reads of 16 rows hit distinct banks); the next tile's loads are in
+// flight while the current one is computed. The S partial sums of a row are
+// added in k-slice order through LDS at the end (deterministic).
+constexpr int kMfmaWaves = 4;
+constexpr int kMfmaBlock = kMfmaWaves * kWave;
+
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4i_t mfma_i8(v4i_t a, v4i_t b) {
+    const v4i_t z = {0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, z, 0, 0, 0);
+}
+
+// 16 bytes of global memory at a 2-byte aligned address (gfx950 global loads
+// take any byte alignment).
+__device__ __forceinline__ uint4 ldg16_a2(const uint8_t* p) {
+    uint4 v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 16);
+    return v;
+}
+
+// Signed bit field (the builtin's result type is unsigned).
+__device__ __forceinline__ int sbfe(uint32_t v, uint32_t off, uint32_t width) {
+    return static_cast<int>(__builtin_amdgcn_sbfe(v, off, width));
+}
+
+// (a & 0x0f0f0f0f) | (b & 0xf0f0f0f0): low nibbles from a, high from b.
+__device__ __forceinline__ uint32_t nibble_merge(uint32_t a, uint32_t b) {
+    return (a & 0x0f0f0f0fu) | (b & 0xf0f0f0f0u);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_move<0xB1>(v));
+    v = fmaxf(v, dpp_move<0x4E>(v));
+    v = fmaxf(v, dpp_move<0x141>(v));
+    v = fmaxf(v, dpp_move<0x140>(v));
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
+// Sum over the four lanes L, L^16, L^32, L^48 (the four groups of a row).
+__device__ __forceinline__ float sum_groups(float v) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+// Per-lane constants of the B decode.
+struct Lane {
+    int g;            // group: elements 16g .. 16g+15 of each 64-element chunk
+    uint32_t hmask;   // Q6_K: the two 2-bit fields of qh this lane's group uses
+    int hl, hr;       // Q6_K: shifts that put them at bits 4, 5 (even / odd chunk)
+    int ns;           // Q4_K: nibble shift
+};
+
+template <int TYPE>
+struct MfmaType;
+
+// Q6_K element i: ql byte 64(i/128) + 32((i%128)/32 & 1) + i%32 (low nibble in
+// quarters 0, 1, high in 2, 3), qh byte 128 + 32(i/128) + i%32 bits
+// 2*quarter, scale byte 192 + 8(i/128) + (i%32)/16 + 2*quarter, d at 208
+// (src/cuda/matmul_q4.cu:105-126). For i = 64cb + 16g + p (chunk cb of the
+// block) that is ql byte 64(cb/2) + 16g + p, qh byte 128 + 32(cb/2) +
+// 16(g%2) + p, quarter 2(cb%2) + g/2, scale byte 192 + 4cb + g. In LDS a block
+// is 224 bytes: its bytes 0..207, then bytes 194..209 at 208 (d at 222).
+template <>
+struct MfmaType<kQ6_K> {
+    static constexpr int kBytes = 210;
+    static constexpr int kPieces = 14;   // 16-byte pieces per block
+    static constexpr int kLast = 194;    // offset of the last (overlapping) piece
+    static constexpr float kXs = -32.0f; // q - 32
+
+    // Quants of chunks 2h (low nibbles, qh bits 2(g/2)) and 2h+1 (high nibbles,
+    // qh bits 4 + 2(g/2)) as int8 operands: the two qh fields are masked once
+    // (bits 6, 7 of each byte end up zero) and moved to bits 4, 5.
+    __device__ __forceinline__ static void quants(uint32_t l, uint32_t h, const Lane& ln, int& even, int& odd) {
+        const uint32_t hm = h & ln.hmask;
+        even = static_cast<int>(nibble_merge(l, hm << ln.hl));
+        odd = static_cast<int>(nibble_merge(l >> 4, hm >> ln.hr));
+    }
+
+    // One block (LDS bytes at blk) against the digits a[4] of its 4 chunks.
+    __device__ __forceinline__ static float block(const uint8_t* blk, const v4i_t* a, const float* xs, float scale,
+                                                  const Lane& ln, float acc) {
+        const uint4 sc = *reinterpret_cast<const uint4*>(blk + 192);
+        const float dh = half_bits(*reinterpret_cast<const uint16_t*>(blk + 222));
+        const uint32_t sw[4] = {sc.x, sc.y, sc.z, sc.w};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {   // chunks 2h, 2h+1 share their ql and qh bytes
+            const uint4 ql = *reinterpret_cast<const uint4*>(blk + 64 * h + 16 * ln.g);
+            const uint4 qh = *reinterpret_cast<const uint4*>(blk + 128 + 32 * h + 16 * (ln.g & 1));
+            const uint32_t L[4] = {ql.x, ql.y, ql.z, ql.w}, H[4] = {qh.x, qh.y, qh.z, qh.w};
+            int q[2][4];   // [chunk][dword]
+#pragma unroll
+            for (int j = 0; j < 4; ++j) quants(L[j], H[j], ln, q[0][j], q[1][j]);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int cb = 2 * h + e;
+                const v4i_t c = mfma_i8(a[cb], v4i_t{q[e][0], q[e][1], q[e][2], q[e][3]});
+                const int t = (c.x * 128 + c.y) * 128 + c.z;   // exact: |t| < 2^30
+                const float P = fmaf(static_cast<float>(t), 128.0f, static_cast<float>(c.w));
+                const float dsc = dh * static_cast<float>(sbfe(sw[cb], 8 * ln.g, 8));
+                acc = fmaf(dsc, fmaf(P, scale, xs[cb]), acc);
+            }
+        }
+        return acc;
+    }
+};
+
+// Q4_K element i: qs byte 16 + 32(i/64) + i%32, low nibble if i%64 < 32,
+// sub-block i/32 with scale_min_k4 (src/cuda/matmul_q4.cu:18-26,76-96); for
+// i = 64cb + 16g + p that is qs byte 16 + 32cb + 16(g%2) + p, nibble g/2,
+// sub-block 2cb + g/2. In LDS a block is its 144 bytes.
+template <>
+struct MfmaType<kQ4_K> {
+    static constexpr int kBytes = 144;
+    static constexpr int kPieces = 9;
+    static constexpr int kLast = 128;
+    static constexpr float kXs = 1.0f;
+
+    __device__ __forceinline__ static float block(const uint8_t* blk, const v4i_t* a, const float* xs, float scale,
+                                                  const Lane& ln, float acc) {
+        const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
+        uint4 qs[4];
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) qs[cb] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * cb + 16 * (ln.g & 1));
+        const float dh = half_bits(hdr.x & 0xffffu), dm = half_bits(hdr.x >> 16);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            const uint4 Q = qs[cb];
+            const v4i_t b = {static_cast<int>((Q.x >> ln.ns) & 0x0f0f0f0fu), static_cast<int>((Q.y >> ln.ns) & 0x0f0f0f0fu),
+                             static_cast<int>((Q.z >> ln.ns) & 0x0f0f0f0fu), static_cast<int>((Q.w >> ln.ns) & 0x0f0f0f0fu)};
+            const v4i_t c = mfma_i8(a[cb], b);
+            const int t = (c.x * 128 + c.y) * 128 + c.z;
+            const float P = fmaf(static_cast<float>(t), 128.0f, static_cast<float>(c.w));
+            // byte j%4 (j = 2cb + g/2) of scale words 0..2 (hdr.y, hdr.z, hdr.w) sits at bit bt.
+            const uint32_t bt = 16 * (cb & 1) + 8 * (ln.g >> 1);
+            uint32_t sc, mn;
+            if (cb < 2) {
+                sc = __builtin_amdgcn_ubfe(hdr.y, bt, 6);
+                mn = __builtin_amdgcn_ubfe(hdr.z, bt, 6);
+            } else {
+                sc = __builtin_amdgcn_ubfe(hdr.w, bt, 4) | (__builtin_amdgcn_ubfe(hdr.y, bt + 6, 2) << 4);
+                mn = __builtin_amdgcn_ubfe(hdr.w, bt + 4, 4) | (__builtin_amdgcn_ubfe(hdr.z, bt + 6, 2) << 4);
+            }
+            acc = fmaf(dh * static_cast<float>(sc), P * scale, acc);
+            acc = fmaf(-(dm * static_cast<float>(mn)), xs[cb], acc);
+        }
+        return acc;
+    }
+};
+
+// LDS layout of a wave's slot: 16 rows of BPW blocks of kPieces x 16 bytes,
+// each row padded to an odd number of 16-byte units (16 rows at that stride
+// start on distinct banks).
+template <int TYPE, int BPW>
+struct MfmaSlot {
+    using T = MfmaType<TYPE>;
+    static constexpr int kBlockLds = 16 * T::kPieces;
+    static constexpr int kRowLds = BPW * kBlockLds + ((BPW * T::kPieces) % 2 ? 32 : 16);   // odd x 16 B
+    static constexpr int kBytes = 16 * kRowLds;
+    static constexpr int kLoads = 16 * BPW * T::kPieces;              // 16-byte pieces per tile
+    static constexpr int kPerLane = (kLoads + kWave - 1) / kWave;
+};
+
+// Occupancy: 4 waves per SIMD (<= 128 VGPRs) for slices of up to 2 blocks.
+template <int TYPE, int BPW>
+__global__ __launch_bounds__(kMfmaBlock) __attribute__((amdgpu_waves_per_eu(BPW <= 2 ? 4 : 2))) void gemv_mfma(
+    const uint8_t* __restrict__ w, int type, const float* __restrict__ x, float* __restrict__ y, int M, int nb,
+    uint64_t ub0, int tiles, int S, int maxcnt) {
+    using T = MfmaType<TYPE>;
+    using Slot = MfmaSlot<TYPE, BPW>;
+    constexpr int NC = 4 * BPW;   // chunks per k-slice
+    extern __shared__ uint4 mfma_lds[];
+    const int lane = threadIdx.x & 63;
+    const int wv = wave_in_block();
+    uint8_t* slot = reinterpret_cast<uint8_t*>(mfma_lds) + wv * Slot::kBytes;
+    float* part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(mfma_lds) + kMfmaWaves * Slot::kBytes);
+    const int g = lane >> 4, n = lane & 15;
+    const int slots = kMfmaWaves / S;
+    const int r = wv % S, sl = wv / S;
+    // Slot u of U runs tiles u, u + U, u + 2U, ... (at most maxcnt): at any
+    // time the whole grid streams through one region of the matrix, which
+    // keeps DRAM pages open (contiguous ranges per slot measured 8% slower).
+    const int U = gridDim.x * slots, t0 = blockIdx.x * slots + sl;
+    const int cnt = t0 < tiles ? (tiles - 1 - t0) / U + 1 : 0;
+    const uint64_t row_bytes = static_cast<uint64_t>(nb) * T::kBytes;
+
+    // This lane's 16-byte pieces of a tile: piece q = lane + 64i is (row,
+    // block, piece j) of the tile, packed as row | j << 4 | block << 8.
+    uint32_t pc[Slot::kPerLane];
+#pragma unroll
+    for (int i = 0; i < Slot::kPerLane; ++i) {
+        const int q = min(lane + kWave * i, Slot::kLoads - 1);
+        const int row = q / (BPW * T::kPieces), rem = q % (BPW * T::kPieces);
+        pc[i] = static_cast<uint32_t>(row | (rem % T::kPieces) << 4 | (rem / T::kPieces) << 8);
+    }
+    const uint8_t* wslice = w + ub0 * T::kBytes + static_cast<uint64_t>(r * BPW) * T::kBytes;
+    auto load_tile = [&](uint4 (&v)[Slot::kPerLane], int t) {
+#pragma unroll
+        for (int i = 0; i < Slot::kPerLane; ++i) {
+            const int row = min(t * 16 + static_cast<int>(pc[i] & 15), M - 1);
+            const uint32_t off = (pc[i] >> 8) * T::kBytes + min(16 * ((pc[i] >> 4) & 15), static_cast<uint32_t>(T::kLast));
+            v[i] = ldg16_a2(wslice + static_cast<uint64_t>(row) * row_bytes + off);
+        }
+    };
+    auto store_tile = [&](const uint4 (&v)[Slot::kPerLane]) {
+#pragma unroll
+        for (int i = 0; i < Slot::kPerLane; ++i)
+            if (i < Slot::kPerLane - 1 || lane + kWave * i < Slot::kLoads)
+                *reinterpret_cast<uint4*>(slot + (pc[i] & 15) * Slot::kRowLds + (pc[i] >> 8) * Slot::kBlockLds +
+                                          16 * ((pc[i] >> 4) & 15)) = v[i];
+    };
+
+    // The first tile's loads go out before x is converted.
+    uint4 pre[Slot::kPerLane];
+    if (cnt > 0) load_tile(pre, t0);
+
+    // x of this k-slice: element 256*r*BPW + 64c + lane of chunk c < NC.
+    const float* xs_base = x + 256 * r * BPW;
+    float xv[NC];
+    bool fin = true;
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        xv[c] = xs_base[64 * c + lane];
+        fin = fin && __builtin_isfinite(xv[c]);
+        amax = fmaxf(amax, fabsf(xv[c]));
+    }
+    const bool nonfinite = __builtin_amdgcn_ballot_w64(!fin) != 0;   // wave-uniform
+    amax = wave_max(nonfinite ? 0.0f : amax);
+    // amax < 2^e, so |x| * 2^F < 2^26. Slices with amax outside [2^-100, 2^100]
+    // take the per-element form too: there 2^-F would leave the normal range
+    // or P * 2^-F could overflow before the block scale shrinks it.
+    const int e = __builtin_amdgcn_frexp_expf(amax);
+    const bool bad = nonfinite || (amax > 0.0f && (e < -100 || e > 100));
+    const int F = amax > 0.0f && !bad ? 26 - e : 0;
+    const float scale = __builtin_amdgcn_ldexpf(1.0f, -F);
+    // Digits through the slot (before any tile is stored there): chunk c as
+    // [g][digit][p], 256 bytes; then lane (n, g) reads digit n%4 of group g.
+    float xs[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int X = bad ? 0 : static_cast<int>(rintf(__builtin_amdgcn_ldexpf(xv[c], F)));
+        const int d3 = sbfe(static_cast<uint32_t>(X), 0, 7);
+        const int X1 = (X - d3) >> 7;
+        const int d2 = sbfe(static_cast<uint32_t>(X1), 0, 7);
+        const int X2 = (X1 - d2) >> 7;
+        const int d1 = sbfe(static_cast<uint32_t>(X2), 0, 7);
+        const int d0 = (X2 - d1) >> 7;
+        uint8_t* dst = slot + c * 256 + g * 64 + n;   // n = element index within group g
+        dst[0] = static_cast<uint8_t>(d0);
+        dst[16] = static_cast<uint8_t>(d1);
+        dst[32] = static_cast<uint8_t>(d2);
+        dst[48] = static_cast<uint8_t>(d3);
+        // sum of X over group g, the same in all 16 lanes of the group
+        xs[c] = T::kXs * (group_sum<16>(static_cast<float>(X)) * scale);
+    }
+    const bool valid = (n >> 2) == g;
+    v4i_t a[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const v4i_t v = *reinterpret_cast<const v4i_t*>(slot + c * 256 + g * 64 + (n & 3) * 16);
+        a[c] = valid ? v : v4i_t{0, 0, 0, 0};
+    }
+
+    const bool any_bad = __syncthreads_or(bad);
+    if (any_bad) {
+        // A non-finite x: the per-element form, the reference's fp32 products,
+        // full K per row by the k-slice 0 wave of each slot.
+        if (r == 0)
+            for (int i = 0; i < cnt; ++i)
+                for (int row = (t0 + i * U) * 16; row < (t0 + i * U) * 16 + 16 && row < M; ++row) {
+                    const uint64_t base = (ub0 + static_cast<uint64_t>(row) * nb) * 256;
+                    float s = 0.f;
+                    for (int k = lane; k < 256 * nb; k += kWave)
+                        s = __builtin_fmaf(dequant_elem(w, type, base + k), x[k], s);
+                    s = group_sum<64>(s);
+                    if (lane == 0) y[row] = s;
+                }
+        return;
+    }
+
+    Lane ln;
+    ln.g = g;
+    const int s2 = 2 * (g >> 1);
+    ln.hmask = 0x33333333u << s2;
+    ln.hl = 4 - s2;
+    ln.hr = s2;
+    ln.ns = 4 * (g >> 1);
+
+    for (int i = 0; i < cnt; ++i) {
+        store_tile(pre);
+        if (i + 1 < cnt) load_tile(pre, t0 + (i + 1) * U);
+        float acc = 0.f;
+#pragma unroll
+        for (int bl = 0; bl < BPW; ++bl)
+            acc = T::block(slot + n * Slot::kRowLds + bl * Slot::kBlockLds, a + 4 * bl, xs + 4 * bl, scale, ln, acc);
+        acc = sum_groups(acc);
+        if (S == 1) {
+            if (lane < 16 && (t0 + i * U) * 16 + lane < M) y[(t0 + i * U) * 16 + lane] = acc;
+        } else if (lane < 16) {
+            part[(wv * maxcnt + i) * 16 + lane] = acc;
+        }
+    }
+    if (S > 1) {
+        __syncthreads();
+        if (r == 0)
+            for (int i = 0; i < cnt; ++i) {
+                if (lane < 16 && (t0 + i * U) * 16 + lane < M) {
+                    float s = part[(wv * maxcnt + i) * 16 + lane];
+                    for (int k = 1; k < S; ++k) s += part[((wv + k) * maxcnt + i) * 16 + lane];
+                    y[(t0 + i * U) * 16 + lane] = s;
+                }
+            }
+    }
+}
+
+// Shapes the MFMA path takes: nb = S * BPW, S in {4, 2, 1}, BPW in 1..4.
+inline bool mfma_split(int nb, int& S, int& bpw) {
+    for (int s : {4, 2, 1})
+        if (nb % s == 0 && nb / s >= 1 && nb / s <= 4) {
+            S = s;
+            bpw = nb / s;
+            return true;
+        }
+    return false;
+}
+
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    return cus[dev];
+}
+
+constexpr int kMfmaMaxCnt = 32;   // tiles per slot in the LDS partial-sum buffer
+
+template <int TYPE, int BPW>
+void launch_mfma_bpw(const uint8_t* w, int type, const float* x, float* y, int M, int nb, uint64_t ub0, int S,
+                     hipStream_t s) {
+    using Slot = MfmaSlot<TYPE, BPW>;
+    const int tiles = (M + 15) / 16;
+    const int slots = kMfmaWaves / S;
+    const size_t lds_max = static_cast<size_t>(kMfmaWaves) * (Slot::kBytes + kMfmaMaxCnt * 64);
+    static const int occ = [&] {
+        int n = 0;
+        return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_mfma<TYPE, BPW>, kMfmaBlock, lds_max) ==
+                               hipSuccess && n > 0 ? n : 1;
+    }();
+    // A persistent grid of the workgroups that fit at once (x converted once
+    // per workgroup), or more when a slot would need over kMfmaMaxCnt tiles.
+    const int64_t resident = static_cast<int64_t>(occ) * device_cus();
+    const int64_t gx = std::min<int64_t>(blocks_for(tiles, slots),
+                                         std::max<int64_t>(resident, blocks_for(tiles, slots * kMfmaMaxCnt)));
+    const int maxcnt = static_cast<int>(blocks_for(tiles, gx * slots));
+    const size_t lds = static_cast<size_t>(kMfmaWaves) * (Slot::kBytes + maxcnt * 64);
+    gemv_mfma<TYPE, BPW><<<static_cast<unsigned>(gx), kMfmaBlock, lds, s>>>(w, type, x, y, M, nb, ub0, tiles, S, maxcnt);
+}
+
+template <int TYPE>
+void launch_mfma(const uint8_t* w, int type, const float* x, float* y, int M, int nb, uint64_t ub0, int S, int bpw,
+                 hipStream_t s) {
+    switch (bpw) {
+        case 1: launch_mfma_bpw<TYPE, 1>(w, type, x, y, M, nb, ub0, S, s); break;
+        case 2: launch_mfma_bpw<TYPE, 2>(w, type, x, y, M, nb, ub0, S, s); break;
+        case 3: launch_mfma_bpw<TYPE, 3>(w, type, x, y, M, nb, ub0, S, s); break;
+        default: launch_mfma_bpw<TYPE, 4>(w, type, x, y, M, nb, ub0, S, s); break;
+    }
+}
+
+// The MFMA path pays a fixed latency per workgroup (converting x, the k-slice
+// reduction), so it takes over from the per-row kernel only on large
+// matrices: measured crossovers at K = 2048 are ~16K rows for Q6_K and
+// between 32K and 248K rows for Q4_K (whose per-row kernel spends fewer VALU
+// operations per byte).
+inline bool mfma_large(int type, int M) {
+    const int tiles = (M + 15) / 16;
+    return type == kQ6_K ? tiles >= 1024 : tiles >= 4096;
+}
+
 template <int TYPE, int R>
 void launch_kquant(const uint8_t* w, const float* x, float* y, int M, int nb, uint64_t ub0, int groups,
                    uint64_t tensor_bytes, const Experts& ex, int n_sel, hipStream_t s) {
@@ -346,7 +777,15 @@ int launch_gemv(const uint8_t* w, int type, uint64_t num_elements, const float* 
     // Units start 16-byte aligned: always for 144-byte blocks, every 8 blocks for 210.
     const bool aligned = aligned16(w) && aligned16(x) && (!ex.idx || ex.x_stride % 4 == 0) &&
                          (type == kQ4_K || ((element_offset / 256) % 8 == 0 && (!ex.idx || (ex.stride / 256) % 8 == 0)));
-    if (kquant && shape_ok && aligned) {
+    int S = 0, bpw = 0;
+    const bool mfma_ok = kquant && !ex.idx && K % 256 == 0 && mfma_split(nb, S, bpw) && element_offset % 256 == 0 &&
+                         mfma_large(type, M);
+    if (mfma_ok) {
+        if (type == kQ4_K)
+            launch_mfma<kQ4_K>(w, type, x, y, M, nb, element_offset / 256, S, bpw, s);
+        else
+            launch_mfma<kQ6_K>(w, type, x, y, M, nb, element_offset / 256, S, bpw, s);
+    } else if (kquant && shape_ok && aligned) {
         const uint64_t ub0 = element_offset / 256;
         const int groups = nb >= 8 ? M : (M + 8 / nb - 1) / (8 / nb);
         if (type == kQ4_K)

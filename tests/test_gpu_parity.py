@@ -643,6 +643,11 @@ GEMV_CASES = [
     # persistent-grid shapes: 2 / 4 rows per tile, 2 slices held in VGPRs, x reloaded (K > 4096)
     ("Q4_K", 5000, 2048, 5000, 0), ("Q4_K", 9000, 4096, 9000, 0), ("Q4_K", 300, 8192, 300, 0),
     ("Q6_K", 5000, 2048, 5000, 0), ("Q6_K", 9000, 4096, 9000, 0), ("Q6_K", 300, 8192, 300, 0),
+    # the MFMA path (Q6_K from 1024 tiles of 16 rows, Q4_K from 4096): k-slices of
+    # 2 / 4 / 1 / 3 blocks, ragged last tiles, element offsets
+    ("Q6_K", 16400, 2048, 16397, 0), ("Q6_K", 16420, 4096, 16401, 16), ("Q6_K", 20000, 512, 19999, 0),
+    ("Q6_K", 16500, 768, 16500, 0), ("Q4_K", 65600, 2048, 65543, 40), ("Q4_K", 65600, 1024, 65600, 0),
+    ("Q4_K", 65536, 3072, 65536, 0),
 ]
 
 
@@ -677,3 +682,49 @@ def test_matmul_dispatch_reuses_x_and_checks_shapes(oracle):
             ops.matmul_dispatch(dw, "Q4_K", rows * K, dx, kw.get("M", rows), K, element_offset=kw.get("element_offset", 0))
     with pytest.raises(QwenError):
         ops.matmul_dispatch(dw, 3, rows * K, dx, rows, K)  # Q4_1: no path
+
+
+@pytest.mark.parametrize("kind,M", [("Q6_K", 16400), ("Q4_K", 65550)])
+def test_matmul_dispatch_mfma_random_blocks(oracle, kind, M):
+    """The MFMA path on GGML blocks with random fp16 fields of both signs
+    (subnormals included) and every quant / scale byte value."""
+    import ggml_blocks
+
+    t, K = ops.GGML_TYPES[kind], 2048
+    r = rng(M + 3)
+    w = ggml_blocks.random_blocks(r, t, M * K // 256)
+    x = r.standard_normal(K).astype(F32)
+    got = host(ops.matmul_dispatch(dev(w), t, M * K, dev(x), M, K))
+    assert_f32_close(got, oracle.gemv(w, t, x, M, K, threads=THREADS), group=M, what=kind)
+
+
+@pytest.mark.parametrize("case", ["nan", "inf", "zero", "tiny", "huge", "small", "large", "outlier"])
+def test_matmul_dispatch_mfma_x_range(oracle, case):
+    """x the integer-digit form covers (|x| from 2^-100 to 2^100 per k-slice,
+    outliers) and x it hands to the per-element form (non-finite, beyond that
+    range); zero x gives +0."""
+    M, K = 16400, 2048
+    w = synth.q6k_table(M, K, seed_tensor=2)
+    x = rng(11).standard_normal(K).astype(F32)
+    if case == "nan":
+        x[777] = np.nan
+    elif case == "inf":
+        x[1500] = np.inf
+    elif case == "zero":
+        x[:] = 0
+    else:
+        x *= F32({"tiny": 1e-33, "huge": 1e33, "small": 1e-25, "large": 1e25, "outlier": 1.0}[case])
+        if case == "outlier":
+            x[5] = 1e4
+    got = host(ops.matmul_dispatch(dev(w), "Q6_K", M * K, dev(x), M, K))
+    ref = oracle.gemv(w, 14, x, M, K, threads=THREADS)
+    if case == "nan":
+        assert np.isnan(got).all()
+    elif case == "inf":
+        assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.array_equal(got[np.isinf(ref)], ref[np.isinf(ref)])
+        assert np.isinf(ref).any()
+    elif case == "zero":
+        assert np.array_equal(got.view(np.uint32), np.zeros(M, np.uint32))
+    else:
+        assert_f32_close(got, ref, group=M, what=case)
+
