@@ -34,7 +34,10 @@ enum qwen_status {
     QWEN_STATUS_INVALID_ARGUMENT = 1, /* bad pointer, size or parameter       */
     QWEN_STATUS_UNSUPPORTED_TYPE = 2, /* GGML type without a dequant path     */
     QWEN_STATUS_OUT_OF_RANGE = 3,     /* row/element range outside the tensor */
-    QWEN_STATUS_LAUNCH_FAILED = 4     /* the HIP runtime rejected the launch  */
+    QWEN_STATUS_LAUNCH_FAILED = 4,    /* the HIP runtime rejected the launch  */
+    QWEN_STATUS_IO_ERROR = 5,         /* GGUF: file unreadable or not GGUF    */
+    QWEN_STATUS_MALFORMED = 6,        /* GGUF: content rejected by the parser */
+    QWEN_STATUS_OUT_OF_MEMORY = 7     /* GGUF: device or pinned allocation    */
 };
 
 /* ABI version of this header (bumped on any signature change). */

@@ -13,11 +13,13 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <unistd.h>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
 #include "gdn.hpp"
+#include "loader_gguf.hpp"
 #include "matmul_q4.hpp"
 #include "ops.hpp"
 #include "rope.hpp"
@@ -74,7 +76,140 @@ float max_abs_diff(const std::vector<float>& a, const std::vector<float>& b) {
 }
 
 // ------------------------------------------------------------------ CPU checks
+
+// ------------------------------------------------------------------ GGUF
+// A small GGUF v3 file: a few metadata kinds and a Q4_K "token_embd.weight"
+// [256 x 4] of known blocks (d = 1, dmin = 0, scale 1, quant = element % 16)
+// plus blk.0 / blk.1 norm weights, so the loader can be driven the way the
+// reference's main.cpp / model.cpp / tokenizer.cpp drive it.
+struct GgufBytes {
+    std::vector<uint8_t> b;
+    template <class T>
+    void put(T v) {
+        const uint8_t* p = reinterpret_cast<const uint8_t*>(&v);
+        b.insert(b.end(), p, p + sizeof(T));
+    }
+    void str(const std::string& s) {
+        put<uint64_t>(s.size());
+        b.insert(b.end(), s.begin(), s.end());
+    }
+    void pad(size_t a) {
+        while (b.size() % a) b.push_back(0);
+    }
+};
+
+std::vector<uint8_t> q4k_known_block() {
+    std::vector<uint8_t> blk(144, 0);
+    blk[0] = 0x00;
+    blk[1] = 0x3c;   // d = 1.0 (fp16), dmin = 0
+    for (int j = 0; j < 4; ++j) blk[4 + j] = 1;   // sub-blocks 0..3: scale 1, min 0
+    for (int j = 8; j < 12; ++j) blk[4 + j] = 1;  // sub-blocks 4..7: low nibbles of bytes 8..11
+    for (int i = 0; i < 128; ++i) blk[16 + i] = static_cast<uint8_t>((i % 16) | ((i % 16) << 4));
+    return blk;
+}
+
+std::string write_gguf(uint32_t version) {
+    GgufBytes f;
+    f.put<uint32_t>(0x46554747u);
+    f.put<uint32_t>(version);
+    f.put<uint64_t>(3);   // tensors
+    f.put<uint64_t>(4);   // metadata
+    f.str("general.architecture");
+    f.put<uint32_t>(8);
+    f.str("qwen35moe");
+    f.str("qwen35moe.full_attention_interval");
+    f.put<uint32_t>(4);
+    f.put<uint32_t>(4);
+    f.str("qwen35moe.rope.freq_base");
+    f.put<uint32_t>(6);
+    f.put<float>(10000000.0f);
+    f.str("tokenizer.ggml.tokens");
+    f.put<uint32_t>(9);
+    f.put<uint32_t>(8);
+    f.put<uint64_t>(2);
+    f.str("hello");
+    f.str("world");
+    const char* names[3] = {"token_embd.weight", "blk.0.attn_norm.weight", "blk.1.attn_norm.weight"};
+    uint64_t off = 0;
+    for (int i = 0; i < 3; ++i) {
+        f.str(names[i]);
+        if (i == 0) {
+            f.put<uint32_t>(2);
+            f.put<int64_t>(256);
+            f.put<int64_t>(4);
+            f.put<uint32_t>(12);   // Q4_K
+        } else {
+            f.put<uint32_t>(1);
+            f.put<int64_t>(8);
+            f.put<uint32_t>(0);    // F32
+        }
+        f.put<uint64_t>(off);
+        off += i == 0 ? 4 * 144 : 32;
+    }
+    f.pad(32);
+    const std::vector<uint8_t> blk = q4k_known_block();
+    for (int r = 0; r < 4; ++r) f.b.insert(f.b.end(), blk.begin(), blk.end());
+    for (int i = 0; i < 16; ++i) f.put<float>(1.0f + i);
+    const std::string path = "/tmp/qwen35_dropin_" + std::to_string(version) + "_" + std::to_string(getpid()) + ".gguf";
+    FILE* fp = std::fopen(path.c_str(), "wb");
+    if (!fp) throw std::runtime_error("cannot write " + path);
+    std::fwrite(f.b.data(), 1, f.b.size(), fp);
+    std::fclose(fp);
+    return path;
+}
+
+void gguf_cpu_checks() {
+    qwen::GgufLoader l;
+    expect(!l.open("/nonexistent/model.gguf"), "GgufLoader::open missing file returns false");
+    const std::string p = write_gguf(3);
+    expect(l.open(p), "GgufLoader::open");
+    expect(l.version() == 3 && l.tensor_count() == 3 && l.metadata_count() == 4, "GGUF header counts");
+    expect(l.get_meta_string("general.architecture") == "qwen35moe", "get_meta_string");
+    expect(l.get_meta_int("qwen35moe.full_attention_interval", 1) == 4, "get_meta_int");
+    expect(l.get_meta_float("qwen35moe.rope.freq_base", 0) == 10000000.0, "get_meta_float");
+    expect(l.get_meta_int("absent.key", -7) == -7 && l.get_meta_int("general.architecture", 5) == 5,
+           "get_meta_int default and unparsable text");
+    const auto* tokens = l.get_meta_array("tokenizer.ggml.tokens");
+    expect(tokens && tokens->size() == 2 && (*tokens)[1] == "world", "get_meta_array");
+    const qwen::QuantTensor* emb = l.get_tensor("token_embd.weight");
+    expect(emb && emb->type == qwen::GgmlType::Q4_K && emb->shape.size() == 2 && emb->shape[0] == 256 &&
+               emb->shape[1] == 4 && emb->num_elements == 1024 && emb->size_bytes == 576 && !emb->device_ptr,
+           "get_tensor token_embd.weight");
+    expect(!l.get_tensor("output.weight") && l.tensors().size() == 3 && l.total_vram_bytes() == 0, "tensors()");
+    expect(qwen::tensor_block_index("blk.12.ffn_up.weight") == 12 && qwen::tensor_block_index("token_embd.weight") == -1 &&
+               qwen::tensor_block_index("blk..x") == -1 && qwen::tensor_block_index("blk.1a.x") == -1,
+           "tensor_block_index");
+    std::remove(p.c_str());
+    const std::string p1 = write_gguf(1);
+    expect_throw([&] { l.open(p1); }, "unsupported GGUF version 1", "GgufLoader::open version 1 throws");
+    std::remove(p1.c_str());
+}
+
+void gguf_gpu_checks() {
+    qwen::GgufLoader l;
+    const std::string p = write_gguf(3);
+    expect(l.open(p) && l.load_tensors_to_gpu(1), "load_tensors_to_gpu(base_layer_count = 1)");
+    const qwen::QuantTensor* emb = l.get_tensor("token_embd.weight");
+    expect(emb->device_ptr && l.get_tensor("blk.0.attn_norm.weight")->device_ptr &&
+               !l.get_tensor("blk.1.attn_norm.weight")->device_ptr && l.total_vram_bytes() == 576 + 32,
+           "blk.1 stays on disk");
+    // src/model.cpp:190: the embedding row of a token straight from the loaded table
+    float* d_out = nullptr;
+    hip_ok(hipMalloc(&d_out, 256 * sizeof(float)), "hipMalloc");
+    qwen::dequantize_row(*emb, d_out, 3, 256);
+    std::vector<float> out(256);
+    hip_ok(hipMemcpy(out.data(), d_out, 256 * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    bool ok = true;
+    for (int i = 0; i < 256; ++i) ok = ok && out[i] == static_cast<float>(i % 16);
+    expect(ok, "dequantize_row of a loaded GGUF table");
+    (void)hipFree(d_out);
+    l.unload_gpu();
+    expect(!l.get_tensor("token_embd.weight")->device_ptr && l.total_vram_bytes() == 0, "unload_gpu");
+    std::remove(p.c_str());
+}
+
 void cpu_checks() {
+    gguf_cpu_checks();
     std::vector<float> dummy(16);
     expect_throw([&] { qwen::rope_forward(nullptr, 3, 2, 8, 4, 100.f); }, "invalid RoPE arguments", "rope null");
     expect_throw([&] { qwen::rope_forward(dummy.data(), 3, 2, 8, 3, 100.f); }, "invalid RoPE arguments", "rope odd");
@@ -182,6 +317,7 @@ void check_block(qwen::GgmlType type, const char* name, const std::vector<uint8_
 }
 
 void gpu_checks() {
+    gguf_gpu_checks();
     const uint8_t packed[12] = {0xc1, 0x82, 0x43, 0x04, 0x85, 0x46, 0x07, 0xc8, 0x91, 0x2a, 0xb3, 0x4c};
     {  // Q4_K
         std::vector<uint8_t> b(144);

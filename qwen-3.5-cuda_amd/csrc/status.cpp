@@ -45,6 +45,9 @@ const char* qwen_status_name(int status) {
         case QWEN_STATUS_UNSUPPORTED_TYPE: return "QWEN_STATUS_UNSUPPORTED_TYPE";
         case QWEN_STATUS_OUT_OF_RANGE: return "QWEN_STATUS_OUT_OF_RANGE";
         case QWEN_STATUS_LAUNCH_FAILED: return "QWEN_STATUS_LAUNCH_FAILED";
+        case QWEN_STATUS_IO_ERROR: return "QWEN_STATUS_IO_ERROR";
+        case QWEN_STATUS_MALFORMED: return "QWEN_STATUS_MALFORMED";
+        case QWEN_STATUS_OUT_OF_MEMORY: return "QWEN_STATUS_OUT_OF_MEMORY";
         default: return "QWEN_STATUS_UNKNOWN";
     }
 }

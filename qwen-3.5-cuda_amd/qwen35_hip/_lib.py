@@ -1,4 +1,5 @@
-"""ctypes view of libqwen35_hip.so (the C ABI declared in include/qwen35_hip.h).
+"""ctypes view of libqwen35_hip.so (the C ABI declared in include/qwen35_hip.h and
+include/qwen35_gguf.h).
 
 The library is built in-tree by the package Makefile. Loading fails loudly when
 it is missing: there is no fallback implementation.
@@ -18,6 +19,9 @@ STATUS_INVALID_ARGUMENT = 1
 STATUS_UNSUPPORTED_TYPE = 2
 STATUS_OUT_OF_RANGE = 3
 STATUS_LAUNCH_FAILED = 4
+STATUS_IO_ERROR = 5
+STATUS_MALFORMED = 6
+STATUS_OUT_OF_MEMORY = 7
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -73,6 +77,18 @@ SIGNATURES: dict[str, list] = {
     "qwen_moe_expert_matmul": [_P, _I, _U64, _U64, _I, _P, _I, _P, _I64, _P, _I, _I, _P],
     "qwen_matmul_type_supported": [_I],
     "qwen_matmul_dispatch": [_P, _I, _U64, _P, _P, _I, _I, _U64, _P],
+    # GGUF loader (include/qwen35_gguf.h)
+    "qwen_gguf_open": [ctypes.c_char_p, _P],
+    "qwen_gguf_close": [_P],
+    "qwen_gguf_get_info": [_P, _P],
+    "qwen_gguf_get_tensor": [_P, _U64, _P],
+    "qwen_gguf_find_tensor": [_P, ctypes.c_char_p, _P],
+    "qwen_gguf_get_meta": [_P, ctypes.c_char_p, _P],
+    "qwen_gguf_get_meta_array_size": [_P, ctypes.c_char_p, _P],
+    "qwen_gguf_get_meta_array_item": [_P, ctypes.c_char_p, _U64, _P],
+    "qwen_gguf_get_meta_key": [_P, _U64, _P, _P],
+    "qwen_gguf_load": [_P, _I, _P],
+    "qwen_gguf_unload": [_P],
 }
 
 _RESTYPES = {"qwen_last_error": ctypes.c_char_p, "qwen_status_name": ctypes.c_char_p,
@@ -82,11 +98,11 @@ _lib = None
 
 
 def header_functions(header: Path | None = None) -> list[str]:
-    """Names of the functions include/qwen35_hip.h declares (for export checks)."""
+    """Names of the functions the C headers (include/*.h) declare (for export checks)."""
     import re
 
-    header = header or PACKAGE_DIR.parent / "include" / "qwen35_hip.h"
-    text = header.read_text()
+    headers = [header] if header else sorted((PACKAGE_DIR.parent / "include").glob("*.h"))
+    text = "\n".join(h.read_text() for h in headers)
     return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(qwen_\w+)\s*\(", text, flags=re.M)))
 
 
