@@ -39,6 +39,7 @@ import argparse
 import ctypes
 import json
 import os
+import struct
 import sys
 import time
 from pathlib import Path
@@ -480,6 +481,60 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def measure_gguf_load(torch, host, path: Path) -> dict:
+    """GGUF file -> device memory (the loader row, src/loader_gguf.cpp:322-381):
+    a file holding the C5 tables as token_embd.weight (Q4_K) and output.weight
+    (Q6_K), 703 MB, written to `path` and loaded three times by the library
+    (median); beside it the reference's scheme (per tensor: read into a host
+    buffer, allocate, synchronous pageable copy) run through torch on the same
+    file. The file sits in the page cache after writing, so both figures are
+    host memory -> PCIe -> HBM, not disk."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import gguf_writer as gw
+    from qwen35_hip.gguf import GgufFile
+
+    q4, q6 = host["dequant_gather_q4_k"]["table"], host["dequant_gather_q6_k"]["table"]
+    ts = [("token_embd.weight", (2048, 248320), 12, memoryview(q4)), ("output.weight", (2048, 248320), 14,
+                                                                       memoryview(q6))]
+    offs = [0, (q4.nbytes + 31) // 32 * 32]
+    head = (b"GGUF" + struct.pack("<IQQ", 3, len(ts), 1) + gw.kv_bytes("general.architecture", gw.STR, "qwen35moe") +
+            b"".join(gw.tensor_info_bytes(n, shp, t, o) for (n, shp, t, _), o in zip(ts, offs)))
+    with open(path, "wb") as f:   # header (tensor infos), then the payload written in place
+        f.write(head)
+        payload = (len(head) + 31) // 32 * 32
+        f.write(b"\0" * (payload - len(head)))
+        f.write(ts[0][3])
+        f.write(b"\0" * ((q4.nbytes + 31) // 32 * 32 - q4.nbytes))
+        f.write(ts[1][3])
+    nbytes = q4.nbytes + q6.nbytes
+    times = []
+    with GgufFile(path) as g:
+        for _ in range(3):
+            t0 = time.perf_counter()
+            g.load()
+            times.append(time.perf_counter() - t0)
+            g.unload()
+    ours = sorted(times)[1]
+    ref_times = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        with open(path, "rb") as f:
+            for k, (_, _, _, b) in enumerate(ts):
+                f.seek(payload + offs[k])
+                buf = bytearray(len(b))
+                f.readinto(buf)
+                d = torch.frombuffer(buf, dtype=torch.uint8).to("cuda:0")
+                torch.cuda.synchronize()
+                del d
+        ref_times.append(time.perf_counter() - t0)
+    ref = min(ref_times)
+    path.unlink()
+    return {"config": "GGUF with the C5 tables (Q4_K token_embd 248320x2048 + Q6_K output), page-cache warm",
+            "bytes": nbytes, "ms": round(ours * 1e3, 2), "gbps": round(nbytes / ours / 1e9, 2),
+            "reference_scheme_ms": round(ref * 1e3, 2), "reference_scheme_gbps": round(nbytes / ref / 1e9, 2)}
+
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description="Fused per-layer kernels on one MI355X")
     ap.add_argument("--gpus", type=int, default=1)
@@ -585,6 +640,13 @@ def main() -> int:
                   f"   copy of same bytes {k.copy_us:8.2f} us {k.bytes / k.copy_us / 1e3:7.1f} GB/s",
                   file=sys.stderr, flush=True)
 
+    gguf = None
+    if not args.no_next and not args.no_per_kernel and not args.kernels:
+        gguf = measure_gguf_load(torch, host, Path(os.environ.get("TMPDIR", "/tmp")) / f"qwen35_bench_{os.getpid()}.gguf")
+        print(f"# gguf load: {gguf['ms']:.1f} ms ({gguf['gbps']:.1f} GB/s); reference scheme "
+              f"{gguf['reference_scheme_ms']:.1f} ms ({gguf['reference_scheme_gbps']:.1f} GB/s)", file=sys.stderr,
+              flush=True)
+
     # ---- roofline of the dominant kernel
     roofline = None
     if not args.no_per_kernel and kernels:
@@ -650,6 +712,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "next_rows": next_rows,
+        "gguf_load": gguf,
     }
     text = json.dumps(line)
     print(text, flush=True)

@@ -15,12 +15,12 @@
 // block per head, 32 blocks).
 //
 // Here the state (value_heads x key_dim x value_dim fp32, 2 MB per layer at
-// 32 x 128 x 128) is read once and written once per call: one wave owns 4
-// value columns of one head, lane L holds rows L, L+64, ... of those columns
-// as float4 in VGPRs, the column sums over rows are wave reductions (DPP +
-// permlane), and the updated rows go back with 16-byte stores. The multi-token
-// entry point keeps the state slice in VGPRs across all tokens of the call
-// (the reference's per-token loop, one launch), reading each token's q, k, v
+// 32 x 128 x 128) is read once and written once per call: one wave owns a few
+// value columns of one head, each column spread over a group of 16 or 32
+// lanes that hold 4 or 8 of its rows in VGPRs, so a column sum over rows is a
+// short per-lane partial plus a 4-5 step DPP reduction. The multi-token entry
+// point keeps the state slice in VGPRs across all tokens of the call (the
+// reference's per-token loop, one launch), reading each token's q, k, v
 // straight from the GDN front end's output rows.
 #include <algorithm>
 #include <cmath>
@@ -51,13 +51,107 @@ __global__ __launch_bounds__(kBlock) void gates_kernel(const float* __restrict__
     }
 }
 
-// One wave per (value head, 4 value columns); RPL rows of the state per lane
+// One wave per (value head, NCOL value columns): column c = L / G of the wave
+// (G = 64 / NCOL lanes per column), rows (L % G) * RPL .. + RPL - 1 of that
+// column in VGPRs (RPL = DK / G). The per-token column sums over rows are a
+// per-lane partial over RPL rows plus a G-lane DPP reduction (4 or 5 steps).
+// Tokens t < rows run in order, the state slice staying in VGPRs; q/k/v of
+// token t sit at t * qkv_stride, beta/decay at t * value_heads, out at
+// t * out_stride. The inputs of token t + kPrefetch are loaded while token t
+// is computed (a ring of kPrefetch register slots; loads past the last token
+// re-read it and are never used).
+constexpr int kPrefetch = 4;
+
+template <int DK, int NCOL>
+__global__ __launch_bounds__(kBlock) void gdn_recurrent_g(float* __restrict__ S, const float* __restrict__ q,
+                                                          const float* __restrict__ k, const float* __restrict__ v,
+                                                          const float* __restrict__ beta,
+                                                          const float* __restrict__ decay, float* __restrict__ out,
+                                                          int rows, int key_heads, int value_heads, int value_dim,
+                                                          int64_t qkv_stride, int64_t out_stride) {
+    constexpr int G = kWave / NCOL;
+    constexpr int RPL = DK / G;
+    static_assert(RPL % 4 == 0 && RPL * G == DK, "rows per lane");
+    constexpr int P = kPrefetch;
+    const int cblocks = value_dim / NCOL;
+    const int wave = blockIdx.x * kWaves + wave_in_block();
+    if (wave >= value_heads * cblocks) return;  // wave-uniform
+    const int lane = threadIdx.x & 63;
+    const int h = wave / cblocks;
+    const int c = lane / G, r0 = (lane % G) * RPL;
+    const int j = NCOL * (wave - h * cblocks) + c;   // this lane's value column
+    const int src = h % key_heads;  // value heads tile as [subgroup][key head]
+    float* Sj = S + static_cast<size_t>(h) * DK * value_dim + static_cast<size_t>(r0) * value_dim + j;
+
+    float kr[P][RPL], qr[P][RPL], vv[P], bt[P], dc[P];
+    auto fetch = [&](int slot, int t) {
+        t = min(t, rows - 1);
+        const float* qt = q + t * qkv_stride + src * DK + r0;
+        const float* kt = k + t * qkv_stride + src * DK + r0;
+#pragma unroll
+        for (int r = 0; r < RPL; r += 4) {
+            const float4 kv = ld4(kt + r), qv = ld4(qt + r);
+            kr[slot][r] = kv.x;
+            kr[slot][r + 1] = kv.y;
+            kr[slot][r + 2] = kv.z;
+            kr[slot][r + 3] = kv.w;
+            qr[slot][r] = qv.x;
+            qr[slot][r + 1] = qv.y;
+            qr[slot][r + 2] = qv.z;
+            qr[slot][r + 3] = qv.w;
+        }
+        vv[slot] = v[t * qkv_stride + static_cast<size_t>(h) * value_dim + j];
+        bt[slot] = beta[static_cast<int64_t>(t) * value_heads + h];
+        dc[slot] = decay[static_cast<int64_t>(t) * value_heads + h];
+    };
+#pragma unroll
+    for (int p = 0; p < P; ++p) fetch(p, p);
+
+    // NCOL lanes of a row read NCOL consecutive floats (the same 16- or 8-byte
+    // pieces per row as any column slicing of the row-major state).
+    float s[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) s[r] = __builtin_nontemporal_load(Sj + static_cast<size_t>(r) * value_dim);
+
+    for (int t0 = 0; t0 < rows; t0 += P) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const int t = t0 + p;
+            if (t >= rows) break;  // wave-uniform
+            // S *= decay; mem = sum_i k_i S_i (this column)
+            const float d = dc[p];
+            float m = 0.f;
+#pragma unroll
+            for (int r = 0; r < RPL; ++r) {
+                s[r] *= d;
+                m = __builtin_fmaf(kr[p][r], s[r], m);
+            }
+            m = group_sum<G>(m);
+            const float dl = (vv[p] - m) * bt[p];
+            // S += k_i * delta; o = sum_i q_i S_i
+            float o = 0.f;
+#pragma unroll
+            for (int r = 0; r < RPL; ++r) {
+                s[r] = __builtin_fmaf(kr[p][r], dl, s[r]);
+                o = __builtin_fmaf(qr[p][r], s[r], o);
+            }
+            o = group_sum<G>(o);
+            if (lane % G == 0) out[t * out_stride + static_cast<size_t>(h) * value_dim + j] = o;
+            fetch(p, t + P);
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) __builtin_nontemporal_store(s[r], Sj + static_cast<size_t>(r) * value_dim);
+}
+
+// Single step (rows = 1, the decode path): one wave per (value head, 4 value
+// columns); RPL rows of the state per lane
 // (key_dim = 64 * RPL). Tokens t < rows run in order, the state slice staying
 // in VGPRs; q/k/v of token t sit at t * qkv_stride, beta/decay at
 // t * value_heads, out at t * out_stride. The inputs of token t + kPrefetch
 // are loaded while token t is computed (a ring of kPrefetch register slots;
 // loads past the last token re-read it and are never used).
-constexpr int kPrefetch = 4;
 
 template <int RPL>
 __global__ __launch_bounds__(kBlock) void gdn_recurrent_v4(float* __restrict__ S, const float* __restrict__ q,
@@ -187,17 +281,29 @@ __global__ __launch_bounds__(kMaxValueDim) void gdn_recurrent_any(
 int launch_recurrent(float* state, const float* q, const float* k, const float* v, const float* beta,
                      const float* decay, float* out, int rows, int key_heads, int value_heads, int key_dim,
                      int value_dim, int64_t qkv_stride, int64_t out_stride, hipStream_t s, const char* what) {
-    const bool vec = value_dim % 4 == 0 && (key_dim == 64 || key_dim == 128) && aligned16(state) && aligned16(v) &&
-                     aligned16(out) && qkv_stride % 4 == 0 && out_stride % 4 == 0;
-    if (vec) {
-        const int waves = value_heads * (value_dim / 4);
-        const unsigned grid = blocks_for(waves, kWaves);
+    const bool vec = value_dim % 4 == 0 && (key_dim == 64 || key_dim == 128) && aligned16(q) && aligned16(k) &&
+                     qkv_stride % 4 == 0;
+    if (vec && rows == 1 && aligned16(state) && aligned16(v) && aligned16(out)) {
+        // One token: the state traffic dominates, read as float4 rows.
+        const unsigned grid = blocks_for(value_heads * (value_dim / 4), kWaves);
         if (key_dim == 64)
             gdn_recurrent_v4<1><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
                                                         value_heads, value_dim, qkv_stride, out_stride);
         else
             gdn_recurrent_v4<2><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
                                                         value_heads, value_dim, qkv_stride, out_stride);
+    } else if (vec) {
+        // Columns per wave: 2 for key dim 128 (two waves per SIMD at the Qwen3.5
+        // shape, 32 value heads x 128 columns), 4 for key dim 64.
+        constexpr int kNcol128 = 2;
+        const int ncol = key_dim == 64 ? 4 : kNcol128;
+        const unsigned grid = blocks_for(value_heads * (value_dim / ncol), kWaves);
+        if (key_dim == 64)
+            gdn_recurrent_g<64, 4><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
+                                                           value_heads, value_dim, qkv_stride, out_stride);
+        else
+            gdn_recurrent_g<128, kNcol128><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
+                                                                   value_heads, value_dim, qkv_stride, out_stride);
     } else {
         gdn_recurrent_any<<<value_heads, kMaxValueDim, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
                                                                value_heads, key_dim, value_dim, qkv_stride,

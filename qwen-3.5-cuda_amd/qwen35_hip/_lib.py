@@ -12,7 +12,8 @@ import os
 from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent.parent
-LIB_PATH = PACKAGE_DIR / "libqwen35_hip.so"
+# The in-tree build; QWEN35_HIP_LIB names another build of the same library.
+LIB_PATH = Path(os.environ.get("QWEN35_HIP_LIB") or PACKAGE_DIR / "libqwen35_hip.so")
 
 STATUS_OK = 0
 STATUS_INVALID_ARGUMENT = 1

@@ -424,7 +424,9 @@ def test_gdn_recurrent_rows(oracle, kh, vh, dk, dv, rows):
 
 
 def test_gdn_recurrent_rows_equals_steps():
-    """One launch over T tokens leaves the same bits as T single-step launches."""
+    """One launch over T tokens matches T single-step launches (the decode path's
+    kernel) to fp32 rounding: the two kernels sum a column's rows in different
+    orders."""
     kh, vh, dk, dv, T = 16, 32, 128, 128, 6
     r = rng(77)
     qkv, b, alpha, a, dt, state = _gdn_inputs(r, T, kh, vh, dk, dv)
@@ -437,8 +439,8 @@ def test_gdn_recurrent_rows_equals_steps():
         o = ops.gdn_recurrent_step(s2, dq[t, :kd].contiguous(), dq[t, kd:2 * kd].contiguous(),
                                    dq[t, 2 * kd:].contiguous(), beta[t].contiguous(), decay[t].contiguous(),
                                    kh, vh, dk, dv)
-        assert_bits_equal(host(o), out[t], f"token {t}")
-    assert_bits_equal(host(s1), host(s2), "state")
+        assert_f32_close(host(o), out[t], group=dv, rtol=1e-5, what=f"token {t}")
+    assert_f32_close(host(s1), host(s2), group=dv, what="state")
 
 
 def test_gdn_recurrent_rejects_wide_values():
