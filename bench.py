@@ -242,6 +242,20 @@ def build_next_rows(torch, ops, synth, host):
         k.gdn = {"rows": rows, "qkv": qkv_h, "beta": np.full((rows, vh), 0.5, np.float32),
                  "decay": np.full((rows, vh), 0.95, np.float32), "state": st0.cpu().numpy()}
         ks.append(k)
+        if rows > 1:
+            # The chunked form on the same inputs (its workspace outside the bytes).
+            ws = torch.empty(ops.load().qwen_gdn_recurrent_chunked_workspace_bytes(rows, vh), dtype=torch.uint8,
+                             device=dev)
+
+            def mk_chunk(i, qkv=qkv, beta=beta, decay=decay, st0=st0, o=o, ws=ws):
+                ss = st0 if i == 0 else st0.clone()
+                qq = qkv if i == 0 else qkv.clone()
+                oo = o if i == 0 else torch.empty_like(o)
+                return lambda: ops.gdn_recurrent_chunked(ss, qq, beta, decay, kh, vh, dk, dv, oo, workspace=ws)
+            kc = Kernel("gdn_recurrent_chunked_4096", "the same 4096 tokens in the chunked form (64-token chunks, "
+                        "fp32 MFMA, 2 launches)", nb, nb, mk_chunk)
+            kc.gdn = k.gdn
+            ks.append(kc)
 
     # Decode attention (attn_kernels.cu:72-195): 16 query / 2 kv heads of 256,
     # 4096 cached keys, sigmoid gate; fused split-K path and the reference's

@@ -163,6 +163,24 @@ int qwen_gdn_recurrent_rows(float* state, const float* q, const float* k, const 
                             int key_heads, int value_heads, int key_dim, int value_dim,
                             int64_t qkv_stride, int64_t out_stride, void* stream);
 
+/* Chunked form of qwen_gdn_recurrent_rows for many tokens (prefill): the same
+ * recurrence re-associated over chunks of 64 tokens (decay ratios as running
+ * products, a 64 x 64 triangular solve per chunk and head, the state updated
+ * once per chunk on fp32 MFMA); equal to the token loop within fp32 rounding.
+ * Arguments as qwen_gdn_recurrent_rows plus a caller-owned device workspace of
+ * at least qwen_gdn_recurrent_chunked_workspace_bytes(rows, value_heads)
+ * (16-byte aligned; contents scratch). Shapes the chunked kernels do not cover
+ * (key_dim != 128, value_dim not a multiple of 16, unaligned q / k) run the
+ * token loop and leave the workspace untouched.
+ * No reference counterpart: the reference runs the per-token step for every
+ * token (src/layer_gdn.cpp:100-106). */
+size_t qwen_gdn_recurrent_chunked_workspace_bytes(int rows, int value_heads);
+int qwen_gdn_recurrent_chunked(float* state, const float* q, const float* k, const float* v,
+                               const float* beta, const float* decay, float* out, int rows,
+                               int key_heads, int value_heads, int key_dim, int value_dim,
+                               int64_t qkv_stride, int64_t out_stride, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
 /* ====================================================================== attention core (decode)
  * One query position against the KV cache, rows [t][kv_heads][dim]; query head h
  * reads kv head h / (heads / kv_heads) (heads a multiple of kv_heads). */

@@ -1,0 +1,471 @@
+// Chunked form of the Gated DeltaNet recurrence for many tokens (prefill).
+//
+// The reference updates the state one token at a time (src/cuda/gdn.cu:108-151,
+// called per token by src/layer_gdn.cpp:100-106): per value head, with key
+// vectors k_t, q_t (key head h % key_heads), value v_t, gates beta_t, d_t,
+//     S <- d_t S;  delta_t = beta_t (v_t - S^T k_t);  S <- S + k_t delta_t^T;
+//     o_t = S^T q_t.
+// Over a chunk of C tokens starting from state S0, with
+//     R[t][i] = d_{i+1} * ... * d_t  (i <= t; the decay between tokens i and t),
+//     gamma_t = d_0 * ... * d_t,
+// the state after token t is gamma_t S0 + sum_{i<=t} R[t][i] k_i delta_i^T, so
+//     delta_t = beta_t (v_t - gamma_t S0^T k_t - sum_{i<t} R[t][i] (k_i.k_t) delta_i)
+//     (I + A) Delta = diag(beta) (V - diag(gamma) K S0),  A[t][i] = beta_t R[t][i] (k_t.k_i), i < t
+//     Delta = T' (V - diag(gamma) X),  T' = (I + A)^-1 diag(beta),  X = K S0
+//     O = diag(gamma) Q S0 + Bm Delta,  Bm[t][i] = R[t][i] (q_t.k_i), i <= t
+//     S_C = gamma_{C-1} S0 + sum_i R[C-1][i] k_i delta_i^T.
+// This is the same sum re-associated (fp32 tolerance against the token loop).
+// The decay ratios are running products, never quotients, so decays that
+// underflow give exact zeros rather than 0/0.
+//
+// Kernel A (one workgroup per (chunk, value head), all chunks in parallel):
+// K K^T and Q K^T on fp32 MFMA (v_mfma_f32_16x16x4f32), the ratios, and T as a
+// blocked inverse (16 x 16 diagonal blocks by forward substitution, the others
+// as MFMA products) -> T', Bm, gamma, R[C-1][.] to the caller's workspace.
+// Kernel B (one workgroup per (value head, 16 state columns), chunks in order,
+// the workgroups of one head on one XCD):
+// X = K S0 and Y = Q S0 (each wave one 16-token M-tile, K = 128 over 32 MFMA
+// steps), Delta = T' (V - gamma X), O = gamma Y + Bm Delta, then the 128 x 16
+// state block updated from K~^T Delta; the block lives in LDS between chunks
+// and is read from / written to the state once per call.
+#include <algorithm>
+
+#include "capi_common.hpp"
+#include "device_common.hpp"
+
+namespace qk {
+namespace {
+
+constexpr int kC = 64;                        // tokens per chunk
+constexpr int kDK = 128;                      // key dim of the chunked path
+constexpr int kNB = 16;                       // state columns per workgroup (kernel B)
+constexpr int kThreads = 256;
+constexpr int kXcds = 8;                      // gfx950: 8 XCDs, workgroups dealt round-robin
+constexpr int kLdA = kC + 4;                  // LDS row stride of the C x C matrices (16-byte rows)
+constexpr size_t kWsFloats = 2 * kC * kC + 2 * kC;   // per (chunk, head): T', Bm, gamma, R[C-1][.]
+
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
+// D[m][n] += sum over the instruction's 4 k-slots of A[m][k] B[k][n]: lane L
+// supplies A[L%16][L/16] and B[L/16][L%16]; D lane L, element r is
+// D[4(L/16) + r][L%16].
+__device__ __forceinline__ v4f_t mfma4(float a, float b, v4f_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// 32 consecutive floats of `row` starting at dim `d0` (zeros for a padding token).
+__device__ __forceinline__ void load32(const float* __restrict__ row, int d0, bool valid, float (&r)[32]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float4 v = valid ? ld4(row + d0 + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+        r[4 * j] = v.x;
+        r[4 * j + 1] = v.y;
+        r[4 * j + 2] = v.z;
+        r[4 * j + 3] = v.w;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restrict__ q, const float* __restrict__ k,
+                                                           const float* __restrict__ beta,
+                                                           const float* __restrict__ decay, float* __restrict__ ws,
+                                                           int rows, int key_heads, int value_heads,
+                                                           int64_t qkv_stride) {
+    __shared__ __align__(16) float Kl[kC][kDK + 4];   // the chunk's K rows
+    __shared__ __align__(16) float G[kC][kLdA];    // K K^T, then A (strictly lower)
+    __shared__ __align__(16) float Pm[kC][kLdA];   // Q K^T, then T
+    __shared__ float sb[kC], sd[kC];
+    const int c = blockIdx.x, h = blockIdx.y;
+    const int t0 = c * kC;
+    const int src = h % key_heads;
+    const int lane = threadIdx.x & 63;
+    const int wv = wave_in_block();
+    const int g = lane >> 4, n = lane & 15;
+    float* wsc = ws + (static_cast<size_t>(c) * value_heads + h) * kWsFloats;
+    float* Tp = wsc;
+    float* Bm = wsc + kC * kC;
+    float* gam = wsc + 2 * kC * kC;
+    float* rr = gam + kC;
+
+    if (threadIdx.x < kC) {  // padding tokens: beta 0 (no update), decay 1
+        const int t = t0 + threadIdx.x;
+        sb[threadIdx.x] = t < rows ? beta[static_cast<int64_t>(t) * value_heads + h] : 0.0f;
+        sd[threadIdx.x] = t < rows ? decay[static_cast<int64_t>(t) * value_heads + h] : 1.0f;
+    }
+
+    // Lower-triangle 16x16 tiles (mt >= nt) of K K^T and Q K^T. Wave w loads
+    // the K and Q rows of tokens 16w .. 16w+15 once (lane: token 16w + L%16,
+    // dims 32(L/16) .. +31, the MFMA k-slot map of both operands) and puts its
+    // K rows in LDS; Q K^T tiles (w, nt <= w) stay with wave w (its Q rows in
+    // VGPRs), the K K^T tiles are dealt so that every wave has five tiles.
+    {
+        const int tok = t0 + 16 * wv + n;
+        const int64_t row = static_cast<int64_t>(min(tok, rows - 1)) * qkv_stride + src * kDK;
+        float kr[32], qr[32];
+        load32(k + row, 32 * g, tok < rows, kr);
+        load32(q + row, 32 * g, tok < rows, qr);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            *reinterpret_cast<float4*>(&Kl[16 * wv + n][32 * g + 4 * j]) =
+                make_float4(kr[4 * j], kr[4 * j + 1], kr[4 * j + 2], kr[4 * j + 3]);
+        __syncthreads();
+        auto tile = [&](const float (&a)[32], int mt, int nt, float (*D)[kLdA]) {
+            v4f_t acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float4 b = *reinterpret_cast<const float4*>(&Kl[16 * nt + n][32 * g + 4 * j]);
+                acc[0] = mfma4(a[4 * j], b.x, acc[0]);
+                acc[1] = mfma4(a[4 * j + 1], b.y, acc[1]);
+                acc[2] = mfma4(a[4 * j + 2], b.z, acc[2]);
+                acc[3] = mfma4(a[4 * j + 3], b.w, acc[3]);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                D[16 * mt + 4 * g + r][16 * nt + n] = (acc[0][r] + acc[1][r]) + (acc[2][r] + acc[3][r]);
+        };
+        for (int nt = 0; nt <= wv; ++nt) tile(qr, wv, nt, Pm);
+        // K K^T tiles (mt, nt), mt >= nt: wave w takes 4 - w of them, A rows from LDS.
+        static constexpr int kTiles[10][2] = {{3, 0}, {3, 1}, {3, 2}, {3, 3}, {2, 0}, {2, 1}, {2, 2}, {1, 0}, {1, 1}, {0, 0}};
+        const int first = wv == 0 ? 0 : wv == 1 ? 4 : wv == 2 ? 7 : 9;
+        for (int i = first; i < first + 4 - wv; ++i) {
+            const int mt = kTiles[i][0], nt = kTiles[i][1];
+            float a[32];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float4 v = *reinterpret_cast<const float4*>(&Kl[16 * mt + n][32 * g + 4 * j]);
+                a[4 * j] = v.x;
+                a[4 * j + 1] = v.y;
+                a[4 * j + 2] = v.z;
+                a[4 * j + 3] = v.w;
+            }
+            tile(a, mt, nt, G);
+        }
+    }
+    __syncthreads();
+
+    // Rows 16wv .. 16wv+15 per wave, lane i = column i: R[t][i] as a running
+    // product (the factor up to the wave's first row rebuilt from the decays,
+    // the same multiplication sequence as one pass over all rows), A and Bm.
+    {
+        const int i = lane;
+        const int ta = 16 * wv;
+        float r = 1.0f;
+        for (int t = i + 1; t < ta; ++t) r *= sd[t];
+        float dv16[16], bv16[16], gv[16], pv[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            dv16[u] = sd[ta + u];
+            bv16[u] = sb[ta + u];
+            gv[u] = G[ta + u][i];
+            pv[u] = Pm[ta + u][i];
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int t = ta + u;
+            if (t > i) r *= dv16[u];
+            G[t][i] = t > i ? (bv16[u] * gv[u]) * r : 0.0f;
+            Bm[t * kC + i] = t >= i ? pv[u] * r : 0.0f;
+        }
+        if (wv == 3) rr[i] = r;  // R[C-1][i]
+        if (wv == 0 && lane < 16) {  // gamma_t = d_0 * ... * d_t, in order
+            float gm = 1.0f;
+            for (int t = 0; t < kC; ++t) {
+                gm *= sd[t];
+                if (t % 16 == lane) gam[t] = gm;
+            }
+        }
+    }
+    __syncthreads();
+
+    // T = (I + A)^-1 in 16 x 16 blocks (A strictly lower). Diagonal blocks by
+    // forward substitution, lane L = block L/16, column L%16:
+    //   T_II[t][j] = [t == j] - sum_{i<t} A_II[t][i] T_II[i][j];
+    // then block rows I = 1..3, wave J computing
+    //   T_IJ = -T_II (sum_{K=J}^{I-1} A_IK T_KJ)
+    // on MFMA. The 4 k-slots of the MFMAs of one 16-deep product map to
+    // k = 4g + q (q the MFMA's index): A operands are 4 consecutive floats of a
+    // row, and a result in the D layout (lane: rows 4g + r) is directly the B
+    // operand of the next product. T goes to Pm's storage (Pm is consumed).
+    float(*T)[kLdA] = Pm;
+    __syncthreads();  // every wave is done reading Pm
+    if (wv == 0) {
+        const int I = lane >> 4, j = lane & 15;
+        float tc[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            float acc[4] = {t == j ? 1.0f : 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int i4 = 0; i4 < t; i4 += 4) {
+                const float4 a = *reinterpret_cast<const float4*>(&G[16 * I + t][16 * I + i4]);
+                acc[0] = __builtin_fmaf(-a.x, tc[i4], acc[0]);
+                if (i4 + 1 < t) acc[1] = __builtin_fmaf(-a.y, tc[i4 + 1], acc[1]);
+                if (i4 + 2 < t) acc[2] = __builtin_fmaf(-a.z, tc[i4 + 2], acc[2]);
+                if (i4 + 3 < t) acc[3] = __builtin_fmaf(-a.w, tc[i4 + 3], acc[3]);
+            }
+            tc[t] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+            T[16 * I + t][16 * I + j] = tc[t];
+        }
+    }
+    __syncthreads();
+    // 16 x 16 x 16 product: acc += X[16xa rows][16xa cols] * Y, X rows from LDS at
+    // (xr, xc), Y given as its D-layout registers (rows 4g + q, column n).
+    auto prod_regs = [&](v4f_t acc, const float(*X)[kLdA], int xr, int xc, const v4f_t& y) {
+        const float4 a = *reinterpret_cast<const float4*>(&X[xr + n][xc + 4 * g]);
+        acc = mfma4(a.x, y[0], acc);
+        acc = mfma4(a.y, y[1], acc);
+        acc = mfma4(a.z, y[2], acc);
+        return mfma4(a.w, y[3], acc);
+    };
+    for (int I = 1; I < 4; ++I) {
+        if (wv < I) {
+            const int J = wv;
+            v4f_t m = {0.f, 0.f, 0.f, 0.f};
+            for (int K = J; K < I; ++K) {
+                v4f_t tkj;  // T_KJ rows 4g + q, column n
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) tkj[q4] = T[16 * K + 4 * g + q4][16 * J + n];
+                m = prod_regs(m, G, 16 * I, 16 * K, tkj);
+            }
+            v4f_t t = prod_regs(v4f_t{0.f, 0.f, 0.f, 0.f}, T, 16 * I, 16 * I, m);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) T[16 * I + 4 * g + r][16 * J + n] = -t[r];
+        }
+        __syncthreads();
+    }
+    // T' = T diag(beta), zeros above the diagonal.
+    for (int e = threadIdx.x; e < kC * kC; e += kThreads) {
+        const int t = e / kC, jj = e % kC;
+        Tp[e] = t >= jj ? T[t][jj] * sb[jj] : 0.0f;
+    }
+}
+
+// One workgroup per CU (51 KB of LDS): one wave per SIMD, so the scheduler may
+// keep every operand load of a chunk in flight.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gdn_chunk_state(float* __restrict__ S, const float* __restrict__ q,
+                                                            const float* __restrict__ k, const float* __restrict__ v,
+                                                            const float* __restrict__ ws, float* __restrict__ out,
+                                                            int rows, int key_heads, int value_heads, int value_dim,
+                                                            int64_t qkv_stride, int64_t out_stride) {
+    __shared__ float Ks[kC][kDK + 5];       // the chunk's K rows (odd stride: column reads hit distinct banks)
+    __shared__ float Rv[kC][kNB + 1];
+    __shared__ float Dl[kC][kNB + 1];
+    __shared__ float Sl[kDK][kNB + 1];      // this block's 128 x 16 state
+    // Workgroup i runs on XCD i % 8 (round-robin dispatch). With the value
+    // heads a multiple of 8, head h's column blocks all get ids i with
+    // i % 8 == h % 8, so the chunk data of a head (K, Q, T', Bm, V) is fetched
+    // into one XCD's L2 instead of every XCD's.
+    const int ncb = value_dim / kNB;
+    int h, cb;
+    if (value_heads % kXcds == 0) {
+        const int x = blockIdx.x % kXcds, j = blockIdx.x / kXcds;
+        h = x + kXcds * (j / ncb);
+        cb = j % ncb;
+    } else {
+        h = blockIdx.x / ncb;
+        cb = blockIdx.x % ncb;
+    }
+    const int j0 = cb * kNB;
+    const int src = h % key_heads;
+    const int lane = threadIdx.x & 63;
+    const int wv = wave_in_block();
+    const int g = lane >> 4, n = lane & 15;
+    float* Sg = S + static_cast<size_t>(h) * kDK * value_dim + j0;
+
+    for (int e = threadIdx.x; e < kDK * kNB; e += kThreads)
+        Sl[e / kNB][e % kNB] = Sg[static_cast<size_t>(e / kNB) * value_dim + e % kNB];
+    __syncthreads();
+
+    // Per-chunk inputs of this lane, each reloaded for the next chunk as soon as
+    // it is dead in the current one (the state-free loads overlap the chain of
+    // MFMAs that the state forces).
+    const int nchunks = (rows + kC - 1) / kC;
+    const int tok = 16 * wv + n;   // token row of this lane's A operands
+    const int tres = 16 * wv + 4 * g;   // first of the 4 token rows of this lane's results
+    float kA[32], qA[32], vv[4], gm[4], glast;
+    float4 tpr[4], bmr[4], rq[4];
+    auto chunk_base = [&](int c) { return ws + (static_cast<size_t>(c) * value_heads + h) * kWsFloats; };
+    auto load_kq = [&](int c) {
+        const int t = c * kC + tok;
+        const int64_t row = static_cast<int64_t>(min(t, rows - 1)) * qkv_stride + src * kDK;
+        load32(k + row, 32 * g, t < rows, kA);
+        load32(q + row, 32 * g, t < rows, qA);
+    };
+    auto load_v = [&](int c) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = c * kC + tres + r;
+            vv[r] = t < rows ? v[static_cast<int64_t>(t) * qkv_stride + static_cast<size_t>(h) * value_dim + j0 + n]
+                             : 0.0f;
+        }
+    };
+    auto load_gam = [&](int c) {
+        const float4 gv = ld4(chunk_base(c) + 2 * kC * kC + tres);
+        gm[0] = gv.x;
+        gm[1] = gv.y;
+        gm[2] = gv.z;
+        gm[3] = gv.w;
+        glast = chunk_base(c)[2 * kC * kC + kC - 1];
+    };
+    auto load_rows16 = [&](float4 (&dst)[4], const float* src16) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) dst[s] = ld4(src16 + 4 * s);
+    };
+    // T' and Bm rows 16wv + n, columns 16g .. 16g+15; R[C-1][16g .. 16g+15].
+    auto tp_row = [&](int c) { return chunk_base(c) + (16 * wv + n) * kC + 16 * g; };
+    auto bm_row = [&](int c) { return chunk_base(c) + kC * kC + (16 * wv + n) * kC + 16 * g; };
+    auto rr_row = [&](int c) { return chunk_base(c) + 2 * kC * kC + kC + 16 * g; };
+    load_kq(0);
+    load_v(0);
+    load_gam(0);
+    load_rows16(tpr, tp_row(0));
+    load_rows16(bmr, bm_row(0));
+    load_rows16(rq, rr_row(0));
+
+    for (int c = 0; c < nchunks; ++c) {
+        const int t0 = c * kC;
+        const int cn = min(c + 1, nchunks - 1);
+
+        // S0 as the B operand (rows 32g + s, column n) and at this wave's rows of
+        // the state update's result tiles (32wv + 16mt + 4g + r).
+        float sB[32], sC[2][4];
+#pragma unroll
+        for (int s = 0; s < 32; ++s) sB[s] = Sl[32 * g + s][n];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sC[mt][r] = Sl[32 * wv + 16 * mt + 4 * g + r][n];
+
+#pragma unroll
+        for (int s = 0; s < 32; ++s) Ks[tok][32 * g + s] = kA[s];
+        v4f_t xa[4], ya[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) xa[u] = ya[u] = v4f_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 32; ++s) {
+            xa[s & 3] = mfma4(kA[s], sB[s], xa[s & 3]);
+            ya[s & 3] = mfma4(qA[s], sB[s], ya[s & 3]);
+        }
+        const v4f_t X = (xa[0] + xa[1]) + (xa[2] + xa[3]);
+        const v4f_t Y = (ya[0] + ya[1]) + (ya[2] + ya[3]);
+        if (c + 1 < nchunks) load_kq(cn);
+
+        // Result rows: tokens 16wv + 4g + r, column n.
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Rv[tres + r][n] = vv[r] - gm[r] * X[r];
+        if (c + 1 < nchunks) load_v(cn);
+        __syncthreads();
+
+        // Delta = T' Rv (this wave's 16 rows; K = the chunk's 64 tokens).
+        float rb[16];
+#pragma unroll
+        for (int s = 0; s < 16; ++s) rb[s] = Rv[16 * g + s][n];
+        v4f_t D0 = {0.f, 0.f, 0.f, 0.f}, D1 = D0;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            D0 = mfma4(tpr[s].x, rb[4 * s], D0);
+            D1 = mfma4(tpr[s].y, rb[4 * s + 1], D1);
+            D0 = mfma4(tpr[s].z, rb[4 * s + 2], D0);
+            D1 = mfma4(tpr[s].w, rb[4 * s + 3], D1);
+        }
+        if (c + 1 < nchunks) load_rows16(tpr, tp_row(cn));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Dl[tres + r][n] = D0[r] + D1[r];
+        __syncthreads();
+
+        // O = gamma Y + Bm Delta.
+        float db[16];   // Delta rows 16g + s, column n (also the state update's B operands)
+#pragma unroll
+        for (int s = 0; s < 16; ++s) db[s] = Dl[16 * g + s][n];
+        v4f_t O0 = {gm[0] * Y[0], gm[1] * Y[1], gm[2] * Y[2], gm[3] * Y[3]}, O1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            O0 = mfma4(bmr[s].x, db[4 * s], O0);
+            O1 = mfma4(bmr[s].y, db[4 * s + 1], O1);
+            O0 = mfma4(bmr[s].z, db[4 * s + 2], O0);
+            O1 = mfma4(bmr[s].w, db[4 * s + 3], O1);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = t0 + tres + r;
+            if (t < rows)
+                out[static_cast<int64_t>(t) * out_stride + static_cast<size_t>(h) * value_dim + j0 + n] = O0[r] + O1[r];
+        }
+        const float gl = glast;
+        if (c + 1 < nchunks) {
+            load_rows16(bmr, bm_row(cn));
+            load_gam(cn);
+        }
+
+        // S rows 32wv + 16mt + (0..15): gamma_{C-1} S0 + sum_t R[C-1][t] k_t Delta_t.
+        const float rk[16] = {rq[0].x, rq[0].y, rq[0].z, rq[0].w, rq[1].x, rq[1].y, rq[1].z, rq[1].w,
+                              rq[2].x, rq[2].y, rq[2].z, rq[2].w, rq[3].x, rq[3].y, rq[3].z, rq[3].w};
+        v4f_t A0 = {0.f, 0.f, 0.f, 0.f}, A1 = A0;
+        const int m0 = 32 * wv + n;
+        float ka[16], kb[16];
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            ka[s] = Ks[16 * g + s][m0];
+            kb[s] = Ks[16 * g + s][m0 + 16];
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            A0 = mfma4(rk[s] * ka[s], db[s], A0);
+            A1 = mfma4(rk[s] * kb[s], db[s], A1);
+        }
+        if (c + 1 < nchunks) load_rows16(rq, rr_row(cn));
+        float sn[2][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sn[0][r] = __builtin_fmaf(gl, sC[0][r], A0[r]);
+            sn[1][r] = __builtin_fmaf(gl, sC[1][r], A1[r]);
+        }
+        __syncthreads();  // every wave is done reading Sl, Ks, Dl of this chunk
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) Sl[32 * wv + 16 * mt + 4 * g + r][n] = sn[mt][r];
+        __syncthreads();
+    }
+
+    for (int e = threadIdx.x; e < kDK * kNB; e += kThreads)
+        Sg[static_cast<size_t>(e / kNB) * value_dim + e % kNB] = Sl[e / kNB][e % kNB];
+}
+
+}  // namespace
+}  // namespace qk
+
+using namespace qk;
+
+extern "C" {
+
+size_t qwen_gdn_recurrent_chunked_workspace_bytes(int rows, int value_heads) {
+    if (rows <= 0 || value_heads <= 0) return 0;
+    return static_cast<size_t>((rows + kC - 1) / kC) * value_heads * kWsFloats * sizeof(float);
+}
+
+int qwen_gdn_recurrent_chunked(float* state, const float* q, const float* k, const float* v, const float* beta,
+                               const float* decay, float* out, int rows, int key_heads, int value_heads,
+                               int key_dim, int value_dim, int64_t qkv_stride, int64_t out_stride, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+    const bool chunked = key_dim == kDK && value_dim > 0 && value_dim % kNB == 0 && aligned16(q) && aligned16(k) &&
+                         aligned16(workspace) && qkv_stride % 4 == 0 && rows > 0 && key_heads > 0 &&
+                         value_heads > 0;
+    if (!chunked)  // shapes outside the chunked kernels: the token loop, no workspace
+        return qwen_gdn_recurrent_rows(state, q, k, v, beta, decay, out, rows, key_heads, value_heads, key_dim,
+                                       value_dim, qkv_stride, out_stride, stream);
+    QK_REQUIRE(state && v && beta && decay && out, "gdn_recurrent_chunked: null pointer");
+    QK_REQUIRE(rows == 1 || (qkv_stride > 0 && out_stride > 0), "gdn_recurrent_chunked: non-positive row stride");
+    const size_t need = qwen_gdn_recurrent_chunked_workspace_bytes(rows, value_heads);
+    QK_REQUIRE(workspace_bytes >= need, "gdn_recurrent_chunked: workspace of %zu bytes, %zu needed", workspace_bytes,
+               need);
+    const hipStream_t s = as_stream(stream);
+    const int nchunks = (rows + kC - 1) / kC;
+    float* ws = static_cast<float*>(workspace);
+    gdn_chunk_prep<<<dim3(nchunks, value_heads), kThreads, 0, s>>>(q, k, beta, decay, ws, rows, key_heads, value_heads,
+                                                                   qkv_stride);
+    gdn_chunk_state<<<(value_dim / kNB) * value_heads, kThreads, 0, s>>>(state, q, k, v, ws, out, rows, key_heads,
+                                                                         value_heads, value_dim, qkv_stride,
+                                                                         out_stride);
+    return check_launch("gdn_recurrent_chunked");
+}
+
+}  // extern "C"

@@ -63,6 +63,8 @@ SIGNATURES: dict[str, list] = {
     "qwen_gdn_gate_values_rows": [_P] * 6 + [_I, _I, _P],
     "qwen_gdn_recurrent_step": [_P] * 7 + [_I, _I, _I, _I, _P],
     "qwen_gdn_recurrent_rows": [_P] * 7 + [_I, _I, _I, _I, _I, _I64, _I64, _P],
+    "qwen_gdn_recurrent_chunked_workspace_bytes": [_I, _I],
+    "qwen_gdn_recurrent_chunked": [_P] * 7 + [_I, _I, _I, _I, _I, _I64, _I64, _P, ctypes.c_size_t, _P],
     "qwen_attn_split_qg": [_P, _P, _P, _I, _I, _P],
     "qwen_attn_scores": [_P, _P, _P, _I, _I, _I, _I, _P],
     "qwen_attn_softmax": [_P, _I, _I, _P],
@@ -93,7 +95,8 @@ SIGNATURES: dict[str, list] = {
 }
 
 _RESTYPES = {"qwen_last_error": ctypes.c_char_p, "qwen_status_name": ctypes.c_char_p,
-             "qwen_attn_decode_workspace_bytes": ctypes.c_size_t}
+             "qwen_attn_decode_workspace_bytes": ctypes.c_size_t,
+             "qwen_gdn_recurrent_chunked_workspace_bytes": ctypes.c_size_t}
 
 _lib = None
 

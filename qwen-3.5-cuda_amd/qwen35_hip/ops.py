@@ -270,6 +270,34 @@ def gdn_recurrent_rows(state, qkv, beta, decay, key_heads, value_heads, key_dim,
     return out
 
 
+def gdn_recurrent_chunked(state, qkv, beta, decay, key_heads, value_heads, key_dim, value_dim, out=None,
+                          workspace=None, stream=None):
+    """qwen_gdn_recurrent_rows' chunked form (prefill): same arguments; `workspace` a
+    uint8 device tensor of at least the required bytes (allocated here if None)."""
+    _dev(state, qkv, beta, decay, dtype=torch.float32)
+    rows, stride = qkv.shape
+    kd = key_heads * key_dim
+    if stride < 2 * kd + value_heads * value_dim:
+        raise ValueError("qkv rows too short for q | k | v")
+    if state.numel() != value_heads * key_dim * value_dim:
+        raise ValueError("state shape does not match the head sizes")
+    _same((rows, value_heads), beta, decay)
+    out = torch.empty((rows, value_heads * value_dim), dtype=torch.float32, device=qkv.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    _same((rows, value_heads * value_dim), out)
+    need = load().qwen_gdn_recurrent_chunked_workspace_bytes(rows, value_heads)
+    if workspace is None:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=qkv.device)
+    _dev(workspace, dtype=torch.uint8)
+    base = qkv.data_ptr()
+    check(load().qwen_gdn_recurrent_chunked(_p(state), ctypes.c_void_p(base), ctypes.c_void_p(base + 4 * kd),
+                                            ctypes.c_void_p(base + 8 * kd), _p(beta), _p(decay), _p(out), rows,
+                                            key_heads, value_heads, key_dim, value_dim, stride,
+                                            value_heads * value_dim, _p(workspace), workspace.numel(),
+                                            _stream(stream)))
+    return out
+
+
 # ------------------------------------------------------------------ attention core (decode)
 def attn_split_qg(qg, heads, dim, stream=None):
     _dev(qg, dtype=torch.float32)

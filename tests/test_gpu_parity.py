@@ -406,6 +406,15 @@ def test_gdn_recurrent_rows(oracle, kh, vh, dk, dv, rows):
     # Oracle token by token, keeping each readout's condition scale sum_i |q_i| |S_ij|:
     # out_j is a dot product that can cancel (a strongly decayed head reads ~1e-4 from
     # terms ~4e-3), so its fp32 error is bounded relative to that scale, not to |out_j|.
+    _check_gdn_recurrence(oracle, qkv, beta, decay, state, out, host(ds), kh, vh, dk, dv)
+
+
+def _check_gdn_recurrence(oracle, qkv, beta, decay, state, out, new_state, kh, vh, dk, dv):
+    """The oracle token by token, keeping each readout's condition scale
+    sum_i |q_i| |S_ij|: out_j is a dot product that can cancel (a strongly decayed
+    head reads ~1e-4 from terms ~4e-3), so its fp32 error is bounded relative to
+    that scale, not to |out_j|."""
+    rows = qkv.shape[0]
     ref_state = state.copy()
     kd = kh * dk
     ref = np.empty_like(out)
@@ -420,7 +429,62 @@ def test_gdn_recurrent_rows(oracle, kh, vh, dk, dv, rows):
     err = np.abs(out.astype(np.float64) - ref) / np.maximum(np.abs(ref.astype(np.float64)), scale)
     worst = np.unravel_index(int(np.argmax(err)), err.shape)
     assert err[worst] <= 1e-5, f"out rel err {err[worst]:.3e} at {worst}: got {out[worst]!r} ref {ref[worst]!r}"
-    assert_f32_close(host(ds), ref_state, group=dv, what="state")
+    assert_f32_close(new_state, ref_state, group=dv, what="state")
+
+
+@pytest.mark.parametrize("rows,gates", [(1, "normal"), (63, "normal"), (64, "normal"), (200, "normal"),
+                                        (700, "normal"), (150, "fast_decay"), (150, "beta_one")])
+def test_gdn_recurrent_chunked(oracle, rows, gates):
+    """The chunked prefill form against the oracle's token loop at the Qwen3.5 GDN shape:
+    partial last chunks, several chunks, decays that underflow to zero inside a chunk
+    (the ratios are running products), and beta near 1 (the triangular solve's
+    largest off-diagonal terms)."""
+    kh, vh, dk, dv = 16, 32, 128, 128
+    r = rng(rows * 3 + len(gates))
+    qkv, b, alpha, a, dt, state = _gdn_inputs(r, rows, kh, vh, dk, dv)
+    if gates == "fast_decay":
+        alpha = (alpha + 60.0).astype(F32)      # softplus ~ 60: decay exp(a * 60) underflows for a < -1.6
+    elif gates == "beta_one":
+        b = (b + 12.0).astype(F32)
+    beta, decay = oracle.gdn_gate_values_rows(b, alpha, a, dt)
+    if gates == "fast_decay":
+        assert (decay == 0).any() and (decay > 0).any()
+    ds = dev(state)
+    ws = torch.empty(ops.load().qwen_gdn_recurrent_chunked_workspace_bytes(rows, vh), dtype=torch.uint8,
+                     device="cuda")
+    out = host(ops.gdn_recurrent_chunked(ds, dev(qkv), dev(beta), dev(decay), kh, vh, dk, dv, workspace=ws))
+    _check_gdn_recurrence(oracle, qkv, beta, decay, state, out, host(ds), kh, vh, dk, dv)
+
+
+def test_gdn_recurrent_chunked_long_and_fallback(oracle):
+    """2048 tokens (32 chunks): the chunked form and the token-loop kernel both
+    against the oracle's token loop (condition-scale bar: late outputs of strongly
+    decayed heads are tiny cancelling sums); key dim 64 (not chunked) runs the
+    token loop; a short workspace is rejected."""
+    from qwen35_hip._lib import QwenError
+
+    kh, vh, dk, dv, T = 16, 32, 128, 128, 2048
+    r = rng(4096)
+    qkv, b, alpha, a, dt, state = _gdn_inputs(r, T, kh, vh, dk, dv)
+    beta, decay = oracle.gdn_gate_values_rows(b, alpha, a, dt)
+    s1, s2, dq = dev(state), dev(state), dev(qkv)
+    o1 = host(ops.gdn_recurrent_chunked(s1, dq, dev(beta), dev(decay), kh, vh, dk, dv))
+    o2 = host(ops.gdn_recurrent_rows(s2, dq, dev(beta), dev(decay), kh, vh, dk, dv))
+    _check_gdn_recurrence(oracle, qkv, beta, decay, state, o1, host(s1), kh, vh, dk, dv)
+    _check_gdn_recurrence(oracle, qkv, beta, decay, state, o2, host(s2), kh, vh, dk, dv)
+    kh, vh, dk, dv, T = 4, 8, 64, 64, 9
+    qkv, b, alpha, a, dt, state = _gdn_inputs(r, T, kh, vh, dk, dv)
+    beta, decay = ops.gdn_gate_values_rows(dev(b), dev(alpha), dev(a), dev(dt))
+    s1, s2, dq = dev(state), dev(state), dev(qkv)
+    o1 = host(ops.gdn_recurrent_chunked(s1, dq, beta, decay, kh, vh, dk, dv,
+                                        workspace=torch.empty(16, dtype=torch.uint8, device="cuda")))
+    o2 = host(ops.gdn_recurrent_rows(s2, dq, beta, decay, kh, vh, dk, dv))
+    assert_bits_equal(o1, o2, "fallback")
+    with pytest.raises(QwenError):
+        qkv, b, alpha, a, dt, state = _gdn_inputs(r, 100, 16, 32, 128, 128)
+        beta, decay = ops.gdn_gate_values_rows(dev(b), dev(alpha), dev(a), dev(dt))
+        ops.gdn_recurrent_chunked(dev(state), dev(qkv), beta, decay, 16, 32, 128, 128,
+                                  workspace=torch.empty(1024, dtype=torch.uint8, device="cuda"))
 
 
 def test_gdn_recurrent_rows_equals_steps():
