@@ -561,6 +561,8 @@ def main() -> int:
     ap.add_argument("--no-next", action="store_true", help="skip the decode GEMV measurements (not part of the step)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
     ap.add_argument("--json-out", default="", help="also write the JSON line to this file")
+    ap.add_argument("--profile-gemv", type=int, default=0, metavar="N",
+                    help="also run the LM-head GEMV N times after the step (counter runs)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="also run the reference copy of BYTES (read) + BYTES (write) three times, for "
                          "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE against known traffic")
@@ -615,6 +617,14 @@ def main() -> int:
         value = bytes_step / (ms_per_step * 1e-3) / 1e9
         print(f"# step: {ms_per_step * 1e3:.1f} us, {value:.1f} GB/s aggregate", file=sys.stderr, flush=True)
         del graph
+
+    if args.profile_gemv:
+        lm = [k for k in build_next_rows(torch, ops, synth, host) if k.name == "gemv_lm_head_q6_k"][0]
+        f = lm.make(0)
+        for _ in range(args.profile_gemv):
+            f()
+        torch.cuda.synchronize()
+        print(f"# LM-head GEMV: {args.profile_gemv} launches", file=sys.stderr, flush=True)
 
     if args.calibrate_copy:
         n = args.calibrate_copy // 16 * 16

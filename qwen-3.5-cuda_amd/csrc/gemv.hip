@@ -28,6 +28,7 @@
 // which is the reference's sum re-associated (fp32 tolerance, not bit-exact:
 // the reference's own order depends on its launch shape).
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "capi_common.hpp"
@@ -684,16 +685,19 @@ inline bool mfma_split(int nb, int& S, int& bpw) {
     return false;
 }
 
-// Compute units of the current device (cached per device).
+// Compute units of the current device (cached per device; callers on several
+// threads may race to fill an entry, all with the same value).
 inline int device_cus() {
-    static int cus[64] = {};
+    static std::atomic<int> cus[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
+    int c = cus[dev].load(std::memory_order_relaxed);
+    if (!c) {
         int n = 0;
-        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+        c = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+        cus[dev].store(c, std::memory_order_relaxed);
     }
-    return cus[dev];
+    return c;
 }
 
 constexpr int kMfmaMaxCnt = 32;   // tiles per slot in the LDS partial-sum buffer

@@ -35,10 +35,15 @@ NAMES = [
     ("rmsnorm_rows_v4", "rmsnorm"),
     ("copy16", "copy"),
     # next rows (kernel symbols; several bench shapes can share one instantiation)
-    ("gemv_kquant<14, 4>", "gemv Q6_K, 4 units/wave (LM head)"),
-    ("gemv_kquant<12, 2>", "gemv Q4_K, 2 units/wave (GDN qkv)"),
-    ("gemv_kquant<12, 1>", "gemv Q4_K, 1 unit/wave (out proj, experts)"),
-    ("gdn_recurrent_v4", "gdn_recurrent (step and 4096-token form)"),
+    ("gemv_mfma<14, 2>", "gemv Q6_K MFMA, 2-block k-slices (LM head)"),
+    ("gemv_mfma<12, 2>", "gemv Q4_K MFMA, 2-block k-slices"),
+    ("gemv_kquant<14, 4>", "gemv Q6_K per-row, 4 units/wave"),
+    ("gemv_kquant<12, 2>", "gemv Q4_K per-row, 2 units/wave (GDN qkv)"),
+    ("gemv_kquant<12, 1>", "gemv Q4_K per-row, 1 unit/wave (out proj, experts)"),
+    ("gdn_recurrent_v4", "gdn_recurrent step (decode)"),
+    ("gdn_recurrent_g", "gdn_recurrent token loop (4096 tokens)"),
+    ("gdn_chunk_prep", "gdn_recurrent chunked: per-chunk prep"),
+    ("gdn_chunk_state", "gdn_recurrent chunked: state walk"),
     ("decode_split", "attn_decode split-K pass"),
     ("decode_combine", "attn_decode combine"),
     ("scores_kernel", "attn_scores (staged)"),
@@ -53,6 +58,8 @@ ALGORITHMIC = {
     "rmsnorm": 598016, "qk_norm_rope": 18878464, "residual_rmsnorm_bf16": 67117056, "swiglu_bf16": 100663296,
     "shared_swiglu_sigmoid_bf16": 12599296, "gdn_frontend": 268763136, "gdn_norm_gate": 201327104,
     "dequant_gather_q4_k": 76578816, "dequant_gather_q6_k": 80904192,
+    # the LM-head GEMV (bench.py next rows: Q6_K 248320 x 2048, x and y fp32)
+    "gemv Q6_K MFMA, 2-block k-slices (LM head)": 418179072,
 }
 
 
@@ -138,11 +145,11 @@ def main(argv=None) -> int:
     print(f"calibration: copy of {cal['copy_bytes_each_way']} B each way read as FETCH {cal['copy_fetch_kib']:.0f} KiB, "
           f"WRITE {cal['copy_write_kib']:.0f} KiB -> {cal['fetch_bytes_per_kib']:.1f} / {cal['write_bytes_per_kib']:.1f} "
           "bytes per counter KiB")
-    print(f"{'kernel':30s} {'fetch B':>12s} {'write B':>12s} {'total B':>12s} {'algorithmic':>12s} {'ratio':>7s}")
+    print(f"{'kernel':44s} {'fetch B':>12s} {'write B':>12s} {'total B':>12s} {'algorithmic':>12s} {'ratio':>7s}")
     for name, r in t.items():
         if name.startswith("_"):
             continue
-        print(f"{name:30s} {r['fetch_bytes']:12d} {r['write_bytes']:12d} {r['bytes_per_launch']:12d} "
+        print(f"{name[:44]:44s} {r['fetch_bytes']:12d} {r['write_bytes']:12d} {r['bytes_per_launch']:12d} "
               f"{r['algorithmic_bytes']:12d} {r['traffic_over_algorithmic']:7.3f}")
     if args.json:
         with open(args.json, "w") as f:
