@@ -347,9 +347,11 @@ def spin_cycles_per_ms(torch) -> float:
     return 2_000_000 / max(s.elapsed_time(e), 1e-3)
 
 
-def steady_state_us(torch, launches, replays: int, spin: int) -> float:
+def steady_state_us(torch, launches, replays: int, spin: int, repeats: int = 5) -> float:
     """us per launch of `launches` (one per buffer set), captured as one graph
-    and replayed; events bracket all replays on the capturing stream."""
+    and replayed; events bracket each batch of replays on the capturing stream.
+    The median over `repeats` batches is returned (single batches of a few ms
+    vary by a few percent on this box)."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -363,16 +365,18 @@ def steady_state_us(torch, launches, replays: int, spin: int) -> float:
             f()
     g.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda._sleep(spin)
-    e0.record()
-    for _ in range(replays):
-        g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / (replays * len(launches))
+    times = []
+    for _ in range(repeats):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(spin)
+        e0.record()
+        for _ in range(replays):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e3 / (replays * len(launches)))
     del g
-    return us
+    return sorted(times)[len(times) // 2]
 
 
 def n_sets(footprint: int) -> int:
@@ -690,13 +694,17 @@ def main() -> int:
     if not args.no_cpu and not args.kernels:
         threads = max(1, min(16, os.cpu_count() or 1))
         per, agg = cpu_baseline(host, kernels, threads, args.cpu_seconds)
+        # the reference's own host code is one thread: the same sample on one core
+        per1, agg1 = cpu_baseline(host, kernels, 1, args.cpu_seconds / 2)
         rows_desc = ", ".join(f"{n} {p['sample_rows']}" for n, p in per.items())
         cpu = {"value": round(agg, 3), "unit": "GB/s", "cores": threads, "kind": "port",
                "sample": ("oracle/liboracle.so (C++ restatement of the reference kernels, -O2, row-parallel "
                           "std::threads) on the first rows of each config (" + rows_desc + "), "
                           f"extrapolated to the full step; host CPU {cpu_model()}"),
                "per_kernel": {n: {"gbps": round(p["gbps"], 3), "us_per_call": round(p["us_per_call"], 1)}
-                              for n, p in per.items()}}
+                              for n, p in per.items()},
+               "single_thread": {"value": round(agg1, 3), "cores": 1,
+                                 "per_kernel": {n: {"gbps": round(p["gbps"], 3)} for n, p in per1.items()}}}
 
     next_rows = None
     if nxt:

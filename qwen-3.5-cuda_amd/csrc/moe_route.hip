@@ -10,9 +10,13 @@
 // the stream, and launches k expert GEMV chains with host-side offsets and k
 // moe_add calls with host-side weights.
 //
-// Here top-k is one wave per token row: lane L holds logits L, L+64, ...; each
-// round is a wave arg-max (value, then lower index) and the winner's lane marks
-// it used; the softmax over the picks runs in the first k lanes. Routing stays
+// Here top-k is one wave per token row. Lane L holds the VPL consecutive logits
+// VPL*L .. VPL*L+VPL-1 and sorts them once, larger value first and lower index
+// first among equal values. Each round is then one wave max over the lanes'
+// heads; among lanes whose head equals it the lowest lane wins (a ballot), which
+// is the lowest index because lanes own increasing index ranges; the winner
+// lane shifts its list. The softmax over the picks runs in the first k lanes.
+// Routing stays
 // on the device: qwen_moe_expert_matmul (gemv.hip) reads the expert ids, and
 // qwen_moe_weighted_sum_rows reads the weights, so no host round trip is needed.
 #include <algorithm>
@@ -28,7 +32,7 @@ constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
 constexpr int kMaxExperts = 16 * kWave;  // logits per row held in VGPRs (16 per lane)
 
-// Wave max / min with DPP inside 16-lane rows, permlane swaps across rows.
+// Wave max with DPP inside 16-lane rows, permlane swaps across rows.
 __device__ __forceinline__ float wave_maxf(float v) {
     v = fmaxf(v, dpp_move<0xB1>(v));
     v = fmaxf(v, dpp_move<0x4E>(v));
@@ -40,24 +44,9 @@ __device__ __forceinline__ float wave_maxf(float v) {
     return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
 
-__device__ __forceinline__ int wave_mini(int v) {
-    v = min(v, __float_as_int(dpp_move<0xB1>(__int_as_float(v))));
-    v = min(v, __float_as_int(dpp_move<0x4E>(__int_as_float(v))));
-    v = min(v, __float_as_int(dpp_move<0x141>(__int_as_float(v))));
-    v = min(v, __float_as_int(dpp_move<0x140>(__int_as_float(v))));
-    auto p = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
-    v = min(static_cast<int>(p[0]), static_cast<int>(p[1]));
-    p = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
-    return min(static_cast<int>(p[0]), static_cast<int>(p[1]));
-}
-
-// Arg-max of (v, i) pairs over the wave: larger value wins, then lower index
-// (the max value first, then the smallest index among the lanes holding it).
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
-    const float m = wave_maxf(v);
-    i = wave_mini(v == m ? i : 0x7fffffff);
-    v = m;
-}
+// (v, i) before (w, j): larger value, then lower index (a total order on a
+// row's finite logits, so the sorted order is unique).
+__device__ __forceinline__ bool ahead(float v, int i, float w, int j) { return v > w || (v == w && i < j); }
 
 template <int VPL>
 __global__ __launch_bounds__(kBlock) void topk_rows_kernel(const float* __restrict__ x, int32_t* __restrict__ idx,
@@ -66,13 +55,27 @@ __global__ __launch_bounds__(kBlock) void topk_rows_kernel(const float* __restri
     if (row >= rows) return;  // wave-uniform
     const int lane = threadIdx.x & 63;
     const float* xr = x + static_cast<size_t>(row) * n;
+    const int i0 = VPL * lane;
     float v[VPL];
+    int vi[VPL];
+    if (VPL % 4 == 0 && n == VPL * kWave && (reinterpret_cast<uintptr_t>(xr) & 15) == 0) {
+#pragma unroll
+        for (int s = 0; s < VPL; s += 4) {
+            const float4 q = ld4(xr + i0 + s);
+            v[s] = q.x;
+            v[s + 1] = q.y;
+            v[s + 2] = q.z;
+            v[s + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < VPL; ++s) v[s] = i0 + s < n ? xr[i0 + s] : -INFINITY;
+    }
     bool finite = true;
 #pragma unroll
     for (int s = 0; s < VPL; ++s) {
-        const int i = lane + s * kWave;
-        v[s] = i < n ? xr[i] : -INFINITY;
-        if (i < n && !isfinite(v[s])) finite = false;
+        vi[s] = i0 + s;
+        if (i0 + s < n && !isfinite(v[s])) finite = false;
     }
     int32_t* ir = idx + static_cast<size_t>(row) * k;
     float* wr = w + static_cast<size_t>(row) * k;
@@ -83,25 +86,41 @@ __global__ __launch_bounds__(kBlock) void topk_rows_kernel(const float* __restri
         }
         return;
     }
-    unsigned used = 0;      // bit s: logit lane + 64 s already picked
+    // Odd-even transposition sort of the lane's list. Padding (-inf, index >= n)
+    // sorts last and is never picked: k <= n and every logit is finite.
+#pragma unroll
+    for (int r = 0; r < VPL; ++r) {
+#pragma unroll
+        for (int s = r & 1; s + 1 < VPL; s += 2) {
+            if (ahead(v[s + 1], vi[s + 1], v[s], vi[s])) {
+                const float tv = v[s];
+                const int ti = vi[s];
+                v[s] = v[s + 1];
+                vi[s] = vi[s + 1];
+                v[s + 1] = tv;
+                vi[s + 1] = ti;
+            }
+        }
+    }
     float pick_v = 0.f;     // lane j < k: value of pick j
     int pick_i = -1;
     for (int j = 0; j < k; ++j) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
+        const float m = wave_maxf(v[0]);
+        const uint64_t tied = __ballot(v[0] == m);
+        const int wl = __builtin_ctzll(tied);            // lowest lane holding the max
+        const int wi = __builtin_amdgcn_readlane(vi[0], wl);
+        if (lane == wl) {
 #pragma unroll
-        for (int s = 0; s < VPL; ++s) {
-            const int i = lane + s * kWave;
-            if (i < n && !((used >> s) & 1u) && (v[s] > bv || bi == 0x7fffffff)) {
-                bv = v[s];
-                bi = i;
+            for (int s = 0; s + 1 < VPL; ++s) {
+                v[s] = v[s + 1];
+                vi[s] = vi[s + 1];
             }
+            v[VPL - 1] = -INFINITY;
+            vi[VPL - 1] = 0x7fffffff;
         }
-        wave_argmax(bv, bi);
-        if ((bi & (kWave - 1)) == lane) used |= 1u << (bi / kWave);
         if (lane == j) {
-            pick_v = bv;
-            pick_i = bi;
+            pick_v = m;
+            pick_i = wi;
         }
     }
     // softmax over the picks (lanes < k); the first pick is the largest

@@ -635,6 +635,25 @@ def test_moe_topk_rows(oracle, rows, n, k):
     assert_f32_close(gw, rw, what="weights")
 
 
+@pytest.mark.parametrize("n,k,offset", [(256, 8, 0), (256, 8, 1), (1024, 64, 0), (200, 16, 0)])
+def test_moe_topk_rows_many_ties(oracle, n, k, offset):
+    """Logits on a coarse grid (a few distinct values per row), so the top k is
+    decided by the lower-index rule between lanes and inside each lane's list;
+    offset 1 starts every row 4 bytes past a 16-byte boundary (scalar loads)."""
+    rows = 512
+    r = rng(n * k + offset)
+    x = (np.round(r.standard_normal((rows, n)) * 2.0) / 4.0).astype(F32)
+    x[0, :] = 1.0                     # every logit tied
+    x[1, ::7] = 9.0                   # a tie of many at the top, spread over lanes
+    buf = dev(np.concatenate([np.zeros(offset, F32), x.ravel()]))
+    xin = buf[offset:].view(rows, n)
+    ri, rw = oracle.moe_topk_rows(x, k)
+    gi, gw = ops.moe_topk_rows(xin, k)
+    gi, gw = host(gi), host(gw)
+    assert np.array_equal(gi, ri), np.argwhere(gi != ri)[:5]
+    assert_f32_close(gw, rw, what="weights")
+
+
 def test_moe_add_and_weighted_sum(oracle):
     r = rng(8)
     rows, k, dim = 64, 8, 2048
