@@ -14,9 +14,9 @@
 //
 // The separate entry points are kept as drop-ins. The fused decode path is a
 // split-K pass plus a combine: workgroup (split, kv head) takes the G = H/Hkv
-// (8 or 16) query heads that share kv head and 16 or 8 keys (4 lanes per
-// (head, key) for the scores, thread = value column for P.V), so every key and value row of
-// the cache is read from HBM once per call; it writes per-split softmax
+// (8 or 16) query heads that share kv head and 32 or 16 keys (thread = (head,
+// key) for the scores, thread = value column for P.V), so every key and value
+// row of the cache is read from HBM once per call; it writes per-split softmax
 // statistics (max, sum of exp) and unnormalised P.V rows to a caller-provided
 // workspace, and the combine rescales the splits to the global max, divides by
 // the total and applies the sigmoid gate.
@@ -129,17 +129,20 @@ __global__ __launch_bounds__(kBlock) void values_kernel(const float* __restrict_
 }
 
 // ---------------------------------------------------------------- fused decode
-// Workgroup (split, kv head): G query heads x L keys; T = 4 lanes per (head,
-// key) pair take interleaved float4 chunks of the 256-wide dot product, so
-// the (G * L * 4)-thread workgroup keeps 4 waves per SIMD busy at Qwen3.5's
-// shape instead of one. All of the split's loads go out before the first wait
-// (a wait on one load waits for all loads issued before it). Keys go through
-// LDS (rows padded to kKeyStride floats: the 4 lanes of a pair and the L keys
-// of a head hit different banks); values stay in VGPRs, thread (half, column)
-// holding its column of one half of the keys; the two halves of P.V meet in
+// Workgroup (split, kv head): G query heads x L keys; kPairLanes lanes per
+// (head, key) pair take interleaved float4 chunks of the 256-wide dot product.
+// At Qwen3.5's shapes one lane per pair and G * L = 256 threads measured
+// fastest (32 keys per split for 8 heads per kv head, 16 for 16): larger
+// splits halve the partial rows the combine reads, and the scores' LDS reads
+// are broadcasts (a wave reads 2 query rows) or 16-byte rows of distinct keys.
+// All of the split's loads go out before the first wait (a wait on one load
+// waits for all loads issued before it). Keys go through LDS (rows padded to
+// kKeyStride floats so the keys of a wave hit different banks); values stay
+// in VGPRs, thread (group, column) holding its column of one group of keys;
+// groups of P.V (when the workgroup has more threads than columns) meet in
 // LDS. Workspace: acc [Hkv][splits][G][D], then m and l [Hkv][splits][G].
 constexpr int kKeyStride = kMaxDim + 4;
-constexpr int kPairLanes = 4;
+constexpr int kPairLanes = 1;
 
 template <int G, int L>
 __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
@@ -158,7 +161,7 @@ __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
     __shared__ float4 q_lds[G][D4];
     __shared__ __align__(16) float k_lds[L][kKeyStride];
     __shared__ __align__(16) float p_lds[G][L];
-    __shared__ float acc_lds[HALVES > 1 ? HALVES - 1 : 1][G][D];
+    __shared__ float acc_lds[HALVES > 1 ? HALVES - 1 : 1][HALVES > 1 ? G : 1][HALVES > 1 ? D : 1];
     const int split = blockIdx.x, kv = blockIdx.y;
     const int tid = threadIdx.x;
     const int t0 = split * L;
@@ -215,7 +218,9 @@ __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
     const float sc = valid ? dot * scale : -INFINITY;
     // max and sum over the L keys of head hh: 4*L consecutive lanes
     constexpr int HL = L * kPairLanes;
-    float m = sc;
+    float m = sc;  // equal across the kPairLanes lanes of a pair already
+    if constexpr (kPairLanes < 2 && HL >= 2) m = fmaxf(m, dpp_move<0xB1>(m));
+    if constexpr (kPairLanes < 4 && HL >= 4) m = fmaxf(m, dpp_move<0x4E>(m));
     if constexpr (HL >= 8) m = fmaxf(m, dpp_move<0x141>(m));
     if constexpr (HL >= 16) m = fmaxf(m, dpp_move<0x140>(m));
     if constexpr (HL >= 32) m = fmaxf(m, __shfl_xor(m, 16));
@@ -332,9 +337,9 @@ __global__ __launch_bounds__(kBlock) void decode_combine(const float* __restrict
     }
 }
 
-// Keys per split of the fused path: 16 for 8 query heads per kv head, 8 for 16
-// (512-thread workgroups either way).
-int split_keys(int group) { return group == 8 ? 16 : 8; }
+// Keys per split of the fused path: 32 for 8 query heads per kv head, 16 for
+// 16 (256-thread workgroups either way).
+int split_keys(int group) { return group == 8 ? 32 : 16; }
 
 int fused_splits(int heads, int kv_heads, int n_keys) {
     const int L = split_keys(heads / kv_heads);
@@ -451,11 +456,11 @@ int qwen_attn_decode(const float* q, const float* k_cache, const float* v_cache,
         const dim3 grid(splits, kv_heads);
         const float scale = host_rsqrt(dim);
         if (g == 8)
-            decode_split<8, 16><<<grid, 8 * 16 * kPairLanes, 0, s>>>(q, k_cache, v_cache, acc, m, l, kv_heads, n_keys,
+            decode_split<8, 32><<<grid, 8 * 32 * kPairLanes, 0, s>>>(q, k_cache, v_cache, acc, m, l, kv_heads, n_keys,
                                                                     splits, scale);
         else
-            decode_split<16, 8><<<grid, 16 * 8 * kPairLanes, 0, s>>>(q, k_cache, v_cache, acc, m, l, kv_heads,
-                                                                    n_keys, splits, scale);
+            decode_split<16, 16><<<grid, 16 * 16 * kPairLanes, 0, s>>>(q, k_cache, v_cache, acc, m, l, kv_heads,
+                                                                      n_keys, splits, scale);
         int st = check_launch("attn_decode");
         if (st) return st;
         decode_combine<<<dim3(heads, (dim + kCombineCols - 1) / kCombineCols), kBlock, 0, s>>>(acc, m, l, gate, out, g,

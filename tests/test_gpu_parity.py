@@ -590,7 +590,9 @@ def test_attn_stages(oracle, pos):
 @pytest.mark.parametrize("heads,kv,dim,pos,gated", [
     (16, 2, 256, 0, True), (16, 2, 256, 31, True), (16, 2, 256, 32, False), (16, 2, 256, 33, True),
     (16, 2, 256, 1000, True), (16, 2, 256, 4095, True), (8, 2, 128, 200, True), (32, 2, 64, 77, False),
-    (6, 2, 256, 50, True), (16, 2, 100, 45, True), (4, 1, 512, 20, True)])
+    (6, 2, 256, 50, True), (16, 2, 100, 45, True), (4, 1, 512, 20, True),
+    (32, 2, 256, 15, True), (32, 2, 256, 16, False), (32, 2, 256, 2047, True), (16, 1, 256, 700, True),
+    (8, 1, 256, 63, True)])
 def test_attn_decode(oracle, heads, kv, dim, pos, gated):
     """Fused decode at the Qwen3.5 attention shape across split boundaries (32 keys per
     split), groups of 4 and 16, and the staged fallback (group 3, dim 100, dim 512)."""
