@@ -346,6 +346,40 @@ def test_dequantize_row(oracle, kind, cols, row):
     assert_bits_equal(got, oracle.dequant_span(table, t, row * cols, cols), f"{kind} row {row}")
 
 
+@pytest.mark.parametrize("kind", ["Q4_0", "Q5_0", "Q8_0", "Q4_K", "Q5_K", "Q6_K"])
+def test_reference_quant_fixtures_on_gpu(kind):
+    """The reference's own block fixtures (tests/kernel_tests.cu:116-223, frozen in
+    tests/golden/reference_fixtures.json) through every GPU dequant path: rows of
+    8 copies of the block via dequantize_row, the gather, and the GEMV with one-hot
+    x (which reads exactly one weight per row: w_j = (d*sc)*q - dmin*m, bit for bit);
+    for Q4_K and Q6_K also at a row count that takes the int8-MFMA GEMV."""
+    import json
+    from pathlib import Path
+
+    fx = json.loads((Path(__file__).resolve().parent / "golden" / "reference_fixtures.json").read_text())["quant"][kind]
+    blk = np.frombuffer(bytes.fromhex(fx["bytes_hex"]), np.uint8)
+    exp_row = np.tile(np.asarray(fx["expected"], F32), 8)
+    cols = exp_row.size
+
+    def table(rows):
+        return dev(np.tile(blk, 8 * rows))
+
+    tab = table(4)
+    got = host(ops.dequantize_row(tab, kind, 4 * cols, 2, cols))
+    assert np.array_equal(got, exp_row), np.argwhere(got != exp_row)[:5]
+    ids = dev(np.array([0, 3, 1, 2, 2], np.int32))
+    got = host(ops.dequant_gather_rows(tab, kind, 4 * cols, ids, cols))
+    assert np.array_equal(got, np.tile(exp_row, (5, 1)))
+    sizes = [64] + ({"Q4_K": [65536], "Q6_K": [16384]}.get(kind, []) if cols == 2048 else [])
+    for M in sizes:
+        w = table(M)
+        for j in (0, 1, 37, cols // 2 + 5, cols - 1):
+            x = np.zeros(cols, F32)
+            x[j] = 1.0
+            y = host(ops.matmul_dispatch(w, kind, M * cols, dev(x), M, cols))
+            assert np.array_equal(y, np.full(M, exp_row[j], F32)), (M, j, y[:4], exp_row[j])
+
+
 # ------------------------------------------------------------------ GDN gates + recurrent state
 def _gdn_inputs(r, rows, kh, vh, dk, dv, extra=0):
     """Front-end-like rows (unit-norm k, q scaled by dk^-1/2, v ~ N(0,1)), gates from raw
