@@ -53,15 +53,20 @@ __device__ __forceinline__ v4f_t mfma4(float a, float b, v4f_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// 32 consecutive floats of `row` starting at dim `d0` (zeros for a padding token).
-__device__ __forceinline__ void load32(const float* __restrict__ row, int d0, bool valid, float (&r)[32]) {
+// The 32 dims of a 128-dim row that lane group g supplies as MFMA k-slots:
+// r[4j + c] = row[16j + 4g + c]. The four groups of a 16-lane column read 64
+// contiguous bytes per load (the same token's row), so a wave's load touches
+// 16 half-lines instead of 64 scattered 16-byte pieces. Zeros for a padding
+// token; `row` is always a real row (callers clamp the token), so the loads
+// are unconditional and the zeros are selected afterwards.
+__device__ __forceinline__ void load32(const float* __restrict__ row, int g, bool valid, float (&r)[32]) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const float4 v = valid ? ld4(row + d0 + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
-        r[4 * j] = v.x;
-        r[4 * j + 1] = v.y;
-        r[4 * j + 2] = v.z;
-        r[4 * j + 3] = v.w;
+        const float4 v = ld4(row + 16 * j + 4 * g);
+        r[4 * j] = valid ? v.x : 0.0f;
+        r[4 * j + 1] = valid ? v.y : 0.0f;
+        r[4 * j + 2] = valid ? v.z : 0.0f;
+        r[4 * j + 3] = valid ? v.w : 0.0f;
     }
 }
 
@@ -101,18 +106,18 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
         const int tok = t0 + 16 * wv + n;
         const int64_t row = static_cast<int64_t>(min(tok, rows - 1)) * qkv_stride + src * kDK;
         float kr[32], qr[32];
-        load32(k + row, 32 * g, tok < rows, kr);
-        load32(q + row, 32 * g, tok < rows, qr);
+        load32(k + row, g, tok < rows, kr);
+        load32(q + row, g, tok < rows, qr);
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-            *reinterpret_cast<float4*>(&Kl[16 * wv + n][32 * g + 4 * j]) =
+            *reinterpret_cast<float4*>(&Kl[16 * wv + n][16 * j + 4 * g]) =
                 make_float4(kr[4 * j], kr[4 * j + 1], kr[4 * j + 2], kr[4 * j + 3]);
         __syncthreads();
         auto tile = [&](const float (&a)[32], int mt, int nt, float (*D)[kLdA]) {
             v4f_t acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float4 b = *reinterpret_cast<const float4*>(&Kl[16 * nt + n][32 * g + 4 * j]);
+                const float4 b = *reinterpret_cast<const float4*>(&Kl[16 * nt + n][16 * j + 4 * g]);
                 acc[0] = mfma4(a[4 * j], b.x, acc[0]);
                 acc[1] = mfma4(a[4 * j + 1], b.y, acc[1]);
                 acc[2] = mfma4(a[4 * j + 2], b.z, acc[2]);
@@ -131,7 +136,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
             float a[32];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float4 v = *reinterpret_cast<const float4*>(&Kl[16 * mt + n][32 * g + 4 * j]);
+                const float4 v = *reinterpret_cast<const float4*>(&Kl[16 * mt + n][16 * j + 4 * g]);
                 a[4 * j] = v.x;
                 a[4 * j + 1] = v.y;
                 a[4 * j + 2] = v.z;
@@ -245,10 +250,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
                                                             const float* __restrict__ ws, float* __restrict__ out,
                                                             int rows, int key_heads, int value_heads, int value_dim,
                                                             int64_t qkv_stride, int64_t out_stride) {
-    __shared__ float Ks[kC][kDK + 5];       // the chunk's K rows (odd stride: column reads hit distinct banks)
-    __shared__ float Rv[kC][kNB + 1];
-    __shared__ float Dl[kC][kNB + 1];
-    __shared__ float Sl[kDK][kNB + 1];      // this block's 128 x 16 state
+    // The tiles a lane reads as MFMA operands along their K dimension are stored
+    // transposed ([column][row]), so those operands are consecutive floats: one
+    // 16-byte LDS read per 4 operands and one wait before the products.
+    __shared__ float Ks[kC][kDK + 5];                 // the chunk's K rows (odd stride: column reads hit distinct banks)
+    __shared__ __align__(16) float RvT[kNB][kC + 4];  // V - gamma X, [column][token]
+    __shared__ __align__(16) float DlT[kNB][kC + 4];  // Delta, [column][token]
+    __shared__ __align__(16) float SlT[kNB][kDK + 4]; // this block's 128 x 16 state, [column][key]
     // Workgroup i runs on XCD i % 8 (round-robin dispatch). With the value
     // heads a multiple of 8, head h's column blocks all get ids i with
     // i % 8 == h % 8, so the chunk data of a head (K, Q, T', Bm, V) is fetched
@@ -271,7 +279,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     float* Sg = S + static_cast<size_t>(h) * kDK * value_dim + j0;
 
     for (int e = threadIdx.x; e < kDK * kNB; e += kThreads)
-        Sl[e / kNB][e % kNB] = Sg[static_cast<size_t>(e / kNB) * value_dim + e % kNB];
+        SlT[e % kNB][e / kNB] = Sg[static_cast<size_t>(e / kNB) * value_dim + e % kNB];
     __syncthreads();
 
     // Per-chunk inputs of this lane, each reloaded for the next chunk as soon as
@@ -283,18 +291,37 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     float kA[32], qA[32], vv[4], gm[4], glast;
     float4 tpr[4], bmr[4], rq[4];
     auto chunk_base = [&](int c) { return ws + (static_cast<size_t>(c) * value_heads + h) * kWsFloats; };
+    // Padding tokens of the last chunk read the last real row and are not
+    // zeroed: the prep kernel gives them beta 0 and decay 1, so their rows and
+    // columns of T' are zero, their Delta is exactly 0 (0 times finite values)
+    // and they add nothing to the state; their outputs are not stored. Keeping
+    // the loaded values raw also keeps the prefetches asynchronous (a select on
+    // a loaded value would wait for the load right away).
+    // k-slot map of every product here: step 4j + c of a 4-wide group g takes
+    // element 16j + 4g + c of the contracted dimension (dims of K / Q, tokens
+    // of T', Bm and R), so each 4 lanes of a row read 64 contiguous bytes.
     auto load_kq = [&](int c) {
-        const int t = c * kC + tok;
-        const int64_t row = static_cast<int64_t>(min(t, rows - 1)) * qkv_stride + src * kDK;
-        load32(k + row, 32 * g, t < rows, kA);
-        load32(q + row, 32 * g, t < rows, qA);
+        const int t = min(c * kC + tok, rows - 1);
+        const float* kr = k + static_cast<int64_t>(t) * qkv_stride + src * kDK + 4 * g;
+        const float* qr = q + static_cast<int64_t>(t) * qkv_stride + src * kDK + 4 * g;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float4 a = ld4(kr + 16 * j), b = ld4(qr + 16 * j);
+            kA[4 * j] = a.x;
+            kA[4 * j + 1] = a.y;
+            kA[4 * j + 2] = a.z;
+            kA[4 * j + 3] = a.w;
+            qA[4 * j] = b.x;
+            qA[4 * j + 1] = b.y;
+            qA[4 * j + 2] = b.z;
+            qA[4 * j + 3] = b.w;
+        }
     };
     auto load_v = [&](int c) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int t = c * kC + tres + r;
-            vv[r] = t < rows ? v[static_cast<int64_t>(t) * qkv_stride + static_cast<size_t>(h) * value_dim + j0 + n]
-                             : 0.0f;
+            const int t = min(c * kC + tres + r, rows - 1);
+            vv[r] = v[static_cast<int64_t>(t) * qkv_stride + static_cast<size_t>(h) * value_dim + j0 + n];
         }
     };
     auto load_gam = [&](int c) {
@@ -303,39 +330,66 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         gm[1] = gv.y;
         gm[2] = gv.z;
         gm[3] = gv.w;
-        glast = chunk_base(c)[2 * kC * kC + kC - 1];
+        // gamma_{C-1} through a vector load: its address is wave-uniform, and as
+        // a scalar load it would share lgkmcnt with the LDS traffic, so every
+        // LDS wait would also wait for it (scalar loads return out of order).
+        // lane & (rows >> 31) is 0 (rows > 0) but not known to the compiler to
+        // be uniform, which keeps the load on the vector path.
+        glast = chunk_base(c)[2 * kC * kC + kC - 1 + (lane & (rows >> 31))];
     };
-    auto load_rows16 = [&](float4 (&dst)[4], const float* src16) {
+    // elements 16s + 4g .. 16s + 4g + 3 (s < 4) of a 64-long row: p = row + 4g
+    auto load_rows16 = [&](float4 (&dst)[4], const float* p) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) dst[s] = ld4(src16 + 4 * s);
+        for (int s = 0; s < 4; ++s) dst[s] = ld4(p + 16 * s);
     };
-    // T' and Bm rows 16wv + n, columns 16g .. 16g+15; R[C-1][16g .. 16g+15].
-    auto tp_row = [&](int c) { return chunk_base(c) + (16 * wv + n) * kC + 16 * g; };
-    auto bm_row = [&](int c) { return chunk_base(c) + kC * kC + (16 * wv + n) * kC + 16 * g; };
-    auto rr_row = [&](int c) { return chunk_base(c) + 2 * kC * kC + kC + 16 * g; };
+    // the same 16 elements of an LDS row (p = row + 4g), as 4 x 16-byte reads
+    auto lds16 = [](float (&dst)[16], const float* p) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float4 t = *reinterpret_cast<const float4*>(p + 16 * s);
+            dst[4 * s] = t.x;
+            dst[4 * s + 1] = t.y;
+            dst[4 * s + 2] = t.z;
+            dst[4 * s + 3] = t.w;
+        }
+    };
+    // T' and Bm rows 16wv + n and R[C-1], at this lane's k-slot columns.
+    auto tp_row = [&](int c) { return chunk_base(c) + (16 * wv + n) * kC + 4 * g; };
+    auto bm_row = [&](int c) { return chunk_base(c) + kC * kC + (16 * wv + n) * kC + 4 * g; };
+    auto rr_row = [&](int c) { return chunk_base(c) + 2 * kC * kC + kC + 4 * g; };
+    // the loop's load order (the wait counts at its head then line up)
     load_kq(0);
     load_v(0);
-    load_gam(0);
     load_rows16(tpr, tp_row(0));
     load_rows16(bmr, bm_row(0));
+    load_gam(0);
     load_rows16(rq, rr_row(0));
 
     for (int c = 0; c < nchunks; ++c) {
         const int t0 = c * kC;
+        // Inputs of chunk cn are prefetched during this chunk (the last chunk
+        // reloads its own; unconditional loads keep the wait counts exact).
         const int cn = min(c + 1, nchunks - 1);
 
-        // S0 as the B operand (rows 32g + s, column n) and at this wave's rows of
-        // the state update's result tiles (32wv + 16mt + 4g + r).
-        float sB[32], sC[2][4];
+        // S0 as the B operand (rows 16j + 4g + c, column n) and at this wave's
+        // rows of the state update's result tiles (32wv + 16mt + 4g + r).
+        float sB[32];
+        float4 sC[2];
 #pragma unroll
-        for (int s = 0; s < 32; ++s) sB[s] = Sl[32 * g + s][n];
+        for (int j = 0; j < 8; ++j) {
+            const float4 t = *reinterpret_cast<const float4*>(&SlT[n][16 * j + 4 * g]);
+            sB[4 * j] = t.x;
+            sB[4 * j + 1] = t.y;
+            sB[4 * j + 2] = t.z;
+            sB[4 * j + 3] = t.w;
+        }
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sC[mt][r] = Sl[32 * wv + 16 * mt + 4 * g + r][n];
+        for (int mt = 0; mt < 2; ++mt) sC[mt] = *reinterpret_cast<const float4*>(&SlT[n][32 * wv + 16 * mt + 4 * g]);
 
 #pragma unroll
-        for (int s = 0; s < 32; ++s) Ks[tok][32 * g + s] = kA[s];
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) Ks[tok][16 * j + 4 * g + c] = kA[4 * j + c];
         v4f_t xa[4], ya[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) xa[u] = ya[u] = v4f_t{0.f, 0.f, 0.f, 0.f};
@@ -346,18 +400,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         }
         const v4f_t X = (xa[0] + xa[1]) + (xa[2] + xa[3]);
         const v4f_t Y = (ya[0] + ya[1]) + (ya[2] + ya[3]);
-        if (c + 1 < nchunks) load_kq(cn);
+        load_kq(cn);
 
         // Result rows: tokens 16wv + 4g + r, column n.
-#pragma unroll
-        for (int r = 0; r < 4; ++r) Rv[tres + r][n] = vv[r] - gm[r] * X[r];
-        if (c + 1 < nchunks) load_v(cn);
+        *reinterpret_cast<float4*>(&RvT[n][tres]) =
+            make_float4(vv[0] - gm[0] * X[0], vv[1] - gm[1] * X[1], vv[2] - gm[2] * X[2], vv[3] - gm[3] * X[3]);
+        load_v(cn);
         __syncthreads();
 
         // Delta = T' Rv (this wave's 16 rows; K = the chunk's 64 tokens).
         float rb[16];
-#pragma unroll
-        for (int s = 0; s < 16; ++s) rb[s] = Rv[16 * g + s][n];
+        lds16(rb, &RvT[n][4 * g]);
         v4f_t D0 = {0.f, 0.f, 0.f, 0.f}, D1 = D0;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -366,15 +419,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
             D0 = mfma4(tpr[s].z, rb[4 * s + 2], D0);
             D1 = mfma4(tpr[s].w, rb[4 * s + 3], D1);
         }
-        if (c + 1 < nchunks) load_rows16(tpr, tp_row(cn));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) Dl[tres + r][n] = D0[r] + D1[r];
+        load_rows16(tpr, tp_row(cn));
+        *reinterpret_cast<float4*>(&DlT[n][tres]) = make_float4(D0[0] + D1[0], D0[1] + D1[1], D0[2] + D1[2],
+                                                                 D0[3] + D1[3]);
         __syncthreads();
 
         // O = gamma Y + Bm Delta.
-        float db[16];   // Delta rows 16g + s, column n (also the state update's B operands)
-#pragma unroll
-        for (int s = 0; s < 16; ++s) db[s] = Dl[16 * g + s][n];
+        float db[16];   // Delta rows 16s + 4g + c, column n (also the state update's B operands)
+        lds16(db, &DlT[n][4 * g]);
         v4f_t O0 = {gm[0] * Y[0], gm[1] * Y[1], gm[2] * Y[2], gm[3] * Y[3]}, O1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -389,13 +441,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
             if (t < rows)
                 out[static_cast<int64_t>(t) * out_stride + static_cast<size_t>(h) * value_dim + j0 + n] = O0[r] + O1[r];
         }
-        const float gl = glast;
-        if (c + 1 < nchunks) {
-            load_rows16(bmr, bm_row(cn));
-            load_gam(cn);
-        }
+        load_rows16(bmr, bm_row(cn));
 
-        // S rows 32wv + 16mt + (0..15): gamma_{C-1} S0 + sum_t R[C-1][t] k_t Delta_t.
+        // S rows 32wv + 16mt + (0..15): gamma_{C-1} S0 + sum_t R[C-1][t] k_t Delta_t
+        // (step 4s + c: token 16s + 4g + c).
         const float rk[16] = {rq[0].x, rq[0].y, rq[0].z, rq[0].w, rq[1].x, rq[1].y, rq[1].z, rq[1].w,
                               rq[2].x, rq[2].y, rq[2].z, rq[2].w, rq[3].x, rq[3].y, rq[3].z, rq[3].w};
         v4f_t A0 = {0.f, 0.f, 0.f, 0.f}, A1 = A0;
@@ -403,31 +452,30 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         float ka[16], kb[16];
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
-            ka[s] = Ks[16 * g + s][m0];
-            kb[s] = Ks[16 * g + s][m0 + 16];
+            const int t = 16 * (s >> 2) + 4 * g + (s & 3);
+            ka[s] = Ks[t][m0];
+            kb[s] = Ks[t][m0 + 16];
         }
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
             A0 = mfma4(rk[s] * ka[s], db[s], A0);
             A1 = mfma4(rk[s] * kb[s], db[s], A1);
         }
-        if (c + 1 < nchunks) load_rows16(rq, rr_row(cn));
-        float sn[2][4];
+        float4 sn[2];
+        sn[0] = make_float4(__builtin_fmaf(glast, sC[0].x, A0[0]), __builtin_fmaf(glast, sC[0].y, A0[1]),
+                            __builtin_fmaf(glast, sC[0].z, A0[2]), __builtin_fmaf(glast, sC[0].w, A0[3]));
+        sn[1] = make_float4(__builtin_fmaf(glast, sC[1].x, A1[0]), __builtin_fmaf(glast, sC[1].y, A1[1]),
+                            __builtin_fmaf(glast, sC[1].z, A1[2]), __builtin_fmaf(glast, sC[1].w, A1[3]));
+        load_gam(cn);      // gamma and R[C-1] are dead for this chunk from here on
+        load_rows16(rq, rr_row(cn));
+        __syncthreads();  // every wave is done reading SlT, Ks, DlT of this chunk
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            sn[0][r] = __builtin_fmaf(gl, sC[0][r], A0[r]);
-            sn[1][r] = __builtin_fmaf(gl, sC[1][r], A1[r]);
-        }
-        __syncthreads();  // every wave is done reading Sl, Ks, Dl of this chunk
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) Sl[32 * wv + 16 * mt + 4 * g + r][n] = sn[mt][r];
+        for (int mt = 0; mt < 2; ++mt) *reinterpret_cast<float4*>(&SlT[n][32 * wv + 16 * mt + 4 * g]) = sn[mt];
         __syncthreads();
     }
 
     for (int e = threadIdx.x; e < kDK * kNB; e += kThreads)
-        Sg[static_cast<size_t>(e / kNB) * value_dim + e % kNB] = Sl[e / kNB][e % kNB];
+        Sg[static_cast<size_t>(e / kNB) * value_dim + e % kNB] = SlT[e % kNB][e / kNB];
 }
 
 }  // namespace
