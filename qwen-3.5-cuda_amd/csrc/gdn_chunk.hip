@@ -253,7 +253,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     // The tiles a lane reads as MFMA operands along their K dimension are stored
     // transposed ([column][row]), so those operands are consecutive floats: one
     // 16-byte LDS read per 4 operands and one wait before the products.
-    __shared__ float Ks[kC][kDK + 5];                 // the chunk's K rows (odd stride: column reads hit distinct banks)
+    __shared__ __align__(16) float KsT[kDK][kC + 4];  // the chunk's K^T, [key][token]
     __shared__ __align__(16) float RvT[kNB][kC + 4];  // V - gamma X, [column][token]
     __shared__ __align__(16) float DlT[kNB][kC + 4];  // Delta, [column][token]
     __shared__ __align__(16) float SlT[kNB][kDK + 4]; // this block's 128 x 16 state, [column][key]
@@ -389,7 +389,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
         for (int j = 0; j < 8; ++j)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) Ks[tok][16 * j + 4 * g + c] = kA[4 * j + c];
+            for (int c = 0; c < 4; ++c) KsT[16 * j + 4 * g + c][tok] = kA[4 * j + c];
         v4f_t xa[4], ya[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) xa[u] = ya[u] = v4f_t{0.f, 0.f, 0.f, 0.f};
@@ -450,12 +450,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         v4f_t A0 = {0.f, 0.f, 0.f, 0.f}, A1 = A0;
         const int m0 = 32 * wv + n;
         float ka[16], kb[16];
-#pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            const int t = 16 * (s >> 2) + 4 * g + (s & 3);
-            ka[s] = Ks[t][m0];
-            kb[s] = Ks[t][m0 + 16];
-        }
+        lds16(ka, &KsT[m0][4 * g]);
+        lds16(kb, &KsT[m0 + 16][4 * g]);
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
             A0 = mfma4(rk[s] * ka[s], db[s], A0);
@@ -468,7 +464,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
                             __builtin_fmaf(glast, sC[1].z, A1[2]), __builtin_fmaf(glast, sC[1].w, A1[3]));
         load_gam(cn);      // gamma and R[C-1] are dead for this chunk from here on
         load_rows16(rq, rr_row(cn));
-        __syncthreads();  // every wave is done reading SlT, Ks, DlT of this chunk
+        __syncthreads();  // every wave is done reading SlT, KsT, DlT of this chunk
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) *reinterpret_cast<float4*>(&SlT[n][32 * wv + 16 * mt + 4 * g]) = sn[mt];
         __syncthreads();
