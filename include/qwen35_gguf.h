@@ -86,9 +86,11 @@ int qwen_gguf_get_meta_key(const qwen_gguf* g, uint64_t index, const char** key,
  * on disk (device_ptr NULL), as the reference does for Qwen3.5's MTP blocks.
  * Reads the file through pinned double-buffered staging with the copies
  * enqueued on `stream` (NULL: an internal non-blocking stream) and
- * synchronises before returning. QWEN_STATUS_OUT_OF_MEMORY if the arena or
- * the pinned staging cannot be allocated, QWEN_STATUS_IO_ERROR if the file
- * cannot be re-read or a copy fails; either way nothing stays loaded.
+ * synchronises before returning; if pinned memory cannot be allocated it
+ * falls back to synchronous copies from the mapped file.
+ * QWEN_STATUS_OUT_OF_MEMORY if the arena cannot be allocated,
+ * QWEN_STATUS_IO_ERROR if the file cannot be re-read or a copy fails; either
+ * way nothing stays loaded.
  * ref: src/loader_gguf.cpp:322-381 (load_tensors_to_gpu) */
 int qwen_gguf_load(qwen_gguf* g, int base_layer_count, void* stream);
 

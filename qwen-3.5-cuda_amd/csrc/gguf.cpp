@@ -352,7 +352,6 @@ bool GgufLoader::load_tensors_to_gpu(int base_layer_count, hipStream_t stream) {
     for (int b = 0; b < 2 && ok; ++b)
         ok = hipHostMalloc(&stage[b], kStageBytes, hipHostMallocDefault) == hipSuccess &&
              hipEventCreateWithFlags(&done[b], hipEventDisableTiming) == hipSuccess;
-    const bool staged = ok;
 
     if (ok) {
         m.advise_sequential();
@@ -383,7 +382,21 @@ bool GgufLoader::load_tensors_to_gpu(int base_layer_count, hipStream_t stream) {
                 }
             }
         }
-        if (ok) ok = hipStreamSynchronize(s) == hipSuccess;
+        // Also on failure: copies already enqueued read the staging buffers and
+        // write the arena, so they must finish before either is freed.
+        const bool synced = hipStreamSynchronize(s) == hipSuccess;
+        ok = ok && synced;
+    } else {
+        // No pinned staging (pinned memory exhausted): synchronous copies
+        // straight from the mapped file, as the reference uploads.
+        (void)hipGetLastError();
+        ok = true;
+        uint8_t* arena = static_cast<uint8_t*>(arena_);
+        for (size_t k = 0; k < sel.size() && ok; ++k) {
+            const QuantTensor& t = tensors_[sel[k]];
+            ok = hipMemcpy(arena + slot[k], m.data() + payload_offset_ + t.offset, t.size_bytes,
+                           hipMemcpyHostToDevice) == hipSuccess;
+        }
     }
     for (int b = 0; b < 2; ++b) {
         if (done[b]) (void)hipEventDestroy(done[b]);
@@ -393,9 +406,7 @@ bool GgufLoader::load_tensors_to_gpu(int base_layer_count, hipStream_t stream) {
     if (!ok) {
         const hipError_t err = hipGetLastError();
         unload_gpu();
-        return fail(staged ? std::string("tensor upload failed: ") + hipGetErrorString(err)
-                           : std::string("pinned staging allocation failed"),
-                    !staged);
+        return fail(std::string("tensor upload failed: ") + hipGetErrorString(err), false);
     }
     for (size_t k = 0; k < sel.size(); ++k) tensors_[sel[k]].device_ptr = static_cast<uint8_t*>(arena_) + slot[k];
     total_vram_bytes_ = data_bytes;
