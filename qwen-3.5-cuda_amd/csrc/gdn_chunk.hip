@@ -78,7 +78,7 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
     __shared__ __align__(16) float Kl[kC][kDK + 4];   // the chunk's K rows
     __shared__ __align__(16) float G[kC][kLdA];    // K K^T, then A (strictly lower)
     __shared__ __align__(16) float Pm[kC][kLdA];   // Q K^T, then T
-    __shared__ float sb[kC], sd[kC];
+    __shared__ __align__(16) float sb[kC], sd[kC];
     const int c = blockIdx.x, h = blockIdx.y;
     const int t0 = c * kC;
     const int src = h % key_heads;
@@ -150,11 +150,25 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
     // Rows 16wv .. 16wv+15 per wave, lane i = column i: R[t][i] as a running
     // product (the factor up to the wave's first row rebuilt from the decays,
     // the same multiplication sequence as one pass over all rows), A and Bm.
+    // The decays are read once into registers (broadcast LDS reads) and the
+    // products run over all 64 positions with the factors outside a lane's
+    // range replaced by 1.0 (exact), so the chains are plain multiplies
+    // without an LDS round trip per step.
     {
         const int i = lane;
         const int ta = 16 * wv;
+        float dall[kC];
+#pragma unroll
+        for (int t = 0; t < kC; t += 4) {
+            const float4 v4 = *reinterpret_cast<const float4*>(&sd[t]);
+            dall[t] = v4.x;
+            dall[t + 1] = v4.y;
+            dall[t + 2] = v4.z;
+            dall[t + 3] = v4.w;
+        }
         float r = 1.0f;
-        for (int t = i + 1; t < ta; ++t) r *= sd[t];
+#pragma unroll
+        for (int t = 1; t < kC - 16; ++t) r *= (t > i && t < ta) ? dall[t] : 1.0f;
         float dv16[16], bv16[16], gv[16], pv[16];
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
@@ -171,12 +185,11 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
             Bm[t * kC + i] = t >= i ? pv[u] * r : 0.0f;
         }
         if (wv == 3) rr[i] = r;  // R[C-1][i]
-        if (wv == 0 && lane < 16) {  // gamma_t = d_0 * ... * d_t, in order
+        if (wv == 0) {  // gamma_t = d_0 * ... * d_t in order, lane t
             float gm = 1.0f;
-            for (int t = 0; t < kC; ++t) {
-                gm *= sd[t];
-                if (t % 16 == lane) gam[t] = gm;
-            }
+#pragma unroll
+            for (int t = 0; t < kC; ++t) gm *= t <= lane ? dall[t] : 1.0f;
+            gam[lane] = gm;
         }
     }
     __syncthreads();
