@@ -347,11 +347,19 @@ def spin_cycles_per_ms(torch) -> float:
     return 2_000_000 / max(s.elapsed_time(e), 1e-3)
 
 
+GRAPH_LAUNCHES = 64  # kernel launches per captured graph in the steady-state timing
+
+
 def steady_state_us(torch, launches, replays: int, spin: int, repeats: int = 5) -> float:
-    """us per launch of `launches` (one per buffer set), captured as one graph
-    and replayed; events bracket each batch of replays on the capturing stream.
-    The median over `repeats` batches is returned (single batches of a few ms
-    vary by a few percent on this box)."""
+    """us per launch of `launches` (one per buffer set, cycled through the sets
+    until the graph holds at least GRAPH_LAUNCHES launches, so the gap between
+    two graph launches is spread over that many kernels rather than over a
+    handful), captured as one graph and replayed; events bracket each batch of
+    replays on the capturing stream. The median over `repeats` batches is
+    returned (single batches of a few ms vary by a few percent on this box)."""
+    cycle = max(1, -(-GRAPH_LAUNCHES // len(launches)))
+    launches = list(launches) * cycle
+    replays = max(1, -(-replays // cycle))
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
