@@ -334,6 +334,32 @@ def build_next_rows(torch, ops, synth, host):
                nb, nb, mk_ex)
     k.gemv = {"type": 12, "table": t[:8 * 512 * 8 * 144], "M": 8 * 512, "K": 2048, "x": x8.cpu().numpy()}
     ks.append(k)
+
+    # A GDN layer's four input projections of one token (layer_gdn.cpp:83-86: qkv 8192, z 4096,
+    # beta 32 and alpha 32 rows of 2048, Q4_K): the reference's four matmul_dispatch calls
+    # against one matmul_dispatch_multi call (one launch). No CPU figure (it would be the
+    # GEMV rows above again).
+    proj = [(8192, 30), (4096, 31), (32, 32), (32, 33)]
+    ptabs = [torch.from_numpy(synth.q4k_table(M, 2048, seed_tensor=s)).to(dev) for M, s in proj]
+    xp = torch.from_numpy(rng.standard_normal(2048).astype(np.float32)).to(dev)
+    ys = [torch.empty(M, dtype=torch.float32, device=dev) for M, _ in proj]
+    nb = sum(M * 8 * 144 + 4 * M for M, _ in proj) + 4 * 2048
+    for name, multi in (("gdn_in_proj_4_calls", False), ("gdn_in_proj_multi", True)):
+        def mk_p(i, multi=multi):
+            tt = ptabs if i == 0 else [tb.clone() for tb in ptabs]
+            if multi:
+                jobs = [(tb, "Q4_K", M * 2048, M, 0, y) for tb, (M, _), y in zip(tt, proj, ys)]
+                return lambda: ops.matmul_dispatch_multi(jobs, xp, 2048)
+
+            def run():
+                for tb, (M, _), y in zip(tt, proj, ys):
+                    ops.matmul_dispatch(tb, "Q4_K", M * 2048, xp, M, 2048, out=y)
+            return run
+        desc = ("GDN input projections qkv/z/beta/alpha, Q4_K [8192|4096|32|32 x 2048], " +
+                ("one matmul_dispatch_multi launch" if multi else "four matmul_dispatch calls (the reference's)"))
+        k = Kernel(name, desc, nb, nb, mk_p)
+        k.no_cpu = True
+        ks.append(k)
     return ks
 
 
@@ -719,9 +745,10 @@ def main() -> int:
         cpu_next = {}
         if not args.no_cpu:
             threads = max(1, min(16, os.cpu_count() or 1))
-            cpu_next, _ = cpu_baseline(host, nxt, threads, args.cpu_seconds / 3,
+            nxt_cpu = [k for k in nxt if not getattr(k, "no_cpu", False)]
+            cpu_next, _ = cpu_baseline(host, nxt_cpu, threads, args.cpu_seconds / 3,
                                        gemv={k.name: getattr(k, "gemv", None) or getattr(k, "gdn", None) or
-                                             getattr(k, "attn", None) or k.route for k in nxt})
+                                             getattr(k, "attn", None) or k.route for k in nxt_cpu})
         next_rows = {
             k.name: {"config": k.config, "bytes": k.bytes, "us_per_call": round(k.us, 3),
                      "gbps": round(k.bytes / k.us / 1e3, 1), "frac_peak": round(k.bytes / k.us / 1e3 / PEAK_GBPS, 4),

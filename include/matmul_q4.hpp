@@ -30,6 +30,19 @@ void moe_expert_matmul(const QuantTensor& weight, uint64_t expert_stride, int n_
                        int n_sel, const float* x, int64_t x_stride, float* y, int M, int K,
                        hipStream_t stream = nullptr);
 
+// Several GEMVs of one x (K elements) in as few launches as possible: y_j =
+// W_j x for each job, the results of n matmul_dispatch calls (the reference
+// makes these calls one after another on one input, src/layer_gdn.cpp:83-86,
+// src/layer_attn.cpp:85-87, src/layer_moe.cpp:145-147). Throws as
+// matmul_dispatch, naming the first job that fails; nothing runs then.
+struct GemvJob {
+    const QuantTensor* weight;
+    float* y;
+    int M;
+    uint64_t element_offset = 0;
+};
+void matmul_dispatch_multi(const GemvJob* jobs, int n, const float* x, int K, hipStream_t stream = nullptr);
+
 // out[i] = element (row * cols + i) of `tensor`.  ref: include/matmul_q4.hpp:24-30
 void dequantize_row(const QuantTensor& tensor, float* out, int row, int cols, hipStream_t stream = nullptr);
 

@@ -324,6 +324,28 @@ int qwen_matmul_type_supported(int type);
 int qwen_matmul_dispatch(const void* weight, int type, uint64_t num_elements, const float* x,
                          float* y, int M, int K, uint64_t element_offset, void* stream);
 
+/* One projection of qwen_matmul_dispatch_multi: the arguments of one
+ * qwen_matmul_dispatch call except x, K and the stream. */
+typedef struct qwen_gemv_desc {
+    const void* weight;       /* device GGML tensor */
+    int type;                 /* GGML type id */
+    int M;                    /* rows */
+    uint64_t num_elements;    /* elements of the tensor */
+    uint64_t element_offset;  /* first element of row 0 */
+    float* y;                 /* output, fp32 [M] */
+} qwen_gemv_desc;
+
+/* n GEMVs of the same x (K elements): y_j = W_j x for each descriptor, with the
+ * results of n qwen_matmul_dispatch calls. The Q4_K / Q6_K projections of one
+ * type run in one launch (up to 8 per launch); other types and shapes take
+ * qwen_matmul_dispatch's kernels one by one. Every descriptor is validated
+ * first, in order, with qwen_matmul_dispatch's statuses and messages (naming
+ * the descriptor); nothing is launched if one fails. 0 <= n <= 64.
+ * The reference issues these as consecutive matmul_dispatch calls on one
+ * input: src/layer_gdn.cpp:83-86 (qkv, z, beta, alpha), src/layer_attn.cpp:85-87
+ * (q|gate, k, v), src/layer_moe.cpp:98 (router), :145-147 (shared expert gate logit, gate, up). */
+int qwen_matmul_dispatch_multi(const qwen_gemv_desc* descs, int n, const float* x, int K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -209,9 +209,9 @@ __device__ __forceinline__ bool select_expert(const Experts& ex, int M, int64_t&
 // starts at block ub0 + row*nb + 8s; when nb | 8, group = 8/nb rows (P) and
 // unit u starts at block ub0 + 8u. A wave owns groups g0 .. g0+R-1.
 template <int TYPE, int R>
-__global__ __launch_bounds__(kGemvBlock) void gemv_kquant(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                          float* __restrict__ y, int M, int nb, uint64_t ub0,
-                                                          int groups, uint64_t tensor_bytes, Experts ex) {
+__device__ __forceinline__ void gemv_kquant_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                 float* __restrict__ y, int M, int nb, uint64_t ub0, int groups,
+                                                 uint64_t tensor_bytes, const Experts& ex) {
     constexpr int BB = KQuant<TYPE>::kBlockBytes;
     constexpr int UB = 8 * BB;             // unit bytes
     constexpr int CPU = UB / 16;           // 16-byte chunks per unit
@@ -291,6 +291,36 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant(const uint8_t* __restr
             if (lane % gl == 0 && g0 + u < groups && row < M) y[row] = t;
         }
     }
+}
+
+template <int TYPE, int R>
+__global__ __launch_bounds__(kGemvBlock) void gemv_kquant(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                          float* __restrict__ y, int M, int nb, uint64_t ub0,
+                                                          int groups, uint64_t tensor_bytes, Experts ex) {
+    gemv_kquant_body<TYPE, R>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex);
+}
+
+// Several matrices of one type against the same x (qwen_matmul_dispatch_multi):
+// launch row blockIdx.y runs matrix d[blockIdx.y]; the grid is sized for the
+// largest, and workgroups past a smaller matrix's rows return at once.
+constexpr int kMultiMax = 8;
+struct GemvMat {
+    const uint8_t* w;
+    float* y;
+    uint64_t ub0;           // first block of row 0
+    uint64_t tensor_bytes;  // bytes of the whole tensor
+    int M;
+    int groups;
+};
+struct GemvMulti {
+    GemvMat d[kMultiMax];
+};
+
+template <int TYPE, int R>
+__global__ __launch_bounds__(kGemvBlock) void gemv_kquant_multi(const float* __restrict__ x, int nb, GemvMulti mu) {
+    const GemvMat& m = mu.d[blockIdx.y];
+    if (static_cast<int64_t>(blockIdx.x) * kGemvWaves * R >= m.groups) return;   // uniform per workgroup
+    gemv_kquant_body<TYPE, R>(m.w, x, m.y, m.M, nb, m.ub0, m.groups, m.tensor_bytes, Experts{nullptr, 0, 0, 0});
 }
 
 // Generic path (any supported type and shape): one wave per row, element-wise
@@ -803,6 +833,44 @@ int launch_gemv(const uint8_t* w, int type, uint64_t num_elements, const float* 
     return check_launch(what);
 }
 
+
+// Whether a plain GEMV of this matrix takes the per-row kernel (the same
+// conditions as launch_gemv without expert selection).
+bool kquant_rowpath(const uint8_t* w, int type, uint64_t num_elements, const float* x, int M, int K,
+                    uint64_t element_offset) {
+    if (type != kQ4_K && type != kQ6_K) return false;
+    const int nb = K / 256;
+    const uint64_t tensor_bytes = (num_elements / 256) * static_cast<uint64_t>(block_bytes(type));
+    int S = 0, bpw = 0;
+    if (K % 256 == 0 && mfma_split(nb, S, bpw) && element_offset % 256 == 0 && mfma_large(type, M)) return false;
+    const bool shape_ok = K % 256 == 0 && (nb % 8 == 0 || 8 % nb == 0) && element_offset % 256 == 0 &&
+                          num_elements % 256 == 0 && tensor_bytes % 16 == 0;
+    const bool aligned = aligned16(w) && aligned16(x) && (type == kQ4_K || (element_offset / 256) % 8 == 0);
+    return shape_ok && aligned;
+}
+
+template <int TYPE, int R>
+void launch_multi_r(const GemvMulti& mu, int n, const float* x, int nb, hipStream_t s) {
+    constexpr int CPU = KQuant<TYPE>::kBlockBytes * 8 / 16;
+    const size_t lds = static_cast<size_t>(kGemvWaves) * R * CPU * 16;
+    int64_t gx = 1;
+    for (int j = 0; j < n; ++j) gx = std::max<int64_t>(gx, blocks_for((mu.d[j].groups + R - 1) / R, kGemvWaves));
+    gemv_kquant_multi<TYPE, R><<<dim3(static_cast<unsigned>(gx), n), kGemvBlock, lds, s>>>(x, nb, mu);
+}
+
+// Up to kMultiMax matrices of one K-quant type, each on the per-row path.
+template <int TYPE>
+void launch_multi(const GemvMulti& mu, int n, const float* x, int nb, hipStream_t s) {
+    int64_t all = 0;   // units per wave as dispatch_kquant picks them, over all matrices
+    for (int j = 0; j < n; ++j) all += mu.d[j].groups;
+    if (all >= 4 * 4096)
+        launch_multi_r<TYPE, 4>(mu, n, x, nb, s);
+    else if (all >= 2 * 4096)
+        launch_multi_r<TYPE, 2>(mu, n, x, nb, s);
+    else
+        launch_multi_r<TYPE, 1>(mu, n, x, nb, s);
+}
+
 }  // namespace
 }  // namespace qk
 
@@ -841,6 +909,64 @@ int qwen_moe_expert_matmul(const void* weight, int type, uint64_t num_elements, 
     return launch_gemv(static_cast<const uint8_t*>(weight), type, num_elements, x, y, M, K, 0,
                        Experts{idx, n_experts, expert_stride, x_stride}, n_sel, as_stream(stream),
                        "moe_expert_matmul");
+}
+
+
+int qwen_matmul_dispatch_multi(const qwen_gemv_desc* descs, int n, const float* x, int K, void* stream) {
+    QK_REQUIRE(n >= 0 && n <= 64, "matmul_dispatch_multi: n = %d outside [0, 64]", n);
+    if (n == 0) return ok();
+    QK_REQUIRE(descs && x, "matmul_dispatch_multi: null pointer");
+    // Validate everything first (qwen_matmul_dispatch's checks, in its order).
+    for (int j = 0; j < n; ++j) {
+        const qwen_gemv_desc& e = descs[j];
+        if (!e.weight) return fail(QWEN_STATUS_INVALID_ARGUMENT, "descriptor %d: tensor is not loaded", j);
+        if (!type_supported(e.type))
+            return fail(QWEN_STATUS_UNSUPPORTED_TYPE, "descriptor %d: unsupported GGML type %d", j, e.type);
+        if (e.M <= 0 || K <= 0 || e.element_offset > e.num_elements ||
+            static_cast<uint64_t>(e.M) * static_cast<uint64_t>(K) > e.num_elements - e.element_offset)
+            return fail(QWEN_STATUS_OUT_OF_RANGE, "descriptor %d: GEMV shape exceeds tensor (M=%d, K=%d)", j, e.M, K);
+        QK_REQUIRE(e.y, "matmul_dispatch_multi: descriptor %d has a null output", j);
+    }
+    const hipStream_t s = as_stream(stream);
+    const int nb = K / 256;
+    for (const int type : {static_cast<int>(kQ4_K), static_cast<int>(kQ6_K)}) {
+        GemvMulti mu{};
+        int m = 0;
+        for (int j = 0; j < n; ++j) {
+            const qwen_gemv_desc& e = descs[j];
+            const auto* w = static_cast<const uint8_t*>(e.weight);
+            if (e.type != type || !kquant_rowpath(w, e.type, e.num_elements, x, e.M, K, e.element_offset)) continue;
+            GemvMat& g = mu.d[m++];
+            g.w = w;
+            g.y = e.y;
+            g.ub0 = e.element_offset / 256;
+            g.tensor_bytes = (e.num_elements / 256) * static_cast<uint64_t>(block_bytes(type));
+            g.M = e.M;
+            g.groups = nb >= 8 ? e.M : (e.M + 8 / nb - 1) / (8 / nb);
+            if (m == kMultiMax) {
+                if (type == kQ4_K) launch_multi<kQ4_K>(mu, m, x, nb, s);
+                else launch_multi<kQ6_K>(mu, m, x, nb, s);
+                m = 0;
+            }
+        }
+        if (m > 0) {
+            if (type == kQ4_K) launch_multi<kQ4_K>(mu, m, x, nb, s);
+            else launch_multi<kQ6_K>(mu, m, x, nb, s);
+        }
+        const int st = check_launch("matmul_dispatch_multi");
+        if (st) return st;
+    }
+    // Everything else: the single-matrix kernels.
+    for (int j = 0; j < n; ++j) {
+        const qwen_gemv_desc& e = descs[j];
+        const auto* w = static_cast<const uint8_t*>(e.weight);
+        if ((e.type == kQ4_K || e.type == kQ6_K) && kquant_rowpath(w, e.type, e.num_elements, x, e.M, K, e.element_offset))
+            continue;
+        const int st = launch_gemv(w, e.type, e.num_elements, x, e.y, e.M, K, e.element_offset,
+                                   Experts{nullptr, 0, 0, 0}, 1, s, "matmul_dispatch_multi");
+        if (st) return st;
+    }
+    return ok();
 }
 
 }  // extern "C"

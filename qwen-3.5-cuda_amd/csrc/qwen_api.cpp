@@ -2,6 +2,7 @@
 // names and signatures (with hipStream_t), throwing std::runtime_error where the
 // reference throws. Each function forwards to its qwen_* C entry point.
 #include <stdexcept>
+#include <vector>
 #include <string>
 
 #include "gdn.hpp"
@@ -227,6 +228,24 @@ void moe_expert_matmul(const QuantTensor& w, uint64_t expert_stride, int n_exper
         throw std::runtime_error("unsupported GGML type for tensor '" + w.name + "'");
     if (status == QWEN_STATUS_OUT_OF_RANGE) throw std::runtime_error("GEMV shape exceeds tensor '" + w.name + "'");
     check(status);
+}
+
+void matmul_dispatch_multi(const GemvJob* jobs, int n, const float* x, int K, hipStream_t stream) {
+    if (n <= 0) return;
+    std::vector<qwen_gemv_desc> d(static_cast<size_t>(n));
+    for (int j = 0; j < n; ++j) {
+        const QuantTensor& w = *jobs[j].weight;
+        // matmul_dispatch's checks and messages per job (src/cuda/matmul_q4.cu:187-195)
+        if (!w.device_ptr) throw std::runtime_error("tensor '" + w.name + "' is not loaded");
+        if (!matmul_type_supported(w.type)) throw std::runtime_error("unsupported GGML type for tensor '" + w.name + "'");
+        const uint64_t need = static_cast<uint64_t>(jobs[j].M) * static_cast<uint64_t>(K);
+        if (jobs[j].M <= 0 || K <= 0 || jobs[j].element_offset > w.num_elements ||
+            need > w.num_elements - jobs[j].element_offset)
+            throw std::runtime_error("GEMV shape exceeds tensor '" + w.name + "'");
+        d[j] = qwen_gemv_desc{w.device_ptr, static_cast<int>(w.type), jobs[j].M, w.num_elements,
+                              jobs[j].element_offset, jobs[j].y};
+    }
+    check(qwen_matmul_dispatch_multi(d.data(), n, x, K, st(stream)));
 }
 
 void dequantize_row(const QuantTensor& tensor, float* out, int row, int cols, hipStream_t stream) {

@@ -805,6 +805,51 @@ def test_matmul_dispatch_reuses_x_and_checks_shapes(oracle):
         ops.matmul_dispatch(dw, 3, rows * K, dx, rows, K)  # Q4_1: no path
 
 
+@pytest.mark.parametrize("K", [2048, 4096, 512])
+def test_matmul_dispatch_multi_equals_single_calls(oracle, K):
+    """A layer's input projections in one call (qwen_matmul_dispatch_multi): the
+    GDN layer's qkv / z / beta / alpha shapes, a row offset, a second type, a
+    non-K-quant tensor (its own kernel) and more same-type matrices than one
+    launch takes; every output bit-equal to its own matmul_dispatch call (the
+    same per-row kernel, whose per-row sums do not depend on the launch), and
+    one of them against the oracle."""
+    import ggml_blocks
+
+    r = rng(K)
+    specs = [("Q4_K", 8192, 0), ("Q4_K", 4096, 0), ("Q8_0", 32, 0), ("Q6_K", 32, 0), ("Q4_K", 300, 7 * K),
+             ("Q6_K", 2048, 8 * K)] + [("Q4_K", 64 + 16 * i, 0) for i in range(9)]
+    jobs, single = [], []
+    for kind, M, off in specs:
+        t = ops.GGML_TYPES[kind]
+        n_el = M * K + off
+        w = dev(ggml_blocks.random_blocks(r, t, n_el // ggml_blocks.BLOCK[t][0]))
+        jobs.append((w, kind, n_el, M, off, torch.full((M,), 3.0, device="cuda")))
+    x = dev(r.standard_normal(K).astype(F32))
+    outs = ops.matmul_dispatch_multi(jobs, x, K)
+    for (w, kind, n_el, M, off, _), got in zip(jobs, outs):
+        ref = ops.matmul_dispatch(w, kind, n_el, x, M, K, element_offset=off)
+        assert_bits_equal(host(got), host(ref), f"{kind} {M}x{K} at {off}")
+    w0, kind0, n0, M0, _, _ = jobs[1]
+    assert_f32_close(host(outs[1]), oracle.gemv(host(w0), 12, host(x), M0, K), group=M0, what="multi vs oracle")
+
+
+def test_matmul_dispatch_multi_rejects_before_launching():
+    """A bad descriptor fails the whole call with matmul_dispatch's status and the
+    descriptor's index, and no output is written."""
+    from qwen35_hip._lib import QwenError, STATUS_OUT_OF_RANGE
+
+    K = 2048
+    w = dev(synth.q4k_table(64, K))
+    x = dev(rng(1).standard_normal(K).astype(F32))
+    a, b = torch.full((64,), 5.0, device="cuda"), torch.full((64,), 5.0, device="cuda")
+    with pytest.raises(QwenError, match="descriptor 1") as e:
+        ops.matmul_dispatch_multi([(w, "Q4_K", 64 * K, 64, 0, a), (w, "Q4_K", 64 * K, 64, K, b)], x, K)
+    assert e.value.status == STATUS_OUT_OF_RANGE
+    torch.cuda.synchronize()
+    assert torch.all(a == 5.0) and torch.all(b == 5.0)
+    assert ops.matmul_dispatch_multi([], x, K) == []
+
+
 @pytest.mark.parametrize("kind,M", [("Q6_K", 16400), ("Q4_K", 65550)])
 def test_matmul_dispatch_mfma_random_blocks(oracle, kind, M):
     """The MFMA path on GGML blocks with random fp16 fields of both signs
