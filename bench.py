@@ -242,6 +242,31 @@ def build_next_rows(torch, ops, synth, host):
         k.gdn = {"rows": rows, "qkv": qkv_h, "beta": np.full((rows, vh), 0.5, np.float32),
                  "decay": np.full((rows, vh), 0.95, np.float32), "state": st0.cpu().numpy()}
         ks.append(k)
+        if rows == 1:
+            # The layer's gates + step (layer_gdn.cpp:100-106): two launches, or the
+            # fused-gate form in one (raw gates in, no beta / decay buffers).
+            braw = torch.from_numpy(rng.standard_normal((1, vh)).astype(np.float32)).to(dev)
+            araw = torch.from_numpy(rng.standard_normal((1, vh)).astype(np.float32)).to(dev)
+            ag = torch.from_numpy(-np.exp(rng.standard_normal(vh)).astype(np.float32)).to(dev)
+            dtg = torch.from_numpy(rng.uniform(-1, 1, vh).astype(np.float32)).to(dev)
+            bt1, dc1 = torch.empty((1, vh), device=dev), torch.empty((1, vh), device=dev)
+            nbg = nb + 2 * vh * 4   # raw gates in place of beta / decay (same count)
+            for gname, fused in (("gdn_gates_step_2_launches", False), ("gdn_gated_step", True)):
+                def mk_g(i, qkv=qkv, st0=st0, o=o, fused=fused):
+                    ss = st0 if i == 0 else st0.clone()
+                    oo = o if i == 0 else torch.empty_like(o)
+                    if fused:
+                        return lambda: ops.gdn_gated_recurrent_rows(ss, qkv, braw, araw, ag, dtg, kh, vh, dk, dv, oo)
+
+                    def run():
+                        ops.gdn_gate_values_rows(braw, araw, ag, dtg, beta=bt1, decay=dc1)
+                        ops.gdn_recurrent_rows(ss, qkv, bt1, dc1, kh, vh, dk, dv, oo)
+                    return run
+                kg = Kernel(gname, "one decode step with its gates from the raw projections: " +
+                            ("gate kernel + step kernel" if not fused else "fused-gate step, one launch"),
+                            nbg, nbg, mk_g)
+                kg.no_cpu = True
+                ks.append(kg)
         if rows > 1:
             # The chunked form on the same inputs (its workspace outside the bytes).
             ws = torch.empty(ops.load().qwen_gdn_recurrent_chunked_workspace_bytes(rows, vh), dtype=torch.uint8,

@@ -52,6 +52,14 @@ void gdn_recurrent_rows(float* state, const float* q, const float* k, const floa
                         const float* decay, float* out, int rows, int key_heads, int value_heads, int key_dim,
                         int value_dim, int64_t qkv_stride, int64_t out_stride, hipStream_t stream);
 
+// gdn_gate_values fused into gdn_recurrent_rows (one launch per decode step,
+// the same bits): beta_raw, alpha_raw [rows x value_heads], a, dt_bias
+// [value_heads]. ref: src/layer_gdn.cpp:100-106
+void gdn_gated_recurrent_rows(float* state, const float* q, const float* k, const float* v, const float* beta_raw,
+                              const float* alpha_raw, const float* a, const float* dt_bias, float* out, int rows,
+                              int key_heads, int value_heads, int key_dim, int value_dim, int64_t qkv_stride = 0,
+                              int64_t out_stride = 0, hipStream_t stream = nullptr);
+
 // gdn_norm_gate over rows x heads x dim.
 void gdn_norm_gate_rows(const float* x, const float* z, const float* weight, float* out, int rows, int heads,
                         int dim, float eps, hipStream_t stream);

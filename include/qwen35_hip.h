@@ -163,6 +163,20 @@ int qwen_gdn_recurrent_rows(float* state, const float* q, const float* k, const 
                             int key_heads, int value_heads, int key_dim, int value_dim,
                             int64_t qkv_stride, int64_t out_stride, void* stream);
 
+/* qwen_gdn_gate_values_rows fused into qwen_gdn_recurrent_rows: the gates of
+ * token t and value head h are evaluated where the recurrence uses them, from
+ * beta_raw and alpha_raw [rows x value_heads] (at t * value_heads) and a,
+ * dt_bias [value_heads], with the same expressions, so the results are the
+ * bits of the two calls in sequence; one launch instead of two per decode step,
+ * and no beta / decay buffers. Other arguments and statuses as
+ * qwen_gdn_recurrent_rows.
+ * ref: src/layer_gdn.cpp:100-106 (gdn_gate_values, then gdn_recurrent_step) */
+int qwen_gdn_gated_recurrent_rows(float* state, const float* q, const float* k, const float* v,
+                                  const float* beta_raw, const float* alpha_raw, const float* a,
+                                  const float* dt_bias, float* out, int rows, int key_heads,
+                                  int value_heads, int key_dim, int value_dim, int64_t qkv_stride,
+                                  int64_t out_stride, void* stream);
+
 /* Chunked form of qwen_gdn_recurrent_rows for many tokens (prefill): the same
  * recurrence re-associated over chunks of 64 tokens (decay ratios as running
  * products, a 64 x 64 triangular solve per chunk and head, the state updated

@@ -39,6 +39,19 @@ constexpr int kMaxValueDim = 256;  // src/cuda/gdn.cu:167-169
 // accurate device expf / log1pf.
 __device__ __forceinline__ float softplus20(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 
+// The gate pair of src/cuda/gdn.cu:93-97, shared by gates_kernel and the
+// recurrence's fused-gate form so that both give the same bits.
+__device__ __forceinline__ float gate_beta(float b) { return 1.0f / (1.0f + expf(-b)); }
+__device__ __forceinline__ float gate_decay(float a, float alpha, float dt) { return expf(a * softplus20(alpha + dt)); }
+
+// Fused-gate form of the recurrence: with `a` set, the kernels' beta / decay
+// arguments hold beta_raw / alpha_raw and the gates are evaluated per token
+// where they are used (a, dt_bias per value head).
+struct RawGates {
+    const float* a;
+    const float* dt;
+};
+
 __global__ __launch_bounds__(kBlock) void gates_kernel(const float* __restrict__ b, const float* __restrict__ alpha,
                                                        const float* __restrict__ a, const float* __restrict__ dt,
                                                        float* __restrict__ beta, float* __restrict__ decay,
@@ -46,8 +59,8 @@ __global__ __launch_bounds__(kBlock) void gates_kernel(const float* __restrict__
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
          i += static_cast<int64_t>(gridDim.x) * kBlock) {
         const int h = static_cast<int>(i % heads);
-        beta[i] = 1.0f / (1.0f + expf(-b[i]));
-        decay[i] = expf(a[h] * softplus20(alpha[i] + dt[h]));
+        beta[i] = gate_beta(b[i]);
+        decay[i] = gate_decay(a[h], alpha[i], dt[h]);
     }
 }
 
@@ -68,7 +81,7 @@ __global__ __launch_bounds__(kBlock) void gdn_recurrent_g(float* __restrict__ S,
                                                           const float* __restrict__ beta,
                                                           const float* __restrict__ decay, float* __restrict__ out,
                                                           int rows, int key_heads, int value_heads, int value_dim,
-                                                          int64_t qkv_stride, int64_t out_stride) {
+                                                          int64_t qkv_stride, int64_t out_stride, RawGates rg) {
     constexpr int G = kWave / NCOL;
     constexpr int RPL = DK / G;
     static_assert(RPL % 4 == 0 && RPL * G == DK, "rows per lane");
@@ -81,6 +94,7 @@ __global__ __launch_bounds__(kBlock) void gdn_recurrent_g(float* __restrict__ S,
     const int c = lane / G, r0 = (lane % G) * RPL;
     const int j = NCOL * (wave - h * cblocks) + c;   // this lane's value column
     const int src = h % key_heads;  // value heads tile as [subgroup][key head]
+    const float ah = rg.a ? rg.a[h] : 0.0f, dth = rg.a ? rg.dt[h] : 0.0f;
     float* Sj = S + static_cast<size_t>(h) * DK * value_dim + static_cast<size_t>(r0) * value_dim + j;
 
     float kr[P][RPL], qr[P][RPL], vv[P], bt[P], dc[P];
@@ -119,7 +133,7 @@ __global__ __launch_bounds__(kBlock) void gdn_recurrent_g(float* __restrict__ S,
             const int t = t0 + p;
             if (t >= rows) break;  // wave-uniform
             // S *= decay; mem = sum_i k_i S_i (this column)
-            const float d = dc[p];
+            const float d = rg.a ? gate_decay(ah, dc[p], dth) : dc[p];
             float m = 0.f;
 #pragma unroll
             for (int r = 0; r < RPL; ++r) {
@@ -127,7 +141,7 @@ __global__ __launch_bounds__(kBlock) void gdn_recurrent_g(float* __restrict__ S,
                 m = __builtin_fmaf(kr[p][r], s[r], m);
             }
             m = group_sum<G>(m);
-            const float dl = (vv[p] - m) * bt[p];
+            const float dl = (vv[p] - m) * (rg.a ? gate_beta(bt[p]) : bt[p]);
             // S += k_i * delta; o = sum_i q_i S_i
             float o = 0.f;
 #pragma unroll
@@ -159,7 +173,7 @@ __global__ __launch_bounds__(kBlock) void gdn_recurrent_v4(float* __restrict__ S
                                                            const float* __restrict__ beta,
                                                            const float* __restrict__ decay, float* __restrict__ out,
                                                            int rows, int key_heads, int value_heads, int value_dim,
-                                                           int64_t qkv_stride, int64_t out_stride) {
+                                                           int64_t qkv_stride, int64_t out_stride, RawGates rg) {
     constexpr int DK = 64 * RPL;
     constexpr int P = kPrefetch;
     const int cblocks = value_dim >> 2;
@@ -169,6 +183,7 @@ __global__ __launch_bounds__(kBlock) void gdn_recurrent_v4(float* __restrict__ S
     const int h = wave / cblocks;
     const int j0 = 4 * (wave - h * cblocks);
     const int src = h % key_heads;  // value heads tile as [subgroup][key head]
+    const float ah = rg.a ? rg.a[h] : 0.0f, dth = rg.a ? rg.dt[h] : 0.0f;
     float* Sh = S + static_cast<size_t>(h) * DK * value_dim + j0;
 
     float kr[P][RPL], qr[P][RPL], bt[P], dc[P];
@@ -199,7 +214,7 @@ __global__ __launch_bounds__(kBlock) void gdn_recurrent_v4(float* __restrict__ S
             const int t = t0 + p;
             if (t >= rows) break;  // wave-uniform
             // S *= decay; mem = sum_i k_i S_i  (per column)
-            const float d = dc[p];
+            const float d = rg.a ? gate_decay(ah, dc[p], dth) : dc[p];
             float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
             for (int r = 0; r < RPL; ++r) {
@@ -216,7 +231,7 @@ __global__ __launch_bounds__(kBlock) void gdn_recurrent_v4(float* __restrict__ S
             m.y = group_sum<64>(m.y);
             m.z = group_sum<64>(m.z);
             m.w = group_sum<64>(m.w);
-            const float b = bt[p];
+            const float b = rg.a ? gate_beta(bt[p]) : bt[p];
             const float4 dl = make_float4((vv[p].x - m.x) * b, (vv[p].y - m.y) * b, (vv[p].z - m.z) * b,
                                           (vv[p].w - m.w) * b);
             // S += k_i * delta; o = sum_i q_i S_i
@@ -250,7 +265,7 @@ __global__ __launch_bounds__(kBlock) void gdn_recurrent_v4(float* __restrict__ S
 __global__ __launch_bounds__(kMaxValueDim) void gdn_recurrent_any(
     float* __restrict__ S, const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ beta, const float* __restrict__ decay, float* __restrict__ out, int rows, int key_heads,
-    int value_heads, int key_dim, int value_dim, int64_t qkv_stride, int64_t out_stride) {
+    int value_heads, int key_dim, int value_dim, int64_t qkv_stride, int64_t out_stride, RawGates rg) {
     const int h = blockIdx.x;
     const int j = threadIdx.x;
     if (j >= value_dim) return;
@@ -259,15 +274,17 @@ __global__ __launch_bounds__(kMaxValueDim) void gdn_recurrent_any(
     for (int t = 0; t < rows; ++t) {
         const float* qt = q + t * qkv_stride + static_cast<size_t>(src) * key_dim;
         const float* kt = k + t * qkv_stride + static_cast<size_t>(src) * key_dim;
-        const float dc = decay[static_cast<int64_t>(t) * value_heads + h];
+        const float dr = decay[static_cast<int64_t>(t) * value_heads + h];
+        const float dc = rg.a ? gate_decay(rg.a[h], dr, rg.dt[h]) : dr;
         float mem = 0.f;
         for (int i = 0; i < key_dim; ++i) {
             float c = Sh[static_cast<size_t>(i) * value_dim] * dc;
             Sh[static_cast<size_t>(i) * value_dim] = c;
             mem = __builtin_fmaf(kt[i], c, mem);
         }
+        const float br = beta[static_cast<int64_t>(t) * value_heads + h];
         const float dl = (v[t * qkv_stride + static_cast<size_t>(h) * value_dim + j] - mem) *
-                         beta[static_cast<int64_t>(t) * value_heads + h];
+                         (rg.a ? gate_beta(br) : br);
         float o = 0.f;
         for (int i = 0; i < key_dim; ++i) {
             const float c = __builtin_fmaf(kt[i], dl, Sh[static_cast<size_t>(i) * value_dim]);
@@ -280,7 +297,8 @@ __global__ __launch_bounds__(kMaxValueDim) void gdn_recurrent_any(
 
 int launch_recurrent(float* state, const float* q, const float* k, const float* v, const float* beta,
                      const float* decay, float* out, int rows, int key_heads, int value_heads, int key_dim,
-                     int value_dim, int64_t qkv_stride, int64_t out_stride, hipStream_t s, const char* what) {
+                     int value_dim, int64_t qkv_stride, int64_t out_stride, hipStream_t s, const char* what,
+                     RawGates rg = RawGates{nullptr, nullptr}) {
     const bool vec = value_dim % 4 == 0 && (key_dim == 64 || key_dim == 128) && aligned16(q) && aligned16(k) &&
                      qkv_stride % 4 == 0;
     if (vec && rows == 1 && aligned16(state) && aligned16(v) && aligned16(out)) {
@@ -288,10 +306,10 @@ int launch_recurrent(float* state, const float* q, const float* k, const float* 
         const unsigned grid = blocks_for(value_heads * (value_dim / 4), kWaves);
         if (key_dim == 64)
             gdn_recurrent_v4<1><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
-                                                        value_heads, value_dim, qkv_stride, out_stride);
+                                                        value_heads, value_dim, qkv_stride, out_stride, rg);
         else
             gdn_recurrent_v4<2><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
-                                                        value_heads, value_dim, qkv_stride, out_stride);
+                                                        value_heads, value_dim, qkv_stride, out_stride, rg);
     } else if (vec) {
         // Columns per wave: 2 for key dim 128 (two waves per SIMD at the Qwen3.5
         // shape, 32 value heads x 128 columns), 4 for key dim 64.
@@ -300,14 +318,14 @@ int launch_recurrent(float* state, const float* q, const float* k, const float* 
         const unsigned grid = blocks_for(value_heads * (value_dim / ncol), kWaves);
         if (key_dim == 64)
             gdn_recurrent_g<64, 4><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
-                                                           value_heads, value_dim, qkv_stride, out_stride);
+                                                           value_heads, value_dim, qkv_stride, out_stride, rg);
         else
             gdn_recurrent_g<128, kNcol128><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
-                                                                   value_heads, value_dim, qkv_stride, out_stride);
+                                                                   value_heads, value_dim, qkv_stride, out_stride, rg);
     } else {
         gdn_recurrent_any<<<value_heads, kMaxValueDim, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
                                                                value_heads, key_dim, value_dim, qkv_stride,
-                                                               out_stride);
+                                                               out_stride, rg);
     }
     return check_launch(what);
 }
@@ -347,6 +365,23 @@ int qwen_gdn_recurrent_rows(float* state, const float* q, const float* k, const 
     QK_REQUIRE(rows == 1 || (qkv_stride > 0 && out_stride > 0), "gdn_recurrent: non-positive row stride");
     return launch_recurrent(state, q, k, v, beta, decay, out, rows, key_heads, value_heads, key_dim, value_dim,
                             qkv_stride, out_stride, as_stream(stream), "gdn_recurrent");
+}
+
+int qwen_gdn_gated_recurrent_rows(float* state, const float* q, const float* k, const float* v, const float* beta_raw,
+                                  const float* alpha_raw, const float* a, const float* dt_bias, float* out, int rows,
+                                  int key_heads, int value_heads, int key_dim, int value_dim, int64_t qkv_stride,
+                                  int64_t out_stride, void* stream) {
+    QK_REQUIRE(rows >= 0 && key_heads >= 0 && value_heads >= 0 && key_dim >= 0 && value_dim >= 0,
+               "gdn_gated_recurrent: negative size");
+    QK_REQUIRE(value_dim <= kMaxValueDim, "GDN value dimension exceeds kernel limit");
+    if (rows == 0 || value_heads == 0 || value_dim == 0) return ok();
+    QK_REQUIRE(key_heads > 0 && key_dim > 0, "gdn_gated_recurrent: key_heads and key_dim must be positive");
+    QK_REQUIRE(state && q && k && v && beta_raw && alpha_raw && a && dt_bias && out,
+               "gdn_gated_recurrent: null pointer");
+    QK_REQUIRE(rows == 1 || (qkv_stride > 0 && out_stride > 0), "gdn_gated_recurrent: non-positive row stride");
+    return launch_recurrent(state, q, k, v, beta_raw, alpha_raw, out, rows, key_heads, value_heads, key_dim,
+                            value_dim, qkv_stride, out_stride, as_stream(stream), "gdn_gated_recurrent",
+                            RawGates{a, dt_bias});
 }
 
 int qwen_gdn_recurrent_step(float* state, const float* q, const float* k, const float* v, const float* beta,

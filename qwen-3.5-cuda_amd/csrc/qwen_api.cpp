@@ -109,6 +109,14 @@ void gdn_recurrent_rows(float* state, const float* q, const float* k, const floa
                                   qkv_stride, out_stride, st(stream)));
 }
 
+void gdn_gated_recurrent_rows(float* state, const float* q, const float* k, const float* v, const float* beta_raw,
+                              const float* alpha_raw, const float* a, const float* dt_bias, float* out, int rows,
+                              int key_heads, int value_heads, int key_dim, int value_dim, int64_t qkv_stride,
+                              int64_t out_stride, hipStream_t stream) {
+    check(qwen_gdn_gated_recurrent_rows(state, q, k, v, beta_raw, alpha_raw, a, dt_bias, out, rows, key_heads,
+                                        value_heads, key_dim, value_dim, qkv_stride, out_stride, st(stream)));
+}
+
 void gdn_frontend_rows(const float* x, const float* weight, const float* hist_in, float* hist_out, float* y, int rows,
                        int channels, int kernel, int k_heads, int key_dim, float eps, hipStream_t stream) {
     check(qwen_gdn_frontend_rows(x, weight, hist_in, hist_out, y, rows, channels, kernel, k_heads, key_dim, eps,

@@ -63,6 +63,7 @@ SIGNATURES: dict[str, list] = {
     "qwen_gdn_gate_values_rows": [_P] * 6 + [_I, _I, _P],
     "qwen_gdn_recurrent_step": [_P] * 7 + [_I, _I, _I, _I, _P],
     "qwen_gdn_recurrent_rows": [_P] * 7 + [_I, _I, _I, _I, _I, _I64, _I64, _P],
+    "qwen_gdn_gated_recurrent_rows": [_P] * 9 + [_I, _I, _I, _I, _I, _I64, _I64, _P],
     "qwen_gdn_recurrent_chunked_workspace_bytes": [_I, _I],
     "qwen_gdn_recurrent_chunked": [_P] * 7 + [_I, _I, _I, _I, _I, _I64, _I64, _P, ctypes.c_size_t, _P],
     "qwen_attn_split_qg": [_P, _P, _P, _I, _I, _P],

@@ -270,6 +270,30 @@ def gdn_recurrent_rows(state, qkv, beta, decay, key_heads, value_heads, key_dim,
     return out
 
 
+def gdn_gated_recurrent_rows(state, qkv, beta_raw, alpha_raw, a, dt_bias, key_heads, value_heads, key_dim,
+                             value_dim, out=None, stream=None):
+    """gdn_gate_values_rows fused into gdn_recurrent_rows: beta_raw, alpha_raw [rows, value_heads],
+    a, dt_bias [value_heads]; other arguments as gdn_recurrent_rows."""
+    _dev(state, qkv, beta_raw, alpha_raw, a, dt_bias, dtype=torch.float32)
+    rows, stride = qkv.shape
+    kd = key_heads * key_dim
+    if stride < 2 * kd + value_heads * value_dim:
+        raise ValueError("qkv rows too short for q | k | v")
+    if state.numel() != value_heads * key_dim * value_dim:
+        raise ValueError("state shape does not match the head sizes")
+    _same((rows, value_heads), beta_raw, alpha_raw)
+    _same((value_heads,), a, dt_bias)
+    out = torch.empty((rows, value_heads * value_dim), dtype=torch.float32, device=qkv.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    _same((rows, value_heads * value_dim), out)
+    base = qkv.data_ptr()
+    check(load().qwen_gdn_gated_recurrent_rows(_p(state), ctypes.c_void_p(base), ctypes.c_void_p(base + 4 * kd),
+                                               ctypes.c_void_p(base + 8 * kd), _p(beta_raw), _p(alpha_raw), _p(a),
+                                               _p(dt_bias), _p(out), rows, key_heads, value_heads, key_dim, value_dim,
+                                               stride, value_heads * value_dim, _stream(stream)))
+    return out
+
+
 def gdn_recurrent_chunked(state, qkv, beta, decay, key_heads, value_heads, key_dim, value_dim, out=None,
                           workspace=None, stream=None):
     """qwen_gdn_recurrent_rows' chunked form (prefill): same arguments; `workspace` a

@@ -541,6 +541,26 @@ def test_gdn_recurrent_rows_equals_steps():
     assert_f32_close(host(s1), host(s2), group=dv, what="state")
 
 
+@pytest.mark.parametrize("rows,kh,vh,dk,dv", [(1, 16, 32, 128, 128), (1, 4, 8, 64, 64), (37, 16, 32, 128, 128),
+                                               (5, 2, 4, 100, 48)])
+def test_gdn_gated_recurrent_equals_gates_then_recurrence(rows, kh, vh, dk, dv):
+    """The fused-gate recurrence (qwen_gdn_gated_recurrent_rows) gives the bits of
+    gdn_gate_values_rows followed by gdn_recurrent_rows on every kernel path (one
+    token, the token loop, the generic form), with gates that reach the softplus
+    threshold (alpha + dt > 20) and saturated betas."""
+    r = rng(rows * 1000 + dk)
+    qkv, b, alpha, a, dt, state = _gdn_inputs(r, rows, kh, vh, dk, dv)
+    alpha[:, 0] = 25.0          # softplus(x) = x branch
+    b[:, 1 % vh] = -30.0        # beta ~ 0
+    beta, decay = ops.gdn_gate_values_rows(dev(b), dev(alpha), dev(a), dev(dt))
+    s1, s2 = dev(state), dev(state)
+    dq = dev(qkv)
+    ref = host(ops.gdn_recurrent_rows(s1, dq, beta, decay, kh, vh, dk, dv))
+    got = host(ops.gdn_gated_recurrent_rows(s2, dq, dev(b), dev(alpha), dev(a), dev(dt), kh, vh, dk, dv))
+    assert_bits_equal(got, ref, "out")
+    assert_bits_equal(host(s2), host(s1), "state")
+
+
 def test_gdn_recurrent_rejects_wide_values():
     from qwen35_hip._lib import QwenError
 
