@@ -385,6 +385,31 @@ def build_next_rows(torch, ops, synth, host):
         k = Kernel(name, desc, nb, nb, mk_p)
         k.no_cpu = True
         ks.append(k)
+
+    # One GDN layer's decode step (layer_gdn.cpp:78-113) composed from the library: the
+    # reference's ten calls against the fused five (qwen35_hip.decode_layers). Bytes: the
+    # five Q4_K projections, the state read and written, conv weights and history.
+    from qwen35_hip.decode_layers import GdnLayerDecode
+    cdim, vdim = 2 * kh * dk + vh * dv, vh * dv
+    lw = [torch.from_numpy(synth.q4k_table(M, K, seed_tensor=s)).to(dev)
+          for M, K, s in ((cdim, 2048, 40), (vdim, 2048, 41), (vh, 2048, 42), (vh, 2048, 43), (2048, vdim, 44))]
+    conv_w = torch.from_numpy((0.5 * rng.standard_normal((cdim, 4))).astype(np.float32)).to(dev)
+    la = torch.from_numpy(-np.exp(rng.standard_normal(vh)).astype(np.float32)).to(dev)
+    ldt = torch.from_numpy(rng.uniform(-1, 1, vh).astype(np.float32)).to(dev)
+    lnw = torch.from_numpy((1 + 0.1 * rng.standard_normal(dv)).astype(np.float32)).to(dev)
+    lx = torch.from_numpy((0.3 * rng.standard_normal(2048)).astype(np.float32)).to(dev)
+    lout = torch.empty(2048, dtype=torch.float32, device=dev)
+    nb = (sum(t.numel() for t in lw) + 2 * vh * dk * dv * 4 + cdim * 4 * 4 + 2 * cdim * 3 * 4 + 2048 * 4 * 2)
+    for name, fused in (("gdn_layer_decode_10_calls", False), ("gdn_layer_decode_fused", True)):
+        def mk_l(i, fused=fused):
+            ww = lw if i == 0 else [t.clone() for t in lw]
+            layer = GdnLayerDecode(*ww, conv_w, la, ldt, lnw)
+            return (lambda: layer.forward(lx, lout)) if fused else (lambda: layer.forward_reference_launches(lx, lout))
+        desc = ("one GDN layer decode step, Q4_K weights, 16/32 heads of 128: " +
+                ("fused entry points, 5 launches" if fused else "the reference's sequence of 10 calls"))
+        k = Kernel(name, desc, nb, nb, mk_l)
+        k.no_cpu = True
+        ks.append(k)
     return ks
 
 

@@ -561,6 +561,36 @@ def test_gdn_gated_recurrent_equals_gates_then_recurrence(rows, kh, vh, dk, dv):
     assert_bits_equal(host(s2), host(s1), "state")
 
 
+def test_gdn_layer_decode_fused_equals_reference_launches():
+    """A GDN layer's decode step (src/layer_gdn.cpp:78-113) through the fused
+    entry points (five launches) against the reference's sequence of calls on the
+    same library (ten launches), three tokens in a row with the conv history and
+    the recurrent state carried: same outputs, state and history (the fused
+    front end's L2 norm sums in another order, so fp32 tolerance)."""
+    from qwen35_hip.decode_layers import GdnLayerDecode
+
+    r = rng(31)
+    dm, kh, vh, dk, dv = 2048, 16, 32, 128, 128
+    cd, vd = 2 * kh * dk + vh * dv, vh * dv
+
+    def q4(M, K, s):
+        return dev(synth.q4k_table(M, K, seed_tensor=s))
+    wq, wz, wb, wa, wo = q4(cd, dm, 40), q4(vd, dm, 41), q4(vh, dm, 42), q4(vh, dm, 43), q4(dm, vd, 44)
+    conv_w = dev((0.5 * r.standard_normal((cd, 4))).astype(F32))
+    a = dev(-np.exp(r.standard_normal(vh)).astype(F32))
+    dt = dev(r.uniform(-1, 1, vh).astype(F32))
+    nw = dev((1 + 0.1 * r.standard_normal(dv)).astype(F32))
+    ref = GdnLayerDecode(wq, wz, wb, wa, wo, conv_w, a, dt, nw)
+    fus = GdnLayerDecode(wq, wz, wb, wa, wo, conv_w, a, dt, nw)
+    for t in range(3):
+        x = dev((0.3 * r.standard_normal(dm)).astype(F32))
+        o_ref = host(ref.forward_reference_launches(x, torch.empty(dm, device="cuda")))
+        o_fus = host(fus.forward(x, torch.empty(dm, device="cuda")))
+        assert_f32_close(o_fus, o_ref, group=dm, what=f"token {t} output")
+        assert_f32_close(host(fus.state), host(ref.state), group=dv, what=f"token {t} state")
+        assert np.array_equal(host(fus.history), host(ref.history)), f"token {t} history"
+
+
 def test_gdn_recurrent_rejects_wide_values():
     from qwen35_hip._lib import QwenError
 
