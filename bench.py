@@ -410,6 +410,64 @@ def build_next_rows(torch, ops, synth, host):
         k = Kernel(name, desc, nb, nb, mk_l)
         k.no_cpu = True
         ks.append(k)
+
+    # One full-attention layer's decode step (layer_attn.cpp:63-111) at position 2047 of a
+    # 4096-row cache: the reference's fifteen calls against the fused five. Bytes: the four
+    # Q4_K projections and the 2048 K and V rows read.
+    from qwen35_hip.decode_layers import AttnLayerDecode
+    apos = 2047
+    aw = [torch.from_numpy(synth.q4k_table(M, K, seed_tensor=s)).to(dev)
+          for M, K, s in ((8192, 2048, 50), (512, 2048, 51), (512, 2048, 52), (2048, 4096, 53))]
+    aqn = torch.from_numpy((1 + 0.1 * rng.standard_normal(256)).astype(np.float32)).to(dev)
+    akn = torch.from_numpy((1 + 0.1 * rng.standard_normal(256)).astype(np.float32)).to(dev)
+    akv = torch.from_numpy(rng.standard_normal((2, apos, 512)).astype(np.float32)).to(dev)
+    nb = sum(t.numel() for t in aw) + 2 * (apos + 1) * 512 * 4 + 4 * 2048 * 2
+    for name, fused in (("attn_layer_decode_15_calls", False), ("attn_layer_decode_fused", True)):
+        def mk_a(i, fused=fused):
+            ww = aw if i == 0 else [t.clone() for t in aw]
+            layer = AttnLayerDecode(*ww, aqn, akn)
+            layer.k_cache[:apos].copy_(akv[0])
+            layer.v_cache[:apos].copy_(akv[1])
+            return ((lambda: layer.forward(lx, apos, lout)) if fused else
+                    (lambda: layer.forward_reference_launches(lx, apos, lout)))
+        desc = ("one attention layer decode step at position 2047, Q4_K weights, 16 query / 2 KV heads of 256: " +
+                ("fused entry points, 5 launches" if fused else "the reference's sequence of 15 calls"))
+        k = Kernel(name, desc, nb, nb, mk_a)
+        k.no_cpu = True
+        ks.append(k)
+
+    # One MoE layer's decode step (layer_moe.cpp:80-159): 256 experts, top 8, Q4_K. The
+    # reference's sequence synchronises with the host to read the expert ids, so it cannot
+    # be captured: it is timed eagerly (wall clock per call), and the fused path both
+    # eagerly and captured. Each buffer set has its own token (so its own experts) and its
+    # own copy of the router and shared expert. Bytes: router, 8 x 3 expert matrices,
+    # the shared expert's four, the 8 expert outputs written and read.
+    from qwen35_hip.decode_layers import MoeLayerDecode
+    E, I, S = 256, 512, 2048
+    ew = [torch.from_numpy(synth.q4k_table(E * M, K, seed_tensor=s)).to(dev)
+          for M, K, s in ((I, 2048, 61), (I, 2048, 62), (2048, I, 63))]
+    sw = [torch.from_numpy(synth.q4k_table(M, K, seed_tensor=s)).to(dev)
+          for M, K, s in ((E, 2048, 60), (1, 2048, 64), (S, 2048, 65), (S, 2048, 66), (2048, S, 67))]
+    q4 = lambda M, K: M * K // 256 * 144  # noqa: E731
+    nb = (q4(E, 2048) + 8 * 3 * q4(I, 2048) + q4(1, 2048) + 3 * q4(S, 2048) + 2 * 8 * 2048 * 4 + 4 * 2048 * 2)
+    for name, fused, eager in (("moe_layer_decode_reference_calls", False, True),
+                               ("moe_layer_decode_fused_eager", True, True),
+                               ("moe_layer_decode_fused", True, False)):
+        def mk_m(i, fused=fused):
+            s = sw if i == 0 else [t.clone() for t in sw]
+            layer = MoeLayerDecode(s[0], *ew, *s[1:])
+            xm = torch.from_numpy((0.05 * np.random.default_rng(1000 + i).standard_normal(2048))
+                                  .astype(np.float32)).to(dev)
+            om = torch.empty(2048, dtype=torch.float32, device=dev)
+            return (lambda: layer.forward(xm, om)) if fused else (lambda: layer.forward_reference_launches(xm, om))
+        desc = ("one MoE layer decode step, 256 experts top 8, 512-wide experts, 2048-wide shared expert, Q4_K: " +
+                ("fused entry points, 10 launches, expert ids on the device" if fused else
+                 "the reference's sequence (8 + 5 x 8 calls and a host round trip for the expert ids)") +
+                ("; eager, wall clock per call" if eager else ""))
+        k = Kernel(name, desc, nb, nb, mk_m)
+        k.no_cpu = True
+        k.eager = eager
+        ks.append(k)
     return ks
 
 
@@ -467,10 +525,33 @@ def n_sets(footprint: int) -> int:
     return max(2, min(2048, -(-ROTATE_BYTES // footprint)))
 
 
+def eager_us(torch, launches, calls: int, repeats: int = 5) -> float:
+    """Wall-clock us per call of `launches` called eagerly in turn (for a sequence
+    that synchronises with the host inside, which no graph can hold), the device
+    synchronised before and after each batch; median over `repeats` batches."""
+    for f in launches:
+        f()
+    torch.cuda.synchronize()
+    n = max(len(launches), calls)
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        for j in range(n):
+            launches[j % len(launches)]()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e6 / n)
+    return sorted(times)[len(times) // 2]
+
+
 def measure_kernel(torch, k: Kernel, spin: int, min_launches: int) -> float:
     sets = n_sets(k.footprint)
     launches = [k.make(i) for i in range(sets)]
     replays = max(1, -(-min_launches // sets))
+    if getattr(k, "eager", False):
+        us = eager_us(torch, launches, max(min_launches, 200))
+        del launches
+        torch.cuda.empty_cache()
+        return us
     us = steady_state_us(torch, launches, replays, spin)
     del launches
     torch.cuda.empty_cache()

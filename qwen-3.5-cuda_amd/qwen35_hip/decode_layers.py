@@ -1,24 +1,29 @@
-"""One Gated DeltaNet layer's decode step composed from the library's entry points.
+"""A layer's decode step composed from the library's entry points, for each of the
+three layer kinds of the reference's decoder (GDN, full attention, MoE).
 
-`GdnLayerDecode` holds a GDN layer's weights and per-layer state as the
-reference's GdnLayer does (src/layer_gdn.cpp:37-57: conv history, recurrent
-state, per-token buffers) and runs the decode step of its forward
-(src/layer_gdn.cpp:78-113) in two ways:
+Each class holds the layer's weights and per-layer state as the reference's
+layer object does and runs its decode forward in two ways: one library call per
+reference call (`forward_reference_launches`) and through the fused entry points
+(`forward`). Weights are GGML tensors (uint8 device tensors of blocks) of one
+K-quant type.
 
-* `forward_reference_launches(x)`: the reference's sequence, one library call per
-  reference call — four projections (:83-86), conv step (:89), Q/K normalize
-  (:97), gates (:100), recurrent step (:103-106), gated norm (:109), output
-  projection (:112): ten launches;
-* `forward(x)`: the fused entry points — the four projections in one
-  `matmul_dispatch_multi`, conv + SiLU + Q/K L2 in `gdn_frontend_rows`, gates +
-  recurrence in `gdn_gated_recurrent_rows`, then the gated norm and the output
-  projection: five launches.
+`GdnLayerDecode` follows the reference's GdnLayer (src/layer_gdn.cpp:37-57: conv
+history, recurrent state, per-token buffers; forward src/layer_gdn.cpp:78-113):
 
-Both update the layer's conv history and recurrent state in place. Weights are
-GGML tensors (uint8 device tensors of blocks) of one K-quant type.
+* `forward_reference_launches(x)`: four projections (:83-86), conv step (:89),
+  Q/K normalize (:97), gates (:100), recurrent step (:103-106), gated norm
+  (:109), output projection (:112): ten launches;
+* `forward(x)`: the four projections in one `matmul_dispatch_multi`, conv + SiLU
+  + Q/K L2 in `gdn_frontend_rows`, gates + recurrence in
+  `gdn_gated_recurrent_rows`, then the gated norm and the output projection:
+  five launches.
+
+Both update the layer's conv history and recurrent state in place.
 """
 
 from __future__ import annotations
+
+import math
 
 import torch
 
@@ -82,4 +87,187 @@ class GdnLayerDecode:
         ops.gdn_norm_gate_rows(self.core.view(self.vh, self.dv), self.z.view(self.vh, self.dv), self.norm_w,
                                out=self.normed.view(self.vh, self.dv), eps=self.eps)
         self._proj("out", self.normed, out, self.vd)
+        return out
+
+
+class AttnLayerDecode:
+    """A full-attention layer's decode step (src/layer_attn.cpp:63-111) with its
+    KV cache (src/layer_attn.cpp:44-46: max_seq_len rows of kv_heads x head_dim
+    floats per cache) and per-token buffers.
+
+    * `forward_reference_launches(x, pos, out)`: the reference's sequence — three
+      projections (:85-87), split (:90), two head norms (:91-92), two RoPE calls
+      (:95-96), two cache copies (:99-100), scores / softmax / values (:103-105),
+      sigmoid gate (:108), output projection (:109): fifteen launches;
+    * `forward(x, pos, out)`: the three projections in one `matmul_dispatch_multi`
+      whose K and V outputs are the cache rows at `pos` (no cache copies), split,
+      Q/K head norm + partial RoPE in one `attn_qk_norm_rope_rows` (K normalized
+      in place in the cache row), `attn_decode` (scores, softmax, values and the
+      sigmoid gate), output projection: five launches.
+    """
+
+    def __init__(self, w_qg, w_k, w_v, w_out, q_norm, k_norm, *, wtype="Q4_K", d_model=2048, heads=16, kv_heads=2,
+                 head_dim=256, rope_dim=64, theta=1e7, eps=1e-6, max_seq_len=4096):
+        self.h, self.kvh, self.hd, self.dm = heads, kv_heads, head_dim, d_model
+        self.rope_dim, self.theta, self.eps, self.max_seq_len = rope_dim, theta, eps, max_seq_len
+        self.qd, self.kd = heads * head_dim, kv_heads * head_dim
+        self.wtype = wtype
+        self.w = {"qg": (w_qg, 2 * self.qd), "k": (w_k, self.kd), "v": (w_v, self.kd), "out": (w_out, d_model)}
+        self.q_norm, self.k_norm = q_norm, k_norm
+        f = dict(dtype=torch.float32, device=q_norm.device)
+        self.k_cache = torch.zeros((max_seq_len, self.kd), **f)      # layer_attn.cpp:44-46
+        self.v_cache = torch.zeros((max_seq_len, self.kd), **f)
+        self.qg = torch.empty(2 * self.qd, **f)
+        self.q = torch.empty(self.qd, **f)
+        self.gate = torch.empty(self.qd, **f)
+        self.k = torch.empty(self.kd, **f)
+        self.v = torch.empty(self.kd, **f)
+        self.scores = torch.empty(heads * max_seq_len, **f)
+        self.attn = torch.empty(self.qd, **f)
+        self.gated = torch.empty(self.qd, **f)
+        nbytes = max(ops.attn_decode_workspace_bytes(heads, kv_heads, head_dim, p) for p in range(max_seq_len))
+        self.workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q_norm.device)
+
+    def _check_pos(self, pos):
+        if pos < 0 or pos >= self.max_seq_len:                        # layer_attn.cpp:75-77
+            raise ValueError("attention position exceeds configured context")
+
+    def _proj(self, name, x, y, K):
+        w, M = self.w[name]
+        ops.matmul_dispatch(w, self.wtype, M * K, x, M, K, out=y)
+
+    def forward_reference_launches(self, x, pos, out):
+        self._check_pos(pos)
+        h, kvh, hd = self.h, self.kvh, self.hd
+        self._proj("qg", x, self.qg, self.dm)
+        self._proj("k", x, self.k, self.dm)
+        self._proj("v", x, self.v, self.dm)
+        ops.attn_split_qg(self.qg, h, hd, q=self.q, g=self.gate)
+        ops.attn_head_norm(self.q.view(h, hd), self.q_norm, eps=self.eps)
+        ops.attn_head_norm(self.k.view(kvh, hd), self.k_norm, eps=self.eps)
+        ops.rope_forward(self.q.view(h, hd), pos, self.rope_dim, self.theta)
+        ops.rope_forward(self.k.view(kvh, hd), pos, self.rope_dim, self.theta)
+        self.k_cache[pos].copy_(self.k)
+        self.v_cache[pos].copy_(self.v)
+        ops.attn_scores(self.q, self.k_cache, h, kvh, hd, pos, out=self.scores)
+        ops.attn_softmax(self.scores, h, pos + 1)
+        ops.attn_values(self.scores, self.v_cache, h, kvh, hd, pos, out=self.attn)
+        ops.attn_sigmoid_gate(self.attn, self.gate, out=self.gated)
+        self._proj("out", self.gated, out, self.qd)
+        return out
+
+    def forward(self, x, pos, out):
+        self._check_pos(pos)
+        h, kvh, hd = self.h, self.kvh, self.hd
+        jobs = [(self.w[n][0], self.wtype, self.w[n][1] * self.dm, self.w[n][1], 0, y)
+                for n, y in (("qg", self.qg), ("k", self.k_cache[pos]), ("v", self.v_cache[pos]))]
+        ops.matmul_dispatch_multi(jobs, x, self.dm)
+        ops.attn_split_qg(self.qg, h, hd, q=self.q, g=self.gate)
+        ops.attn_qk_norm_rope_rows(self.q.view(1, h, hd), self.k_cache[pos].view(1, kvh, hd), self.q_norm,
+                                   self.k_norm, pos0=pos, rope_dim=self.rope_dim, theta=self.theta, eps=self.eps)
+        ops.attn_decode(self.q, self.k_cache, self.v_cache, h, kvh, hd, pos, gate=self.gate,
+                        workspace=self.workspace, out=self.gated)
+        self._proj("out", self.gated, out, self.qd)
+        return out
+
+
+class MoeLayerDecode:
+    """A MoE layer's decode step (src/layer_moe.cpp:80-159): router, top-k,
+    k routed experts (gate, up, SiLU x up, down, weighted add) and the gated
+    shared expert.
+
+    * `forward_reference_launches(x, out)`: the reference's sequence — router
+      projection and top-k (:95-96), the ids and weights copied to the host with a
+      stream synchronisation and checked there (:99-117), a zero fill (:104), five
+      launches per routed expert (:120-135), shared expert gate / gate / up
+      projections, SiLU x up, down projection, gated add (:138-146) and the copy
+      out (:147): 8 + 5k launches and a host round trip;
+    * `forward(x, out)`: the router and the three shared-expert projections of x
+      in one `matmul_dispatch_multi`, top-k on the device, the k routed gate and up
+      projections as two `moe_expert_matmul` launches reading the ids on the
+      device, one SiLU x up over the routed and shared hidden rows together, the
+      routed down projections in one launch, the shared down projection, a zero
+      fill, the weighted sum of the k expert outputs and the gated shared add:
+      ten launches, no host round trip. The host-side routing check is the one
+      part this path leaves out (the top-k kernel's weights are a softmax, finite
+      and normalised by construction).
+    """
+
+    def __init__(self, w_router, w_gate, w_up, w_down, w_sgate, w_sg, w_su, w_sd, *, wtype="Q4_K", d_model=2048,
+                 experts=256, k=8, inter=512, shared=2048):
+        self.dm, self.E, self.k, self.I, self.S = d_model, experts, k, inter, shared
+        self.wtype = wtype
+        self.w = {"router": (w_router, experts), "sgate": (w_sgate, 1), "sg": (w_sg, shared), "su": (w_su, shared),
+                  "sd": (w_sd, d_model)}
+        self.experts_w = {"gate": w_gate, "up": w_up, "down": w_down}
+        f = dict(dtype=torch.float32, device=w_router.device)
+        self.router = torch.empty(experts, **f)
+        self.top_idx = torch.empty(k, dtype=torch.int32, device=w_router.device)
+        self.top_w = torch.empty(k, **f)
+        # routed rows [k, inter] followed by the shared expert's [shared] row, so one
+        # SiLU x up launch covers both
+        self.gate_all = torch.empty(k * inter + shared, **f)
+        self.up_all = torch.empty(k * inter + shared, **f)
+        self.hidden_all = torch.empty(k * inter + shared, **f)
+        self.expert_out = torch.empty((k, d_model), **f)
+        self.sgate = torch.empty(1, **f)
+        self.shared_out = torch.empty(d_model, **f)
+        self.accum = torch.empty(d_model, **f)
+        self.h_idx = torch.empty(k, dtype=torch.int32).pin_memory()
+        self.h_w = torch.empty(k, dtype=torch.float32).pin_memory()
+
+    def _proj(self, name, x, y, K):
+        w, M = self.w[name]
+        ops.matmul_dispatch(w, self.wtype, M * K, x, M, K, out=y)
+
+    def _expert_proj(self, name, e, x, y, M, K):
+        ops.matmul_dispatch(self.experts_w[name], self.wtype, self.E * M * K, x, M, K, element_offset=e * M * K, out=y)
+
+    def forward_reference_launches(self, x, out):
+        k, I, S, dm = self.k, self.I, self.S, self.dm
+        self._proj("router", x, self.router, dm)
+        ops.moe_topk_rows(self.router.view(1, self.E), k, idx=self.top_idx.view(1, k), weights=self.top_w.view(1, k))
+        self.h_idx.copy_(self.top_idx, non_blocking=True)
+        self.h_w.copy_(self.top_w, non_blocking=True)
+        torch.cuda.current_stream().synchronize()
+        self.accum.zero_()
+        ids, wts = self.h_idx.tolist(), self.h_w.tolist()
+        if any(e < 0 or e >= self.E or not math.isfinite(w) or w < 0 for e, w in zip(ids, wts)):
+            raise RuntimeError("invalid/non-finite MoE routing result")
+        if not math.isfinite(sum(wts)) or abs(sum(wts) - 1.0) > 1e-4:
+            raise RuntimeError("MoE routing weights are not normalized")
+        g, u, hdn = self.gate_all[:I], self.up_all[:I], self.hidden_all[:I]
+        for e, wt in zip(ids, wts):
+            self._expert_proj("gate", e, x, g, I, dm)
+            self._expert_proj("up", e, x, u, I, dm)
+            ops.moe_silu_mul(g, u, out=hdn)
+            self._expert_proj("down", e, hdn, self.expert_out[0], dm, I)
+            ops.moe_add(self.accum, self.expert_out[0], wt)
+        self._proj("sgate", x, self.sgate, dm)
+        sg, su, sh = self.gate_all[k * I:], self.up_all[k * I:], self.hidden_all[k * I:]
+        self._proj("sg", x, sg, dm)
+        self._proj("su", x, su, dm)
+        ops.moe_silu_mul(sg, su, out=sh)
+        self._proj("sd", sh, self.shared_out, S)
+        ops.moe_shared_add_rows(self.accum.view(1, dm), self.shared_out.view(1, dm), self.sgate)
+        out.copy_(self.accum)
+        return out
+
+    def forward(self, x, out):
+        k, I, S, dm, E = self.k, self.I, self.S, self.dm, self.E
+        jobs = [(self.w[n][0], self.wtype, self.w[n][1] * dm, self.w[n][1], 0, y)
+                for n, y in (("router", self.router), ("sgate", self.sgate), ("sg", self.gate_all[k * I:]),
+                             ("su", self.up_all[k * I:]))]
+        ops.matmul_dispatch_multi(jobs, x, dm)
+        ops.moe_topk_rows(self.router.view(1, E), k, idx=self.top_idx.view(1, k), weights=self.top_w.view(1, k))
+        for name, y in (("gate", self.gate_all), ("up", self.up_all)):
+            ops.moe_expert_matmul(self.experts_w[name], self.wtype, E * I * dm, I * dm, E, self.top_idx, x, 0, I, dm,
+                                  out=y[:k * I].view(k, I))
+        ops.moe_silu_mul(self.gate_all, self.up_all, out=self.hidden_all)
+        ops.moe_expert_matmul(self.experts_w["down"], self.wtype, E * dm * I, dm * I, E, self.top_idx,
+                              self.hidden_all, I, dm, I, out=self.expert_out)
+        self._proj("sd", self.hidden_all[k * I:], self.shared_out, S)
+        out.zero_()
+        ops.moe_weighted_sum_rows(out.view(1, dm), self.expert_out.view(1, k, dm), self.top_w.view(1, k))
+        ops.moe_shared_add_rows(out.view(1, dm), self.shared_out.view(1, dm), self.sgate)
         return out

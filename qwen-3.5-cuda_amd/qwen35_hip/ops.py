@@ -323,12 +323,15 @@ def gdn_recurrent_chunked(state, qkv, beta, decay, key_heads, value_heads, key_d
 
 
 # ------------------------------------------------------------------ attention core (decode)
-def attn_split_qg(qg, heads, dim, stream=None):
+def attn_split_qg(qg, heads, dim, q=None, g=None, stream=None):
     _dev(qg, dtype=torch.float32)
     if qg.numel() != 2 * heads * dim:
         raise ValueError("qg must hold heads x 2 x dim values")
-    q = torch.empty(heads * dim, dtype=torch.float32, device=qg.device)
-    g = torch.empty_like(q)
+    q = torch.empty(heads * dim, dtype=torch.float32, device=qg.device) if q is None else q
+    g = torch.empty_like(q) if g is None else g
+    _dev(q, g, dtype=torch.float32)
+    if q.numel() < heads * dim or g.numel() < heads * dim:
+        raise ValueError("q / g outputs smaller than heads x dim")
     check(load().qwen_attn_split_qg(_p(qg), _p(q), _p(g), heads, dim, _stream(stream)))
     return q, g
 

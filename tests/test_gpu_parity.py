@@ -591,6 +591,77 @@ def test_gdn_layer_decode_fused_equals_reference_launches():
         assert np.array_equal(host(fus.history), host(ref.history)), f"token {t} history"
 
 
+def _attn_layer_pair(r, max_seq_len):
+    from qwen35_hip.decode_layers import AttnLayerDecode
+
+    dm, h, kvh, hd = 2048, 16, 2, 256
+    ws = [dev(synth.q4k_table(M, K, seed_tensor=s)) for M, K, s in
+          ((2 * h * hd, dm, 50), (kvh * hd, dm, 51), (kvh * hd, dm, 52), (dm, h * hd, 53))]
+    qn, kn = dev((1 + 0.1 * r.standard_normal(hd)).astype(F32)), dev((1 + 0.1 * r.standard_normal(hd)).astype(F32))
+    return (AttnLayerDecode(*ws, qn, kn, max_seq_len=max_seq_len),
+            AttnLayerDecode(*ws, qn, kn, max_seq_len=max_seq_len))
+
+
+@pytest.mark.parametrize("start", [0, 700])
+def test_attn_layer_decode_fused_equals_reference_launches(start):
+    """A full-attention layer's decode step (src/layer_attn.cpp:63-111) through
+    the fused entry points (five launches: projections straight into the cache
+    rows, split, Q/K norm + RoPE, attention decode, output projection) against the
+    reference's sequence of fifteen calls on the same library, three tokens in a
+    row from position `start` (0, and 700 over a cache whose earlier rows hold the
+    same random keys and values in both layers): same output and cache rows
+    within fp32 tolerance (the attention sums run in another order), the V rows
+    bit for bit."""
+    r = rng(37 + start)
+    ref, fus = _attn_layer_pair(r, 1024)
+    if start:
+        kv = dev((r.standard_normal((2, start, 512))).astype(F32))
+        for layer in (ref, fus):
+            layer.k_cache[:start].copy_(kv[0])
+            layer.v_cache[:start].copy_(kv[1])
+    for pos in range(start, start + 3):
+        x = dev((0.3 * r.standard_normal(2048)).astype(F32))
+        o_ref = host(ref.forward_reference_launches(x, pos, torch.empty(2048, device="cuda")))
+        o_fus = host(fus.forward(x, pos, torch.empty(2048, device="cuda")))
+        assert_f32_close(o_fus, o_ref, group=2048, what=f"pos {pos} output")
+        assert_f32_close(host(fus.k_cache[pos]), host(ref.k_cache[pos]), group=256, what=f"pos {pos} K row")
+        assert np.array_equal(host(fus.v_cache[pos]), host(ref.v_cache[pos])), f"pos {pos} V row"
+
+
+def test_attn_layer_decode_rejects_position_past_context():
+    r = rng(38)
+    _, fus = _attn_layer_pair(r, 16)
+    x = torch.zeros(2048, device="cuda")
+    with pytest.raises(ValueError, match="attention position exceeds configured context"):
+        fus.forward(x, 16, torch.empty(2048, device="cuda"))
+
+
+def test_moe_layer_decode_fused_equals_reference_launches():
+    """A MoE layer's decode step (src/layer_moe.cpp:80-159, 256 experts, top 8,
+    512-wide experts, 2048-wide shared expert) through the fused entry points (ten
+    launches, the expert ids staying on the device) against the reference's
+    sequence (router, top-k, host round trip and check, five calls per routed
+    expert, the shared expert's six calls): same routing, same output within fp32
+    tolerance, over three tokens."""
+    from qwen35_hip.decode_layers import MoeLayerDecode
+
+    r = rng(39)
+    dm, E, k, I, S = 2048, 256, 8, 512, 2048
+
+    def q4(M, K, s):
+        return dev(synth.q4k_table(M, K, seed_tensor=s))
+    ws = [q4(E, dm, 60), q4(E * I, dm, 61), q4(E * I, dm, 62), q4(E * dm, I, 63), q4(1, dm, 64), q4(S, dm, 65),
+          q4(S, dm, 66), q4(dm, S, 67)]
+    ref, fus = MoeLayerDecode(*ws), MoeLayerDecode(*ws)
+    for t in range(3):
+        x = dev((0.05 * r.standard_normal(dm)).astype(F32))
+        o_ref = host(ref.forward_reference_launches(x, torch.empty(dm, device="cuda")))
+        o_fus = host(fus.forward(x, torch.empty(dm, device="cuda")))
+        assert np.array_equal(host(fus.top_idx), host(ref.top_idx)), f"token {t} routing"
+        assert len(set(host(fus.top_idx).tolist())) == k
+        assert_f32_close(o_fus, o_ref, group=dm, what=f"token {t} output")
+
+
 def test_gdn_recurrent_rejects_wide_values():
     from qwen35_hip._lib import QwenError
 
