@@ -272,6 +272,39 @@ int qwen_moe_expert_matmul(const void* weight, int type, uint64_t num_elements, 
                            int n_experts, const int32_t* idx, int n_sel, const float* x,
                            int64_t x_stride, float* y, int M, int K, void* stream);
 
+/* The routed experts' gate and up projections of one token in one launch (the
+ * reference's 2 x n_sel matmul_dispatch calls, src/layer_moe.cpp:131-132):
+ * gate_out[j] = Wg_e x, up_out[j] = Wu_e x, e = idx[j] (on the device), j < n_sel;
+ * gate_out, up_out [n_sel x M]. Both tensors of one type and element count, expert e
+ * at element offset e * expert_stride. Bit-equal to two qwen_moe_expert_matmul calls
+ * (x_stride 0); an id outside [0, n_experts) gives NaN rows. */
+int qwen_moe_expert_gate_up(const void* w_gate, const void* w_up, int type, uint64_t num_elements,
+                            uint64_t expert_stride, int n_experts, const int32_t* idx, int n_sel,
+                            const float* x, float* gate_out, float* up_out, int M, int K, void* stream);
+
+/* The rest of a MoE layer's decode step after the gate / up projections,
+ * src/layer_moe.cpp:133-147 (SiLU x up and the down projection per routed expert,
+ * moe_add from a zeroed accumulator in routing order, the shared expert's SiLU x up
+ * and down projection, the sigmoid-gated shared add):
+ *   out = sum_j weights[j] * Wd_e (SiLU(gate[j]) * up[j])      (e = idx[j], j < n_sel)
+ *       + sigmoid(shared_logit[0]) * Wsd (SiLU(shared_gate) * shared_up)
+ * gate, up [n_sel x inter]; shared_gate, shared_up [shared_dim]; out [d_model]
+ * (written, not accumulated). Down expert e at element offset e * expert_stride.
+ * One launch for inter = 512, shared_dim a multiple of 2048 up to 4096, n_sel <= 8
+ * and Q4_K / Q6_K weights; other shapes run the same steps as separate launches
+ * through `workspace`, which must hold qwen_moe_down_combine_workspace_bytes() bytes
+ * in every case. Bit-equal to the separate calls (qwen_moe_silu_mul,
+ * qwen_moe_expert_matmul, qwen_matmul_dispatch, qwen_moe_weighted_sum_rows into a
+ * zeroed out, qwen_moe_shared_add_rows); an invalid expert id makes out NaN. No
+ * counterpart entry point in the reference (it fuses the calls cited above). */
+size_t qwen_moe_down_combine_workspace_bytes(int n_sel, int inter, int shared_dim, int d_model);
+int qwen_moe_down_combine(const void* w_down, int down_type, uint64_t down_elements, uint64_t expert_stride,
+                          int n_experts, const int32_t* idx, const float* weights, int n_sel,
+                          const float* gate, const float* up, int inter, const void* w_shared_down,
+                          int shared_type, uint64_t shared_elements, const float* shared_gate,
+                          const float* shared_up, int shared_dim, const float* shared_logit, float* out,
+                          int d_model, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ====================================================================== MoE
  * h = silu(g) * u (fp32).  ref: src/layer_moe.cpp:10 (moe_silu_mul decl),
  * src/cuda/moe.cu:61-72 */

@@ -258,6 +258,37 @@ void cpu_checks() {
                  "GEMV shape exceeds tensor 'blk.0.attn_q.weight'", "matmul_dispatch offset past the end");
     expect_throw([&] { qwen::matmul_dispatch(wq, dummy.data(), dummy.data(), 0, 512); },
                  "GEMV shape exceeds tensor 'blk.0.attn_q.weight'", "matmul_dispatch M = 0");
+    // the fused MoE entry points name the tensor the reference's separate calls would
+    qwen::QuantTensor wg = wq, wu = wq, wd = wq, wsd = wq;
+    wg.name = "blk.0.ffn_gate_exps.weight";
+    wu.name = "blk.0.ffn_up_exps.weight";
+    wd.name = "blk.0.ffn_down_exps.weight";
+    wsd.name = "blk.0.ffn_down_shexp.weight";
+    wg.num_elements = wu.num_elements = wd.num_elements = 4 * 2 * 512;    // 4 experts of 2 x 512
+    wsd.num_elements = 2 * 512;
+    wu.device_ptr = nullptr;
+    const int32_t* no_ids = nullptr;
+    expect_throw([&] { qwen::moe_expert_gate_up(wg, wu, 1024, 4, no_ids, 2, dummy.data(), dummy.data(), dummy.data(),
+                                                2, 512); },
+                 "tensor 'blk.0.ffn_up_exps.weight' is not loaded", "moe_expert_gate_up unloaded up tensor");
+    wu.device_ptr = dummy.data();
+    expect_throw([&] { qwen::moe_expert_gate_up(wg, wu, 1024, 4, no_ids, 2, dummy.data(), dummy.data(), dummy.data(),
+                                                3, 512); },
+                 "GEMV shape exceeds tensor 'blk.0.ffn_gate_exps.weight'", "moe_expert_gate_up rows past the expert");
+    wsd.device_ptr = nullptr;
+    expect_throw([&] { qwen::moe_down_combine(wd, 1024, 4, no_ids, dummy.data(), 2, dummy.data(), dummy.data(), 512, wsd,
+                                              dummy.data(), dummy.data(), 512, dummy.data(), dummy.data(), 2,
+                                              dummy.data(), 1 << 20); },
+                 "tensor 'blk.0.ffn_down_shexp.weight' is not loaded", "moe_down_combine unloaded shared tensor");
+    wsd.device_ptr = dummy.data();
+    expect_throw([&] { qwen::moe_down_combine(wd, 1024, 4, no_ids, dummy.data(), 2, dummy.data(), dummy.data(), 512, wsd,
+                                              dummy.data(), dummy.data(), 1024, dummy.data(), dummy.data(), 2,
+                                              dummy.data(), 1 << 20); },
+                 "GEMV shape exceeds tensor 'blk.0.ffn_down_shexp.weight'", "moe_down_combine shared rows past the end");
+    expect_throw([&] { qwen::moe_down_combine(wd, 1024, 4, no_ids, dummy.data(), 2, dummy.data(), dummy.data(), 1024,
+                                              wsd, dummy.data(), dummy.data(), 512, dummy.data(), dummy.data(), 2,
+                                              dummy.data(), 1 << 20); },
+                 "GEMV shape exceeds tensor 'blk.0.ffn_down_exps.weight'", "moe_down_combine expert rows past the end");
     expect(qwen::calculate_tensor_bytes(qwen::GgmlType::Q4_K, 2048) == 8 * 144 &&
                qwen::calculate_tensor_bytes(qwen::GgmlType::Q6_K, 100) == 0,
            "calculate_tensor_bytes");

@@ -67,15 +67,32 @@ struct LaneX {
     float s[4];    // sums of x per scale run (Q4_K: s[0], s[1]; Q6_K: 32*sum per quarter)
 };
 
-template <int TYPE>
-__device__ __forceinline__ void load_lane_x(LaneX<TYPE>& lx, const float* __restrict__ x, int xb, int j) {
-    const float* xblk = x + static_cast<size_t>(xb) * 256;
+// Sources of x: a vector in memory, or SiLU(g) * u evaluated at load time
+// (the same per-element expression as the moe_silu_mul kernel, so the values
+// have the bits of that kernel's output).
+struct PlainX {
+    const float* x;
+    __device__ __forceinline__ float4 operator()(size_t i) const { return ld4(x + i); }
+};
+struct SiluMulX {
+    const float* g;
+    const float* u;
+    __device__ __forceinline__ float4 operator()(size_t i) const {
+        const float4 s = silu4(ld4(g + i));
+        const float4 b = ld4(u + i);
+        return make_float4(s.x * b.x, s.y * b.y, s.z * b.z, s.w * b.w);
+    }
+};
+
+template <int TYPE, class XS>
+__device__ __forceinline__ void load_lane_x_from(LaneX<TYPE>& lx, const XS& xs, int xb, int j) {
+    const size_t xblk = static_cast<size_t>(xb) * 256;
     if constexpr (TYPE == kQ4_K) {
-        const float* lo = xblk + 64 * (j >> 1) + 16 * (j & 1);
+        const size_t lo = xblk + 64 * (j >> 1) + 16 * (j & 1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            lx.v[i] = ld4(lo + 4 * i);
-            lx.v[4 + i] = ld4(lo + 32 + 4 * i);
+            lx.v[i] = xs(lo + 4 * i);
+            lx.v[4 + i] = xs(lo + 32 + 4 * i);
         }
         float a = 0.f, b = 0.f;
 #pragma unroll
@@ -87,11 +104,11 @@ __device__ __forceinline__ void load_lane_x(LaneX<TYPE>& lx, const float* __rest
         lx.s[1] = b;
         lx.s[2] = lx.s[3] = 0.f;
     } else {
-        const float* base = xblk + 128 * (j >> 2) + 8 * (j & 3);
+        const size_t base = xblk + 128 * (j >> 2) + 8 * (j & 3);
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
-            lx.v[2 * qq] = ld4(base + 32 * qq);
-            lx.v[2 * qq + 1] = ld4(base + 32 * qq + 4);
+            lx.v[2 * qq] = xs(base + 32 * qq);
+            lx.v[2 * qq + 1] = xs(base + 32 * qq + 4);
         }
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
@@ -99,6 +116,11 @@ __device__ __forceinline__ void load_lane_x(LaneX<TYPE>& lx, const float* __rest
             lx.s[qq] = 32.0f * (((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)));
         }
     }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void load_lane_x(LaneX<TYPE>& lx, const float* __restrict__ x, int xb, int j) {
+    load_lane_x_from<TYPE>(lx, PlainX{x}, xb, j);
 }
 
 // sum over the 4 bytes of `q` (unsigned) times 4 x values.
@@ -179,10 +201,11 @@ __device__ __forceinline__ float block_dot(const uint8_t* blk, const LaneX<TYPE>
     }
 }
 
-// Device-side expert selection (MoE): launch row blockIdx.y runs selected
-// expert idx[blockIdx.y] -- weight rows at element offset idx * stride -- on
-// x + blockIdx.y * x_stride, writing y + blockIdx.y * M. An id outside
-// [0, n_experts) gives a NaN row. idx == nullptr: a plain GEMV.
+// Device-side expert selection (MoE): selection slot j (the launch row
+// blockIdx.y, or half of it for the gate/up launch) runs selected expert
+// idx[j] -- weight rows at element offset idx * stride -- on x + j * x_stride,
+// writing y + j * M. An id outside [0, n_experts) gives a NaN row.
+// idx == nullptr: a plain GEMV.
 struct Experts {
     const int32_t* idx;
     int n_experts;
@@ -190,13 +213,12 @@ struct Experts {
     int64_t x_stride;
 };
 
-// Applies the selection of launch row blockIdx.y; false if the expert id is
-// invalid (the caller writes NaN rows).
-__device__ __forceinline__ bool select_expert(const Experts& ex, int M, int64_t& x_off, int64_t& y_off,
+// Applies the selection of slot j; false if the expert id is invalid (the
+// caller writes NaN rows).
+__device__ __forceinline__ bool select_expert(const Experts& ex, int j, int M, int64_t& x_off, int64_t& y_off,
                                               uint64_t& element_offset) {
     x_off = y_off = 0;
     if (!ex.idx) return true;
-    const int j = blockIdx.y;
     const int e = ex.idx[j];
     x_off = static_cast<int64_t>(j) * ex.x_stride;
     y_off = static_cast<int64_t>(j) * M;
@@ -211,7 +233,7 @@ __device__ __forceinline__ bool select_expert(const Experts& ex, int M, int64_t&
 template <int TYPE, int R>
 __device__ __forceinline__ void gemv_kquant_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                  float* __restrict__ y, int M, int nb, uint64_t ub0, int groups,
-                                                 uint64_t tensor_bytes, const Experts& ex) {
+                                                 uint64_t tensor_bytes, const Experts& ex, int sel) {
     constexpr int BB = KQuant<TYPE>::kBlockBytes;
     constexpr int UB = 8 * BB;             // unit bytes
     constexpr int CPU = UB / 16;           // 16-byte chunks per unit
@@ -227,7 +249,7 @@ __device__ __forceinline__ void gemv_kquant_body(const uint8_t* __restrict__ w, 
     const int P = packed ? 8 / nb : 1;     // rows per unit
     uint64_t eoff = 0;
     int64_t x_off, y_off;
-    const bool ok_e = select_expert(ex, M, x_off, y_off, eoff);
+    const bool ok_e = select_expert(ex, sel, M, x_off, y_off, eoff);
     x += x_off;
     y += y_off;
     if (!ok_e) {  // uniform per workgroup: no barrier is reached
@@ -297,7 +319,21 @@ template <int TYPE, int R>
 __global__ __launch_bounds__(kGemvBlock) void gemv_kquant(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                           float* __restrict__ y, int M, int nb, uint64_t ub0,
                                                           int groups, uint64_t tensor_bytes, Experts ex) {
-    gemv_kquant_body<TYPE, R>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex);
+    gemv_kquant_body<TYPE, R>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, blockIdx.y);
+}
+
+// The routed experts' gate and up projections of one token in one launch:
+// launch rows 0 .. n_sel-1 run the gate tensor, n_sel .. 2 n_sel-1 the up
+// tensor, each for selection slot blockIdx.y mod n_sel (uniform per workgroup).
+template <int TYPE, int R>
+__global__ __launch_bounds__(kGemvBlock) void gemv_kquant_gate_up(const uint8_t* __restrict__ wg,
+                                                                  const uint8_t* __restrict__ wu,
+                                                                  const float* __restrict__ x, float* __restrict__ yg,
+                                                                  float* __restrict__ yu, int M, int nb, int groups,
+                                                                  uint64_t tensor_bytes, Experts ex, int n_sel) {
+    const bool up = static_cast<int>(blockIdx.y) >= n_sel;
+    gemv_kquant_body<TYPE, R>(up ? wu : wg, x, up ? yu : yg, M, nb, 0, groups, tensor_bytes, ex,
+                              up ? static_cast<int>(blockIdx.y) - n_sel : static_cast<int>(blockIdx.y));
 }
 
 // Several matrices of one type against the same x (qwen_matmul_dispatch_multi):
@@ -320,7 +356,115 @@ template <int TYPE, int R>
 __global__ __launch_bounds__(kGemvBlock) void gemv_kquant_multi(const float* __restrict__ x, int nb, GemvMulti mu) {
     const GemvMat& m = mu.d[blockIdx.y];
     if (static_cast<int64_t>(blockIdx.x) * kGemvWaves * R >= m.groups) return;   // uniform per workgroup
-    gemv_kquant_body<TYPE, R>(m.w, x, m.y, m.M, nb, m.ub0, m.groups, m.tensor_bytes, Experts{nullptr, 0, 0, 0});
+    gemv_kquant_body<TYPE, R>(m.w, x, m.y, m.M, nb, m.ub0, m.groups, m.tensor_bytes, Experts{nullptr, 0, 0, 0}, 0);
+}
+
+// ------------------------------------------------------------ MoE down + combine
+// The rest of a MoE layer's decode step after the routed gate / up projections
+// (src/layer_moe.cpp:134-147) in one launch, for routed experts of inter = 512
+// (2 blocks per row: rows 4q .. 4q+3 of one expert are one 8-block unit) and
+// a shared expert of shared_dim = 2048 * SS. A workgroup owns output rows
+// 4q .. 4q+3; wave w
+//   * decodes the unit of rows 4q .. 4q+3 of routed expert j = w + 4t (t < KT)
+//     against x = SiLU(gate_j) * up_j, evaluated while x is loaded;
+//   * computes row 4q + w of the shared expert's down projection against
+//     x = SiLU(shared_gate) * shared_up;
+// with the per-row kernel's units, lane map and reductions, so each expert
+// output and the shared output have the bits of the separate launches (SiLU x
+// up, the expert GEMVs, the shared GEMV). Lanes 0..3 of wave 0 then combine
+// row 4q + lane in the reference's order (moe_add per expert from a zeroed
+// accumulator, then the gated shared add): acc = 0; acc = fma(w_j, e_j, acc)
+// for j < k; acc += shared * sigmoid(logit).
+constexpr int kDcInter = 512;
+
+template <int TE, int TS, int KT, int SS>
+__global__ __launch_bounds__(kGemvBlock) void moe_down_combine_kernel(
+        const uint8_t* __restrict__ wd, uint64_t expert_blocks, int n_experts, const int32_t* __restrict__ idx,
+        const float* __restrict__ wts, int k, const float* __restrict__ g, const float* __restrict__ u,
+        const uint8_t* __restrict__ wsd, const float* __restrict__ sg, const float* __restrict__ su,
+        const float* __restrict__ slogit, float* __restrict__ out) {
+    constexpr int BE = KQuant<TE>::kBlockBytes, BS = KQuant<TS>::kBlockBytes;
+    constexpr int CE = BE * 8 / 16, CS = BS * 8 / 16;   // 16-byte chunks per unit (72 or 105)
+    static_assert(CE > kWave && CE <= 2 * kWave && CS > kWave && CS <= 2 * kWave, "two chunks per lane");
+    constexpr int SLOT = KT * CE + SS * CS;
+    __shared__ uint4 stage[kGemvWaves][SLOT];
+    __shared__ float part[4 * KT][4];
+    __shared__ float spart[4];
+    const int lane = threadIdx.x & 63, w = wave_in_block();
+    const int b = lane >> 3, jj = lane & 7;
+    const int q = blockIdx.x;
+    const bool tail = lane + kWave < CE;
+
+    // Every unit's bytes requested before the first wait.
+    uint4 ce[KT][2], cs[SS][2];
+    bool valid[KT];
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+        const int j = w + 4 * t;
+        const int e = j < k ? idx[j] : 0;
+        valid[t] = e >= 0 && e < n_experts;
+        const uint8_t* unit = wd + (static_cast<uint64_t>(valid[t] ? e : 0) * expert_blocks + 8 * q) * BE;
+        ce[t][0] = ld16_nt(unit + 16 * lane);
+        ce[t][1] = tail ? ld16_nt(unit + 16 * (lane + kWave)) : make_uint4(0, 0, 0, 0);
+    }
+    const int row = 4 * q + w;
+#pragma unroll
+    for (int s = 0; s < SS; ++s) {
+        const uint8_t* unit = wsd + (static_cast<uint64_t>(row) * 8 * SS + 8 * s) * BS;
+        cs[s][0] = ld16_nt(unit + 16 * lane);
+        cs[s][1] = lane + kWave < CS ? ld16_nt(unit + 16 * (lane + kWave)) : make_uint4(0, 0, 0, 0);
+    }
+    LaneX<TE> lxe[KT];
+    LaneX<TS> lxs[SS];
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+        const int j = min(w + 4 * t, k - 1);
+        load_lane_x_from<TE>(lxe[t], SiluMulX{g + static_cast<size_t>(j) * kDcInter,
+                                              u + static_cast<size_t>(j) * kDcInter}, b & 1, jj);
+    }
+#pragma unroll
+    for (int s = 0; s < SS; ++s) load_lane_x_from<TS>(lxs[s], SiluMulX{sg, su}, 8 * s + b, jj);
+
+    uint4* slot = stage[w];
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+        slot[t * CE + lane] = ce[t][0];
+        if (tail) slot[t * CE + kWave + lane] = ce[t][1];
+    }
+#pragma unroll
+    for (int s = 0; s < SS; ++s) {
+        slot[KT * CE + s * CS + lane] = cs[s][0];
+        if (lane + kWave < CS) slot[KT * CE + s * CS + kWave + lane] = cs[s][1];
+    }
+    __syncthreads();
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(slot);
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+        float a = 0.f;
+        a += block_dot<TE>(base + t * CE * 16 + b * BE, lxe[t], jj);
+        a = group_sum<16>(a);
+        const int j = w + 4 * t;
+        if (j < k && (lane & 15) == 0) part[j][lane >> 4] = valid[t] ? a : __builtin_nanf("");
+    }
+    {
+        float a = 0.f;
+#pragma unroll
+        for (int s = 0; s < SS; ++s) a += block_dot<TS>(base + (KT * CE + s * CS) * 16 + b * BS, lxs[s], jj);
+        a = group_sum<64>(a);
+        if (lane == 0) spart[w] = a;
+    }
+    __syncthreads();
+    if (w == 0 && lane < 4) {
+        float acc = 0.f;
+        for (int j = 0; j < k; ++j) acc = __builtin_fmaf(wts[j], part[j][lane], acc);
+        const float sc = sigmoid(slogit[0]);
+        acc += spart[lane] * sc;
+        out[4 * q + lane] = acc;
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void fill_zero(float* __restrict__ p, int n) {
+    for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) p[i] = 0.f;
 }
 
 // Generic path (any supported type and shape): one wave per row, element-wise
@@ -332,7 +476,7 @@ __global__ __launch_bounds__(kBlock) void gemv_any(const uint8_t* __restrict__ w
     const int row = blockIdx.x * (kBlock / kWave) + wave_in_block();
     if (row >= M) return;
     int64_t x_off, y_off;
-    const bool ok_e = select_expert(ex, M, x_off, y_off, element_offset);
+    const bool ok_e = select_expert(ex, blockIdx.y, M, x_off, y_off, element_offset);
     x += x_off;
     y += y_off;
     if (!ok_e) {
@@ -871,6 +1015,66 @@ void launch_multi(const GemvMulti& mu, int n, const float* x, int nb, hipStream_
         launch_multi_r<TYPE, 1>(mu, n, x, nb, s);
 }
 
+template <int TYPE, int R>
+void launch_gate_up_r(const uint8_t* wg, const uint8_t* wu, const float* x, float* yg, float* yu, int M, int nb,
+                      int groups, uint64_t tensor_bytes, const Experts& ex, int n_sel, hipStream_t s) {
+    constexpr int CPU = KQuant<TYPE>::kBlockBytes * 8 / 16;
+    const size_t lds = static_cast<size_t>(kGemvWaves) * R * CPU * 16;
+    const int waves = (groups + R - 1) / R;
+    gemv_kquant_gate_up<TYPE, R><<<dim3(blocks_for(waves, kGemvWaves), 2 * n_sel), kGemvBlock, lds, s>>>(
+        wg, wu, x, yg, yu, M, nb, groups, tensor_bytes, ex, n_sel);
+}
+
+// Units per wave as dispatch_kquant picks them for the 2 n_sel matrices.
+template <int TYPE>
+void launch_gate_up(const uint8_t* wg, const uint8_t* wu, const float* x, float* yg, float* yu, int M, int nb,
+                    int groups, uint64_t tensor_bytes, const Experts& ex, int n_sel, hipStream_t s) {
+    const int64_t all = static_cast<int64_t>(groups) * 2 * n_sel;
+    if (all >= 4 * 4096)
+        launch_gate_up_r<TYPE, 4>(wg, wu, x, yg, yu, M, nb, groups, tensor_bytes, ex, n_sel, s);
+    else if (all >= 2 * 4096)
+        launch_gate_up_r<TYPE, 2>(wg, wu, x, yg, yu, M, nb, groups, tensor_bytes, ex, n_sel, s);
+    else
+        launch_gate_up_r<TYPE, 1>(wg, wu, x, yg, yu, M, nb, groups, tensor_bytes, ex, n_sel, s);
+}
+
+struct DownCombine {
+    const uint8_t* wd;
+    uint64_t expert_blocks;
+    int n_experts;
+    const int32_t* idx;
+    const float* wts;
+    int k;
+    const float *g, *u;
+    const uint8_t* wsd;
+    const float *sg, *su, *slogit;
+    float* out;
+    int d_model;
+};
+
+template <int TE, int TS, int KT, int SS>
+void launch_dc(const DownCombine& a, hipStream_t s) {
+    moe_down_combine_kernel<TE, TS, KT, SS><<<a.d_model / 4, kGemvBlock, 0, s>>>(
+        a.wd, a.expert_blocks, a.n_experts, a.idx, a.wts, a.k, a.g, a.u, a.wsd, a.sg, a.su, a.slogit, a.out);
+}
+
+template <int TE, int TS>
+void launch_dc_t(const DownCombine& a, int ss, hipStream_t s) {
+    if (a.k <= 4)
+        ss == 1 ? launch_dc<TE, TS, 1, 1>(a, s) : launch_dc<TE, TS, 1, 2>(a, s);
+    else
+        ss == 1 ? launch_dc<TE, TS, 2, 1>(a, s) : launch_dc<TE, TS, 2, 2>(a, s);
+}
+
+void launch_down_combine(const DownCombine& a, int te, int ts, int ss, hipStream_t s) {
+    if (te == kQ4_K)
+        ts == kQ4_K ? launch_dc_t<kQ4_K, kQ4_K>(a, ss, s) : launch_dc_t<kQ4_K, kQ6_K>(a, ss, s);
+    else
+        ts == kQ4_K ? launch_dc_t<kQ6_K, kQ4_K>(a, ss, s) : launch_dc_t<kQ6_K, kQ6_K>(a, ss, s);
+}
+
+inline size_t align16(size_t n) { return (n + 15) / 16 * 16; }
+
 }  // namespace
 }  // namespace qk
 
@@ -911,6 +1115,107 @@ int qwen_moe_expert_matmul(const void* weight, int type, uint64_t num_elements, 
                        "moe_expert_matmul");
 }
 
+
+int qwen_moe_expert_gate_up(const void* w_gate, const void* w_up, int type, uint64_t num_elements,
+                            uint64_t expert_stride, int n_experts, const int32_t* idx, int n_sel, const float* x,
+                            float* gate_out, float* up_out, int M, int K, void* stream) {
+    if (!w_gate || !w_up) return fail(QWEN_STATUS_INVALID_ARGUMENT, "tensor is not loaded");
+    if (!type_supported(type)) return fail(QWEN_STATUS_UNSUPPORTED_TYPE, "unsupported GGML type %d", type);
+    QK_REQUIRE(n_sel >= 0 && n_experts > 0, "moe_expert_gate_up: bad n_sel %d / n_experts %d", n_sel, n_experts);
+    if (M <= 0 || K <= 0 || static_cast<uint64_t>(M) * static_cast<uint64_t>(K) > expert_stride ||
+        expert_stride > num_elements / static_cast<uint64_t>(n_experts))
+        return fail(QWEN_STATUS_OUT_OF_RANGE, "GEMV shape exceeds tensor (M=%d, K=%d, %d experts)", M, K, n_experts);
+    if (n_sel == 0) return ok();
+    QK_REQUIRE(idx && x && gate_out && up_out, "moe_expert_gate_up: null pointer");
+    QK_REQUIRE(n_sel <= 32767, "moe_expert_gate_up: n_sel %d too large", n_sel);
+    const hipStream_t s = as_stream(stream);
+    const auto* wg = static_cast<const uint8_t*>(w_gate);
+    const auto* wu = static_cast<const uint8_t*>(w_up);
+    const Experts ex{idx, n_experts, expert_stride, 0};
+    const int nb = K / 256;
+    const uint64_t tensor_bytes = (num_elements / 256) * static_cast<uint64_t>(block_bytes(type));
+    // The per-row kernel's conditions (launch_gemv, expert form) for both tensors.
+    const bool rowpath = (type == kQ4_K || type == kQ6_K) && K % 256 == 0 && (nb % 8 == 0 || 8 % nb == 0) &&
+                         num_elements % 256 == 0 && tensor_bytes % 16 == 0 && expert_stride % 256 == 0 &&
+                         aligned16(wg) && aligned16(wu) && aligned16(x) &&
+                         (type == kQ4_K || (expert_stride / 256) % 8 == 0);
+    if (!rowpath) {
+        const int rc = launch_gemv(wg, type, num_elements, x, gate_out, M, K, 0, ex, n_sel, s, "moe_expert_gate_up");
+        if (rc) return rc;
+        return launch_gemv(wu, type, num_elements, x, up_out, M, K, 0, ex, n_sel, s, "moe_expert_gate_up");
+    }
+    const int groups = nb >= 8 ? M : (M + 8 / nb - 1) / (8 / nb);
+    if (type == kQ4_K)
+        launch_gate_up<kQ4_K>(wg, wu, x, gate_out, up_out, M, nb, groups, tensor_bytes, ex, n_sel, s);
+    else
+        launch_gate_up<kQ6_K>(wg, wu, x, gate_out, up_out, M, nb, groups, tensor_bytes, ex, n_sel, s);
+    return check_launch("moe_expert_gate_up");
+}
+
+size_t qwen_moe_down_combine_workspace_bytes(int n_sel, int inter, int shared_dim, int d_model) {
+    if (n_sel < 0 || inter < 0 || shared_dim < 0 || d_model < 0) return 0;
+    const size_t f = sizeof(float);
+    return align16(f * n_sel * static_cast<size_t>(inter)) + align16(f * shared_dim) +
+           align16(f * n_sel * static_cast<size_t>(d_model)) + align16(f * d_model);
+}
+
+int qwen_moe_down_combine(const void* w_down, int down_type, uint64_t down_elements, uint64_t expert_stride,
+                          int n_experts, const int32_t* idx, const float* weights, int n_sel, const float* gate,
+                          const float* up, int inter, const void* w_shared_down, int shared_type,
+                          uint64_t shared_elements, const float* shared_gate, const float* shared_up, int shared_dim,
+                          const float* shared_logit, float* out, int d_model, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+    if (!w_down || !w_shared_down) return fail(QWEN_STATUS_INVALID_ARGUMENT, "tensor is not loaded");
+    if (!type_supported(down_type)) return fail(QWEN_STATUS_UNSUPPORTED_TYPE, "unsupported GGML type %d", down_type);
+    if (!type_supported(shared_type))
+        return fail(QWEN_STATUS_UNSUPPORTED_TYPE, "unsupported GGML type %d", shared_type);
+    QK_REQUIRE(n_sel > 0 && n_sel <= 64 && n_experts > 0, "moe_down_combine: bad n_sel %d / n_experts %d", n_sel,
+               n_experts);
+    if (d_model <= 0 || inter <= 0 ||
+        static_cast<uint64_t>(d_model) * static_cast<uint64_t>(inter) > expert_stride ||
+        expert_stride > down_elements / static_cast<uint64_t>(n_experts))
+        return fail(QWEN_STATUS_OUT_OF_RANGE, "GEMV shape exceeds tensor (M=%d, K=%d, %d experts)", d_model, inter,
+                    n_experts);
+    if (shared_dim <= 0 || static_cast<uint64_t>(d_model) * static_cast<uint64_t>(shared_dim) > shared_elements)
+        return fail(QWEN_STATUS_OUT_OF_RANGE, "GEMV shape exceeds tensor (M=%d, K=%d)", d_model, shared_dim);
+    QK_REQUIRE(idx && weights && gate && up && shared_gate && shared_up && shared_logit && out && workspace,
+               "moe_down_combine: null pointer");
+    const size_t need = qwen_moe_down_combine_workspace_bytes(n_sel, inter, shared_dim, d_model);
+    QK_REQUIRE(workspace_bytes >= need, "moe_down_combine: workspace of %zu bytes, need %zu", workspace_bytes, need);
+    const hipStream_t s = as_stream(stream);
+    const auto* wd = static_cast<const uint8_t*>(w_down);
+    const auto* wsd = static_cast<const uint8_t*>(w_shared_down);
+    const auto kq = [](int t) { return t == kQ4_K || t == kQ6_K; };
+    const bool fused = kq(down_type) && kq(shared_type) && inter == kDcInter && shared_dim % 2048 == 0 &&
+                       shared_dim <= 4096 && d_model % 4 == 0 && n_sel <= 8 && expert_stride % 2048 == 0 &&
+                       aligned16(wd) && aligned16(wsd) && aligned16(gate) && aligned16(up) &&
+                       aligned16(shared_gate) && aligned16(shared_up);
+    if (fused) {
+        const DownCombine a{wd, expert_stride / 256, n_experts, idx, weights, n_sel, gate, up, wsd, shared_gate,
+                            shared_up, shared_logit, out, d_model};
+        launch_down_combine(a, down_type, shared_type, shared_dim / 2048, s);
+        return check_launch("moe_down_combine");
+    }
+    // Other shapes: the same steps as separate launches through the workspace.
+    auto* hid = static_cast<float*>(workspace);
+    auto* shid = reinterpret_cast<float*>(reinterpret_cast<char*>(hid) + align16(4 * n_sel * static_cast<size_t>(inter)));
+    auto* eo = reinterpret_cast<float*>(reinterpret_cast<char*>(shid) + align16(4 * static_cast<size_t>(shared_dim)));
+    auto* so = reinterpret_cast<float*>(reinterpret_cast<char*>(eo) + align16(4 * n_sel * static_cast<size_t>(d_model)));
+    int rc = qwen_moe_silu_mul(gate, up, hid, n_sel * inter, stream);
+    if (!rc) rc = qwen_moe_silu_mul(shared_gate, shared_up, shid, shared_dim, stream);
+    if (!rc)
+        rc = launch_gemv(wd, down_type, down_elements, hid, eo, d_model, inter, 0,
+                         Experts{idx, n_experts, expert_stride, inter}, n_sel, s, "moe_down_combine");
+    if (!rc)
+        rc = launch_gemv(wsd, shared_type, shared_elements, shid, so, d_model, shared_dim, 0,
+                         Experts{nullptr, 0, 0, 0}, 1, s, "moe_down_combine");
+    if (rc) return rc;
+    fill_zero<<<blocks_for(d_model, kBlock), kBlock, 0, s>>>(out, d_model);
+    rc = check_launch("moe_down_combine");
+    if (!rc) rc = qwen_moe_weighted_sum_rows(out, eo, weights, 1, n_sel, d_model, stream);
+    if (!rc) rc = qwen_moe_shared_add_rows(out, so, shared_logit, 1, d_model, stream);
+    return rc;
+}
 
 int qwen_matmul_dispatch_multi(const qwen_gemv_desc* descs, int n, const float* x, int K, void* stream) {
     QK_REQUIRE(n >= 0 && n <= 64, "matmul_dispatch_multi: n = %d outside [0, 64]", n);

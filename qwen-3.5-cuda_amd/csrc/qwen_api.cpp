@@ -238,6 +238,61 @@ void moe_expert_matmul(const QuantTensor& w, uint64_t expert_stride, int n_exper
     check(status);
 }
 
+namespace {
+// matmul_dispatch's messages for tensor w (src/cuda/matmul_q4.cu:187-195).
+void throw_tensor_status(int status, const QuantTensor& w) {
+    if (status == QWEN_STATUS_INVALID_ARGUMENT && !w.device_ptr)
+        throw std::runtime_error("tensor '" + w.name + "' is not loaded");
+    if (status == QWEN_STATUS_UNSUPPORTED_TYPE)
+        throw std::runtime_error("unsupported GGML type for tensor '" + w.name + "'");
+    if (status == QWEN_STATUS_OUT_OF_RANGE) throw std::runtime_error("GEMV shape exceeds tensor '" + w.name + "'");
+}
+}  // namespace
+
+void moe_expert_gate_up(const QuantTensor& w_gate, const QuantTensor& w_up, uint64_t expert_stride, int n_experts,
+                        const int32_t* idx, int n_sel, const float* x, float* gate_out, float* up_out, int M, int K,
+                        hipStream_t stream) {
+    if (w_gate.type != w_up.type || w_gate.num_elements != w_up.num_elements) {
+        moe_expert_matmul(w_gate, expert_stride, n_experts, idx, n_sel, x, 0, gate_out, M, K, stream);
+        moe_expert_matmul(w_up, expert_stride, n_experts, idx, n_sel, x, 0, up_out, M, K, stream);
+        return;
+    }
+    const int status = qwen_moe_expert_gate_up(w_gate.device_ptr, w_up.device_ptr, static_cast<int>(w_gate.type),
+                                               w_gate.num_elements, expert_stride, n_experts, idx, n_sel, x, gate_out,
+                                               up_out, M, K, st(stream));
+    throw_tensor_status(status, w_gate.device_ptr && !w_up.device_ptr ? w_up : w_gate);
+    check(status);
+}
+
+size_t moe_down_combine_workspace_bytes(int n_sel, int inter, int shared_dim, int d_model) {
+    return qwen_moe_down_combine_workspace_bytes(n_sel, inter, shared_dim, d_model);
+}
+
+void moe_down_combine(const QuantTensor& w_down, uint64_t expert_stride, int n_experts, const int32_t* idx,
+                      const float* weights, int n_sel, const float* gate, const float* up, int inter,
+                      const QuantTensor& w_shared_down, const float* shared_gate, const float* shared_up,
+                      int shared_dim, const float* shared_logit, float* out, int d_model, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream) {
+    // Tensor checks in the order the reference's calls meet them: the routed
+    // down projection first, then the shared expert's.
+    for (const QuantTensor* w : {&w_down, &w_shared_down}) {
+        if (!w->device_ptr) throw std::runtime_error("tensor '" + w->name + "' is not loaded");
+        if (!matmul_type_supported(w->type))
+            throw std::runtime_error("unsupported GGML type for tensor '" + w->name + "'");
+    }
+    const int status = qwen_moe_down_combine(
+        w_down.device_ptr, static_cast<int>(w_down.type), w_down.num_elements, expert_stride, n_experts, idx, weights,
+        n_sel, gate, up, inter, w_shared_down.device_ptr, static_cast<int>(w_shared_down.type),
+        w_shared_down.num_elements, shared_gate, shared_up, shared_dim, shared_logit, out, d_model, workspace,
+        workspace_bytes, st(stream));
+    if (status == QWEN_STATUS_OUT_OF_RANGE) {
+        const bool routed = static_cast<uint64_t>(d_model) * static_cast<uint64_t>(inter) > expert_stride ||
+                            n_experts <= 0 || expert_stride > w_down.num_elements / static_cast<uint64_t>(n_experts);
+        throw std::runtime_error("GEMV shape exceeds tensor '" + (routed ? w_down : w_shared_down).name + "'");
+    }
+    check(status);
+}
+
 void matmul_dispatch_multi(const GemvJob* jobs, int n, const float* x, int K, hipStream_t stream) {
     if (n <= 0) return;
     std::vector<qwen_gemv_desc> d(static_cast<size_t>(n));

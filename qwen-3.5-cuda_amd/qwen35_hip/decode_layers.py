@@ -184,13 +184,12 @@ class MoeLayerDecode:
       out (:147): 8 + 5k launches and a host round trip;
     * `forward(x, out)`: the router and the three shared-expert projections of x
       in one `matmul_dispatch_multi`, top-k on the device, the k routed gate and up
-      projections as two `moe_expert_matmul` launches reading the ids on the
-      device, one SiLU x up over the routed and shared hidden rows together, the
-      routed down projections in one launch, the shared down projection, a zero
-      fill, the weighted sum of the k expert outputs and the gated shared add:
-      ten launches, no host round trip. The host-side routing check is the one
-      part this path leaves out (the top-k kernel's weights are a softmax, finite
-      and normalised by construction).
+      projections in one `moe_expert_gate_up` launch reading the ids on the
+      device, then `moe_down_combine`: SiLU x up, the routed and shared down
+      projections and the weighted, gated combine in one launch: four launches,
+      no host round trip. The host-side routing check is the one part this path
+      leaves out (the top-k kernel's weights are a softmax, finite and normalised
+      by construction).
     """
 
     def __init__(self, w_router, w_gate, w_up, w_down, w_sgate, w_sg, w_su, w_sd, *, wtype="Q4_K", d_model=2048,
@@ -213,6 +212,8 @@ class MoeLayerDecode:
         self.sgate = torch.empty(1, **f)
         self.shared_out = torch.empty(d_model, **f)
         self.accum = torch.empty(d_model, **f)
+        self.workspace = torch.empty(max(16, ops.moe_down_combine_workspace_bytes(k, inter, shared, d_model)),
+                                     dtype=torch.uint8, device=w_router.device)
         self.h_idx = torch.empty(k, dtype=torch.int32).pin_memory()
         self.h_w = torch.empty(k, dtype=torch.float32).pin_memory()
 
@@ -260,14 +261,10 @@ class MoeLayerDecode:
                              ("su", self.up_all[k * I:]))]
         ops.matmul_dispatch_multi(jobs, x, dm)
         ops.moe_topk_rows(self.router.view(1, E), k, idx=self.top_idx.view(1, k), weights=self.top_w.view(1, k))
-        for name, y in (("gate", self.gate_all), ("up", self.up_all)):
-            ops.moe_expert_matmul(self.experts_w[name], self.wtype, E * I * dm, I * dm, E, self.top_idx, x, 0, I, dm,
-                                  out=y[:k * I].view(k, I))
-        ops.moe_silu_mul(self.gate_all, self.up_all, out=self.hidden_all)
-        ops.moe_expert_matmul(self.experts_w["down"], self.wtype, E * dm * I, dm * I, E, self.top_idx,
-                              self.hidden_all, I, dm, I, out=self.expert_out)
-        self._proj("sd", self.hidden_all[k * I:], self.shared_out, S)
-        out.zero_()
-        ops.moe_weighted_sum_rows(out.view(1, dm), self.expert_out.view(1, k, dm), self.top_w.view(1, k))
-        ops.moe_shared_add_rows(out.view(1, dm), self.shared_out.view(1, dm), self.sgate)
+        ops.moe_expert_gate_up(self.experts_w["gate"], self.experts_w["up"], self.wtype, E * I * dm, I * dm, E,
+                               self.top_idx, x, I, dm, gate_out=self.gate_all[:k * I], up_out=self.up_all[:k * I])
+        ops.moe_down_combine(self.experts_w["down"], self.wtype, E * dm * I, dm * I, E, self.top_idx, self.top_w,
+                             self.gate_all, self.up_all, I, self.w["sd"][0], self.wtype, dm * S,
+                             self.gate_all[k * I:], self.up_all[k * I:], self.sgate, dm, out=out,
+                             workspace=self.workspace)
         return out

@@ -455,6 +455,63 @@ def moe_expert_matmul(weight, ggml_type, num_elements, expert_stride, n_experts,
     return out
 
 
+def moe_expert_gate_up(w_gate, w_up, ggml_type, num_elements, expert_stride, n_experts, idx, x, M, K, gate_out=None,
+                       up_out=None, stream=None):
+    """gate_out[j] = Wg_{idx[j]} x, up_out[j] = Wu_{idx[j]} x in one launch; [n_sel, M] each."""
+    _dev(w_gate, w_up, dtype=torch.uint8)
+    _dev(idx, dtype=torch.int32)
+    _dev(x, dtype=torch.float32)
+    t = GGML_TYPES[ggml_type] if isinstance(ggml_type, str) else int(ggml_type)
+    n_sel = idx.numel()
+    if x.numel() < K:
+        raise ValueError(f"x has {x.numel()} elements, K = {K}")
+    gate_out = torch.empty((n_sel, M), dtype=torch.float32, device=x.device) if gate_out is None else gate_out
+    up_out = torch.empty((n_sel, M), dtype=torch.float32, device=x.device) if up_out is None else up_out
+    _dev(gate_out, up_out, dtype=torch.float32)
+    if gate_out.numel() < n_sel * M or up_out.numel() < n_sel * M:
+        raise ValueError("outputs smaller than n_sel x M")
+    check(load().qwen_moe_expert_gate_up(_p(w_gate), _p(w_up), t, num_elements, expert_stride, n_experts, _p(idx),
+                                         n_sel, _p(x), _p(gate_out), _p(up_out), M, K, _stream(stream)))
+    return gate_out, up_out
+
+
+def moe_down_combine_workspace_bytes(n_sel, inter, shared_dim, d_model) -> int:
+    return int(load().qwen_moe_down_combine_workspace_bytes(n_sel, inter, shared_dim, d_model))
+
+
+def moe_down_combine(w_down, down_type, down_elements, expert_stride, n_experts, idx, weights, gate, up, inter,
+                     w_shared_down, shared_type, shared_elements, shared_gate, shared_up, shared_logit, d_model,
+                     out=None, workspace=None, stream=None):
+    """out [d_model] = sum_j weights[j] Wd_{idx[j]} (SiLU(gate[j]) * up[j])
+    + sigmoid(shared_logit[0]) Wsd (SiLU(shared_gate) * shared_up)."""
+    _dev(w_down, w_shared_down, dtype=torch.uint8)
+    _dev(idx, dtype=torch.int32)
+    _dev(weights, gate, up, shared_gate, shared_up, shared_logit, dtype=torch.float32)
+    n_sel = idx.numel()
+    _same((n_sel,), weights)
+    if gate.numel() < n_sel * inter or up.numel() < n_sel * inter:
+        raise ValueError("gate / up smaller than n_sel x inter")
+    shared_dim = shared_gate.numel()
+    _same((shared_dim,), shared_up)
+    if shared_logit.numel() < 1:
+        raise ValueError("shared_logit is empty")
+    td = GGML_TYPES[down_type] if isinstance(down_type, str) else int(down_type)
+    ts = GGML_TYPES[shared_type] if isinstance(shared_type, str) else int(shared_type)
+    nbytes = moe_down_combine_workspace_bytes(n_sel, inter, shared_dim, d_model)
+    if workspace is None:
+        workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=gate.device)
+    _dev(workspace)
+    out = torch.empty(d_model, dtype=torch.float32, device=gate.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    if out.numel() < d_model:
+        raise ValueError("out smaller than d_model")
+    check(load().qwen_moe_down_combine(_p(w_down), td, down_elements, expert_stride, n_experts, _p(idx), _p(weights),
+                                       n_sel, _p(gate), _p(up), inter, _p(w_shared_down), ts, shared_elements,
+                                       _p(shared_gate), _p(shared_up), shared_dim, _p(shared_logit), _p(out), d_model,
+                                       _p(workspace), workspace.numel() * workspace.element_size(), _stream(stream)))
+    return out
+
+
 # ------------------------------------------------------------------ MoE
 def moe_silu_mul(g, u, out=None, stream=None):
     _dev(g, u, dtype=torch.float32)

@@ -638,7 +638,7 @@ def test_attn_layer_decode_rejects_position_past_context():
 
 def test_moe_layer_decode_fused_equals_reference_launches():
     """A MoE layer's decode step (src/layer_moe.cpp:80-159, 256 experts, top 8,
-    512-wide experts, 2048-wide shared expert) through the fused entry points (ten
+    512-wide experts, 2048-wide shared expert) through the fused entry points (four
     launches, the expert ids staying on the device) against the reference's
     sequence (router, top-k, host round trip and check, five calls per routed
     expert, the shared expert's six calls): same routing, same output within fp32
@@ -847,6 +847,89 @@ def test_moe_expert_matmul(oracle, kind, M, K):
     got0 = host(ops.moe_expert_matmul(dev(table), t, n_el, M * K, E, dev(ids[:3]), dev(xs[0]), 0, M, K))
     ref0 = oracle.moe_expert_gemv(table, t, ids[:3], E, M * K, xs[0], 0, M, K)
     assert_f32_close(got0, ref0, group=M, what=f"{kind} shared x")
+
+
+@pytest.mark.parametrize("kind,M,K", [("Q4_K", 512, 2048), ("Q6_K", 512, 2048), ("Q4_K", 256, 4096),
+                                      ("Q8_0", 96, 512)])
+def test_moe_expert_gate_up_equals_two_expert_matmuls(kind, M, K):
+    """The routed gate and up projections in one launch give the bits of two
+    moe_expert_matmul calls (x_stride 0), invalid ids included (NaN rows); Q8_0
+    takes the generic kernel inside the same entry point."""
+    t = ops.GGML_TYPES[kind]
+    E = 12
+    r = rng(M + K + t + 1)
+    tg, tu = (dev(_gemv_weight(kind, E * M, K, r)) for _ in range(2))
+    n_el = E * M * K
+    ids = dev(np.array([7, 0, 11, 3, 12, 5, -1, 9], np.int32))
+    x = dev(r.standard_normal(K).astype(F32))
+    g, u = ops.moe_expert_gate_up(tg, tu, t, n_el, M * K, E, ids, x, M, K)
+    g_ref = ops.moe_expert_matmul(tg, t, n_el, M * K, E, ids, x, 0, M, K)
+    u_ref = ops.moe_expert_matmul(tu, t, n_el, M * K, E, ids, x, 0, M, K)
+    assert_bits_equal(host(g), host(g_ref), what=f"{kind} gate")
+    assert_bits_equal(host(u), host(u_ref), what=f"{kind} up")
+    assert np.isnan(host(g)[6]).all() and np.isnan(host(u)[6]).all()
+
+
+def _down_combine_separate(wd, td, nd, stride, E, ids, wts, g, u, inter, wsd, tsd, nsd, sg, su, logit, dm):
+    """The separate calls the fused entry point replaces (src/layer_moe.cpp:133-147)."""
+    k = ids.numel()
+    hid = ops.moe_silu_mul(g.reshape(-1)[:k * inter], u.reshape(-1)[:k * inter])
+    shid = ops.moe_silu_mul(sg, su)
+    eo = ops.moe_expert_matmul(wd, td, nd, stride, E, ids, hid, inter, dm, inter)
+    so = ops.matmul_dispatch(wsd, tsd, nsd, shid, dm, sg.numel())
+    out = torch.zeros(dm, device="cuda")
+    ops.moe_weighted_sum_rows(out.view(1, dm), eo.view(1, k, dm), wts.view(1, k))
+    ops.moe_shared_add_rows(out.view(1, dm), so.view(1, dm), logit)
+    return out
+
+
+@pytest.mark.parametrize("td,tsd,k,inter,S,dm", [
+    ("Q4_K", "Q4_K", 8, 512, 2048, 2048),    # the model's shapes: one launch
+    ("Q6_K", "Q4_K", 8, 512, 2048, 2048),
+    ("Q4_K", "Q6_K", 5, 512, 4096, 1024),    # 5 experts (a partly idle wave), 2-slice shared rows
+    ("Q6_K", "Q6_K", 3, 512, 2048, 512),
+    ("Q4_K", "Q4_K", 8, 1024, 1024, 768),   # other shapes: separate launches through the workspace
+    ("Q4_K", "Q6_K", 8, 512, 2048, 998),
+])
+def test_moe_down_combine_equals_separate_calls(td, tsd, k, inter, S, dm):
+    """SiLU x up, the routed down projections, the shared expert and the
+    weighted, gated combine in one entry point give the bits of the separate
+    calls, for the fused kernel's shapes and for the fallback's."""
+    r = rng(k * 1000 + inter + S + dm)
+    E = 16
+    stride = dm * inter
+    wd = dev(_gemv_weight(td, E * dm, inter, r))
+    wsd = dev(_gemv_weight(tsd, dm, S, r))
+    nd, nsd = E * stride, dm * S
+    ids = dev(r.permutation(E)[:k].astype(np.int32))
+    w = r.uniform(0.1, 1, k).astype(F32)
+    wts = dev(w / w.sum())
+    g, u = dev(r.standard_normal((k, inter)).astype(F32)), dev(r.standard_normal((k, inter)).astype(F32))
+    g[0, :5] = torch.tensor([-50.0, -41.0, 0.0, 30.0, -39.5])   # SiLU's exact-form range
+    sg, su = dev(r.standard_normal(S).astype(F32)), dev(r.standard_normal(S).astype(F32))
+    logit = dev(np.array([0.3], F32))
+    got = ops.moe_down_combine(wd, td, nd, stride, E, ids, wts, g, u, inter, wsd, tsd, nsd, sg, su, logit, dm)
+    ref = _down_combine_separate(wd, ops.GGML_TYPES[td], nd, stride, E, ids, wts, g, u, inter, wsd,
+                                 ops.GGML_TYPES[tsd], nsd, sg, su, logit, dm)
+    assert_bits_equal(host(got), host(ref), what=f"{td}/{tsd} k={k} inter={inter} S={S} dm={dm}")
+    # an invalid expert id makes the output NaN, as the separate calls' NaN row does
+    bad = ids.clone()
+    bad[k - 1] = E
+    got = host(ops.moe_down_combine(wd, td, nd, stride, E, bad, wts, g, u, inter, wsd, tsd, nsd, sg, su, logit, dm))
+    assert np.isnan(got).all()
+
+
+def test_moe_down_combine_rejects_small_workspace():
+    from qwen35_hip._lib import QwenError
+
+    t = dev(synth.q4k_table(16 * 2048, 512, seed_tensor=1))
+    ts = dev(synth.q4k_table(2048, 2048, seed_tensor=2))
+    z = torch.zeros(8 * 2048, device="cuda")
+    ids = torch.zeros(8, dtype=torch.int32, device="cuda")
+    ws = torch.empty(64, dtype=torch.uint8, device="cuda")
+    with pytest.raises(QwenError, match="workspace of 64 bytes"):
+        ops.moe_down_combine(t, "Q4_K", t.numel() // 144 * 256, 2048 * 512, 16, ids, z[:8], z, z, 512, ts, "Q4_K",
+                             2048 * 2048, z[:2048], z[:2048], z[:1], 2048, workspace=ws)
 
 
 # ------------------------------------------------------------------ quantized GEMV
