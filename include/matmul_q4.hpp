@@ -60,6 +60,9 @@ struct GemvJob {
     float* y;
     int M;
     uint64_t element_offset = 0;
+    // s > 0: write the rows in attn_split_qg's layout (pairs of s-row halves,
+    // first halves to y[0, M/2), second halves to y[M/2, M)), M % (2 s) == 0.
+    int split = 0;
 };
 void matmul_dispatch_multi(const GemvJob* jobs, int n, const float* x, int K, hipStream_t stream = nullptr);
 

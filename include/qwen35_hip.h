@@ -380,6 +380,11 @@ typedef struct qwen_gemv_desc {
     uint64_t num_elements;    /* elements of the tensor */
     uint64_t element_offset;  /* first element of row 0 */
     float* y;                 /* output, fp32 [M] */
+    int split;                /* 0: y[m] = row m. s > 0: the rows are M / (2 s) pairs of s-row
+                                 halves (attention's fused query | gate projection, one pair per
+                                 head) written as y[0 .. M/2) = the first halves, y[M/2 .. M) =
+                                 the second: the projection followed by attn_split_qg
+                                 (src/layer_attn.cpp:85,90), bit for bit. M % (2 s) == 0. */
 } qwen_gemv_desc;
 
 /* n GEMVs of the same x (K elements): y_j = W_j x for each descriptor, with the

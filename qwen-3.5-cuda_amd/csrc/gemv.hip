@@ -227,13 +227,24 @@ __device__ __forceinline__ bool select_expert(const Experts& ex, int j, int M, i
     return true;
 }
 
+// Output index of GEMV row m. split > 0: the rows are M / (2 split) pairs of
+// split-row halves (the fused query | gate projection of attention, one pair
+// per head) and the first halves go to y[0, M/2), the second halves to
+// y[M/2, M): the layout attn_split_qg produces (src/cuda/attn_kernels.cu:16-24).
+__device__ __forceinline__ int64_t out_index(int64_t m, int M, int split) {
+    if (split <= 0) return m;
+    const int64_t pair = m / (2 * split), r = m - pair * 2 * split;
+    return r < split ? pair * split + r : M / 2 + pair * split + (r - split);
+}
+
 // Fast path. Row groups: when 8 | nb, group = one row and unit (row, slice s)
 // starts at block ub0 + row*nb + 8s; when nb | 8, group = 8/nb rows (P) and
 // unit u starts at block ub0 + 8u. A wave owns groups g0 .. g0+R-1.
 template <int TYPE, int R>
 __device__ __forceinline__ void gemv_kquant_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                  float* __restrict__ y, int M, int nb, uint64_t ub0, int groups,
-                                                 uint64_t tensor_bytes, const Experts& ex, int sel) {
+                                                 uint64_t tensor_bytes, const Experts& ex, int sel,
+                                                 int split = 0) {
     constexpr int BB = KQuant<TYPE>::kBlockBytes;
     constexpr int UB = 8 * BB;             // unit bytes
     constexpr int CPU = UB / 16;           // 16-byte chunks per unit
@@ -299,7 +310,7 @@ __device__ __forceinline__ void gemv_kquant_body(const uint8_t* __restrict__ w, 
             const float t = group_sum<64>(acc[u]);
             if (lane == u) out = t;
         }
-        if (lane < R && g0 + lane < M) y[g0 + lane] = out;
+        if (lane < R && g0 + lane < M) y[out_index(g0 + lane, M, split)] = out;
     } else {
         // Lanes 8*nb*p .. 8*nb*(p+1)-1 hold row P*g + p.
         const int gl = 8 * nb;
@@ -310,7 +321,7 @@ __device__ __forceinline__ void gemv_kquant_body(const uint8_t* __restrict__ w, 
             else if (gl == 16) t = group_sum<16>(acc[u]);
             else t = group_sum<32>(acc[u]);
             const int row = (g0 + u) * P + lane / gl;
-            if (lane % gl == 0 && g0 + u < groups && row < M) y[row] = t;
+            if (lane % gl == 0 && g0 + u < groups && row < M) y[out_index(row, M, split)] = t;
         }
     }
 }
@@ -347,6 +358,7 @@ struct GemvMat {
     uint64_t tensor_bytes;  // bytes of the whole tensor
     int M;
     int groups;
+    int split;              // out_index layout (0: y[m] = row m)
 };
 struct GemvMulti {
     GemvMat d[kMultiMax];
@@ -356,7 +368,8 @@ template <int TYPE, int R>
 __global__ __launch_bounds__(kGemvBlock) void gemv_kquant_multi(const float* __restrict__ x, int nb, GemvMulti mu) {
     const GemvMat& m = mu.d[blockIdx.y];
     if (static_cast<int64_t>(blockIdx.x) * kGemvWaves * R >= m.groups) return;   // uniform per workgroup
-    gemv_kquant_body<TYPE, R>(m.w, x, m.y, m.M, nb, m.ub0, m.groups, m.tensor_bytes, Experts{nullptr, 0, 0, 0}, 0);
+    gemv_kquant_body<TYPE, R>(m.w, x, m.y, m.M, nb, m.ub0, m.groups, m.tensor_bytes, Experts{nullptr, 0, 0, 0}, 0,
+                              m.split);
 }
 
 // ------------------------------------------------------------ MoE down + combine
@@ -471,7 +484,7 @@ __global__ __launch_bounds__(kBlock) void fill_zero(float* __restrict__ p, int n
 // decode.
 __global__ __launch_bounds__(kBlock) void gemv_any(const uint8_t* __restrict__ w, int type,
                                                    const float* __restrict__ x, float* __restrict__ y, int M, int K,
-                                                   uint64_t element_offset, Experts ex) {
+                                                   uint64_t element_offset, Experts ex, int split) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * (kBlock / kWave) + wave_in_block();
     if (row >= M) return;
@@ -487,7 +500,7 @@ __global__ __launch_bounds__(kBlock) void gemv_any(const uint8_t* __restrict__ w
     float s = 0.f;
     for (int k = lane; k < K; k += kWave) s = __builtin_fmaf(dequant_elem(w, type, base + k), x[k], s);
     s = group_sum<64>(s);
-    if (lane == 0) y[row] = s;
+    if (lane == 0) y[out_index(row, M, split)] = s;
 }
 
 // ------------------------------------------------------------------ MFMA path
@@ -972,21 +985,23 @@ int launch_gemv(const uint8_t* w, int type, uint64_t num_elements, const float* 
             dispatch_kquant<kQ6_K>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, n_sel, s);
     } else {
         gemv_any<<<dim3(blocks_for(M, kBlock / kWave), n_sel), kBlock, 0, s>>>(w, type, x, y, M, K, element_offset,
-                                                                             ex);
+                                                                             ex, 0);
     }
     return check_launch(what);
 }
 
 
 // Whether a plain GEMV of this matrix takes the per-row kernel (the same
-// conditions as launch_gemv without expert selection).
+// conditions as launch_gemv without expert selection). A split output layout
+// (out_index) takes it whenever the shape allows, large or not.
 bool kquant_rowpath(const uint8_t* w, int type, uint64_t num_elements, const float* x, int M, int K,
-                    uint64_t element_offset) {
+                    uint64_t element_offset, bool split = false) {
     if (type != kQ4_K && type != kQ6_K) return false;
     const int nb = K / 256;
     const uint64_t tensor_bytes = (num_elements / 256) * static_cast<uint64_t>(block_bytes(type));
     int S = 0, bpw = 0;
-    if (K % 256 == 0 && mfma_split(nb, S, bpw) && element_offset % 256 == 0 && mfma_large(type, M)) return false;
+    if (!split && K % 256 == 0 && mfma_split(nb, S, bpw) && element_offset % 256 == 0 && mfma_large(type, M))
+        return false;
     const bool shape_ok = K % 256 == 0 && (nb % 8 == 0 || 8 % nb == 0) && element_offset % 256 == 0 &&
                           num_elements % 256 == 0 && tensor_bytes % 16 == 0;
     const bool aligned = aligned16(w) && aligned16(x) && (type == kQ4_K || (element_offset / 256) % 8 == 0);
@@ -1231,6 +1246,8 @@ int qwen_matmul_dispatch_multi(const qwen_gemv_desc* descs, int n, const float* 
             static_cast<uint64_t>(e.M) * static_cast<uint64_t>(K) > e.num_elements - e.element_offset)
             return fail(QWEN_STATUS_OUT_OF_RANGE, "descriptor %d: GEMV shape exceeds tensor (M=%d, K=%d)", j, e.M, K);
         QK_REQUIRE(e.y, "matmul_dispatch_multi: descriptor %d has a null output", j);
+        QK_REQUIRE(e.split >= 0 && (e.split == 0 || e.M % (2 * e.split) == 0),
+                   "matmul_dispatch_multi: descriptor %d: split %d does not pair the %d rows", j, e.split, e.M);
     }
     const hipStream_t s = as_stream(stream);
     const int nb = K / 256;
@@ -1240,7 +1257,8 @@ int qwen_matmul_dispatch_multi(const qwen_gemv_desc* descs, int n, const float* 
         for (int j = 0; j < n; ++j) {
             const qwen_gemv_desc& e = descs[j];
             const auto* w = static_cast<const uint8_t*>(e.weight);
-            if (e.type != type || !kquant_rowpath(w, e.type, e.num_elements, x, e.M, K, e.element_offset)) continue;
+            if (e.type != type || !kquant_rowpath(w, e.type, e.num_elements, x, e.M, K, e.element_offset, e.split > 0))
+                continue;
             GemvMat& g = mu.d[m++];
             g.w = w;
             g.y = e.y;
@@ -1248,6 +1266,7 @@ int qwen_matmul_dispatch_multi(const qwen_gemv_desc* descs, int n, const float* 
             g.tensor_bytes = (e.num_elements / 256) * static_cast<uint64_t>(block_bytes(type));
             g.M = e.M;
             g.groups = nb >= 8 ? e.M : (e.M + 8 / nb - 1) / (8 / nb);
+            g.split = e.split;
             if (m == kMultiMax) {
                 if (type == kQ4_K) launch_multi<kQ4_K>(mu, m, x, nb, s);
                 else launch_multi<kQ6_K>(mu, m, x, nb, s);
@@ -1265,8 +1284,17 @@ int qwen_matmul_dispatch_multi(const qwen_gemv_desc* descs, int n, const float* 
     for (int j = 0; j < n; ++j) {
         const qwen_gemv_desc& e = descs[j];
         const auto* w = static_cast<const uint8_t*>(e.weight);
-        if ((e.type == kQ4_K || e.type == kQ6_K) && kquant_rowpath(w, e.type, e.num_elements, x, e.M, K, e.element_offset))
+        if ((e.type == kQ4_K || e.type == kQ6_K) &&
+            kquant_rowpath(w, e.type, e.num_elements, x, e.M, K, e.element_offset, e.split > 0))
             continue;
+        if (e.split > 0) {   // the generic kernel writes the split layout itself
+            gemv_any<<<dim3(blocks_for(e.M, kBlock / kWave), 1), kBlock, 0, s>>>(w, e.type, x, e.y, e.M, K,
+                                                                                e.element_offset,
+                                                                                Experts{nullptr, 0, 0, 0}, e.split);
+            const int st = check_launch("matmul_dispatch_multi");
+            if (st) return st;
+            continue;
+        }
         const int st = launch_gemv(w, e.type, e.num_elements, x, e.y, e.M, K, e.element_offset,
                                    Experts{nullptr, 0, 0, 0}, 1, s, "matmul_dispatch_multi");
         if (st) return st;

@@ -306,7 +306,7 @@ void matmul_dispatch_multi(const GemvJob* jobs, int n, const float* x, int K, hi
             need > w.num_elements - jobs[j].element_offset)
             throw std::runtime_error("GEMV shape exceeds tensor '" + w.name + "'");
         d[j] = qwen_gemv_desc{w.device_ptr, static_cast<int>(w.type), jobs[j].M, w.num_elements,
-                              jobs[j].element_offset, jobs[j].y};
+                              jobs[j].element_offset, jobs[j].y, jobs[j].split};
     }
     check(qwen_matmul_dispatch_multi(d.data(), n, x, K, st(stream)));
 }

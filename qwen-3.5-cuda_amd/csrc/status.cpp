@@ -34,7 +34,7 @@ int check_launch(const char* what) {
 
 extern "C" {
 
-int qwen_abi_version(void) { return 1; }
+int qwen_abi_version(void) { return 2; }
 
 const char* qwen_last_error(void) { return qk::g_message; }
 

@@ -100,10 +100,11 @@ class AttnLayerDecode:
       (:95-96), two cache copies (:99-100), scores / softmax / values (:103-105),
       sigmoid gate (:108), output projection (:109): fifteen launches;
     * `forward(x, pos, out)`: the three projections in one `matmul_dispatch_multi`
-      whose K and V outputs are the cache rows at `pos` (no cache copies), split,
-      Q/K head norm + partial RoPE in one `attn_qk_norm_rope_rows` (K normalized
-      in place in the cache row), `attn_decode` (scores, softmax, values and the
-      sigmoid gate), output projection: five launches.
+      whose query | gate output is written already split (q, then the gate) and
+      whose K and V outputs are the cache rows at `pos` (no split launch, no cache
+      copies), Q/K head norm + partial RoPE in one `attn_qk_norm_rope_rows` (K
+      normalized in place in the cache row), `attn_decode` (scores, softmax,
+      values and the sigmoid gate), output projection: four launches.
     """
 
     def __init__(self, w_qg, w_k, w_v, w_out, q_norm, k_norm, *, wtype="Q4_K", d_model=2048, heads=16, kv_heads=2,
@@ -159,14 +160,14 @@ class AttnLayerDecode:
     def forward(self, x, pos, out):
         self._check_pos(pos)
         h, kvh, hd = self.h, self.kvh, self.hd
-        jobs = [(self.w[n][0], self.wtype, self.w[n][1] * self.dm, self.w[n][1], 0, y)
-                for n, y in (("qg", self.qg), ("k", self.k_cache[pos]), ("v", self.v_cache[pos]))]
-        ops.matmul_dispatch_multi(jobs, x, self.dm)
-        ops.attn_split_qg(self.qg, h, hd, q=self.q, g=self.gate)
-        ops.attn_qk_norm_rope_rows(self.q.view(1, h, hd), self.k_cache[pos].view(1, kvh, hd), self.q_norm,
+        jobs = [(self.w[n][0], self.wtype, self.w[n][1] * self.dm, self.w[n][1], 0, y, s)
+                for n, y, s in (("qg", self.qg, hd), ("k", self.k_cache[pos], 0), ("v", self.v_cache[pos], 0))]
+        ops.matmul_dispatch_multi(jobs, x, self.dm)        # qg = [q | gate] (the split layout)
+        q, gate = self.qg[:self.qd], self.qg[self.qd:]
+        ops.attn_qk_norm_rope_rows(q.view(1, h, hd), self.k_cache[pos].view(1, kvh, hd), self.q_norm,
                                    self.k_norm, pos0=pos, rope_dim=self.rope_dim, theta=self.theta, eps=self.eps)
-        ops.attn_decode(self.q, self.k_cache, self.v_cache, h, kvh, hd, pos, gate=self.gate,
-                        workspace=self.workspace, out=self.gated)
+        ops.attn_decode(q, self.k_cache, self.v_cache, h, kvh, hd, pos, gate=gate, workspace=self.workspace,
+                        out=self.gated)
         self._proj("out", self.gated, out, self.qd)
         return out
 

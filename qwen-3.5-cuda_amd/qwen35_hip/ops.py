@@ -584,24 +584,30 @@ def dequantize_row(table, ggml_type, num_elements: int, row: int, cols: int, out
 class GemvDesc(ctypes.Structure):
     """qwen_gemv_desc (include/qwen35_hip.h)."""
     _fields_ = [("weight", ctypes.c_void_p), ("type", ctypes.c_int), ("M", ctypes.c_int),
-                ("num_elements", ctypes.c_uint64), ("element_offset", ctypes.c_uint64), ("y", ctypes.c_void_p)]
+                ("num_elements", ctypes.c_uint64), ("element_offset", ctypes.c_uint64), ("y", ctypes.c_void_p),
+                ("split", ctypes.c_int)]
 
 
 def matmul_dispatch_multi(jobs, x, K: int, stream=None):
-    """jobs: (weight uint8 tensor, ggml type, num_elements, M, element_offset, out float32 [M] or None);
-    y_j = W_j x for every job, all from one x [K]. Returns the outputs."""
+    """jobs: (weight uint8 tensor, ggml type, num_elements, M, element_offset, out float32 [M] or None
+    [, split]); y_j = W_j x for every job, all from one x [K]. split s > 0 writes the rows in the
+    attn_split_qg layout (pairs of s-row halves: first halves to out[:M/2], second to out[M/2:]).
+    Returns the outputs."""
     _dev(x, dtype=torch.float32)
     if x.numel() < K:
         raise ValueError(f"x has {x.numel()} elements, K = {K}")
     descs = (GemvDesc * max(1, len(jobs)))()
     outs = []
-    for j, (w, t, ne, M, off, out) in enumerate(jobs):
+    for j, job in enumerate(jobs):
+        w, t, ne, M, off, out = job[:6]
+        split = job[6] if len(job) > 6 else 0
         _dev(w, dtype=torch.uint8)
         out = torch.empty(M, dtype=torch.float32, device=x.device) if out is None else out
         _dev(out, dtype=torch.float32)
         if out.numel() < M:
             raise ValueError(f"job {j}: out has {out.numel()} elements, M = {M}")
-        descs[j] = GemvDesc(w.data_ptr(), GGML_TYPES[t] if isinstance(t, str) else int(t), M, ne, off, out.data_ptr())
+        descs[j] = GemvDesc(w.data_ptr(), GGML_TYPES[t] if isinstance(t, str) else int(t), M, ne, off, out.data_ptr(),
+                            split)
         outs.append(out)
     check(load().qwen_matmul_dispatch_multi(ctypes.cast(descs, ctypes.c_void_p), len(jobs), _p(x), K,
                                             _stream(stream)))

@@ -60,7 +60,7 @@ def test_cxx_dropin_symbols_exported():
 
 
 def test_status_names(lib):
-    assert lib.qwen_abi_version() == 1
+    assert lib.qwen_abi_version() == 2
     names = [lib.qwen_status_name(i).decode() for i in range(5)]
     assert names == ["QWEN_STATUS_OK", "QWEN_STATUS_INVALID_ARGUMENT", "QWEN_STATUS_UNSUPPORTED_TYPE",
                      "QWEN_STATUS_OUT_OF_RANGE", "QWEN_STATUS_LAUNCH_FAILED"]

@@ -541,6 +541,38 @@ def test_gdn_recurrent_rows_equals_steps():
     assert_f32_close(host(s1), host(s2), group=dv, what="state")
 
 
+@pytest.mark.parametrize("kind,heads,hd,K", [("Q4_K", 16, 256, 2048), ("Q6_K", 4, 256, 2048), ("Q4_K", 8, 64, 512),
+                                             ("Q8_0", 4, 32, 256)])
+def test_matmul_dispatch_multi_split_equals_projection_then_split(kind, heads, hd, K):
+    """A descriptor with split = head_dim writes the fused query | gate
+    projection in attn_split_qg's layout: bit-equal to matmul_dispatch followed
+    by attn_split_qg (src/layer_attn.cpp:85,90), on the per-row kernel (Q4_K,
+    Q6_K, packed rows at K = 512) and the generic one (Q8_0); an unsplit
+    descriptor in the same call is unaffected."""
+    r = rng(heads * hd + K)
+    M = 2 * heads * hd
+    t = ops.GGML_TYPES[kind]
+    w = dev(_gemv_weight(kind, M, K, r))
+    w2 = dev(_gemv_weight(kind, 96, K, r))
+    x = dev(r.standard_normal(K).astype(F32))
+    ys, y2 = torch.empty(M, device="cuda"), torch.empty(96, device="cuda")
+    ops.matmul_dispatch_multi([(w, t, M * K, M, 0, ys, hd), (w2, t, 96 * K, 96, 0, y2)], x, K)
+    full = ops.matmul_dispatch(w, t, M * K, x, M, K)
+    q, g = ops.attn_split_qg(full, heads, hd)
+    assert_bits_equal(host(ys[:M // 2]), host(q), what=f"{kind} q")
+    assert_bits_equal(host(ys[M // 2:]), host(g), what=f"{kind} gate")
+    assert_bits_equal(host(y2), host(ops.matmul_dispatch(w2, t, 96 * K, x, 96, K)), what=f"{kind} unsplit")
+
+
+def test_matmul_dispatch_multi_rejects_unpaired_split():
+    from qwen35_hip._lib import QwenError
+
+    w = dev(synth.q4k_table(96, 2048, seed_tensor=1))
+    x = torch.zeros(2048, device="cuda")
+    with pytest.raises(QwenError, match="descriptor 0: split 64 does not pair the 96 rows"):
+        ops.matmul_dispatch_multi([(w, "Q4_K", 96 * 2048, 96, 0, None, 64)], x, 2048)
+
+
 @pytest.mark.parametrize("rows,kh,vh,dk,dv", [(1, 16, 32, 128, 128), (1, 4, 8, 64, 64), (37, 16, 32, 128, 128),
                                                (5, 2, 4, 100, 48)])
 def test_gdn_gated_recurrent_equals_gates_then_recurrence(rows, kh, vh, dk, dv):
@@ -605,8 +637,9 @@ def _attn_layer_pair(r, max_seq_len):
 @pytest.mark.parametrize("start", [0, 700])
 def test_attn_layer_decode_fused_equals_reference_launches(start):
     """A full-attention layer's decode step (src/layer_attn.cpp:63-111) through
-    the fused entry points (five launches: projections straight into the cache
-    rows, split, Q/K norm + RoPE, attention decode, output projection) against the
+    the fused entry points (four launches: projections with the query | gate
+    rows written split and K, V straight into the cache rows, Q/K norm + RoPE,
+    attention decode, output projection) against the
     reference's sequence of fifteen calls on the same library, three tokens in a
     row from position `start` (0, and 700 over a cache whose earlier rows hold the
     same random keys and values in both layers): same output and cache rows
