@@ -408,6 +408,7 @@ def build_next_rows(torch, ops, synth, host):
         desc = ("one GDN layer decode step, Q4_K weights, 16/32 heads of 128: " +
                 ("fused entry points, 5 launches" if fused else "the reference's sequence of 10 calls"))
         k = Kernel(name, desc, nb, nb, mk_l)
+        k.layer = True
         k.no_cpu = True
         ks.append(k)
 
@@ -433,6 +434,7 @@ def build_next_rows(torch, ops, synth, host):
         desc = ("one attention layer decode step at position 2047, Q4_K weights, 16 query / 2 KV heads of 256: " +
                 ("fused entry points, 5 launches" if fused else "the reference's sequence of 15 calls"))
         k = Kernel(name, desc, nb, nb, mk_a)
+        k.layer = True
         k.no_cpu = True
         ks.append(k)
 
@@ -465,6 +467,7 @@ def build_next_rows(torch, ops, synth, host):
                  "the reference's sequence (8 + 5 x 8 calls and a host round trip for the expert ids)") +
                 ("; eager, wall clock per call" if eager else ""))
         k = Kernel(name, desc, nb, nb, mk_m)
+        k.layer = True
         k.no_cpu = True
         k.eager = eager
         ks.append(k)
@@ -728,6 +731,9 @@ def main() -> int:
     ap.add_argument("--no-per-kernel", action="store_true", help="skip the per-kernel and copy measurements")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-next", action="store_true", help="skip the decode GEMV measurements (not part of the step)")
+    ap.add_argument("--no-layers", action="store_true",
+                    help="skip the layer-composition rows (their 1-token calls of the step kernels would mix into a "
+                         "kernel trace of the step kernels)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget")
     ap.add_argument("--json-out", default="", help="also write the JSON line to this file")
     ap.add_argument("--profile-gemv", type=int, default=0, metavar="N",
@@ -826,6 +832,8 @@ def main() -> int:
         nxt = build_next_rows(torch, ops, synth, host)
         if args.kernels:
             nxt = [k for k in nxt if k.name in keep]
+        if args.no_layers:
+            nxt = [k for k in nxt if not getattr(k, "layer", False)]
         for k in nxt:
             k.us = measure_kernel(torch, k, spin, args.launches)
             k.copy_us = measure_copy(torch, bench_lib, k.bytes, spin, args.launches)

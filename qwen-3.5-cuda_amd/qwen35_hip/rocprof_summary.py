@@ -40,6 +40,9 @@ NAMES = [
     ("gemv_kquant<14, 4>", "gemv Q6_K per-row, 4 units/wave"),
     ("gemv_kquant<12, 2>", "gemv Q4_K per-row, 2 units/wave (GDN qkv)"),
     ("gemv_kquant<12, 1>", "gemv Q4_K per-row, 1 unit/wave (out proj, experts)"),
+    ("gemv_kquant_multi", "gemv per-row, several matrices of one x (matmul_dispatch_multi)"),
+    ("gemv_kquant_gate_up", "gemv per-row, routed experts' gate + up (moe_expert_gate_up)"),
+    ("moe_down_combine_kernel", "moe_down_combine (routed + shared down, combine)"),
     ("gdn_recurrent_v4", "gdn_recurrent step (decode)"),
     ("gdn_recurrent_g", "gdn_recurrent token loop (4096 tokens)"),
     ("gdn_chunk_prep", "gdn_recurrent chunked: per-chunk prep"),
