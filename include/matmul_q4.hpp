@@ -38,17 +38,29 @@ void moe_expert_gate_up(const QuantTensor& w_gate, const QuantTensor& w_up, uint
                         const int32_t* idx, int n_sel, const float* x, float* gate_out, float* up_out, int M, int K,
                         hipStream_t stream = nullptr);
 
-// The rest of a MoE layer's decode step after the gate / up GEMVs
-// (src/layer_moe.cpp:133-147): out = sum_j weights[j] Wd_{idx[j]} (SiLU(gate[j])
-// * up[j]) + sigmoid(shared_logit[0]) Wsd (SiLU(shared_gate) * shared_up).
-// workspace: moe_down_combine_workspace_bytes(n_sel, inter, shared_dim, d_model)
-// bytes of device memory. Throws as matmul_dispatch, naming the tensor.
-size_t moe_down_combine_workspace_bytes(int n_sel, int inter, int shared_dim, int d_model);
+// The SwiGLU hidden rows of a MoE layer's decode step in one launch
+// (src/layer_moe.cpp:131-133, :146-148): hidden[j] = SiLU(Wg_{idx[j]} x) *
+// (Wu_{idx[j]} x) [n_sel x inter], and, when shared_gate is non-null,
+// shared_hidden = SiLU(Wsg x) * (Wsu x) [shared_dim]. workspace:
+// moe_expert_swiglu_workspace_bytes(n_sel, inter, shared_dim) bytes of device
+// memory. Throws as matmul_dispatch, naming the tensor.
+size_t moe_expert_swiglu_workspace_bytes(int n_sel, int inter, int shared_dim);
+void moe_expert_swiglu(const QuantTensor& w_gate, const QuantTensor& w_up, uint64_t expert_stride, int n_experts,
+                       const int32_t* idx, int n_sel, int inter, const QuantTensor* shared_gate,
+                       const QuantTensor* shared_up, int shared_dim, const float* x, int K, float* hidden,
+                       float* shared_hidden, void* workspace, size_t workspace_bytes, hipStream_t stream = nullptr);
+
+// The rest of a MoE layer's decode step after the SwiGLU hidden rows
+// (src/layer_moe.cpp:135-147): out = sum_j weights[j] Wd_{idx[j]} hidden[j] +
+// sigmoid(shared_logit[0]) Wsd shared_hidden. workspace:
+// moe_down_combine_workspace_bytes(n_sel, d_model) bytes of device memory.
+// Throws as matmul_dispatch, naming the tensor.
+size_t moe_down_combine_workspace_bytes(int n_sel, int d_model);
 void moe_down_combine(const QuantTensor& w_down, uint64_t expert_stride, int n_experts, const int32_t* idx,
-                      const float* weights, int n_sel, const float* gate, const float* up, int inter,
-                      const QuantTensor& w_shared_down, const float* shared_gate, const float* shared_up,
-                      int shared_dim, const float* shared_logit, float* out, int d_model, void* workspace,
-                      size_t workspace_bytes, hipStream_t stream = nullptr);
+                      const float* weights, int n_sel, const float* hidden, int inter,
+                      const QuantTensor& w_shared_down, const float* shared_hidden, int shared_dim,
+                      const float* shared_logit, float* out, int d_model, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream = nullptr);
 
 // Several GEMVs of one x (K elements) in as few launches as possible: y_j =
 // W_j x for each job, the results of n matmul_dispatch calls (the reference

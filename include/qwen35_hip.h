@@ -282,28 +282,46 @@ int qwen_moe_expert_gate_up(const void* w_gate, const void* w_up, int type, uint
                             uint64_t expert_stride, int n_experts, const int32_t* idx, int n_sel,
                             const float* x, float* gate_out, float* up_out, int M, int K, void* stream);
 
-/* The rest of a MoE layer's decode step after the gate / up projections,
- * src/layer_moe.cpp:133-147 (SiLU x up and the down projection per routed expert,
- * moe_add from a zeroed accumulator in routing order, the shared expert's SiLU x up
- * and down projection, the sigmoid-gated shared add):
- *   out = sum_j weights[j] * Wd_e (SiLU(gate[j]) * up[j])      (e = idx[j], j < n_sel)
- *       + sigmoid(shared_logit[0]) * Wsd (SiLU(shared_gate) * shared_up)
- * gate, up [n_sel x inter]; shared_gate, shared_up [shared_dim]; out [d_model]
- * (written, not accumulated). Down expert e at element offset e * expert_stride.
- * One launch for inter = 512, shared_dim a multiple of 2048 up to 4096, n_sel <= 8
- * and Q4_K / Q6_K weights; other shapes run the same steps as separate launches
- * through `workspace`, which must hold qwen_moe_down_combine_workspace_bytes() bytes
- * in every case. Bit-equal to the separate calls (qwen_moe_silu_mul,
- * qwen_moe_expert_matmul, qwen_matmul_dispatch, qwen_moe_weighted_sum_rows into a
- * zeroed out, qwen_moe_shared_add_rows); an invalid expert id makes out NaN. No
+/* The SwiGLU hidden rows of a MoE layer's decode step in one launch
+ * (src/layer_moe.cpp:131-133 per routed expert, :146-148 for the shared expert):
+ *   hidden[j]     = SiLU(Wg_e x) * (Wu_e x)       e = idx[j] (on the device), j < n_sel
+ *   shared_hidden = SiLU(Wsg x) * (Wsu x)          (when w_shared_gate / w_shared_up are given)
+ * hidden [n_sel x inter], shared_hidden [shared_dim], x [K]. Routed expert e at element
+ * offset e * expert_stride of w_gate / w_up (one type and element count); the shared
+ * tensors may have another type. Bit-equal to the separate calls (two GEMVs each, then
+ * qwen_moe_silu_mul); an invalid id gives NaN rows. Q4_K / Q6_K with K a multiple of
+ * 2048 run in one launch; other shapes take the separate kernels through `workspace`
+ * (qwen_moe_expert_swiglu_workspace_bytes() bytes, required in every case). No
  * counterpart entry point in the reference (it fuses the calls cited above). */
-size_t qwen_moe_down_combine_workspace_bytes(int n_sel, int inter, int shared_dim, int d_model);
+size_t qwen_moe_expert_swiglu_workspace_bytes(int n_sel, int inter, int shared_dim);
+int qwen_moe_expert_swiglu(const void* w_gate, const void* w_up, int type, uint64_t num_elements,
+                           uint64_t expert_stride, int n_experts, const int32_t* idx, int n_sel, int inter,
+                           const void* w_shared_gate, const void* w_shared_up, int shared_type,
+                           uint64_t shared_elements, int shared_dim, const float* x, int K, float* hidden,
+                           float* shared_hidden, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The rest of a MoE layer's decode step after the SwiGLU hidden rows,
+ * src/layer_moe.cpp:135-147 (the down projection per routed expert, moe_add from a
+ * zeroed accumulator in routing order, the shared expert's down projection, the
+ * sigmoid-gated shared add):
+ *   out = sum_j weights[j] * Wd_e hidden[j]  (e = idx[j], j < n_sel)
+ *       + sigmoid(shared_logit[0]) * Wsd shared_hidden
+ * hidden [n_sel x inter], shared_hidden [shared_dim], out [d_model] (written, not
+ * accumulated). Down expert e at element offset e * expert_stride. One launch for
+ * inter = 512, shared_dim a multiple of 2048 up to 4096, n_sel <= 8 and Q4_K / Q6_K
+ * weights; other shapes run the same steps as separate launches through `workspace`,
+ * which must hold qwen_moe_down_combine_workspace_bytes() bytes in every case.
+ * Bit-equal to the separate calls (qwen_moe_expert_matmul, qwen_matmul_dispatch,
+ * qwen_moe_weighted_sum_rows into a zeroed out, qwen_moe_shared_add_rows); an invalid
+ * expert id makes out NaN. No counterpart entry point in the reference (it fuses the
+ * calls cited above). */
+size_t qwen_moe_down_combine_workspace_bytes(int n_sel, int d_model);
 int qwen_moe_down_combine(const void* w_down, int down_type, uint64_t down_elements, uint64_t expert_stride,
                           int n_experts, const int32_t* idx, const float* weights, int n_sel,
-                          const float* gate, const float* up, int inter, const void* w_shared_down,
-                          int shared_type, uint64_t shared_elements, const float* shared_gate,
-                          const float* shared_up, int shared_dim, const float* shared_logit, float* out,
-                          int d_model, void* workspace, size_t workspace_bytes, void* stream);
+                          const float* hidden, int inter, const void* w_shared_down, int shared_type,
+                          uint64_t shared_elements, const float* shared_hidden, int shared_dim,
+                          const float* shared_logit, float* out, int d_model, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 /* ====================================================================== MoE
  * h = silu(g) * u (fp32).  ref: src/layer_moe.cpp:10 (moe_silu_mul decl),

@@ -276,19 +276,34 @@ void cpu_checks() {
                                                 3, 512); },
                  "GEMV shape exceeds tensor 'blk.0.ffn_gate_exps.weight'", "moe_expert_gate_up rows past the expert");
     wsd.device_ptr = nullptr;
-    expect_throw([&] { qwen::moe_down_combine(wd, 1024, 4, no_ids, dummy.data(), 2, dummy.data(), dummy.data(), 512, wsd,
-                                              dummy.data(), dummy.data(), 512, dummy.data(), dummy.data(), 2,
-                                              dummy.data(), 1 << 20); },
+    expect_throw([&] { qwen::moe_down_combine(wd, 1024, 4, no_ids, dummy.data(), 2, dummy.data(), 512, wsd,
+                                              dummy.data(), 512, dummy.data(), dummy.data(), 2, dummy.data(),
+                                              1 << 20); },
                  "tensor 'blk.0.ffn_down_shexp.weight' is not loaded", "moe_down_combine unloaded shared tensor");
     wsd.device_ptr = dummy.data();
-    expect_throw([&] { qwen::moe_down_combine(wd, 1024, 4, no_ids, dummy.data(), 2, dummy.data(), dummy.data(), 512, wsd,
-                                              dummy.data(), dummy.data(), 1024, dummy.data(), dummy.data(), 2,
-                                              dummy.data(), 1 << 20); },
+    expect_throw([&] { qwen::moe_down_combine(wd, 1024, 4, no_ids, dummy.data(), 2, dummy.data(), 512, wsd,
+                                              dummy.data(), 1024, dummy.data(), dummy.data(), 2, dummy.data(),
+                                              1 << 20); },
                  "GEMV shape exceeds tensor 'blk.0.ffn_down_shexp.weight'", "moe_down_combine shared rows past the end");
-    expect_throw([&] { qwen::moe_down_combine(wd, 1024, 4, no_ids, dummy.data(), 2, dummy.data(), dummy.data(), 1024,
-                                              wsd, dummy.data(), dummy.data(), 512, dummy.data(), dummy.data(), 2,
-                                              dummy.data(), 1 << 20); },
+    expect_throw([&] { qwen::moe_down_combine(wd, 1024, 4, no_ids, dummy.data(), 2, dummy.data(), 1024, wsd,
+                                              dummy.data(), 512, dummy.data(), dummy.data(), 2, dummy.data(),
+                                              1 << 20); },
                  "GEMV shape exceeds tensor 'blk.0.ffn_down_exps.weight'", "moe_down_combine expert rows past the end");
+    qwen::QuantTensor wsg = wq, wsu = wq;
+    wsg.name = "blk.0.ffn_gate_shexp.weight";
+    wsu.name = "blk.0.ffn_up_shexp.weight";
+    wsg.num_elements = wsu.num_elements = 2 * 512;
+    wsu.device_ptr = nullptr;
+    expect_throw([&] { qwen::moe_expert_swiglu(wg, wu, 1024, 4, no_ids, 2, 2, &wsg, &wsu, 2, dummy.data(), 512,
+                                               dummy.data(), dummy.data(), dummy.data(), 1 << 20); },
+                 "tensor 'blk.0.ffn_up_shexp.weight' is not loaded", "moe_expert_swiglu unloaded shared up");
+    wsu.device_ptr = dummy.data();
+    expect_throw([&] { qwen::moe_expert_swiglu(wg, wu, 1024, 4, no_ids, 2, 3, &wsg, &wsu, 2, dummy.data(), 512,
+                                               dummy.data(), dummy.data(), dummy.data(), 1 << 20); },
+                 "GEMV shape exceeds tensor 'blk.0.ffn_gate_exps.weight'", "moe_expert_swiglu routed rows past the end");
+    expect_throw([&] { qwen::moe_expert_swiglu(wg, wu, 1024, 4, no_ids, 2, 2, &wsg, &wsu, 3, dummy.data(), 512,
+                                               dummy.data(), dummy.data(), dummy.data(), 1 << 20); },
+                 "GEMV shape exceeds tensor 'blk.0.ffn_gate_shexp.weight'", "moe_expert_swiglu shared rows past the end");
     expect(qwen::calculate_tensor_bytes(qwen::GgmlType::Q4_K, 2048) == 8 * 144 &&
                qwen::calculate_tensor_bytes(qwen::GgmlType::Q6_K, 100) == 0,
            "calculate_tensor_bytes");

@@ -67,32 +67,15 @@ struct LaneX {
     float s[4];    // sums of x per scale run (Q4_K: s[0], s[1]; Q6_K: 32*sum per quarter)
 };
 
-// Sources of x: a vector in memory, or SiLU(g) * u evaluated at load time
-// (the same per-element expression as the moe_silu_mul kernel, so the values
-// have the bits of that kernel's output).
-struct PlainX {
-    const float* x;
-    __device__ __forceinline__ float4 operator()(size_t i) const { return ld4(x + i); }
-};
-struct SiluMulX {
-    const float* g;
-    const float* u;
-    __device__ __forceinline__ float4 operator()(size_t i) const {
-        const float4 s = silu4(ld4(g + i));
-        const float4 b = ld4(u + i);
-        return make_float4(s.x * b.x, s.y * b.y, s.z * b.z, s.w * b.w);
-    }
-};
-
-template <int TYPE, class XS>
-__device__ __forceinline__ void load_lane_x_from(LaneX<TYPE>& lx, const XS& xs, int xb, int j) {
-    const size_t xblk = static_cast<size_t>(xb) * 256;
+template <int TYPE>
+__device__ __forceinline__ void load_lane_x(LaneX<TYPE>& lx, const float* __restrict__ x, int xb, int j) {
+    const float* xblk = x + static_cast<size_t>(xb) * 256;
     if constexpr (TYPE == kQ4_K) {
-        const size_t lo = xblk + 64 * (j >> 1) + 16 * (j & 1);
+        const float* lo = xblk + 64 * (j >> 1) + 16 * (j & 1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            lx.v[i] = xs(lo + 4 * i);
-            lx.v[4 + i] = xs(lo + 32 + 4 * i);
+            lx.v[i] = ld4(lo + 4 * i);
+            lx.v[4 + i] = ld4(lo + 32 + 4 * i);
         }
         float a = 0.f, b = 0.f;
 #pragma unroll
@@ -104,11 +87,11 @@ __device__ __forceinline__ void load_lane_x_from(LaneX<TYPE>& lx, const XS& xs, 
         lx.s[1] = b;
         lx.s[2] = lx.s[3] = 0.f;
     } else {
-        const size_t base = xblk + 128 * (j >> 2) + 8 * (j & 3);
+        const float* base = xblk + 128 * (j >> 2) + 8 * (j & 3);
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
-            lx.v[2 * qq] = xs(base + 32 * qq);
-            lx.v[2 * qq + 1] = xs(base + 32 * qq + 4);
+            lx.v[2 * qq] = ld4(base + 32 * qq);
+            lx.v[2 * qq + 1] = ld4(base + 32 * qq + 4);
         }
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
@@ -116,11 +99,6 @@ __device__ __forceinline__ void load_lane_x_from(LaneX<TYPE>& lx, const XS& xs, 
             lx.s[qq] = 32.0f * (((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)));
         }
     }
-}
-
-template <int TYPE>
-__device__ __forceinline__ void load_lane_x(LaneX<TYPE>& lx, const float* __restrict__ x, int xb, int j) {
-    load_lane_x_from<TYPE>(lx, PlainX{x}, xb, j);
 }
 
 // sum over the 4 bytes of `q` (unsigned) times 4 x values.
@@ -347,6 +325,89 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant_gate_up(const uint8_t*
                               up ? static_cast<int>(blockIdx.y) - n_sel : static_cast<int>(blockIdx.y));
 }
 
+// The SwiGLU hidden rows of a MoE layer in one launch: h = SiLU(Wg x) * (Wu x)
+// for the routed experts (launch rows 0 .. n_sel-1, expert ids on the device)
+// and the shared expert (launch row n_sel). A wave takes R rows of both
+// tensors -- 2R units staged in LDS, one set of x values for all of them --
+// and evaluates each row as the per-row kernel does (same units, lane map and
+// reductions) before SiLU(gate) * up, so h has the bits of the two GEMVs
+// followed by moe_silu_mul. Rows of 8 | nb blocks (K a multiple of 2048).
+struct PairJob {
+    const uint8_t* wg;
+    const uint8_t* wu;
+    float* h;
+    int M;
+    Experts ex;     // idx == nullptr: no expert selection
+};
+
+template <int TYPE, int R>
+__global__ __launch_bounds__(kGemvBlock) void gemv_kquant_swiglu(const float* __restrict__ x, int nb, PairJob routed,
+                                                                 PairJob shared, int n_sel) {
+    constexpr int BB = KQuant<TYPE>::kBlockBytes;
+    constexpr int UB = 8 * BB;
+    constexpr int CPU = UB / 16;
+    constexpr int NC = (2 * R * CPU + kWave - 1) / kWave;
+    extern __shared__ uint4 gemv_stage[];
+    const bool sh = static_cast<int>(blockIdx.y) == n_sel;
+    const PairJob& jb = sh ? shared : routed;
+    if (static_cast<int64_t>(blockIdx.x) * kGemvWaves * R >= jb.M) return;   // uniform per workgroup
+    const int lane = threadIdx.x & 63;
+    const int wv = wave_in_block();
+    uint4* slot = gemv_stage + wv * (2 * R * CPU);
+    const int g0 = (blockIdx.x * kGemvWaves + wv) * R;
+    const int b = lane >> 3, j = lane & 7;
+    const int S = nb >> 3;
+    uint64_t eoff = 0;
+    int64_t x_off, y_off;
+    const bool ok_e = select_expert(jb.ex, sh ? 0 : static_cast<int>(blockIdx.y), jb.M, x_off, y_off, eoff);
+    float* h = jb.h + y_off;
+    if (!ok_e) {
+        if (lane < R && g0 + lane < jb.M) h[g0 + lane] = __builtin_nanf("");
+        return;
+    }
+    const uint64_t ub = eoff / 256;
+
+    float ag[R], au[R];
+#pragma unroll
+    for (int u = 0; u < R; ++u) ag[u] = au[u] = 0.f;
+    for (int s = 0; s < S; ++s) {
+        LaneX<TYPE> lx;
+        load_lane_x<TYPE>(lx, x, 8 * s + b, j);
+        uint4 ch[NC];
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int c = lane + i * kWave;
+            const int u = c / CPU;                   // 0 .. R-1 gate, R .. 2R-1 up
+            const int k = c - u * CPU;
+            const int g = min(g0 + (u < R ? u : u - R), jb.M - 1);
+            const uint64_t byte = (ub + static_cast<uint64_t>(g) * nb + 8 * s) * BB + 16 * static_cast<uint64_t>(k);
+            const bool in = i < NC - 1 || c < 2 * R * CPU;
+            ch[i] = in ? ld16_nt((u < R ? jb.wg : jb.wu) + byte) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int c = lane + i * kWave;
+            if (i < NC - 1 || c < 2 * R * CPU) slot[c] = ch[i];
+        }
+        __syncthreads();
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(slot);
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+            ag[u] += block_dot<TYPE>(base + u * UB + b * BB, lx, j);
+            au[u] += block_dot<TYPE>(base + (R + u) * UB + b * BB, lx, j);
+        }
+        if (s + 1 < S) __syncthreads();
+    }
+    float out = 0.f;
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const float tg = group_sum<64>(ag[u]);
+        const float tu = group_sum<64>(au[u]);
+        if (lane == u) out = silu(tg) * tu;
+    }
+    if (lane < R && g0 + lane < jb.M) h[g0 + lane] = out;
+}
+
 // Several matrices of one type against the same x (qwen_matmul_dispatch_multi):
 // launch row blockIdx.y runs matrix d[blockIdx.y]; the grid is sized for the
 // largest, and workgroups past a smaller matrix's rows return at once.
@@ -373,18 +434,17 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant_multi(const float* __r
 }
 
 // ------------------------------------------------------------ MoE down + combine
-// The rest of a MoE layer's decode step after the routed gate / up projections
-// (src/layer_moe.cpp:134-147) in one launch, for routed experts of inter = 512
+// The rest of a MoE layer's decode step after the SwiGLU hidden rows
+// (src/layer_moe.cpp:135-147) in one launch, for routed experts of inter = 512
 // (2 blocks per row: rows 4q .. 4q+3 of one expert are one 8-block unit) and
 // a shared expert of shared_dim = 2048 * SS. A workgroup owns output rows
 // 4q .. 4q+3; wave w
 //   * decodes the unit of rows 4q .. 4q+3 of routed expert j = w + 4t (t < KT)
-//     against x = SiLU(gate_j) * up_j, evaluated while x is loaded;
-//   * computes row 4q + w of the shared expert's down projection against
-//     x = SiLU(shared_gate) * shared_up;
+//     against that expert's hidden row;
+//   * computes row 4q + w of the shared expert's down projection;
 // with the per-row kernel's units, lane map and reductions, so each expert
-// output and the shared output have the bits of the separate launches (SiLU x
-// up, the expert GEMVs, the shared GEMV). Lanes 0..3 of wave 0 then combine
+// output and the shared output have the bits of the separate launches (the
+// expert GEMVs, the shared GEMV). Lanes 0..3 of wave 0 then combine
 // row 4q + lane in the reference's order (moe_add per expert from a zeroed
 // accumulator, then the gated shared add): acc = 0; acc = fma(w_j, e_j, acc)
 // for j < k; acc += shared * sigmoid(logit).
@@ -393,9 +453,8 @@ constexpr int kDcInter = 512;
 template <int TE, int TS, int KT, int SS>
 __global__ __launch_bounds__(kGemvBlock) void moe_down_combine_kernel(
         const uint8_t* __restrict__ wd, uint64_t expert_blocks, int n_experts, const int32_t* __restrict__ idx,
-        const float* __restrict__ wts, int k, const float* __restrict__ g, const float* __restrict__ u,
-        const uint8_t* __restrict__ wsd, const float* __restrict__ sg, const float* __restrict__ su,
-        const float* __restrict__ slogit, float* __restrict__ out) {
+        const float* __restrict__ wts, int k, const float* __restrict__ hid, const uint8_t* __restrict__ wsd,
+        const float* __restrict__ shid, const float* __restrict__ slogit, float* __restrict__ out) {
     constexpr int BE = KQuant<TE>::kBlockBytes, BS = KQuant<TS>::kBlockBytes;
     constexpr int CE = BE * 8 / 16, CS = BS * 8 / 16;   // 16-byte chunks per unit (72 or 105)
     static_assert(CE > kWave && CE <= 2 * kWave && CS > kWave && CS <= 2 * kWave, "two chunks per lane");
@@ -432,11 +491,10 @@ __global__ __launch_bounds__(kGemvBlock) void moe_down_combine_kernel(
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
         const int j = min(w + 4 * t, k - 1);
-        load_lane_x_from<TE>(lxe[t], SiluMulX{g + static_cast<size_t>(j) * kDcInter,
-                                              u + static_cast<size_t>(j) * kDcInter}, b & 1, jj);
+        load_lane_x<TE>(lxe[t], hid + static_cast<size_t>(j) * kDcInter, b & 1, jj);
     }
 #pragma unroll
-    for (int s = 0; s < SS; ++s) load_lane_x_from<TS>(lxs[s], SiluMulX{sg, su}, 8 * s + b, jj);
+    for (int s = 0; s < SS; ++s) load_lane_x<TS>(lxs[s], shid, 8 * s + b, jj);
 
     uint4* slot = stage[w];
 #pragma unroll
@@ -1060,9 +1118,9 @@ struct DownCombine {
     const int32_t* idx;
     const float* wts;
     int k;
-    const float *g, *u;
+    const float* hid;
     const uint8_t* wsd;
-    const float *sg, *su, *slogit;
+    const float *shid, *slogit;
     float* out;
     int d_model;
 };
@@ -1070,7 +1128,7 @@ struct DownCombine {
 template <int TE, int TS, int KT, int SS>
 void launch_dc(const DownCombine& a, hipStream_t s) {
     moe_down_combine_kernel<TE, TS, KT, SS><<<a.d_model / 4, kGemvBlock, 0, s>>>(
-        a.wd, a.expert_blocks, a.n_experts, a.idx, a.wts, a.k, a.g, a.u, a.wsd, a.sg, a.su, a.slogit, a.out);
+        a.wd, a.expert_blocks, a.n_experts, a.idx, a.wts, a.k, a.hid, a.wsd, a.shid, a.slogit, a.out);
 }
 
 template <int TE, int TS>
@@ -1089,6 +1147,26 @@ void launch_down_combine(const DownCombine& a, int te, int ts, int ss, hipStream
 }
 
 inline size_t align16(size_t n) { return (n + 15) / 16 * 16; }
+
+template <int TYPE, int R>
+void launch_swiglu_r(const float* x, int nb, const PairJob& routed, const PairJob& shared, int n_sel, hipStream_t s) {
+    constexpr int CPU = KQuant<TYPE>::kBlockBytes * 8 / 16;
+    const size_t lds = static_cast<size_t>(kGemvWaves) * 2 * R * CPU * 16;
+    const int rows = std::max(n_sel > 0 ? routed.M : 0, shared.M);
+    const int rows_y = n_sel + (shared.M > 0 ? 1 : 0);
+    gemv_kquant_swiglu<TYPE, R><<<dim3(blocks_for((rows + R - 1) / R, kGemvWaves), rows_y), kGemvBlock, lds, s>>>(
+        x, nb, routed, shared, n_sel);
+}
+
+// One launch for the routed rows (n_sel > 0) and / or the shared rows (shared.M > 0).
+template <int TYPE>
+void launch_swiglu(const float* x, int nb, const PairJob& routed, const PairJob& shared, int n_sel, hipStream_t s) {
+    const int64_t rows = static_cast<int64_t>(n_sel) * routed.M + shared.M;
+    if (rows >= 8192)
+        launch_swiglu_r<TYPE, 2>(x, nb, routed, shared, n_sel, s);
+    else
+        launch_swiglu_r<TYPE, 1>(x, nb, routed, shared, n_sel, s);
+}
 
 }  // namespace
 }  // namespace qk
@@ -1167,19 +1245,101 @@ int qwen_moe_expert_gate_up(const void* w_gate, const void* w_up, int type, uint
     return check_launch("moe_expert_gate_up");
 }
 
-size_t qwen_moe_down_combine_workspace_bytes(int n_sel, int inter, int shared_dim, int d_model) {
-    if (n_sel < 0 || inter < 0 || shared_dim < 0 || d_model < 0) return 0;
+size_t qwen_moe_expert_swiglu_workspace_bytes(int n_sel, int inter, int shared_dim) {
+    if (n_sel < 0 || inter < 0 || shared_dim < 0) return 0;
+    return 2 * align16(sizeof(float) * (n_sel * static_cast<size_t>(inter) + shared_dim));
+}
+
+namespace {
+// The per-row pair kernel's conditions for one gate / up pair of tensors.
+bool swiglu_rowpath(const uint8_t* wg, const uint8_t* wu, int type, uint64_t num_elements, uint64_t expert_stride,
+                    const float* x, int K) {
+    const int nb = K / 256;
+    const uint64_t tensor_bytes = (num_elements / 256) * static_cast<uint64_t>(block_bytes(type));
+    return (type == kQ4_K || type == kQ6_K) && K % 2048 == 0 && num_elements % 256 == 0 && tensor_bytes % 16 == 0 &&
+           expert_stride % 2048 == 0 && aligned16(wg) && aligned16(wu) && aligned16(x) && nb >= 8;
+}
+}  // namespace
+
+int qwen_moe_expert_swiglu(const void* w_gate, const void* w_up, int type, uint64_t num_elements,
+                           uint64_t expert_stride, int n_experts, const int32_t* idx, int n_sel, int inter,
+                           const void* w_shared_gate, const void* w_shared_up, int shared_type,
+                           uint64_t shared_elements, int shared_dim, const float* x, int K, float* hidden,
+                           float* shared_hidden, void* workspace, size_t workspace_bytes, void* stream) {
+    const bool has_shared = w_shared_gate || w_shared_up;
+    if (!w_gate || !w_up || (has_shared && (!w_shared_gate || !w_shared_up)))
+        return fail(QWEN_STATUS_INVALID_ARGUMENT, "tensor is not loaded");
+    if (!type_supported(type)) return fail(QWEN_STATUS_UNSUPPORTED_TYPE, "unsupported GGML type %d", type);
+    if (has_shared && !type_supported(shared_type))
+        return fail(QWEN_STATUS_UNSUPPORTED_TYPE, "unsupported GGML type %d", shared_type);
+    QK_REQUIRE(n_sel >= 0 && n_sel <= 32767 && n_experts > 0, "moe_expert_swiglu: bad n_sel %d / n_experts %d",
+               n_sel, n_experts);
+    if (inter <= 0 || K <= 0 || static_cast<uint64_t>(inter) * static_cast<uint64_t>(K) > expert_stride ||
+        expert_stride > num_elements / static_cast<uint64_t>(n_experts))
+        return fail(QWEN_STATUS_OUT_OF_RANGE, "GEMV shape exceeds tensor (M=%d, K=%d, %d experts)", inter, K,
+                    n_experts);
+    if (has_shared && (shared_dim <= 0 || static_cast<uint64_t>(shared_dim) * static_cast<uint64_t>(K) > shared_elements))
+        return fail(QWEN_STATUS_OUT_OF_RANGE, "GEMV shape exceeds tensor (M=%d, K=%d)", shared_dim, K);
+    const int sdim = has_shared ? shared_dim : 0;
+    QK_REQUIRE(x && (n_sel == 0 || (idx && hidden)) && (!has_shared || shared_hidden),
+               "moe_expert_swiglu: null pointer");
+    const size_t need = qwen_moe_expert_swiglu_workspace_bytes(n_sel, inter, sdim);
+    QK_REQUIRE(workspace || need == 0, "moe_expert_swiglu: null workspace");
+    QK_REQUIRE(workspace_bytes >= need, "moe_expert_swiglu: workspace of %zu bytes, need %zu", workspace_bytes, need);
+    const hipStream_t s = as_stream(stream);
+    const auto* wg = static_cast<const uint8_t*>(w_gate);
+    const auto* wu = static_cast<const uint8_t*>(w_up);
+    const auto* wsg = static_cast<const uint8_t*>(w_shared_gate);
+    const auto* wsu = static_cast<const uint8_t*>(w_shared_up);
+    const Experts ex{idx, n_experts, expert_stride, 0};
+    const Experts none{nullptr, 0, 0, 0};
+    const bool r_fast = n_sel > 0 && swiglu_rowpath(wg, wu, type, num_elements, expert_stride, x, K);
+    const bool s_fast = has_shared && swiglu_rowpath(wsg, wsu, shared_type, shared_elements, 2048, x, K);
+    const PairJob routed{wg, wu, hidden, inter, ex};
+    const PairJob shared{wsg, wsu, shared_hidden, sdim, none};
+    const PairJob off{nullptr, nullptr, nullptr, 0, none};
+    const int nb = K / 256;
+    auto launch = [&](int t, const PairJob& r, const PairJob& sj, int n) {
+        if (t == kQ4_K) launch_swiglu<kQ4_K>(x, nb, r, sj, n, s);
+        else launch_swiglu<kQ6_K>(x, nb, r, sj, n, s);
+    };
+    if (r_fast && s_fast && type == shared_type) {
+        launch(type, routed, shared, n_sel);
+    } else {
+        if (r_fast) launch(type, routed, off, n_sel);
+        if (s_fast) launch(shared_type, off, shared, 0);
+    }
+    int rc = check_launch("moe_expert_swiglu");
+    // Other shapes: the two GEMVs into the workspace, then SiLU x up.
+    auto* gbuf = static_cast<float*>(workspace);
+    auto* ubuf = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + need / 2);
+    const size_t nr = static_cast<size_t>(n_sel) * inter;
+    if (!rc && n_sel > 0 && !r_fast) {
+        rc = launch_gemv(wg, type, num_elements, x, gbuf, inter, K, 0, ex, n_sel, s, "moe_expert_swiglu");
+        if (!rc) rc = launch_gemv(wu, type, num_elements, x, ubuf, inter, K, 0, ex, n_sel, s, "moe_expert_swiglu");
+        if (!rc) rc = qwen_moe_silu_mul(gbuf, ubuf, hidden, static_cast<int>(nr), stream);
+    }
+    if (!rc && has_shared && !s_fast) {
+        rc = launch_gemv(wsg, shared_type, shared_elements, x, gbuf + nr, sdim, K, 0, none, 1, s, "moe_expert_swiglu");
+        if (!rc)
+            rc = launch_gemv(wsu, shared_type, shared_elements, x, ubuf + nr, sdim, K, 0, none, 1, s,
+                             "moe_expert_swiglu");
+        if (!rc) rc = qwen_moe_silu_mul(gbuf + nr, ubuf + nr, shared_hidden, sdim, stream);
+    }
+    return rc;
+}
+
+size_t qwen_moe_down_combine_workspace_bytes(int n_sel, int d_model) {
+    if (n_sel < 0 || d_model < 0) return 0;
     const size_t f = sizeof(float);
-    return align16(f * n_sel * static_cast<size_t>(inter)) + align16(f * shared_dim) +
-           align16(f * n_sel * static_cast<size_t>(d_model)) + align16(f * d_model);
+    return align16(f * n_sel * static_cast<size_t>(d_model)) + align16(f * d_model);
 }
 
 int qwen_moe_down_combine(const void* w_down, int down_type, uint64_t down_elements, uint64_t expert_stride,
-                          int n_experts, const int32_t* idx, const float* weights, int n_sel, const float* gate,
-                          const float* up, int inter, const void* w_shared_down, int shared_type,
-                          uint64_t shared_elements, const float* shared_gate, const float* shared_up, int shared_dim,
-                          const float* shared_logit, float* out, int d_model, void* workspace,
-                          size_t workspace_bytes, void* stream) {
+                          int n_experts, const int32_t* idx, const float* weights, int n_sel, const float* hidden,
+                          int inter, const void* w_shared_down, int shared_type, uint64_t shared_elements,
+                          const float* shared_hidden, int shared_dim, const float* shared_logit, float* out,
+                          int d_model, void* workspace, size_t workspace_bytes, void* stream) {
     if (!w_down || !w_shared_down) return fail(QWEN_STATUS_INVALID_ARGUMENT, "tensor is not loaded");
     if (!type_supported(down_type)) return fail(QWEN_STATUS_UNSUPPORTED_TYPE, "unsupported GGML type %d", down_type);
     if (!type_supported(shared_type))
@@ -1193,9 +1353,9 @@ int qwen_moe_down_combine(const void* w_down, int down_type, uint64_t down_eleme
                     n_experts);
     if (shared_dim <= 0 || static_cast<uint64_t>(d_model) * static_cast<uint64_t>(shared_dim) > shared_elements)
         return fail(QWEN_STATUS_OUT_OF_RANGE, "GEMV shape exceeds tensor (M=%d, K=%d)", d_model, shared_dim);
-    QK_REQUIRE(idx && weights && gate && up && shared_gate && shared_up && shared_logit && out && workspace,
+    QK_REQUIRE(idx && weights && hidden && shared_hidden && shared_logit && out && workspace,
                "moe_down_combine: null pointer");
-    const size_t need = qwen_moe_down_combine_workspace_bytes(n_sel, inter, shared_dim, d_model);
+    const size_t need = qwen_moe_down_combine_workspace_bytes(n_sel, d_model);
     QK_REQUIRE(workspace_bytes >= need, "moe_down_combine: workspace of %zu bytes, need %zu", workspace_bytes, need);
     const hipStream_t s = as_stream(stream);
     const auto* wd = static_cast<const uint8_t*>(w_down);
@@ -1203,26 +1363,20 @@ int qwen_moe_down_combine(const void* w_down, int down_type, uint64_t down_eleme
     const auto kq = [](int t) { return t == kQ4_K || t == kQ6_K; };
     const bool fused = kq(down_type) && kq(shared_type) && inter == kDcInter && shared_dim % 2048 == 0 &&
                        shared_dim <= 4096 && d_model % 4 == 0 && n_sel <= 8 && expert_stride % 2048 == 0 &&
-                       aligned16(wd) && aligned16(wsd) && aligned16(gate) && aligned16(up) &&
-                       aligned16(shared_gate) && aligned16(shared_up);
+                       aligned16(wd) && aligned16(wsd) && aligned16(hidden) && aligned16(shared_hidden);
     if (fused) {
-        const DownCombine a{wd, expert_stride / 256, n_experts, idx, weights, n_sel, gate, up, wsd, shared_gate,
-                            shared_up, shared_logit, out, d_model};
+        const DownCombine a{wd, expert_stride / 256, n_experts, idx, weights, n_sel, hidden, wsd, shared_hidden,
+                            shared_logit, out, d_model};
         launch_down_combine(a, down_type, shared_type, shared_dim / 2048, s);
         return check_launch("moe_down_combine");
     }
     // Other shapes: the same steps as separate launches through the workspace.
-    auto* hid = static_cast<float*>(workspace);
-    auto* shid = reinterpret_cast<float*>(reinterpret_cast<char*>(hid) + align16(4 * n_sel * static_cast<size_t>(inter)));
-    auto* eo = reinterpret_cast<float*>(reinterpret_cast<char*>(shid) + align16(4 * static_cast<size_t>(shared_dim)));
+    auto* eo = static_cast<float*>(workspace);
     auto* so = reinterpret_cast<float*>(reinterpret_cast<char*>(eo) + align16(4 * n_sel * static_cast<size_t>(d_model)));
-    int rc = qwen_moe_silu_mul(gate, up, hid, n_sel * inter, stream);
-    if (!rc) rc = qwen_moe_silu_mul(shared_gate, shared_up, shid, shared_dim, stream);
-    if (!rc)
-        rc = launch_gemv(wd, down_type, down_elements, hid, eo, d_model, inter, 0,
+    int rc = launch_gemv(wd, down_type, down_elements, hidden, eo, d_model, inter, 0,
                          Experts{idx, n_experts, expert_stride, inter}, n_sel, s, "moe_down_combine");
     if (!rc)
-        rc = launch_gemv(wsd, shared_type, shared_elements, shid, so, d_model, shared_dim, 0,
+        rc = launch_gemv(wsd, shared_type, shared_elements, shared_hidden, so, d_model, shared_dim, 0,
                          Experts{nullptr, 0, 0, 0}, 1, s, "moe_down_combine");
     if (rc) return rc;
     fill_zero<<<blocks_for(d_model, kBlock), kBlock, 0, s>>>(out, d_model);

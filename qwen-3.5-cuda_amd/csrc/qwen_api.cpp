@@ -264,15 +264,48 @@ void moe_expert_gate_up(const QuantTensor& w_gate, const QuantTensor& w_up, uint
     check(status);
 }
 
-size_t moe_down_combine_workspace_bytes(int n_sel, int inter, int shared_dim, int d_model) {
-    return qwen_moe_down_combine_workspace_bytes(n_sel, inter, shared_dim, d_model);
+size_t moe_expert_swiglu_workspace_bytes(int n_sel, int inter, int shared_dim) {
+    return qwen_moe_expert_swiglu_workspace_bytes(n_sel, inter, shared_dim);
+}
+
+void moe_expert_swiglu(const QuantTensor& w_gate, const QuantTensor& w_up, uint64_t expert_stride, int n_experts,
+                       const int32_t* idx, int n_sel, int inter, const QuantTensor* shared_gate,
+                       const QuantTensor* shared_up, int shared_dim, const float* x, int K, float* hidden,
+                       float* shared_hidden, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!shared_gate != !shared_up) throw std::invalid_argument("moe_expert_swiglu: shared gate without shared up");
+    // matmul_dispatch's checks in the order the reference's calls meet the tensors
+    std::vector<const QuantTensor*> ts{&w_gate, &w_up};
+    if (shared_gate) ts.insert(ts.end(), {shared_gate, shared_up});
+    for (const QuantTensor* w : ts) {
+        if (!w->device_ptr) throw std::runtime_error("tensor '" + w->name + "' is not loaded");
+        if (!matmul_type_supported(w->type))
+            throw std::runtime_error("unsupported GGML type for tensor '" + w->name + "'");
+    }
+    if (w_gate.type != w_up.type || w_gate.num_elements != w_up.num_elements ||
+        (shared_gate && (shared_gate->type != shared_up->type || shared_gate->num_elements != shared_up->num_elements)))
+        throw std::invalid_argument("moe_expert_swiglu: gate and up tensors differ in type or size");
+    const int status = qwen_moe_expert_swiglu(
+        w_gate.device_ptr, w_up.device_ptr, static_cast<int>(w_gate.type), w_gate.num_elements, expert_stride,
+        n_experts, idx, n_sel, inter, shared_gate ? shared_gate->device_ptr : nullptr, shared_up ? shared_up->device_ptr : nullptr,
+        shared_gate ? static_cast<int>(shared_gate->type) : 0, shared_gate ? shared_gate->num_elements : 0,
+        shared_dim, x, K, hidden, shared_hidden, workspace, workspace_bytes, st(stream));
+    if (status == QWEN_STATUS_OUT_OF_RANGE) {
+        const bool routed = static_cast<uint64_t>(inter) * static_cast<uint64_t>(K) > expert_stride || n_experts <= 0 ||
+                            expert_stride > w_gate.num_elements / static_cast<uint64_t>(n_experts);
+        throw std::runtime_error("GEMV shape exceeds tensor '" + (routed ? w_gate : *shared_gate).name + "'");
+    }
+    check(status);
+}
+
+size_t moe_down_combine_workspace_bytes(int n_sel, int d_model) {
+    return qwen_moe_down_combine_workspace_bytes(n_sel, d_model);
 }
 
 void moe_down_combine(const QuantTensor& w_down, uint64_t expert_stride, int n_experts, const int32_t* idx,
-                      const float* weights, int n_sel, const float* gate, const float* up, int inter,
-                      const QuantTensor& w_shared_down, const float* shared_gate, const float* shared_up,
-                      int shared_dim, const float* shared_logit, float* out, int d_model, void* workspace,
-                      size_t workspace_bytes, hipStream_t stream) {
+                      const float* weights, int n_sel, const float* hidden, int inter,
+                      const QuantTensor& w_shared_down, const float* shared_hidden, int shared_dim,
+                      const float* shared_logit, float* out, int d_model, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream) {
     // Tensor checks in the order the reference's calls meet them: the routed
     // down projection first, then the shared expert's.
     for (const QuantTensor* w : {&w_down, &w_shared_down}) {
@@ -282,9 +315,9 @@ void moe_down_combine(const QuantTensor& w_down, uint64_t expert_stride, int n_e
     }
     const int status = qwen_moe_down_combine(
         w_down.device_ptr, static_cast<int>(w_down.type), w_down.num_elements, expert_stride, n_experts, idx, weights,
-        n_sel, gate, up, inter, w_shared_down.device_ptr, static_cast<int>(w_shared_down.type),
-        w_shared_down.num_elements, shared_gate, shared_up, shared_dim, shared_logit, out, d_model, workspace,
-        workspace_bytes, st(stream));
+        n_sel, hidden, inter, w_shared_down.device_ptr, static_cast<int>(w_shared_down.type),
+        w_shared_down.num_elements, shared_hidden, shared_dim, shared_logit, out, d_model, workspace, workspace_bytes,
+        st(stream));
     if (status == QWEN_STATUS_OUT_OF_RANGE) {
         const bool routed = static_cast<uint64_t>(d_model) * static_cast<uint64_t>(inter) > expert_stride ||
                             n_experts <= 0 || expert_stride > w_down.num_elements / static_cast<uint64_t>(n_experts);

@@ -80,8 +80,11 @@ SIGNATURES: dict[str, list] = {
     "qwen_moe_weighted_sum_rows": [_P, _P, _P, _I, _I, _I, _P],
     "qwen_moe_expert_matmul": [_P, _I, _U64, _U64, _I, _P, _I, _P, _I64, _P, _I, _I, _P],
     "qwen_moe_expert_gate_up": [_P, _P, _I, _U64, _U64, _I, _P, _I, _P, _P, _P, _I, _I, _P],
-    "qwen_moe_down_combine_workspace_bytes": [_I, _I, _I, _I],
-    "qwen_moe_down_combine": [_P, _I, _U64, _U64, _I, _P, _P, _I, _P, _P, _I, _P, _I, _U64, _P, _P, _I, _P, _P, _I,
+    "qwen_moe_expert_swiglu_workspace_bytes": [_I, _I, _I],
+    "qwen_moe_expert_swiglu": [_P, _P, _I, _U64, _U64, _I, _P, _I, _I, _P, _P, _I, _U64, _I, _P, _I, _P, _P, _P,
+                               ctypes.c_size_t, _P],
+    "qwen_moe_down_combine_workspace_bytes": [_I, _I],
+    "qwen_moe_down_combine": [_P, _I, _U64, _U64, _I, _P, _P, _I, _P, _I, _P, _I, _U64, _P, _I, _P, _P, _I,
                               _P, ctypes.c_size_t, _P],
     "qwen_matmul_type_supported": [_I],
     "qwen_matmul_dispatch": [_P, _I, _U64, _P, _P, _I, _I, _U64, _P],
@@ -103,7 +106,8 @@ SIGNATURES: dict[str, list] = {
 _RESTYPES = {"qwen_last_error": ctypes.c_char_p, "qwen_status_name": ctypes.c_char_p,
              "qwen_attn_decode_workspace_bytes": ctypes.c_size_t,
              "qwen_gdn_recurrent_chunked_workspace_bytes": ctypes.c_size_t,
-             "qwen_moe_down_combine_workspace_bytes": ctypes.c_size_t}
+             "qwen_moe_down_combine_workspace_bytes": ctypes.c_size_t,
+             "qwen_moe_expert_swiglu_workspace_bytes": ctypes.c_size_t}
 
 _lib = None
 

@@ -183,11 +183,11 @@ class MoeLayerDecode:
       launches per routed expert (:120-135), shared expert gate / gate / up
       projections, SiLU x up, down projection, gated add (:138-146) and the copy
       out (:147): 8 + 5k launches and a host round trip;
-    * `forward(x, out)`: the router and the three shared-expert projections of x
-      in one `matmul_dispatch_multi`, top-k on the device, the k routed gate and up
-      projections in one `moe_expert_gate_up` launch reading the ids on the
-      device, then `moe_down_combine`: SiLU x up, the routed and shared down
-      projections and the weighted, gated combine in one launch: four launches,
+    * `forward(x, out)`: the router and the shared-expert gate logit in one
+      `matmul_dispatch_multi`, top-k on the device, `moe_expert_swiglu` (the k
+      routed experts' and the shared expert's gate and up projections with SiLU x
+      up, the ids read on the device) and `moe_down_combine` (the routed and
+      shared down projections and the weighted, gated combine): four launches,
       no host round trip. The host-side routing check is the one part this path
       leaves out (the top-k kernel's weights are a softmax, finite and normalised
       by construction).
@@ -213,7 +213,9 @@ class MoeLayerDecode:
         self.sgate = torch.empty(1, **f)
         self.shared_out = torch.empty(d_model, **f)
         self.accum = torch.empty(d_model, **f)
-        self.workspace = torch.empty(max(16, ops.moe_down_combine_workspace_bytes(k, inter, shared, d_model)),
+        self.workspace = torch.empty(max(16, ops.moe_down_combine_workspace_bytes(k, d_model)),
+                                     dtype=torch.uint8, device=w_router.device)
+        self.ws_swiglu = torch.empty(max(16, ops.moe_expert_swiglu_workspace_bytes(k, inter, shared)),
                                      dtype=torch.uint8, device=w_router.device)
         self.h_idx = torch.empty(k, dtype=torch.int32).pin_memory()
         self.h_w = torch.empty(k, dtype=torch.float32).pin_memory()
@@ -258,14 +260,14 @@ class MoeLayerDecode:
     def forward(self, x, out):
         k, I, S, dm, E = self.k, self.I, self.S, self.dm, self.E
         jobs = [(self.w[n][0], self.wtype, self.w[n][1] * dm, self.w[n][1], 0, y)
-                for n, y in (("router", self.router), ("sgate", self.sgate), ("sg", self.gate_all[k * I:]),
-                             ("su", self.up_all[k * I:]))]
+                for n, y in (("router", self.router), ("sgate", self.sgate))]
         ops.matmul_dispatch_multi(jobs, x, dm)
         ops.moe_topk_rows(self.router.view(1, E), k, idx=self.top_idx.view(1, k), weights=self.top_w.view(1, k))
-        ops.moe_expert_gate_up(self.experts_w["gate"], self.experts_w["up"], self.wtype, E * I * dm, I * dm, E,
-                               self.top_idx, x, I, dm, gate_out=self.gate_all[:k * I], up_out=self.up_all[:k * I])
+        ops.moe_expert_swiglu(self.experts_w["gate"], self.experts_w["up"], self.wtype, E * I * dm, I * dm, E,
+                              self.top_idx, x, I, dm, self.w["sg"][0], self.w["su"][0], self.wtype, S * dm, S,
+                              hidden=self.hidden_all[:k * I], shared_hidden=self.hidden_all[k * I:],
+                              workspace=self.ws_swiglu)
         ops.moe_down_combine(self.experts_w["down"], self.wtype, E * dm * I, dm * I, E, self.top_idx, self.top_w,
-                             self.gate_all, self.up_all, I, self.w["sd"][0], self.wtype, dm * S,
-                             self.gate_all[k * I:], self.up_all[k * I:], self.sgate, dm, out=out,
-                             workspace=self.workspace)
+                             self.hidden_all, I, self.w["sd"][0], self.wtype, dm * S, self.hidden_all[k * I:],
+                             self.sgate, dm, out=out, workspace=self.workspace)
         return out

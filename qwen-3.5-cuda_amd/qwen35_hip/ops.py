@@ -475,39 +475,82 @@ def moe_expert_gate_up(w_gate, w_up, ggml_type, num_elements, expert_stride, n_e
     return gate_out, up_out
 
 
-def moe_down_combine_workspace_bytes(n_sel, inter, shared_dim, d_model) -> int:
-    return int(load().qwen_moe_down_combine_workspace_bytes(n_sel, inter, shared_dim, d_model))
+def moe_expert_swiglu_workspace_bytes(n_sel, inter, shared_dim) -> int:
+    return int(load().qwen_moe_expert_swiglu_workspace_bytes(n_sel, inter, shared_dim))
 
 
-def moe_down_combine(w_down, down_type, down_elements, expert_stride, n_experts, idx, weights, gate, up, inter,
-                     w_shared_down, shared_type, shared_elements, shared_gate, shared_up, shared_logit, d_model,
-                     out=None, workspace=None, stream=None):
-    """out [d_model] = sum_j weights[j] Wd_{idx[j]} (SiLU(gate[j]) * up[j])
-    + sigmoid(shared_logit[0]) Wsd (SiLU(shared_gate) * shared_up)."""
+def moe_expert_swiglu(w_gate, w_up, ggml_type, num_elements, expert_stride, n_experts, idx, x, inter, K,
+                      w_shared_gate=None, w_shared_up=None, shared_type=None, shared_elements=0, shared_dim=0,
+                      hidden=None, shared_hidden=None, workspace=None, stream=None):
+    """hidden[j] = SiLU(Wg_{idx[j]} x) * (Wu_{idx[j]} x) [n_sel, inter]; with the shared tensors also
+    shared_hidden = SiLU(Wsg x) * (Wsu x) [shared_dim]. Returns (hidden, shared_hidden or None)."""
+    _dev(w_gate, w_up, dtype=torch.uint8)
+    _dev(idx, dtype=torch.int32)
+    _dev(x, dtype=torch.float32)
+    t = GGML_TYPES[ggml_type] if isinstance(ggml_type, str) else int(ggml_type)
+    n_sel = idx.numel()
+    if x.numel() < K:
+        raise ValueError(f"x has {x.numel()} elements, K = {K}")
+    has_shared = w_shared_gate is not None
+    if has_shared:
+        _dev(w_shared_gate, w_shared_up, dtype=torch.uint8)
+        ts = GGML_TYPES[shared_type] if isinstance(shared_type, str) else int(shared_type)
+    else:
+        ts, shared_dim = 0, 0
+    hidden = torch.empty((n_sel, inter), dtype=torch.float32, device=x.device) if hidden is None else hidden
+    _dev(hidden, dtype=torch.float32)
+    if hidden.numel() < n_sel * inter:
+        raise ValueError("hidden smaller than n_sel x inter")
+    if has_shared:
+        shared_hidden = (torch.empty(shared_dim, dtype=torch.float32, device=x.device) if shared_hidden is None
+                         else shared_hidden)
+        _dev(shared_hidden, dtype=torch.float32)
+        if shared_hidden.numel() < shared_dim:
+            raise ValueError("shared_hidden smaller than shared_dim")
+    nbytes = moe_expert_swiglu_workspace_bytes(n_sel, inter, shared_dim)
+    if workspace is None:
+        workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=x.device)
+    _dev(workspace)
+    check(load().qwen_moe_expert_swiglu(_p(w_gate), _p(w_up), t, num_elements, expert_stride, n_experts, _p(idx),
+                                        n_sel, inter, _p(w_shared_gate) if has_shared else None,
+                                        _p(w_shared_up) if has_shared else None, ts, shared_elements, shared_dim,
+                                        _p(x), K, _p(hidden), _p(shared_hidden) if has_shared else None,
+                                        _p(workspace), workspace.numel() * workspace.element_size(),
+                                        _stream(stream)))
+    return hidden, (shared_hidden if has_shared else None)
+
+
+def moe_down_combine_workspace_bytes(n_sel, d_model) -> int:
+    return int(load().qwen_moe_down_combine_workspace_bytes(n_sel, d_model))
+
+
+def moe_down_combine(w_down, down_type, down_elements, expert_stride, n_experts, idx, weights, hidden, inter,
+                     w_shared_down, shared_type, shared_elements, shared_hidden, shared_logit, d_model, out=None,
+                     workspace=None, stream=None):
+    """out [d_model] = sum_j weights[j] Wd_{idx[j]} hidden[j] + sigmoid(shared_logit[0]) Wsd shared_hidden."""
     _dev(w_down, w_shared_down, dtype=torch.uint8)
     _dev(idx, dtype=torch.int32)
-    _dev(weights, gate, up, shared_gate, shared_up, shared_logit, dtype=torch.float32)
+    _dev(weights, hidden, shared_hidden, shared_logit, dtype=torch.float32)
     n_sel = idx.numel()
     _same((n_sel,), weights)
-    if gate.numel() < n_sel * inter or up.numel() < n_sel * inter:
-        raise ValueError("gate / up smaller than n_sel x inter")
-    shared_dim = shared_gate.numel()
-    _same((shared_dim,), shared_up)
+    if hidden.numel() < n_sel * inter:
+        raise ValueError("hidden smaller than n_sel x inter")
+    shared_dim = shared_hidden.numel()
     if shared_logit.numel() < 1:
         raise ValueError("shared_logit is empty")
     td = GGML_TYPES[down_type] if isinstance(down_type, str) else int(down_type)
     ts = GGML_TYPES[shared_type] if isinstance(shared_type, str) else int(shared_type)
-    nbytes = moe_down_combine_workspace_bytes(n_sel, inter, shared_dim, d_model)
+    nbytes = moe_down_combine_workspace_bytes(n_sel, d_model)
     if workspace is None:
-        workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=gate.device)
+        workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=hidden.device)
     _dev(workspace)
-    out = torch.empty(d_model, dtype=torch.float32, device=gate.device) if out is None else out
+    out = torch.empty(d_model, dtype=torch.float32, device=hidden.device) if out is None else out
     _dev(out, dtype=torch.float32)
     if out.numel() < d_model:
         raise ValueError("out smaller than d_model")
     check(load().qwen_moe_down_combine(_p(w_down), td, down_elements, expert_stride, n_experts, _p(idx), _p(weights),
-                                       n_sel, _p(gate), _p(up), inter, _p(w_shared_down), ts, shared_elements,
-                                       _p(shared_gate), _p(shared_up), shared_dim, _p(shared_logit), _p(out), d_model,
+                                       n_sel, _p(hidden), inter, _p(w_shared_down), ts, shared_elements,
+                                       _p(shared_hidden), shared_dim, _p(shared_logit), _p(out), d_model,
                                        _p(workspace), workspace.numel() * workspace.element_size(), _stream(stream)))
     return out
 

@@ -903,13 +903,47 @@ def test_moe_expert_gate_up_equals_two_expert_matmuls(kind, M, K):
     assert np.isnan(host(g)[6]).all() and np.isnan(host(u)[6]).all()
 
 
-def _down_combine_separate(wd, td, nd, stride, E, ids, wts, g, u, inter, wsd, tsd, nsd, sg, su, logit, dm):
-    """The separate calls the fused entry point replaces (src/layer_moe.cpp:133-147)."""
+@pytest.mark.parametrize("kind,skind,k,inter,S,K", [
+    ("Q4_K", "Q4_K", 8, 512, 2048, 2048),    # the model's shapes: one launch
+    ("Q6_K", "Q4_K", 8, 512, 2048, 2048),    # shared expert of another type: two launches
+    ("Q4_K", "Q4_K", 3, 768, 1024, 4096),    # two 8-block slices per row
+    ("Q4_K", "Q4_K", 4, 512, 512, 512),      # K = 512: the separate kernels through the workspace
+    ("Q8_0", "Q6_K", 2, 96, 2048, 2048),     # routed through the workspace, shared in one launch
+])
+def test_moe_expert_swiglu_equals_gemvs_then_silu_mul(kind, skind, k, inter, S, K):
+    """The SwiGLU hidden rows of the routed experts and the shared expert give the
+    bits of the separate calls (gate and up GEMVs, then moe_silu_mul), invalid ids
+    included (NaN rows), on the one-launch kernel and on the workspace path."""
+    r = rng(k * 100 + inter + S + K + ops.GGML_TYPES[kind])
+    E = 12
+    t, ts = ops.GGML_TYPES[kind], ops.GGML_TYPES[skind]
+    wg, wu = dev(_gemv_weight(kind, E * inter, K, r)), dev(_gemv_weight(kind, E * inter, K, r))
+    wsg, wsu = dev(_gemv_weight(skind, S, K, r)), dev(_gemv_weight(skind, S, K, r))
+    ids = r.permutation(E)[:k].astype(np.int32)
+    ids[-1] = -1 if k > 2 else ids[-1]
+    ids = dev(ids)
+    x = dev(r.standard_normal(K).astype(F32))
+    n_el, stride = E * inter * K, inter * K
+    h, sh = ops.moe_expert_swiglu(wg, wu, t, n_el, stride, E, ids, x, inter, K, wsg, wsu, ts, S * K, S)
+    g_ref = ops.moe_expert_matmul(wg, t, n_el, stride, E, ids, x, 0, inter, K)
+    u_ref = ops.moe_expert_matmul(wu, t, n_el, stride, E, ids, x, 0, inter, K)
+    assert_bits_equal(host(h), host(ops.moe_silu_mul(g_ref, u_ref)), what=f"{kind} routed")
+    sg = ops.matmul_dispatch(wsg, ts, S * K, x, S, K)
+    su = ops.matmul_dispatch(wsu, ts, S * K, x, S, K)
+    assert_bits_equal(host(sh), host(ops.moe_silu_mul(sg, su)), what=f"{skind} shared")
+    if k > 2:
+        assert np.isnan(host(h)[-1]).all()
+    # routed experts only (no shared tensors)
+    h2, none = ops.moe_expert_swiglu(wg, wu, t, n_el, stride, E, ids, x, inter, K)
+    assert none is None
+    assert_bits_equal(host(h2), host(h), what=f"{kind} routed only")
+
+
+def _down_combine_separate(wd, td, nd, stride, E, ids, wts, hid, inter, wsd, tsd, nsd, shid, logit, dm):
+    """The separate calls the fused entry point replaces (src/layer_moe.cpp:135-147)."""
     k = ids.numel()
-    hid = ops.moe_silu_mul(g.reshape(-1)[:k * inter], u.reshape(-1)[:k * inter])
-    shid = ops.moe_silu_mul(sg, su)
     eo = ops.moe_expert_matmul(wd, td, nd, stride, E, ids, hid, inter, dm, inter)
-    so = ops.matmul_dispatch(wsd, tsd, nsd, shid, dm, sg.numel())
+    so = ops.matmul_dispatch(wsd, tsd, nsd, shid, dm, shid.numel())
     out = torch.zeros(dm, device="cuda")
     ops.moe_weighted_sum_rows(out.view(1, dm), eo.view(1, k, dm), wts.view(1, k))
     ops.moe_shared_add_rows(out.view(1, dm), so.view(1, dm), logit)
@@ -925,9 +959,9 @@ def _down_combine_separate(wd, td, nd, stride, E, ids, wts, g, u, inter, wsd, ts
     ("Q4_K", "Q6_K", 8, 512, 2048, 998),
 ])
 def test_moe_down_combine_equals_separate_calls(td, tsd, k, inter, S, dm):
-    """SiLU x up, the routed down projections, the shared expert and the
-    weighted, gated combine in one entry point give the bits of the separate
-    calls, for the fused kernel's shapes and for the fallback's."""
+    """The routed down projections, the shared expert's and the weighted, gated
+    combine in one entry point give the bits of the separate calls, for the fused
+    kernel's shapes and for the fallback's."""
     r = rng(k * 1000 + inter + S + dm)
     E = 16
     stride = dm * inter
@@ -937,18 +971,17 @@ def test_moe_down_combine_equals_separate_calls(td, tsd, k, inter, S, dm):
     ids = dev(r.permutation(E)[:k].astype(np.int32))
     w = r.uniform(0.1, 1, k).astype(F32)
     wts = dev(w / w.sum())
-    g, u = dev(r.standard_normal((k, inter)).astype(F32)), dev(r.standard_normal((k, inter)).astype(F32))
-    g[0, :5] = torch.tensor([-50.0, -41.0, 0.0, 30.0, -39.5])   # SiLU's exact-form range
-    sg, su = dev(r.standard_normal(S).astype(F32)), dev(r.standard_normal(S).astype(F32))
+    hid = dev(r.standard_normal((k, inter)).astype(F32))
+    shid = dev(r.standard_normal(S).astype(F32))
     logit = dev(np.array([0.3], F32))
-    got = ops.moe_down_combine(wd, td, nd, stride, E, ids, wts, g, u, inter, wsd, tsd, nsd, sg, su, logit, dm)
-    ref = _down_combine_separate(wd, ops.GGML_TYPES[td], nd, stride, E, ids, wts, g, u, inter, wsd,
-                                 ops.GGML_TYPES[tsd], nsd, sg, su, logit, dm)
+    got = ops.moe_down_combine(wd, td, nd, stride, E, ids, wts, hid, inter, wsd, tsd, nsd, shid, logit, dm)
+    ref = _down_combine_separate(wd, ops.GGML_TYPES[td], nd, stride, E, ids, wts, hid, inter, wsd,
+                                 ops.GGML_TYPES[tsd], nsd, shid, logit, dm)
     assert_bits_equal(host(got), host(ref), what=f"{td}/{tsd} k={k} inter={inter} S={S} dm={dm}")
     # an invalid expert id makes the output NaN, as the separate calls' NaN row does
     bad = ids.clone()
     bad[k - 1] = E
-    got = host(ops.moe_down_combine(wd, td, nd, stride, E, bad, wts, g, u, inter, wsd, tsd, nsd, sg, su, logit, dm))
+    got = host(ops.moe_down_combine(wd, td, nd, stride, E, bad, wts, hid, inter, wsd, tsd, nsd, shid, logit, dm))
     assert np.isnan(got).all()
 
 
@@ -961,8 +994,8 @@ def test_moe_down_combine_rejects_small_workspace():
     ids = torch.zeros(8, dtype=torch.int32, device="cuda")
     ws = torch.empty(64, dtype=torch.uint8, device="cuda")
     with pytest.raises(QwenError, match="workspace of 64 bytes"):
-        ops.moe_down_combine(t, "Q4_K", t.numel() // 144 * 256, 2048 * 512, 16, ids, z[:8], z, z, 512, ts, "Q4_K",
-                             2048 * 2048, z[:2048], z[:2048], z[:1], 2048, workspace=ws)
+        ops.moe_down_combine(t, "Q4_K", t.numel() // 144 * 256, 2048 * 512, 16, ids, z[:8], z, 512, ts, "Q4_K",
+                             2048 * 2048, z[:2048], z[:1], 2048, workspace=ws)
 
 
 # ------------------------------------------------------------------ quantized GEMV
