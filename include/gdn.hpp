@@ -60,6 +60,15 @@ void gdn_gated_recurrent_rows(float* state, const float* q, const float* k, cons
                               int key_heads, int value_heads, int key_dim, int value_dim, int64_t qkv_stride = 0,
                               int64_t out_stride = 0, hipStream_t stream = nullptr);
 
+// One decode token after the input projections (src/layer_gdn.cpp:89-106):
+// gdn_frontend_rows on x [C] (history hist_in -> hist_out, output y [C]) then
+// gdn_gated_recurrent_rows on y, the same bits, one launch when hist_out does
+// not overlap hist_in (key dim 128, conv kernel 4).
+void gdn_decode_step(const float* x, const float* conv_weight, const float* hist_in, float* hist_out, float* y,
+                     float* state, const float* beta_raw, const float* alpha_raw, const float* a,
+                     const float* dt_bias, float* out, int key_heads, int value_heads, int key_dim, int value_dim,
+                     int kernel, float eps = 1e-6f, hipStream_t stream = nullptr);
+
 // gdn_norm_gate over rows x heads x dim.
 void gdn_norm_gate_rows(const float* x, const float* z, const float* weight, float* out, int rows, int heads,
                         int dim, float eps, hipStream_t stream);

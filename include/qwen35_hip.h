@@ -177,6 +177,22 @@ int qwen_gdn_gated_recurrent_rows(float* state, const float* q, const float* k, 
                                   int value_heads, int key_dim, int value_dim, int64_t qkv_stride,
                                   int64_t out_stride, void* stream);
 
+/* One decode token of a GDN layer after its input projections, in one launch:
+ * qwen_gdn_frontend_rows on the row x [C] (C = 2 key_heads key_dim + value_heads
+ * value_dim; conv weights [C x kernel], history hist_in -> hist_out) writing y [C],
+ * then qwen_gdn_gated_recurrent_rows on y's q | k | v with beta_raw, alpha_raw
+ * [value_heads] into state and out [value_heads x value_dim]. Results are the
+ * bits of those two calls. One launch for kernel 4, key_dim 128, value_dim a
+ * multiple of 4, value_heads a multiple of key_heads, 16-byte aligned pointers and
+ * hist_out not overlapping hist_in; otherwise the two calls (which also allow
+ * hist_out == hist_in). Statuses as those calls.
+ * ref: src/layer_gdn.cpp:89-106 (gdn_conv_step, gdn_qk_normalize, gdn_gate_values,
+ * gdn_recurrent_step) */
+int qwen_gdn_decode_step(const float* x, const float* conv_weight, const float* hist_in, float* hist_out,
+                         float* y, float* state, const float* beta_raw, const float* alpha_raw,
+                         const float* a, const float* dt_bias, float* out, int key_heads, int value_heads,
+                         int key_dim, int value_dim, int kernel, float eps, void* stream);
+
 /* Chunked form of qwen_gdn_recurrent_rows for many tokens (prefill): the same
  * recurrence re-associated over chunks of 64 tokens (decay ratios as running
  * products, a 64 x 64 triangular solve per chunk and head, the state updated

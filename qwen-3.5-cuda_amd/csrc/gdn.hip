@@ -20,6 +20,7 @@
 
 #include "capi_common.hpp"
 #include "device_common.hpp"
+#include "gdn_common.hpp"
 
 namespace qk {
 namespace {
@@ -29,19 +30,6 @@ constexpr int kConvTile = 64;    // tokens per thread tile (generic front end)
 constexpr int kConvRows = 4;     // rows per wave (vector front end)
 constexpr int kConvWaves = 8;    // waves per workgroup (vector front end)
 constexpr int kGateUnroll = 4;   // head groups in flight per wave (norm_gate)
-
-// Exactly-rounded 1/sqrt(n) for the q scale, so the device multiplies by the
-// same constant as the host oracle (src/cuda/gdn.cu:76).
-float host_rsqrt(int n) { return static_cast<float>(1.0 / std::sqrt(static_cast<double>(n))); }
-
-__device__ __forceinline__ float conv4(float h0, float h1, float h2, float xv, float4 w) {
-    // sum = 0; sum += h0*w0; sum += h1*w1; sum += h2*w2; sum += x*w3, each a
-    // fused multiply-add as nvcc contracts it (src/cuda/gdn.cu:13-17).
-    float s = __builtin_fmaf(h0, w.x, 0.0f);
-    s = __builtin_fmaf(h1, w.y, s);
-    s = __builtin_fmaf(h2, w.z, s);
-    return __builtin_fmaf(xv, w.w, s);
-}
 
 // ---------------------------------------------------- front end, kernel size 4
 // Workgroup = 256 channels (float4 per lane) x W waves x R rows: wave v owns
@@ -77,13 +65,8 @@ __global__ __launch_bounds__(W * kWave) void gdn_frontend_k4(const float* __rest
     float4 h0 = make_float4(0.f, 0.f, 0.f, 0.f), h1 = h0, h2 = h0;  // x[t-3], x[t-2], x[t-1]
     if (wv == 0) {
         if (T0 == 0) {
-            const float4 a = ld4(hist_in + 3 * static_cast<size_t>(cc));
-            const float4 b = ld4(hist_in + 3 * static_cast<size_t>(cc) + 4);
-            const float4 d = ld4(hist_in + 3 * static_cast<size_t>(cc) + 8);
-            // [ch0: j0 j1 j2 | ch1: j0 j1 j2 | ch2 ... | ch3 ...]
-            h0 = make_float4(a.x, a.w, b.z, d.y);
-            h1 = make_float4(a.y, b.x, b.w, d.z);
-            h2 = make_float4(a.z, b.y, d.x, d.w);
+            history4(ld4(hist_in + 3 * static_cast<size_t>(cc)), ld4(hist_in + 3 * static_cast<size_t>(cc) + 4),
+                     ld4(hist_in + 3 * static_cast<size_t>(cc) + 8), h0, h1, h2);
         } else {
             h0 = ld4(x + static_cast<size_t>(T0 - 3) * C + cc);
             h1 = ld4(x + static_cast<size_t>(T0 - 2) * C + cc);

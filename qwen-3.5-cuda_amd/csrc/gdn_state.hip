@@ -27,6 +27,7 @@
 
 #include "capi_common.hpp"
 #include "device_common.hpp"
+#include "gdn_common.hpp"
 
 namespace qk {
 namespace {
@@ -260,6 +261,135 @@ __global__ __launch_bounds__(kBlock) void gdn_recurrent_v4(float* __restrict__ S
     for (int r = 0; r < RPL; ++r) st4_nt(Sh + static_cast<size_t>(lane + 64 * r) * value_dim, s[r]);
 }
 
+// One decode token of a GDN layer after its input projections, in one launch:
+// the front end (causal conv of kernel 4 + SiLU, Q/K L2 norm) and the
+// fused-gate recurrence. Key dim 128. Each wave is a wave of gdn_recurrent_v4<2>
+// -- (value head h, columns j0..j0+3), state rows L and L+64 in lane L -- that
+// first evaluates the front end for what it reads: the 256 q | k channels of
+// key head h % key_heads in gdn_frontend_k4<32>'s layout (lane L: channels
+// 4L..4L+3 of q for L < 32, of k for L >= 32; a 32-lane sum of squares per
+// head), moved to the recurrence's layout with lane permutes, and its 4 value
+// channels. So every value equals what gdn_frontend_rows writes and the
+// recurrence reads, bit for bit. Writes: the front end's output row y and the
+// new history (q | k channels of key head g by the wave h = g, j0 = 0; value
+// channels by the wave that reads them), the state and the output. hist_out
+// must not overlap hist_in: up to 64 waves read one key head's history while
+// one of them writes it.
+__global__ __launch_bounds__(kBlock) void gdn_decode_fused(
+        const float* __restrict__ x, const float* __restrict__ cw, const float* __restrict__ hin,
+        float* __restrict__ hout, float* __restrict__ y, float* __restrict__ S, const float* __restrict__ beta_raw,
+        const float* __restrict__ alpha_raw, const float* __restrict__ a, const float* __restrict__ dt,
+        float* __restrict__ out, int key_heads, int value_heads, int value_dim, float eps, float qscale) {
+    constexpr int DK = 128;
+    const int cblocks = value_dim >> 2;
+    const int wave = blockIdx.x * kWaves + wave_in_block();
+    if (wave >= value_heads * cblocks) return;  // wave-uniform; no barrier below
+    const int lane = threadIdx.x & 63;
+    const int h = wave / cblocks;
+    const int j0 = 4 * (wave - h * cblocks);
+    const int src = h % key_heads;
+    const int kd = key_heads * DK;
+    const bool is_q = lane < 32;
+    const size_t c = static_cast<size_t>(is_q ? src * DK + 4 * lane : kd + src * DK + 4 * (lane - 32));
+    const size_t cv = static_cast<size_t>(2 * kd + h * value_dim + j0);
+    float* Sh = S + static_cast<size_t>(h) * DK * value_dim + j0;
+
+    // Every load issued before the first use: taps, history and input of the
+    // lane's q | k channels and of the wave's value channels, the gates, the
+    // state slice.
+    const float4 w0 = ld4(cw + 4 * c), w1 = ld4(cw + 4 * c + 4), w2 = ld4(cw + 4 * c + 8), w3 = ld4(cw + 4 * c + 12);
+    const float4 ha = ld4(hin + 3 * c), hb = ld4(hin + 3 * c + 4), hd = ld4(hin + 3 * c + 8);
+    const float4 xv = ld4(x + c);
+    const float4 u0 = ld4(cw + 4 * cv), u1 = ld4(cw + 4 * cv + 4), u2 = ld4(cw + 4 * cv + 8), u3 = ld4(cw + 4 * cv + 12);
+    const float4 va = ld4(hin + 3 * cv), vb = ld4(hin + 3 * cv + 4), vd = ld4(hin + 3 * cv + 8);
+    const float4 vx = ld4(x + cv);
+    const float br = beta_raw[h], ar = alpha_raw[h], ah = a[h], dth = dt[h];
+    float4 s[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) s[r] = ld4_nt(Sh + static_cast<size_t>(lane + 64 * r) * value_dim);
+
+    // q | k front end (gdn_frontend_k4<32>, one row)
+    float4 h0, h1, h2;
+    history4(ha, hb, hd, h0, h1, h2);
+    float4 f = silu4(make_float4(conv4(h0.x, h1.x, h2.x, xv.x, w0), conv4(h0.y, h1.y, h2.y, xv.y, w1),
+                                 conv4(h0.z, h1.z, h2.z, xv.z, w2), conv4(h0.w, h1.w, h2.w, xv.w, w3)));
+    const float ss = group_sum<32>(sumsq4(f));
+    const float rr = rsqrtf(ss + eps);
+    const float sc = is_q ? rr * qscale : rr;
+    f.x *= sc;
+    f.y *= sc;
+    f.z *= sc;
+    f.w *= sc;
+    // value channels (no norm)
+    float4 g0, g1, g2;
+    history4(va, vb, vd, g0, g1, g2);
+    const float4 vv = silu4(make_float4(conv4(g0.x, g1.x, g2.x, vx.x, u0), conv4(g0.y, g1.y, g2.y, vx.y, u1),
+                                        conv4(g0.z, g1.z, g2.z, vx.z, u2), conv4(g0.w, g1.w, g2.w, vx.w, u3)));
+
+    if (h == src && j0 == 0) {   // one wave per key head writes its q | k channels
+        st4(y + c, f);
+        st4(hout + 3 * c, make_float4(h1.x, h2.x, xv.x, h1.y));
+        st4(hout + 3 * c + 4, make_float4(h2.y, xv.y, h1.z, h2.z));
+        st4(hout + 3 * c + 8, make_float4(xv.z, h1.w, h2.w, xv.w));
+    }
+    if (lane == 0) {
+        st4(y + cv, vv);
+        st4(hout + 3 * cv, make_float4(g1.x, g2.x, vx.x, g1.y));
+        st4(hout + 3 * cv + 4, make_float4(g2.y, vx.y, g1.z, g2.z));
+        st4(hout + 3 * cv + 8, make_float4(vx.z, g1.w, g2.w, vx.w));
+    }
+
+    // Recurrence layout: lane L needs q, k of rows L and L + 64 -- channel i
+    // sits in lane i / 4 (q) or 32 + i / 4 (k), component i % 4 = L % 4.
+    auto pick = [&](int from) {
+        const float px = __shfl(f.x, from), py = __shfl(f.y, from), pz = __shfl(f.z, from), pw = __shfl(f.w, from);
+        const int k4 = lane & 3;
+        return k4 == 0 ? px : k4 == 1 ? py : k4 == 2 ? pz : pw;
+    };
+    const float qr[2] = {pick(lane >> 2), pick(16 + (lane >> 2))};
+    const float kr[2] = {pick(32 + (lane >> 2)), pick(48 + (lane >> 2))};
+
+    // gdn_recurrent_v4<2>, one token, gates from the raw projections
+    const float d = gate_decay(ah, ar, dth);
+    float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        s[r].x *= d;
+        s[r].y *= d;
+        s[r].z *= d;
+        s[r].w *= d;
+        m.x = __builtin_fmaf(kr[r], s[r].x, m.x);
+        m.y = __builtin_fmaf(kr[r], s[r].y, m.y);
+        m.z = __builtin_fmaf(kr[r], s[r].z, m.z);
+        m.w = __builtin_fmaf(kr[r], s[r].w, m.w);
+    }
+    m.x = group_sum<64>(m.x);
+    m.y = group_sum<64>(m.y);
+    m.z = group_sum<64>(m.z);
+    m.w = group_sum<64>(m.w);
+    const float b = gate_beta(br);
+    const float4 dl = make_float4((vv.x - m.x) * b, (vv.y - m.y) * b, (vv.z - m.z) * b, (vv.w - m.w) * b);
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        s[r].x = __builtin_fmaf(kr[r], dl.x, s[r].x);
+        s[r].y = __builtin_fmaf(kr[r], dl.y, s[r].y);
+        s[r].z = __builtin_fmaf(kr[r], dl.z, s[r].z);
+        s[r].w = __builtin_fmaf(kr[r], dl.w, s[r].w);
+        o.x = __builtin_fmaf(qr[r], s[r].x, o.x);
+        o.y = __builtin_fmaf(qr[r], s[r].y, o.y);
+        o.z = __builtin_fmaf(qr[r], s[r].z, o.z);
+        o.w = __builtin_fmaf(qr[r], s[r].w, o.w);
+    }
+    o.x = group_sum<64>(o.x);
+    o.y = group_sum<64>(o.y);
+    o.z = group_sum<64>(o.z);
+    o.w = group_sum<64>(o.w);
+    if (lane == 0) st4(out + static_cast<size_t>(h) * value_dim + j0, o);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) st4_nt(Sh + static_cast<size_t>(lane + 64 * r) * value_dim, s[r]);
+}
+
 // Any key / value dim (value_dim <= 256): one block per value head, thread j
 // owns column j and walks the rows, as the reference does.
 __global__ __launch_bounds__(kMaxValueDim) void gdn_recurrent_any(
@@ -382,6 +512,39 @@ int qwen_gdn_gated_recurrent_rows(float* state, const float* q, const float* k, 
     return launch_recurrent(state, q, k, v, beta_raw, alpha_raw, out, rows, key_heads, value_heads, key_dim,
                             value_dim, qkv_stride, out_stride, as_stream(stream), "gdn_gated_recurrent",
                             RawGates{a, dt_bias});
+}
+
+int qwen_gdn_decode_step(const float* x, const float* conv_weight, const float* hist_in, float* hist_out, float* y,
+                         float* state, const float* beta_raw, const float* alpha_raw, const float* a,
+                         const float* dt_bias, float* out, int key_heads, int value_heads, int key_dim, int value_dim,
+                         int kernel, float eps, void* stream) {
+    QK_REQUIRE(key_heads > 0 && value_heads > 0 && key_dim > 0 && value_dim > 0 && kernel >= 2,
+               "gdn_decode_step: bad shape (heads %d / %d, dims %d / %d, kernel %d)", key_heads, value_heads, key_dim,
+               value_dim, kernel);
+    QK_REQUIRE(value_dim <= kMaxValueDim, "GDN value dimension exceeds kernel limit");
+    QK_REQUIRE(x && conv_weight && hist_in && hist_out && y && state && beta_raw && alpha_raw && a && dt_bias && out,
+               "gdn_decode_step: null pointer");
+    const int64_t C = 2 * static_cast<int64_t>(key_heads) * key_dim + static_cast<int64_t>(value_heads) * value_dim;
+    QK_REQUIRE(C < (int64_t{1} << 31), "gdn_decode_step: %lld channels", static_cast<long long>(C));
+    const auto lo = reinterpret_cast<uintptr_t>(hist_in), hi = lo + static_cast<uintptr_t>(C) * (kernel - 1) * 4;
+    const auto olo = reinterpret_cast<uintptr_t>(hist_out), ohi = olo + static_cast<uintptr_t>(C) * (kernel - 1) * 4;
+    const bool disjoint = ohi <= lo || hi <= olo;
+    const bool fused = disjoint && kernel == 4 && key_dim == 128 && value_dim % 4 == 0 && value_heads % key_heads == 0 &&
+                       aligned16(x) && aligned16(conv_weight) && aligned16(hist_in) && aligned16(hist_out) &&
+                       aligned16(y) && aligned16(state) && aligned16(out);
+    if (!fused) {   // the two calls it fuses (the front end may update the history in place)
+        int rc = qwen_gdn_frontend_rows(x, conv_weight, hist_in, hist_out, y, 1, static_cast<int>(C), kernel,
+                                        key_heads, key_dim, eps, stream);
+        if (rc) return rc;
+        const int64_t kd = static_cast<int64_t>(key_heads) * key_dim;
+        return qwen_gdn_gated_recurrent_rows(state, y, y + kd, y + 2 * kd, beta_raw, alpha_raw, a, dt_bias, out, 1,
+                                             key_heads, value_heads, key_dim, value_dim, 0, 0, stream);
+    }
+    const unsigned grid = blocks_for(static_cast<int64_t>(value_heads) * (value_dim / 4), kWaves);
+    gdn_decode_fused<<<grid, kBlock, 0, as_stream(stream)>>>(x, conv_weight, hist_in, hist_out, y, state, beta_raw,
+                                                             alpha_raw, a, dt_bias, out, key_heads, value_heads,
+                                                             value_dim, eps, host_rsqrt(key_dim));
+    return check_launch("gdn_decode_step");
 }
 
 int qwen_gdn_recurrent_step(float* state, const float* q, const float* k, const float* v, const float* beta,

@@ -117,6 +117,14 @@ void gdn_gated_recurrent_rows(float* state, const float* q, const float* k, cons
                                         value_heads, key_dim, value_dim, qkv_stride, out_stride, st(stream)));
 }
 
+void gdn_decode_step(const float* x, const float* conv_weight, const float* hist_in, float* hist_out, float* y,
+                     float* state, const float* beta_raw, const float* alpha_raw, const float* a,
+                     const float* dt_bias, float* out, int key_heads, int value_heads, int key_dim, int value_dim,
+                     int kernel, float eps, hipStream_t stream) {
+    check(qwen_gdn_decode_step(x, conv_weight, hist_in, hist_out, y, state, beta_raw, alpha_raw, a, dt_bias, out,
+                               key_heads, value_heads, key_dim, value_dim, kernel, eps, st(stream)));
+}
+
 void gdn_frontend_rows(const float* x, const float* weight, const float* hist_in, float* hist_out, float* y, int rows,
                        int channels, int kernel, int k_heads, int key_dim, float eps, hipStream_t stream) {
     check(qwen_gdn_frontend_rows(x, weight, hist_in, hist_out, y, rows, channels, kernel, k_heads, key_dim, eps,

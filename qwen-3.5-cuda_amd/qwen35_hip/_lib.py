@@ -79,6 +79,7 @@ SIGNATURES: dict[str, list] = {
     "qwen_moe_add": [_P, _P, _F, _I, _P],
     "qwen_moe_weighted_sum_rows": [_P, _P, _P, _I, _I, _I, _P],
     "qwen_moe_expert_matmul": [_P, _I, _U64, _U64, _I, _P, _I, _P, _I64, _P, _I, _I, _P],
+    "qwen_gdn_decode_step": [_P] * 11 + [_I, _I, _I, _I, _I, _F, _P],
     "qwen_moe_expert_gate_up": [_P, _P, _I, _U64, _U64, _I, _P, _I, _P, _P, _P, _I, _I, _P],
     "qwen_moe_expert_swiglu_workspace_bytes": [_I, _I, _I],
     "qwen_moe_expert_swiglu": [_P, _P, _I, _U64, _U64, _I, _P, _I, _I, _P, _P, _I, _U64, _I, _P, _I, _P, _P, _P,

@@ -14,11 +14,13 @@ history, recurrent state, per-token buffers; forward src/layer_gdn.cpp:78-113):
   Q/K normalize (:97), gates (:100), recurrent step (:103-106), gated norm
   (:109), output projection (:112): ten launches;
 * `forward(x)`: the four projections in one `matmul_dispatch_multi`, conv + SiLU
-  + Q/K L2 in `gdn_frontend_rows`, gates + recurrence in
-  `gdn_gated_recurrent_rows`, then the gated norm and the output projection:
-  five launches.
+  + Q/K L2 + gates + recurrence in `gdn_decode_step` (the bits of
+  `gdn_frontend_rows` followed by `gdn_gated_recurrent_rows`), then the gated
+  norm and the output projection: four launches.
 
-Both update the layer's conv history and recurrent state in place.
+Both update the layer's conv history and recurrent state (the fused step writes
+the new history into a second buffer and the two are swapped, since the
+one-launch step cannot update it in place).
 """
 
 from __future__ import annotations
@@ -43,6 +45,7 @@ class GdnLayerDecode:
         dev = conv_w.device
         f = dict(dtype=torch.float32, device=dev)
         self.history = torch.zeros((self.cd, conv_w.shape[1] - 1), **f)      # layer_gdn.cpp:42-44
+        self._history_next = torch.empty_like(self.history)   # the fused step writes the new history here
         self.state = torch.zeros((value_heads, key_dim, value_dim), **f)     # layer_gdn.cpp:38
         self.qkv = torch.empty(self.cd, **f)
         self.z = torch.empty(self.vd, **f)
@@ -79,11 +82,10 @@ class GdnLayerDecode:
         jobs = [(self.w[n][0], self.wtype, self.w[n][1] * self.dm, self.w[n][1], 0, y)
                 for n, y in (("qkv", self.qkv), ("z", self.z), ("beta", self.beta_raw), ("alpha", self.alpha_raw))]
         ops.matmul_dispatch_multi(jobs, x, self.dm)
-        ops.gdn_frontend_rows(self.qkv.view(1, self.cd), self.conv_w, self.history, hist_out=self.history,
-                              y=self.conv.view(1, self.cd), k_heads=self.kh, key_dim=self.dk, eps=self.eps)
-        ops.gdn_gated_recurrent_rows(self.state, self.conv.view(1, self.cd), self.beta_raw.view(1, self.vh),
-                                     self.alpha_raw.view(1, self.vh), self.a, self.dt, self.kh, self.vh, self.dk,
-                                     self.dv, out=self.core.view(1, self.vd))
+        ops.gdn_decode_step(self.qkv, self.conv_w, self.history, self._history_next, self.state, self.beta_raw,
+                            self.alpha_raw, self.a, self.dt, self.kh, self.vh, self.dk, self.dv, y=self.conv,
+                            out=self.core, eps=self.eps)
+        self.history, self._history_next = self._history_next, self.history
         ops.gdn_norm_gate_rows(self.core.view(self.vh, self.dv), self.z.view(self.vh, self.dv), self.norm_w,
                                out=self.normed.view(self.vh, self.dv), eps=self.eps)
         self._proj("out", self.normed, out, self.vd)

@@ -294,6 +294,29 @@ def gdn_gated_recurrent_rows(state, qkv, beta_raw, alpha_raw, a, dt_bias, key_he
     return out
 
 
+def gdn_decode_step(x, conv_w, hist_in, hist_out, state, beta_raw, alpha_raw, a, dt_bias, key_heads, value_heads,
+                    key_dim, value_dim, y=None, out=None, eps=1e-6, stream=None):
+    """One decode token after the projections: gdn_frontend_rows on x [C] (hist_in -> hist_out, y [C]),
+    then gdn_gated_recurrent_rows on y (state in place, out [value_heads * value_dim])."""
+    _dev(x, conv_w, hist_in, hist_out, state, beta_raw, alpha_raw, a, dt_bias, dtype=torch.float32)
+    C = 2 * key_heads * key_dim + value_heads * value_dim
+    K = conv_w.shape[-1]
+    if x.numel() != C or conv_w.numel() != C * K or hist_in.numel() != C * (K - 1) or hist_out.numel() != C * (K - 1):
+        raise ValueError("x, conv weights or history do not match the channel count")
+    if state.numel() != value_heads * key_dim * value_dim:
+        raise ValueError("state must be [value_heads, key_dim, value_dim]")
+    _same((value_heads,), beta_raw, alpha_raw, a, dt_bias)
+    y = torch.empty(C, dtype=torch.float32, device=x.device) if y is None else y
+    out = torch.empty(value_heads * value_dim, dtype=torch.float32, device=x.device) if out is None else out
+    _dev(y, out, dtype=torch.float32)
+    if y.numel() != C or out.numel() != value_heads * value_dim:
+        raise ValueError("y or out of the wrong size")
+    check(load().qwen_gdn_decode_step(_p(x), _p(conv_w), _p(hist_in), _p(hist_out), _p(y), _p(state), _p(beta_raw),
+                                      _p(alpha_raw), _p(a), _p(dt_bias), _p(out), key_heads, value_heads, key_dim,
+                                      value_dim, K, eps, _stream(stream)))
+    return out
+
+
 def gdn_recurrent_chunked(state, qkv, beta, decay, key_heads, value_heads, key_dim, value_dim, out=None,
                           workspace=None, stream=None):
     """qwen_gdn_recurrent_rows' chunked form (prefill): same arguments; `workspace` a

@@ -573,6 +573,41 @@ def test_matmul_dispatch_multi_rejects_unpaired_split():
         ops.matmul_dispatch_multi([(w, "Q4_K", 96 * 2048, 96, 0, None, 64)], x, 2048)
 
 
+@pytest.mark.parametrize("kh,vh,dk,dv,alias", [(16, 32, 128, 128, False), (4, 8, 128, 64, False),
+                                               (16, 32, 128, 128, True), (2, 4, 64, 32, False)])
+def test_gdn_decode_step_equals_frontend_then_gated_recurrence(kh, vh, dk, dv, alias):
+    """The one-launch decode step (front end + fused-gate recurrence) gives the
+    bits of gdn_frontend_rows (one row) followed by gdn_gated_recurrent_rows:
+    conv output, new history, state and output, over three tokens with the
+    history carried; an in-place history (alias) and key dim 64 take the two
+    calls inside the same entry point."""
+    r = rng(kh * vh + dk + dv + alias)
+    C = 2 * kh * dk + vh * dv
+    cw = dev((0.5 * r.standard_normal((C, 4))).astype(F32))
+    a = dev(-np.exp(r.standard_normal(vh)).astype(F32))
+    dt = dev(r.uniform(-1, 1, vh).astype(F32))
+    st_f = dev((0.1 * r.standard_normal((vh, dk, dv))).astype(F32))
+    st_r = st_f.clone()
+    hist_f = dev(r.standard_normal((C, 3)).astype(F32))
+    hist_r = hist_f.clone()
+    spare = torch.empty_like(hist_f)
+    for t in range(3):
+        x = dev(r.standard_normal(C).astype(F32))
+        br, ar = dev(r.standard_normal(vh).astype(F32)), dev(r.standard_normal(vh).astype(F32))
+        # reference: the two calls, history in place
+        y_r, _ = ops.gdn_frontend_rows(x.view(1, C), cw, hist_r, hist_out=hist_r, k_heads=kh, key_dim=dk)
+        o_r = ops.gdn_gated_recurrent_rows(st_r, y_r, br.view(1, vh), ar.view(1, vh), a, dt, kh, vh, dk, dv)
+        y_f = torch.empty(C, device="cuda")
+        hout = hist_f if alias else spare
+        o_f = ops.gdn_decode_step(x, cw, hist_f, hout, st_f, br, ar, a, dt, kh, vh, dk, dv, y=y_f)
+        if not alias:
+            hist_f, spare = spare, hist_f
+        assert_bits_equal(host(y_f), host(y_r).reshape(-1), what=f"token {t} conv output")
+        assert_bits_equal(host(hist_f), host(hist_r), what=f"token {t} history")
+        assert_bits_equal(host(o_f), host(o_r).reshape(-1), what=f"token {t} output")
+        assert_bits_equal(host(st_f), host(st_r), what=f"token {t} state")
+
+
 @pytest.mark.parametrize("rows,kh,vh,dk,dv", [(1, 16, 32, 128, 128), (1, 4, 8, 64, 64), (37, 16, 32, 128, 128),
                                                (5, 2, 4, 100, 48)])
 def test_gdn_gated_recurrent_equals_gates_then_recurrence(rows, kh, vh, dk, dv):
@@ -595,7 +630,7 @@ def test_gdn_gated_recurrent_equals_gates_then_recurrence(rows, kh, vh, dk, dv):
 
 def test_gdn_layer_decode_fused_equals_reference_launches():
     """A GDN layer's decode step (src/layer_gdn.cpp:78-113) through the fused
-    entry points (five launches) against the reference's sequence of calls on the
+    entry points (four launches) against the reference's sequence of calls on the
     same library (ten launches), three tokens in a row with the conv history and
     the recurrent state carried: same outputs, state and history (the fused
     front end's L2 norm sums in another order, so fp32 tolerance)."""
