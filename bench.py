@@ -463,7 +463,7 @@ def build_next_rows(torch, ops, synth, host):
             om = torch.empty(2048, dtype=torch.float32, device=dev)
             return (lambda: layer.forward(xm, om)) if fused else (lambda: layer.forward_reference_launches(xm, om))
         desc = ("one MoE layer decode step, 256 experts top 8, 512-wide experts, 2048-wide shared expert, Q4_K: " +
-                ("fused entry points, 4 launches, expert ids on the device" if fused else
+                ("fused entry points, 3 launches, expert ids on the device" if fused else
                  "the reference's sequence (8 + 5 x 8 calls and a host round trip for the expert ids)") +
                 ("; eager, wall clock per call" if eager else ""))
         k = Kernel(name, desc, nb, nb, mk_m)

@@ -50,6 +50,15 @@ void moe_expert_swiglu(const QuantTensor& w_gate, const QuantTensor& w_up, uint6
                        const QuantTensor* shared_up, int shared_dim, const float* x, int K, float* hidden,
                        float* shared_hidden, void* workspace, size_t workspace_bytes, hipStream_t stream = nullptr);
 
+// moe_topk (src/layer_moe.cpp:99) fused into moe_expert_swiglu: the k ids and
+// weights come from the router logits [n_experts] and are written to idx,
+// weights for the later calls. Throws as moe_expert_swiglu.
+void moe_route_swiglu(const float* logits, int32_t* idx, float* weights, int k, const QuantTensor& w_gate,
+                      const QuantTensor& w_up, uint64_t expert_stride, int n_experts, int inter,
+                      const QuantTensor* shared_gate, const QuantTensor* shared_up, int shared_dim, const float* x,
+                      int K, float* hidden, float* shared_hidden, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream = nullptr);
+
 // The rest of a MoE layer's decode step after the SwiGLU hidden rows
 // (src/layer_moe.cpp:135-147): out = sum_j weights[j] Wd_{idx[j]} hidden[j] +
 // sigmoid(shared_logit[0]) Wsd shared_hidden. workspace:

@@ -316,6 +316,24 @@ int qwen_moe_expert_swiglu(const void* w_gate, const void* w_up, int type, uint6
                            uint64_t shared_elements, int shared_dim, const float* x, int K, float* hidden,
                            float* shared_hidden, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The routing of a MoE decode step fused into qwen_moe_expert_swiglu: the ids and
+ * weights of the k experts come from the n_experts router logits (top-k then softmax
+ * over the picks, src/layer_moe.cpp:99, src/cuda/moe.cu:7-51, computed by the code of
+ * qwen_moe_topk_rows) and are written to idx, weights [k] for the later calls; the
+ * hidden rows are those of qwen_moe_expert_swiglu with these ids. Equals
+ * qwen_moe_topk_rows (one row) followed by qwen_moe_expert_swiglu, bit for bit, for
+ * finite logits; a non-finite logit gives idx[0] = -1, weights[0] = NaN (the rest
+ * untouched, as the top-k call) and a NaN hidden row 0 (on the one-launch path every
+ * routed row is NaN). n_experts <= 256, k <= 64.
+ * Other arguments and statuses as qwen_moe_expert_swiglu. No counterpart entry point in
+ * the reference (it fuses the calls cited above). */
+int qwen_moe_route_swiglu(const float* logits, int32_t* idx, float* weights, int k, const void* w_gate,
+                          const void* w_up, int type, uint64_t num_elements, uint64_t expert_stride,
+                          int n_experts, int inter, const void* w_shared_gate, const void* w_shared_up,
+                          int shared_type, uint64_t shared_elements, int shared_dim, const float* x, int K,
+                          float* hidden, float* shared_hidden, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
 /* The rest of a MoE layer's decode step after the SwiGLU hidden rows,
  * src/layer_moe.cpp:135-147 (the down projection per routed expert, moe_add from a
  * zeroed accumulator in routing order, the shared expert's down projection, the

@@ -34,6 +34,7 @@
 #include "capi_common.hpp"
 #include "device_common.hpp"
 #include "ggml_common.hpp"
+#include "moe_common.hpp"
 
 namespace qk {
 namespace {
@@ -332,6 +333,12 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant_gate_up(const uint8_t*
 // and evaluates each row as the per-row kernel does (same units, lane map and
 // reductions) before SiLU(gate) * up, so h has the bits of the two GEMVs
 // followed by moe_silu_mul. Rows of 8 | nb blocks (K a multiple of 2048).
+//
+// VPL > 0: the expert ids come from the router logits instead (routing fused
+// in): wave 0 of every routed workgroup runs the top-k of the moe_topk_rows
+// kernel (topk_row, the same code, so the same ids and weights) into LDS, and
+// workgroup (0, 0) also writes ids and weights out for the later launches. A
+// non-finite logit row makes every routed hidden row NaN.
 struct PairJob {
     const uint8_t* wg;
     const uint8_t* wu;
@@ -339,10 +346,15 @@ struct PairJob {
     int M;
     Experts ex;     // idx == nullptr: no expert selection
 };
+struct RouteJob {
+    const float* logits;   // n_experts router logits
+    int32_t* idx;          // out: the n_sel picks
+    float* w;              // out: their softmax weights
+};
 
-template <int TYPE, int R>
+template <int TYPE, int R, int VPL>
 __global__ __launch_bounds__(kGemvBlock) void gemv_kquant_swiglu(const float* __restrict__ x, int nb, PairJob routed,
-                                                                 PairJob shared, int n_sel) {
+                                                                 PairJob shared, int n_sel, RouteJob rt) {
     constexpr int BB = KQuant<TYPE>::kBlockBytes;
     constexpr int UB = 8 * BB;
     constexpr int CPU = UB / 16;
@@ -357,9 +369,32 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant_swiglu(const float* __
     const int g0 = (blockIdx.x * kGemvWaves + wv) * R;
     const int b = lane >> 3, j = lane & 7;
     const int S = nb >> 3;
+    Experts ex = jb.ex;
+    if constexpr (VPL > 0) {
+        __shared__ int32_t sidx[kWave];
+        if (!sh) {   // uniform per workgroup
+            if (wv == 0) {
+                int pi;
+                float pw;
+                const bool fin = topk_row<VPL>(rt.logits, ex.n_experts, n_sel, pi, pw);
+                if (lane < n_sel) sidx[lane] = fin ? pi : -1;
+                if (blockIdx.x == 0 && blockIdx.y == 0) {
+                    if (fin && lane < n_sel) {
+                        rt.idx[lane] = pi;
+                        rt.w[lane] = pw;
+                    } else if (!fin && lane == 0) {
+                        rt.idx[0] = -1;
+                        rt.w[0] = __builtin_nanf("");
+                    }
+                }
+            }
+            __syncthreads();
+            ex.idx = sidx;
+        }
+    }
     uint64_t eoff = 0;
     int64_t x_off, y_off;
-    const bool ok_e = select_expert(jb.ex, sh ? 0 : static_cast<int>(blockIdx.y), jb.M, x_off, y_off, eoff);
+    const bool ok_e = select_expert(ex, sh ? 0 : static_cast<int>(blockIdx.y), jb.M, x_off, y_off, eoff);
     float* h = jb.h + y_off;
     if (!ok_e) {
         if (lane < R && g0 + lane < jb.M) h[g0 + lane] = __builtin_nanf("");
@@ -1148,24 +1183,38 @@ void launch_down_combine(const DownCombine& a, int te, int ts, int ss, hipStream
 
 inline size_t align16(size_t n) { return (n + 15) / 16 * 16; }
 
-template <int TYPE, int R>
-void launch_swiglu_r(const float* x, int nb, const PairJob& routed, const PairJob& shared, int n_sel, hipStream_t s) {
+template <int TYPE, int R, int VPL>
+void launch_swiglu_r(const float* x, int nb, const PairJob& routed, const PairJob& shared, int n_sel,
+                     const RouteJob& rt, hipStream_t s) {
     constexpr int CPU = KQuant<TYPE>::kBlockBytes * 8 / 16;
     const size_t lds = static_cast<size_t>(kGemvWaves) * 2 * R * CPU * 16;
     const int rows = std::max(n_sel > 0 ? routed.M : 0, shared.M);
     const int rows_y = n_sel + (shared.M > 0 ? 1 : 0);
-    gemv_kquant_swiglu<TYPE, R><<<dim3(blocks_for((rows + R - 1) / R, kGemvWaves), rows_y), kGemvBlock, lds, s>>>(
-        x, nb, routed, shared, n_sel);
+    gemv_kquant_swiglu<TYPE, R, VPL>
+        <<<dim3(blocks_for((rows + R - 1) / R, kGemvWaves), rows_y), kGemvBlock, lds, s>>>(x, nb, routed, shared,
+                                                                                          n_sel, rt);
 }
 
-// One launch for the routed rows (n_sel > 0) and / or the shared rows (shared.M > 0).
-template <int TYPE>
-void launch_swiglu(const float* x, int nb, const PairJob& routed, const PairJob& shared, int n_sel, hipStream_t s) {
+template <int TYPE, int VPL>
+void launch_swiglu_v(const float* x, int nb, const PairJob& routed, const PairJob& shared, int n_sel,
+                     const RouteJob& rt, hipStream_t s) {
     const int64_t rows = static_cast<int64_t>(n_sel) * routed.M + shared.M;
     if (rows >= 8192)
-        launch_swiglu_r<TYPE, 2>(x, nb, routed, shared, n_sel, s);
+        launch_swiglu_r<TYPE, 2, VPL>(x, nb, routed, shared, n_sel, rt, s);
     else
-        launch_swiglu_r<TYPE, 1>(x, nb, routed, shared, n_sel, s);
+        launch_swiglu_r<TYPE, 1, VPL>(x, nb, routed, shared, n_sel, rt, s);
+}
+
+// One launch for the routed rows (n_sel > 0) and / or the shared rows
+// (shared.M > 0); with rt.logits set, the routing of the routed rows too
+// (vpl = logits per lane of the top-k, 1, 2 or 4).
+template <int TYPE>
+void launch_swiglu(const float* x, int nb, const PairJob& routed, const PairJob& shared, int n_sel,
+                   const RouteJob& rt, int vpl, hipStream_t s) {
+    if (!rt.logits) launch_swiglu_v<TYPE, 0>(x, nb, routed, shared, n_sel, rt, s);
+    else if (vpl == 1) launch_swiglu_v<TYPE, 1>(x, nb, routed, shared, n_sel, rt, s);
+    else if (vpl == 2) launch_swiglu_v<TYPE, 2>(x, nb, routed, shared, n_sel, rt, s);
+    else launch_swiglu_v<TYPE, 4>(x, nb, routed, shared, n_sel, rt, s);
 }
 
 }  // namespace
@@ -1261,19 +1310,25 @@ bool swiglu_rowpath(const uint8_t* wg, const uint8_t* wu, int type, uint64_t num
 }
 }  // namespace
 
-int qwen_moe_expert_swiglu(const void* w_gate, const void* w_up, int type, uint64_t num_elements,
-                           uint64_t expert_stride, int n_experts, const int32_t* idx, int n_sel, int inter,
-                           const void* w_shared_gate, const void* w_shared_up, int shared_type,
-                           uint64_t shared_elements, int shared_dim, const float* x, int K, float* hidden,
-                           float* shared_hidden, void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+// qwen_moe_expert_swiglu, and with `logits` set qwen_moe_route_swiglu: the ids
+// (and weights) then come from the router logits and are written to idx / w.
+int expert_swiglu(const void* w_gate, const void* w_up, int type, uint64_t num_elements, uint64_t expert_stride,
+                  int n_experts, const float* logits, int32_t* idx, float* w, int n_sel, int inter,
+                  const void* w_shared_gate, const void* w_shared_up, int shared_type, uint64_t shared_elements,
+                  int shared_dim, const float* x, int K, float* hidden, float* shared_hidden, void* workspace,
+                  size_t workspace_bytes, void* stream, const char* what) {
     const bool has_shared = w_shared_gate || w_shared_up;
     if (!w_gate || !w_up || (has_shared && (!w_shared_gate || !w_shared_up)))
         return fail(QWEN_STATUS_INVALID_ARGUMENT, "tensor is not loaded");
     if (!type_supported(type)) return fail(QWEN_STATUS_UNSUPPORTED_TYPE, "unsupported GGML type %d", type);
     if (has_shared && !type_supported(shared_type))
         return fail(QWEN_STATUS_UNSUPPORTED_TYPE, "unsupported GGML type %d", shared_type);
-    QK_REQUIRE(n_sel >= 0 && n_sel <= 32767 && n_experts > 0, "moe_expert_swiglu: bad n_sel %d / n_experts %d",
-               n_sel, n_experts);
+    QK_REQUIRE(n_sel >= 0 && n_sel <= 32767 && n_experts > 0, "%s: bad n_sel %d / n_experts %d", what, n_sel,
+               n_experts);
+    if (logits)
+        QK_REQUIRE(n_sel > 0 && n_sel <= n_experts && n_sel <= kWave && n_experts <= 4 * kWave,
+                   "%s: need 0 < k <= min(n, 64) and n <= %d (n=%d, k=%d)", what, 4 * kWave, n_experts, n_sel);
     if (inter <= 0 || K <= 0 || static_cast<uint64_t>(inter) * static_cast<uint64_t>(K) > expert_stride ||
         expert_stride > num_elements / static_cast<uint64_t>(n_experts))
         return fail(QWEN_STATUS_OUT_OF_RANGE, "GEMV shape exceeds tensor (M=%d, K=%d, %d experts)", inter, K,
@@ -1281,11 +1336,11 @@ int qwen_moe_expert_swiglu(const void* w_gate, const void* w_up, int type, uint6
     if (has_shared && (shared_dim <= 0 || static_cast<uint64_t>(shared_dim) * static_cast<uint64_t>(K) > shared_elements))
         return fail(QWEN_STATUS_OUT_OF_RANGE, "GEMV shape exceeds tensor (M=%d, K=%d)", shared_dim, K);
     const int sdim = has_shared ? shared_dim : 0;
-    QK_REQUIRE(x && (n_sel == 0 || (idx && hidden)) && (!has_shared || shared_hidden),
-               "moe_expert_swiglu: null pointer");
+    QK_REQUIRE(x && (n_sel == 0 || (idx && hidden)) && (!has_shared || shared_hidden) && (!logits || w),
+               "%s: null pointer", what);
     const size_t need = qwen_moe_expert_swiglu_workspace_bytes(n_sel, inter, sdim);
-    QK_REQUIRE(workspace || need == 0, "moe_expert_swiglu: null workspace");
-    QK_REQUIRE(workspace_bytes >= need, "moe_expert_swiglu: workspace of %zu bytes, need %zu", workspace_bytes, need);
+    QK_REQUIRE(workspace || need == 0, "%s: null workspace", what);
+    QK_REQUIRE(workspace_bytes >= need, "%s: workspace of %zu bytes, need %zu", what, workspace_bytes, need);
     const hipStream_t s = as_stream(stream);
     const auto* wg = static_cast<const uint8_t*>(w_gate);
     const auto* wu = static_cast<const uint8_t*>(w_up);
@@ -1299,34 +1354,62 @@ int qwen_moe_expert_swiglu(const void* w_gate, const void* w_up, int type, uint6
     const PairJob shared{wsg, wsu, shared_hidden, sdim, none};
     const PairJob off{nullptr, nullptr, nullptr, 0, none};
     const int nb = K / 256;
-    auto launch = [&](int t, const PairJob& r, const PairJob& sj, int n) {
-        if (t == kQ4_K) launch_swiglu<kQ4_K>(x, nb, r, sj, n, s);
-        else launch_swiglu<kQ6_K>(x, nb, r, sj, n, s);
+    const int vpl = (n_experts + kWave - 1) / kWave;
+    int rc = 0;
+    // Routing without the fused kernel: the top-k launch first.
+    if (logits && !r_fast) rc = qwen_moe_topk_rows(logits, idx, w, 1, n_experts, n_sel, stream);
+    if (rc) return rc;
+    const RouteJob rt{logits && r_fast ? logits : nullptr, idx, w};
+    const RouteJob no_rt{nullptr, nullptr, nullptr};
+    auto launch = [&](int t, const PairJob& r, const PairJob& sj, int n, const RouteJob& rj) {
+        if (t == kQ4_K) launch_swiglu<kQ4_K>(x, nb, r, sj, n, rj, vpl, s);
+        else launch_swiglu<kQ6_K>(x, nb, r, sj, n, rj, vpl, s);
     };
     if (r_fast && s_fast && type == shared_type) {
-        launch(type, routed, shared, n_sel);
+        launch(type, routed, shared, n_sel, rt);
     } else {
-        if (r_fast) launch(type, routed, off, n_sel);
-        if (s_fast) launch(shared_type, off, shared, 0);
+        if (r_fast) launch(type, routed, off, n_sel, rt);
+        if (s_fast) launch(shared_type, off, shared, 0, no_rt);
     }
-    int rc = check_launch("moe_expert_swiglu");
+    rc = check_launch(what);
     // Other shapes: the two GEMVs into the workspace, then SiLU x up.
     auto* gbuf = static_cast<float*>(workspace);
     auto* ubuf = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + need / 2);
     const size_t nr = static_cast<size_t>(n_sel) * inter;
     if (!rc && n_sel > 0 && !r_fast) {
-        rc = launch_gemv(wg, type, num_elements, x, gbuf, inter, K, 0, ex, n_sel, s, "moe_expert_swiglu");
-        if (!rc) rc = launch_gemv(wu, type, num_elements, x, ubuf, inter, K, 0, ex, n_sel, s, "moe_expert_swiglu");
+        rc = launch_gemv(wg, type, num_elements, x, gbuf, inter, K, 0, ex, n_sel, s, what);
+        if (!rc) rc = launch_gemv(wu, type, num_elements, x, ubuf, inter, K, 0, ex, n_sel, s, what);
         if (!rc) rc = qwen_moe_silu_mul(gbuf, ubuf, hidden, static_cast<int>(nr), stream);
     }
     if (!rc && has_shared && !s_fast) {
-        rc = launch_gemv(wsg, shared_type, shared_elements, x, gbuf + nr, sdim, K, 0, none, 1, s, "moe_expert_swiglu");
-        if (!rc)
-            rc = launch_gemv(wsu, shared_type, shared_elements, x, ubuf + nr, sdim, K, 0, none, 1, s,
-                             "moe_expert_swiglu");
+        rc = launch_gemv(wsg, shared_type, shared_elements, x, gbuf + nr, sdim, K, 0, none, 1, s, what);
+        if (!rc) rc = launch_gemv(wsu, shared_type, shared_elements, x, ubuf + nr, sdim, K, 0, none, 1, s, what);
         if (!rc) rc = qwen_moe_silu_mul(gbuf + nr, ubuf + nr, shared_hidden, sdim, stream);
     }
     return rc;
+}
+}  // namespace
+
+int qwen_moe_expert_swiglu(const void* w_gate, const void* w_up, int type, uint64_t num_elements,
+                           uint64_t expert_stride, int n_experts, const int32_t* idx, int n_sel, int inter,
+                           const void* w_shared_gate, const void* w_shared_up, int shared_type,
+                           uint64_t shared_elements, int shared_dim, const float* x, int K, float* hidden,
+                           float* shared_hidden, void* workspace, size_t workspace_bytes, void* stream) {
+    return expert_swiglu(w_gate, w_up, type, num_elements, expert_stride, n_experts, nullptr,
+                         const_cast<int32_t*>(idx), nullptr, n_sel, inter, w_shared_gate, w_shared_up, shared_type,
+                         shared_elements, shared_dim, x, K, hidden, shared_hidden, workspace, workspace_bytes, stream,
+                         "moe_expert_swiglu");
+}
+
+int qwen_moe_route_swiglu(const float* logits, int32_t* idx, float* weights, int k, const void* w_gate,
+                          const void* w_up, int type, uint64_t num_elements, uint64_t expert_stride, int n_experts,
+                          int inter, const void* w_shared_gate, const void* w_shared_up, int shared_type,
+                          uint64_t shared_elements, int shared_dim, const float* x, int K, float* hidden,
+                          float* shared_hidden, void* workspace, size_t workspace_bytes, void* stream) {
+    QK_REQUIRE(logits, "moe_route_swiglu: null pointer");
+    return expert_swiglu(w_gate, w_up, type, num_elements, expert_stride, n_experts, logits, idx, weights, k, inter,
+                         w_shared_gate, w_shared_up, shared_type, shared_elements, shared_dim, x, K, hidden,
+                         shared_hidden, workspace, workspace_bytes, stream, "moe_route_swiglu");
 }
 
 size_t qwen_moe_down_combine_workspace_bytes(int n_sel, int d_model) {

@@ -276,10 +276,9 @@ size_t moe_expert_swiglu_workspace_bytes(int n_sel, int inter, int shared_dim) {
     return qwen_moe_expert_swiglu_workspace_bytes(n_sel, inter, shared_dim);
 }
 
-void moe_expert_swiglu(const QuantTensor& w_gate, const QuantTensor& w_up, uint64_t expert_stride, int n_experts,
-                       const int32_t* idx, int n_sel, int inter, const QuantTensor* shared_gate,
-                       const QuantTensor* shared_up, int shared_dim, const float* x, int K, float* hidden,
-                       float* shared_hidden, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+namespace {
+void swiglu_checks(const QuantTensor& w_gate, const QuantTensor& w_up, const QuantTensor* shared_gate,
+                   const QuantTensor* shared_up) {
     if (!shared_gate != !shared_up) throw std::invalid_argument("moe_expert_swiglu: shared gate without shared up");
     // matmul_dispatch's checks in the order the reference's calls meet the tensors
     std::vector<const QuantTensor*> ts{&w_gate, &w_up};
@@ -292,17 +291,46 @@ void moe_expert_swiglu(const QuantTensor& w_gate, const QuantTensor& w_up, uint6
     if (w_gate.type != w_up.type || w_gate.num_elements != w_up.num_elements ||
         (shared_gate && (shared_gate->type != shared_up->type || shared_gate->num_elements != shared_up->num_elements)))
         throw std::invalid_argument("moe_expert_swiglu: gate and up tensors differ in type or size");
-    const int status = qwen_moe_expert_swiglu(
-        w_gate.device_ptr, w_up.device_ptr, static_cast<int>(w_gate.type), w_gate.num_elements, expert_stride,
-        n_experts, idx, n_sel, inter, shared_gate ? shared_gate->device_ptr : nullptr, shared_up ? shared_up->device_ptr : nullptr,
-        shared_gate ? static_cast<int>(shared_gate->type) : 0, shared_gate ? shared_gate->num_elements : 0,
-        shared_dim, x, K, hidden, shared_hidden, workspace, workspace_bytes, st(stream));
+}
+
+void swiglu_status(int status, const QuantTensor& w_gate, const QuantTensor* shared_gate, uint64_t expert_stride,
+                   int n_experts, int inter, int K) {
     if (status == QWEN_STATUS_OUT_OF_RANGE) {
         const bool routed = static_cast<uint64_t>(inter) * static_cast<uint64_t>(K) > expert_stride || n_experts <= 0 ||
                             expert_stride > w_gate.num_elements / static_cast<uint64_t>(n_experts);
         throw std::runtime_error("GEMV shape exceeds tensor '" + (routed ? w_gate : *shared_gate).name + "'");
     }
     check(status);
+}
+}  // namespace
+
+void moe_expert_swiglu(const QuantTensor& w_gate, const QuantTensor& w_up, uint64_t expert_stride, int n_experts,
+                       const int32_t* idx, int n_sel, int inter, const QuantTensor* shared_gate,
+                       const QuantTensor* shared_up, int shared_dim, const float* x, int K, float* hidden,
+                       float* shared_hidden, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    swiglu_checks(w_gate, w_up, shared_gate, shared_up);
+    const int status = qwen_moe_expert_swiglu(
+        w_gate.device_ptr, w_up.device_ptr, static_cast<int>(w_gate.type), w_gate.num_elements, expert_stride,
+        n_experts, idx, n_sel, inter, shared_gate ? shared_gate->device_ptr : nullptr,
+        shared_up ? shared_up->device_ptr : nullptr, shared_gate ? static_cast<int>(shared_gate->type) : 0,
+        shared_gate ? shared_gate->num_elements : 0, shared_dim, x, K, hidden, shared_hidden, workspace,
+        workspace_bytes, st(stream));
+    swiglu_status(status, w_gate, shared_gate, expert_stride, n_experts, inter, K);
+}
+
+void moe_route_swiglu(const float* logits, int32_t* idx, float* weights, int k, const QuantTensor& w_gate,
+                      const QuantTensor& w_up, uint64_t expert_stride, int n_experts, int inter,
+                      const QuantTensor* shared_gate, const QuantTensor* shared_up, int shared_dim, const float* x,
+                      int K, float* hidden, float* shared_hidden, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream) {
+    swiglu_checks(w_gate, w_up, shared_gate, shared_up);
+    const int status = qwen_moe_route_swiglu(
+        logits, idx, weights, k, w_gate.device_ptr, w_up.device_ptr, static_cast<int>(w_gate.type),
+        w_gate.num_elements, expert_stride, n_experts, inter, shared_gate ? shared_gate->device_ptr : nullptr,
+        shared_up ? shared_up->device_ptr : nullptr, shared_gate ? static_cast<int>(shared_gate->type) : 0,
+        shared_gate ? shared_gate->num_elements : 0, shared_dim, x, K, hidden, shared_hidden, workspace,
+        workspace_bytes, st(stream));
+    swiglu_status(status, w_gate, shared_gate, expert_stride, n_experts, inter, K);
 }
 
 size_t moe_down_combine_workspace_bytes(int n_sel, int d_model) {

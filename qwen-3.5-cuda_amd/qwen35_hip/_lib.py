@@ -84,6 +84,8 @@ SIGNATURES: dict[str, list] = {
     "qwen_moe_expert_swiglu_workspace_bytes": [_I, _I, _I],
     "qwen_moe_expert_swiglu": [_P, _P, _I, _U64, _U64, _I, _P, _I, _I, _P, _P, _I, _U64, _I, _P, _I, _P, _P, _P,
                                ctypes.c_size_t, _P],
+    "qwen_moe_route_swiglu": [_P, _P, _P, _I, _P, _P, _I, _U64, _U64, _I, _I, _P, _P, _I, _U64, _I, _P, _I, _P, _P,
+                              _P, ctypes.c_size_t, _P],
     "qwen_moe_down_combine_workspace_bytes": [_I, _I],
     "qwen_moe_down_combine": [_P, _I, _U64, _U64, _I, _P, _P, _I, _P, _I, _P, _I, _U64, _P, _I, _P, _P, _I,
                               _P, ctypes.c_size_t, _P],

@@ -186,13 +186,13 @@ class MoeLayerDecode:
       projections, SiLU x up, down projection, gated add (:138-146) and the copy
       out (:147): 8 + 5k launches and a host round trip;
     * `forward(x, out)`: the router and the shared-expert gate logit in one
-      `matmul_dispatch_multi`, top-k on the device, `moe_expert_swiglu` (the k
-      routed experts' and the shared expert's gate and up projections with SiLU x
-      up, the ids read on the device) and `moe_down_combine` (the routed and
-      shared down projections and the weighted, gated combine): four launches,
-      no host round trip. The host-side routing check is the one part this path
-      leaves out (the top-k kernel's weights are a softmax, finite and normalised
-      by construction).
+      `matmul_dispatch_multi`, then `moe_route_swiglu` (the top-k of the router
+      logits, and the k routed experts' and the shared expert's gate and up
+      projections with SiLU x up) and `moe_down_combine` (the routed and shared
+      down projections and the weighted, gated combine): three launches, no host
+      round trip. The host-side routing check is the one part this path leaves
+      out (the top-k weights are a softmax, finite and normalised by
+      construction; a non-finite router logit makes the output NaN).
     """
 
     def __init__(self, w_router, w_gate, w_up, w_down, w_sgate, w_sg, w_su, w_sd, *, wtype="Q4_K", d_model=2048,
@@ -264,11 +264,10 @@ class MoeLayerDecode:
         jobs = [(self.w[n][0], self.wtype, self.w[n][1] * dm, self.w[n][1], 0, y)
                 for n, y in (("router", self.router), ("sgate", self.sgate))]
         ops.matmul_dispatch_multi(jobs, x, dm)
-        ops.moe_topk_rows(self.router.view(1, E), k, idx=self.top_idx.view(1, k), weights=self.top_w.view(1, k))
-        ops.moe_expert_swiglu(self.experts_w["gate"], self.experts_w["up"], self.wtype, E * I * dm, I * dm, E,
-                              self.top_idx, x, I, dm, self.w["sg"][0], self.w["su"][0], self.wtype, S * dm, S,
-                              hidden=self.hidden_all[:k * I], shared_hidden=self.hidden_all[k * I:],
-                              workspace=self.ws_swiglu)
+        ops.moe_route_swiglu(self.router, k, self.experts_w["gate"], self.experts_w["up"], self.wtype, E * I * dm,
+                             I * dm, x, I, dm, self.w["sg"][0], self.w["su"][0], self.wtype, S * dm, S,
+                             idx=self.top_idx, weights=self.top_w, hidden=self.hidden_all[:k * I],
+                             shared_hidden=self.hidden_all[k * I:], workspace=self.ws_swiglu)
         ops.moe_down_combine(self.experts_w["down"], self.wtype, E * dm * I, dm * I, E, self.top_idx, self.top_w,
                              self.hidden_all, I, self.w["sd"][0], self.wtype, dm * S, self.hidden_all[k * I:],
                              self.sgate, dm, out=out, workspace=self.workspace)

@@ -543,6 +543,52 @@ def moe_expert_swiglu(w_gate, w_up, ggml_type, num_elements, expert_stride, n_ex
     return hidden, (shared_hidden if has_shared else None)
 
 
+def moe_route_swiglu(logits, k, w_gate, w_up, ggml_type, num_elements, expert_stride, x, inter, K,
+                     w_shared_gate=None, w_shared_up=None, shared_type=None, shared_elements=0, shared_dim=0,
+                     idx=None, weights=None, hidden=None, shared_hidden=None, workspace=None, stream=None):
+    """moe_topk_rows on the router logits [n_experts] fused into moe_expert_swiglu.
+    Returns (idx int32 [k], weights [k], hidden [k, inter], shared_hidden or None)."""
+    _dev(logits, dtype=torch.float32)
+    _dev(w_gate, w_up, dtype=torch.uint8)
+    _dev(x, dtype=torch.float32)
+    n_experts = logits.numel()
+    t = GGML_TYPES[ggml_type] if isinstance(ggml_type, str) else int(ggml_type)
+    if x.numel() < K:
+        raise ValueError(f"x has {x.numel()} elements, K = {K}")
+    idx = torch.empty(k, dtype=torch.int32, device=x.device) if idx is None else idx
+    weights = torch.empty(k, dtype=torch.float32, device=x.device) if weights is None else weights
+    _dev(idx, dtype=torch.int32)
+    _dev(weights, dtype=torch.float32)
+    _same((k,), idx, weights)
+    has_shared = w_shared_gate is not None
+    if has_shared:
+        _dev(w_shared_gate, w_shared_up, dtype=torch.uint8)
+        ts = GGML_TYPES[shared_type] if isinstance(shared_type, str) else int(shared_type)
+    else:
+        ts, shared_dim = 0, 0
+    hidden = torch.empty((k, inter), dtype=torch.float32, device=x.device) if hidden is None else hidden
+    _dev(hidden, dtype=torch.float32)
+    if hidden.numel() < k * inter:
+        raise ValueError("hidden smaller than k x inter")
+    if has_shared:
+        shared_hidden = (torch.empty(shared_dim, dtype=torch.float32, device=x.device) if shared_hidden is None
+                         else shared_hidden)
+        _dev(shared_hidden, dtype=torch.float32)
+        if shared_hidden.numel() < shared_dim:
+            raise ValueError("shared_hidden smaller than shared_dim")
+    nbytes = moe_expert_swiglu_workspace_bytes(k, inter, shared_dim)
+    if workspace is None:
+        workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=x.device)
+    _dev(workspace)
+    check(load().qwen_moe_route_swiglu(_p(logits), _p(idx), _p(weights), k, _p(w_gate), _p(w_up), t, num_elements,
+                                       expert_stride, n_experts, inter, _p(w_shared_gate) if has_shared else None,
+                                       _p(w_shared_up) if has_shared else None, ts, shared_elements, shared_dim,
+                                       _p(x), K, _p(hidden), _p(shared_hidden) if has_shared else None,
+                                       _p(workspace), workspace.numel() * workspace.element_size(),
+                                       _stream(stream)))
+    return idx, weights, hidden, (shared_hidden if has_shared else None)
+
+
 def moe_down_combine_workspace_bytes(n_sel, d_model) -> int:
     return int(load().qwen_moe_down_combine_workspace_bytes(n_sel, d_model))
 

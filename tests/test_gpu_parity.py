@@ -706,7 +706,7 @@ def test_attn_layer_decode_rejects_position_past_context():
 
 def test_moe_layer_decode_fused_equals_reference_launches():
     """A MoE layer's decode step (src/layer_moe.cpp:80-159, 256 experts, top 8,
-    512-wide experts, 2048-wide shared expert) through the fused entry points (four
+    512-wide experts, 2048-wide shared expert) through the fused entry points (three
     launches, the expert ids staying on the device) against the reference's
     sequence (router, top-k, host round trip and check, five calls per routed
     expert, the shared expert's six calls): same routing, same output within fp32
@@ -972,6 +972,46 @@ def test_moe_expert_swiglu_equals_gemvs_then_silu_mul(kind, skind, k, inter, S, 
     h2, none = ops.moe_expert_swiglu(wg, wu, t, n_el, stride, E, ids, x, inter, K)
     assert none is None
     assert_bits_equal(host(h2), host(h), what=f"{kind} routed only")
+
+
+@pytest.mark.parametrize("kind,n,k,inter,S,K", [
+    ("Q4_K", 256, 8, 512, 2048, 2048),     # the model's shapes: one launch, 4 logits per lane
+    ("Q6_K", 128, 4, 256, 2048, 2048),     # 2 logits per lane
+    ("Q4_K", 48, 6, 512, 0, 2048),         # 1 logit per lane, no shared expert
+    ("Q4_K", 256, 8, 512, 512, 512),       # K = 512: top-k launch + the separate kernels
+])
+def test_moe_route_swiglu_equals_topk_then_swiglu(kind, n, k, inter, S, K):
+    """Routing fused into the SwiGLU GEMV gives the ids, weights and hidden rows of
+    moe_topk_rows followed by moe_expert_swiglu, bit for bit, with ties in the
+    logits; a non-finite logit gives the top-k kernel's (-1, NaN) and a NaN row 0."""
+    r = rng(n + k + inter + S + K)
+    t = ops.GGML_TYPES[kind]
+    wg, wu = dev(_gemv_weight(kind, n * inter, K, r)), dev(_gemv_weight(kind, n * inter, K, r))
+    shared = {}
+    if S:
+        shared = dict(w_shared_gate=dev(_gemv_weight(kind, S, K, r)), w_shared_up=dev(_gemv_weight(kind, S, K, r)),
+                      shared_type=t, shared_elements=S * K, shared_dim=S)
+    x = dev(r.standard_normal(K).astype(F32))
+    lg = r.standard_normal(n).astype(F32)
+    lg[5] = lg[9] = lg.max() + 1          # a tie for the first pick
+    logits = dev(lg)
+    n_el, stride = n * inter * K, inter * K
+    idx, w, h, sh = ops.moe_route_swiglu(logits, k, wg, wu, t, n_el, stride, x, inter, K, **shared)
+    i_ref, w_ref = ops.moe_topk_rows(logits.view(1, n), k)
+    h_ref, sh_ref = ops.moe_expert_swiglu(wg, wu, t, n_el, stride, n, i_ref.view(-1), x, inter, K,
+                                          shared.get("w_shared_gate"), shared.get("w_shared_up"),
+                                          shared.get("shared_type"), shared.get("shared_elements", 0), S)
+    assert np.array_equal(host(idx), host(i_ref).reshape(-1)) and host(idx)[0] == 5
+    assert_bits_equal(host(w), host(w_ref).reshape(-1), what="weights")
+    assert_bits_equal(host(h), host(h_ref), what=f"{kind} routed")
+    if S:
+        assert_bits_equal(host(sh), host(sh_ref), what=f"{kind} shared")
+    lg[3] = np.inf
+    idx.fill_(7)
+    _, _, h2, _ = ops.moe_route_swiglu(dev(lg), k, wg, wu, t, n_el, stride, x, inter, K, idx=idx, weights=w,
+                                       **shared)
+    assert host(idx)[0] == -1 and np.isnan(host(w)[0]) and (host(idx)[1:] == 7).all()
+    assert np.isnan(host(h2)[0]).all()
 
 
 def _down_combine_separate(wd, td, nd, stride, E, ids, wts, hid, inter, wsd, tsd, nsd, shid, logit, dm):
