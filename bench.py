@@ -51,6 +51,7 @@ sys.path.insert(0, str(ROOT / "qwen-3.5-cuda_amd"))
 
 METRIC = "achieved HBM GB/s (% of MI355X peak) + µs/call per fused norm/RoPE/act kernel"
 PEAK_GBPS = 8000.0  # MI355X HBM3E
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 ROTATE_BYTES = 1 << 30
 
 
@@ -215,6 +216,26 @@ def build_next_rows(torch, ops, synth, host):
     t = synth.q4k_table(2048, 4096, seed_tensor=20)
     add("gemv_out_q4_k", "Q4_K [2048 x 4096] x f32 [4096] (layer_gdn.cpp:112 output projection)", "Q4_K",
         torch.from_numpy(t).to(dev), 2048 * 4096, 2048, 4096, [0], 144, t)
+    # Prefill: the same projections for 4096 tokens in one matmul_rows call (matrix
+    # cores). Compute-bound: reported as algorithmic TFLOP/s (2 M K per token) and as
+    # the share of the bf16 MFMA peak the three exact bf16 parts of x use (3x).
+    T = 4096
+    xg = torch.from_numpy(rng.standard_normal((T, 2048)).astype(np.float32)).to(dev)
+    for name, kind, make, M, K, bpb, seed in (("gemm_qkv_q4_k_4096", "Q4_K", synth.q4k_table, 8192, 2048, 144, 16),
+                                              ("gemm_qkv_q6_k_4096", "Q6_K", synth.q6k_table, 8192, 2048, 210, 17)):
+        wt = torch.from_numpy(make(M, K, seed_tensor=seed)).to(dev)
+        yg = torch.empty((T, M), dtype=torch.float32, device=dev)
+
+        def mk_gemm(i, wt=wt, yg=yg, kind=kind, M=M, K=K):
+            xx = xg if i == 0 else xg.clone()
+            yy = yg if i == 0 else torch.empty_like(yg)
+            return lambda: ops.matmul_rows(wt, kind, M * K, xx, M, K, out=yy)
+        nb = M * (K // 256) * bpb + 4 * T * K + 4 * T * M
+        k = Kernel(name, f"{kind} [{M} x {K}] x f32 [{T} x {K}] (layer_gdn.cpp:83 qkv projection over a "
+                   f"{T}-token prompt, one matmul_rows call)", nb, nb, mk_gemm)
+        k.flops = 2 * T * M * K
+        k.no_cpu = True
+        ks.append(k)
     # GDN recurrent state (gdn.cu:108-172): 16 key / 32 value heads of 128, state 2 MB.
     kh, vh, dk, dv = 16, 32, 128, 128
     c = host["gdn_frontend"]
@@ -838,7 +859,8 @@ def main() -> int:
             k.us = measure_kernel(torch, k, spin, args.launches)
             k.copy_us = measure_copy(torch, bench_lib, k.bytes, spin, args.launches)
             print(f"# {k.name:28s} {k.us:9.2f} us  {k.bytes / k.us / 1e3:7.1f} GB/s ({k.bytes / k.us / 1e3 / PEAK_GBPS:6.1%})"
-                  f"   copy of same bytes {k.copy_us:8.2f} us {k.bytes / k.copy_us / 1e3:7.1f} GB/s",
+                  f"   copy of same bytes {k.copy_us:8.2f} us {k.bytes / k.copy_us / 1e3:7.1f} GB/s" +
+                  (f"   {k.flops / k.us / 1e6:.1f} TFLOP/s" if getattr(k, "flops", None) else ""),
                   file=sys.stderr, flush=True)
 
     gguf = None
@@ -892,7 +914,10 @@ def main() -> int:
             k.name: {"config": k.config, "bytes": k.bytes, "us_per_call": round(k.us, 3),
                      "gbps": round(k.bytes / k.us / 1e3, 1), "frac_peak": round(k.bytes / k.us / 1e3 / PEAK_GBPS, 4),
                      "copy_same_bytes_us": round(k.copy_us, 3),
-                     "cpu_gbps": round(cpu_next[k.name]["gbps"], 3) if k.name in cpu_next else None}
+                     "cpu_gbps": round(cpu_next[k.name]["gbps"], 3) if k.name in cpu_next else None,
+                     **({"tflops": round(k.flops / k.us / 1e6, 1),
+                         "mfma_bf16_frac": round(3 * k.flops / k.us / 1e6 / PEAK_BF16_TFLOPS, 4)}
+                        if getattr(k, "flops", None) else {})}
             for k in nxt}
 
     line = {

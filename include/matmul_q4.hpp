@@ -23,6 +23,12 @@ bool matmul_type_supported(GgmlType type);
 void matmul_dispatch(const QuantTensor& weight, const float* x, float* y, int M, int K, hipStream_t stream = nullptr,
                      uint64_t element_offset = 0);
 
+// matmul_dispatch for each of `rows` tokens in one call: y[t*M + m] = sum_k
+// W[element_offset + m*K + k] * x[t*K + k] (matrix cores for Q4_K / Q6_K at
+// rows >= 16, fp32 accuracy). Throws as matmul_dispatch.
+void matmul_rows(const QuantTensor& weight, const float* x, float* y, int rows, int M, int K,
+                 hipStream_t stream = nullptr, uint64_t element_offset = 0);
+
 // n_sel expert GEMVs with the expert ids on the device: y[j] = W_{idx[j]} x_j,
 // expert e at element offset e * expert_stride, x_j = x + j * x_stride, y
 // [n_sel x M]; an invalid id gives a NaN row. Throws as matmul_dispatch.

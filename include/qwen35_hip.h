@@ -423,6 +423,20 @@ int qwen_matmul_type_supported(int type);
 int qwen_matmul_dispatch(const void* weight, int type, uint64_t num_elements, const float* x,
                          float* y, int M, int K, uint64_t element_offset, void* stream);
 
+/* rows GEMVs of one matrix: y[t][m] = sum_{k<K} W[element_offset + m*K + k] * x[t][k]
+ * for t < rows, m < M (x fp32 [rows x K], y fp32 [rows x M], row-major) -- the
+ * reference's per-token matmul_dispatch over a prompt as one call. Q4_K and
+ * Q6_K with K % 256 == 0, element_offset % 256 == 0, x 16-byte aligned and
+ * rows >= 16 run on the matrix cores (x split exactly into three bf16 parts,
+ * exact products, fp32 sums: an fp32 dot product's accuracy, not the
+ * reference's bits); other cases run qwen_matmul_dispatch once per token.
+ * rows == 0 is a no-op. Statuses and messages as qwen_matmul_dispatch; rows < 0
+ * or a NULL x / y -> QWEN_STATUS_INVALID_ARGUMENT.
+ * ref: src/cuda/matmul_q4.cu:140-167,185-207 (the GEMV it batches), called per
+ * token by the layers (src/layer_gdn.cpp:83-86, src/layer_attn.cpp:85-87) */
+int qwen_matmul_rows(const void* weight, int type, uint64_t num_elements, const float* x, float* y,
+                     int rows, int M, int K, uint64_t element_offset, void* stream);
+
 /* One projection of qwen_matmul_dispatch_multi: the arguments of one
  * qwen_matmul_dispatch call except x, K and the stream. */
 typedef struct qwen_gemv_desc {

@@ -234,6 +234,18 @@ void matmul_dispatch(const QuantTensor& w, const float* x, float* y, int M, int 
     check(status);
 }
 
+void matmul_rows(const QuantTensor& w, const float* x, float* y, int rows, int M, int K, hipStream_t stream,
+                 uint64_t element_offset) {
+    const int status = qwen_matmul_rows(w.device_ptr, static_cast<int>(w.type), w.num_elements, x, y, rows, M, K,
+                                        element_offset, st(stream));
+    if (status == QWEN_STATUS_INVALID_ARGUMENT && !w.device_ptr)
+        throw std::runtime_error("tensor '" + w.name + "' is not loaded");
+    if (status == QWEN_STATUS_UNSUPPORTED_TYPE)
+        throw std::runtime_error("unsupported GGML type for tensor '" + w.name + "'");
+    if (status == QWEN_STATUS_OUT_OF_RANGE) throw std::runtime_error("GEMV shape exceeds tensor '" + w.name + "'");
+    check(status);
+}
+
 void moe_expert_matmul(const QuantTensor& w, uint64_t expert_stride, int n_experts, const int32_t* idx, int n_sel,
                        const float* x, int64_t x_stride, float* y, int M, int K, hipStream_t stream) {
     const int status = qwen_moe_expert_matmul(w.device_ptr, static_cast<int>(w.type), w.num_elements, expert_stride,

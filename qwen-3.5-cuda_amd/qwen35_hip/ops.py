@@ -726,6 +726,26 @@ def matmul_dispatch_multi(jobs, x, K: int, stream=None):
     return outs
 
 
+def matmul_rows(weight, ggml_type, num_elements: int, x, M: int, K: int, element_offset: int = 0, out=None,
+                stream=None):
+    """matmul_dispatch for every row of x: x float32 [rows, K] -> y float32 [rows, M],
+    y[t, m] = sum_k W[element_offset + m*K + k] * x[t, k] (one call; matrix cores for
+    Q4_K / Q6_K at 16 rows or more)."""
+    _dev(weight, dtype=torch.uint8)
+    _dev(x, dtype=torch.float32)
+    if x.dim() != 2 or x.shape[1] != K:
+        raise ValueError(f"x must be [rows, {K}], got {tuple(x.shape)}")
+    rows = x.shape[0]
+    t = GGML_TYPES[ggml_type] if isinstance(ggml_type, str) else int(ggml_type)
+    out = torch.empty(rows, M, dtype=torch.float32, device=x.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    if out.numel() < rows * M:
+        raise ValueError(f"out has {out.numel()} elements, rows * M = {rows * M}")
+    check(load().qwen_matmul_rows(_p(weight), t, num_elements, _p(x), _p(out), rows, M, K, element_offset,
+                                  _stream(stream)))
+    return out
+
+
 def matmul_dispatch(weight, ggml_type, num_elements: int, x, M: int, K: int, element_offset: int = 0, out=None,
                     stream=None):
     """weight: uint8 device tensor of GGML blocks; x float32 [K] -> y float32 [M],

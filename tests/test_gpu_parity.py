@@ -1239,3 +1239,68 @@ def test_matmul_dispatch_mfma_x_range(oracle, case):
     else:
         assert_f32_close(got, ref, group=M, what=case)
 
+
+
+# ------------------------------------------------------------------ batched GEMV (prefill GEMM)
+GEMM_CASES = [   # kind, tokens, M, K, first row (element offset = row * K)
+    ("Q4_K", 64, 512, 2048, 0), ("Q4_K", 100, 300, 2048, 0), ("Q4_K", 16, 256, 256, 0),
+    ("Q4_K", 200, 1000, 4096, 3), ("Q6_K", 64, 512, 2048, 0), ("Q6_K", 77, 333, 2048, 5),
+    ("Q6_K", 130, 256, 512, 0), ("Q6_K", 16, 17, 256, 0),
+    ("Q4_K", 7, 512, 2048, 0), ("Q6_K", 15, 100, 768, 0), ("Q8_0", 20, 96, 512, 0), ("Q4_K", 40, 64, 320, 0),
+]
+
+
+@pytest.mark.parametrize("kind,T,M,K,row0", GEMM_CASES)
+def test_matmul_rows(oracle, kind, T, M, K, row0):
+    """matmul_rows (T tokens in one call) against the oracle's GEMV of each
+    token (src/cuda/matmul_q4.cu:140-167): the matrix-core path for Q4_K / Q6_K
+    at 16 tokens or more (ragged token and row tiles, a row offset), the
+    per-token GEMV below 16 tokens, for K % 256 != 0 and for other types.
+    Output rows past T stay untouched."""
+    t = ops.GGML_TYPES[kind]
+    r = rng(T * 31 + M + K)
+    n_rows = M + row0
+    w = _gemv_weight(kind, n_rows, K, r)
+    x = r.standard_normal((T, K)).astype(F32)
+    out = torch.full((T + 1, M), 5.0, device="cuda")
+    ops.matmul_rows(dev(w), t, n_rows * K, dev(x), M, K, element_offset=row0 * K, out=out)
+    got = host(out)
+    ref = np.stack([oracle.gemv(w, t, x[i], M, K, element_offset=row0 * K, threads=THREADS) for i in range(T)])
+    assert_f32_close(got[:T], ref, group=M, what=f"{kind} {T}x{M}x{K} @ row {row0}")
+    assert np.all(got[T:] == 5.0)
+
+
+@pytest.mark.parametrize("kind,T,M,K", [("Q4_K", 4096, 8192, 2048), ("Q6_K", 1024, 2048, 4096)])
+def test_matmul_rows_prefill_shapes(oracle, kind, T, M, K):
+    """Prefill shapes (the GDN qkv projection over 4096 tokens; a Q6_K output
+    projection over 1024): sampled tokens against the oracle's GEMV and against
+    matmul_dispatch of the same token on the GPU, both within the fp32 bar;
+    inputs with a wide dynamic range (per-token scales 2^-20 .. 2^20) keep it."""
+    t = ops.GGML_TYPES[kind]
+    r = rng(T + M + K)
+    w = _gemv_weight(kind, M, K, r)
+    x = r.standard_normal((T, K)).astype(F32)
+    x *= np.exp2(r.integers(-20, 21, size=(T, 1))).astype(F32)
+    dw, dx = dev(w), dev(x)
+    got = host(ops.matmul_rows(dw, t, M * K, dx, M, K))
+    for i in (0, 1, 63, 64, T // 2 + 5, T - 1):
+        ref = oracle.gemv(w, t, x[i], M, K, threads=THREADS)
+        assert_f32_close(got[i], ref, group=M, what=f"{kind} token {i} vs oracle")
+        gv = host(ops.matmul_dispatch(dw, t, M * K, dx[i], M, K))
+        assert_f32_close(got[i], gv, group=M, what=f"{kind} token {i} vs matmul_dispatch")
+
+
+def test_matmul_rows_checks_shapes():
+    """Statuses of matmul_dispatch (src/cuda/matmul_q4.cu:187-195) plus the token count."""
+    from qwen35_hip._lib import QwenError
+
+    rows, K = 48, 2048
+    dw = dev(synth.q4k_table(rows, K))
+    dx = torch.zeros(32, K, device="cuda")
+    for M, off in ((rows + 1, 0), (0, 0), (rows, K)):
+        with pytest.raises(QwenError, match="GEMV shape exceeds tensor"):
+            ops.matmul_rows(dw, "Q4_K", rows * K, dx, M, K, element_offset=off)
+    with pytest.raises(QwenError):
+        ops.matmul_rows(dw, 3, rows * K, dx, rows, K)   # Q4_1: no path
+    empty = ops.matmul_rows(dw, "Q4_K", rows * K, dx[:0], rows, K)
+    assert empty.shape == (0, rows)
