@@ -25,9 +25,11 @@ void matmul_dispatch(const QuantTensor& weight, const float* x, float* y, int M,
 
 // matmul_dispatch for each of `rows` tokens in one call: y[t*M + m] = sum_k
 // W[element_offset + m*K + k] * x[t*K + k] (matrix cores for Q4_K / Q6_K at
-// rows >= 16, fp32 accuracy). Throws as matmul_dispatch.
-void matmul_rows(const QuantTensor& weight, const float* x, float* y, int rows, int M, int K,
-                 hipStream_t stream = nullptr, uint64_t element_offset = 0);
+// rows >= 16, fp32 accuracy), with a device workspace of
+// matmul_rows_workspace_bytes(rows, K) bytes. Throws as matmul_dispatch.
+size_t matmul_rows_workspace_bytes(int rows, int K);
+void matmul_rows(const QuantTensor& weight, const float* x, float* y, int rows, int M, int K, void* workspace,
+                 size_t workspace_bytes, hipStream_t stream = nullptr, uint64_t element_offset = 0);
 
 // n_sel expert GEMVs with the expert ids on the device: y[j] = W_{idx[j]} x_j,
 // expert e at element offset e * expert_stride, x_j = x + j * x_stride, y

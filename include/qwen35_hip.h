@@ -427,15 +427,25 @@ int qwen_matmul_dispatch(const void* weight, int type, uint64_t num_elements, co
  * for t < rows, m < M (x fp32 [rows x K], y fp32 [rows x M], row-major) -- the
  * reference's per-token matmul_dispatch over a prompt as one call. Q4_K and
  * Q6_K with K % 256 == 0, element_offset % 256 == 0, x 16-byte aligned and
- * rows >= 16 run on the matrix cores (x split exactly into three bf16 parts,
- * exact products, fp32 sums: an fp32 dot product's accuracy, not the
- * reference's bits); other cases run qwen_matmul_dispatch once per token.
- * rows == 0 is a no-op. Statuses and messages as qwen_matmul_dispatch; rows < 0
- * or a NULL x / y -> QWEN_STATUS_INVALID_ARGUMENT.
+ * rows >= 16 run on the matrix cores: each token row is scaled by a power of
+ * two and split exactly into two fp16 parts (prep kernel, into the workspace),
+ * the quants enter as exact fp16 integers, products are exact and sums fp32 --
+ * an fp32 dot product's accuracy, not the reference's bits. Those cases need a
+ * 16-byte aligned workspace of qwen_matmul_rows_workspace_bytes(rows, K)
+ * bytes (QWEN_STATUS_INVALID_ARGUMENT otherwise); the other cases run
+ * qwen_matmul_dispatch once per token and ignore it. A row of x holding an
+ * infinity gives non-finite outputs (the NaN / infinity pattern may differ
+ * from the reference's). rows == 0 is a no-op. Statuses and messages as
+ * qwen_matmul_dispatch; rows < 0 or a NULL x / y -> QWEN_STATUS_INVALID_ARGUMENT.
  * ref: src/cuda/matmul_q4.cu:140-167,185-207 (the GEMV it batches), called per
  * token by the layers (src/layer_gdn.cpp:83-86, src/layer_attn.cpp:85-87) */
 int qwen_matmul_rows(const void* weight, int type, uint64_t num_elements, const float* x, float* y,
-                     int rows, int M, int K, uint64_t element_offset, void* stream);
+                     int rows, int M, int K, uint64_t element_offset, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* Workspace bytes qwen_matmul_rows needs for rows tokens of K elements (0 when
+ * the call takes the per-token path: rows < 16 or K % 256 != 0). */
+size_t qwen_matmul_rows_workspace_bytes(int rows, int K);
 
 /* One projection of qwen_matmul_dispatch_multi: the arguments of one
  * qwen_matmul_dispatch call except x, K and the stream. */

@@ -4,33 +4,37 @@
 // matmul_dispatch (src/cuda/matmul_q4.cu:140-167,185-207) called once per
 // token; batched, it is a contraction for the matrix cores.
 //
-// Exact operands in bf16. The quants are small integers (Q4_K 0..15, Q6_K
-// q - 32 in -32..31), exact in bf16, so they are the B operand as they are. x
-// is split into three bf16 parts x = x1 + x2 + x3 by truncation (x1 keeps the
-// top 8 significant bits, x2 the next 8 of the remainder, x3 the rest), each
-// exact, so sum_k q x = sum_k q x1 + q x2 + q x3 with exact products and fp32
-// accumulation inside the MFMA -- the accuracy of an fp32 dot product at 3
-// bf16 MFMAs per product, well above the fp32 MFMA rate. The block scales are
-// applied per scale group on the fp32 results:
-//   Q4_K (32-element groups): sum (d sc q - dmin m) x = (d sc) P - (dmin m) S
-//   Q6_K (16-element groups): sum d sc (q - 32) x      = (d sc) P'
-// with P = sum q x, P' = sum (q - 32) x over the group and S = sum x. The
-// (d sc) P terms are one fp32 FMA per result and group; the Q4_K min terms of
-// a whole block, sum_g (dmin m_g) S_g, are one small fp32 MFMA product per
-// block (v_mfma_f32_16x16x4f32: 8 groups = K of 8) into the same
-// accumulators, so they cost no VALU per group.
+// Exact fp16 operands. A prep kernel scales each token row by a power of two,
+// v = x * 2^e with max |v| in [2^14, 2^15), and splits it into two fp16 parts
+// v = h + l (h = fp16(v), l = fp16(v - h)): |v - h - l| <= 2^-22 |v| (or
+// 2^-25 absolute for the smallest values), so the products below carry an
+// fp32 dot product's accuracy. The weights enter as exact small integers:
+//   Q4_K: B = q * sc (q 0..15, sc 0..63: at most 945, exact in fp16), so the
+//         MFMA accumulator sums a whole 256-element block across its eight
+//         scale groups, and per block
+//         y += d * P_block - dmin * sum_g m_g S_g        (P = sum (q sc) v)
+//         with S_g the group sums of v; the min terms are one fp32 MFMA
+//         product per block ([tokens x groups] x [groups x rows]).
+//   Q6_K: B = q - 32 (exact); the signed 8-bit scales do not fit in the fp16
+//         operand, so per 16-element group y += (d sc) P_g (one FMA).
+// The result is scaled back by 2^-e (exact). Products of fp16 values are exact
+// in the MFMA's fp32 accumulation, so the roundings are those of an fp32 sum.
+//
+// fp16 operands are built with v_perm / v_pk_add_f16 only: bytes b < 1024
+// placed under 0x64 give the fp16 1024 + b, and one packed fp16 add of -1024
+// (Q4_K after the integer q * sc, Q6_K -1056 for q - 32) leaves the exact
+// value. The perm pairs bytes (0, 2) and (1, 3) of a word, so the prep kernel
+// stores x in that order within each 4 consecutive elements (0, 2, 1, 3);
+// A and B then agree slot by slot.
 //
 // Work: a workgroup owns 64 tokens x 256 weight rows; wave w owns rows
-// 64w .. 64w+63 for all 64 tokens. Per 32-element stage the workgroup splits
-// x[64 tokens][32] into the three parts in LDS (one pass of 8 values per
-// thread; Q4_K also the per-token group sums), double-buffered so that one
-// barrier per stage suffices, with the next stage's x and quants loaded while
-// the current one is computed. Each wave reads its weight rows' quants and
-// scales straight from global memory and turns them into bf16 B operands in
-// registers. Q4_K runs 16 x 16 tiles on v_mfma_f32_16x16x32_bf16 (K = one
-// 32-element group); Q6_K runs 32 x 32 tiles on v_mfma_f32_32x32x16_bf16
-// (K = one 16-element group, full rate).
+// 64w .. 64w+63 for all 64 tokens. Per 32-element stage the workgroup copies
+// the two fp16 parts of x[64 tokens][32] to LDS (double-buffered, one barrier
+// per stage), with the next stage's x and quants loaded while the current one
+// is computed. Q4_K: 16 x 16 tiles on v_mfma_f32_16x16x32_f16. Q6_K: 32 x 32
+// tiles on v_mfma_f32_32x32x16_f16 (K = one 16-element scale group).
 #include <algorithm>
+#include <cfloat>
 
 #include "capi_common.hpp"
 #include "device_common.hpp"
@@ -39,7 +43,8 @@
 namespace qk {
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
@@ -48,37 +53,92 @@ constexpr int kGemmBlock = kGemmWaves * kWave;
 constexpr int kGT = 64;            // tokens per workgroup
 constexpr int kGR = 256;           // weight rows per workgroup (64 per wave)
 constexpr int kGemmMinRows = 16;   // fewer tokens: one GEMV per token
-constexpr int kXRow = 40;          // bf16 per staged token row (32 + 8 padding)
+constexpr int kXRow = 40;          // halves per staged token row (32 + 8 padding)
 
-typedef uint16_t XStage[3][kGT][kXRow];   // one stage of x: three bf16 parts
+typedef uint16_t XStage[2][kGT][kXRow];   // one stage of x: the two fp16 parts
 
-// x = x1 + x2 + x3, each a bf16 (the top halves of fp32 values), by truncation.
-__device__ __forceinline__ void split3(float x, uint32_t& a, uint32_t& b, uint32_t& c) {
-    const uint32_t xb = __float_as_uint(x);
-    const float r1 = x - __uint_as_float(xb & 0xffff0000u);
-    const uint32_t rb = __float_as_uint(r1);
-    const float r2 = r1 - __uint_as_float(rb & 0xffff0000u);
-    a = xb >> 16;
-    b = rb >> 16;
-    c = __float_as_uint(r2) >> 16;
-}
+// Workspace: per token the exponent e, the group sums of v per 32 elements and
+// the fp16 parts [T][K/32][2][32].
+inline size_t ws_align(size_t b) { return (b + 255) & ~size_t{255}; }
+inline size_t ws_exp_bytes(int T) { return ws_align(4 * static_cast<size_t>(T)); }
+inline size_t ws_sum_bytes(int T, int K) { return ws_align(4 * static_cast<size_t>(T) * (K / 32)); }
+inline size_t ws_bytes(int T, int K) { return ws_exp_bytes(T) + ws_sum_bytes(T, K) + 4 * static_cast<size_t>(T) * K; }
 
-// The bf16 (top halves) of two floats in one word, lo in bits 0..15.
-__device__ __forceinline__ uint32_t pack_top(float lo, float hi) {
-    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
-}
-
-// bf16 of the four bytes of v (small integers), each minus BIAS (exact).
-template <int BIAS>
-__device__ __forceinline__ void bytes_bf16(uint32_t v, uint32_t& w0, uint32_t& w1) {
-    float f[4] = {static_cast<float>(v & 0xff), static_cast<float>((v >> 8) & 0xff),
-                  static_cast<float>((v >> 16) & 0xff), static_cast<float>(v >> 24)};
-    if constexpr (BIAS != 0) {
+__device__ __forceinline__ float wave_max_abs(float v) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) f[i] -= static_cast<float>(BIAS);
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t half_bits_of(float v) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
+// One wave per token: e, the two fp16 parts of x * 2^e (element order 0, 2, 1, 3
+// within each 4) and the sums of x * 2^e per 32 elements. K % 256 == 0.
+__global__ __launch_bounds__(256) void gemm_prep_x(const float* __restrict__ x, int* __restrict__ ex,
+                                                   float* __restrict__ sx, uint16_t* __restrict__ xp, int T, int K) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= T) return;   // the whole wave
+    const float* row = x + static_cast<size_t>(t) * K;
+    float m = 0.f;
+    for (int k = 4 * lane; k < K; k += 256) {
+        const float4 v = ld4(row + k);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
-    w0 = pack_top(f[0], f[1]);
-    w1 = pack_top(f[2], f[3]);
+    m = wave_max_abs(m);
+    int e = 0;   // zero or non-finite rows: unscaled
+    if (m > 0.f && m <= FLT_MAX) {
+        int em;
+        frexpf(m, &em);   // m in [2^(em-1), 2^em)
+        e = 15 - em;
+    }
+    if (lane == 0) ex[t] = e;
+    const int nst = K >> 5;
+    for (int k = 4 * lane; k < K; k += 256) {
+        const float4 v4 = ld4(row + k);
+        const float v[4] = {ldexpf(v4.x, e), ldexpf(v4.y, e), ldexpf(v4.z, e), ldexpf(v4.w, e)};
+        uint32_t h[4], l[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const _Float16 hh = static_cast<_Float16>(v[i]);
+            h[i] = __builtin_bit_cast(uint16_t, hh);
+            l[i] = half_bits_of(v[i] - static_cast<float>(hh));
+        }
+        uint16_t* dst = xp + (static_cast<size_t>(t) * nst + (k >> 5)) * 64 + (k & 31);
+        *reinterpret_cast<uint2*>(dst) = make_uint2(h[0] | (h[2] << 16), h[1] | (h[3] << 16));
+        *reinterpret_cast<uint2*>(dst + 32) = make_uint2(l[0] | (l[2] << 16), l[1] | (l[3] << 16));
+        float s = (v[0] + v[1]) + (v[2] + v[3]);
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        s += __shfl_xor(s, 4);
+        if ((lane & 7) == 0) sx[static_cast<size_t>(t) * nst + (k >> 5)] = s;
+    }
+}
+
+// A thread's share of one stage of x: 32 bytes (part p: fp16 part p/2, halves
+// 16 (p%2) .. +15 of its token's 32).
+struct XRegs {
+    uint4 a, b;
+};
+
+__device__ __forceinline__ XRegs load_x(const uint16_t* __restrict__ src) {
+    return XRegs{ld16(src), ld16(src + 8)};
+}
+
+__device__ __forceinline__ void store_x(const XRegs& r, XStage& xs, int tok, int part) {
+    uint16_t* d = &xs[part >> 1][tok][16 * (part & 1)];
+    st16(d, r.a);
+    st16(d + 8, r.b);
+}
+
+// Bytes (0, 2) and (1, 3) of n placed under `hi` (byte values 0 or 0x64).
+__device__ __forceinline__ uint32_t bytes02(uint32_t hi, uint32_t n) { return __builtin_amdgcn_perm(hi, n, 0x04020400u); }
+__device__ __forceinline__ uint32_t bytes13(uint32_t hi, uint32_t n) { return __builtin_amdgcn_perm(hi, n, 0x04030401u); }
+
+__device__ __forceinline__ uint32_t hadd2(uint32_t w, _Float16 c) {
+    const f16x2_t r = __builtin_bit_cast(f16x2_t, w) + f16x2_t{c, c};
+    return __builtin_bit_cast(uint32_t, r);
 }
 
 // Q4_K (scale, min) of sub-block sb from the block header hdr (d, dmin,
@@ -91,36 +151,17 @@ __device__ __forceinline__ void q4k_scale_min(const uint4& hdr, int sb, uint32_t
     m = lo ? (b & 63) : (((c >> 4) & 15) | ((b >> 2) & 0x30));
 }
 
-// x of one stage for thread (token tok, part): 8 values at k0 + 8 part.
-struct XRegs {
-    float4 a, b;
-};
-
-__device__ __forceinline__ XRegs load_x(const float* __restrict__ xrow, int k0) {
-    return XRegs{ld4(xrow + k0), ld4(xrow + k0 + 4)};
+// fp16 q * sc of four quants (bytes of n, each < 16), sc < 64: two words in
+// the order (0, 2), (1, 3).
+__device__ __forceinline__ void q4_operand(uint32_t n, uint32_t sc, uint32_t& w02, uint32_t& w13) {
+    w02 = hadd2(__umul24(bytes02(0, n), sc) + 0x64006400u, static_cast<_Float16>(-1024.0f));
+    w13 = hadd2(__umul24(bytes13(0, n), sc) + 0x64006400u, static_cast<_Float16>(-1024.0f));
 }
 
-// Stage the three bf16 parts of a thread's 8 values; returns the sum of the
-// token's 32 values of the stage (complete in every lane of the token's quad).
-__device__ __forceinline__ float store_x(const XRegs& r, XStage& xs, int tok, int part) {
-    const float v[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
-    uint32_t p[3][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t a0, b0, c0, a1, b1, c1;
-        split3(v[2 * i], a0, b0, c0);
-        split3(v[2 * i + 1], a1, b1, c1);
-        p[0][i] = a0 | (a1 << 16);
-        p[1][i] = b0 | (b1 << 16);
-        p[2][i] = c0 | (c1 << 16);
-    }
-#pragma unroll
-    for (int q = 0; q < 3; ++q)
-        *reinterpret_cast<uint4*>(&xs[q][tok][8 * part]) = make_uint4(p[q][0], p[q][1], p[q][2], p[q][3]);
-    float s = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-    s += dpp_move<0xB1>(s);   // quad_perm [1,0,3,2]
-    s += dpp_move<0x4E>(s);   // quad_perm [2,3,0,1]
-    return s;
+// fp16 q - 32 of four 6-bit quants (bytes of q): two words in the order (0, 2), (1, 3).
+__device__ __forceinline__ void q6_operand(uint32_t q, uint32_t& w02, uint32_t& w13) {
+    w02 = hadd2(bytes02(0x64646464u, q), static_cast<_Float16>(-1056.0f));
+    w13 = hadd2(bytes13(0x64646464u, q), static_cast<_Float16>(-1056.0f));
 }
 
 // ------------------------------------------------------------------ Q4_K
@@ -128,91 +169,86 @@ __device__ __forceinline__ float store_x(const XRegs& r, XStage& xs, int tok, in
 // sub-block i/32 (src/cuda/matmul_q4.cu:76-96). Lane (lr, lk) of stage sb
 // takes elements 32 sb + 8 lk .. +7: qs bytes 16 + 32(sb/2) + 8 lk .. +7,
 // nibble sb%2.
-__global__ __launch_bounds__(kGemmBlock) void gemm_q4k(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                       float* __restrict__ y, int T, int M, int K, uint64_t ub0) {
+__global__ __launch_bounds__(kGemmBlock, 2) void gemm_q4k(const uint8_t* __restrict__ w, const int* __restrict__ ex,
+                                                          const float* __restrict__ sx,
+                                                          const uint16_t* __restrict__ xp, float* __restrict__ y,
+                                                          int T, int M, int K, uint64_t ub0) {
     __shared__ __align__(16) XStage xs[2];
-    __shared__ __align__(16) float ssum[2][8][kGT];   // [block parity][sub-block][token]
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int t0 = blockIdx.y * kGT;
     const int r0 = blockIdx.x * kGR + wv * 64;
-    const int nb = K >> 8;
+    const int nb = K >> 8, nst = K >> 5;
     const int tok = tid >> 2, part = tid & 3;
-    const float* xrow = x + static_cast<size_t>(min(t0 + tok, T - 1)) * K + 8 * part;
+    const uint16_t* xsrc = xp + static_cast<size_t>(min(t0 + tok, T - 1)) * nst * 64 + 32 * (part >> 1) +
+                           16 * (part & 1);
     const int lr = lane & 15, lk = lane >> 4;
     const uint8_t* wrow[4];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
         wrow[rt] = w + (ub0 + static_cast<uint64_t>(min(r0 + 16 * rt + lr, M - 1)) * nb) * 144;
+    // the min-term A operands read S of tokens 16 tt + lr, groups 4 j + lk
+    const float* srow[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) srow[tt] = sx + static_cast<size_t>(min(t0 + 16 * tt + lr, T - 1)) * nst + lk;
 
-    f32x4_t acc[4][4];
+    f32x4_t acc[4][4], C[4][4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) acc[tt][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int rt = 0; rt < 4; ++rt) acc[tt][rt] = C[tt][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     uint4 hdr[4];
     uint2 qb[4];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
-        hdr[rt] = *reinterpret_cast<const uint4*>(wrow[rt]);
+        hdr[rt] = ld16(wrow[rt]);
         qb[rt] = *reinterpret_cast<const uint2*>(wrow[rt] + 16 + 8 * lk);
     }
-    {
-        const float s = store_x(load_x(xrow, 0), xs[0], tok, part);
-        if (part == 0) ssum[0][0][tok] = s;
-    }
+    store_x(load_x(xsrc), xs[0], tok, part);
     __syncthreads();
 
-    const int stages = K >> 5;
-    for (int g = 0; g < stages; ++g) {
+    for (int g = 0; g < nst; ++g) {
         const int sb = g & 7, cur = g & 1;
         const int gn = g + 1;
-        const bool more = gn < stages;
-        if (sb == 7) {
-            // min terms of the block (all 8 group sums are staged): acc[t][row] -=
-            // sum_g (dmin m_g)[row] S_g[t], as [16 tokens x 4 groups] x [4 groups x
-            // 16 rows] fp32 products, twice.
-            const int par = (g >> 3) & 1;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                float bm[4];
-#pragma unroll
-                for (int rt = 0; rt < 4; ++rt) {
-                    uint32_t sc, mm;
-                    q4k_scale_min(hdr[rt], 4 * j + lk, sc, mm);
-                    bm[rt] = half_bits(hdr[rt].x >> 16) * static_cast<float>(mm);
-                }
-#pragma unroll
-                for (int tt = 0; tt < 4; ++tt) {
-                    const float a = -ssum[par][4 * j + lk][16 * tt + lr];
-#pragma unroll
-                    for (int rt = 0; rt < 4; ++rt)
-                        acc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bm[rt], acc[tt][rt], 0, 0, 0);
-                }
-            }
-        }
-        // this stage's B operands and group scales; then the quants and x of the
-        // next stage are loaded into the same registers, in flight during the products
-        bf16x8_t B[4];
-        float Ag[4];
+        const bool more = gn < nst;
+        // this stage's B operands; then the next stage's quants and x are loaded
+        // into the same registers, in flight during the products
+        f16x8_t B[4];
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
             const int shn = 4 * (sb & 1);
-            uint32_t e[4];
-            bytes_bf16<0>((qb[rt].x >> shn) & 0x0f0f0f0fu, e[0], e[1]);
-            bytes_bf16<0>((qb[rt].y >> shn) & 0x0f0f0f0fu, e[2], e[3]);
-            __builtin_memcpy(&B[rt], e, 16);
             uint32_t sc, mm;
             q4k_scale_min(hdr[rt], sb, sc, mm);
-            Ag[rt] = half_bits(hdr[rt].x & 0xffffu) * static_cast<float>(sc);
+            uint32_t e[4];
+            q4_operand((qb[rt].x >> shn) & 0x0f0f0f0fu, sc, e[0], e[1]);
+            q4_operand((qb[rt].y >> shn) & 0x0f0f0f0fu, sc, e[2], e[3]);
+            __builtin_memcpy(&B[rt], e, 16);
+        }
+        float dsc[4], dmn[2][4], smin[2][4];
+        if (sb == 7) {
+            // block epilogue operands (before the header is replaced)
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                dsc[rt] = half_bits(hdr[rt].x & 0xffffu);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    uint32_t sc, mm;
+                    q4k_scale_min(hdr[rt], 4 * j + lk, sc, mm);
+                    dmn[j][rt] = half_bits(hdr[rt].x >> 16) * static_cast<float>(mm);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt) smin[j][tt] = -srow[tt][(g & ~7) + 4 * j];
         }
         XRegs xn;
         if (more) {
-            xn = load_x(xrow, 32 * gn);
+            xn = load_x(xsrc + static_cast<size_t>(gn) * 64);
             const size_t blk = static_cast<size_t>(gn >> 3) * 144;
             if ((gn & 7) == 0) {
 #pragma unroll
-                for (int rt = 0; rt < 4; ++rt) hdr[rt] = *reinterpret_cast<const uint4*>(wrow[rt] + blk);
+                for (int rt = 0; rt < 4; ++rt) hdr[rt] = ld16(wrow[rt] + blk);
             }
             if ((gn & 1) == 0) {
 #pragma unroll
@@ -223,38 +259,44 @@ __global__ __launch_bounds__(kGemmBlock) void gemm_q4k(const uint8_t* __restrict
         const XStage& xc = xs[cur];
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
-            bf16x8_t A[3];
+            f16x8_t A[2];
 #pragma unroll
-            for (int q = 0; q < 3; ++q) A[q] = *reinterpret_cast<const bf16x8_t*>(&xc[q][16 * tt + lr][8 * lk]);
-            f32x4_t C[4];
+            for (int p = 0; p < 2; ++p) A[p] = *reinterpret_cast<const f16x8_t*>(&xc[p][16 * tt + lr][8 * lk]);
 #pragma unroll
-            for (int rt = 0; rt < 4; ++rt)
-                C[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[0], B[rt], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            for (int rt = 0; rt < 4; ++rt) C[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], B[rt], C[tt][rt], 0, 0, 0);
 #pragma unroll
-            for (int rt = 0; rt < 4; ++rt) C[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[1], B[rt], C[rt], 0, 0, 0);
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) C[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[2], B[rt], C[rt], 0, 0, 0);
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) acc[tt][rt][r] = __builtin_fmaf(Ag[rt], C[rt][r], acc[tt][rt][r]);
+            for (int rt = 0; rt < 4; ++rt) C[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1], B[rt], C[tt][rt], 0, 0, 0);
         }
-        if (more) {
-            const float s = store_x(xn, xs[cur ^ 1], tok, part);
-            if (part == 0) ssum[(gn >> 3) & 1][gn & 7][tok] = s;
+        if (sb == 7) {
+            // acc += d P_block; acc -= sum_g (dmin m_g) S_g as [16 tokens x 4 groups] x
+            // [4 groups x 16 rows] fp32 products, twice
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+                for (int rt = 0; rt < 4; ++rt) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[tt][rt][r] = __builtin_fmaf(dsc[rt], C[tt][rt][r], acc[tt][rt][r]);
+                    C[tt][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(smin[j][tt], dmn[j][rt], acc[tt][rt], 0, 0, 0);
+                }
         }
+        if (more) store_x(xn, xs[cur ^ 1], tok, part);
         __syncthreads();
     }
     // lane L holds C[4 (L/16) + r][L % 16] of tile (tt, rt): token 16 tt + 4 lk + r, row 16 rt + lr
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-            const int row = r0 + 16 * rt + lr;
+        for (int r = 0; r < 4; ++r) {
+            const int t = t0 + 16 * tt + 4 * lk + r;
+            if (t >= T) continue;
+            const int e = -ex[t];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = t0 + 16 * tt + 4 * lk + r;
-                if (t < T && row < M) y[static_cast<size_t>(t) * M + row] = acc[tt][rt][r];
+            for (int rt = 0; rt < 4; ++rt) {
+                const int row = r0 + 16 * rt + lr;
+                if (row < M) y[static_cast<size_t>(t) * M + row] = ldexpf(acc[tt][rt][r], e);
             }
         }
 }
@@ -295,15 +337,17 @@ __device__ __forceinline__ Q6Quants q6_load(const uint8_t* const (&wrow)[2], int
     return q;
 }
 
-__global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                          float* __restrict__ y, int T, int M, int K, uint64_t ub0) {
+__global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const uint8_t* __restrict__ w, const int* __restrict__ ex,
+                                                          const uint16_t* __restrict__ xp, float* __restrict__ y,
+                                                          int T, int M, int K, uint64_t ub0) {
     __shared__ __align__(16) XStage xs[2];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int t0 = blockIdx.y * kGT;
     const int r0 = blockIdx.x * kGR + wv * 64;
-    const int nb = K >> 8;
+    const int nb = K >> 8, nst = K >> 5;
     const int tok = tid >> 2, part = tid & 3;
-    const float* xrow = x + static_cast<size_t>(min(t0 + tok, T - 1)) * K + 8 * part;
+    const uint16_t* xsrc = xp + static_cast<size_t>(min(t0 + tok, T - 1)) * nst * 64 + 32 * (part >> 1) +
+                           16 * (part & 1);
     const int l32 = lane & 31, lh = lane >> 5;
     const uint8_t* wrow[2];
 #pragma unroll
@@ -326,18 +370,17 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const uint8_t* __restr
         __builtin_memcpy(&scl[rt], __builtin_assume_aligned(wrow[rt] + 192, 2), 16);
         dh[rt] = half_bits(*reinterpret_cast<const uint16_t*>(__builtin_assume_aligned(wrow[rt] + 208, 2)));
     }
-    store_x(load_x(xrow, 0), xs[0], tok, part);
+    store_x(load_x(xsrc), xs[0], tok, part);
     __syncthreads();
 
-    const int stages = K >> 5;
-    for (int g = 0; g < stages; ++g) {
+    for (int g = 0; g < nst; ++g) {
         const int sg = g & 7, quarter = sg & 3, cur = g & 1;
         const int gn = g + 1;
-        const bool more = gn < stages;
+        const bool more = gn < nst;
         // this stage's B operands and group scales (both steps); then the next
         // stage's quants, scales and x are loaded into the same registers
         const int nsh = 4 * (quarter >> 1), hsh = 2 * quarter;
-        bf16x8_t B[2][2];
+        f16x8_t B[2][2];
         float Ag[2][2];
 #pragma unroll
         for (int h = 0; h < 2; ++h)
@@ -346,8 +389,8 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const uint8_t* __restr
                 const uint32_t q0 = ((qc.ql[rt][h].x >> nsh) & 0x0f0f0f0fu) | (((qc.qh[rt][h].x >> hsh) & 0x03030303u) << 4);
                 const uint32_t q1 = ((qc.ql[rt][h].y >> nsh) & 0x0f0f0f0fu) | (((qc.qh[rt][h].y >> hsh) & 0x03030303u) << 4);
                 uint32_t e[4];
-                bytes_bf16<32>(q0, e[0], e[1]);
-                bytes_bf16<32>(q1, e[2], e[3]);
+                q6_operand(q0, e[0], e[1]);
+                q6_operand(q1, e[2], e[3]);
                 __builtin_memcpy(&B[h][rt], e, 16);
                 const int si = 2 * sg + h;   // scale byte si of the block
                 const uint32_t sw = si < 8 ? (si < 4 ? scl[rt].x : scl[rt].y) : (si < 12 ? scl[rt].z : scl[rt].w);
@@ -355,7 +398,7 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const uint8_t* __restr
             }
         XRegs xn;
         if (more) {
-            xn = load_x(xrow, 32 * gn);
+            xn = load_x(xsrc + static_cast<size_t>(gn) * 64);
             qc = q6_load(wrow, gn, lh);
             if ((gn & 7) == 0) {
 #pragma unroll
@@ -371,20 +414,19 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const uint8_t* __restr
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
-                bf16x8_t A[3];
+                f16x8_t A[2];
 #pragma unroll
-                for (int q = 0; q < 3; ++q)
-                    A[q] = *reinterpret_cast<const bf16x8_t*>(&xc[q][32 * tt + l32][16 * h + 8 * lh]);
+                for (int p = 0; p < 2; ++p)
+                    A[p] = *reinterpret_cast<const f16x8_t*>(&xc[p][32 * tt + l32][16 * h + 8 * lh]);
 #pragma unroll
                 for (int rt = 0; rt < 2; ++rt) {
-                    f32x16_t C;
+                    f32x16_t Cq;
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) C[i] = 0.f;
-                    C = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[0], B[h][rt], C, 0, 0, 0);
-                    C = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[1], B[h][rt], C, 0, 0, 0);
-                    C = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[2], B[h][rt], C, 0, 0, 0);
+                    for (int i = 0; i < 16; ++i) Cq[i] = 0.f;
+                    Cq = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[0], B[h][rt], Cq, 0, 0, 0);
+                    Cq = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[1], B[h][rt], Cq, 0, 0, 0);
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) acc[tt][rt][i] = __builtin_fmaf(Ag[h][rt], C[i], acc[tt][rt][i]);
+                    for (int i = 0; i < 16; ++i) acc[tt][rt][i] = __builtin_fmaf(Ag[h][rt], Cq[i], acc[tt][rt][i]);
                 }
             }
         if (more) store_x(xn, xs[cur ^ 1], tok, part);
@@ -394,14 +436,21 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const uint8_t* __restr
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-            const int row = r0 + 32 * rt + l32;
+        for (int i = 0; i < 16; ++i) {
+            const int t = t0 + 32 * tt + 8 * (i >> 2) + 4 * lh + (i & 3);
+            if (t >= T) continue;
+            const int e = -ex[t];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int t = t0 + 32 * tt + 8 * (i >> 2) + 4 * lh + (i & 3);
-                if (t < T && row < M) y[static_cast<size_t>(t) * M + row] = acc[tt][rt][i];
+            for (int rt = 0; rt < 2; ++rt) {
+                const int row = r0 + 32 * rt + l32;
+                if (row < M) y[static_cast<size_t>(t) * M + row] = ldexpf(acc[tt][rt][i], e);
             }
         }
+}
+
+bool gemm_path(int type, int rows, int K, uint64_t element_offset, const float* x) {
+    return (type == kQ4_K || type == kQ6_K) && rows >= kGemmMinRows && K % 256 == 0 && element_offset % 256 == 0 &&
+           aligned16(x) && rows <= 65535 * kGT;
 }
 
 }  // namespace
@@ -411,8 +460,13 @@ using namespace qk;
 
 extern "C" {
 
+size_t qwen_matmul_rows_workspace_bytes(int rows, int K) {
+    if (rows < kGemmMinRows || K <= 0 || K % 256 != 0) return 0;
+    return ws_bytes(rows, K);
+}
+
 int qwen_matmul_rows(const void* weight, int type, uint64_t num_elements, const float* x, float* y, int rows, int M,
-                     int K, uint64_t element_offset, void* stream) {
+                     int K, uint64_t element_offset, void* workspace, size_t workspace_bytes, void* stream) {
     if (!weight) return fail(QWEN_STATUS_INVALID_ARGUMENT, "tensor is not loaded");
     if (!type_supported(type)) return fail(QWEN_STATUS_UNSUPPORTED_TYPE, "unsupported GGML type %d", type);
     if (M <= 0 || K <= 0 || element_offset > num_elements ||
@@ -421,9 +475,7 @@ int qwen_matmul_rows(const void* weight, int type, uint64_t num_elements, const 
     QK_REQUIRE(rows >= 0, "matmul_rows: negative rows %d", rows);
     if (rows == 0) return ok();
     QK_REQUIRE(x && y, "matmul_rows: null pointer");
-    const bool mfma = (type == kQ4_K || type == kQ6_K) && rows >= kGemmMinRows && K % 256 == 0 &&
-                      element_offset % 256 == 0 && aligned16(x) && rows <= 65535 * kGT;
-    if (!mfma) {   // one GEMV per token (the reference's own loop)
+    if (!gemm_path(type, rows, K, element_offset, x)) {   // one GEMV per token (the reference's own loop)
         for (int t = 0; t < rows; ++t) {
             const int rc = qwen_matmul_dispatch(weight, type, num_elements, x + static_cast<size_t>(t) * K,
                                                 y + static_cast<size_t>(t) * M, M, K, element_offset, stream);
@@ -431,10 +483,22 @@ int qwen_matmul_rows(const void* weight, int type, uint64_t num_elements, const 
         }
         return ok();
     }
+    const size_t need = ws_bytes(rows, K);
+    QK_REQUIRE(workspace && workspace_bytes >= need && aligned16(workspace),
+               "matmul_rows: workspace of %zu bytes (16-byte aligned) needed, got %zu", need,
+               workspace ? workspace_bytes : size_t{0});
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    int* ex = reinterpret_cast<int*>(ws);
+    float* sx = reinterpret_cast<float*>(ws + ws_exp_bytes(rows));
+    uint16_t* xp = reinterpret_cast<uint16_t*>(ws + ws_exp_bytes(rows) + ws_sum_bytes(rows, K));
+    const hipStream_t s = as_stream(stream);
+    gemm_prep_x<<<blocks_for(rows, 4), 256, 0, s>>>(x, ex, sx, xp, rows, K);
     const dim3 grid(blocks_for(M, kGR), blocks_for(rows, kGT));
-    const auto k = type == kQ4_K ? gemm_q4k : gemm_q6k;
-    k<<<grid, kGemmBlock, 0, as_stream(stream)>>>(static_cast<const uint8_t*>(weight), x, y, rows, M, K,
-                                                  element_offset / 256);
+    const uint8_t* w = static_cast<const uint8_t*>(weight);
+    if (type == kQ4_K)
+        gemm_q4k<<<grid, kGemmBlock, 0, s>>>(w, ex, sx, xp, y, rows, M, K, element_offset / 256);
+    else
+        gemm_q6k<<<grid, kGemmBlock, 0, s>>>(w, ex, xp, y, rows, M, K, element_offset / 256);
     return check_launch("matmul_rows");
 }
 

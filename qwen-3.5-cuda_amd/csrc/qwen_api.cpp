@@ -234,10 +234,12 @@ void matmul_dispatch(const QuantTensor& w, const float* x, float* y, int M, int 
     check(status);
 }
 
-void matmul_rows(const QuantTensor& w, const float* x, float* y, int rows, int M, int K, hipStream_t stream,
-                 uint64_t element_offset) {
+size_t matmul_rows_workspace_bytes(int rows, int K) { return qwen_matmul_rows_workspace_bytes(rows, K); }
+
+void matmul_rows(const QuantTensor& w, const float* x, float* y, int rows, int M, int K, void* workspace,
+                 size_t workspace_bytes, hipStream_t stream, uint64_t element_offset) {
     const int status = qwen_matmul_rows(w.device_ptr, static_cast<int>(w.type), w.num_elements, x, y, rows, M, K,
-                                        element_offset, st(stream));
+                                        element_offset, workspace, workspace_bytes, st(stream));
     if (status == QWEN_STATUS_INVALID_ARGUMENT && !w.device_ptr)
         throw std::runtime_error("tensor '" + w.name + "' is not loaded");
     if (status == QWEN_STATUS_UNSUPPORTED_TYPE)

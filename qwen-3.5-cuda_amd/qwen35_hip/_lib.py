@@ -92,7 +92,8 @@ SIGNATURES: dict[str, list] = {
     "qwen_matmul_type_supported": [_I],
     "qwen_matmul_dispatch": [_P, _I, _U64, _P, _P, _I, _I, _U64, _P],
     "qwen_matmul_dispatch_multi": [_P, _I, _P, _I, _P],
-    "qwen_matmul_rows": [_P, _I, _U64, _P, _P, _I, _I, _I, _U64, _P],
+    "qwen_matmul_rows": [_P, _I, _U64, _P, _P, _I, _I, _I, _U64, _P, ctypes.c_size_t, _P],
+    "qwen_matmul_rows_workspace_bytes": [_I, _I],
     # GGUF loader (include/qwen35_gguf.h)
     "qwen_gguf_open": [ctypes.c_char_p, _P],
     "qwen_gguf_close": [_P],
@@ -109,6 +110,7 @@ SIGNATURES: dict[str, list] = {
 
 _RESTYPES = {"qwen_last_error": ctypes.c_char_p, "qwen_status_name": ctypes.c_char_p,
              "qwen_attn_decode_workspace_bytes": ctypes.c_size_t,
+             "qwen_matmul_rows_workspace_bytes": ctypes.c_size_t,
              "qwen_gdn_recurrent_chunked_workspace_bytes": ctypes.c_size_t,
              "qwen_moe_down_combine_workspace_bytes": ctypes.c_size_t,
              "qwen_moe_expert_swiglu_workspace_bytes": ctypes.c_size_t}

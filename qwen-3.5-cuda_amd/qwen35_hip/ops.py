@@ -726,11 +726,15 @@ def matmul_dispatch_multi(jobs, x, K: int, stream=None):
     return outs
 
 
+def matmul_rows_workspace_bytes(rows: int, K: int) -> int:
+    return load().qwen_matmul_rows_workspace_bytes(rows, K)
+
+
 def matmul_rows(weight, ggml_type, num_elements: int, x, M: int, K: int, element_offset: int = 0, out=None,
-                stream=None):
+                workspace=None, stream=None):
     """matmul_dispatch for every row of x: x float32 [rows, K] -> y float32 [rows, M],
     y[t, m] = sum_k W[element_offset + m*K + k] * x[t, k] (one call; matrix cores for
-    Q4_K / Q6_K at 16 rows or more)."""
+    Q4_K / Q6_K at 16 rows or more, with a workspace allocated here unless given)."""
     _dev(weight, dtype=torch.uint8)
     _dev(x, dtype=torch.float32)
     if x.dim() != 2 or x.shape[1] != K:
@@ -741,8 +745,11 @@ def matmul_rows(weight, ggml_type, num_elements: int, x, M: int, K: int, element
     _dev(out, dtype=torch.float32)
     if out.numel() < rows * M:
         raise ValueError(f"out has {out.numel()} elements, rows * M = {rows * M}")
+    if workspace is None:
+        workspace = torch.empty(max(1, matmul_rows_workspace_bytes(rows, K)), dtype=torch.uint8, device=x.device)
+    _dev(workspace, dtype=torch.uint8)
     check(load().qwen_matmul_rows(_p(weight), t, num_elements, _p(x), _p(out), rows, M, K, element_offset,
-                                  _stream(stream)))
+                                  _p(workspace), workspace.numel(), _stream(stream)))
     return out
 
 

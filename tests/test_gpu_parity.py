@@ -1304,3 +1304,23 @@ def test_matmul_rows_checks_shapes():
         ops.matmul_rows(dw, 3, rows * K, dx, rows, K)   # Q4_1: no path
     empty = ops.matmul_rows(dw, "Q4_K", rows * K, dx[:0], rows, K)
     assert empty.shape == (0, rows)
+    need = ops.matmul_rows_workspace_bytes(32, K)
+    assert need >= 32 * K * 4 and ops.matmul_rows_workspace_bytes(15, K) == 0
+    with pytest.raises(QwenError, match="workspace"):
+        ops.matmul_rows(dw, "Q4_K", rows * K, dx, rows, K, workspace=torch.empty(need - 16, dtype=torch.uint8,
+                                                                                   device="cuda"))
+
+
+def test_matmul_rows_nonfinite_and_zero_rows(oracle):
+    """A token row holding an infinity gives a non-finite output row (as the
+    reference's products do); an all-zero row gives zeros; neighbours are unaffected."""
+    K, M, T = 2048, 256, 32
+    w = synth.q4k_table(M, K)
+    x = rng(11).standard_normal((T, K)).astype(F32)
+    x[3, 100] = np.inf
+    x[5] = 0.0
+    got = host(ops.matmul_rows(dev(w), "Q4_K", M * K, dev(x), M, K))
+    assert not np.isfinite(got[3]).any()
+    assert np.all(got[5] == 0.0)
+    for i in (0, 4, 6, T - 1):
+        assert_f32_close(got[i], oracle.gemv(w, 12, x[i], M, K), group=M, what=f"token {i}")
