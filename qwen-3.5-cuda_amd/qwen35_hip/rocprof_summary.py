@@ -54,6 +54,9 @@ NAMES = [
     ("values_kernel", "attn_values (staged)"),
     ("topk_rows_kernel", "moe_topk_rows"),
     ("weighted_sum_v4", "moe_weighted_sum_rows"),
+    ("gemm_prep_x", "matmul_rows prep (x to fp16 parts)"),
+    ("gemm_q4k", "matmul_rows Q4_K GEMM, fp16 MFMA"),
+    ("gemm_q6k", "matmul_rows Q6_K GEMM, fp16 MFMA"),
 ]
 
 # algorithmic bytes per call at the BASELINE configs (bench.py computes the same)
