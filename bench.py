@@ -435,6 +435,25 @@ def build_next_rows(torch, ops, synth, host):
         k.no_cpu = True
         ks.append(k)
 
+    # The same GDN layer over a 4096-token prompt in one pass (GdnLayerDecode.prefill: GEMM
+    # projections, front end over all rows, chunked recurrence); the reference runs the
+    # decode step 4096 times. Bytes: weights once, x and out, the state read and written.
+    TP = 4096
+    lxs = torch.from_numpy((0.3 * rng.standard_normal((TP, 2048))).astype(np.float32)).to(dev)
+    lpo = torch.empty((TP, 2048), dtype=torch.float32, device=dev)
+
+    def mk_pre(i):
+        layer = GdnLayerDecode(*lw, conv_w, la, ldt, lnw)
+        return lambda: layer.prefill(lxs, lpo)
+    nbp = sum(t.numel() for t in lw) + 2 * TP * 2048 * 4 + 2 * vh * dk * dv * 4
+    k = Kernel("gdn_layer_prefill_4096", "one GDN layer over a 4096-token prompt in one pass (matmul_rows "
+               "projections, front end, chunked recurrence, gated norm), eager wall clock per call", nbp, 1 << 30,
+               mk_pre)
+    k.layer = True
+    k.no_cpu = True
+    k.eager = True
+    ks.append(k)
+
     # One full-attention layer's decode step (layer_attn.cpp:63-111) at position 2047 of a
     # 4096-row cache: the reference's fifteen calls against the fused five. Bytes: the four
     # Q4_K projections and the 2048 K and V rows read.

@@ -21,6 +21,13 @@ history, recurrent state, per-token buffers; forward src/layer_gdn.cpp:78-113):
 Both update the layer's conv history and recurrent state (the fused step writes
 the new history into a second buffer and the two are swapped, since the
 one-launch step cannot update it in place).
+
+`GdnLayerDecode.prefill(xs)` runs a prompt of T tokens through the same layer
+in one pass, where the reference runs its decode forward T times: the four
+input projections and the output projection as `matmul_rows` GEMMs, the front
+end over all rows (`gdn_frontend_rows`, history carried), the gates of all
+rows, the chunked recurrence (`gdn_recurrent_chunked`) and the gated norm. It
+leaves the history and state where T decode steps leave them.
 """
 
 from __future__ import annotations
@@ -89,6 +96,34 @@ class GdnLayerDecode:
         ops.gdn_norm_gate_rows(self.core.view(self.vh, self.dv), self.z.view(self.vh, self.dv), self.norm_w,
                                out=self.normed.view(self.vh, self.dv), eps=self.eps)
         self._proj("out", self.normed, out, self.vd)
+        return out
+
+
+    def prefill(self, xs, out=None):
+        """xs [T, d_model] -> out [T, d_model]: T tokens of this layer in one pass
+        (src/layer_gdn.cpp:78-113 applied token by token in the reference)."""
+        T = xs.shape[0]
+        f = dict(dtype=torch.float32, device=xs.device)
+        out = torch.empty((T, self.dm), **f) if out is None else out
+        ws = torch.empty(max(1, ops.matmul_rows_workspace_bytes(T, self.dm), ops.matmul_rows_workspace_bytes(T, self.vd)),
+                         dtype=torch.uint8, device=xs.device)
+        proj = {}
+        for n in ("qkv", "z", "beta", "alpha"):
+            w, M = self.w[n]
+            proj[n] = ops.matmul_rows(w, self.wtype, M * self.dm, xs, M, self.dm, workspace=ws)
+        conv = torch.empty((T, self.cd), **f)
+        ops.gdn_frontend_rows(proj["qkv"], self.conv_w, self.history, self._history_next, y=conv, k_heads=self.kh,
+                              key_dim=self.dk, eps=self.eps)
+        self.history, self._history_next = self._history_next, self.history
+        beta, decay = torch.empty((T, self.vh), **f), torch.empty((T, self.vh), **f)
+        ops.gdn_gate_values_rows(proj["beta"], proj["alpha"], self.a, self.dt, beta=beta, decay=decay)
+        core = torch.empty((T, self.vd), **f)
+        ops.gdn_recurrent_chunked(self.state, conv, beta, decay, self.kh, self.vh, self.dk, self.dv, out=core)
+        normed = torch.empty_like(core)
+        ops.gdn_norm_gate_rows(core.view(T, self.vh, self.dv), proj["z"].view(T, self.vh, self.dv), self.norm_w,
+                               out=normed.view(T, self.vh, self.dv), eps=self.eps)
+        w, M = self.w["out"]
+        ops.matmul_rows(w, self.wtype, M * self.vd, normed, M, self.vd, out=out, workspace=ws)
         return out
 
 

@@ -658,6 +658,50 @@ def test_gdn_layer_decode_fused_equals_reference_launches():
         assert np.array_equal(host(fus.history), host(ref.history)), f"token {t} history"
 
 
+@pytest.mark.parametrize("T", [16, 100, 200])
+def test_gdn_layer_prefill_equals_decode_steps(T):
+    """A prompt of T tokens through a GDN layer in one pass (GEMM projections,
+    front end over all rows, chunked recurrence) against T decode steps of the
+    same layer (src/layer_gdn.cpp:78-113 per token), from the same random
+    history and state: outputs, final state and history. The two sum the
+    projections, the L2 norms and the recurrence in different orders. The
+    synthetic Q4_K weights have a mean near +1, so each projection of a
+    zero-mean x cancels ~45x over K = 2048 and the two paths' inputs to the
+    recurrence differ by ~1e-6 relative; the recurrence carries that into its
+    state. Bars: outputs 1e-4 of the row rms, state 2e-3 of the head rms (small
+    entries of strongly decayed heads, measured up to 1e-3 of their row rms), history
+    (projection outputs) 1e-5 of the token's rms. A wiring mistake (a layout, a carried buffer)
+    gives errors of order 1."""
+    from qwen35_hip.decode_layers import GdnLayerDecode
+
+    r = rng(T + 5)
+    dm, kh, vh, dk, dv = 2048, 16, 32, 128, 128
+    cd, vd = 2 * kh * dk + vh * dv, vh * dv
+
+    def q4(M, K, s):
+        return dev(synth.q4k_table(M, K, seed_tensor=s))
+    wq, wz, wb, wa, wo = q4(cd, dm, 40), q4(vd, dm, 41), q4(vh, dm, 42), q4(vh, dm, 43), q4(dm, vd, 44)
+    conv_w = dev((0.5 * r.standard_normal((cd, 4))).astype(F32))
+    a = dev(-np.exp(r.standard_normal(vh)).astype(F32))
+    dt = dev(r.uniform(-1, 1, vh).astype(F32))
+    nw = dev((1 + 0.1 * r.standard_normal(dv)).astype(F32))
+    step = GdnLayerDecode(wq, wz, wb, wa, wo, conv_w, a, dt, nw)
+    pre = GdnLayerDecode(wq, wz, wb, wa, wo, conv_w, a, dt, nw)
+    hist0 = dev(r.standard_normal((cd, 3)).astype(F32))
+    st0 = dev((0.05 * r.standard_normal((vh, dk, dv))).astype(F32))
+    for layer in (step, pre):
+        layer.history.copy_(hist0)
+        layer.state.copy_(st0)
+    xs = dev((0.3 * r.standard_normal((T, dm))).astype(F32))
+    o_step = np.stack([host(step.forward(xs[t], torch.empty(dm, device="cuda"))) for t in range(T)])
+    o_pre = host(pre.prefill(xs))
+    assert_f32_close(o_pre, o_step, group=dm, rtol=1e-4, what=f"{T} tokens output")
+    assert_f32_close(host(pre.state), host(step.state), group=dk * dv, rtol=2e-3, what="state")
+    # history [C, 3] holds the last 3 tokens' qkv projections: compare per token (rms over its C channels)
+    assert_f32_close(np.ascontiguousarray(host(pre.history).T), np.ascontiguousarray(host(step.history).T), group=cd,
+                     what="history")
+
+
 def _attn_layer_pair(r, max_seq_len):
     from qwen35_hip.decode_layers import AttnLayerDecode
 
