@@ -95,6 +95,12 @@ struct GemvJob {
 };
 void matmul_dispatch_multi(const GemvJob* jobs, int n, const float* x, int K, hipStream_t stream = nullptr);
 
+// matmul_rows for the n jobs of one x [rows x K] (one prep, one GEMM launch per
+// K-quant type): job j writes y_j [rows x M_j]; split must be 0. Bit-equal to n
+// matmul_rows calls. Throws as matmul_dispatch_multi.
+void matmul_rows_multi(const GemvJob* jobs, int n, const float* x, int rows, int K, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream = nullptr);
+
 // out[i] = element (row * cols + i) of `tensor`.  ref: include/matmul_q4.hpp:24-30
 void dequantize_row(const QuantTensor& tensor, float* out, int row, int cols, hipStream_t stream = nullptr);
 

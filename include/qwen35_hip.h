@@ -474,6 +474,18 @@ typedef struct qwen_gemv_desc {
  * (q|gate, k, v), src/layer_moe.cpp:98 (router), :145-147 (shared expert gate logit, gate, up). */
 int qwen_matmul_dispatch_multi(const qwen_gemv_desc* descs, int n, const float* x, int K, void* stream);
 
+/* qwen_matmul_rows for n matrices of the same x [rows x K]: y_j [rows x M_j] =
+ * x W_j^T for each descriptor (split must be 0), with the results of n
+ * qwen_matmul_rows calls bit for bit. x is prepared once (one prep launch) and
+ * the Q4_K / Q6_K matrices of one type run in one GEMM launch (up to 8 per
+ * launch), so small matrices (a layer's 32-row gate projections) share the
+ * launch of the large ones; other types and offsets take the per-token path.
+ * Validation as qwen_matmul_dispatch_multi; workspace as qwen_matmul_rows
+ * (qwen_matmul_rows_workspace_bytes(rows, K)). 0 <= n <= 64.
+ * ref: the per-token calls of src/layer_gdn.cpp:83-86, src/layer_attn.cpp:85-87 over a prompt */
+int qwen_matmul_rows_multi(const qwen_gemv_desc* descs, int n, const float* x, int rows, int K,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

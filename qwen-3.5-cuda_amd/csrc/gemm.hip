@@ -57,6 +57,33 @@ constexpr int kXRow = 40;          // halves per staged token row (32 + 8 paddin
 
 typedef uint16_t XStage[2][kGT][kXRow];   // one stage of x: the two fp16 parts
 
+// Matrices of one launch (all of one K-quant type, one x): workgroup column
+// blockIdx.x in [start[j], start[j+1]) works on rows (blockIdx.x - start[j]) * kGR ..
+// of matrix j.
+constexpr int kGemmJobs = 8;
+struct GemmJobs {
+    const uint8_t* w[kGemmJobs];
+    float* y[kGemmJobs];
+    uint64_t ub0[kGemmJobs];   // first block of row 0
+    int M[kGemmJobs];
+    int start[kGemmJobs + 1];
+    int n;
+};
+
+struct GemmJob {
+    const uint8_t* w;
+    float* y;
+    uint64_t ub0;
+    int M, mb;
+};
+
+__device__ __forceinline__ GemmJob gemm_job(const GemmJobs& jobs) {
+    const int bx = static_cast<int>(blockIdx.x);
+    int j = 0;
+    while (j + 1 < jobs.n && bx >= jobs.start[j + 1]) ++j;
+    return GemmJob{jobs.w[j], jobs.y[j], jobs.ub0[j], jobs.M[j], bx - jobs.start[j]};
+}
+
 // Workspace: per token the exponent e, the group sums of v per 32 elements and
 // the fp16 parts [T][K/32][2][32].
 inline size_t ws_align(size_t b) { return (b + 255) & ~size_t{255}; }
@@ -169,14 +196,18 @@ __device__ __forceinline__ void q6_operand(uint32_t q, uint32_t& w02, uint32_t& 
 // sub-block i/32 (src/cuda/matmul_q4.cu:76-96). Lane (lr, lk) of stage sb
 // takes elements 32 sb + 8 lk .. +7: qs bytes 16 + 32(sb/2) + 8 lk .. +7,
 // nibble sb%2.
-__global__ __launch_bounds__(kGemmBlock, 2) void gemm_q4k(const uint8_t* __restrict__ w, const int* __restrict__ ex,
+__global__ __launch_bounds__(kGemmBlock, 2) void gemm_q4k(const GemmJobs jobs, const int* __restrict__ ex,
                                                           const float* __restrict__ sx,
-                                                          const uint16_t* __restrict__ xp, float* __restrict__ y,
-                                                          int T, int M, int K, uint64_t ub0) {
+                                                          const uint16_t* __restrict__ xp, int T, int K) {
     __shared__ __align__(16) XStage xs[2];
+    const GemmJob job = gemm_job(jobs);
+    const uint8_t* __restrict__ w = job.w;
+    float* __restrict__ y = job.y;
+    const int M = job.M;
+    const uint64_t ub0 = job.ub0;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int t0 = blockIdx.y * kGT;
-    const int r0 = blockIdx.x * kGR + wv * 64;
+    const int r0 = job.mb * kGR + wv * 64;
     const int nb = K >> 8, nst = K >> 5;
     const int tok = tid >> 2, part = tid & 3;
     const uint16_t* xsrc = xp + static_cast<size_t>(min(t0 + tok, T - 1)) * nst * 64 + 32 * (part >> 1) +
@@ -337,13 +368,17 @@ __device__ __forceinline__ Q6Quants q6_load(const uint8_t* const (&wrow)[2], int
     return q;
 }
 
-__global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const uint8_t* __restrict__ w, const int* __restrict__ ex,
-                                                          const uint16_t* __restrict__ xp, float* __restrict__ y,
-                                                          int T, int M, int K, uint64_t ub0) {
+__global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const GemmJobs jobs, const int* __restrict__ ex,
+                                                          const uint16_t* __restrict__ xp, int T, int K) {
     __shared__ __align__(16) XStage xs[2];
+    const GemmJob job = gemm_job(jobs);
+    const uint8_t* __restrict__ w = job.w;
+    float* __restrict__ y = job.y;
+    const int M = job.M;
+    const uint64_t ub0 = job.ub0;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int t0 = blockIdx.y * kGT;
-    const int r0 = blockIdx.x * kGR + wv * 64;
+    const int r0 = job.mb * kGR + wv * 64;
     const int nb = K >> 8, nst = K >> 5;
     const int tok = tid >> 2, part = tid & 3;
     const uint16_t* xsrc = xp + static_cast<size_t>(min(t0 + tok, T - 1)) * nst * 64 + 32 * (part >> 1) +
@@ -448,9 +483,52 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const uint8_t* __restr
         }
 }
 
-bool gemm_path(int type, int rows, int K, uint64_t element_offset, const float* x) {
-    return (type == kQ4_K || type == kQ6_K) && rows >= kGemmMinRows && K % 256 == 0 && element_offset % 256 == 0 &&
-           aligned16(x) && rows <= 65535 * kGT;
+bool gemm_rows_ok(int rows, int K, const float* x) {
+    return rows >= kGemmMinRows && K % 256 == 0 && aligned16(x) && rows <= 65535 * kGT;
+}
+
+bool gemm_job_ok(int type, uint64_t element_offset) {
+    return (type == kQ4_K || type == kQ6_K) && element_offset % 256 == 0;
+}
+
+struct Prepared {
+    const int* ex;
+    const float* sx;
+    const uint16_t* xp;
+};
+
+// Checks the workspace and launches the prep kernel.
+int prepare_x(const float* x, int rows, int K, void* workspace, size_t workspace_bytes, hipStream_t s, Prepared& p) {
+    const size_t need = ws_bytes(rows, K);
+    QK_REQUIRE(workspace && workspace_bytes >= need && aligned16(workspace),
+               "matmul_rows: workspace of %zu bytes (16-byte aligned) needed, got %zu", need,
+               workspace ? workspace_bytes : size_t{0});
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    int* ex = reinterpret_cast<int*>(ws);
+    float* sx = reinterpret_cast<float*>(ws + ws_exp_bytes(rows));
+    uint16_t* xp = reinterpret_cast<uint16_t*>(ws + ws_exp_bytes(rows) + ws_sum_bytes(rows, K));
+    gemm_prep_x<<<blocks_for(rows, 4), 256, 0, s>>>(x, ex, sx, xp, rows, K);
+    p = Prepared{ex, sx, xp};
+    return check_launch("matmul_rows prep");
+}
+
+void launch_gemm(int type, const GemmJobs& jobs, const Prepared& p, int rows, int K, hipStream_t s) {
+    const dim3 grid(jobs.start[jobs.n], blocks_for(rows, kGT));
+    if (type == kQ4_K)
+        gemm_q4k<<<grid, kGemmBlock, 0, s>>>(jobs, p.ex, p.sx, p.xp, rows, K);
+    else
+        gemm_q6k<<<grid, kGemmBlock, 0, s>>>(jobs, p.ex, p.xp, rows, K);
+}
+
+// One GEMV per token (the reference's own loop).
+int per_token(const void* weight, int type, uint64_t num_elements, const float* x, float* y, int rows, int M, int K,
+              uint64_t element_offset, void* stream) {
+    for (int t = 0; t < rows; ++t) {
+        const int rc = qwen_matmul_dispatch(weight, type, num_elements, x + static_cast<size_t>(t) * K,
+                                            y + static_cast<size_t>(t) * M, M, K, element_offset, stream);
+        if (rc) return rc;
+    }
+    return ok();
 }
 
 }  // namespace
@@ -475,31 +553,81 @@ int qwen_matmul_rows(const void* weight, int type, uint64_t num_elements, const 
     QK_REQUIRE(rows >= 0, "matmul_rows: negative rows %d", rows);
     if (rows == 0) return ok();
     QK_REQUIRE(x && y, "matmul_rows: null pointer");
-    if (!gemm_path(type, rows, K, element_offset, x)) {   // one GEMV per token (the reference's own loop)
-        for (int t = 0; t < rows; ++t) {
-            const int rc = qwen_matmul_dispatch(weight, type, num_elements, x + static_cast<size_t>(t) * K,
-                                                y + static_cast<size_t>(t) * M, M, K, element_offset, stream);
-            if (rc) return rc;
-        }
-        return ok();
-    }
-    const size_t need = ws_bytes(rows, K);
-    QK_REQUIRE(workspace && workspace_bytes >= need && aligned16(workspace),
-               "matmul_rows: workspace of %zu bytes (16-byte aligned) needed, got %zu", need,
-               workspace ? workspace_bytes : size_t{0});
-    uint8_t* ws = static_cast<uint8_t*>(workspace);
-    int* ex = reinterpret_cast<int*>(ws);
-    float* sx = reinterpret_cast<float*>(ws + ws_exp_bytes(rows));
-    uint16_t* xp = reinterpret_cast<uint16_t*>(ws + ws_exp_bytes(rows) + ws_sum_bytes(rows, K));
+    if (!gemm_rows_ok(rows, K, x) || !gemm_job_ok(type, element_offset))
+        return per_token(weight, type, num_elements, x, y, rows, M, K, element_offset, stream);
     const hipStream_t s = as_stream(stream);
-    gemm_prep_x<<<blocks_for(rows, 4), 256, 0, s>>>(x, ex, sx, xp, rows, K);
-    const dim3 grid(blocks_for(M, kGR), blocks_for(rows, kGT));
-    const uint8_t* w = static_cast<const uint8_t*>(weight);
-    if (type == kQ4_K)
-        gemm_q4k<<<grid, kGemmBlock, 0, s>>>(w, ex, sx, xp, y, rows, M, K, element_offset / 256);
-    else
-        gemm_q6k<<<grid, kGemmBlock, 0, s>>>(w, ex, xp, y, rows, M, K, element_offset / 256);
+    Prepared p;
+    if (const int rc = prepare_x(x, rows, K, workspace, workspace_bytes, s, p)) return rc;
+    GemmJobs jobs{};
+    jobs.w[0] = static_cast<const uint8_t*>(weight);
+    jobs.y[0] = y;
+    jobs.ub0[0] = element_offset / 256;
+    jobs.M[0] = M;
+    jobs.start[0] = 0;
+    jobs.start[1] = static_cast<int>(blocks_for(M, kGR));
+    jobs.n = 1;
+    launch_gemm(type, jobs, p, rows, K, s);
     return check_launch("matmul_rows");
+}
+
+int qwen_matmul_rows_multi(const qwen_gemv_desc* descs, int n, const float* x, int rows, int K, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    QK_REQUIRE(n >= 0 && n <= 64, "matmul_rows_multi: n = %d outside [0, 64]", n);
+    if (n == 0) return ok();
+    QK_REQUIRE(descs, "matmul_rows_multi: null descriptors");
+    for (int j = 0; j < n; ++j) {
+        const qwen_gemv_desc& e = descs[j];
+        if (!e.weight) return fail(QWEN_STATUS_INVALID_ARGUMENT, "descriptor %d: tensor is not loaded", j);
+        if (!type_supported(e.type))
+            return fail(QWEN_STATUS_UNSUPPORTED_TYPE, "descriptor %d: unsupported GGML type %d", j, e.type);
+        if (e.M <= 0 || K <= 0 || e.element_offset > e.num_elements ||
+            static_cast<uint64_t>(e.M) * static_cast<uint64_t>(K) > e.num_elements - e.element_offset)
+            return fail(QWEN_STATUS_OUT_OF_RANGE, "descriptor %d: GEMV shape exceeds tensor (M=%d, K=%d)", j, e.M, K);
+        QK_REQUIRE(e.split == 0, "matmul_rows_multi: descriptor %d: split rows are not supported", j);
+        QK_REQUIRE(e.y, "matmul_rows_multi: descriptor %d has a null output", j);
+    }
+    QK_REQUIRE(rows >= 0, "matmul_rows_multi: negative rows %d", rows);
+    if (rows == 0) return ok();
+    QK_REQUIRE(x, "matmul_rows_multi: null x");
+    const bool gemm = gemm_rows_ok(rows, K, x);
+    const hipStream_t s = as_stream(stream);
+    Prepared p{};
+    bool prepared = false;
+    for (const int type : {static_cast<int>(kQ4_K), static_cast<int>(kQ6_K)}) {
+        GemmJobs jobs{};
+        auto flush = [&]() {
+            if (jobs.n == 0) return;
+            launch_gemm(type, jobs, p, rows, K, s);
+            jobs.n = 0;
+        };
+        for (int j = 0; gemm && j < n; ++j) {
+            const qwen_gemv_desc& e = descs[j];
+            if (e.type != type || !gemm_job_ok(e.type, e.element_offset)) continue;
+            if (!prepared) {
+                if (const int rc = prepare_x(x, rows, K, workspace, workspace_bytes, s, p)) return rc;
+                prepared = true;
+            }
+            const int k = jobs.n;
+            jobs.w[k] = static_cast<const uint8_t*>(e.weight);
+            jobs.y[k] = e.y;
+            jobs.ub0[k] = e.element_offset / 256;
+            jobs.M[k] = e.M;
+            if (k == 0) jobs.start[0] = 0;
+            jobs.start[k + 1] = jobs.start[k] + static_cast<int>(blocks_for(e.M, kGR));
+            jobs.n = k + 1;
+            if (jobs.n == kGemmJobs) flush();
+        }
+        flush();
+    }
+    if (prepared)
+        if (const int rc = check_launch("matmul_rows_multi")) return rc;
+    for (int j = 0; j < n; ++j) {   // the rest: one GEMV per token
+        const qwen_gemv_desc& e = descs[j];
+        if (gemm && gemm_job_ok(e.type, e.element_offset)) continue;
+        if (const int rc = per_token(e.weight, e.type, e.num_elements, x, e.y, rows, e.M, K, e.element_offset, stream))
+            return rc;
+    }
+    return ok();
 }
 
 }  // extern "C"

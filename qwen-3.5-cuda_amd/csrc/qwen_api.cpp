@@ -376,8 +376,9 @@ void moe_down_combine(const QuantTensor& w_down, uint64_t expert_stride, int n_e
     check(status);
 }
 
-void matmul_dispatch_multi(const GemvJob* jobs, int n, const float* x, int K, hipStream_t stream) {
-    if (n <= 0) return;
+namespace {
+// matmul_dispatch's checks and messages per job, then the C descriptor table.
+std::vector<qwen_gemv_desc> gemv_descs(const GemvJob* jobs, int n, int K) {
     std::vector<qwen_gemv_desc> d(static_cast<size_t>(n));
     for (int j = 0; j < n; ++j) {
         const QuantTensor& w = *jobs[j].weight;
@@ -391,7 +392,21 @@ void matmul_dispatch_multi(const GemvJob* jobs, int n, const float* x, int K, hi
         d[j] = qwen_gemv_desc{w.device_ptr, static_cast<int>(w.type), jobs[j].M, w.num_elements,
                               jobs[j].element_offset, jobs[j].y, jobs[j].split};
     }
+    return d;
+}
+}  // namespace
+
+void matmul_dispatch_multi(const GemvJob* jobs, int n, const float* x, int K, hipStream_t stream) {
+    if (n <= 0) return;
+    const std::vector<qwen_gemv_desc> d = gemv_descs(jobs, n, K);
     check(qwen_matmul_dispatch_multi(d.data(), n, x, K, st(stream)));
+}
+
+void matmul_rows_multi(const GemvJob* jobs, int n, const float* x, int rows, int K, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream) {
+    if (n <= 0) return;
+    const std::vector<qwen_gemv_desc> d = gemv_descs(jobs, n, K);
+    check(qwen_matmul_rows_multi(d.data(), n, x, rows, K, workspace, workspace_bytes, st(stream)));
 }
 
 void dequantize_row(const QuantTensor& tensor, float* out, int row, int cols, hipStream_t stream) {

@@ -94,6 +94,7 @@ SIGNATURES: dict[str, list] = {
     "qwen_matmul_dispatch_multi": [_P, _I, _P, _I, _P],
     "qwen_matmul_rows": [_P, _I, _U64, _P, _P, _I, _I, _I, _U64, _P, ctypes.c_size_t, _P],
     "qwen_matmul_rows_workspace_bytes": [_I, _I],
+    "qwen_matmul_rows_multi": [_P, _I, _P, _I, _I, _P, ctypes.c_size_t, _P],
     # GGUF loader (include/qwen35_gguf.h)
     "qwen_gguf_open": [ctypes.c_char_p, _P],
     "qwen_gguf_close": [_P],

@@ -24,7 +24,8 @@ one-launch step cannot update it in place).
 
 `GdnLayerDecode.prefill(xs)` runs a prompt of T tokens through the same layer
 in one pass, where the reference runs its decode forward T times: the four
-input projections and the output projection as `matmul_rows` GEMMs, the front
+input projections in one `matmul_rows_multi` (one prep, one GEMM launch) and the
+output projection in `matmul_rows`, the front
 end over all rows (`gdn_frontend_rows`, history carried), the gates of all
 rows, the chunked recurrence (`gdn_recurrent_chunked`) and the gated norm. It
 leaves the history and state where T decode steps leave them.
@@ -107,10 +108,10 @@ class GdnLayerDecode:
         out = torch.empty((T, self.dm), **f) if out is None else out
         ws = torch.empty(max(1, ops.matmul_rows_workspace_bytes(T, self.dm), ops.matmul_rows_workspace_bytes(T, self.vd)),
                          dtype=torch.uint8, device=xs.device)
-        proj = {}
-        for n in ("qkv", "z", "beta", "alpha"):
-            w, M = self.w[n]
-            proj[n] = ops.matmul_rows(w, self.wtype, M * self.dm, xs, M, self.dm, workspace=ws)
+        names = ("qkv", "z", "beta", "alpha")
+        outs = ops.matmul_rows_multi([(self.w[n][0], self.wtype, self.w[n][1] * self.dm, self.w[n][1], 0, None)
+                                      for n in names], xs, self.dm, workspace=ws)
+        proj = dict(zip(names, outs))
         conv = torch.empty((T, self.cd), **f)
         ops.gdn_frontend_rows(proj["qkv"], self.conv_w, self.history, self._history_next, y=conv, k_heads=self.kh,
                               key_dim=self.dk, eps=self.eps)

@@ -753,6 +753,32 @@ def matmul_rows(weight, ggml_type, num_elements: int, x, M: int, K: int, element
     return out
 
 
+def matmul_rows_multi(jobs, x, K: int, workspace=None, stream=None):
+    """jobs: (weight uint8 tensor, ggml type, num_elements, M, element_offset, out float32 [rows, M]
+    or None); y_j = x W_j^T for every job from one x [rows, K] (one prep, one GEMM launch per
+    K-quant type). Returns the outputs."""
+    _dev(x, dtype=torch.float32)
+    if x.dim() != 2 or x.shape[1] != K:
+        raise ValueError(f"x must be [rows, {K}], got {tuple(x.shape)}")
+    rows = x.shape[0]
+    descs = (GemvDesc * max(1, len(jobs)))()
+    outs = []
+    for j, (w, t, ne, M, off, out) in enumerate(jobs):
+        _dev(w, dtype=torch.uint8)
+        out = torch.empty(rows, M, dtype=torch.float32, device=x.device) if out is None else out
+        _dev(out, dtype=torch.float32)
+        if out.numel() < rows * M:
+            raise ValueError(f"job {j}: out has {out.numel()} elements, rows * M = {rows * M}")
+        descs[j] = GemvDesc(w.data_ptr(), GGML_TYPES[t] if isinstance(t, str) else int(t), M, ne, off, out.data_ptr(), 0)
+        outs.append(out)
+    if workspace is None:
+        workspace = torch.empty(max(1, matmul_rows_workspace_bytes(rows, K)), dtype=torch.uint8, device=x.device)
+    _dev(workspace, dtype=torch.uint8)
+    check(load().qwen_matmul_rows_multi(ctypes.cast(descs, ctypes.c_void_p), len(jobs), _p(x), rows, K,
+                                        _p(workspace), workspace.numel(), _stream(stream)))
+    return outs
+
+
 def matmul_dispatch(weight, ggml_type, num_elements: int, x, M: int, K: int, element_offset: int = 0, out=None,
                     stream=None):
     """weight: uint8 device tensor of GGML blocks; x float32 [K] -> y float32 [M],

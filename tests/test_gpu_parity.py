@@ -1334,6 +1334,33 @@ def test_matmul_rows_prefill_shapes(oracle, kind, T, M, K):
         assert_f32_close(got[i], gv, group=M, what=f"{kind} token {i} vs matmul_dispatch")
 
 
+@pytest.mark.parametrize("T", [16, 300])
+def test_matmul_rows_multi_equals_single_calls(T):
+    """Several matrices of one x in one call (one prep, one GEMM launch per K-quant
+    type): the GDN layer's qkv / z / beta / alpha shapes, a Q6_K matrix, a row offset,
+    a Q8_0 matrix and a block-misaligned offset (per-token path), and more Q4_K
+    matrices than one launch takes; each output bit-equal to its own matmul_rows call."""
+    import ggml_blocks
+
+    r = rng(T + 77)
+    K = 2048
+    specs = [("Q4_K", 8192, 0), ("Q4_K", 4096, 0), ("Q4_K", 32, 0), ("Q4_K", 32, 0), ("Q6_K", 300, 0),
+             ("Q4_K", 100, 5 * K), ("Q8_0", 64, 0), ("Q4_K", 48, 96 + K)] + \
+        [("Q4_K", 64 + 16 * i, 0) for i in range(8)]
+    jobs = []
+    for kind, M, off in specs:
+        t = ops.GGML_TYPES[kind]
+        n_el = M * K + off + (256 if off % 256 else 0)
+        n_el = -(-n_el // ggml_blocks.BLOCK[t][0]) * ggml_blocks.BLOCK[t][0]
+        w = dev(ggml_blocks.random_blocks(r, t, n_el // ggml_blocks.BLOCK[t][0]))
+        jobs.append((w, kind, n_el, M, off, torch.full((T, M), 3.0, device="cuda")))
+    x = dev(r.standard_normal((T, K)).astype(F32))
+    outs = ops.matmul_rows_multi(jobs, x, K)
+    for (w, kind, n_el, M, off, _), got in zip(jobs, outs):
+        ref = ops.matmul_rows(w, kind, n_el, x, M, K, element_offset=off)
+        assert_bits_equal(host(got), host(ref), what=f"{kind} {M} rows @ {off}")
+
+
 def test_matmul_rows_checks_shapes():
     """Statuses of matmul_dispatch (src/cuda/matmul_q4.cu:187-195) plus the token count."""
     from qwen35_hip._lib import QwenError
