@@ -131,3 +131,29 @@ def test_size_and_pointer_validation(lib):
     assert lib.qwen_swiglu_bf16(FAKE, FAKE, FAKE, -1, ST) == INV
     assert lib.qwen_shared_swiglu_sigmoid_rows_bf16(FAKE, FAKE, NULL, FAKE, 2, 8, ST) == INV
     assert "null" in msg(lib)
+
+
+def test_matmul_rows_host_validation(lib):
+    """matmul_rows / matmul_rows_multi reject bad arguments on the host, in
+    matmul_dispatch's order (src/cuda/matmul_q4.cu:187-195), before any launch;
+    the workspace size is the prep layout (exponents, group sums, fp16 parts)."""
+    INV, OK = _lib.STATUS_INVALID_ARGUMENT, _lib.STATUS_OK
+    UNS, OOR = _lib.STATUS_UNSUPPORTED_TYPE, _lib.STATUS_OUT_OF_RANGE
+    q4 = 12
+    assert lib.qwen_matmul_rows(NULL, q4, 4096, FAKE, FAKE, 32, 16, 256, 0, NULL, 0, ST) == INV
+    assert "not loaded" in msg(lib)
+    assert lib.qwen_matmul_rows(FAKE, 3, 4096, FAKE, FAKE, 32, 16, 256, 0, NULL, 0, ST) == UNS
+    assert lib.qwen_matmul_rows(FAKE, q4, 4096, FAKE, FAKE, 32, 17, 256, 0, NULL, 0, ST) == OOR
+    assert lib.qwen_matmul_rows(FAKE, q4, 4096, FAKE, FAKE, 32, 16, 256, 256, NULL, 0, ST) == OOR
+    assert lib.qwen_matmul_rows(FAKE, q4, 4096, FAKE, FAKE, -1, 16, 256, 0, NULL, 0, ST) == INV
+    assert lib.qwen_matmul_rows(FAKE, q4, 4096, NULL, NULL, 0, 16, 256, 0, NULL, 0, ST) == OK
+    # the matrix-core path needs its workspace: checked before the prep launch
+    aligned = 1 << 20
+    assert lib.qwen_matmul_rows(FAKE, q4, 4096, aligned, aligned, 32, 16, 256, 0, NULL, 0, ST) == INV
+    assert "workspace" in msg(lib)
+    assert lib.qwen_matmul_rows_workspace_bytes(15, 2048) == 0
+    assert lib.qwen_matmul_rows_workspace_bytes(64, 300) == 0
+    # 64 tokens x 2048: 256 B of exponents, 64 x 64 sums, 64 x 2048 x 2 halves
+    assert lib.qwen_matmul_rows_workspace_bytes(64, 2048) == 256 + 64 * 64 * 4 + 64 * 2048 * 4
+    assert lib.qwen_matmul_rows_multi(NULL, 65, FAKE, 32, 256, NULL, 0, ST) == INV
+    assert lib.qwen_matmul_rows_multi(NULL, 0, NULL, 32, 256, NULL, 0, ST) == OK
