@@ -101,45 +101,69 @@ __device__ __forceinline__ uint32_t half_bits_of(float v) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
 }
 
-// One wave per token: e, the two fp16 parts of x * 2^e (element order 0, 2, 1, 3
-// within each 4) and the sums of x * 2^e per 32 elements. K % 256 == 0.
-__global__ __launch_bounds__(256) void gemm_prep_x(const float* __restrict__ x, int* __restrict__ ex,
-                                                   float* __restrict__ sx, uint16_t* __restrict__ xp, int T, int K) {
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (t >= T) return;   // the whole wave
-    const float* row = x + static_cast<size_t>(t) * K;
-    float m = 0.f;
-    for (int k = 4 * lane; k < K; k += 256) {
-        const float4 v = ld4(row + k);
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+// The two fp16 parts of v (element order 0, 2, 1, 3) and the sums of v per 32
+// elements, for the 4 values of lane `lane` at k (k = 4 lane + 256 i).
+__device__ __forceinline__ void prep_store(const float4 v4, int e, int k, int lane, size_t t, int nst,
+                                           float* __restrict__ sx, uint16_t* __restrict__ xp) {
+    const float v[4] = {ldexpf(v4.x, e), ldexpf(v4.y, e), ldexpf(v4.z, e), ldexpf(v4.w, e)};
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const _Float16 hh = static_cast<_Float16>(v[i]);
+        h[i] = __builtin_bit_cast(uint16_t, hh);
+        l[i] = half_bits_of(v[i] - static_cast<float>(hh));
     }
-    m = wave_max_abs(m);
+    uint16_t* dst = xp + (t * nst + (k >> 5)) * 64 + (k & 31);
+    *reinterpret_cast<uint2*>(dst) = make_uint2(h[0] | (h[2] << 16), h[1] | (h[3] << 16));
+    *reinterpret_cast<uint2*>(dst + 32) = make_uint2(l[0] | (l[2] << 16), l[1] | (l[3] << 16));
+    float s = (v[0] + v[1]) + (v[2] + v[3]);
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if ((lane & 7) == 0) sx[t * nst + (k >> 5)] = s;
+}
+
+__device__ __forceinline__ int prep_exponent(float m) {
     int e = 0;   // zero or non-finite rows: unscaled
     if (m > 0.f && m <= FLT_MAX) {
         int em;
         frexpf(m, &em);   // m in [2^(em-1), 2^em)
         e = 15 - em;
     }
-    if (lane == 0) ex[t] = e;
+    return e;
+}
+
+__device__ __forceinline__ float max_abs4(float m, const float4& v) {
+    return fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+}
+
+// One wave per token: e, the two fp16 parts of x * 2^e (element order 0, 2, 1, 3
+// within each 4) and the sums of x * 2^e per 32 elements. K % 256 == 0. NIT > 0:
+// K == 256 NIT, the row is held in registers (read once); NIT == 0: any K, read twice.
+template <int NIT>
+__global__ __launch_bounds__(256) void gemm_prep_x(const float* __restrict__ x, int* __restrict__ ex,
+                                                   float* __restrict__ sx, uint16_t* __restrict__ xp, int T, int K) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= T) return;   // the whole wave
+    const float* row = x + static_cast<size_t>(t) * K;
     const int nst = K >> 5;
-    for (int k = 4 * lane; k < K; k += 256) {
-        const float4 v4 = ld4(row + k);
-        const float v[4] = {ldexpf(v4.x, e), ldexpf(v4.y, e), ldexpf(v4.z, e), ldexpf(v4.w, e)};
-        uint32_t h[4], l[4];
+    float m = 0.f;
+    if constexpr (NIT > 0) {
+        float4 v[NIT];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const _Float16 hh = static_cast<_Float16>(v[i]);
-            h[i] = __builtin_bit_cast(uint16_t, hh);
-            l[i] = half_bits_of(v[i] - static_cast<float>(hh));
+        for (int i = 0; i < NIT; ++i) {
+            v[i] = ld4(row + 4 * lane + 256 * i);
+            m = max_abs4(m, v[i]);
         }
-        uint16_t* dst = xp + (static_cast<size_t>(t) * nst + (k >> 5)) * 64 + (k & 31);
-        *reinterpret_cast<uint2*>(dst) = make_uint2(h[0] | (h[2] << 16), h[1] | (h[3] << 16));
-        *reinterpret_cast<uint2*>(dst + 32) = make_uint2(l[0] | (l[2] << 16), l[1] | (l[3] << 16));
-        float s = (v[0] + v[1]) + (v[2] + v[3]);
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        s += __shfl_xor(s, 4);
-        if ((lane & 7) == 0) sx[static_cast<size_t>(t) * nst + (k >> 5)] = s;
+        const int e = prep_exponent(wave_max_abs(m));
+        if (lane == 0) ex[t] = e;
+#pragma unroll
+        for (int i = 0; i < NIT; ++i) prep_store(v[i], e, 4 * lane + 256 * i, lane, t, nst, sx, xp);
+    } else {
+        for (int k = 4 * lane; k < K; k += 256) m = max_abs4(m, ld4(row + k));
+        const int e = prep_exponent(wave_max_abs(m));
+        if (lane == 0) ex[t] = e;
+        for (int k = 4 * lane; k < K; k += 256) prep_store(ld4(row + k), e, k, lane, t, nst, sx, xp);
     }
 }
 
@@ -507,7 +531,14 @@ int prepare_x(const float* x, int rows, int K, void* workspace, size_t workspace
     int* ex = reinterpret_cast<int*>(ws);
     float* sx = reinterpret_cast<float*>(ws + ws_exp_bytes(rows));
     uint16_t* xp = reinterpret_cast<uint16_t*>(ws + ws_exp_bytes(rows) + ws_sum_bytes(rows, K));
-    gemm_prep_x<<<blocks_for(rows, 4), 256, 0, s>>>(x, ex, sx, xp, rows, K);
+    const unsigned grid = blocks_for(rows, 4);
+    switch (K) {
+        case 512: gemm_prep_x<2><<<grid, 256, 0, s>>>(x, ex, sx, xp, rows, K); break;
+        case 1024: gemm_prep_x<4><<<grid, 256, 0, s>>>(x, ex, sx, xp, rows, K); break;
+        case 2048: gemm_prep_x<8><<<grid, 256, 0, s>>>(x, ex, sx, xp, rows, K); break;
+        case 4096: gemm_prep_x<16><<<grid, 256, 0, s>>>(x, ex, sx, xp, rows, K); break;
+        default: gemm_prep_x<0><<<grid, 256, 0, s>>>(x, ex, sx, xp, rows, K); break;
+    }
     p = Prepared{ex, sx, xp};
     return check_launch("matmul_rows prep");
 }
