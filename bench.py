@@ -59,8 +59,9 @@ class Kernel:
     """A config: `make(i)` returns a launch closure bound to buffer set i
     (set 0 = the base buffers; i > 0 = fresh copies)."""
 
-    def __init__(self, name, config, nbytes, footprint, make):
+    def __init__(self, name, config, nbytes, footprint, make, in_step=True):
         self.name, self.config, self.bytes, self.footprint, self.make = name, config, nbytes, footprint, make
+        self.in_step = in_step  # False: measured per kernel, its work done in the step by another entry point
         self.us = None
         self.copy_us = None
 
@@ -124,7 +125,7 @@ def build_workload(torch, ops, synth):
         gg, uu, hh = cp(g4, i), cp(u4, i), new(h4, i, h4)
         return lambda: ops.swiglu_bf16(gg, uu, hh)
     nb = 3 * g4.numel() * 2
-    ks.append(Kernel("swiglu_bf16", "C3b bf16 [4096x8x512]", nb, nb, mk_sw))
+    ks.append(Kernel("swiglu_bf16", "C3b bf16 [4096x8x512]", nb, nb, mk_sw, in_step=False))
 
     c = synth.c3_shared()
     host["shared_swiglu_sigmoid_bf16"] = c
@@ -135,7 +136,17 @@ def build_workload(torch, ops, synth):
         gg, uu, ll, hh = cp(g5, i), cp(u5, i), cp(l5, i), new(h5, i, h5)
         return lambda: ops.shared_swiglu_sigmoid_rows_bf16(gg, uu, ll, hh)
     nb = 3 * g5.numel() * 2 + l5.numel() * 4
-    ks.append(Kernel("shared_swiglu_sigmoid_bf16", "C3c bf16 [4096x512] + logits [4096]", nb, nb, mk_sh))
+    ks.append(Kernel("shared_swiglu_sigmoid_bf16", "C3c bf16 [4096x512] + logits [4096]", nb, nb, mk_sh,
+                     in_step=False))
+
+    # C3b + C3c as the MoE layer runs them: one launch (src/layer_moe.cpp:135,149,153)
+    def mk_rs(i):
+        gg, uu, hh = cp(g4, i), cp(u4, i), new(h4, i, h4)
+        sg, su, sl, sh = cp(g5, i), cp(u5, i), cp(l5, i), new(h5, i, h5)
+        return lambda: ops.swiglu_routed_shared_bf16(gg, uu, sg, su, sl, out=hh, shared_out=sh)
+    nb = 3 * g4.numel() * 2 + 3 * g5.numel() * 2 + l5.numel() * 4
+    ks.append(Kernel("swiglu_routed_shared_bf16", "C3b+C3c bf16 routed [4096x8x512] + shared [4096x512] x sigmoid, "
+                     "one launch", nb, nb, mk_rs))
 
     c = synth.c4_frontend()
     host["gdn_frontend"] = c
@@ -622,9 +633,59 @@ def measure_copy(torch, bench_lib, nbytes: int, spin: int, min_launches: int) ->
     return us
 
 
-def cpu_baseline(host, kernels, threads: int, budget_s: float, gemv=None):
-    """Times the oracle on a bounded sample of every config; returns per-kernel
-    results and the aggregate GB/s (full-step bytes / extrapolated full-step time)."""
+SWEEP_SIZES = [598_016, 1 << 20, 2 << 20, 4 << 20, 8 << 20, 12_599_296, 16 << 20, 18_878_464, 32 << 20, 64 << 20]
+
+
+def copy_sweep(torch, bench_lib, spin: int, min_launches: int) -> list[dict]:
+    """Streaming-copy forms at the small sizes where the fused kernels miss 70% of
+    peak (C1 0.6 MB, C3c 12.6 MB, C2 18.9 MB) and around them: one-shot grids of
+    1..16 16-byte vectors per thread and 64/256/1024-thread workgroups, with and
+    without the nontemporal hint; persistent (grid-stride) grids of 256..2048
+    workgroups; and the in-place form (src == dst, as C2 reads and writes the same
+    lines). `bytes` counts the read and the write, as the kernels' algorithmic
+    bytes do; each form is timed like a kernel (steady state, >= 1 GiB rotated)."""
+    forms = [(u, b, 0, nt, False) for nt in (1, 0) for b in (64, 256, 1024) for u in (1, 2, 4, 8, 16)]
+    forms += [(u, 256, g, 1, False) for u in (1, 4) for g in (256, 512, 1024, 2048)]
+    forms += [(u, 256, 0, 1, True) for u in (1, 2, 8)]
+    fn = bench_lib.qwen_bench_copy_form
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_int, ctypes.c_void_p]
+    out = []
+    for nbytes in SWEEP_SIZES:
+        half = (nbytes // 2 + 15) // 16 * 16
+        sets = n_sets(2 * half)
+        bufs = [(torch.empty(half, dtype=torch.uint8, device="cuda:0"),
+                 torch.empty(half, dtype=torch.uint8, device="cuda:0")) for _ in range(sets)]
+        best = None
+        for u, b, g, nt, inplace in forms:
+            def launcher(src, dst, u=u, b=b, g=g, nt=nt, inplace=inplace):
+                d = src if inplace else dst
+
+                def f():
+                    if fn(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(d.data_ptr()), half, u, b, g, nt,
+                          ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)):
+                        raise RuntimeError("qwen_bench_copy_form failed")
+                return f
+            us = steady_state_us(torch, [launcher(a, c) for a, c in bufs], max(1, -(-min_launches // sets)), spin,
+                                 repeats=3)
+            rec = {"bytes": 2 * half, "unroll": u, "block": b, "grid_cap": g, "nt": nt, "inplace": inplace,
+                   "us": round(us, 3), "gbps": round(2 * half / us / 1e3, 1)}
+            out.append(rec)
+            if not inplace and (best is None or us < best["us"]):
+                best = rec
+        print(f"# copy sweep {2 * half:>10d} B: best {best['us']:7.2f} us {best['gbps']:7.1f} GB/s "
+              f"(unroll {best['unroll']}, block {best['block']}, grid cap {best['grid_cap']}, nt {best['nt']})",
+              file=sys.stderr, flush=True)
+        del bufs
+        torch.cuda.empty_cache()
+    return out
+
+
+def cpu_rates_sampled(host, kernels, threads: int, budget_s: float, gemv=None):
+    """The oracle's CPU rate for the next-row kernels (decode GEMVs, routing,
+    attention, recurrence; not part of the step), timed on a bounded sample of
+    rows and scaled to the full shape; returns per-kernel results and the
+    aggregate GB/s."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import pyoracle as orc
 
@@ -699,14 +760,93 @@ def cpu_baseline(host, kernels, threads: int, budget_s: float, gemv=None):
     return per, tot_b / tot_t / 1e9
 
 
+def cpu_step_fns(orc, host, th: int) -> dict:
+    """The CPU restatement of every step kernel on its full BASELINE config, in
+    the reference's form: C3b and C3c are the two calls the reference makes
+    (src/layer_moe.cpp:135,149), C2 is per head norm + RoPE (layer_attn.cpp:91-96)."""
+    c = host
+    f = {
+        "rmsnorm": lambda: orc.rmsnorm_rows(c["rmsnorm"]["x"], c["rmsnorm"]["w"], threads=th),
+        "qk_norm_rope": lambda: orc.qk_norm_rope_rows(
+            c["qk_norm_rope"]["q"], c["qk_norm_rope"]["k"], c["qk_norm_rope"]["qw"], c["qk_norm_rope"]["kw"],
+            pos=c["qk_norm_rope"]["pos"], rope_dim=64, theta=1e7, threads=th),
+        "residual_rmsnorm_bf16": lambda: orc.residual_rmsnorm_rows(
+            c["residual_rmsnorm_bf16"]["x"], c["residual_rmsnorm_bf16"]["branch"], c["residual_rmsnorm_bf16"]["w"],
+            threads=th),
+        "swiglu_bf16": lambda: orc.swiglu_bf16(c["swiglu_bf16"]["g"], c["swiglu_bf16"]["u"], threads=th),
+        "shared_swiglu_sigmoid_bf16": lambda: orc.shared_swiglu_sigmoid_bf16(
+            c["shared_swiglu_sigmoid_bf16"]["g"], c["shared_swiglu_sigmoid_bf16"]["u"],
+            c["shared_swiglu_sigmoid_bf16"]["logits"], threads=th),
+        "gdn_frontend": lambda: orc.gdn_frontend_rows(c["gdn_frontend"]["x"], c["gdn_frontend"]["w"],
+                                                      c["gdn_frontend"]["hist"], threads=th),
+        "gdn_norm_gate": lambda: orc.norm_gate_rows(c["gdn_norm_gate"]["x"], c["gdn_norm_gate"]["z"],
+                                                    c["gdn_norm_gate"]["w"], threads=th),
+    }
+    f["swiglu_routed_shared_bf16"] = lambda: (f["swiglu_bf16"](), f["shared_swiglu_sigmoid_bf16"]())
+    for name in ("dequant_gather_q4_k", "dequant_gather_q6_k"):
+        g = c[name]
+        f[name] = lambda g=g: orc.dequant_gather(g["table"], g["type"], g["ids"], 2048, threads=th)
+    return f
+
+
+def cpu_baseline(host, kernels, threads: int, repeats: int = 3) -> tuple[dict, float]:
+    """The reference CPU path on this host: the float-math build of the oracle
+    (oracle/liboracle_fp32.so: the same restatement of the reference kernels,
+    float expf / sqrtf / sinf / cosf and float sums, -O2, no fast-math) run on
+    the FULL config of every kernel, row-parallel over `threads` std::threads;
+    each kernel warmed once, then the median of `repeats` calls. Returns
+    per-kernel {us_per_call, gbps} and the step's aggregate GB/s (step bytes over
+    the sum of the step kernels' times)."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import pyoracle as orc
+
+    per, tot_b, tot_t = {}, 0.0, 0.0
+    with orc.fp32_math():
+        fns = cpu_step_fns(orc, host, threads)
+        for k in kernels:
+            fn = fns[k.name]
+            fn()
+            times = []
+            for _ in range(repeats):
+                t0 = time.perf_counter()
+                fn()
+                times.append(time.perf_counter() - t0)
+            sec = sorted(times)[len(times) // 2]
+            per[k.name] = {"gbps": k.bytes / sec / 1e9, "us_per_call": sec * 1e6}
+            if k.in_step:
+                tot_b += k.bytes
+                tot_t += sec
+    return per, tot_b / tot_t / 1e9
+
+
+def cpu_threads() -> tuple[int, int, int]:
+    """(threads used, CPUs this process may run on, logical CPUs of the host).
+    The pool is the CPUs this process may run on, capped by OMP_NUM_THREADS when
+    the environment sets it (the GPU box sets it to its CPU share per GPU)."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    used = min(avail, int(cap)) if cap.isdigit() and int(cap) > 0 else avail
+    return max(1, used), avail, os.cpu_count() or avail
+
+
 def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it: model name, family / model /
+    stepping, cache and clock of the first processor entry."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if not line.strip():
+                break
+            k, _, v = line.partition(":")
+            fields[k.strip()] = v.strip()
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    return (f"{fields.get('model name', 'unknown')} (vendor {fields.get('vendor_id', '?')}, family "
+            f"{fields.get('cpu family', '?')}, model {fields.get('model', '?')}, stepping {fields.get('stepping', '?')}, "
+            f"cache {fields.get('cache size', '?')}, {fields.get('cpu MHz', '?')} MHz)")
 
 
 def measure_gguf_load(torch, host, path: Path) -> dict:
@@ -780,6 +920,8 @@ def main() -> int:
     ap.add_argument("--json-out", default="", help="also write the JSON line to this file")
     ap.add_argument("--profile-gemv", type=int, default=0, metavar="N",
                     help="also run the LM-head GEMV N times after the step (counter runs)")
+    ap.add_argument("--copy-sweep", default="", metavar="JSON",
+                    help="only run the streaming-copy sweep at small sizes and write its records to JSON")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="also run the reference copy of BYTES (read) + BYTES (write) three times, for "
                          "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE against known traffic")
@@ -798,6 +940,10 @@ def main() -> int:
     bench_lib = ctypes.CDLL(str(PACKAGE_DIR / "libqwen35_benchutil.so"))
     bench_lib.qwen_bench_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
     torch.cuda.set_device(0)
+    if args.copy_sweep:
+        recs = copy_sweep(torch, bench_lib, int(spin_cycles_per_ms(torch) * 2.0), args.launches)
+        Path(args.copy_sweep).write_text(json.dumps(recs, indent=0) + "\n")
+        return 0
     t_setup = time.perf_counter()
     kernels, host = build_workload(torch, ops, synth)
     if args.kernels:
@@ -808,9 +954,10 @@ def main() -> int:
     spin = int(spin_cycles_per_ms(torch) * 2.0)
 
     # ---- the step: K graph replays (the contract)
-    ms_per_step, value, bytes_step = 0.0, 0.0, sum(k.bytes for k in kernels)
-    if kernels:  # (empty only in a profiling run of the decode GEMVs)
-        base = [k.make(0) for k in kernels]
+    step = [k for k in kernels if k.in_step]
+    ms_per_step, value, bytes_step = 0.0, 0.0, sum(k.bytes for k in step)
+    if step:  # (empty only in a profiling run of the decode GEMVs)
+        base = [k.make(0) for k in step]
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -905,30 +1052,36 @@ def main() -> int:
                     "copy_same_bytes_gbps": round(dom.bytes / dom.copy_us / 1e3, 1),
                     "copy_1gib_gbps": round(big / copy_big / 1e3, 1)}
 
-    # ---- CPU baseline
+    # ---- CPU baseline: the reference path on this host's cores, full configs
     cpu = None
     if not args.no_cpu and not args.kernels:
-        threads = max(1, min(16, os.cpu_count() or 1))
-        per, agg = cpu_baseline(host, kernels, threads, args.cpu_seconds)
-        # the reference's own host code is one thread: the same sample on one core
-        per1, agg1 = cpu_baseline(host, kernels, 1, args.cpu_seconds / 2)
-        rows_desc = ", ".join(f"{n} {p['sample_rows']}" for n, p in per.items())
+        threads, avail, logical = cpu_threads()
+        t_cpu = time.perf_counter()
+        per, agg = cpu_baseline(host, kernels, threads)
+        # the reference's own host code is one thread: the same full configs on one core
+        per1, agg1 = cpu_baseline(host, kernels, 1, repeats=1)
+        print(f"# cpu baseline: {agg:.2f} GB/s on {threads} threads, {agg1:.2f} GB/s on 1 "
+              f"({time.perf_counter() - t_cpu:.1f} s)", file=sys.stderr, flush=True)
         cpu = {"value": round(agg, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-               "sample": ("oracle/liboracle.so (C++ restatement of the reference kernels, -O2, row-parallel "
-                          "std::threads) on the first rows of each config (" + rows_desc + "), "
-                          f"extrapolated to the full step; host CPU {cpu_model()}"),
+               "sample": ("full configs C1-C5 (every row of every config, no extrapolation; C3 as the reference's "
+                          "two SwiGLU calls): oracle/liboracle_fp32.so, the C++ restatement of the reference kernels "
+                          "with float math, -O2, row-parallel std::threads; step GB/s = step bytes / summed "
+                          "per-kernel median time"),
+               "host_cpu": cpu_model(), "host_logical_cpus": logical, "cpus_available": avail,
                "per_kernel": {n: {"gbps": round(p["gbps"], 3), "us_per_call": round(p["us_per_call"], 1)}
                               for n, p in per.items()},
                "single_thread": {"value": round(agg1, 3), "cores": 1,
-                                 "per_kernel": {n: {"gbps": round(p["gbps"], 3)} for n, p in per1.items()}}}
+                                 "per_kernel": {n: {"gbps": round(p["gbps"], 3),
+                                                    "us_per_call": round(p["us_per_call"], 1)}
+                                                for n, p in per1.items()}}}
 
     next_rows = None
     if nxt:
         cpu_next = {}
         if not args.no_cpu:
-            threads = max(1, min(16, os.cpu_count() or 1))
+            threads = cpu_threads()[0]
             nxt_cpu = [k for k in nxt if not getattr(k, "no_cpu", False)]
-            cpu_next, _ = cpu_baseline(host, nxt_cpu, threads, args.cpu_seconds / 3,
+            cpu_next, _ = cpu_rates_sampled(host, nxt_cpu, threads, args.cpu_seconds / 3,
                                        gemv={k.name: getattr(k, "gemv", None) or getattr(k, "gdn", None) or
                                              getattr(k, "attn", None) or k.route for k in nxt_cpu})
         next_rows = {

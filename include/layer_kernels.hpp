@@ -81,6 +81,12 @@ void swiglu_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* hidden, int
 void shared_swiglu_sigmoid_rows_bf16(const uint16_t* gate, const uint16_t* up, const float* logits,
                                      uint16_t* hidden, int rows, int dim, hipStream_t stream);
 
+// Routed SwiGLU over n elements and the shared expert's gated SwiGLU (rows x dim)
+// in one launch; each output equals the separate call.
+void swiglu_routed_shared_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* hidden, int64_t n,
+                               const uint16_t* shared_gate, const uint16_t* shared_up, const float* logits,
+                               uint16_t* shared_hidden, int rows, int dim, hipStream_t stream);
+
 }  // namespace qwen
 
 #endif  // QWEN35_LAYER_KERNELS_HPP

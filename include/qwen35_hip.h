@@ -382,6 +382,19 @@ int qwen_swiglu_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* hidden,
 int qwen_shared_swiglu_sigmoid_rows_bf16(const uint16_t* gate, const uint16_t* up,
                                          const float* logits, uint16_t* hidden, int rows, int dim,
                                          void* stream);
+/* Both SwiGLUs of a MoE layer in one launch: the routed experts'
+ * hidden = bf16(silu(gate) * up) over n elements (as qwen_swiglu_bf16) and the
+ * shared expert's shared_hidden[t] = bf16((silu(shared_gate[t]) * shared_up[t]) *
+ * sigmoid(logits[t])) over rows x dim (as qwen_shared_swiglu_sigmoid_rows_bf16);
+ * each output equals its separate entry point bit for bit. Replaces the calls at
+ * src/layer_moe.cpp:135 (per expert), :149 and :153 (src/cuda/moe.cu:61-101).
+ * Either part may be empty (n == 0 or rows * dim == 0); pointers of an empty part
+ * may be NULL. Shapes or pointers outside the 16-byte vector kernel (n or dim not
+ * a multiple of 8, pointers not 16-byte aligned) run as the two separate launches. */
+int qwen_swiglu_routed_shared_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* hidden,
+                                   int64_t n, const uint16_t* shared_gate,
+                                   const uint16_t* shared_up, const float* logits,
+                                   uint16_t* shared_hidden, int rows, int dim, void* stream);
 
 /* ================================================================== dequant
  * GGML type ids as in include/quantized.hpp:12-35 (F32 0, F16 1, Q4_0 2,

@@ -10,7 +10,9 @@
 //
 // Math functions: the reference calls CUDA's expf / rsqrtf / cosf / sinf. The
 // oracle evaluates each in double precision and rounds to float once, so its
-// value is within one float ulp of the exact function value.
+// value is within one float ulp of the exact function value. (Built with
+// ORACLE_FP32_MATH, as liboracle_fp32.so, the same source evaluates them and the
+// sums of squares in float instead: that build is only the timed CPU baseline.)
 // Sums of squares: the reference's order is fixed by its launch shape (strided
 // per-thread partials, then a shuffle tree). The oracle accumulates the exact
 // squares in double and rounds the total once, which is closer to the exact sum
@@ -39,13 +41,16 @@ inline uint32_t f32_to_bits(float f) {
     return u;
 }
 
-// Split [0, n) into contiguous chunks, one per thread.
+// Split [0, n) into contiguous chunks, one per thread, each thread taking at
+// least kMinItemsPerThread items (a thread costs tens of microseconds to start).
+constexpr int64_t kMinItemsPerThread = 16;
+
 void parallel_for(int64_t n, int threads, const std::function<void(int64_t, int64_t)>& fn) {
-    if (threads <= 1 || n < 2) {
+    const int64_t t = std::min<int64_t>(threads, n / kMinItemsPerThread);
+    if (t <= 1) {
         fn(0, n);
         return;
     }
-    const int64_t t = std::min<int64_t>(threads, n);
     std::vector<std::thread> pool;
     pool.reserve(static_cast<size_t>(t));
     for (int64_t k = 0; k < t; ++k) {
@@ -56,6 +61,23 @@ void parallel_for(int64_t n, int threads, const std::function<void(int64_t, int6
     for (auto& th : pool) th.join();
 }
 
+#ifdef ORACLE_FP32_MATH
+// The CPU-baseline build (liboracle_fp32.so, timed by bench.py, never the
+// checker): float math as the reference's host-side checks write it
+// (tests/kernel_tests.cu:305-308: 1.f / std::sqrt(float), float products) --
+// the C library's float expf / sqrtf / cosf / sinf, and squares summed in one
+// float accumulator in index order.
+inline float sum_squares(const float* x, int64_t n) {
+    float s = 0.0f;
+    for (int64_t i = 0; i < n; ++i) s += x[i] * x[i];
+    return s;
+}
+
+inline float exp_f(float x) { return std::exp(x); }
+inline float rsqrt_f(float x) { return 1.0f / std::sqrt(x); }
+inline float cos_f(float x) { return std::cos(x); }
+inline float sin_f(float x) { return std::sin(x); }
+#else
 // Sum of squares of n floats: exact squares accumulated in double, rounded once.
 inline float sum_squares(const float* x, int64_t n) {
     double s = 0.0;
@@ -64,6 +86,10 @@ inline float sum_squares(const float* x, int64_t n) {
 }
 
 inline float exp_f(float x) { return static_cast<float>(std::exp(static_cast<double>(x))); }
+inline float rsqrt_f(float x) { return static_cast<float>(1.0 / std::sqrt(static_cast<double>(x))); }
+inline float cos_f(float x) { return static_cast<float>(std::cos(static_cast<double>(x))); }
+inline float sin_f(float x) { return static_cast<float>(std::sin(static_cast<double>(x))); }
+#endif
 
 }  // namespace
 
@@ -78,7 +104,7 @@ float or_silu(float x) { return x / (1.0f + exp_f(-x)); }
 float or_sigmoid(float x) { return 1.0f / (1.0f + exp_f(-x)); }
 
 // rsqrtf(x), evaluated exactly and rounded once.
-float or_rsqrt(float x) { return static_cast<float>(1.0 / std::sqrt(static_cast<double>(x))); }
+float or_rsqrt(float x) { return rsqrt_f(x); }
 
 // IEEE binary16 -> binary32, exact (subnormals included); NaNs stay NaN with
 // the quiet bit set.                     -- src/cuda/matmul_q4.cu:13-16
@@ -308,8 +334,8 @@ static void rope_head(float* p, int pos, int rope_dim, const float* den) {
     const int half = rope_dim / 2;
     for (int i = 0; i < half; ++i) {
         const float th = static_cast<float>(pos) / den[i];
-        const float c = static_cast<float>(std::cos(static_cast<double>(th)));
-        const float s = static_cast<float>(std::sin(static_cast<double>(th)));
+        const float c = cos_f(th);
+        const float s = sin_f(th);
         const float a = p[i];
         const float b = p[i + half];
         p[i] = a * c - b * s;
@@ -360,23 +386,25 @@ void or_qk_norm_rope_rows(float* q, float* k, const float* qw, const float* kw, 
 void or_conv_rows(const float* x, const float* w, const float* hist_in, float* hist_out, float* y, int rows,
                   int channels, int kernel, int threads) {
     const int hk = kernel - 1;
-    parallel_for(channels, threads, [&](int64_t lo, int64_t hi) {
-        std::vector<float> win(static_cast<size_t>(hk > 0 ? hk : 1));
-        for (int64_t c = lo; c < hi; ++c) {
-            for (int j = 0; j < hk; ++j) win[static_cast<size_t>(j)] = hist_in[c * hk + j];
-            const float* wc = w + c * kernel;
-            for (int64_t t = 0; t < rows; ++t) {
-                const float xv = x[t * channels + c];
+    // Input s of channel c: x row s, or for s < 0 the carried history (entry
+    // hk + s holds x[s]), so every output row depends only on inputs and the
+    // rows can be split across threads; the per-element fmaf order is the
+    // reference's sliding window, oldest first.
+    auto xin = [&](int64_t s, int64_t c) -> float {
+        return s >= 0 ? x[s * channels + c] : hist_in[c * hk + (hk + s)];
+    };
+    parallel_for(rows, threads, [&](int64_t lo, int64_t hi) {
+        for (int64_t t = lo; t < hi; ++t)
+            for (int64_t c = 0; c < channels; ++c) {
+                const float* wc = w + c * kernel;
                 float sum = 0.0f;
-                for (int j = 0; j < hk; ++j) sum = std::fmaf(win[static_cast<size_t>(j)], wc[j], sum);
-                sum = std::fmaf(xv, wc[kernel - 1], sum);
-                for (int j = 0; j + 1 < hk; ++j) win[static_cast<size_t>(j)] = win[static_cast<size_t>(j + 1)];
-                if (hk > 0) win[static_cast<size_t>(hk - 1)] = xv;
+                for (int j = 0; j < hk; ++j) sum = std::fmaf(xin(t - hk + j, c), wc[j], sum);
+                sum = std::fmaf(x[t * channels + c], wc[kernel - 1], sum);
                 y[t * channels + c] = or_silu(sum);
             }
-            for (int j = 0; j < hk; ++j) hist_out[c * hk + j] = win[static_cast<size_t>(j)];
-        }
     });
+    for (int64_t c = 0; c < channels; ++c)
+        for (int j = 0; j < hk; ++j) hist_out[c * hk + j] = xin(static_cast<int64_t>(rows) - hk + j, c);
 }
 
 // Per-head L2 norm of q and k in place; q also scaled by rsqrtf(dim). eps is

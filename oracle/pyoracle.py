@@ -70,7 +70,9 @@ _SIGS = {
     "or_attn_decode": ([_P, _P, _P, _P, _P, _P, _I, _I, _I, _I], None),
 }
 
-_lib = None
+_libs: dict[str, ctypes.CDLL] = {}
+_variant = "exact"
+_PATHS = {"exact": LIB_PATH, "fp32": HERE / "liboracle_fp32.so"}
 
 
 def build() -> None:
@@ -78,17 +80,34 @@ def build() -> None:
 
 
 def lib() -> ctypes.CDLL:
-    global _lib
-    if _lib is None:
-        if not LIB_PATH.exists():
+    """The checker build (double-evaluated math), or inside `fp32_math()` the
+    float-math build that bench.py times as the CPU baseline."""
+    if _variant not in _libs:
+        path = _PATHS[_variant]
+        if not path.exists():
             build()
-        l = ctypes.CDLL(str(LIB_PATH))
+        l = ctypes.CDLL(str(path))
         for name, (args, res) in _SIGS.items():
             f = getattr(l, name)
             f.argtypes = args
             f.restype = res
-        _lib = l
-    return _lib
+        _libs[_variant] = l
+    return _libs[_variant]
+
+
+class fp32_math:
+    """Context: the wrappers call liboracle_fp32.so (float math, float sums of
+    squares, as the reference's host loops) -- the timed CPU baseline only."""
+
+    def __enter__(self):
+        global _variant
+        self._prev, _variant = _variant, "fp32"
+        return self
+
+    def __exit__(self, *exc):
+        global _variant
+        _variant = self._prev
+        return False
 
 
 def _c(a: np.ndarray, dtype) -> np.ndarray:

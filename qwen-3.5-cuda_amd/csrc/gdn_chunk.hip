@@ -32,6 +32,7 @@
 
 #include "capi_common.hpp"
 #include "device_common.hpp"
+#include "gdn_common.hpp"
 
 namespace qk {
 namespace {
@@ -503,6 +504,9 @@ int qwen_gdn_recurrent_chunked(float* state, const float* q, const float* k, con
                                const float* decay, float* out, int rows, int key_heads, int value_heads,
                                int key_dim, int value_dim, int64_t qkv_stride, int64_t out_stride, void* workspace,
                                size_t workspace_bytes, void* stream) {
+    // The same limit as the token loop, checked before the path is chosen, so
+    // the status does not depend on which path a call's alignment selects.
+    QK_REQUIRE(value_dim <= kMaxValueDim, "GDN value dimension exceeds kernel limit");
     const bool chunked = key_dim == kDK && value_dim > 0 && value_dim % kNB == 0 && aligned16(q) && aligned16(k) &&
                          aligned16(workspace) && qkv_stride % 4 == 0 && rows > 0 && key_heads > 0 &&
                          value_heads > 0;

@@ -1,5 +1,6 @@
 // Gated DeltaNet pieces shared by the front-end kernels (gdn.hip) and the
-// fused decode step (gdn_state.hip), so both evaluate the same expressions.
+// fused decode step (gdn_state.hip), so both evaluate the same expressions, and
+// the limit the recurrent entry points share (gdn_state.hip, gdn_chunk.hip).
 #ifndef QWEN35_GDN_COMMON_HPP
 #define QWEN35_GDN_COMMON_HPP
 
@@ -8,6 +9,10 @@
 #include <cmath>
 
 namespace qk {
+
+// Largest value-head dimension the recurrence accepts; every recurrent entry
+// point rejects more with the reference's message (src/cuda/gdn.cu:167-169).
+constexpr int kMaxValueDim = 256;
 
 // Exactly-rounded 1/sqrt(n) for the q scale, so the device multiplies by the
 // same constant as the host oracle (src/cuda/gdn.cu:76).

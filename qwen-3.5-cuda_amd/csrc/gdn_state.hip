@@ -34,7 +34,6 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
-constexpr int kMaxValueDim = 256;  // src/cuda/gdn.cu:167-169
 
 // softplus with the reference's threshold; log1p(exp(x)) evaluated with the
 // accurate device expf / log1pf.

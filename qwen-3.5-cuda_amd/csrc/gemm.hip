@@ -123,14 +123,33 @@ __device__ __forceinline__ void prep_store(const float4 v4, int e, int k, int la
     if ((lane & 7) == 0) sx[t * nst + (k >> 5)] = s;
 }
 
+// Exponent slot of a token row holding an infinity: the fp16 split cannot carry
+// it (h = inf, l = inf - inf = NaN would turn the whole output row into NaN),
+// so the GEMM evaluates that row's outputs per element instead.
+constexpr int kRowNonFinite = 0x7fffffff;
+
+// e for a row whose largest |x| is m (NaN is ignored by the max; a NaN row's
+// outputs are NaN either way): zero rows unscaled, rows with an infinity marked.
 __device__ __forceinline__ int prep_exponent(float m) {
-    int e = 0;   // zero or non-finite rows: unscaled
-    if (m > 0.f && m <= FLT_MAX) {
+    if (!(m <= FLT_MAX)) return kRowNonFinite;
+    int e = 0;
+    if (m > 0.f) {
         int em;
         frexpf(m, &em);   // m in [2^(em-1), 2^em)
         e = 15 - em;
     }
     return e;
+}
+
+// y for (token row x, weight row at element `base`) when x holds an infinity:
+// the reference's per-element fp32 products and sum (src/cuda/matmul_q4.cu:
+// 140-167), so inf * w, 0 * inf = NaN and +inf + -inf = NaN give the same
+// pattern of infinities and NaNs as its GEMV.
+__device__ float row_dot_per_element(const uint8_t* __restrict__ w, int type, uint64_t base,
+                                     const float* __restrict__ x, int K) {
+    float s = 0.f;
+    for (int k = 0; k < K; ++k) s = __builtin_fmaf(dequant_elem(w, type, base + k), x[k], s);
+    return s;
 }
 
 __device__ __forceinline__ float max_abs4(float m, const float4& v) {
@@ -157,13 +176,15 @@ __global__ __launch_bounds__(256) void gemm_prep_x(const float* __restrict__ x, 
         }
         const int e = prep_exponent(wave_max_abs(m));
         if (lane == 0) ex[t] = e;
+        const int es = e == kRowNonFinite ? 0 : e;   // a marked row's parts are not used
 #pragma unroll
-        for (int i = 0; i < NIT; ++i) prep_store(v[i], e, 4 * lane + 256 * i, lane, t, nst, sx, xp);
+        for (int i = 0; i < NIT; ++i) prep_store(v[i], es, 4 * lane + 256 * i, lane, t, nst, sx, xp);
     } else {
         for (int k = 4 * lane; k < K; k += 256) m = max_abs4(m, ld4(row + k));
         const int e = prep_exponent(wave_max_abs(m));
         if (lane == 0) ex[t] = e;
-        for (int k = 4 * lane; k < K; k += 256) prep_store(ld4(row + k), e, k, lane, t, nst, sx, xp);
+        const int es = e == kRowNonFinite ? 0 : e;
+        for (int k = 4 * lane; k < K; k += 256) prep_store(ld4(row + k), es, k, lane, t, nst, sx, xp);
     }
 }
 
@@ -222,7 +243,8 @@ __device__ __forceinline__ void q6_operand(uint32_t q, uint32_t& w02, uint32_t& 
 // nibble sb%2.
 __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q4k(const GemmJobs jobs, const int* __restrict__ ex,
                                                           const float* __restrict__ sx,
-                                                          const uint16_t* __restrict__ xp, int T, int K) {
+                                                          const uint16_t* __restrict__ xp,
+                                                          const float* __restrict__ x, int T, int K) {
     __shared__ __align__(16) XStage xs[2];
     const GemmJob job = gemm_job(jobs);
     const uint8_t* __restrict__ w = job.w;
@@ -347,11 +369,20 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q4k(const GemmJobs jobs, c
         for (int r = 0; r < 4; ++r) {
             const int t = t0 + 16 * tt + 4 * lk + r;
             if (t >= T) continue;
-            const int e = -ex[t];
+            const int et = ex[t];
+            if (et == kRowNonFinite) {
+                for (int rt = 0; rt < 4; ++rt) {
+                    const int row = r0 + 16 * rt + lr;
+                    if (row < M)
+                        y[static_cast<size_t>(t) * M + row] = row_dot_per_element(
+                            w, kQ4_K, (ub0 + static_cast<uint64_t>(row) * nb) * 256, x + static_cast<size_t>(t) * K, K);
+                }
+                continue;
+            }
 #pragma unroll
             for (int rt = 0; rt < 4; ++rt) {
                 const int row = r0 + 16 * rt + lr;
-                if (row < M) y[static_cast<size_t>(t) * M + row] = ldexpf(acc[tt][rt][r], e);
+                if (row < M) y[static_cast<size_t>(t) * M + row] = ldexpf(acc[tt][rt][r], -et);
             }
         }
 }
@@ -393,7 +424,8 @@ __device__ __forceinline__ Q6Quants q6_load(const uint8_t* const (&wrow)[2], int
 }
 
 __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const GemmJobs jobs, const int* __restrict__ ex,
-                                                          const uint16_t* __restrict__ xp, int T, int K) {
+                                                          const uint16_t* __restrict__ xp,
+                                                          const float* __restrict__ x, int T, int K) {
     __shared__ __align__(16) XStage xs[2];
     const GemmJob job = gemm_job(jobs);
     const uint8_t* __restrict__ w = job.w;
@@ -498,11 +530,20 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const GemmJobs jobs, c
         for (int i = 0; i < 16; ++i) {
             const int t = t0 + 32 * tt + 8 * (i >> 2) + 4 * lh + (i & 3);
             if (t >= T) continue;
-            const int e = -ex[t];
+            const int et = ex[t];
+            if (et == kRowNonFinite) {
+                for (int rt = 0; rt < 2; ++rt) {
+                    const int row = r0 + 32 * rt + l32;
+                    if (row < M)
+                        y[static_cast<size_t>(t) * M + row] = row_dot_per_element(
+                            w, kQ6_K, (ub0 + static_cast<uint64_t>(row) * nb) * 256, x + static_cast<size_t>(t) * K, K);
+                }
+                continue;
+            }
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt) {
                 const int row = r0 + 32 * rt + l32;
-                if (row < M) y[static_cast<size_t>(t) * M + row] = ldexpf(acc[tt][rt][i], e);
+                if (row < M) y[static_cast<size_t>(t) * M + row] = ldexpf(acc[tt][rt][i], -et);
             }
         }
 }
@@ -519,6 +560,7 @@ struct Prepared {
     const int* ex;
     const float* sx;
     const uint16_t* xp;
+    const float* x;   // the token rows themselves (rows holding an infinity)
 };
 
 // Checks the workspace and launches the prep kernel.
@@ -539,16 +581,16 @@ int prepare_x(const float* x, int rows, int K, void* workspace, size_t workspace
         case 4096: gemm_prep_x<16><<<grid, 256, 0, s>>>(x, ex, sx, xp, rows, K); break;
         default: gemm_prep_x<0><<<grid, 256, 0, s>>>(x, ex, sx, xp, rows, K); break;
     }
-    p = Prepared{ex, sx, xp};
+    p = Prepared{ex, sx, xp, x};
     return check_launch("matmul_rows prep");
 }
 
 void launch_gemm(int type, const GemmJobs& jobs, const Prepared& p, int rows, int K, hipStream_t s) {
     const dim3 grid(jobs.start[jobs.n], blocks_for(rows, kGT));
     if (type == kQ4_K)
-        gemm_q4k<<<grid, kGemmBlock, 0, s>>>(jobs, p.ex, p.sx, p.xp, rows, K);
+        gemm_q4k<<<grid, kGemmBlock, 0, s>>>(jobs, p.ex, p.sx, p.xp, p.x, rows, K);
     else
-        gemm_q6k<<<grid, kGemmBlock, 0, s>>>(jobs, p.ex, p.xp, rows, K);
+        gemm_q6k<<<grid, kGemmBlock, 0, s>>>(jobs, p.ex, p.xp, p.x, rows, K);
 }
 
 // One GEMV per token (the reference's own loop).

@@ -321,6 +321,16 @@ bool GgufLoader::load_tensors_to_gpu(int base_layer_count, hipStream_t stream) {
         if (base_layer_count < 0 || blk < 0 || blk < base_layer_count) sel.push_back(i);
     }
     std::sort(sel.begin(), sel.end(), [&](size_t a, size_t b) { return tensors_[a].offset < tensors_[b].offset; });
+    // The file may have changed since open(): every selected tensor must still
+    // lie inside this mapping, or the copies would read past it (SIGBUS). The
+    // reference's read fails instead ("Error reading binary tensor data",
+    // src/loader_gguf.cpp:355-360); this check runs before any device call.
+    const uint64_t avail = m.size() - payload_offset_;
+    for (size_t i : sel) {
+        const QuantTensor& t = tensors_[i];
+        if (t.offset > avail || t.size_bytes > avail - t.offset)
+            return fail("cannot re-read GGUF file " + filepath_ + ": tensor '" + t.name + "' lies past its end", false);
+    }
     std::vector<uint64_t> slot(sel.size());
     uint64_t arena_bytes = 0, data_bytes = 0;
     for (size_t k = 0; k < sel.size(); ++k) {

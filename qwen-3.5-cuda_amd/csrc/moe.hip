@@ -4,9 +4,9 @@
 // Reference semantics: silu_mul_kernel (src/cuda/moe.cu:61-67) and shared_kernel
 // (src/cuda/moe.cu:90-96, out += x * sigmoid(gate[0])). The reference runs one
 // launch per expert per token with 4-byte accesses; here a launch covers every
-// token and expert, each thread moves 16-byte vectors and keeps U vectors in
-// flight, and the bf16 forms do the math in fp32 with one round-to-nearest-even
-// at the store.
+// token and expert (and, in swiglu_routed_shared, the shared expert as well),
+// each thread moves 16-byte vectors and keeps U vectors in flight, and the bf16
+// forms do the math in fp32 with one round-to-nearest-even at the store.
 #include <algorithm>
 
 #include "capi_common.hpp"
@@ -53,13 +53,13 @@ __device__ __forceinline__ uint4 swiglu8(uint4 g, uint4 u, float scale) {
 // expert's rows x dim layout with one logit per row (dim % 8 == 0, so a chunk
 // never straddles two rows).
 template <bool SCALED>
-__global__ __launch_bounds__(kBlock) void swiglu_bf16_v8(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
-                                                         const float* __restrict__ logits, uint16_t* __restrict__ h,
-                                                         int64_t n8, int dim8) {
-    const int64_t first = static_cast<int64_t>(blockIdx.x) * kUnroll * kBlock + threadIdx.x;
+__device__ __forceinline__ void swiglu_block(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+                                             const float* __restrict__ logits, uint16_t* __restrict__ h, int64_t n8,
+                                             int dim8, unsigned block) {
+    const int64_t first = static_cast<int64_t>(block) * kUnroll * kBlock + threadIdx.x;
     uint4 gv[kUnroll], uv[kUnroll];
     float sc[kUnroll];
-    if (static_cast<int64_t>(blockIdx.x + 1) * kUnroll * kBlock <= n8) {  // block-uniform
+    if (static_cast<int64_t>(block + 1) * kUnroll * kBlock <= n8) {  // block-uniform
 #pragma unroll
         for (int k = 0; k < kUnroll; ++k) {
             gv[k] = ld16_nt(g + 8 * (first + k * kBlock));
@@ -77,6 +77,38 @@ __global__ __launch_bounds__(kBlock) void swiglu_bf16_v8(const uint16_t* __restr
                                                    SCALED ? sigmoid(logits[i / dim8]) : 1.0f));
         }
     }
+}
+
+template <bool SCALED>
+__global__ __launch_bounds__(kBlock) void swiglu_bf16_v8(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+                                                         const float* __restrict__ logits, uint16_t* __restrict__ h,
+                                                         int64_t n8, int dim8) {
+    swiglu_block<SCALED>(g, u, logits, h, n8, dim8, blockIdx.x);
+}
+
+// One part of the routed + shared launch: n8 chunks of 8 bf16 from `blocks`
+// workgroups.
+struct SwigluPart {
+    const uint16_t* g;
+    const uint16_t* u;
+    const float* logits;   // shared part only
+    uint16_t* h;
+    int64_t n8;
+    int dim8;
+    unsigned blocks;
+};
+
+// The MoE layer's two SwiGLUs in one grid: workgroups [0, routed.blocks) take
+// the routed experts' rows, the rest the shared expert's rows with their
+// sigmoid gate. Each workgroup runs exactly the code of the separate launches,
+// so the outputs equal them bit for bit; one launch drains once where two
+// would each pay their own ramp and tail.
+__global__ __launch_bounds__(kBlock) void swiglu_routed_shared_v8(const SwigluPart routed, const SwigluPart shared) {
+    if (blockIdx.x < routed.blocks)  // block-uniform
+        swiglu_block<false>(routed.g, routed.u, nullptr, routed.h, routed.n8, 1, blockIdx.x);
+    else
+        swiglu_block<true>(shared.g, shared.u, shared.logits, shared.h, shared.n8, shared.dim8,
+                           blockIdx.x - routed.blocks);
 }
 
 __device__ __forceinline__ float bf16_at(const uint16_t* p) { return __uint_as_float(static_cast<uint32_t>(*p) << 16); }
@@ -122,11 +154,16 @@ __global__ __launch_bounds__(kBlock) void shared_add_rows(float* __restrict__ ac
 
 unsigned stride_grid(int64_t items) { return static_cast<unsigned>(std::min<int64_t>(blocks_for(items, kBlock), 8192)); }
 
+// The 16-byte-vector kernels apply: whole chunks (and whole chunks per row when
+// a logit scales each row), 16-byte aligned pointers, chunk indices in int32.
+bool swiglu_vec_ok(const uint16_t* g, const uint16_t* u, const float* logits, const uint16_t* h, int64_t n, int dim) {
+    return n % 8 == 0 && n / 8 < (int64_t{1} << 31) && (!logits || dim % 8 == 0) && aligned16(g) && aligned16(u) &&
+           aligned16(h);
+}
+
 int swiglu_common(const uint16_t* g, const uint16_t* u, const float* logits, uint16_t* h, int64_t n, int dim,
                   hipStream_t s, const char* what) {
-    const bool vec = n % 8 == 0 && n / 8 < (int64_t{1} << 31) && (!logits || dim % 8 == 0) && aligned16(g) &&
-                     aligned16(u) && aligned16(h);
-    if (vec) {
+    if (swiglu_vec_ok(g, u, logits, h, n, dim)) {
         const int64_t n8 = n / 8;
         const unsigned grid = blocks_for(n8, static_cast<int64_t>(kUnroll) * kBlock);
         if (logits)
@@ -160,6 +197,33 @@ int qwen_shared_swiglu_sigmoid_rows_bf16(const uint16_t* gate, const uint16_t* u
     QK_REQUIRE(gate && up && logits && hidden, "shared_swiglu_sigmoid: null pointer");
     return swiglu_common(gate, up, logits, hidden, static_cast<int64_t>(rows) * dim, dim, as_stream(stream),
                          "shared_swiglu_sigmoid");
+}
+
+int qwen_swiglu_routed_shared_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* hidden, int64_t n,
+                                   const uint16_t* shared_gate, const uint16_t* shared_up, const float* logits,
+                                   uint16_t* shared_hidden, int rows, int dim, void* stream) {
+    QK_REQUIRE(n >= 0 && rows >= 0 && dim >= 0, "swiglu_routed_shared: negative size");
+    const int64_t ns = static_cast<int64_t>(rows) * dim;
+    QK_REQUIRE(n == 0 || (gate && up && hidden), "swiglu_routed_shared: null routed pointer");
+    QK_REQUIRE(ns == 0 || (shared_gate && shared_up && logits && shared_hidden),
+               "swiglu_routed_shared: null shared pointer");
+    const hipStream_t s = as_stream(stream);
+    if (n > 0 && ns > 0 && swiglu_vec_ok(gate, up, nullptr, hidden, n, 1) &&
+        swiglu_vec_ok(shared_gate, shared_up, logits, shared_hidden, ns, dim)) {
+        const int64_t per = static_cast<int64_t>(kUnroll) * kBlock;
+        const SwigluPart r{gate, up, nullptr, hidden, n / 8, 1, blocks_for(n / 8, per)};
+        const SwigluPart sh{shared_gate, shared_up, logits, shared_hidden, ns / 8, dim / 8, blocks_for(ns / 8, per)};
+        QK_REQUIRE(static_cast<uint64_t>(r.blocks) + sh.blocks <= 0x7fffffffu,
+                   "swiglu_routed_shared: %lld + %lld elements exceed one launch", static_cast<long long>(n),
+                   static_cast<long long>(ns));
+        swiglu_routed_shared_v8<<<r.blocks + sh.blocks, kBlock, 0, s>>>(r, sh);
+        return check_launch("swiglu_routed_shared");
+    }
+    // shapes or pointers outside the vector kernel: the two separate launches
+    if (n > 0)
+        if (const int rc = swiglu_common(gate, up, nullptr, hidden, n, 1, s, "swiglu_routed_shared")) return rc;
+    if (ns > 0) return swiglu_common(shared_gate, shared_up, logits, shared_hidden, ns, dim, s, "swiglu_routed_shared");
+    return ok();
 }
 
 int qwen_moe_silu_mul(const float* gate, const float* up, float* hidden, int n, void* stream) {

@@ -218,48 +218,14 @@ void shared_swiglu_sigmoid_rows_bf16(const uint16_t* gate, const uint16_t* up, c
     check(qwen_shared_swiglu_sigmoid_rows_bf16(gate, up, logits, hidden, rows, dim, st(stream)));
 }
 
+void swiglu_routed_shared_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* hidden, int64_t n,
+                               const uint16_t* shared_gate, const uint16_t* shared_up, const float* logits,
+                               uint16_t* shared_hidden, int rows, int dim, hipStream_t stream) {
+    check(qwen_swiglu_routed_shared_bf16(gate, up, hidden, n, shared_gate, shared_up, logits, shared_hidden, rows,
+                                         dim, st(stream)));
+}
+
 // ---- matmul_q4.hpp
-bool matmul_type_supported(GgmlType type) { return qwen_matmul_type_supported(static_cast<int>(type)) != 0; }
-
-void matmul_dispatch(const QuantTensor& w, const float* x, float* y, int M, int K, hipStream_t stream,
-                     uint64_t element_offset) {
-    const int status = qwen_matmul_dispatch(w.device_ptr, static_cast<int>(w.type), w.num_elements, x, y, M, K,
-                                            element_offset, st(stream));
-    // Reference messages, src/cuda/matmul_q4.cu:187-195.
-    if (status == QWEN_STATUS_INVALID_ARGUMENT && !w.device_ptr)
-        throw std::runtime_error("tensor '" + w.name + "' is not loaded");
-    if (status == QWEN_STATUS_UNSUPPORTED_TYPE)
-        throw std::runtime_error("unsupported GGML type for tensor '" + w.name + "'");
-    if (status == QWEN_STATUS_OUT_OF_RANGE) throw std::runtime_error("GEMV shape exceeds tensor '" + w.name + "'");
-    check(status);
-}
-
-size_t matmul_rows_workspace_bytes(int rows, int K) { return qwen_matmul_rows_workspace_bytes(rows, K); }
-
-void matmul_rows(const QuantTensor& w, const float* x, float* y, int rows, int M, int K, void* workspace,
-                 size_t workspace_bytes, hipStream_t stream, uint64_t element_offset) {
-    const int status = qwen_matmul_rows(w.device_ptr, static_cast<int>(w.type), w.num_elements, x, y, rows, M, K,
-                                        element_offset, workspace, workspace_bytes, st(stream));
-    if (status == QWEN_STATUS_INVALID_ARGUMENT && !w.device_ptr)
-        throw std::runtime_error("tensor '" + w.name + "' is not loaded");
-    if (status == QWEN_STATUS_UNSUPPORTED_TYPE)
-        throw std::runtime_error("unsupported GGML type for tensor '" + w.name + "'");
-    if (status == QWEN_STATUS_OUT_OF_RANGE) throw std::runtime_error("GEMV shape exceeds tensor '" + w.name + "'");
-    check(status);
-}
-
-void moe_expert_matmul(const QuantTensor& w, uint64_t expert_stride, int n_experts, const int32_t* idx, int n_sel,
-                       const float* x, int64_t x_stride, float* y, int M, int K, hipStream_t stream) {
-    const int status = qwen_moe_expert_matmul(w.device_ptr, static_cast<int>(w.type), w.num_elements, expert_stride,
-                                              n_experts, idx, n_sel, x, x_stride, y, M, K, st(stream));
-    if (status == QWEN_STATUS_INVALID_ARGUMENT && !w.device_ptr)
-        throw std::runtime_error("tensor '" + w.name + "' is not loaded");
-    if (status == QWEN_STATUS_UNSUPPORTED_TYPE)
-        throw std::runtime_error("unsupported GGML type for tensor '" + w.name + "'");
-    if (status == QWEN_STATUS_OUT_OF_RANGE) throw std::runtime_error("GEMV shape exceeds tensor '" + w.name + "'");
-    check(status);
-}
-
 namespace {
 // matmul_dispatch's messages for tensor w (src/cuda/matmul_q4.cu:187-195).
 void throw_tensor_status(int status, const QuantTensor& w) {
@@ -270,6 +236,34 @@ void throw_tensor_status(int status, const QuantTensor& w) {
     if (status == QWEN_STATUS_OUT_OF_RANGE) throw std::runtime_error("GEMV shape exceeds tensor '" + w.name + "'");
 }
 }  // namespace
+
+bool matmul_type_supported(GgmlType type) { return qwen_matmul_type_supported(static_cast<int>(type)) != 0; }
+
+void matmul_dispatch(const QuantTensor& w, const float* x, float* y, int M, int K, hipStream_t stream,
+                     uint64_t element_offset) {
+    const int status = qwen_matmul_dispatch(w.device_ptr, static_cast<int>(w.type), w.num_elements, x, y, M, K,
+                                            element_offset, st(stream));
+    throw_tensor_status(status, w);
+    check(status);
+}
+
+size_t matmul_rows_workspace_bytes(int rows, int K) { return qwen_matmul_rows_workspace_bytes(rows, K); }
+
+void matmul_rows(const QuantTensor& w, const float* x, float* y, int rows, int M, int K, void* workspace,
+                 size_t workspace_bytes, hipStream_t stream, uint64_t element_offset) {
+    const int status = qwen_matmul_rows(w.device_ptr, static_cast<int>(w.type), w.num_elements, x, y, rows, M, K,
+                                        element_offset, workspace, workspace_bytes, st(stream));
+    throw_tensor_status(status, w);
+    check(status);
+}
+
+void moe_expert_matmul(const QuantTensor& w, uint64_t expert_stride, int n_experts, const int32_t* idx, int n_sel,
+                       const float* x, int64_t x_stride, float* y, int M, int K, hipStream_t stream) {
+    const int status = qwen_moe_expert_matmul(w.device_ptr, static_cast<int>(w.type), w.num_elements, expert_stride,
+                                              n_experts, idx, n_sel, x, x_stride, y, M, K, st(stream));
+    throw_tensor_status(status, w);
+    check(status);
+}
 
 void moe_expert_gate_up(const QuantTensor& w_gate, const QuantTensor& w_up, uint64_t expert_stride, int n_experts,
                         const int32_t* idx, int n_sel, const float* x, float* gate_out, float* up_out, int M, int K,

@@ -56,6 +56,7 @@ SIGNATURES: dict[str, list] = {
     "qwen_moe_shared_add_rows": [_P, _P, _P, _I, _I, _P],
     "qwen_swiglu_bf16": [_P, _P, _P, _I64, _P],
     "qwen_shared_swiglu_sigmoid_rows_bf16": [_P, _P, _P, _P, _I, _I, _P],
+    "qwen_swiglu_routed_shared_bf16": [_P, _P, _P, _I64, _P, _P, _P, _P, _I, _I, _P],
     "qwen_type_supported": [_I],
     "qwen_dequantize_row": [_P, _I, _U64, _P, _I, _I, _P],
     "qwen_dequant_gather_rows": [_P, _I, _U64, _P, _I, _I, _P, _P],

@@ -668,6 +668,26 @@ def shared_swiglu_sigmoid_rows_bf16(g, u, logits, out=None, stream=None):
     return out
 
 
+def swiglu_routed_shared_bf16(g, u, sg, su, logits, out=None, shared_out=None, stream=None):
+    """Routed SwiGLU over g, u (any shape) and the shared expert's gated SwiGLU
+    over sg, su [rows x dim] with logits [rows], in one launch; returns
+    (out, shared_out)."""
+    _dev(g, u, sg, su, dtype=BF16)
+    _dev(logits, dtype=torch.float32)
+    _same(g.shape, u)
+    rows, dim = _rows(sg)
+    _same(sg.shape, su)
+    _same((rows,), logits)
+    out = torch.empty_like(g) if out is None else out
+    shared_out = torch.empty_like(sg) if shared_out is None else shared_out
+    _dev(out, shared_out, dtype=BF16)
+    _same(g.shape, out)
+    _same(sg.shape, shared_out)
+    check(load().qwen_swiglu_routed_shared_bf16(_p(g), _p(u), _p(out), g.numel(), _p(sg), _p(su), _p(logits),
+                                                _p(shared_out), rows, dim, _stream(stream)))
+    return out, shared_out
+
+
 # ------------------------------------------------------------------ dequant
 def dequant_gather_rows(table, ggml_type, num_elements: int, ids, cols: int, out=None, stream=None):
     """table: uint8 device tensor of GGML blocks; ids int32 [n]; -> float32 [n, cols]."""

@@ -56,6 +56,30 @@ def assert_f32_close(got, ref, group: int | None = None, rtol: float = RTOL_F32,
         f"got {got.flat[worst]!r} ref {ref.flat[worst]!r}")
 
 
+def floor_audit(got, ref, group: int, what: str = "") -> dict:
+    """How much of an fp32 comparison the rms floor carries: the largest plain
+    relative error |got - ref| / |ref|, how many elements exceed RTOL_F32 by that
+    measure (they pass only because of the floor), the largest error of those
+    measured against the floor, and the largest |ref| / rms among them (so a
+    reader can see they are the near-zero outputs of cancelling sums). Printed
+    with a fixed prefix so a test log can be searched for it."""
+    g = np.asarray(got, dtype=np.float64).reshape(-1, group)
+    r = np.asarray(ref, dtype=np.float64).reshape(-1, group)
+    ok = ~np.isnan(r)
+    err = np.where(ok, np.abs(g - r), 0.0)
+    plain = np.where(np.abs(r) > 0, err / np.where(np.abs(r) > 0, np.abs(r), 1.0), np.where(err > 0, np.inf, 0.0))
+    rms = np.sqrt(np.mean(np.where(ok, r * r, 0.0), axis=1, keepdims=True))
+    rms = np.where(rms == 0, 1.0, rms)
+    floor_only = ok & (plain > RTOL_F32)
+    rep = {"what": what, "elements": int(r.size), "max_plain_rel_err": float(plain[ok].max()) if ok.any() else 0.0,
+           "floor_only": int(floor_only.sum()),
+           "floor_only_max_err_over_rms": float((err / rms)[floor_only].max()) if floor_only.any() else 0.0,
+           "floor_only_max_abs_ref_over_rms": float((np.abs(r) / rms)[floor_only].max()) if floor_only.any() else 0.0,
+           "max_err_over_rms": float((err / rms).max())}
+    print(f"FLOOR-AUDIT {rep}", flush=True)
+    return rep
+
+
 def bf16_ordered(bits: np.ndarray) -> np.ndarray:
     b = np.asarray(bits, dtype=np.uint16).astype(np.int32)
     return np.where(b & 0x8000, -(b & 0x7FFF), b)

@@ -157,3 +157,27 @@ def test_matmul_rows_host_validation(lib):
     assert lib.qwen_matmul_rows_workspace_bytes(64, 2048) == 256 + 64 * 64 * 4 + 64 * 2048 * 4
     assert lib.qwen_matmul_rows_multi(NULL, 65, FAKE, 32, 256, NULL, 0, ST) == INV
     assert lib.qwen_matmul_rows_multi(NULL, 0, NULL, 32, 256, NULL, 0, ST) == OK
+
+
+def test_gdn_value_dim_limit_on_every_recurrent_path(lib):
+    """value_dim above 256 is rejected with the reference's message
+    (src/cuda/gdn.cu:167-169) by the token loop and by the chunked entry point
+    whatever the pointers' alignment (which would otherwise pick the path)."""
+    INV = _lib.STATUS_INVALID_ARGUMENT
+    aligned, odd = ctypes.c_void_p(1 << 20), ctypes.c_void_p((1 << 20) + 4)
+    for p in (aligned, odd):
+        st = lib.qwen_gdn_recurrent_chunked(p, p, p, p, p, p, p, 64, 16, 32, 128, 512, 8192, 4096, p, 1 << 30, ST)
+        assert st == INV and msg(lib) == "GDN value dimension exceeds kernel limit"
+    assert lib.qwen_gdn_recurrent_rows(aligned, aligned, aligned, aligned, aligned, aligned, aligned, 4, 16, 32, 128,
+                                       512, 8192, 4096, ST) == INV
+    assert msg(lib) == "GDN value dimension exceeds kernel limit"
+
+
+def test_swiglu_routed_shared_validation(lib):
+    INV, OK = _lib.STATUS_INVALID_ARGUMENT, _lib.STATUS_OK
+    f = lib.qwen_swiglu_routed_shared_bf16
+    assert f(FAKE, FAKE, FAKE, -8, FAKE, FAKE, FAKE, FAKE, 1, 8, ST) == INV
+    assert f(FAKE, FAKE, FAKE, 8, FAKE, FAKE, FAKE, FAKE, -1, 8, ST) == INV
+    assert f(NULL, FAKE, FAKE, 8, FAKE, FAKE, FAKE, FAKE, 1, 8, ST) == INV and "routed" in msg(lib)
+    assert f(FAKE, FAKE, FAKE, 8, FAKE, FAKE, NULL, FAKE, 1, 8, ST) == INV and "shared" in msg(lib)
+    assert f(NULL, NULL, NULL, 0, NULL, NULL, NULL, NULL, 0, 512, ST) == OK  # both parts empty

@@ -236,6 +236,26 @@ def test_alignment_text_rules(tmp_path):
             assert f.info()["payload_offset"] % align == 0
 
 
+def test_load_after_truncation_is_an_io_error(tmp_path):
+    """A file cut short between open and load: the upload re-maps it and finds a
+    tensor past the new end before any device call, so this runs on the CPU.
+    The reference's read reports the failure instead of faulting
+    (src/loader_gguf.cpp:355-360)."""
+    rng = np.random.default_rng(6)
+    ts = _tensors(rng, layers=1)
+    data = gw.build(META, ts)
+    p = _write(tmp_path, "cut.gguf", data)
+    with GgufFile(p) as f:
+        last = max(f.tensors(), key=lambda g: g.offset)
+        with open(p, "r+b") as fh:
+            fh.truncate(len(data) - 7)
+        with pytest.raises(QwenError) as e:
+            f.load()
+        assert e.value.status == _lib.STATUS_IO_ERROR, e.value
+        assert "cannot re-read GGUF file" in str(e.value) and last.name in str(e.value)
+        assert f.info()["device_bytes"] == 0 and all(g.device_ptr is None for g in f.tensors())
+
+
 # ------------------------------------------------------------------ device upload
 @pytest.mark.gpu
 def test_load_bytes_and_layer_filter(tmp_path):

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import assert_bf16_close, assert_bits_equal, assert_f32_close
+from conftest import assert_bf16_close, assert_bits_equal, assert_f32_close, floor_audit
 from qwen35_hip import ops, synth
 
 pytestmark = pytest.mark.gpu
@@ -117,8 +117,10 @@ def test_residual_rmsnorm_shapes(oracle, rows, n):
 def test_encoder_forward(oracle):
     table = rng(9).standard_normal((100, 2048)).astype(F32)
     t = dev(table)
-    for tok in (0, 57, 99):
-        assert_bits_equal(host(ops.encoder_forward(tok, t)), table[tok])
+    ids = np.array([0, 57, 99, 57], np.int32)
+    want = oracle.encoder_rows(ids, table)
+    for j, tok in enumerate(ids):
+        assert_bits_equal(host(ops.encoder_forward(int(tok), t)), want[j])
 
 
 # ------------------------------------------------------------------ attention
@@ -129,8 +131,16 @@ def test_qk_norm_rope_config_c2(oracle):
                                theta=c["theta"], eps=c["eps"])
     rq, rk = oracle.qk_norm_rope_rows(c["q"], c["k"], c["qw"], c["kw"], pos=c["pos"], rope_dim=c["rope_dim"],
                                       theta=c["theta"], eps=c["eps"], threads=THREADS)
-    assert_f32_close(host(q), rq, group=256, what="C2 q")
-    assert_f32_close(host(k), rk, group=256, what="C2 k")
+    gq, gk = host(q), host(k)
+    assert_f32_close(gq, rq, group=256, what="C2 q")
+    assert_f32_close(gk, rk, group=256, what="C2 k")
+    # The rms floor must only carry near-zero outputs of the rotation: every
+    # element that passes only through it sits far below its head's rms, and its
+    # error is within the bar measured against that rms.
+    for name, g, r in (("C2 q", gq, rq), ("C2 k", gk, rk)):
+        a = floor_audit(g, r, 256, name)
+        assert a["floor_only"] <= 1e-3 * a["elements"], a
+        assert a["floor_only_max_abs_ref_over_rms"] < 0.05, a
 
 
 @pytest.mark.parametrize("hd,rd,qh,kh", [(128, 64, 4, 2), (128, 128, 3, 1), (64, 32, 5, 3), (256, 256, 2, 1),
@@ -181,8 +191,12 @@ def test_gdn_frontend_config_c4a(oracle, random_history):
                                  key_dim=c["key_dim"], eps=c["eps"])
     ry, rh = oracle.gdn_frontend_rows(c["x"], c["w"], c["hist"], c["k_heads"], c["key_dim"], c["eps"],
                                       threads=THREADS)
-    assert_f32_close(host(y), ry, group=128, what="C4a y")
+    gy = host(y)
+    assert_f32_close(gy, ry, group=128, what="C4a y")
     assert_bits_equal(host(h), rh, "C4a history")
+    a = floor_audit(gy, ry, 128, f"C4a y (random history {random_history})")
+    assert a["floor_only"] <= 1e-3 * a["elements"], a
+    assert a["floor_only_max_abs_ref_over_rms"] < 0.05, a
 
 
 @pytest.mark.parametrize("rows,channels,kernel,heads,dim", [
@@ -256,6 +270,43 @@ def test_shared_swiglu_config_c3c(oracle):
     c = synth.c3_shared()
     got = host(ops.shared_swiglu_sigmoid_rows_bf16(dev(c["g"]), dev(c["u"]), dev(c["logits"])))
     assert_bf16_close(got, oracle.shared_swiglu_sigmoid_bf16(c["g"], c["u"], c["logits"]), what="C3c")
+
+
+def test_swiglu_routed_shared_config_c3(oracle):
+    """C3's routed [4096 x 8 x 512] and shared [4096 x 512] SwiGLU in one launch:
+    each output within 1 bf16 ulp of the oracle and bit-equal to the separate
+    entry points (the same per-chunk code runs in both)."""
+    c, cs = synth.c3_swiglu(), synth.c3_shared()
+    g, u, sg, su, lg = dev(c["g"]), dev(c["u"]), dev(cs["g"]), dev(cs["u"]), dev(cs["logits"])
+    h, hs = ops.swiglu_routed_shared_bf16(g, u, sg, su, lg)
+    got, got_s = host(h), host(hs)
+    assert_bf16_close(got, oracle.swiglu_bf16(c["g"], c["u"], threads=THREADS), what="C3 routed")
+    assert_bf16_close(got_s, oracle.shared_swiglu_sigmoid_bf16(cs["g"], cs["u"], cs["logits"]), what="C3 shared")
+    assert np.array_equal(got, host(ops.swiglu_bf16(g, u)))
+    assert np.array_equal(got_s, host(ops.shared_swiglu_sigmoid_rows_bf16(sg, su, lg)))
+
+
+@pytest.mark.parametrize("n,rows,dim,offset", [
+    (8 * 1000, 3, 520, 0),      # ragged last workgroup in both parts
+    (4096, 1, 8, 0),            # one shared row of one chunk
+    (37 * 3, 3, 37, 0),         # not whole chunks: the two separate launches
+    (8 * 64, 5, 64, 1),         # misaligned routed pointers: the two separate launches
+    (0, 7, 512, 0),             # routed part empty
+    (8 * 512, 0, 512, 0),       # shared part empty
+])
+def test_swiglu_routed_shared_shapes(oracle, n, rows, dim, offset):
+    r = rng(n + rows * 7 + dim)
+    g = synth.to_bf16_bits(2 * r.standard_normal(n + offset).astype(F32))
+    u = synth.to_bf16_bits(2 * r.standard_normal(n + offset).astype(F32))
+    sg = synth.to_bf16_bits(2 * r.standard_normal((rows, dim)).astype(F32))
+    su = synth.to_bf16_bits(2 * r.standard_normal((rows, dim)).astype(F32))
+    lg = r.standard_normal(rows).astype(F32)
+    dg, du = dev(g)[offset:], dev(u)[offset:]
+    h, hs = ops.swiglu_routed_shared_bf16(dg, du, dev(sg), dev(su), dev(lg))
+    if n:
+        assert_bf16_close(host(h), oracle.swiglu_bf16(g[offset:], u[offset:]), what="routed")
+    if rows:
+        assert_bf16_close(host(hs), oracle.shared_swiglu_sigmoid_bf16(sg, su, lg), what="shared")
 
 
 def test_swiglu_exhaustive_and_odd(oracle):
@@ -1291,6 +1342,8 @@ GEMM_CASES = [   # kind, tokens, M, K, first row (element offset = row * K)
     ("Q4_K", 200, 1000, 4096, 3), ("Q6_K", 64, 512, 2048, 0), ("Q6_K", 77, 333, 2048, 5),
     ("Q6_K", 130, 256, 512, 0), ("Q6_K", 16, 17, 256, 0),
     ("Q4_K", 7, 512, 2048, 0), ("Q6_K", 15, 100, 768, 0), ("Q8_0", 20, 96, 512, 0), ("Q4_K", 40, 64, 320, 0),
+    # the prep kernel's register form at K = 1024 and its two-pass form at K above 256 outside 512..4096
+    ("Q4_K", 32, 256, 1024, 0), ("Q6_K", 32, 256, 1024, 0), ("Q6_K", 48, 100, 1536, 0), ("Q4_K", 20, 300, 3072, 1),
 ]
 
 
@@ -1382,16 +1435,28 @@ def test_matmul_rows_checks_shapes():
                                                                                    device="cuda"))
 
 
-def test_matmul_rows_nonfinite_and_zero_rows(oracle):
-    """A token row holding an infinity gives a non-finite output row (as the
-    reference's products do); an all-zero row gives zeros; neighbours are unaffected."""
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
+def test_matmul_rows_nonfinite_and_zero_rows(oracle, kind):
+    """Token rows holding infinities give the reference's pattern of +-inf and
+    NaN (its per-element fp32 products: w * inf = +-inf, 0 * inf = NaN,
+    +inf + -inf = NaN), a NaN row gives NaN, an all-zero row gives +0, and
+    neighbouring rows are unaffected."""
     K, M, T = 2048, 256, 32
-    w = synth.q4k_table(M, K)
+    t = ops.GGML_TYPES[kind]
+    w = synth.q4k_table(M, K) if kind == "Q4_K" else synth.q6k_table(M, K)
     x = rng(11).standard_normal((T, K)).astype(F32)
-    x[3, 100] = np.inf
+    x[3, 100] = np.inf                      # one infinity
+    x[7, 10], x[7, 2000] = np.inf, -np.inf  # both signs in one row
+    x[9, 5] = np.nan
+    x[9, 6] = np.inf                        # NaN beside an infinity
     x[5] = 0.0
-    got = host(ops.matmul_rows(dev(w), "Q4_K", M * K, dev(x), M, K))
-    assert not np.isfinite(got[3]).any()
-    assert np.all(got[5] == 0.0)
-    for i in (0, 4, 6, T - 1):
-        assert_f32_close(got[i], oracle.gemv(w, 12, x[i], M, K), group=M, what=f"token {i}")
+    got = host(ops.matmul_rows(dev(w), kind, M * K, dev(x), M, K))
+    for i in (3, 7, 9):
+        ref = oracle.gemv(w, t, x[i], M, K)
+        assert np.array_equal(np.isnan(got[i]), np.isnan(ref)), f"token {i}: NaN pattern"
+        inf = np.isinf(ref)
+        assert np.array_equal(got[i][inf], ref[inf]) and np.array_equal(np.isinf(got[i]), inf), f"token {i}: inf"
+    assert np.isinf(oracle.gemv(w, t, x[3], M, K)).any()
+    assert np.array_equal(got[5].view(np.uint32), np.zeros(M, np.uint32))
+    for i in (0, 4, 6, 8, 10, T - 1):
+        assert_f32_close(got[i], oracle.gemv(w, t, x[i], M, K), group=M, what=f"token {i}")

@@ -246,6 +246,65 @@ def test_residual_rmsnorm_f32_and_bf16(oracle):
     assert_bf16_close(n16, bf16_of(ref.astype(F32)))
 
 
+def special_f32() -> np.ndarray:
+    """Signed zeros, the smallest and largest subnormals, the smallest normal,
+    values whose sum overflows or cancels exactly, infinities and NaNs."""
+    tiny = np.finfo(F32).smallest_subnormal
+    big = np.finfo(F32).max
+    base = np.array([0.0, -0.0, tiny, -tiny, 2 * tiny, np.finfo(F32).smallest_normal - tiny,
+                     np.finfo(F32).smallest_normal, -np.finfo(F32).smallest_normal, 1.0, -1.0, 1.5, big, -big,
+                     np.inf, -np.inf, np.nan, 3.0e38, 1e-30, -1e-30], dtype=F32)
+    return base
+
+
+def test_residual_add_matches_numpy(oracle):
+    """out = x1 + x2 (src/cuda/ops.cu:115-125) against numpy's float32 add: every
+    pair of special values (signed zeros, subnormals, overflow to inf,
+    inf - inf = NaN, NaN inputs) and random values across the exponent range."""
+    s = special_f32()
+    a = np.repeat(s, s.size)
+    b = np.tile(s, s.size)
+    got = oracle.residual_add(a, b)
+    with np.errstate(all="ignore"):
+        ref = (a + b).astype(F32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert_bits_equal(got[~nan], ref[~nan], "special pairs")
+    # signed zero rules and overflow, spelled out
+    # (a list: as dict keys 0.0 and -0.0 would collide)
+    pairs = [(0.0, -0.0, 0x00000000), (-0.0, -0.0, 0x80000000), (1.0, -1.0, 0x00000000)]
+    for x, y, bits in pairs:
+        assert oracle.residual_add(np.array([x], F32), np.array([y], F32)).view(np.uint32)[0] == bits
+    big = np.finfo(F32).max
+    assert oracle.residual_add(np.array([big], F32), np.array([big], F32))[0] == np.inf
+    tiny = np.finfo(F32).smallest_subnormal
+    assert oracle.residual_add(np.array([tiny], F32), np.array([tiny], F32))[0] == 2 * tiny  # no flush to zero
+    rng = np.random.default_rng(71)
+    bits = rng.integers(0, 1 << 32, size=(2, 100_003), dtype=np.uint64).astype(np.uint32)
+    x, y = bits[0].view(F32), bits[1].view(F32)
+    got = oracle.residual_add(x, y)
+    with np.errstate(all="ignore"):
+        ref = x + y
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert_bits_equal(got[~nan], ref[~nan], "random bit patterns")
+
+
+def test_encoder_rows_matches_table_indexing(oracle):
+    """out[t] = table[ids[t]] (src/cuda/ops.cu:128-138) against numpy fancy
+    indexing, bit for bit, with repeated ids, the first and last rows and rows
+    holding NaN payloads and signed zeros (a copy, not arithmetic)."""
+    rng = np.random.default_rng(72)
+    table = rng.standard_normal((97, 40)).astype(F32)
+    table[5, :3] = np.array([-0.0, np.inf, -np.inf], dtype=F32)
+    table[7].view(np.uint32)[:] = 0x7FC01234  # NaN with a payload
+    ids = np.array([0, 96, 5, 7, 5, 31, 0], dtype=np.int32)
+    got = oracle.encoder_rows(ids, table)
+    assert got.shape == (ids.size, 40)
+    assert np.array_equal(got.view(np.uint32), table[ids].view(np.uint32))
+    assert oracle.encoder_rows(np.zeros(0, np.int32), table).shape == (0, 40)
+
+
 # ------------------------------------------------------------------ RoPE
 def test_rope_reference_fixture(oracle):
     fx = GOLDEN["rope"]
@@ -639,3 +698,43 @@ def test_swiglu_and_shared(oracle):
     x = rng.standard_normal((64, 512)).astype(F32)
     got = oracle.shared_add_rows(acc, x, lg)
     assert_f32_close(got, acc + x * sig64(lg)[:, None], group=512, rtol=1e-6)
+
+
+# ------------------------------------------------------------------ timed CPU baseline build
+def test_fp32_math_build_computes_the_same_functions(oracle):
+    """liboracle_fp32.so (float math and float sums: what bench.py times as the
+    reference CPU path) computes the step's functions within the parity bars of
+    the checker build, so the timed baseline does the same work."""
+    from qwen35_hip import synth
+
+    c1, c2, c3, c4 = synth.c1_rmsnorm(rows=8), synth.c2_qk_rope(rows=16), synth.c3_residual(rows=8), synth.c4_norm_gate(rows=8)
+    fe = synth.c4_frontend(rows=40, channels=1024, random_history=True)
+    fe["k_heads"], fe["key_dim"] = 2, 128
+    sw, sh = synth.c3_swiglu(rows=8), synth.c3_shared(rows=8)
+
+    def run():
+        return {
+            "rms": oracle.rmsnorm_rows(c1["x"], c1["w"]),
+            "rope": oracle.qk_norm_rope_rows(c2["q"], c2["k"], c2["qw"], c2["kw"], pos=c2["pos"], rope_dim=64,
+                                             theta=1e7),
+            "res": oracle.residual_rmsnorm_rows(c3["x"], c3["branch"], c3["w"]),
+            "fe": oracle.gdn_frontend_rows(fe["x"], fe["w"], fe["hist"], 2, 128),
+            "ng": oracle.norm_gate_rows(c4["x"], c4["z"], c4["w"]),
+            "sw": oracle.swiglu_bf16(sw["g"], sw["u"]),
+            "sh": oracle.shared_swiglu_sigmoid_bf16(sh["g"], sh["u"], sh["logits"]),
+        }
+
+    exact = run()
+    with oracle.fp32_math():
+        f32 = run()
+    assert_f32_close(f32["rms"], exact["rms"], what="rmsnorm")
+    for a, b in zip(f32["rope"], exact["rope"]):
+        assert_f32_close(a, b, group=256, what="qk_norm_rope")
+    assert np.array_equal(f32["res"][0], exact["res"][0])
+    assert_bf16_close(f32["res"][1], exact["res"][1], what="residual_rmsnorm")
+    assert_f32_close(f32["fe"][0], exact["fe"][0], group=128, what="gdn_frontend")
+    assert_bits_equal(f32["fe"][1], exact["fe"][1], "history")
+    assert_f32_close(f32["ng"], exact["ng"], what="norm_gate")
+    assert_bf16_close(f32["sw"], exact["sw"], what="swiglu")
+    assert_bf16_close(f32["sh"], exact["sh"], what="shared swiglu")
+    assert oracle.lib() is not None and oracle._variant == "exact"
