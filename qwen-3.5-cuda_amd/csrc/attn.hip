@@ -6,11 +6,13 @@
 // theta = pos / powf(base, 2i/rd)), called as src/layer_attn.cpp:91-96.
 //
 // Mapping: a head of head_dim = 4*LPH floats is held by LPH lanes as one float4
-// each (head_dim 256 = one wave per head). The sum of squares is a DPP group
-// reduction; the RoPE partner of dims (i..i+3) sits half/4 lanes away and is
-// fetched with ds_bpermute. Each lane group evaluates the 1..2 sincos values of
-// its own head's (position, pair) once and hands them to the lanes that need
-// them, instead of every rotary lane recomputing them.
+// each. The sum of squares is a DPP group reduction; the RoPE partner of dims
+// (i..i+3) sits half/4 lanes away. Each lane group evaluates the sincos values
+// of its own head's (position, pair) once and hands them to the lanes that need
+// them, instead of every rotary lane recomputing them. The production shape
+// (head_dim 256, rope_dim 64) has its own form: three heads of one token per
+// wave, one set of angles for the three, cross-lane moves by DPP and permlane
+// swaps only (qk_norm_rope_grouped).
 //
 // The inverse-frequency denominators powf(theta, 2i/rd) are computed on the host
 // (double pow, rounded once) and passed as kernel arguments: a one-ulp change in
@@ -45,20 +47,9 @@ RopeDen make_den(int lo, int count, int rope_dim, float theta) {
 }
 
 // ------------------------------------------------------------ vector kernel
-// R64: the production shape (head_dim 256, rope_dim 64), where every value the
-// rotation needs moves through VALU cross-lane ops instead of ds_bpermute:
-// lane 16r + m evaluates the angle of pair 4*(m % 8) + r, so rotary lane m
-// (m < 16) finds its four pairs at lanes m, m+16, m+32, m+48 (gathered with
-// v_permlane16_swap / v_permlane32_swap), and its partner 8 lanes away in the
-// same 16-lane row (DPP row_ror:8).
-__device__ __forceinline__ float pl16_hi(float v) {  // lane m (even row) <- lane m + 16
-    return __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)[1]);
-}
-__device__ __forceinline__ float pl32_hi(float v) {  // lane m (< 32) <- lane m + 32
-    return __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false)[1]);
-}
-
-template <int LPH, bool NORM, bool ROPE, bool R64>
+// Any head_dim of 64, 128 or 256 floats (LPH = 16, 32, 64 lanes per head): the
+// RoPE partner and the angles move through ds_bpermute.
+template <int LPH, bool NORM, bool ROPE>
 __global__ __launch_bounds__(kBlock) void qk_norm_rope_v4(float* __restrict__ q, float* __restrict__ k,
                                                           const float* __restrict__ qw, const float* __restrict__ kw,
                                                           const int32_t* __restrict__ pos, int pos0, int rows,
@@ -93,27 +84,17 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_v4(float* __restrict__ q,
     float fp = 0.f, dn0 = 1.f, dn1 = 1.f;
     if constexpr (ROPE) {
         fp = static_cast<float>(pos ? pos[t] : pos0 + t);
-        if constexpr (R64) {
-            // lane 16r + m evaluates pair 4*(m % 8) + r
-            dn0 = den.den[4 * (lane & 7) + (lane >> 4)];
-        } else {
-            dn0 = den.den[min(lg, kMaxDen - 1)];
-            dn1 = den.den[min(lg + LPH, kMaxDen - 1)];
-        }
+        dn0 = den.den[min(lg, kMaxDen - 1)];
+        dn1 = den.den[min(lg + LPH, kMaxDen - 1)];
     }
     float4 v = ld4_nt(p + 4 * lg);
     const float4 wv = NORM ? ld4(wt + 4 * lg) : make_float4(1.f, 1.f, 1.f, 1.f);
 
-    // Rotation angles of this group's head (pairs lg and lg + LPH, or the R64
-    // assignment above).
+    // Rotation angles of this group's head (pairs lg and lg + LPH).
     float c0 = 1.f, s0 = 0.f, c1 = 1.f, s1 = 0.f;
     if constexpr (ROPE) {
-        if constexpr (R64) {
-            sincosf(fp / dn0, &s0, &c0);
-        } else {
-            if (lg < half) sincosf(fp / dn0, &s0, &c0);
-            if (lg + LPH < half) sincosf(fp / dn1, &s1, &c1);
-        }
+        if (lg < half) sincosf(fp / dn0, &s0, &c0);
+        if (lg + LPH < half) sincosf(fp / dn1, &s1, &c1);
     }
 
     if constexpr (NORM) {
@@ -125,27 +106,7 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_v4(float* __restrict__ q,
         v.w = v.w * (r * wv.w);
     }
 
-    if constexpr (ROPE && R64) {
-        const bool first = lane < 8, second = lane >= 8 && lane < 16;
-        const float pv[4] = {dpp_move<0x128>(v.x), dpp_move<0x128>(v.y), dpp_move<0x128>(v.z),
-                             dpp_move<0x128>(v.w)};
-        const float c01 = pl16_hi(c0), s01 = pl16_hi(s0);
-        const float cs[4] = {c0, c01, pl32_hi(c0), pl32_hi(c01)};
-        const float sn[4] = {s0, s01, pl32_hi(s0), pl32_hi(s01)};
-        const float a[4] = {v.x, v.y, v.z, v.w};
-        float o[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (first)
-                o[j] = a[j] * cs[j] - pv[j] * sn[j];  // x[i]      = a c - b s
-            else if (second)
-                o[j] = a[j] * cs[j] + pv[j] * sn[j];  // x[i+half] = b c + a s
-            else
-                o[j] = a[j];
-        }
-        v = make_float4(o[0], o[1], o[2], o[3]);
-    }
-    if constexpr (ROPE && !R64) {
+    if constexpr (ROPE) {
         const int d0 = 4 * lg;
         const bool first = d0 < half;                 // dims i..i+3, partner i+half
         const bool second = !first && d0 < rope_dim;  // dims i+half.., partner i
@@ -194,6 +155,100 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_v4(float* __restrict__ q,
     if (active) st4_nt(p + 4 * lg, v);
 }
 
+// ------------------------------------------------------------ grouped heads
+// The production shape (head_dim 256, rope_dim 64) with HPW heads of one token
+// per wave: every lane holds one float4 of each head, all HPW row loads are in
+// flight together, and the token's rotation angles are evaluated once for the
+// HPW heads. Every value the rotation needs moves through VALU cross-lane ops
+// instead of ds_bpermute: lane 16r + m evaluates the angle of pair
+// 4*(m % 8) + r, so rotary lane m (m < 16) finds its four pairs at lanes m,
+// m+16, m+32, m+48 (gathered with v_permlane16_swap / v_permlane32_swap), and
+// its partner 8 lanes away in the same 16-lane row (DPP row_ror:8). Head h of a
+// token is Q head h for h < q_heads, else K head h - q_heads; a group may hold
+// both. At C2 (16 + 2 heads, 18.9 MB in place) three heads per wave in
+// 192-thread workgroups measured 4.5 us against 5.5 us for one head per wave
+// (launch shapes swept on the MI355X): more bytes in flight per wave and 3
+// waves per SIMD, all resident at once.
+constexpr int kGroupHeads = 3;
+constexpr int kGroupBlock = 192;
+
+__device__ __forceinline__ float pl16_hi(float v) {  // lane m (even row) <- lane m + 16
+    return __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)[1]);
+}
+__device__ __forceinline__ float pl32_hi(float v) {  // lane m (< 32) <- lane m + 32
+    return __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false)[1]);
+}
+
+// POS: positions from the array `pos`, else pos0 + t.
+template <int HPW, bool NORM, bool POS>
+__global__ __launch_bounds__(kGroupBlock) void qk_norm_rope_grouped(float* __restrict__ q, float* __restrict__ k,
+                                                                   const float* __restrict__ qw,
+                                                                   const float* __restrict__ kw,
+                                                                   const int32_t* __restrict__ pos, int pos0, int rows,
+                                                                   int q_heads, int k_heads, RopeDen den, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int hpr = q_heads + k_heads;
+    const int gpt = (hpr + HPW - 1) / HPW;  // head groups per token
+    const int wave = static_cast<int>(blockIdx.x) * (kGroupBlock / kWave) + wave_in_block();
+    if (wave >= rows * gpt) return;  // wave-uniform (the host checks rows * gpt < 2^31)
+    const int t = wave / gpt;
+    const int h0 = (wave - t * gpt) * HPW;
+    // Issue order: the position (a scalar load) and the denominator, then the
+    // rows and weights, then the angle math, which waits only for the first two.
+    // No load sits behind a branch, so the scalar argument loads are not
+    // serialised behind waits.
+    const float fp = static_cast<float>(POS ? pos[t] : pos0 + t);
+    const float dn0 = den.den[4 * (lane & 7) + (lane >> 4)];  // lane 16r + m: pair 4(m % 8) + r
+    float4 v[HPW];
+    float* ptr[HPW];
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) {
+        const int h = min(h0 + j, hpr - 1);  // clamped: loads never branch
+        ptr[j] = (h < q_heads) ? q + (static_cast<size_t>(t) * q_heads + h) * 256
+                               : k + (static_cast<size_t>(t) * k_heads + (h - q_heads)) * 256;
+        v[j] = ld4_nt(ptr[j] + 4 * lane);
+    }
+    float4 wq = make_float4(1.f, 1.f, 1.f, 1.f), wk = wq;
+    if constexpr (NORM) {
+        // a tensor with no heads may come without weights: read the other's
+        wq = ld4((q_heads > 0 ? qw : kw) + 4 * lane);
+        wk = ld4((k_heads > 0 ? kw : qw) + 4 * lane);
+    }
+    float s0, c0;
+    sincosf(fp / dn0, &s0, &c0);
+    const float c01 = pl16_hi(c0), s01 = pl16_hi(s0);
+    const float cs[4] = {c0, c01, pl32_hi(c0), pl32_hi(c01)};
+    const float sn[4] = {s0, s01, pl32_hi(s0), pl32_hi(s01)};
+    const bool first = lane < 8, second = lane >= 8 && lane < 16;
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) {
+        const int h = h0 + j;
+        float4 x = v[j];
+        if constexpr (NORM) {
+            const float4 wv = (min(h, hpr - 1) < q_heads) ? wq : wk;
+            const float ss = group_sum<kWave>(sumsq4(x));
+            const float r = rsqrtf(ss / 256.0f + eps);
+            x.x = x.x * (r * wv.x);
+            x.y = x.y * (r * wv.y);
+            x.z = x.z * (r * wv.z);
+            x.w = x.w * (r * wv.w);
+        }
+        const float pv[4] = {dpp_move<0x128>(x.x), dpp_move<0x128>(x.y), dpp_move<0x128>(x.z), dpp_move<0x128>(x.w)};
+        const float a[4] = {x.x, x.y, x.z, x.w};
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (first)
+                o[i] = a[i] * cs[i] - pv[i] * sn[i];  // x[i]      = a c - b s
+            else if (second)
+                o[i] = a[i] * cs[i] + pv[i] * sn[i];  // x[i+half] = b c + a s
+            else
+                o[i] = a[i];
+        }
+        if (h < hpr) st4_nt(ptr[j] + 4 * lane, make_float4(o[0], o[1], o[2], o[3]));  // wave-uniform
+    }
+}
+
 // ------------------------------------------------------------ generic kernels
 // Any head_dim / alignment: one block per head, in place.
 __global__ __launch_bounds__(kBlock) void head_norm_any(float* __restrict__ x, const float* __restrict__ w, int dim,
@@ -236,17 +291,23 @@ void launch_vec(int lph, float* q, float* k, const float* qw, const float* kw, c
     const int hpw = kWave / lph;
     const int64_t waves = (heads + hpw - 1) / hpw;
     const dim3 grid(blocks_for(waves, kBlock / kWave)), block(kBlock);
-    if (lph == 64 && ROPE && rope_dim == 64)
-        qk_norm_rope_v4<64, NORM, ROPE, true><<<grid, block, 0, s>>>(q, k, qw, kw, pos, pos0, rows, qh, kh, rope_dim, den,
-                                                                    eps);
-    else if (lph == 64)
-        qk_norm_rope_v4<64, NORM, ROPE, false><<<grid, block, 0, s>>>(q, k, qw, kw, pos, pos0, rows, qh, kh, rope_dim,
+    if (lph == 64 && ROPE && rope_dim == 64) {
+        const int64_t gwaves = static_cast<int64_t>(rows) * ((qh + kh + kGroupHeads - 1) / kGroupHeads);
+        const unsigned ggrid = blocks_for(gwaves, kGroupBlock / kWave);
+        if (pos)
+            qk_norm_rope_grouped<kGroupHeads, NORM, true><<<ggrid, kGroupBlock, 0, s>>>(q, k, qw, kw, pos, pos0, rows,
+                                                                                       qh, kh, den, eps);
+        else
+            qk_norm_rope_grouped<kGroupHeads, NORM, false><<<ggrid, kGroupBlock, 0, s>>>(q, k, qw, kw, pos, pos0, rows,
+                                                                                        qh, kh, den, eps);
+    } else if (lph == 64)
+        qk_norm_rope_v4<64, NORM, ROPE><<<grid, block, 0, s>>>(q, k, qw, kw, pos, pos0, rows, qh, kh, rope_dim,
                                                                      den, eps);
     else if (lph == 32)
-        qk_norm_rope_v4<32, NORM, ROPE, false><<<grid, block, 0, s>>>(q, k, qw, kw, pos, pos0, rows, qh, kh, rope_dim,
+        qk_norm_rope_v4<32, NORM, ROPE><<<grid, block, 0, s>>>(q, k, qw, kw, pos, pos0, rows, qh, kh, rope_dim,
                                                                      den, eps);
     else
-        qk_norm_rope_v4<16, NORM, ROPE, false><<<grid, block, 0, s>>>(q, k, qw, kw, pos, pos0, rows, qh, kh, rope_dim,
+        qk_norm_rope_v4<16, NORM, ROPE><<<grid, block, 0, s>>>(q, k, qw, kw, pos, pos0, rows, qh, kh, rope_dim,
                                                                      den, eps);
 }
 

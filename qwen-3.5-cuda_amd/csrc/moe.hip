@@ -16,7 +16,9 @@ namespace qk {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kUnroll = 2;  // 16-byte chunks of each input in flight per thread (best of 1/2/4/8 on gfx950)
+// 16-byte chunks of each input in flight per thread: best of 1/2/4/8 at C3b's
+// 100 MB, and at C3c's 12.6 MB (4.0 us, against 4.2 us with one).
+constexpr int kUnroll = 2;
 
 // ------------------------------------------------------------ bf16 SwiGLU
 // Eight bf16 pairs (one 16-byte chunk of g and of u) -> eight bf16 outputs,
@@ -52,25 +54,29 @@ __device__ __forceinline__ uint4 swiglu8(uint4 g, uint4 u, float scale) {
 // 2*kUnroll streaming loads are issued before any math. SCALED: the shared
 // expert's rows x dim layout with one logit per row (dim % 8 == 0, so a chunk
 // never straddles two rows).
-template <bool SCALED>
+template <int U, bool SCALED>
 __device__ __forceinline__ void swiglu_block(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
                                              const float* __restrict__ logits, uint16_t* __restrict__ h, int64_t n8,
                                              int dim8, unsigned block) {
-    const int64_t first = static_cast<int64_t>(block) * kUnroll * kBlock + threadIdx.x;
-    uint4 gv[kUnroll], uv[kUnroll];
-    float sc[kUnroll];
-    if (static_cast<int64_t>(block + 1) * kUnroll * kBlock <= n8) {  // block-uniform
+    const int64_t first = static_cast<int64_t>(block) * U * kBlock + threadIdx.x;
+    uint4 gv[U], uv[U];
+    float sc[U];
+    if (static_cast<int64_t>(block + 1) * U * kBlock <= n8) {  // block-uniform
 #pragma unroll
-        for (int k = 0; k < kUnroll; ++k) {
+        for (int k = 0; k < U; ++k) {
+            if (SCALED) sc[k] = logits[static_cast<int>(first + k * kBlock) / dim8];  // n8 < 2^31 (host check)
             gv[k] = ld16_nt(g + 8 * (first + k * kBlock));
             uv[k] = ld16_nt(u + 8 * (first + k * kBlock));
-            if (SCALED) sc[k] = logits[static_cast<int>(first + k * kBlock) / dim8];  // n8 < 2^31 (host check)
         }
+        // Every load is issued before any math: without this fence the
+        // scheduler hoists the first sigmoid above the later loads, and each
+        // output then waits for two memory round trips instead of one.
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int k = 0; k < kUnroll; ++k)
+        for (int k = 0; k < U; ++k)
             st16_nt(h + 8 * (first + k * kBlock), swiglu8<SCALED>(gv[k], uv[k], SCALED ? sigmoid(sc[k]) : 1.0f));
     } else {
-        for (int k = 0; k < kUnroll; ++k) {
+        for (int k = 0; k < U; ++k) {
             const int64_t i = first + k * kBlock;
             if (i < n8)
                 st16_nt(h + 8 * i, swiglu8<SCALED>(ld16_nt(g + 8 * i), ld16_nt(u + 8 * i),
@@ -79,11 +85,11 @@ __device__ __forceinline__ void swiglu_block(const uint16_t* __restrict__ g, con
     }
 }
 
-template <bool SCALED>
+template <int U, bool SCALED>
 __global__ __launch_bounds__(kBlock) void swiglu_bf16_v8(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
                                                          const float* __restrict__ logits, uint16_t* __restrict__ h,
                                                          int64_t n8, int dim8) {
-    swiglu_block<SCALED>(g, u, logits, h, n8, dim8, blockIdx.x);
+    swiglu_block<U, SCALED>(g, u, logits, h, n8, dim8, blockIdx.x);
 }
 
 // One part of the routed + shared launch: n8 chunks of 8 bf16 from `blocks`
@@ -105,10 +111,10 @@ struct SwigluPart {
 // would each pay their own ramp and tail.
 __global__ __launch_bounds__(kBlock) void swiglu_routed_shared_v8(const SwigluPart routed, const SwigluPart shared) {
     if (blockIdx.x < routed.blocks)  // block-uniform
-        swiglu_block<false>(routed.g, routed.u, nullptr, routed.h, routed.n8, 1, blockIdx.x);
+        swiglu_block<kUnroll, false>(routed.g, routed.u, nullptr, routed.h, routed.n8, 1, blockIdx.x);
     else
-        swiglu_block<true>(shared.g, shared.u, shared.logits, shared.h, shared.n8, shared.dim8,
-                           blockIdx.x - routed.blocks);
+        swiglu_block<kUnroll, true>(shared.g, shared.u, shared.logits, shared.h, shared.n8, shared.dim8,
+                                    blockIdx.x - routed.blocks);
 }
 
 __device__ __forceinline__ float bf16_at(const uint16_t* p) { return __uint_as_float(static_cast<uint32_t>(*p) << 16); }
@@ -167,9 +173,9 @@ int swiglu_common(const uint16_t* g, const uint16_t* u, const float* logits, uin
         const int64_t n8 = n / 8;
         const unsigned grid = blocks_for(n8, static_cast<int64_t>(kUnroll) * kBlock);
         if (logits)
-            swiglu_bf16_v8<true><<<grid, kBlock, 0, s>>>(g, u, logits, h, n8, dim / 8);
+            swiglu_bf16_v8<kUnroll, true><<<grid, kBlock, 0, s>>>(g, u, logits, h, n8, dim / 8);
         else
-            swiglu_bf16_v8<false><<<grid, kBlock, 0, s>>>(g, u, nullptr, h, n8, 1);
+            swiglu_bf16_v8<kUnroll, false><<<grid, kBlock, 0, s>>>(g, u, nullptr, h, n8, 1);
     } else {
         swiglu_bf16_any<<<stride_grid(n), kBlock, 0, s>>>(g, u, logits, h, n, dim);
     }

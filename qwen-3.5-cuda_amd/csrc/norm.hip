@@ -4,9 +4,10 @@
 // Reference semantics: src/cuda/ops.cu:25-138 (rmsnorm_kernel,
 // rmsnorm_gated_kernel, residual_add_kernel, encoder_kernel). The reference
 // launches one 256-thread block per call and re-reads x for the second pass;
-// here one wave64 owns a row, holds the row in VGPRs between the reduction and
-// the scale (x is read from HBM once), reduces with DPP row ops plus four
-// readlanes, and moves data in 16-byte vectors.
+// here one wave64 owns a row (two waves when there are few rows), holds the row
+// in VGPRs between the reduction and the scale (x is read from HBM once),
+// reduces with DPP row ops and permlane swaps, and moves data in 16-byte
+// vectors.
 #include <algorithm>
 #include <type_traits>
 
@@ -52,15 +53,12 @@ __global__ __launch_bounds__(STAGE ? kStageWaves * kWave : kWave) void rmsnorm_r
     const size_t base = static_cast<size_t>(live ? row : rows - 1) * n;
     float4 v[MAXC], wv[MAXC];
     float4 g[GATED ? MAXC : 1];
-    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
-        const int i = c * kWave + lane;
-        const int ic = min(i, n4 - 1);
+        const int ic = min(c * kWave + lane, n4 - 1);
         v[c] = ld4_nt(x + base + 4 * ic);
         if constexpr (!STAGE) wv[c] = ld4(w + 4 * ic);
         if constexpr (GATED) g[c] = ld4_nt(gate + base + 4 * ic);
-        if (i >= n4) v[c] = zero;
     }
     if constexpr (STAGE) {
         stage_rows_weights(wl, w, n4);
@@ -68,9 +66,12 @@ __global__ __launch_bounds__(STAGE ? kStageWaves * kWave : kWave) void rmsnorm_r
         for (int c = 0; c < MAXC; ++c) wv[c] = wl[min(c * kWave + lane, n4 - 1)];
     }
     if (!live) return;
+    // Chunks past the row end (clamped loads) are left out of the sum by a
+    // select once every load is issued: overwriting a load's destination
+    // registers in the load loop would make each load wait for the previous one.
     float ss = 0.f;
 #pragma unroll
-    for (int c = 0; c < MAXC; ++c) ss += sumsq4(v[c]);
+    for (int c = 0; c < MAXC; ++c) ss += c * kWave + lane < n4 ? sumsq4(v[c]) : 0.f;
     ss = group_sum<kWave>(ss);
     const float r = rsqrtf(ss / static_cast<float>(n) + eps);
 #pragma unroll
@@ -89,6 +90,68 @@ __global__ __launch_bounds__(STAGE ? kStageWaves * kWave : kWave) void rmsnorm_r
             o.w *= sg.w;
         }
         if (i < n4) st4_nt(out + base + 4 * i, o);
+    }
+}
+
+// Few rows (fewer than kSplitRows, e.g. the 36 rows of one prompt's final
+// norm): kSplitWaves waves share a row, wave v holding the 64-float4 chunks
+// v, v + kSplitWaves, ...; the two wave sums meet in LDS and are added in wave
+// order. Twice the waves in flight for the same bytes: at 36 x 2048 it measured
+// 2.16 us against 2.50 us with one wave per row (a plain copy of the same bytes
+// takes 1.87 us).
+constexpr int kSplitWaves = 2;
+constexpr int kSplitRows = 256;
+
+// FULL: n4 == MAXC * kSplitWaves * 64 (every chunk inside the row: no clamps or
+// masks, so the loads take immediate offsets and the sum needs no selects).
+template <int MAXC, bool GATED, bool FULL>
+__global__ __launch_bounds__(kSplitWaves * kWave) void rmsnorm_rows_split(
+    const float* __restrict__ x, const float* __restrict__ gate, const float* __restrict__ w, float* __restrict__ out,
+    int n, float eps) {
+    __shared__ float part[kSplitWaves];
+    const int lane = threadIdx.x & 63;
+    const int wv = wave_in_block();
+    const int n4 = n >> 2;
+    const size_t base = static_cast<size_t>(blockIdx.x) * n;
+    auto chunk = [&](int c) { return (c * kSplitWaves + wv) * kWave + lane; };
+    auto at = [&](int c) { return FULL ? chunk(c) : min(chunk(c), n4 - 1); };  // clamped: loads never branch
+    float4 v[MAXC], wt[MAXC];
+    float4 g[GATED ? MAXC : 1];
+    // the row (from HBM) first, then the gate and the weights (shared by every
+    // row, so mostly cache hits): the row's round trip starts earliest
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) v[c] = ld4_nt(x + base + 4 * at(c));
+    if constexpr (GATED) {
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) g[c] = ld4_nt(gate + base + 4 * at(c));
+    }
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) wt[c] = ld4(w + 4 * at(c));
+    float ss = 0.f;  // chunks past the row end left out by a select (see rmsnorm_rows_v4)
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) ss += (FULL || chunk(c) < n4) ? sumsq4(v[c]) : 0.f;
+    ss = group_sum<kWave>(ss);
+    if (lane == 0) part[wv] = ss;
+    __syncthreads();
+    ss = part[0];
+#pragma unroll
+    for (int k = 1; k < kSplitWaves; ++k) ss += part[k];
+    const float r = rsqrtf(ss / static_cast<float>(n) + eps);
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        float4 o;
+        o.x = v[c].x * r * wt[c].x;
+        o.y = v[c].y * r * wt[c].y;
+        o.z = v[c].z * r * wt[c].z;
+        o.w = v[c].w * r * wt[c].w;
+        if constexpr (GATED) {
+            const float4 sg = silu4(g[c]);
+            o.x *= sg.x;
+            o.y *= sg.y;
+            o.z *= sg.z;
+            o.w *= sg.w;
+        }
+        if (FULL || chunk(c) < n4) st4_nt(out + base + 4 * chunk(c), o);
     }
 }
 
@@ -317,7 +380,25 @@ int launch_rmsnorm(const float* x, const float* gate, const float* w, float* out
                    hipStream_t s) {
     const int n4 = n / 4;
     const bool vec = (n % 4 == 0) && aligned16(x) && aligned16(w) && aligned16(out) && (!GATED || aligned16(gate));
-    if (vec && n4 <= 16 * kWave) {
+    constexpr int kSplit = kSplitWaves * kWave;
+    if (vec && rows < kSplitRows && n4 <= 8 * kSplit) {
+        const dim3 grid(rows), block(kSplit);
+        const auto go = [&](auto maxc) {
+            constexpr int M = decltype(maxc)::value;
+            if (n4 == M * kSplit)
+                rmsnorm_rows_split<M, GATED, true><<<grid, block, 0, s>>>(x, gate, w, out, n, eps);
+            else
+                rmsnorm_rows_split<M, GATED, false><<<grid, block, 0, s>>>(x, gate, w, out, n, eps);
+        };
+        if (n4 <= kSplit)
+            go(std::integral_constant<int, 1>{});
+        else if (n4 <= 2 * kSplit)
+            go(std::integral_constant<int, 2>{});
+        else if (n4 <= 4 * kSplit)
+            go(std::integral_constant<int, 4>{});
+        else
+            go(std::integral_constant<int, 8>{});
+    } else if (vec && n4 <= 16 * kWave) {
         launch_row_shape(rows, size_t(n4) * 16, [&](auto stage, dim3 grid, dim3 block, size_t lds) {
             constexpr bool S = decltype(stage)::value;
             if (n4 <= kWave)
