@@ -256,6 +256,23 @@ int qwen_attn_decode(const float* q, const float* k_cache, const float* v_cache,
                      float* out, int heads, int kv_heads, int dim, int pos, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* qwen_attn_decode without a workspace argument and without any allocation: the
+ * split-K partials live in a fixed device array of
+ * qwen_attn_decode_noalloc_max_scratch_bytes() bytes (8 MiB) inside the library,
+ * one copy per GPU, held until the process ends. No counterpart in the reference:
+ * this entry point is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Shapes whose qwen_attn_decode_workspace_bytes exceed the array are rejected with
+ * INVALID_ARGUMENT (16 query / 2 kv heads of 256: up to 16,256 keys; 8 query heads
+ * per kv head: 516 bytes per key for 16 query heads). Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (several streams or host threads)
+ * race and must be serialised by the caller. Nothing in the array has to start at
+ * zero. Output equals qwen_attn_decode's bit for bit. */
+size_t qwen_attn_decode_noalloc_max_scratch_bytes(void);
+int qwen_attn_decode_noalloc(const float* q, const float* k_cache, const float* v_cache,
+                             const float* gate, float* out, int heads, int kv_heads, int dim,
+                             int pos, void* stream);
+
 /* ====================================================================== MoE routing
  * The reference picks experts on the device, copies them to the host and syncs
  * (src/layer_moe.cpp:98-106); these entry points keep the routing on the device. */

@@ -22,9 +22,17 @@
 // the total and applies the sigmoid gate.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "capi_common.hpp"
 #include "device_common.hpp"
+
+// Scratch of qwen_attn_decode_noalloc (its split-K partials): a device array,
+// one copy on every GPU the library runs on, held until the process ends. In
+// host code this name is a host-side stand-in, not a device address: the host
+// uses the address hipGetSymbolAddress returns for the current device.
+constexpr size_t kDecodeScratchBytes = size_t{8} << 20;
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
 
 namespace qk {
 namespace {
@@ -357,6 +365,34 @@ size_t fused_workspace_bytes(int heads, int kv_heads, int dim, int n_keys) {
     return static_cast<size_t>(fused_splits(heads, kv_heads, n_keys)) * heads * (dim + 2) * sizeof(float);
 }
 
+// The device address of `scratch` on the current device, looked up once per
+// device (hipGetSymbolAddress with that device current) and kept.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int decode_scratch(void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(QWEN_STATUS_LAUNCH_FAILED, "attn_decode_noalloc: no current device");
+    }
+    QK_REQUIRE(dev >= 0 && dev < kMaxDevices, "attn_decode_noalloc: device %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return fail(QWEN_STATUS_LAUNCH_FAILED, "attn_decode_noalloc: hipGetSymbolAddress failed on device %d: %s",
+                        dev, hipGetErrorString(e));
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return ok();
+}
+
 }  // namespace
 }  // namespace qk
 
@@ -438,13 +474,13 @@ size_t qwen_attn_decode_workspace_bytes(int heads, int kv_heads, int dim, int po
                : staged;
 }
 
-int qwen_attn_decode(const float* q, const float* k_cache, const float* v_cache, const float* gate, float* out,
-                     int heads, int kv_heads, int dim, int pos, void* workspace, size_t workspace_bytes,
-                     void* stream) {
-    QK_ATTN_SHAPE("attn_decode");
-    QK_REQUIRE(q && k_cache && v_cache && out && workspace, "attn_decode: null pointer");
-    const size_t need = qwen_attn_decode_workspace_bytes(heads, kv_heads, dim, pos);
-    QK_REQUIRE(workspace_bytes >= need, "attn_decode: workspace of %zu bytes, need %zu", workspace_bytes, need);
+}  // extern "C"
+
+namespace {
+
+// qwen_attn_decode on a workspace already checked against the shape.
+int attn_decode_ws(const float* q, const float* k_cache, const float* v_cache, const float* gate, float* out,
+                   int heads, int kv_heads, int dim, int pos, void* workspace, void* stream) {
     hipStream_t s = as_stream(stream);
     const int n_keys = pos + 1;
     if (fused_ok(heads, kv_heads, dim, n_keys) && aligned16(q) && aligned16(k_cache)) {
@@ -473,6 +509,36 @@ int qwen_attn_decode(const float* q, const float* k_cache, const float* v_cache,
     if (!st) st = qwen_attn_values(sc, v_cache, out, heads, kv_heads, dim, pos, stream);
     if (!st && gate) st = qwen_attn_sigmoid_gate(out, gate, out, heads * dim, stream);
     return st;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qwen_attn_decode(const float* q, const float* k_cache, const float* v_cache, const float* gate, float* out,
+                     int heads, int kv_heads, int dim, int pos, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+    QK_ATTN_SHAPE("attn_decode");
+    QK_REQUIRE(q && k_cache && v_cache && out && workspace, "attn_decode: null pointer");
+    const size_t need = qwen_attn_decode_workspace_bytes(heads, kv_heads, dim, pos);
+    QK_REQUIRE(workspace_bytes >= need, "attn_decode: workspace of %zu bytes, need %zu", workspace_bytes, need);
+    return attn_decode_ws(q, k_cache, v_cache, gate, out, heads, kv_heads, dim, pos, workspace, stream);
+}
+
+size_t qwen_attn_decode_noalloc_max_scratch_bytes(void) { return kDecodeScratchBytes; }
+
+int qwen_attn_decode_noalloc(const float* q, const float* k_cache, const float* v_cache, const float* gate,
+                             float* out, int heads, int kv_heads, int dim, int pos, void* stream) {
+    QK_ATTN_SHAPE("attn_decode_noalloc");
+    QK_REQUIRE(q && k_cache && v_cache && out, "attn_decode_noalloc: null pointer");
+    const size_t need = qwen_attn_decode_workspace_bytes(heads, kv_heads, dim, pos);
+    QK_REQUIRE(need <= kDecodeScratchBytes,
+               "attn_decode_noalloc: this shape needs %zu bytes of scratch, beyond the fixed %zu (heads=%d "
+               "kv_heads=%d dim=%d pos=%d); use qwen_attn_decode with a workspace",
+               need, kDecodeScratchBytes, heads, kv_heads, dim, pos);
+    void* ws = nullptr;
+    if (const int rc = decode_scratch(&ws)) return rc;
+    return attn_decode_ws(q, k_cache, v_cache, gate, out, heads, kv_heads, dim, pos, ws, stream);
 }
 
 }  // extern "C"

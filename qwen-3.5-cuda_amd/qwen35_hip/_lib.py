@@ -75,6 +75,8 @@ SIGNATURES: dict[str, list] = {
     "qwen_attn_kv_store": [_P, _P, _P, _P, _I, _I, _I, _P],
     "qwen_attn_decode_workspace_bytes": [_I, _I, _I, _I],
     "qwen_attn_decode": [_P] * 5 + [_I, _I, _I, _I, _P, ctypes.c_size_t, _P],
+    "qwen_attn_decode_noalloc_max_scratch_bytes": [],
+    "qwen_attn_decode_noalloc": [_P] * 5 + [_I, _I, _I, _I, _P],
     "qwen_moe_topk": [_P, _P, _P, _I, _I, _P],
     "qwen_moe_topk_rows": [_P, _P, _P, _I, _I, _I, _P],
     "qwen_moe_add": [_P, _P, _F, _I, _P],
@@ -112,6 +114,7 @@ SIGNATURES: dict[str, list] = {
 
 _RESTYPES = {"qwen_last_error": ctypes.c_char_p, "qwen_status_name": ctypes.c_char_p,
              "qwen_attn_decode_workspace_bytes": ctypes.c_size_t,
+             "qwen_attn_decode_noalloc_max_scratch_bytes": ctypes.c_size_t,
              "qwen_matmul_rows_workspace_bytes": ctypes.c_size_t,
              "qwen_gdn_recurrent_chunked_workspace_bytes": ctypes.c_size_t,
              "qwen_moe_down_combine_workspace_bytes": ctypes.c_size_t,

@@ -429,6 +429,21 @@ def attn_decode(q, k_cache, v_cache, heads, kv_heads, dim, pos, gate=None, works
     return out
 
 
+def attn_decode_noalloc(q, k_cache, v_cache, heads, kv_heads, dim, pos, gate=None, out=None, stream=None):
+    """attn_decode with the library's fixed device scratch instead of a workspace
+    (no device allocation in the call when `out` is given)."""
+    _dev(q, k_cache, v_cache, dtype=torch.float32)
+    _attn_check(q, k_cache, heads, kv_heads, dim, pos)
+    _attn_check(q, v_cache, heads, kv_heads, dim, pos)
+    if gate is not None:
+        _dev(gate, dtype=torch.float32)
+    out = torch.empty(heads * dim, dtype=torch.float32, device=q.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    check(load().qwen_attn_decode_noalloc(_p(q), _p(k_cache), _p(v_cache), _p(gate), _p(out), heads, kv_heads, dim,
+                                          pos, _stream(stream)))
+    return out
+
+
 # ------------------------------------------------------------------ MoE routing
 def moe_topk_rows(logits, k, idx=None, weights=None, stream=None):
     """logits [rows, n] (or [n]) -> idx int32, weights float32 [rows, k]."""

@@ -181,3 +181,14 @@ def test_swiglu_routed_shared_validation(lib):
     assert f(NULL, FAKE, FAKE, 8, FAKE, FAKE, FAKE, FAKE, 1, 8, ST) == INV and "routed" in msg(lib)
     assert f(FAKE, FAKE, FAKE, 8, FAKE, FAKE, NULL, FAKE, 1, 8, ST) == INV and "shared" in msg(lib)
     assert f(NULL, NULL, NULL, 0, NULL, NULL, NULL, NULL, 0, 512, ST) == OK  # both parts empty
+
+
+def test_attn_decode_noalloc_host_validation(lib):
+    """Shape, pointer and scratch-size checks come before any device call."""
+    INV = _lib.STATUS_INVALID_ARGUMENT
+    f = lib.qwen_attn_decode_noalloc
+    assert lib.qwen_attn_decode_noalloc_max_scratch_bytes() == 8 << 20
+    assert f(FAKE, FAKE, FAKE, NULL, FAKE, 6, 4, 64, 3, ST) == INV  # heads not a multiple of kv_heads
+    assert f(NULL, FAKE, FAKE, NULL, FAKE, 16, 2, 256, 3, ST) == INV and "null" in msg(lib)
+    assert lib.qwen_attn_decode_workspace_bytes(64, 8, 256, 19999) > 8 << 20
+    assert f(FAKE, FAKE, FAKE, NULL, FAKE, 64, 8, 256, 19999, ST) == INV and "scratch" in msg(lib)
