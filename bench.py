@@ -23,8 +23,8 @@ each kernel gets enough copies of its buffers that consecutive launches touch
 >= 1 GiB of distinct memory (4x the MALL); the rotating launches are captured in
 a graph and timed with HIP events around R replays on the launching stream;
 us/call = elapsed / launches. The same measurement of a plain 16-byte-vector
-copy of the same byte count is reported beside each kernel as the box's
-practical ceiling. Algorithmic bytes count every input read once and every
+copy of the same byte count (the fastest of three launch shapes, COPY_FORMS) is
+reported beside each kernel as the box's practical ceiling. Algorithmic bytes count every input read once and every
 output written once. The roofline object reports the kernel with the largest
 time per step; its "traffic" comes from the committed rocprofv3 counter runs
 (profiles/traffic.json) when present.
@@ -538,9 +538,10 @@ def spin_cycles_per_ms(torch) -> float:
 
 
 GRAPH_LAUNCHES = 64  # kernel launches per captured graph in the steady-state timing
+TIMED_LAUNCHES: dict[str, int] = {}  # kernel name -> launches in its timed batches (for --timed-counts)
 
 
-def steady_state_us(torch, launches, replays: int, spin: int, repeats: int = 5) -> float:
+def steady_state_us(torch, launches, replays: int, spin: int, repeats: int = 5, name: str | None = None) -> float:
     """us per launch of `launches` (one per buffer set, cycled through the sets
     until the graph holds at least GRAPH_LAUNCHES launches, so the gap between
     two graph launches is spread over that many kernels rather than over a
@@ -574,6 +575,8 @@ def steady_state_us(torch, launches, replays: int, spin: int, repeats: int = 5) 
         torch.cuda.synchronize()
         times.append(e0.elapsed_time(e1) * 1e3 / (replays * len(launches)))
     del g
+    if name:
+        TIMED_LAUNCHES[name] = repeats * replays * len(launches)
     return sorted(times)[len(times) // 2]
 
 
@@ -608,26 +611,39 @@ def measure_kernel(torch, k: Kernel, spin: int, min_launches: int) -> float:
         del launches
         torch.cuda.empty_cache()
         return us
-    us = steady_state_us(torch, launches, replays, spin)
+    us = steady_state_us(torch, launches, replays, spin, name=k.name)
     del launches
     torch.cuda.empty_cache()
     return us
 
 
+# Copy forms the per-kernel ceiling takes the best of (unroll, block): the
+# reference streaming copy (8 x 16 B per thread, 256 threads: the fastest form
+# from ~64 MB up) and the two forms the small-size sweep found fastest below
+# that (one vector per thread in 256-thread workgroups; four per thread in
+# single-wave workgroups).
+COPY_FORMS = [(8, 256), (1, 256), (4, 64)]
+
+
 def measure_copy(torch, bench_lib, nbytes: int, spin: int, min_launches: int) -> float:
+    """us per launch of the fastest COPY_FORMS copy of nbytes (half read, half
+    written), timed like a kernel."""
     half = (nbytes // 2 + 15) // 16 * 16
     sets = n_sets(2 * half)
     bufs = [(torch.empty(half, dtype=torch.uint8, device="cuda:0"), torch.empty(half, dtype=torch.uint8, device="cuda:0"))
             for _ in range(sets)]
+    fn = bench_lib.qwen_bench_copy_form
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_int, ctypes.c_void_p]
 
-    def launcher(src, dst):
+    def launcher(src, dst, u, b):
         def f():
-            rc = bench_lib.qwen_bench_copy(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), half,
-                                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-            if rc:
-                raise RuntimeError("qwen_bench_copy failed")
+            if fn(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), half, u, b, 0, 1,
+                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)):
+                raise RuntimeError("qwen_bench_copy_form failed")
         return f
-    us = steady_state_us(torch, [launcher(s, d) for s, d in bufs], max(1, -(-min_launches // sets)), spin)
+    us = min(steady_state_us(torch, [launcher(s, d, u, b) for s, d in bufs], max(1, -(-min_launches // sets)), spin)
+             for u, b in COPY_FORMS)
     del bufs
     torch.cuda.empty_cache()
     return us
@@ -676,6 +692,13 @@ def copy_sweep(torch, bench_lib, spin: int, min_launches: int) -> list[dict]:
         print(f"# copy sweep {2 * half:>10d} B: best {best['us']:7.2f} us {best['gbps']:7.1f} GB/s "
               f"(unroll {best['unroll']}, block {best['block']}, grid cap {best['grid_cap']}, nt {best['nt']})",
               file=sys.stderr, flush=True)
+        mine = sorted((r for r in out if r["bytes"] == 2 * half), key=lambda r: r["us"])
+        std = next(r for r in mine if (r["unroll"], r["block"], r["grid_cap"], r["nt"], r["inplace"]) ==
+                   (8, 256, 0, 1, False))
+        for r in mine[:5] + [std]:
+            print(f"#   {r['us']:8.3f} us {r['gbps']:8.1f} GB/s  unroll {r['unroll']:2d} block {r['block']:4d} "
+                  f"grid cap {r['grid_cap']:4d} nt {r['nt']} {'in place' if r['inplace'] else ''}"
+                  f"{'  <- bench.py reference copy form' if r is std else ''}", file=sys.stderr, flush=True)
         del bufs
         torch.cuda.empty_cache()
     return out
@@ -920,6 +943,13 @@ def main() -> int:
     ap.add_argument("--json-out", default="", help="also write the JSON line to this file")
     ap.add_argument("--profile-gemv", type=int, default=0, metavar="N",
                     help="also run the LM-head GEMV N times after the step (counter runs)")
+    ap.add_argument("--timed-counts", default="", metavar="JSON",
+                    help="write each kernel's number of launches in its timed batches (for a steady-state trace)")
+    ap.add_argument("--no-step", action="store_true",
+                    help="skip the step graph (a trace of the per-kernel steady state only)")
+    ap.add_argument("--step-all", action="store_true",
+                    help="counter runs: put every kernel in the step graph, also those whose work the step does "
+                         "through another entry point (C3b and C3c, done in the step by the routed+shared launch)")
     ap.add_argument("--copy-sweep", default="", metavar="JSON",
                     help="only run the streaming-copy sweep at small sizes and write its records to JSON")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
@@ -954,9 +984,9 @@ def main() -> int:
     spin = int(spin_cycles_per_ms(torch) * 2.0)
 
     # ---- the step: K graph replays (the contract)
-    step = [k for k in kernels if k.in_step]
+    step = [k for k in kernels if k.in_step or args.step_all]
     ms_per_step, value, bytes_step = 0.0, 0.0, sum(k.bytes for k in step)
-    if step:  # (empty only in a profiling run of the decode GEMVs)
+    if step and not args.no_step:  # (empty only in a profiling run of the decode GEMVs)
         base = [k.make(0) for k in step]
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -1119,6 +1149,8 @@ def main() -> int:
         "next_rows": next_rows,
         "gguf_load": gguf,
     }
+    if args.timed_counts:
+        Path(args.timed_counts).write_text(json.dumps(TIMED_LAUNCHES, indent=1) + "\n")
     text = json.dumps(line)
     print(text, flush=True)
     if args.json_out:

@@ -2,6 +2,10 @@
 
   python -m qwen35_hip.rocprof_summary stats   KERNEL_STATS.csv
       per-kernel dispatch count and average / min / max duration (us)
+  python -m qwen35_hip.rocprof_summary steady KERNEL_TRACE.csv TIMED.json
+      per-kernel duration (us) over the dispatches of the steady-state timed
+      batches only: the last N dispatches of each kernel, N from the counts
+      bench.py --timed-counts wrote (no step-graph, warm-up or eager dispatches)
   python -m qwen35_hip.rocprof_summary traffic FETCH.csv WRITE.csv COPY_BYTES [--json OUT]
       per-kernel FETCH_SIZE / WRITE_SIZE (KiB per dispatch, from two --pmc runs),
       scaled to bytes by the factor that makes the reference copy of COPY_BYTES
@@ -24,14 +28,17 @@ from collections import defaultdict
 NAMES = [
     ("gdn_frontend_k4", "gdn_frontend"),
     ("norm_gate_v4", "gdn_norm_gate"),
-    ("swiglu_bf16_v8ILb1", "shared_swiglu_sigmoid_bf16"),
-    ("swiglu_bf16_v8ILb0", "swiglu_bf16"),
-    ("swiglu_bf16_v8<true>", "shared_swiglu_sigmoid_bf16"),
-    ("swiglu_bf16_v8<false>", "swiglu_bf16"),
+    ("swiglu_routed_shared_v8", "swiglu_routed_shared_bf16"),
+    ("swiglu_bf16_v8ILi2ELb1", "shared_swiglu_sigmoid_bf16"),
+    ("swiglu_bf16_v8ILi2ELb0", "swiglu_bf16"),
+    ("swiglu_bf16_v8<2, true>", "shared_swiglu_sigmoid_bf16"),
+    ("swiglu_bf16_v8<2, false>", "swiglu_bf16"),
     ("gather_q4k", "dequant_gather_q4_k"),
     ("gather_q6k", "dequant_gather_q6_k"),
     ("residual_rmsnorm_bf16_v8", "residual_rmsnorm_bf16"),
+    ("qk_norm_rope_grouped", "qk_norm_rope"),
     ("qk_norm_rope_v4", "qk_norm_rope"),
+    ("rmsnorm_rows_split", "rmsnorm"),
     ("rmsnorm_rows_v4", "rmsnorm"),
     ("copy16", "copy"),
     # next rows (kernel symbols; several bench shapes can share one instantiation)
@@ -63,7 +70,7 @@ NAMES = [
 ALGORITHMIC = {
     "rmsnorm": 598016, "qk_norm_rope": 18878464, "residual_rmsnorm_bf16": 67117056, "swiglu_bf16": 100663296,
     "shared_swiglu_sigmoid_bf16": 12599296, "gdn_frontend": 268763136, "gdn_norm_gate": 201327104,
-    "dequant_gather_q4_k": 76578816, "dequant_gather_q6_k": 80904192,
+    "dequant_gather_q4_k": 76578816, "dequant_gather_q6_k": 80904192, "swiglu_routed_shared_bf16": 113262592,
     # the LM-head GEMV (bench.py next rows: Q6_K 248320 x 2048, x and y fp32)
     "gemv Q6_K MFMA, 2-block k-slices (LM head)": 418179072,
 }
@@ -90,6 +97,27 @@ def stats(path: str) -> dict:
         table[name] = {"calls": calls, "avg_us": total / calls / 1e3, "min_us": min(float(r["MinNs"]) for r in rs) / 1e3,
                        "max_us": max(float(r["MaxNs"]) for r in rs) / 1e3}
     return table
+
+
+def steady(trace_csv: str, timed_json: str) -> dict:
+    """Duration statistics over each kernel's last N dispatches, N = the number
+    of launches in its timed batches (bench.py --timed-counts): in a run that
+    measures each kernel once, those are exactly the timed graph replays."""
+    timed = json.load(open(timed_json))
+    disp = defaultdict(list)
+    for r in csv.DictReader(open(trace_csv)):
+        name = kernel_name(r["Kernel_Name"])
+        if name in timed:
+            disp[name].append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    out = {}
+    for name, n in timed.items():
+        d = sorted(disp.get(name, []))[-n:]
+        if not d:
+            continue
+        us = sorted((e - b) / 1e3 for b, e in d)
+        out[name] = {"dispatches": len(us), "of_total": len(disp[name]), "avg_us": sum(us) / len(us),
+                     "median_us": us[len(us) // 2], "min_us": us[0], "max_us": us[-1]}
+    return out
 
 
 def counter_means(path: str, counter: str) -> dict:
@@ -132,6 +160,9 @@ def main(argv=None) -> int:
     sub = ap.add_subparsers(dest="cmd", required=True)
     a = sub.add_parser("stats")
     a.add_argument("csv")
+    c = sub.add_parser("steady")
+    c.add_argument("trace_csv")
+    c.add_argument("timed_json")
     b = sub.add_parser("traffic")
     b.add_argument("fetch_csv")
     b.add_argument("write_csv")
@@ -145,6 +176,15 @@ def main(argv=None) -> int:
             gbps = ALGORITHMIC.get(name, 0) / r["avg_us"] / 1e3 if name in ALGORITHMIC else float("nan")
             print(f"{name[:44]:44s} {r['calls']:6d} {r['avg_us']:9.2f} {r['min_us']:9.2f} {r['max_us']:9.2f} "
                   f"{gbps:11.1f}")
+        return 0
+    if args.cmd == "steady":
+        t = steady(args.trace_csv, args.timed_json)
+        print(f"{'kernel':44s} {'timed':>6s} {'of':>6s} {'avg us':>8s} {'median':>8s} {'min us':>8s} {'max us':>8s} "
+              f"{'GB/s (avg)':>11s}")
+        for name, r in sorted(t.items(), key=lambda kv: -kv[1]["avg_us"]):
+            gbps = ALGORITHMIC[name] / r["avg_us"] / 1e3 if name in ALGORITHMIC else float("nan")
+            print(f"{name[:44]:44s} {r['dispatches']:6d} {r['of_total']:6d} {r['avg_us']:8.2f} {r['median_us']:8.2f} "
+                  f"{r['min_us']:8.2f} {r['max_us']:8.2f} {gbps:11.1f}")
         return 0
     t = traffic(args.fetch_csv, args.write_csv, args.copy_bytes)
     cal = t["_calibration"]
