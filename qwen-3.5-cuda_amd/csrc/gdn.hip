@@ -27,8 +27,12 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kConvTile = 64;    // tokens per thread tile (generic front end)
-constexpr int kConvRows = 4;     // rows per wave (vector front end)
-constexpr int kConvWaves = 8;    // waves per workgroup (vector front end)
+// Vector front end: rows per wave and waves per workgroup. Swept at C4a (4096 x
+// 8192): 3 x 8 = 44.5 us, 4 x 8 = 44.9, 4 x 4 = 45.9, 6 x 8 = 46.4, 8 x 8 = 50.2;
+// one or two rows per wave (halo rows then come from two or three waves back,
+// through LDS) 45.3-57 us. Three is the fewest rows a wave can hand on whole.
+constexpr int kConvRows = 3;
+constexpr int kConvWaves = 8;
 constexpr int kGateUnroll = 4;   // head groups in flight per wave (norm_gate)
 
 // ---------------------------------------------------- front end, kernel size 4
