@@ -21,7 +21,9 @@
 // short per-lane partial plus a 4-5 step DPP reduction. The multi-token entry
 // point keeps the state slice in VGPRs across all tokens of the call (the
 // reference's per-token loop, one launch), reading each token's q, k, v
-// straight from the GDN front end's output rows.
+// straight from the GDN front end's output rows. A single token (the decode
+// step) reads the state as whole 128-byte lines instead: a workgroup of four
+// waves per (value head, 32 columns), column sums through DPP and LDS.
 #include <algorithm>
 #include <cmath>
 
@@ -159,8 +161,8 @@ __global__ __launch_bounds__(kBlock) void gdn_recurrent_g(float* __restrict__ S,
     for (int r = 0; r < RPL; ++r) __builtin_nontemporal_store(s[r], Sj + static_cast<size_t>(r) * value_dim);
 }
 
-// Single step (rows = 1, the decode path): one wave per (value head, 4 value
-// columns); RPL rows of the state per lane
+// Single step with value_dim % 32 != 0 (gdn_step_tile takes the others): one
+// wave per (value head, 4 value columns); RPL rows of the state per lane
 // (key_dim = 64 * RPL). Tokens t < rows run in order, the state slice staying
 // in VGPRs; q/k/v of token t sit at t * qkv_stride, beta/decay at
 // t * value_heads, out at t * out_stride. The inputs of token t + kPrefetch
@@ -260,42 +262,174 @@ __global__ __launch_bounds__(kBlock) void gdn_recurrent_v4(float* __restrict__ S
     for (int r = 0; r < RPL; ++r) st4_nt(Sh + static_cast<size_t>(lane + 64 * r) * value_dim, s[r]);
 }
 
+// Single token with value_dim % 32 == 0 (the decode path): one workgroup of
+// kTileWaves waves per (value head h, kTileCols = 32 value columns). Lane L holds
+// columns 4 * (L / 8) .. + 3 of the block and wave w rows
+// w * DK / 4 + L % 8 + 8 r (r < DK / 32): the 8 lanes of a column group read 8
+// rows and the 8 groups the 32 columns of each, so one float4 load instruction
+// covers 8 whole 128-byte lines of the state (a 4-column slice per wave, as
+// gdn_recurrent_v4 reads, touches 64 lines with 16 bytes each and runs ~40%
+// longer at the Qwen3.5 shape). A column's sums over rows: a per-lane partial,
+// an 8-lane DPP sum, and the waves' partials added through LDS in wave order.
+constexpr int kTileWaves = kWaves;
+constexpr int kTileLanes = 8;                        // lanes per column group
+constexpr int kTileGroups = kWave / kTileLanes;      // column groups per wave
+constexpr int kTileCols = 4 * kTileGroups;           // value columns per workgroup
+
+// One token on a lane's slice (RPL rows kr / qr of k / q, the state rows s at
+// St + 8 r * value_dim, value columns vv, gates b / d): S *= d; m = k . S;
+// delta = (v - m) b; S += k delta; o = q . S. Stores the state slice and
+// returns o summed over the workgroup (wave 0; other waves get a partial).
+// red: 2 * kTileWaves * kTileGroups float4 of LDS; every thread of the
+// workgroup must call it (two barriers).
+template <int RPL>
+__device__ __forceinline__ float4 tile_step(float4 (&s)[RPL], const float (&kr)[RPL], const float (&qr)[RPL],
+                                            float4 vv, float b, float d, float* St, int value_dim, float4* red,
+                                            int w, int cg, int rl) {
+    float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+        s[r].x *= d;
+        s[r].y *= d;
+        s[r].z *= d;
+        s[r].w *= d;
+        m.x = __builtin_fmaf(kr[r], s[r].x, m.x);
+        m.y = __builtin_fmaf(kr[r], s[r].y, m.y);
+        m.z = __builtin_fmaf(kr[r], s[r].z, m.z);
+        m.w = __builtin_fmaf(kr[r], s[r].w, m.w);
+    }
+    m.x = group_sum<kTileLanes>(m.x);
+    m.y = group_sum<kTileLanes>(m.y);
+    m.z = group_sum<kTileLanes>(m.z);
+    m.w = group_sum<kTileLanes>(m.w);
+    if (rl == 0) red[w * kTileGroups + cg] = m;
+    __syncthreads();
+    m = red[cg];
+#pragma unroll
+    for (int x = 1; x < kTileWaves; ++x) {
+        const float4 u = red[x * kTileGroups + cg];
+        m.x += u.x;
+        m.y += u.y;
+        m.z += u.z;
+        m.w += u.w;
+    }
+    const float4 dl = make_float4((vv.x - m.x) * b, (vv.y - m.y) * b, (vv.z - m.z) * b, (vv.w - m.w) * b);
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+        s[r].x = __builtin_fmaf(kr[r], dl.x, s[r].x);
+        s[r].y = __builtin_fmaf(kr[r], dl.y, s[r].y);
+        s[r].z = __builtin_fmaf(kr[r], dl.z, s[r].z);
+        s[r].w = __builtin_fmaf(kr[r], dl.w, s[r].w);
+        o.x = __builtin_fmaf(qr[r], s[r].x, o.x);
+        o.y = __builtin_fmaf(qr[r], s[r].y, o.y);
+        o.z = __builtin_fmaf(qr[r], s[r].z, o.z);
+        o.w = __builtin_fmaf(qr[r], s[r].w, o.w);
+    }
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) st4_nt(St + static_cast<size_t>(kTileLanes * r) * value_dim, s[r]);
+    o.x = group_sum<kTileLanes>(o.x);
+    o.y = group_sum<kTileLanes>(o.y);
+    o.z = group_sum<kTileLanes>(o.z);
+    o.w = group_sum<kTileLanes>(o.w);
+    float4* ro = red + kTileWaves * kTileGroups;
+    if (rl == 0) ro[w * kTileGroups + cg] = o;
+    __syncthreads();
+    if (w == 0) {
+        o = ro[cg];
+#pragma unroll
+        for (int x = 1; x < kTileWaves; ++x) {
+            const float4 u = ro[x * kTileGroups + cg];
+            o.x += u.x;
+            o.y += u.y;
+            o.z += u.z;
+            o.w += u.w;
+        }
+    }
+    return o;
+}
+
+// The tile form of one token (key dim DK = 64 or 128). Grid: exactly
+// value_heads * value_dim / kTileCols workgroups of kBlock threads.
+template <int DK>
+__global__ __launch_bounds__(kBlock) void gdn_step_tile(float* __restrict__ S, const float* __restrict__ q,
+                                                        const float* __restrict__ k, const float* __restrict__ v,
+                                                        const float* __restrict__ beta,
+                                                        const float* __restrict__ decay, float* __restrict__ out,
+                                                        int key_heads, int value_dim, RawGates rg) {
+    constexpr int RPL = DK / (kTileWaves * kTileLanes);
+    static_assert(RPL * kTileWaves * kTileLanes == DK, "key dim");
+    __shared__ float4 red[2 * kTileWaves * kTileGroups];
+    const int lane = threadIdx.x & 63;
+    const int w = wave_in_block();
+    const int cblocks = value_dim / kTileCols;
+    const int h = blockIdx.x / cblocks;
+    const int cg = lane / kTileLanes, rl = lane % kTileLanes;
+    const int j0 = (blockIdx.x - h * cblocks) * kTileCols + 4 * cg;
+    const int src = h % key_heads;  // value heads tile as [subgroup][key head]
+    const int r0 = w * (DK / kTileWaves) + rl;
+    float* St = S + (static_cast<size_t>(h) * DK + r0) * value_dim + j0;
+    const float* kt = k + src * DK + r0;
+    const float* qt = q + src * DK + r0;
+    float kr[RPL], qr[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+        kr[r] = kt[kTileLanes * r];
+        qr[r] = qt[kTileLanes * r];
+    }
+    const float4 vv = ld4(v + static_cast<size_t>(h) * value_dim + j0);
+    float4 s[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) s[r] = ld4_nt(St + static_cast<size_t>(kTileLanes * r) * value_dim);
+    const float br = beta[h], dr = decay[h];
+    const float d = rg.a ? gate_decay(rg.a[h], dr, rg.dt[h]) : dr;
+    const float b = rg.a ? gate_beta(br) : br;
+    const float4 o = tile_step<RPL>(s, kr, qr, vv, b, d, St, value_dim, red, w, cg, rl);
+    if (w == 0 && rl == 0) st4(out + static_cast<size_t>(h) * value_dim + j0, o);
+}
+
 // One decode token of a GDN layer after its input projections, in one launch:
 // the front end (causal conv of kernel 4 + SiLU, Q/K L2 norm) and the
-// fused-gate recurrence. Key dim 128. Each wave is a wave of gdn_recurrent_v4<2>
-// -- (value head h, columns j0..j0+3), state rows L and L+64 in lane L -- that
-// first evaluates the front end for what it reads: the 256 q | k channels of
-// key head h % key_heads in gdn_frontend_k4<32>'s layout (lane L: channels
-// 4L..4L+3 of q for L < 32, of k for L >= 32; a 32-lane sum of squares per
-// head), moved to the recurrence's layout with lane permutes, and its 4 value
-// channels. So every value equals what gdn_frontend_rows writes and the
-// recurrence reads, bit for bit. Writes: the front end's output row y and the
-// new history (q | k channels of key head g by the wave h = g, j0 = 0; value
-// channels by the wave that reads them), the state and the output. hist_out
-// must not overlap hist_in: up to 64 waves read one key head's history while
-// one of them writes it.
+// fused-gate recurrence. Key dim 128, value_dim % kTileCols == 0. Each
+// workgroup is a workgroup of gdn_step_tile<128> -- (value head h, columns
+// cb * 32 ..), lane L of wave w holding columns j0 = cb * 32 + 4 (L / 8) .. + 3
+// and rows w * 32 + L % 8 + 8 r -- whose waves first evaluate the front end for
+// what they read: the 256 q | k channels of key head h % key_heads in
+// gdn_frontend_k4<32>'s layout (lane L: channels 4L..4L+3 of q for L < 32, of k
+// for L >= 32; a 32-lane sum of squares per head), moved to the recurrence's
+// layout with lane permutes, and each lane its 4 value channels. So every value
+// equals what gdn_frontend_rows writes and the recurrence reads, bit for bit.
+// Writes: the front end's output row y and the new history (q | k channels of
+// key head g by wave 0 of workgroup h = g, cb = 0; value channels by wave 0 of
+// the workgroup that reads them), the state and the output. hist_out must not
+// overlap hist_in: many waves read one key head's history while one of them
+// writes it. Grid: exactly value_heads * value_dim / kTileCols workgroups.
 __global__ __launch_bounds__(kBlock) void gdn_decode_fused(
         const float* __restrict__ x, const float* __restrict__ cw, const float* __restrict__ hin,
         float* __restrict__ hout, float* __restrict__ y, float* __restrict__ S, const float* __restrict__ beta_raw,
         const float* __restrict__ alpha_raw, const float* __restrict__ a, const float* __restrict__ dt,
-        float* __restrict__ out, int key_heads, int value_heads, int value_dim, float eps, float qscale) {
+        float* __restrict__ out, int key_heads, int value_dim, float eps, float qscale) {
     constexpr int DK = 128;
-    const int cblocks = value_dim >> 2;
-    const int wave = blockIdx.x * kWaves + wave_in_block();
-    if (wave >= value_heads * cblocks) return;  // wave-uniform; no barrier below
+    constexpr int RPL = DK / (kTileWaves * kTileLanes);
+    __shared__ float4 red[2 * kTileWaves * kTileGroups];
     const int lane = threadIdx.x & 63;
-    const int h = wave / cblocks;
-    const int j0 = 4 * (wave - h * cblocks);
+    const int w = wave_in_block();
+    const int cblocks = value_dim / kTileCols;
+    const int h = blockIdx.x / cblocks;
+    const int cb = blockIdx.x - h * cblocks;
+    const int cg = lane / kTileLanes, rl = lane % kTileLanes;
+    const int j0 = cb * kTileCols + 4 * cg;
     const int src = h % key_heads;
     const int kd = key_heads * DK;
+    const int r0 = w * (DK / kTileWaves) + rl;
     const bool is_q = lane < 32;
     const size_t c = static_cast<size_t>(is_q ? src * DK + 4 * lane : kd + src * DK + 4 * (lane - 32));
     const size_t cv = static_cast<size_t>(2 * kd + h * value_dim + j0);
-    float* Sh = S + static_cast<size_t>(h) * DK * value_dim + j0;
+    float* St = S + (static_cast<size_t>(h) * DK + r0) * value_dim + j0;
 
     // Every load issued before the first use: taps, history and input of the
-    // lane's q | k channels and of the wave's value channels, the gates, the
-    // state slice.
+    // lane's q | k channels and of its value channels, the gates, the state
+    // slice.
     const float4 w0 = ld4(cw + 4 * c), w1 = ld4(cw + 4 * c + 4), w2 = ld4(cw + 4 * c + 8), w3 = ld4(cw + 4 * c + 12);
     const float4 ha = ld4(hin + 3 * c), hb = ld4(hin + 3 * c + 4), hd = ld4(hin + 3 * c + 8);
     const float4 xv = ld4(x + c);
@@ -303,9 +437,9 @@ __global__ __launch_bounds__(kBlock) void gdn_decode_fused(
     const float4 va = ld4(hin + 3 * cv), vb = ld4(hin + 3 * cv + 4), vd = ld4(hin + 3 * cv + 8);
     const float4 vx = ld4(x + cv);
     const float br = beta_raw[h], ar = alpha_raw[h], ah = a[h], dth = dt[h];
-    float4 s[2];
+    float4 s[RPL];
 #pragma unroll
-    for (int r = 0; r < 2; ++r) s[r] = ld4_nt(Sh + static_cast<size_t>(lane + 64 * r) * value_dim);
+    for (int r = 0; r < RPL; ++r) s[r] = ld4_nt(St + static_cast<size_t>(kTileLanes * r) * value_dim);
 
     // q | k front end (gdn_frontend_k4<32>, one row)
     float4 h0, h1, h2;
@@ -325,68 +459,40 @@ __global__ __launch_bounds__(kBlock) void gdn_decode_fused(
     const float4 vv = silu4(make_float4(conv4(g0.x, g1.x, g2.x, vx.x, u0), conv4(g0.y, g1.y, g2.y, vx.y, u1),
                                         conv4(g0.z, g1.z, g2.z, vx.z, u2), conv4(g0.w, g1.w, g2.w, vx.w, u3)));
 
-    if (h == src && j0 == 0) {   // one wave per key head writes its q | k channels
+    if (h == src && cb == 0 && w == 0) {   // one wave per key head writes its q | k channels
         st4(y + c, f);
         st4(hout + 3 * c, make_float4(h1.x, h2.x, xv.x, h1.y));
         st4(hout + 3 * c + 4, make_float4(h2.y, xv.y, h1.z, h2.z));
         st4(hout + 3 * c + 8, make_float4(xv.z, h1.w, h2.w, xv.w));
     }
-    if (lane == 0) {
+    if (w == 0 && rl == 0) {   // each column group's value channels once
         st4(y + cv, vv);
         st4(hout + 3 * cv, make_float4(g1.x, g2.x, vx.x, g1.y));
         st4(hout + 3 * cv + 4, make_float4(g2.y, vx.y, g1.z, g2.z));
         st4(hout + 3 * cv + 8, make_float4(vx.z, g1.w, g2.w, vx.w));
     }
 
-    // Recurrence layout: lane L needs q, k of rows L and L + 64 -- channel i
-    // sits in lane i / 4 (q) or 32 + i / 4 (k), component i % 4 = L % 4.
+    // Recurrence layout: lane L needs q, k of rows i = r0 + 8 r -- channel i sits
+    // in lane i / 4 (q) or 32 + i / 4 (k), component i % 4 = L % 4 (r0 - L % 8
+    // and 8 r are multiples of 4).
     auto pick = [&](int from) {
         const float px = __shfl(f.x, from), py = __shfl(f.y, from), pz = __shfl(f.z, from), pw = __shfl(f.w, from);
         const int k4 = lane & 3;
         return k4 == 0 ? px : k4 == 1 ? py : k4 == 2 ? pz : pw;
     };
-    const float qr[2] = {pick(lane >> 2), pick(16 + (lane >> 2))};
-    const float kr[2] = {pick(32 + (lane >> 2)), pick(48 + (lane >> 2))};
+    float qr[RPL], kr[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+        const int from = (r0 + kTileLanes * r) >> 2;
+        qr[r] = pick(from);
+        kr[r] = pick(32 + from);
+    }
 
-    // gdn_recurrent_v4<2>, one token, gates from the raw projections
+    // gdn_step_tile<128>, gates from the raw projections
     const float d = gate_decay(ah, ar, dth);
-    float4 m = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        s[r].x *= d;
-        s[r].y *= d;
-        s[r].z *= d;
-        s[r].w *= d;
-        m.x = __builtin_fmaf(kr[r], s[r].x, m.x);
-        m.y = __builtin_fmaf(kr[r], s[r].y, m.y);
-        m.z = __builtin_fmaf(kr[r], s[r].z, m.z);
-        m.w = __builtin_fmaf(kr[r], s[r].w, m.w);
-    }
-    m.x = group_sum<64>(m.x);
-    m.y = group_sum<64>(m.y);
-    m.z = group_sum<64>(m.z);
-    m.w = group_sum<64>(m.w);
     const float b = gate_beta(br);
-    const float4 dl = make_float4((vv.x - m.x) * b, (vv.y - m.y) * b, (vv.z - m.z) * b, (vv.w - m.w) * b);
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        s[r].x = __builtin_fmaf(kr[r], dl.x, s[r].x);
-        s[r].y = __builtin_fmaf(kr[r], dl.y, s[r].y);
-        s[r].z = __builtin_fmaf(kr[r], dl.z, s[r].z);
-        s[r].w = __builtin_fmaf(kr[r], dl.w, s[r].w);
-        o.x = __builtin_fmaf(qr[r], s[r].x, o.x);
-        o.y = __builtin_fmaf(qr[r], s[r].y, o.y);
-        o.z = __builtin_fmaf(qr[r], s[r].z, o.z);
-        o.w = __builtin_fmaf(qr[r], s[r].w, o.w);
-    }
-    o.x = group_sum<64>(o.x);
-    o.y = group_sum<64>(o.y);
-    o.z = group_sum<64>(o.z);
-    o.w = group_sum<64>(o.w);
-    if (lane == 0) st4(out + static_cast<size_t>(h) * value_dim + j0, o);
-#pragma unroll
-    for (int r = 0; r < 2; ++r) st4_nt(Sh + static_cast<size_t>(lane + 64 * r) * value_dim, s[r]);
+    const float4 o = tile_step<RPL>(s, kr, qr, vv, b, d, St, value_dim, red, w, cg, rl);
+    if (w == 0 && rl == 0) st4(out + static_cast<size_t>(h) * value_dim + j0, o);
 }
 
 // Any key / value dim (value_dim <= 256): one block per value head, thread j
@@ -430,8 +536,15 @@ int launch_recurrent(float* state, const float* q, const float* k, const float* 
                      RawGates rg = RawGates{nullptr, nullptr}) {
     const bool vec = value_dim % 4 == 0 && (key_dim == 64 || key_dim == 128) && aligned16(q) && aligned16(k) &&
                      qkv_stride % 4 == 0;
-    if (vec && rows == 1 && aligned16(state) && aligned16(v) && aligned16(out)) {
-        // One token: the state traffic dominates, read as float4 rows.
+    if (vec && rows == 1 && value_dim % kTileCols == 0 && aligned16(state) && aligned16(v) && aligned16(out)) {
+        // One token: the state traffic dominates, read as whole 128-byte lines.
+        const unsigned grid = static_cast<unsigned>(value_heads * (value_dim / kTileCols));
+        if (key_dim == 64)
+            gdn_step_tile<64><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, key_heads, value_dim, rg);
+        else
+            gdn_step_tile<128><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, key_heads, value_dim, rg);
+    } else if (vec && rows == 1 && aligned16(state) && aligned16(v) && aligned16(out)) {
+        // One token, value_dim % 32 != 0: 4-column float4 slices.
         const unsigned grid = blocks_for(value_heads * (value_dim / 4), kWaves);
         if (key_dim == 64)
             gdn_recurrent_v4<1><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
@@ -528,7 +641,8 @@ int qwen_gdn_decode_step(const float* x, const float* conv_weight, const float* 
     const auto lo = reinterpret_cast<uintptr_t>(hist_in), hi = lo + static_cast<uintptr_t>(C) * (kernel - 1) * 4;
     const auto olo = reinterpret_cast<uintptr_t>(hist_out), ohi = olo + static_cast<uintptr_t>(C) * (kernel - 1) * 4;
     const bool disjoint = ohi <= lo || hi <= olo;
-    const bool fused = disjoint && kernel == 4 && key_dim == 128 && value_dim % 4 == 0 && value_heads % key_heads == 0 &&
+    const bool fused = disjoint && kernel == 4 && key_dim == 128 && value_dim % kTileCols == 0 &&
+                       value_heads % key_heads == 0 &&
                        aligned16(x) && aligned16(conv_weight) && aligned16(hist_in) && aligned16(hist_out) &&
                        aligned16(y) && aligned16(state) && aligned16(out);
     if (!fused) {   // the two calls it fuses (the front end may update the history in place)
@@ -539,10 +653,10 @@ int qwen_gdn_decode_step(const float* x, const float* conv_weight, const float* 
         return qwen_gdn_gated_recurrent_rows(state, y, y + kd, y + 2 * kd, beta_raw, alpha_raw, a, dt_bias, out, 1,
                                              key_heads, value_heads, key_dim, value_dim, 0, 0, stream);
     }
-    const unsigned grid = blocks_for(static_cast<int64_t>(value_heads) * (value_dim / 4), kWaves);
+    const unsigned grid = static_cast<unsigned>(value_heads * (value_dim / kTileCols));
     gdn_decode_fused<<<grid, kBlock, 0, as_stream(stream)>>>(x, conv_weight, hist_in, hist_out, y, state, beta_raw,
-                                                             alpha_raw, a, dt_bias, out, key_heads, value_heads,
-                                                             value_dim, eps, host_rsqrt(key_dim));
+                                                             alpha_raw, a, dt_bias, out, key_heads, value_dim, eps,
+                                                             host_rsqrt(key_dim));
     return check_launch("gdn_decode_step");
 }
 

@@ -479,10 +479,13 @@ def test_gdn_recurrent_reference_fixture():
 
 
 @pytest.mark.parametrize("kh,vh,dk,dv,rows", [(16, 32, 128, 128, 1), (16, 32, 128, 128, 37), (4, 8, 64, 64, 9),
-                                              (2, 4, 96, 100, 5), (3, 6, 128, 256, 3)])
+                                              (2, 4, 96, 100, 5), (3, 6, 128, 256, 3), (4, 8, 64, 64, 1),
+                                              (3, 6, 128, 256, 1), (3, 6, 128, 36, 1), (2, 4, 64, 100, 1)])
 def test_gdn_recurrent_rows(oracle, kh, vh, dk, dv, rows):
     """Qwen3.5 GDN shape (16 key / 32 value heads of 128), a token count that is not a
-    multiple of the 4-deep prefetch, key dim 64, and generic shapes (dk 96, dv 100 / 256)."""
+    multiple of the 4-deep prefetch, key dim 64, and generic shapes (dk 96, dv 100 / 256);
+    one token on the 32-column tile (key dim 64 / 128, dv 64 / 256) and on the
+    4-column slices (dv 36 / 100)."""
     r = rng(kh * 1000 + rows)
     qkv, b, alpha, a, dt, state = _gdn_inputs(r, rows, kh, vh, dk, dv, extra=8)
     beta, decay = oracle.gdn_gate_values_rows(b, alpha, a, dt)
@@ -625,13 +628,14 @@ def test_matmul_dispatch_multi_rejects_unpaired_split():
 
 
 @pytest.mark.parametrize("kh,vh,dk,dv,alias", [(16, 32, 128, 128, False), (4, 8, 128, 64, False),
-                                               (16, 32, 128, 128, True), (2, 4, 64, 32, False)])
+                                               (16, 32, 128, 128, True), (2, 4, 64, 32, False),
+                                               (2, 4, 128, 36, False), (2, 6, 128, 256, False)])
 def test_gdn_decode_step_equals_frontend_then_gated_recurrence(kh, vh, dk, dv, alias):
     """The one-launch decode step (front end + fused-gate recurrence) gives the
     bits of gdn_frontend_rows (one row) followed by gdn_gated_recurrent_rows:
     conv output, new history, state and output, over three tokens with the
-    history carried; an in-place history (alias) and key dim 64 take the two
-    calls inside the same entry point."""
+    history carried; an in-place history (alias), key dim 64 and a value dim
+    that is not a multiple of 32 take the two calls inside the same entry point."""
     r = rng(kh * vh + dk + dv + alias)
     C = 2 * kh * dk + vh * dv
     cw = dev((0.5 * r.standard_normal((C, 4))).astype(F32))
@@ -660,7 +664,7 @@ def test_gdn_decode_step_equals_frontend_then_gated_recurrence(kh, vh, dk, dv, a
 
 
 @pytest.mark.parametrize("rows,kh,vh,dk,dv", [(1, 16, 32, 128, 128), (1, 4, 8, 64, 64), (37, 16, 32, 128, 128),
-                                               (5, 2, 4, 100, 48)])
+                                               (5, 2, 4, 100, 48), (1, 3, 6, 128, 36)])
 def test_gdn_gated_recurrent_equals_gates_then_recurrence(rows, kh, vh, dk, dv):
     """The fused-gate recurrence (qwen_gdn_gated_recurrent_rows) gives the bits of
     gdn_gate_values_rows followed by gdn_recurrent_rows on every kernel path (one
