@@ -13,8 +13,9 @@
 //         MFMA accumulator sums a whole 256-element block across its eight
 //         scale groups, and per block
 //         y += d * P_block - dmin * sum_g m_g S_g        (P = sum (q sc) v)
-//         with S_g the group sums of v; the min terms are one fp32 MFMA
-//         product per block ([tokens x groups] x [groups x rows]).
+//         with S_g the group sums of v; the min terms are one fp16 MFMA per
+//         tile and block (v_mfma_f32_16x16x16_f16, k = 8 groups x 2 parts):
+//         m_g exact, S_g 2^-5 split into two fp16 parts like x (22 bits).
 //   Q6_K: B = q - 32 (exact); the signed 8-bit scales do not fit in the fp16
 //         operand, so per 16-element group y += (d sc) P_g (one FMA).
 // The result is scaled back by 2^-e (exact). Products of fp16 values are exact
@@ -45,6 +46,7 @@ namespace {
 
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
@@ -264,9 +266,10 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q4k(const GemmJobs jobs, c
     for (int rt = 0; rt < 4; ++rt)
         wrow[rt] = w + (ub0 + static_cast<uint64_t>(min(r0 + 16 * rt + lr, M - 1)) * nb) * 144;
     // the min-term A operands read S of tokens 16 tt + lr, groups 4 j + lk
+    // the min-term A operands read S of tokens 16 tt + lr, groups 2 lk, 2 lk + 1
     const float* srow[4];
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) srow[tt] = sx + static_cast<size_t>(min(t0 + 16 * tt + lr, T - 1)) * nst + lk;
+    for (int tt = 0; tt < 4; ++tt) srow[tt] = sx + static_cast<size_t>(min(t0 + 16 * tt + lr, T - 1)) * nst + 2 * lk;
 
     f32x4_t acc[4][4], C[4][4];
 #pragma unroll
@@ -283,11 +286,20 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q4k(const GemmJobs jobs, c
     }
     store_x(load_x(xsrc), xs[0], tok, part);
     __syncthreads();
+    float sg[2][4];   // the block's group sums S (loaded at its first stage)
 
     for (int g = 0; g < nst; ++g) {
         const int sb = g & 7, cur = g & 1;
         const int gn = g + 1;
         const bool more = gn < nst;
+        if (sb == 0) {
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const float2 v = *reinterpret_cast<const float2*>(srow[tt] + g);
+                sg[0][tt] = v.x;
+                sg[1][tt] = v.y;
+            }
+        }
         // this stage's B operands; then the next stage's quants and x are loaded
         // into the same registers, in flight during the products
         f16x8_t B[4];
@@ -301,23 +313,10 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q4k(const GemmJobs jobs, c
             q4_operand((qb[rt].y >> shn) & 0x0f0f0f0fu, sc, e[2], e[3]);
             __builtin_memcpy(&B[rt], e, 16);
         }
-        float dsc[4], dmn[2][4], smin[2][4];
+        uint4 hdr_e[4];   // the block's header, kept for its epilogue
         if (sb == 7) {
-            // block epilogue operands (before the header is replaced)
 #pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
-                dsc[rt] = half_bits(hdr[rt].x & 0xffffu);
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    uint32_t sc, mm;
-                    q4k_scale_min(hdr[rt], 4 * j + lk, sc, mm);
-                    dmn[j][rt] = half_bits(hdr[rt].x >> 16) * static_cast<float>(mm);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int tt = 0; tt < 4; ++tt) smin[j][tt] = -srow[tt][(g & ~7) + 4 * j];
+            for (int rt = 0; rt < 4; ++rt) hdr_e[rt] = hdr[rt];
         }
         XRegs xn;
         if (more) {
@@ -345,18 +344,40 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q4k(const GemmJobs jobs, c
             for (int rt = 0; rt < 4; ++rt) C[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1], B[rt], C[tt][rt], 0, 0, 0);
         }
         if (sb == 7) {
-            // acc += d P_block; acc -= sum_g (dmin m_g) S_g as [16 tokens x 4 groups] x
-            // [4 groups x 16 rows] fp32 products, twice
+            // acc += d P_block; then the block's min terms P_min = sum_g m_g S_g 2^-5
+            // as one [16 tokens x 16] x [16 x 16 rows] fp16 product per tile, k =
+            // (group 2 lk + i / 2, part i % 2) in lane (lr, lk): the two fp16 parts
+            // of S 2^-5 (|S| < 2^20) against m_g twice; acc -= dmin 2^5 P_min.
+            float dsc[4], dmn5[4];
+            f16x4_t Bm[4], As[4];
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt) {
+                uint32_t sc, m0, m1;
+                q4k_scale_min(hdr_e[rt], 2 * lk, sc, m0);
+                q4k_scale_min(hdr_e[rt], 2 * lk + 1, sc, m1);
+                const _Float16 a0 = static_cast<_Float16>(static_cast<float>(m0));
+                const _Float16 a1 = static_cast<_Float16>(static_cast<float>(m1));
+                Bm[rt] = f16x4_t{a0, a0, a1, a1};
+                dsc[rt] = half_bits(hdr_e[rt].x & 0xffffu);
+                dmn5[rt] = -32.0f * half_bits(hdr_e[rt].x >> 16);
+            }
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const float s0 = sg[0][tt] * 0.03125f, s1 = sg[1][tt] * 0.03125f;
+                const _Float16 h0 = static_cast<_Float16>(s0), h1 = static_cast<_Float16>(s1);
+                As[tt] = f16x4_t{h0, static_cast<_Float16>(s0 - static_cast<float>(h0)), h1,
+                                 static_cast<_Float16>(s1 - static_cast<float>(h1))};
+            }
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
                 for (int rt = 0; rt < 4; ++rt) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc[tt][rt][r] = __builtin_fmaf(dsc[rt], C[tt][rt][r], acc[tt][rt][r]);
-                    C[tt][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                    C[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x16f16(As[tt], Bm[rt], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        acc[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x4f32(smin[j][tt], dmn[j][rt], acc[tt][rt], 0, 0, 0);
+                    for (int r = 0; r < 4; ++r) acc[tt][rt][r] = __builtin_fmaf(dmn5[rt], C[tt][rt][r], acc[tt][rt][r]);
+                    C[tt][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
                 }
         }
         if (more) store_x(xn, xs[cur ^ 1], tok, part);
