@@ -11,9 +11,13 @@
       scaled to bytes by the factor that makes the reference copy of COPY_BYTES
       read + COPY_BYTES written read exactly its known traffic, next to each
       kernel's algorithmic bytes
+  python -m qwen35_hip.rocprof_summary counters COUNTERS.csv [...] [--match SYM] [--stages N]
+      mean per dispatch of every counter of the --pmc runs for the kernels whose
+      symbol contains SYM; per wave and K stage with SQ_WAVES; the MFMA-busy
+      share (SQ_VALU_MFMA_BUSY_CYCLES over 1024 SIMDs x SQ_BUSY_CYCLES / 32 SEs)
 
-Kernel symbols are mapped to the bench.py kernel names; the reference copy is
-"copy16" (libqwen35_benchutil.so).
+Kernel symbols are mapped to the bench.py kernel names; the reference copies are
+"copy16" and "copy_form" (libqwen35_benchutil.so).
 """
 
 from __future__ import annotations
@@ -41,6 +45,7 @@ NAMES = [
     ("rmsnorm_rows_split", "rmsnorm"),
     ("rmsnorm_rows_v4", "rmsnorm"),
     ("copy16", "copy"),
+    ("copy_form", "copy"),
     # next rows (kernel symbols; several bench shapes can share one instantiation)
     ("gemv_mfma<14, 2>", "gemv Q6_K MFMA, 2-block k-slices (LM head)"),
     ("gemv_mfma<12, 2>", "gemv Q4_K MFMA, 2-block k-slices"),
@@ -50,7 +55,9 @@ NAMES = [
     ("gemv_kquant_multi", "gemv per-row, several matrices of one x (matmul_dispatch_multi)"),
     ("gemv_kquant_gate_up", "gemv per-row, routed experts' gate + up (moe_expert_gate_up)"),
     ("moe_down_combine_kernel", "moe_down_combine (routed + shared down, combine)"),
-    ("gdn_recurrent_v4", "gdn_recurrent step (decode)"),
+    ("gdn_step_tile", "gdn_recurrent step (decode, 32-column tiles)"),
+    ("gdn_recurrent_v4", "gdn_recurrent step (decode, 4-column slices)"),
+    ("gdn_decode_fused", "gdn_decode_step (front end + gated step, one launch)"),
     ("gdn_recurrent_g", "gdn_recurrent token loop (4096 tokens)"),
     ("gdn_chunk_prep", "gdn_recurrent chunked: per-chunk prep"),
     ("gdn_chunk_state", "gdn_recurrent chunked: state walk"),
@@ -155,6 +162,43 @@ def traffic(fetch_csv: str, write_csv: str, copy_bytes: int) -> dict:
     return out
 
 
+# SIMDs and shader engines of an MI355X (256 CUs x 4 SIMDs, 8 XCDs x 4 SEs):
+# SQ_VALU_MFMA_BUSY_CYCLES sums over SIMDs, SQ_BUSY_CYCLES over shader engines.
+MI355X_SIMDS = 1024
+MI355X_SES = 32
+
+
+def counters(paths: list[str], match: str, stages: int) -> dict:
+    """Mean per dispatch of every counter in the given counter_collection CSVs, for the
+    kernels whose symbol contains `match`; with SQ_WAVES, per wave and per K stage
+    (`stages` stages per wave) figures; with SQ_VALU_MFMA_BUSY_CYCLES and SQ_BUSY_CYCLES,
+    the MFMA-busy share of the kernel's SIMD cycles."""
+    acc = defaultdict(lambda: defaultdict(list))
+    for path in paths:
+        for r in csv.DictReader(open(path)):
+            sym = r["Kernel_Name"]
+            if match not in sym:
+                continue
+            name = kernel_name(sym) or sym[:60]
+            acc[name][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    out = {}
+    for name, cs in acc.items():
+        m = {c: sum(v) / len(v) for c, v in cs.items()}
+        d = {"mean_per_dispatch": m, "dispatches": {c: len(v) for c, v in cs.items()}}
+        waves = m.get("SQ_WAVES")
+        if waves:
+            d["per_wave_stage"] = {c: m[c] / waves / stages for c in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS",
+                                                                      "SQ_VALU_MFMA_BUSY_CYCLES") if c in m}
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in m and "SQ_BUSY_CYCLES" in m:
+            cycles = m["SQ_BUSY_CYCLES"] / MI355X_SES
+            d["kernel_cycles"] = cycles
+            d["mfma_busy"] = m["SQ_VALU_MFMA_BUSY_CYCLES"] / (MI355X_SIMDS * cycles)
+        if "SQ_WAIT_ANY" in m and "SQ_WAVE_CYCLES" in m:
+            d["wait_share"] = m["SQ_WAIT_ANY"] / m["SQ_WAVE_CYCLES"]
+        out[name] = d
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -168,7 +212,24 @@ def main(argv=None) -> int:
     b.add_argument("write_csv")
     b.add_argument("copy_bytes", type=int)
     b.add_argument("--json", default="")
+    k = sub.add_parser("counters")
+    k.add_argument("csv", nargs="+")
+    k.add_argument("--match", default="gemm_")
+    k.add_argument("--stages", type=int, default=64, help="K stages per wave (K / 32)")
     args = ap.parse_args(argv)
+    if args.cmd == "counters":
+        for name, d in counters(args.csv, args.match, args.stages).items():
+            print(name)
+            for c, v in sorted(d["mean_per_dispatch"].items()):
+                print(f"   {c:28s} {v:16.6g}   ({d['dispatches'][c]} dispatches)")
+            for c, v in d.get("per_wave_stage", {}).items():
+                print(f"   per wave and stage: {c:28s} {v:10.1f}")
+            if "mfma_busy" in d:
+                print(f"   kernel cycles (SQ_BUSY_CYCLES / {MI355X_SES} SEs): {d['kernel_cycles']:.0f}; MFMA busy "
+                      f"{100 * d['mfma_busy']:.1f}% of {MI355X_SIMDS} SIMDs")
+            if "wait_share" in d:
+                print(f"   SQ_WAIT_ANY / SQ_WAVE_CYCLES: {100 * d['wait_share']:.1f}%")
+        return 0
     if args.cmd == "stats":
         t = stats(args.csv)
         print(f"{'kernel':44s} {'calls':>6s} {'avg us':>9s} {'min us':>9s} {'max us':>9s} {'GB/s (avg)':>11s}")
