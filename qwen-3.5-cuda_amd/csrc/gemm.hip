@@ -265,7 +265,6 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q4k(const GemmJobs jobs, c
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
         wrow[rt] = w + (ub0 + static_cast<uint64_t>(min(r0 + 16 * rt + lr, M - 1)) * nb) * 144;
-    // the min-term A operands read S of tokens 16 tt + lr, groups 4 j + lk
     // the min-term A operands read S of tokens 16 tt + lr, groups 2 lk, 2 lk + 1
     const float* srow[4];
 #pragma unroll

@@ -1391,6 +1391,31 @@ def test_matmul_rows_prefill_shapes(oracle, kind, T, M, K):
         assert_f32_close(got[i], gv, group=M, what=f"{kind} token {i} vs matmul_dispatch")
 
 
+@pytest.mark.parametrize("kind", ["Q4_K", "Q6_K"])
+def test_matmul_rows_extreme_block_scales(oracle, kind):
+    """Block scales across fp16's range (zero, subnormal, 2^-14 .. 65504 for d and,
+    in Q4_K, dmin) mixed within each row: the matrix-core path (its exact fp16
+    operands, the min terms' two-part group sums, the per-block d and dmin
+    products) against the oracle's GEMV, within the fp32 bar."""
+    T, M, K = 64, 256, 2048
+    t = ops.GGML_TYPES[kind]
+    r = rng(91 + t)
+    scales = np.array([0.0, 2.0 ** -24, 2.0 ** -20, 2.0 ** -14, 1e-3, 0.5, 3.0, 1000.0, 65504.0], dtype=np.float16)
+    if kind == "Q4_K":
+        w = synth.q4k_table(M, K, seed_tensor=3).reshape(-1, 144).copy()
+        w[:, 0:2] = r.choice(scales, size=len(w)).view(np.uint8).reshape(-1, 2)
+        w[:, 2:4] = r.choice(scales, size=len(w)).view(np.uint8).reshape(-1, 2)
+    else:
+        w = synth.q6k_table(M, K, seed_tensor=3).reshape(-1, 210).copy()
+        w[:, 208:210] = r.choice(scales, size=len(w)).view(np.uint8).reshape(-1, 2)
+    w = w.reshape(-1)
+    x = r.standard_normal((T, K)).astype(F32)
+    got = host(ops.matmul_rows(dev(w), t, M * K, dev(x), M, K))
+    assert np.isfinite(got).all()
+    for i in (0, 1, 17, 40, T - 1):
+        assert_f32_close(got[i], oracle.gemv(w, t, x[i], M, K, threads=THREADS), group=M, what=f"{kind} token {i}")
+
+
 @pytest.mark.parametrize("T", [16, 300])
 def test_matmul_rows_multi_equals_single_calls(T):
     """Several matrices of one x in one call (one prep, one GEMM launch per K-quant
