@@ -28,14 +28,19 @@
 // stores x in that order within each 4 consecutive elements (0, 2, 1, 3);
 // A and B then agree slot by slot.
 //
-// Work: a workgroup owns 64 tokens x 256 weight rows; wave w owns rows
-// 64w .. 64w+63 for all 64 tokens. Per 32-element stage the workgroup copies
-// the two fp16 parts of x[64 tokens][32] to LDS (double-buffered, one barrier
-// per stage), with the next stage's x and quants loaded while the current one
-// is computed. Q4_K: 16 x 16 tiles on v_mfma_f32_16x16x32_f16. Q6_K: 32 x 32
-// tiles on v_mfma_f32_32x32x16_f16 (K = one 16-element scale group).
+// Work, per 32-element stage (one barrier per stage). Q4_K: a workgroup of 8
+// waves owns 128 tokens x 256 weight rows, its operands arrive through an LDS
+// ring three stages ahead and the next stage's B operands are decoded while the
+// current stage's products run (16 x 16 tiles on v_mfma_f32_16x16x32_f16; the
+// kernel's own comment has the details). Q6_K: a workgroup of 4 waves owns 64
+// tokens x 256 weight rows, wave w rows 64w .. 64w+63; the two fp16 parts of
+// x[64 tokens][32] are copied to LDS (double-buffered) with the next stage's x
+// and quants loaded while the current one is computed; 32 x 32 tiles on
+// v_mfma_f32_32x32x16_f16 (K = one 16-element scale group).
 #include <algorithm>
 #include <cfloat>
+#include <type_traits>
+#include <utility>
 
 #include "capi_common.hpp"
 #include "device_common.hpp"
@@ -243,151 +248,267 @@ __device__ __forceinline__ void q6_operand(uint32_t q, uint32_t& w02, uint32_t& 
 // sub-block i/32 (src/cuda/matmul_q4.cu:76-96). Lane (lr, lk) of stage sb
 // takes elements 32 sb + 8 lk .. +7: qs bytes 16 + 32(sb/2) + 8 lk .. +7,
 // nibble sb%2.
-__global__ __launch_bounds__(kGemmBlock, 2) void gemm_q4k(const GemmJobs jobs, const int* __restrict__ ex,
-                                                          const float* __restrict__ sx,
-                                                          const uint16_t* __restrict__ xp,
-                                                          const float* __restrict__ x, int T, int K) {
-    __shared__ __align__(16) XStage xs[2];
+//
+// A workgroup (8 waves, one per CU) owns 128 tokens x 256 weight rows; wave w
+// owns rows 64 (w % 4) .. +63 for tokens 64 (w / 4) .. +63. Its operands come
+// through an LDS ring filled by global_load_lds_dwordx4 (no VGPRs, no LDS store
+// instructions) kQ4Dist stages ahead: x per stage, the quant bytes per pair of
+// stages (both nibbles), the headers and group sums per block. While stage g's
+// products run, waves w and w + 4 (same rows) each decode two of the four row
+// tiles of stage g + 1's B operands into an LDS slot that both read after the
+// stage's barrier, so the decode's VALU work hides under the matrix cores.
+constexpr int kQ4Waves = 8;
+constexpr int kQ4Block = kQ4Waves * kWave;
+constexpr int kQ4T = 128;                   // tokens per workgroup
+constexpr int kQ4Dist = 3;                  // ring distance (stages)
+constexpr int kQ4XSlots = 4;                // x slots (one stage each)
+constexpr int kQ4QSlots = 2;                // quant slots (one pair of stages each)
+typedef uint16_t Q4XSlot[2][kQ4T][32];      // one stage of x: [fp16 part][token][k], 16-byte chunks swizzled
+typedef uint8_t Q4QSlot[kGR][32];           // one pair's quant bytes
+typedef uint8_t Q4HSlot[kGR][16];           // one block's headers (d, dmin, scales)
+typedef float Q4SSlot[kQ4T][8];             // one block's group sums
+typedef f16x8_t Q4BSlot[4][4][kWave];       // B operands: [row group][row tile][lane]
+
+template <int S>
+using IC = std::integral_constant<int, S>;
+
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(IC<I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// A value the compiler may not fold into its users (keeps v_fmac_f32 from
+// becoming v_fma_mix_f32, which issues at half the rate).
+__device__ __forceinline__ float opaque(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// 16 bytes per lane global -> LDS (m0 + 16 lane). As inline assembly the
+// compiler neither counts these loads nor waits for them; the kernel waits on
+// its own vmcnt (only stricter for the compiler's own loads, of which the main
+// loop has none).
+__device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// This wave's loads in ring group j: 2 (x) + 1 (a pair's quant bytes, even j) +
+// 2 (headers and group sums, a block's first stage).
+__host__ __device__ constexpr int q4_group_loads(int j) {
+    return 2 + ((j & 1) == 0 ? 1 : 0) + ((j & 7) == 0 ? 2 : 0);
+}
+
+__global__ __launch_bounds__(kQ4Block, 1) void gemm_q4k(const GemmJobs jobs, const int* __restrict__ ex,
+                                                         const float* __restrict__ sx, const uint16_t* __restrict__ xp,
+                                                         const float* __restrict__ x, int T, int K) {
+    __shared__ __align__(16) Q4XSlot xr[kQ4XSlots];
+    __shared__ __align__(16) Q4QSlot qr[kQ4QSlots];
+    __shared__ __align__(16) Q4HSlot hr[2];
+    __shared__ __align__(16) Q4SSlot sr[2];
+    __shared__ __align__(16) Q4BSlot bs[2];
     const GemmJob job = gemm_job(jobs);
     const uint8_t* __restrict__ w = job.w;
     float* __restrict__ y = job.y;
     const int M = job.M;
     const uint64_t ub0 = job.ub0;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int t0 = blockIdx.y * kGT;
-    const int r0 = job.mb * kGR + wv * 64;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+    const int rg = wv & 3, th = wv >> 2;                       // row group, token half
+    const int t0w = blockIdx.y * kQ4T;                         // the workgroup's first token
+    const int tw = t0w + 64 * th;                              // this wave's first token
+    const int rw0 = job.mb * kGR;                              // the workgroup's first row
+    const int r0 = rw0 + 64 * rg;                              // this wave's first row
     const int nb = K >> 8, nst = K >> 5;
-    const int tok = tid >> 2, part = tid & 3;
-    const uint16_t* xsrc = xp + static_cast<size_t>(min(t0 + tok, T - 1)) * nst * 64 + 32 * (part >> 1) +
-                           16 * (part & 1);
     const int lr = lane & 15, lk = lane >> 4;
-    const uint8_t* wrow[4];
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-        wrow[rt] = w + (ub0 + static_cast<uint64_t>(min(r0 + 16 * rt + lr, M - 1)) * nb) * 144;
-    // the min-term A operands read S of tokens 16 tt + lr, groups 2 lk, 2 lk + 1
-    const float* srow[4];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) srow[tt] = sx + static_cast<size_t>(min(t0 + 16 * tt + lr, T - 1)) * nst + 2 * lk;
+    const uint8_t* wbase = w + ub0 * 144;
+    const uint8_t* xpb = reinterpret_cast<const uint8_t*>(xp);
+    // Ring loads of a wave (byte offsets; stage and block offsets go into the
+    // scalar base). x: part wv / 4, tokens 32 (wv % 4) + 16 i + lane / 4 (i < 2);
+    // the lane at chunk c of its token's 64 bytes loads chunk c ^ ((token / 4) % 4),
+    // which spreads the A reads over the LDS banks. Quant bytes: rows 32 wv + lane / 2.
+    // Headers: rows 64 (wv % 4) + lane; group sums: tokens 32 (wv % 4) + lane / 2
+    // (waves 4-7 repeat 0-3: the same bytes to the same place).
+    const int xtk0 = 32 * (wv & 3);
+    auto xoff = [&](int i) {
+        const int tk = xtk0 + 16 * i + (lane >> 2);
+        const int ch = (lane & 3) ^ ((tk >> 2) & 3);
+        return 2u * (static_cast<uint32_t>(min(t0w + tk, T - 1)) * static_cast<uint32_t>(nst) * 64u + 32u * (wv >> 2) + 8u * ch);
+    };
+    const uint32_t qo = static_cast<uint32_t>(min(rw0 + 32 * wv + (lane >> 1), M - 1)) * static_cast<uint32_t>(nb) * 144u + 16u +
+                        16u * (lane & 1);
+    const uint32_t ho = static_cast<uint32_t>(min(r0 + lane, M - 1)) * static_cast<uint32_t>(nb) * 144u;
+    const uint32_t so = 4u * (static_cast<uint32_t>(min(t0w + 32 * rg + (lane >> 1), T - 1)) * static_cast<uint32_t>(nst) +
+                              4u * (lane & 1));
+    auto lds_addr = [](const void* l) {
+        return __builtin_amdgcn_readfirstlane(
+            static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const void __attribute__((address_space(3)))*)(l))));
+    };
+    const uint32_t xr_a = lds_addr(&xr[0][0][0][0]), qr_a = lds_addr(&qr[0][0][0]), hr_a = lds_addr(&hr[0][0][0]),
+                   sr_a = lds_addr(&sr[0][0][0]);
+    // ring group gs, in 4 parts: x (2 halves), the pair's quant bytes (even gs),
+    // the block's headers and group sums (its first stage)
+    auto issue_part = [&](int gs, int part) {
+        if (part < 2) {
+            dma16(xoff(part), xpb + static_cast<size_t>(gs) * 128,
+                  xr_a + static_cast<uint32_t>(gs % kQ4XSlots) * sizeof(Q4XSlot) + ((wv >> 2) * kQ4T + xtk0 + 16 * part) * 64u);
+        } else if (part == 2) {
+            if ((gs & 1) == 0)
+                dma16(qo, wbase + static_cast<size_t>(gs >> 3) * 144 + 32 * ((gs & 7) >> 1),
+                      qr_a + static_cast<uint32_t>((gs >> 1) % kQ4QSlots) * sizeof(Q4QSlot) + 32u * wv * 32u);
+        } else if ((gs & 7) == 0) {
+            const uint32_t hb = (gs >> 3) & 1;
+            dma16(ho, wbase + static_cast<size_t>(gs >> 3) * 144, hr_a + hb * sizeof(Q4HSlot) + 64u * rg * 16u);
+            dma16(so, sx + gs, sr_a + hb * sizeof(Q4SSlot) + 32u * rg * 32u);
+        }
+    };
+    // B operand of row tile rt of stage gs (scale group SB of its block)
+    auto decode_rt = [&](auto sbI, int gs, int rt) {
+        constexpr int SB = decltype(sbI)::value;
+        const int qs = (gs >> 1) % kQ4QSlots, hb = (gs >> 3) & 1;
+        const uint32_t* hw = reinterpret_cast<const uint32_t*>(&hr[hb][64 * rg + 16 * rt + lr][0]);
+        uint32_t sc;   // scale_min_k4 (src/cuda/matmul_q4.cu:18-26), scale part
+        if constexpr (SB < 4)
+            sc = (hw[1] >> (8 * SB)) & 63u;
+        else
+            sc = ((hw[3] >> (8 * (SB - 4))) & 15u) | (((hw[1] >> (8 * (SB - 4) + 6)) & 3u) << 4);
+        const uint2 qb = *reinterpret_cast<const uint2*>(&qr[qs][64 * rg + 16 * rt + lr][8 * lk]);
+        const uint32_t n0 = ((SB & 1) ? (qb.x >> 4) : qb.x) & 0x0f0f0f0fu;
+        const uint32_t n1 = ((SB & 1) ? (qb.y >> 4) : qb.y) & 0x0f0f0f0fu;
+        uint32_t e[4];
+        q4_operand(n0, sc, e[0], e[1]);
+        q4_operand(n1, sc, e[2], e[3]);
+        f16x8_t r;
+        __builtin_memcpy(&r, e, 16);
+        return r;
+    };
+    auto wait_ring = [](int n) {   // at most n of this wave's ring loads in flight
+        switch (n) {
+            case 2: wait_vm<2>(); break;
+            case 3: wait_vm<3>(); break;
+            case 5: wait_vm<5>(); break;
+            default: wait_vm<0>(); break;
+        }
+    };
+    auto barrier = []() {   // LDS stores (the B slot) complete; the ring's loads stay in flight
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
 
     f32x4_t acc[4][4], C[4][4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) acc[tt][rt] = C[tt][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int rt = 0; rt < 4; ++rt) acc[tt][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    uint4 hdr[4];
-    uint2 qb[4];
+    // groups 0 .. kQ4Dist - 1 (nst >= 8); groups 0 and 1 complete
+    {
+        int pend = 0;
+        for (int gs = 0; gs < kQ4Dist; ++gs) {
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-        hdr[rt] = ld16(wrow[rt]);
-        qb[rt] = *reinterpret_cast<const uint2*>(wrow[rt] + 16 + 8 * lk);
+            for (int part = 0; part < 4; ++part) issue_part(gs, part);
+            if (gs >= 2) pend += q4_group_loads(gs);
+        }
+        wait_ring(pend);
     }
-    store_x(load_x(xsrc), xs[0], tok, part);
-    __syncthreads();
-    float sg[2][4];   // the block's group sums S (loaded at its first stage)
+    barrier();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) bs[0][rg][2 * th + i][lane] = decode_rt(IC<0>{}, 0, 2 * th + i);
+    barrier();
 
-    for (int g = 0; g < nst; ++g) {
-        const int sb = g & 7, cur = g & 1;
-        const int gn = g + 1;
-        const bool more = gn < nst;
-        if (sb == 0) {
+    // the A operand of lane (lr, lk): token 16 tt + lr, k 8 lk .. + 7 = chunk lk ^ ((lr / 4) % 4)
+    const int ach = 8 * (lk ^ ((lr >> 2) & 3));
+    // the min-term operand of lane (lr, lk): groups 2 lk, 2 lk + 1
+    const bool mlo = lk < 2;
+    const uint32_t msh = 16u * (lk & 1);
+    for (int b = 0; b < nb; ++b) {
+        const int g0 = 8 * b;
+        static_for<8>([&](auto sI) {
+            constexpr int S = decltype(sI)::value;
+            const int g = g0 + S;
+            const bool iss = g + kQ4Dist < nst;
+            const bool dec = g + 1 < nst;
+            f16x8_t B[4];
 #pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                const float2 v = *reinterpret_cast<const float2*>(srow[tt] + g);
-                sg[0][tt] = v.x;
-                sg[1][tt] = v.y;
-            }
-        }
-        // this stage's B operands; then the next stage's quants and x are loaded
-        // into the same registers, in flight during the products
-        f16x8_t B[4];
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-            const int shn = 4 * (sb & 1);
-            uint32_t sc, mm;
-            q4k_scale_min(hdr[rt], sb, sc, mm);
-            uint32_t e[4];
-            q4_operand((qb[rt].x >> shn) & 0x0f0f0f0fu, sc, e[0], e[1]);
-            q4_operand((qb[rt].y >> shn) & 0x0f0f0f0fu, sc, e[2], e[3]);
-            __builtin_memcpy(&B[rt], e, 16);
-        }
-        uint4 hdr_e[4];   // the block's header, kept for its epilogue
-        if (sb == 7) {
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) hdr_e[rt] = hdr[rt];
-        }
-        XRegs xn;
-        if (more) {
-            xn = load_x(xsrc + static_cast<size_t>(gn) * 64);
-            const size_t blk = static_cast<size_t>(gn >> 3) * 144;
-            if ((gn & 7) == 0) {
-#pragma unroll
-                for (int rt = 0; rt < 4; ++rt) hdr[rt] = ld16(wrow[rt] + blk);
-            }
-            if ((gn & 1) == 0) {
-#pragma unroll
-                for (int rt = 0; rt < 4; ++rt)
-                    qb[rt] = *reinterpret_cast<const uint2*>(wrow[rt] + blk + 16 + 32 * ((gn & 7) >> 1) + 8 * lk);
-            }
-        }
-        const XStage& xc = xs[cur];
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            f16x8_t A[2];
-#pragma unroll
-            for (int p = 0; p < 2; ++p) A[p] = *reinterpret_cast<const f16x8_t*>(&xc[p][16 * tt + lr][8 * lk]);
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) C[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], B[rt], C[tt][rt], 0, 0, 0);
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) C[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1], B[rt], C[tt][rt], 0, 0, 0);
-        }
-        if (sb == 7) {
-            // acc += d P_block; then the block's min terms P_min = sum_g m_g S_g 2^-5
-            // as one [16 tokens x 16] x [16 x 16 rows] fp16 product per tile, k =
-            // (group 2 lk + i / 2, part i % 2) in lane (lr, lk): the two fp16 parts
-            // of S 2^-5 (|S| < 2^20) against m_g twice; acc -= dmin 2^5 P_min.
+            for (int rt = 0; rt < 4; ++rt) B[rt] = bs[S & 1][rg][rt][lane];
+            // the block's epilogue operands (last stage): d, -32 dmin and m_g
             float dsc[4], dmn5[4];
-            f16x4_t Bm[4], As[4];
-#pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
-                uint32_t sc, m0, m1;
-                q4k_scale_min(hdr_e[rt], 2 * lk, sc, m0);
-                q4k_scale_min(hdr_e[rt], 2 * lk + 1, sc, m1);
-                const _Float16 a0 = static_cast<_Float16>(static_cast<float>(m0));
-                const _Float16 a1 = static_cast<_Float16>(static_cast<float>(m1));
-                Bm[rt] = f16x4_t{a0, a0, a1, a1};
-                dsc[rt] = half_bits(hdr_e[rt].x & 0xffffu);
-                dmn5[rt] = -32.0f * half_bits(hdr_e[rt].x >> 16);
-            }
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                const float s0 = sg[0][tt] * 0.03125f, s1 = sg[1][tt] * 0.03125f;
-                const _Float16 h0 = static_cast<_Float16>(s0), h1 = static_cast<_Float16>(s1);
-                As[tt] = f16x4_t{h0, static_cast<_Float16>(s0 - static_cast<float>(h0)), h1,
-                                 static_cast<_Float16>(s1 - static_cast<float>(h1))};
-            }
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt)
+            f16x4_t Bm[4];
+            if constexpr (S == 7) {
 #pragma unroll
                 for (int rt = 0; rt < 4; ++rt) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[tt][rt][r] = __builtin_fmaf(dsc[rt], C[tt][rt][r], acc[tt][rt][r]);
-                    C[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x16f16(As[tt], Bm[rt], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[tt][rt][r] = __builtin_fmaf(dmn5[rt], C[tt][rt][r], acc[tt][rt][r]);
-                    C[tt][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                    const uint4 h = *reinterpret_cast<const uint4*>(&hr[b & 1][64 * rg + 16 * rt + lr][0]);
+                    const uint32_t z = h.z, wq = h.w;
+                    const uint32_t l0 = (z >> msh) & 63u, l1 = (z >> (msh + 8)) & 63u;
+                    const uint32_t h0 = ((wq >> (msh + 4)) & 15u) | (((z >> (msh + 6)) & 3u) << 4);
+                    const uint32_t h1 = ((wq >> (msh + 12)) & 15u) | (((z >> (msh + 14)) & 3u) << 4);
+                    const uint32_t m0 = mlo ? l0 : h0, m1 = mlo ? l1 : h1;
+                    // fp16 1024 + m (bits 0x6400 | m) minus 1024: the exact small integers
+                    const uint32_t pk = hadd2(((m1 << 16) | m0) + 0x64006400u, static_cast<_Float16>(-1024.0f));
+                    const f16x2_t p2 = __builtin_bit_cast(f16x2_t, pk);
+                    Bm[rt] = f16x4_t{p2[0], p2[0], p2[1], p2[1]};
+                    dsc[rt] = opaque(half_bits(h.x & 0xffffu));
+                    dmn5[rt] = opaque(-32.0f * half_bits(h.x >> 16));
                 }
-        }
-        if (more) store_x(xn, xs[cur ^ 1], tok, part);
-        __syncthreads();
+            }
+            const Q4XSlot& xc = xr[g % kQ4XSlots];
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                if (iss) issue_part(g + kQ4Dist, tt);
+                if (dec && (tt & 1)) {
+                    const int rt = 2 * th + (tt >> 1);
+                    bs[(S + 1) & 1][rg][rt][lane] = decode_rt(IC<(S + 1) & 7>{}, g + 1, rt);
+                }
+                f16x8_t A[2];
+#pragma unroll
+                for (int p = 0; p < 2; ++p) A[p] = *reinterpret_cast<const f16x8_t*>(&xc[p][64 * th + 16 * tt + lr][ach]);
+                // a block's first stage starts its sums from zero
+#pragma unroll
+                for (int rt = 0; rt < 4; ++rt)
+                    C[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[0], B[rt], S == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : C[tt][rt], 0, 0, 0);
+#pragma unroll
+                for (int rt = 0; rt < 4; ++rt) C[tt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[1], B[rt], C[tt][rt], 0, 0, 0);
+                if constexpr (S == 7) {
+                    // token tile tt of the block is complete: acc += d P_block - 32 dmin P_min with
+                    // P_min = sum_g m_g (S_g 2^-5) as one [16 tokens x 16] x [16 x 16 rows] fp16
+                    // product, k = (group 2 lk + i / 2, part i % 2): the two fp16 parts of S 2^-5
+                    // (|S| < 2^20) against m_g twice
+                    const float2 v = *reinterpret_cast<const float2*>(&sr[b & 1][64 * th + 16 * tt + lr][2 * lk]);
+                    const float s0 = v.x * 0.03125f, s1 = v.y * 0.03125f;
+                    const _Float16 a0 = static_cast<_Float16>(s0), a1 = static_cast<_Float16>(s1);
+                    const f16x4_t As = f16x4_t{a0, static_cast<_Float16>(s0 - static_cast<float>(a0)), a1,
+                                               static_cast<_Float16>(s1 - static_cast<float>(a1))};
+#pragma unroll
+                    for (int rt = 0; rt < 4; ++rt) {
+                        const f32x4_t pm = __builtin_amdgcn_mfma_f32_16x16x16f16(As, Bm[rt], f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[tt][rt][r] = __builtin_fmaf(dsc[rt], C[tt][rt][r], acc[tt][rt][r]);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[tt][rt][r] = __builtin_fmaf(dmn5[rt], pm[r], acc[tt][rt][r]);
+                    }
+                }
+            }
+            // group g + 2 (the next stage's decode) complete; group g + 3 may stay in flight
+            wait_ring(g + 3 < nst ? q4_group_loads((S + 3) & 7) : 0);
+            barrier();
+        });
     }
     // lane L holds C[4 (L/16) + r][L % 16] of tile (tt, rt): token 16 tt + 4 lk + r, row 16 rt + lr
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int t = t0 + 16 * tt + 4 * lk + r;
+            const int t = tw + 16 * tt + 4 * lk + r;
             if (t >= T) continue;
             const int et = ex[t];
             if (et == kRowNonFinite) {
@@ -568,12 +689,17 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const GemmJobs jobs, c
         }
 }
 
+// The Q4_K kernel's ring loads address x's fp16 parts and the weight rows with
+// 32-bit byte offsets.
 bool gemm_rows_ok(int rows, int K, const float* x) {
-    return rows >= kGemmMinRows && K % 256 == 0 && aligned16(x) && rows <= 65535 * kGT;
+    return rows >= kGemmMinRows && K % 256 == 0 && aligned16(x) && rows <= 65535 * kGT &&
+           4 * static_cast<uint64_t>(rows) * static_cast<uint64_t>(K) < (uint64_t{1} << 32);
 }
 
-bool gemm_job_ok(int type, uint64_t element_offset) {
-    return (type == kQ4_K || type == kQ6_K) && element_offset % 256 == 0;
+bool gemm_job_ok(int type, uint64_t element_offset, int M, int K) {
+    if (element_offset % 256 != 0) return false;
+    if (type == kQ6_K) return true;
+    return type == kQ4_K && static_cast<uint64_t>(M) * static_cast<uint64_t>(K / 256) * 144 < (uint64_t{1} << 32);
 }
 
 struct Prepared {
@@ -606,11 +732,10 @@ int prepare_x(const float* x, int rows, int K, void* workspace, size_t workspace
 }
 
 void launch_gemm(int type, const GemmJobs& jobs, const Prepared& p, int rows, int K, hipStream_t s) {
-    const dim3 grid(jobs.start[jobs.n], blocks_for(rows, kGT));
     if (type == kQ4_K)
-        gemm_q4k<<<grid, kGemmBlock, 0, s>>>(jobs, p.ex, p.sx, p.xp, p.x, rows, K);
+        gemm_q4k<<<dim3(jobs.start[jobs.n], blocks_for(rows, kQ4T)), kQ4Block, 0, s>>>(jobs, p.ex, p.sx, p.xp, p.x, rows, K);
     else
-        gemm_q6k<<<grid, kGemmBlock, 0, s>>>(jobs, p.ex, p.xp, p.x, rows, K);
+        gemm_q6k<<<dim3(jobs.start[jobs.n], blocks_for(rows, kGT)), kGemmBlock, 0, s>>>(jobs, p.ex, p.xp, p.x, rows, K);
 }
 
 // One GEMV per token (the reference's own loop).
@@ -646,7 +771,7 @@ int qwen_matmul_rows(const void* weight, int type, uint64_t num_elements, const 
     QK_REQUIRE(rows >= 0, "matmul_rows: negative rows %d", rows);
     if (rows == 0) return ok();
     QK_REQUIRE(x && y, "matmul_rows: null pointer");
-    if (!gemm_rows_ok(rows, K, x) || !gemm_job_ok(type, element_offset))
+    if (!gemm_rows_ok(rows, K, x) || !gemm_job_ok(type, element_offset, M, K))
         return per_token(weight, type, num_elements, x, y, rows, M, K, element_offset, stream);
     const hipStream_t s = as_stream(stream);
     Prepared p;
@@ -695,7 +820,7 @@ int qwen_matmul_rows_multi(const qwen_gemv_desc* descs, int n, const float* x, i
         };
         for (int j = 0; gemm && j < n; ++j) {
             const qwen_gemv_desc& e = descs[j];
-            if (e.type != type || !gemm_job_ok(e.type, e.element_offset)) continue;
+            if (e.type != type || !gemm_job_ok(e.type, e.element_offset, e.M, K)) continue;
             if (!prepared) {
                 if (const int rc = prepare_x(x, rows, K, workspace, workspace_bytes, s, p)) return rc;
                 prepared = true;
@@ -716,7 +841,7 @@ int qwen_matmul_rows_multi(const qwen_gemv_desc* descs, int n, const float* x, i
         if (const int rc = check_launch("matmul_rows_multi")) return rc;
     for (int j = 0; j < n; ++j) {   // the rest: one GEMV per token
         const qwen_gemv_desc& e = descs[j];
-        if (gemm && gemm_job_ok(e.type, e.element_offset)) continue;
+        if (gemm && gemm_job_ok(e.type, e.element_offset, e.M, K)) continue;
         if (const int rc = per_token(e.weight, e.type, e.num_elements, x, e.y, rows, e.M, K, e.element_offset, stream))
             return rc;
     }
