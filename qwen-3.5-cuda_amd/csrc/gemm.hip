@@ -28,15 +28,15 @@
 // stores x in that order within each 4 consecutive elements (0, 2, 1, 3);
 // A and B then agree slot by slot.
 //
-// Work, per 32-element stage (one barrier per stage). Q4_K: a workgroup of 8
-// waves owns 128 tokens x 256 weight rows, its operands arrive through an LDS
-// ring three stages ahead and the next stage's B operands are decoded while the
-// current stage's products run (16 x 16 tiles on v_mfma_f32_16x16x32_f16; the
-// kernel's own comment has the details). Q6_K: a workgroup of 4 waves owns 64
-// tokens x 256 weight rows, wave w rows 64w .. 64w+63; the two fp16 parts of
-// x[64 tokens][32] are copied to LDS (double-buffered) with the next stage's x
-// and quants loaded while the current one is computed; 32 x 32 tiles on
-// v_mfma_f32_32x32x16_f16 (K = one 16-element scale group).
+// Work, per 32-element stage (one barrier per stage): a workgroup of 8 waves
+// owns 128 tokens x 256 weight rows, wave w rows 64 (w % 4) .. +63 of token half
+// w / 4, and the next stage's B operands are decoded (each wave pair splitting
+// the work, through LDS) while the current stage's products run. Q4_K: 16 x 16
+// tiles on v_mfma_f32_16x16x32_f16, operands through an LDS ring filled three
+// stages ahead by global -> LDS loads. Q6_K: 32 x 32 tiles on
+// v_mfma_f32_32x32x16_f16 (K = one 16-element scale group), x staged through
+// LDS from registers, quant bytes and scales per half-block through LDS. The
+// kernels' own comments have the details.
 #include <algorithm>
 #include <cfloat>
 #include <type_traits>
@@ -55,14 +55,10 @@ typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kGemmWaves = 4;
-constexpr int kGemmBlock = kGemmWaves * kWave;
-constexpr int kGT = 64;            // tokens per workgroup
 constexpr int kGR = 256;           // weight rows per workgroup (64 per wave)
 constexpr int kGemmMinRows = 16;   // fewer tokens: one GEMV per token
+constexpr int kGemmMaxRows = 65535 * 128;   // token blocks of 128 in grid.y
 constexpr int kXRow = 40;          // halves per staged token row (32 + 8 padding)
-
-typedef uint16_t XStage[2][kGT][kXRow];   // one stage of x: the two fp16 parts
 
 // Matrices of one launch (all of one K-quant type, one x): workgroup column
 // blockIdx.x in [start[j], start[j+1]) works on rows (blockIdx.x - start[j]) * kGR ..
@@ -205,12 +201,6 @@ __device__ __forceinline__ XRegs load_x(const uint16_t* __restrict__ src) {
     return XRegs{ld16(src), ld16(src + 8)};
 }
 
-__device__ __forceinline__ void store_x(const XRegs& r, XStage& xs, int tok, int part) {
-    uint16_t* d = &xs[part >> 1][tok][16 * (part & 1)];
-    st16(d, r.a);
-    st16(d + 8, r.b);
-}
-
 // Bytes (0, 2) and (1, 3) of n placed under `hi` (byte values 0 or 0x64).
 __device__ __forceinline__ uint32_t bytes02(uint32_t hi, uint32_t n) { return __builtin_amdgcn_perm(hi, n, 0x04020400u); }
 __device__ __forceinline__ uint32_t bytes13(uint32_t hi, uint32_t n) { return __builtin_amdgcn_perm(hi, n, 0x04030401u); }
@@ -218,16 +208,6 @@ __device__ __forceinline__ uint32_t bytes13(uint32_t hi, uint32_t n) { return __
 __device__ __forceinline__ uint32_t hadd2(uint32_t w, _Float16 c) {
     const f16x2_t r = __builtin_bit_cast(f16x2_t, w) + f16x2_t{c, c};
     return __builtin_bit_cast(uint32_t, r);
-}
-
-// Q4_K (scale, min) of sub-block sb from the block header hdr (d, dmin,
-// scales[12]): scale_min_k4, src/cuda/matmul_q4.cu:18-26. Branch-free in sb.
-__device__ __forceinline__ void q4k_scale_min(const uint4& hdr, int sb, uint32_t& sc, uint32_t& m) {
-    const int sh = 8 * (sb & 3);
-    const uint32_t a = hdr.y >> sh, b = hdr.z >> sh, c = hdr.w >> sh;
-    const bool lo = sb < 4;
-    sc = lo ? (a & 63) : ((c & 15) | ((a >> 2) & 0x30));
-    m = lo ? (b & 63) : (((c >> 4) & 15) | ((b >> 2) & 0x30));
 }
 
 // fp16 q * sc of four quants (bytes of n, each < 16), sc < 64: two words in
@@ -529,62 +509,115 @@ __global__ __launch_bounds__(kQ4Block, 1) void gemm_q4k(const GemmJobs jobs, con
 }
 
 // ------------------------------------------------------------------ Q6_K
-// 8 bytes at a 2-byte aligned address (gfx950 global loads take any byte
-// alignment; Q6_K blocks are 210 bytes).
-__device__ __forceinline__ uint2 ldg8_a2(const uint8_t* p) {
-    uint2 v;
-    __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 8);
-    return v;
-}
-
 // Element i of a block (src/cuda/matmul_q4.cu:105-126): ql byte 64(i/128) +
 // 32((i%128)/32 & 1) + i%32 (low nibble in quarters 0, 1 of a half, high in
 // 2, 3), qh byte 128 + 32(i/128) + i%32 bits 2*quarter, scale byte 192 + i/16,
 // d at 208. Stage sg of a block (elements 32 sg ..) is half sg/4, quarter
 // sg%4; lane (l32, lh) of step h takes elements 32 sg + 16 h + 8 lh .. +7:
 // eight consecutive ql and qh bytes, scale 2 sg + h.
-struct Q6Quants {
-    uint2 ql[2][2], qh[2][2];   // [row tile][step]
-};
+//
+// A workgroup (8 waves, one per CU) owns 128 tokens x 256 weight rows; wave w
+// owns rows 64 (w % 4) .. +63 for tokens 64 (w / 4) .. +63 (2 x 2 tiles of
+// 32 x 32 on v_mfma_f32_32x32x16_f16, k = one 16-element scale group, so each
+// group's product is scaled by d * sc in fp32 before it joins the sums). x goes
+// through LDS from registers (the next stage loaded while the current one
+// computes). The quant bytes and scales of a half-block (4 stages: 64 ql
+// bytes, both nibbles; 32 qh bytes; the 16 scales and d) are staged per row in
+// LDS with coalesced 16-byte loads four stages ahead; waves w and w + 4 (same
+// rows) split the next stage's B decode (wave w / 4 takes step h = w / 4) into
+// an LDS slot both read after the stage's barrier.
+constexpr int kQ6Waves = 8;
+constexpr int kQ6Block = kQ6Waves * kWave;
+constexpr int kQ6T = 128;                    // tokens per workgroup
+typedef uint16_t Q6XStage[2][kQ6T][kXRow];   // one stage of x: the two fp16 parts
+typedef f16x8_t Q6BSlot[4][2][2][kWave];     // B operands: [row group][step h][row tile][lane]
+// One half-block of a row: ql bytes 64 half .. +63 | qh bytes 128 + 32 half .. +31 |
+// scales (block bytes 192..207) | block bytes 194..209 (d in the last two) | pad (row
+// stride 36 dwords spreads a wave's 32 rows over the LDS banks)
+typedef uint8_t Q6WSlot[kGR][144];
 
-__device__ __forceinline__ Q6Quants q6_load(const uint8_t* const (&wrow)[2], int g, int lh) {
-    const int sg = g & 7;
-    const int off_l = 64 * (sg >> 2) + 32 * (sg & 1) + 8 * lh;
-    const int off_h = 128 + 32 * (sg >> 2) + 8 * lh;
-    Q6Quants q;
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-        const uint8_t* blk = wrow[rt] + static_cast<size_t>(g >> 3) * 210;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            q.ql[rt][h] = ldg8_a2(blk + off_l + 16 * h);
-            q.qh[rt][h] = ldg8_a2(blk + off_h + 16 * h);
-        }
-    }
-    return q;
+// 16 bytes at a 2-byte aligned address (gfx950 global loads take any byte
+// alignment; Q6_K blocks are 210 bytes).
+__device__ __forceinline__ uint4 ldg16_a2(const uint8_t* p) {
+    uint4 v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 16);
+    return v;
 }
 
-__global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const GemmJobs jobs, const int* __restrict__ ex,
-                                                          const uint16_t* __restrict__ xp,
-                                                          const float* __restrict__ x, int T, int K) {
-    __shared__ __align__(16) XStage xs[2];
+__global__ __launch_bounds__(kQ6Block, 1) void gemm_q6k(const GemmJobs jobs, const int* __restrict__ ex,
+                                                         const uint16_t* __restrict__ xp, const float* __restrict__ x,
+                                                         int T, int K) {
+    __shared__ __align__(16) Q6XStage xs[2];
+    __shared__ __align__(16) Q6BSlot bs[2];
+    __shared__ __align__(16) Q6WSlot wsl[2];
     const GemmJob job = gemm_job(jobs);
     const uint8_t* __restrict__ w = job.w;
     float* __restrict__ y = job.y;
     const int M = job.M;
     const uint64_t ub0 = job.ub0;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int t0 = blockIdx.y * kGT;
-    const int r0 = job.mb * kGR + wv * 64;
-    const int nb = K >> 8, nst = K >> 5;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+    const int rg = wv & 3, th = wv >> 2;                       // row group, token half (= decode step)
+    const int t0w = blockIdx.y * kQ6T;
+    const int tw = t0w + 64 * th;
+    const int rw0 = job.mb * kGR;
+    const int r0 = rw0 + 64 * rg;
+    const int nb = K >> 8, nst = K >> 5, nhb = nst >> 2;
     const int tok = tid >> 2, part = tid & 3;
-    const uint16_t* xsrc = xp + static_cast<size_t>(min(t0 + tok, T - 1)) * nst * 64 + 32 * (part >> 1) +
-                           16 * (part & 1);
+    const uint16_t* xsrc = xp + static_cast<size_t>(min(t0w + tok, T - 1)) * nst * 64 + 32 * (part >> 1) + 16 * (part & 1);
     const int l32 = lane & 31, lh = lane >> 5;
-    const uint8_t* wrow[2];
+    auto store_xs = [&](const XRegs& r, Q6XStage& d) {
+        uint16_t* p = &d[part >> 1][tok][16 * (part & 1)];
+        st16(p, r.a);
+        st16(p + 8, r.b);
+    };
+    // half-block j of every row: thread tid loads 16-byte pieces tid + 512 i (i < 4)
+    // of the 2048 (row c / 8, piece c % 8: ql 0-3, qh 4-5, scales 6, d 7)
+    uint4 wst[4];
+    auto wstage_load = [&](int j) {
+        const int half = j & 1;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-        wrow[rt] = w + (ub0 + static_cast<uint64_t>(min(r0 + 32 * rt + l32, M - 1)) * nb) * 210;
+        for (int i = 0; i < 4; ++i) {
+            const int c = tid + 512 * i;
+            const int row = c >> 3, piece = c & 7;
+            const uint8_t* blk = w + (ub0 + static_cast<uint64_t>(min(rw0 + row, M - 1)) * nb + (j >> 1)) * 210;
+            const int off = piece < 4 ? 64 * half + 16 * piece
+                                      : piece < 6 ? 128 + 32 * half + 16 * (piece - 4) : 192 + 2 * (piece - 6);
+            wst[i] = ldg16_a2(blk + off);
+        }
+    };
+    auto wstage_store = [&](int j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = tid + 512 * i;
+            *reinterpret_cast<uint4*>(&wsl[j & 1][c >> 3][16 * (c & 7)]) = wst[i];
+        }
+    };
+    // this wave's share of stage g's B operands (step h = th, both row tiles): q - 32
+    auto decode = [&](int g) {
+        const int sg = g & 7, quarter = sg & 3;
+        const int nsh = 4 * (quarter >> 1), hsh = 2 * quarter;
+        const Q6WSlot& sl = wsl[(g >> 2) & 1];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+            const int row = 64 * rg + 32 * rt + l32;
+            const uint2 ql = *reinterpret_cast<const uint2*>(&sl[row][32 * (quarter & 1) + 16 * th + 8 * lh]);
+            const uint2 qh = *reinterpret_cast<const uint2*>(&sl[row][64 + 16 * th + 8 * lh]);
+            const uint32_t q0 = ((ql.x >> nsh) & 0x0f0f0f0fu) | (((qh.x >> hsh) & 0x03030303u) << 4);
+            const uint32_t q1 = ((ql.y >> nsh) & 0x0f0f0f0fu) | (((qh.y >> hsh) & 0x03030303u) << 4);
+            uint32_t e[4];
+            q6_operand(q0, e[0], e[1]);
+            q6_operand(q1, e[2], e[3]);
+            f16x8_t r;
+            __builtin_memcpy(&r, e, 16);
+            bs[g & 1][rg][th][rt][lane] = r;
+        }
+    };
+    auto barrier = []() {   // LDS stores complete, then the workgroup meets
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
 
     f32x16_t acc[2][2];
 #pragma unroll
@@ -594,54 +627,52 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const GemmJobs jobs, c
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[tt][rt][i] = 0.f;
 
-    uint4 scl[2];
-    float dh[2];
-    Q6Quants qc = q6_load(wrow, 0, lh);
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-        __builtin_memcpy(&scl[rt], __builtin_assume_aligned(wrow[rt] + 192, 2), 16);
-        dh[rt] = half_bits(*reinterpret_cast<const uint16_t*>(__builtin_assume_aligned(wrow[rt] + 208, 2)));
+    wstage_load(0);
+    wstage_store(0);
+    if (nhb > 1) {   // K >= 256: nhb >= 2
+        wstage_load(1);
+        wstage_store(1);
     }
-    store_x(load_x(xsrc), xs[0], tok, part);
-    __syncthreads();
+    store_xs(load_x(xsrc), xs[0]);
+    barrier();
+    decode(0);
+    barrier();
 
     for (int g = 0; g < nst; ++g) {
-        const int sg = g & 7, quarter = sg & 3, cur = g & 1;
+        const int sg = g & 7, cur = g & 1;
         const int gn = g + 1;
         const bool more = gn < nst;
-        // this stage's B operands and group scales (both steps); then the next
-        // stage's quants, scales and x are loaded into the same registers
-        const int nsh = 4 * (quarter >> 1), hsh = 2 * quarter;
-        f16x8_t B[2][2];
+        // d * sc of this stage's two groups for the lane's two rows
         float Ag[2][2];
+        {
+            const Q6WSlot& sl = wsl[(g >> 2) & 1];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const int row = 64 * rg + 32 * rt + l32;
+                const uint32_t sp = *reinterpret_cast<const uint16_t*>(&sl[row][96 + 2 * sg]);   // scales 2 sg, 2 sg + 1
+                const float d = half_bits(*reinterpret_cast<const uint16_t*>(&sl[row][126]));
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    Ag[h][rt] = d * static_cast<float>(static_cast<int>(__builtin_amdgcn_sbfe(sp, 8 * h, 8)));
+            }
+        }
+        XRegs xn;
+        if (more) xn = load_x(xsrc + static_cast<size_t>(gn) * 64);
+        // half-block k + 1 (loaded at half-block k - 1's first stage) goes into k - 1's
+        // slot at half-block k's first stage (k - 1's decodes and scale reads ended with
+        // the previous barrier); then half-block k + 2 is loaded
+        const int jh = g >> 2;
+        if ((g & 3) == 0) {
+            if (jh >= 1 && jh + 1 < nhb) wstage_store(jh + 1);
+            if (jh + 2 < nhb) wstage_load(jh + 2);
+        }
+        f16x8_t B[2][2];
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-                const uint32_t q0 = ((qc.ql[rt][h].x >> nsh) & 0x0f0f0f0fu) | (((qc.qh[rt][h].x >> hsh) & 0x03030303u) << 4);
-                const uint32_t q1 = ((qc.ql[rt][h].y >> nsh) & 0x0f0f0f0fu) | (((qc.qh[rt][h].y >> hsh) & 0x03030303u) << 4);
-                uint32_t e[4];
-                q6_operand(q0, e[0], e[1]);
-                q6_operand(q1, e[2], e[3]);
-                __builtin_memcpy(&B[h][rt], e, 16);
-                const int si = 2 * sg + h;   // scale byte si of the block
-                const uint32_t sw = si < 8 ? (si < 4 ? scl[rt].x : scl[rt].y) : (si < 12 ? scl[rt].z : scl[rt].w);
-                Ag[h][rt] = dh[rt] * static_cast<float>(static_cast<int>(__builtin_amdgcn_sbfe(sw, 8 * (si & 3), 8)));
-            }
-        XRegs xn;
-        if (more) {
-            xn = load_x(xsrc + static_cast<size_t>(gn) * 64);
-            qc = q6_load(wrow, gn, lh);
-            if ((gn & 7) == 0) {
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt) {
-                    const uint8_t* blk = wrow[rt] + static_cast<size_t>(gn >> 3) * 210;
-                    __builtin_memcpy(&scl[rt], __builtin_assume_aligned(blk + 192, 2), 16);
-                    dh[rt] = half_bits(*reinterpret_cast<const uint16_t*>(__builtin_assume_aligned(blk + 208, 2)));
-                }
-            }
-        }
-        const XStage& xc = xs[cur];
+            for (int rt = 0; rt < 2; ++rt) B[h][rt] = bs[cur][rg][h][rt][lane];
+        if (more) decode(gn);
+        const Q6XStage& xc = xs[cur];
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -649,7 +680,7 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const GemmJobs jobs, c
                 f16x8_t A[2];
 #pragma unroll
                 for (int p = 0; p < 2; ++p)
-                    A[p] = *reinterpret_cast<const f16x8_t*>(&xc[p][32 * tt + l32][16 * h + 8 * lh]);
+                    A[p] = *reinterpret_cast<const f16x8_t*>(&xc[p][64 * th + 32 * tt + l32][16 * h + 8 * lh]);
 #pragma unroll
                 for (int rt = 0; rt < 2; ++rt) {
                     f32x16_t Cq;
@@ -661,15 +692,15 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const GemmJobs jobs, c
                     for (int i = 0; i < 16; ++i) acc[tt][rt][i] = __builtin_fmaf(Ag[h][rt], Cq[i], acc[tt][rt][i]);
                 }
             }
-        if (more) store_x(xn, xs[cur ^ 1], tok, part);
-        __syncthreads();
+        if (more) store_xs(xn, xs[cur ^ 1]);
+        barrier();
     }
     // lane L holds C[8 (i/4) + 4 (L/32) + i%4][L % 32] of tile (tt, rt) in register i
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int t = t0 + 32 * tt + 8 * (i >> 2) + 4 * lh + (i & 3);
+            const int t = tw + 32 * tt + 8 * (i >> 2) + 4 * lh + (i & 3);
             if (t >= T) continue;
             const int et = ex[t];
             if (et == kRowNonFinite) {
@@ -692,7 +723,7 @@ __global__ __launch_bounds__(kGemmBlock, 2) void gemm_q6k(const GemmJobs jobs, c
 // The Q4_K kernel's ring loads address x's fp16 parts and the weight rows with
 // 32-bit byte offsets.
 bool gemm_rows_ok(int rows, int K, const float* x) {
-    return rows >= kGemmMinRows && K % 256 == 0 && aligned16(x) && rows <= 65535 * kGT &&
+    return rows >= kGemmMinRows && K % 256 == 0 && aligned16(x) && rows <= kGemmMaxRows &&
            4 * static_cast<uint64_t>(rows) * static_cast<uint64_t>(K) < (uint64_t{1} << 32);
 }
 
@@ -735,7 +766,7 @@ void launch_gemm(int type, const GemmJobs& jobs, const Prepared& p, int rows, in
     if (type == kQ4_K)
         gemm_q4k<<<dim3(jobs.start[jobs.n], blocks_for(rows, kQ4T)), kQ4Block, 0, s>>>(jobs, p.ex, p.sx, p.xp, p.x, rows, K);
     else
-        gemm_q6k<<<dim3(jobs.start[jobs.n], blocks_for(rows, kGT)), kGemmBlock, 0, s>>>(jobs, p.ex, p.xp, p.x, rows, K);
+        gemm_q6k<<<dim3(jobs.start[jobs.n], blocks_for(rows, kQ6T)), kQ6Block, 0, s>>>(jobs, p.ex, p.xp, p.x, rows, K);
 }
 
 // One GEMV per token (the reference's own loop).
