@@ -1348,6 +1348,9 @@ GEMM_CASES = [   # kind, tokens, M, K, first row (element offset = row * K)
     ("Q4_K", 7, 512, 2048, 0), ("Q6_K", 15, 100, 768, 0), ("Q8_0", 20, 96, 512, 0), ("Q4_K", 40, 64, 320, 0),
     # the prep kernel's register form at K = 1024 and its two-pass form at K above 256 outside 512..4096
     ("Q4_K", 32, 256, 1024, 0), ("Q6_K", 32, 256, 1024, 0), ("Q6_K", 48, 100, 1536, 0), ("Q4_K", 20, 300, 3072, 1),
+    # an odd number of blocks per row (the rings' block and half-block slots alternate unevenly), token
+    # counts one past a 128-token tile and one short of two
+    ("Q4_K", 129, 300, 1280, 2), ("Q6_K", 257, 260, 1280, 0), ("Q4_K", 255, 512, 768, 0), ("Q6_K", 129, 513, 768, 8),
 ]
 
 
