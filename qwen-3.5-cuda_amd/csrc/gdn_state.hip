@@ -22,8 +22,9 @@
 // point keeps the state slice in VGPRs across all tokens of the call (the
 // reference's per-token loop, one launch), reading each token's q, k, v
 // straight from the GDN front end's output rows. A single token (the decode
-// step) reads the state as whole 128-byte lines instead: a workgroup of four
-// waves per (value head, 32 columns), column sums through DPP and LDS.
+// step) reads the state in row-major tiles instead: a workgroup of two waves
+// per (value head, 16 columns), the two tiles of a 128-byte line segment on one
+// XCD, column sums through DPP and LDS.
 #include <algorithm>
 #include <cmath>
 
@@ -161,7 +162,7 @@ __global__ __launch_bounds__(kBlock) void gdn_recurrent_g(float* __restrict__ S,
     for (int r = 0; r < RPL; ++r) __builtin_nontemporal_store(s[r], Sj + static_cast<size_t>(r) * value_dim);
 }
 
-// Single step with value_dim % 32 != 0 (gdn_step_tile takes the others): one
+// Single step with value_dim % 16 != 0 (gdn_step_tile takes the others): one
 // wave per (value head, 4 value columns); RPL rows of the state per lane
 // (key_dim = 64 * RPL). Tokens t < rows run in order, the state slice staying
 // in VGPRs; q/k/v of token t sit at t * qkv_stride, beta/decay at
@@ -262,19 +263,38 @@ __global__ __launch_bounds__(kBlock) void gdn_recurrent_v4(float* __restrict__ S
     for (int r = 0; r < RPL; ++r) st4_nt(Sh + static_cast<size_t>(lane + 64 * r) * value_dim, s[r]);
 }
 
-// Single token with value_dim % 32 == 0 (the decode path): one workgroup of
-// kTileWaves waves per (value head h, kTileCols = 32 value columns). Lane L holds
-// columns 4 * (L / 8) .. + 3 of the block and wave w rows
-// w * DK / 4 + L % 8 + 8 r (r < DK / 32): the 8 lanes of a column group read 8
-// rows and the 8 groups the 32 columns of each, so one float4 load instruction
-// covers 8 whole 128-byte lines of the state (a 4-column slice per wave, as
-// gdn_recurrent_v4 reads, touches 64 lines with 16 bytes each and runs ~40%
-// longer at the Qwen3.5 shape). A column's sums over rows: a per-lane partial,
-// an 8-lane DPP sum, and the waves' partials added through LDS in wave order.
-constexpr int kTileWaves = kWaves;
-constexpr int kTileLanes = 8;                        // lanes per column group
+// Single token with value_dim % 16 == 0 (the decode path): one workgroup of
+// kTileWaves = 2 waves per (value head h, kTileCols = 16 value columns). Lane L
+// holds columns 4 * (L / 16) .. + 3 of the tile and wave w rows
+// w * DK / 2 + L % 16 + 16 r (r < DK / 32): the 16 lanes of a column group read
+// 16 rows and the 4 groups the 16 columns of each, so one float4 load
+// instruction covers 16 64-byte halves of state lines. The two tiles that share
+// a 128-byte line segment run on one XCD (tile_of_block), whose L2 then fetches
+// the line once. A column's sums over rows: a per-lane partial, a 16-lane DPP
+// sum, and the two waves' partials added through LDS in wave order. The state
+// loads are issued before anything else the kernel loads.
+//
+// Measured at 32 x 128 x 128 against the earlier tiles of four waves x 32
+// columns (8 lanes per column, whole 128-byte lines per workgroup, 128
+// workgroups): 2.93 against 3.38 us per call, the same bytes on twice as many
+// CUs; 16-column tiles in plain block order (line halves on two XCDs) take
+// 3.66 us.
+constexpr int kTileWaves = 2;
+constexpr int kTileBlock = kTileWaves * kWave;
+constexpr int kTileLanes = 16;                       // lanes per column group
 constexpr int kTileGroups = kWave / kTileLanes;      // column groups per wave
 constexpr int kTileCols = 4 * kTileGroups;           // value columns per workgroup
+
+// Tile of workgroup b in a grid of exactly `tiles` workgroups. Workgroups are
+// dealt to the 8 XCDs round robin (b % 8), so tiles 2 l and 2 l + 1 (the two
+// halves of a 128-byte line segment when value_dim % 32 == 0) go to workgroups
+// b and b + 8 of a group of 16; the last tiles % 16 keep their own index. A
+// bijection on [0, tiles).
+__device__ __forceinline__ int tile_of_block(int b, int tiles) {
+    if (b >= (tiles & ~15)) return b;
+    const int idx = b >> 3;
+    return (((idx >> 1) << 3) + (b & 7)) * 2 + (idx & 1);
+}
 
 // One token on a lane's slice (RPL rows kr / qr of k / q, the state rows s at
 // St + 8 r * value_dim, value columns vv, gates b / d): S *= d; m = k . S;
@@ -350,25 +370,30 @@ __device__ __forceinline__ float4 tile_step(float4 (&s)[RPL], const float (&kr)[
 }
 
 // The tile form of one token (key dim DK = 64 or 128). Grid: exactly
-// value_heads * value_dim / kTileCols workgroups of kBlock threads.
+// value_heads * value_dim / kTileCols workgroups of kTileBlock threads.
 template <int DK>
-__global__ __launch_bounds__(kBlock) void gdn_step_tile(float* __restrict__ S, const float* __restrict__ q,
-                                                        const float* __restrict__ k, const float* __restrict__ v,
-                                                        const float* __restrict__ beta,
-                                                        const float* __restrict__ decay, float* __restrict__ out,
-                                                        int key_heads, int value_dim, RawGates rg) {
+__global__ __launch_bounds__(kTileBlock) void gdn_step_tile(float* __restrict__ S, const float* __restrict__ q,
+                                                            const float* __restrict__ k, const float* __restrict__ v,
+                                                            const float* __restrict__ beta,
+                                                            const float* __restrict__ decay, float* __restrict__ out,
+                                                            int key_heads, int value_dim, RawGates rg) {
     constexpr int RPL = DK / (kTileWaves * kTileLanes);
     static_assert(RPL * kTileWaves * kTileLanes == DK, "key dim");
     __shared__ float4 red[2 * kTileWaves * kTileGroups];
     const int lane = threadIdx.x & 63;
     const int w = wave_in_block();
     const int cblocks = value_dim / kTileCols;
-    const int h = blockIdx.x / cblocks;
+    const int tile = tile_of_block(blockIdx.x, gridDim.x);
+    const int h = tile / cblocks;
     const int cg = lane / kTileLanes, rl = lane % kTileLanes;
-    const int j0 = (blockIdx.x - h * cblocks) * kTileCols + 4 * cg;
-    const int src = h % key_heads;  // value heads tile as [subgroup][key head]
+    const int j0 = (tile - h * cblocks) * kTileCols + 4 * cg;
     const int r0 = w * (DK / kTileWaves) + rl;
     float* St = S + (static_cast<size_t>(h) * DK + r0) * value_dim + j0;
+    float4 s[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) s[r] = ld4_nt(St + static_cast<size_t>(kTileLanes * r) * value_dim);
+    __builtin_amdgcn_sched_barrier(0);   // the state loads first
+    const int src = h % key_heads;       // value heads tile as [subgroup][key head]
     const float* kt = k + src * DK + r0;
     const float* qt = q + src * DK + r0;
     float kr[RPL], qr[RPL];
@@ -378,9 +403,6 @@ __global__ __launch_bounds__(kBlock) void gdn_step_tile(float* __restrict__ S, c
         qr[r] = qt[kTileLanes * r];
     }
     const float4 vv = ld4(v + static_cast<size_t>(h) * value_dim + j0);
-    float4 s[RPL];
-#pragma unroll
-    for (int r = 0; r < RPL; ++r) s[r] = ld4_nt(St + static_cast<size_t>(kTileLanes * r) * value_dim);
     const float br = beta[h], dr = decay[h];
     const float d = rg.a ? gate_decay(rg.a[h], dr, rg.dt[h]) : dr;
     const float b = rg.a ? gate_beta(br) : br;
@@ -392,19 +414,19 @@ __global__ __launch_bounds__(kBlock) void gdn_step_tile(float* __restrict__ S, c
 // the front end (causal conv of kernel 4 + SiLU, Q/K L2 norm) and the
 // fused-gate recurrence. Key dim 128, value_dim % kTileCols == 0. Each
 // workgroup is a workgroup of gdn_step_tile<128> -- (value head h, columns
-// cb * 32 ..), lane L of wave w holding columns j0 = cb * 32 + 4 (L / 8) .. + 3
-// and rows w * 32 + L % 8 + 8 r -- whose waves first evaluate the front end for
+// cb * 16 ..), lane L of wave w holding columns j0 = cb * 16 + 4 (L / 16) .. + 3
+// and rows w * 64 + L % 16 + 16 r -- whose waves first evaluate the front end for
 // what they read: the 256 q | k channels of key head h % key_heads in
 // gdn_frontend_k4<32>'s layout (lane L: channels 4L..4L+3 of q for L < 32, of k
 // for L >= 32; a 32-lane sum of squares per head), moved to the recurrence's
 // layout with lane permutes, and each lane its 4 value channels. So every value
 // equals what gdn_frontend_rows writes and the recurrence reads, bit for bit.
 // Writes: the front end's output row y and the new history (q | k channels of
-// key head g by wave 0 of workgroup h = g, cb = 0; value channels by wave 0 of
+// key head g by wave 0 of the tile h = g, cb = 0; value channels by wave 0 of
 // the workgroup that reads them), the state and the output. hist_out must not
 // overlap hist_in: many waves read one key head's history while one of them
 // writes it. Grid: exactly value_heads * value_dim / kTileCols workgroups.
-__global__ __launch_bounds__(kBlock) void gdn_decode_fused(
+__global__ __launch_bounds__(kTileBlock) void gdn_decode_fused(
         const float* __restrict__ x, const float* __restrict__ cw, const float* __restrict__ hin,
         float* __restrict__ hout, float* __restrict__ y, float* __restrict__ S, const float* __restrict__ beta_raw,
         const float* __restrict__ alpha_raw, const float* __restrict__ a, const float* __restrict__ dt,
@@ -415,21 +437,25 @@ __global__ __launch_bounds__(kBlock) void gdn_decode_fused(
     const int lane = threadIdx.x & 63;
     const int w = wave_in_block();
     const int cblocks = value_dim / kTileCols;
-    const int h = blockIdx.x / cblocks;
-    const int cb = blockIdx.x - h * cblocks;
+    const int tile = tile_of_block(blockIdx.x, gridDim.x);
+    const int h = tile / cblocks;
+    const int cb = tile - h * cblocks;
     const int cg = lane / kTileLanes, rl = lane % kTileLanes;
     const int j0 = cb * kTileCols + 4 * cg;
+    const int r0 = w * (DK / kTileWaves) + rl;
+    float* St = S + (static_cast<size_t>(h) * DK + r0) * value_dim + j0;
+    float4 s[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) s[r] = ld4_nt(St + static_cast<size_t>(kTileLanes * r) * value_dim);
     const int src = h % key_heads;
     const int kd = key_heads * DK;
-    const int r0 = w * (DK / kTileWaves) + rl;
     const bool is_q = lane < 32;
     const size_t c = static_cast<size_t>(is_q ? src * DK + 4 * lane : kd + src * DK + 4 * (lane - 32));
     const size_t cv = static_cast<size_t>(2 * kd + h * value_dim + j0);
-    float* St = S + (static_cast<size_t>(h) * DK + r0) * value_dim + j0;
 
-    // Every load issued before the first use: taps, history and input of the
-    // lane's q | k channels and of its value channels, the gates, the state
-    // slice.
+    // Every load issued before the first use, the state slice's first: taps,
+    // history and input of the lane's q | k channels and of its value
+    // channels, the gates.
     const float4 w0 = ld4(cw + 4 * c), w1 = ld4(cw + 4 * c + 4), w2 = ld4(cw + 4 * c + 8), w3 = ld4(cw + 4 * c + 12);
     const float4 ha = ld4(hin + 3 * c), hb = ld4(hin + 3 * c + 4), hd = ld4(hin + 3 * c + 8);
     const float4 xv = ld4(x + c);
@@ -437,9 +463,7 @@ __global__ __launch_bounds__(kBlock) void gdn_decode_fused(
     const float4 va = ld4(hin + 3 * cv), vb = ld4(hin + 3 * cv + 4), vd = ld4(hin + 3 * cv + 8);
     const float4 vx = ld4(x + cv);
     const float br = beta_raw[h], ar = alpha_raw[h], ah = a[h], dth = dt[h];
-    float4 s[RPL];
-#pragma unroll
-    for (int r = 0; r < RPL; ++r) s[r] = ld4_nt(St + static_cast<size_t>(kTileLanes * r) * value_dim);
+    __builtin_amdgcn_sched_barrier(0);
 
     // q | k front end (gdn_frontend_k4<32>, one row)
     float4 h0, h1, h2;
@@ -540,11 +564,11 @@ int launch_recurrent(float* state, const float* q, const float* k, const float* 
         // One token: the state traffic dominates, read as whole 128-byte lines.
         const unsigned grid = static_cast<unsigned>(value_heads * (value_dim / kTileCols));
         if (key_dim == 64)
-            gdn_step_tile<64><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, key_heads, value_dim, rg);
+            gdn_step_tile<64><<<grid, kTileBlock, 0, s>>>(state, q, k, v, beta, decay, out, key_heads, value_dim, rg);
         else
-            gdn_step_tile<128><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, key_heads, value_dim, rg);
+            gdn_step_tile<128><<<grid, kTileBlock, 0, s>>>(state, q, k, v, beta, decay, out, key_heads, value_dim, rg);
     } else if (vec && rows == 1 && aligned16(state) && aligned16(v) && aligned16(out)) {
-        // One token, value_dim % 32 != 0: 4-column float4 slices.
+        // One token, value_dim % 16 != 0: 4-column float4 slices.
         const unsigned grid = blocks_for(value_heads * (value_dim / 4), kWaves);
         if (key_dim == 64)
             gdn_recurrent_v4<1><<<grid, kBlock, 0, s>>>(state, q, k, v, beta, decay, out, rows, key_heads,
@@ -654,7 +678,7 @@ int qwen_gdn_decode_step(const float* x, const float* conv_weight, const float* 
                                              key_heads, value_heads, key_dim, value_dim, 0, 0, stream);
     }
     const unsigned grid = static_cast<unsigned>(value_heads * (value_dim / kTileCols));
-    gdn_decode_fused<<<grid, kBlock, 0, as_stream(stream)>>>(x, conv_weight, hist_in, hist_out, y, state, beta_raw,
+    gdn_decode_fused<<<grid, kTileBlock, 0, as_stream(stream)>>>(x, conv_weight, hist_in, hist_out, y, state, beta_raw,
                                                              alpha_raw, a, dt_bias, out, key_heads, value_dim, eps,
                                                              host_rsqrt(key_dim));
     return check_launch("gdn_decode_step");

@@ -55,7 +55,7 @@ NAMES = [
     ("gemv_kquant_multi", "gemv per-row, several matrices of one x (matmul_dispatch_multi)"),
     ("gemv_kquant_gate_up", "gemv per-row, routed experts' gate + up (moe_expert_gate_up)"),
     ("moe_down_combine_kernel", "moe_down_combine (routed + shared down, combine)"),
-    ("gdn_step_tile", "gdn_recurrent step (decode, 32-column tiles)"),
+    ("gdn_step_tile", "gdn_recurrent step (decode, 16-column tiles)"),
     ("gdn_recurrent_v4", "gdn_recurrent step (decode, 4-column slices)"),
     ("gdn_decode_fused", "gdn_decode_step (front end + gated step, one launch)"),
     ("gdn_recurrent_g", "gdn_recurrent token loop (4096 tokens)"),

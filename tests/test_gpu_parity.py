@@ -480,12 +480,14 @@ def test_gdn_recurrent_reference_fixture():
 
 @pytest.mark.parametrize("kh,vh,dk,dv,rows", [(16, 32, 128, 128, 1), (16, 32, 128, 128, 37), (4, 8, 64, 64, 9),
                                               (2, 4, 96, 100, 5), (3, 6, 128, 256, 3), (4, 8, 64, 64, 1),
-                                              (3, 6, 128, 256, 1), (3, 6, 128, 36, 1), (2, 4, 64, 100, 1)])
+                                              (3, 6, 128, 256, 1), (3, 6, 128, 36, 1), (2, 4, 64, 100, 1),
+                                              (3, 6, 128, 48, 1), (1, 5, 64, 80, 1)])
 def test_gdn_recurrent_rows(oracle, kh, vh, dk, dv, rows):
     """Qwen3.5 GDN shape (16 key / 32 value heads of 128), a token count that is not a
     multiple of the 4-deep prefetch, key dim 64, and generic shapes (dk 96, dv 100 / 256);
-    one token on the 32-column tile (key dim 64 / 128, dv 64 / 256) and on the
-    4-column slices (dv 36 / 100)."""
+    one token on the 16-column tile (key dim 64 / 128, dv 64 / 256; dv 48 / 80, whose
+    18 / 25 tiles leave 2 / 9 outside the XCD-paired groups of 16) and on the 4-column
+    slices (dv 36 / 100)."""
     r = rng(kh * 1000 + rows)
     qkv, b, alpha, a, dt, state = _gdn_inputs(r, rows, kh, vh, dk, dv, extra=8)
     beta, decay = oracle.gdn_gate_values_rows(b, alpha, a, dt)
@@ -629,7 +631,8 @@ def test_matmul_dispatch_multi_rejects_unpaired_split():
 
 @pytest.mark.parametrize("kh,vh,dk,dv,alias", [(16, 32, 128, 128, False), (4, 8, 128, 64, False),
                                                (16, 32, 128, 128, True), (2, 4, 64, 32, False),
-                                               (2, 4, 128, 36, False), (2, 6, 128, 256, False)])
+                                               (2, 4, 128, 36, False), (2, 6, 128, 256, False),
+                                               (3, 6, 128, 48, False)])
 def test_gdn_decode_step_equals_frontend_then_gated_recurrence(kh, vh, dk, dv, alias):
     """The one-launch decode step (front end + fused-gate recurrence) gives the
     bits of gdn_frontend_rows (one row) followed by gdn_gated_recurrent_rows:
