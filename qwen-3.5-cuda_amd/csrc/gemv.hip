@@ -22,7 +22,11 @@
 // loads (contiguous, fully coalesced), then lane L decodes 32 elements of
 // block L/8 of each unit. That lane->element map is the same for every unit,
 // so the lane's 32 x values are loaded once and stay in VGPRs across all R
-// units. The dot product runs on the raw quants and the block scale is
+// units. Q4_K rows of whole units skip the LDS copy: lane L loads block L/8's
+// 16-byte header and its own 16 qs bytes straight into VGPRs (the lane's x
+// values are 128 B against 16 B of quants, so x, not the weights, is most of
+// what a CU moves; issuing it first lets each row's decode start when that
+// row's loads are back). The dot product runs on the raw quants and the block scale is
 // applied once per run of 16 (Q4_K) or 8 (Q6_K) elements:
 //   sum((d*sc*q - dmin*m) * x) = (d*sc) * sum(q*x) - (dmin*m) * sum(x)
 // which is the reference's sum re-associated (fp32 tolerance, not bit-exact:
@@ -68,27 +72,35 @@ struct LaneX {
     float s[4];    // sums of x per scale run (Q4_K: s[0], s[1]; Q6_K: 32*sum per quarter)
 };
 
+// The lane's x values only (Q4_K); lane_x_sums completes the LaneX.
+__device__ __forceinline__ void load_lane_x_values(LaneX<kQ4_K>& lx, const float* __restrict__ x, int xb, int j) {
+    const float* lo = x + static_cast<size_t>(xb) * 256 + 64 * (j >> 1) + 16 * (j & 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        lx.v[i] = ld4(lo + 4 * i);
+        lx.v[4 + i] = ld4(lo + 32 + 4 * i);
+    }
+}
+
+__device__ __forceinline__ void lane_x_sums(LaneX<kQ4_K>& lx) {
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        a += (lx.v[i].x + lx.v[i].y) + (lx.v[i].z + lx.v[i].w);
+        b += (lx.v[4 + i].x + lx.v[4 + i].y) + (lx.v[4 + i].z + lx.v[4 + i].w);
+    }
+    lx.s[0] = a;
+    lx.s[1] = b;
+    lx.s[2] = lx.s[3] = 0.f;
+}
+
 template <int TYPE>
 __device__ __forceinline__ void load_lane_x(LaneX<TYPE>& lx, const float* __restrict__ x, int xb, int j) {
-    const float* xblk = x + static_cast<size_t>(xb) * 256;
     if constexpr (TYPE == kQ4_K) {
-        const float* lo = xblk + 64 * (j >> 1) + 16 * (j & 1);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            lx.v[i] = ld4(lo + 4 * i);
-            lx.v[4 + i] = ld4(lo + 32 + 4 * i);
-        }
-        float a = 0.f, b = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            a += (lx.v[i].x + lx.v[i].y) + (lx.v[i].z + lx.v[i].w);
-            b += (lx.v[4 + i].x + lx.v[4 + i].y) + (lx.v[4 + i].z + lx.v[4 + i].w);
-        }
-        lx.s[0] = a;
-        lx.s[1] = b;
-        lx.s[2] = lx.s[3] = 0.f;
+        load_lane_x_values(lx, x, xb, j);
+        lane_x_sums(lx);
     } else {
-        const float* base = xblk + 128 * (j >> 2) + 8 * (j & 3);
+        const float* base = x + static_cast<size_t>(xb) * 256 + 128 * (j >> 2) + 8 * (j & 3);
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
             lx.v[2 * qq] = ld4(base + 32 * qq);
@@ -102,6 +114,12 @@ __device__ __forceinline__ void load_lane_x(LaneX<TYPE>& lx, const float* __rest
     }
 }
 
+// v, hidden from the optimiser (no code).
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // sum over the 4 bytes of `q` (unsigned) times 4 x values.
 __device__ __forceinline__ float dot_u8x4(uint32_t q, float4 xv, float acc) {
     acc = __builtin_fmaf(static_cast<float>(q & 0xffu), xv.x, acc);
@@ -110,43 +128,51 @@ __device__ __forceinline__ float dot_u8x4(uint32_t q, float4 xv, float acc) {
     return __builtin_fmaf(static_cast<float>(q >> 24), xv.w, acc);
 }
 
+// Contribution of one Q4_K block to lane j's partial dot product, from the
+// block's first 16 bytes (hdr: d, dmin, scales[12]) and its qs bytes
+// 16j..16j+15 (q).
+__device__ __forceinline__ float block_dot_q4k(uint4 hdr, uint4 q, const LaneX<kQ4_K>& lx, int j) {
+    const float d = half_bits(hdr.x & 0xffffu);
+    const float dmin = half_bits(hdr.x >> 16);
+    // scale_min_k4 (src/cuda/matmul_q4.cu:18-26) for sub-blocks 2g, 2g+1:
+    // sub < 4 reads bytes sub, sub+4; sub >= 4 combines byte sub+4 with the
+    // top two bits of bytes sub-4 and sub. t = sub % 4 for both pairs.
+    const int g = j >> 1;
+    const int sh = 16 * (g & 1);                 // byte 2g%4 of each scale word
+    const uint32_t a = hdr.y >> sh, b = hdr.z >> sh, c = hdr.w >> sh;
+    uint32_t sc0, m0, sc1, m1;
+    if (g < 2) {
+        sc0 = a & 63;
+        sc1 = (a >> 8) & 63;
+        m0 = b & 63;
+        m1 = (b >> 8) & 63;
+    } else {
+        sc0 = (c & 15) | ((a >> 2) & 0x30);
+        sc1 = ((c >> 8) & 15) | ((a >> 10) & 0x30);
+        m0 = ((c >> 4) & 15) | ((b >> 2) & 0x30);
+        m1 = ((c >> 12) & 15) | ((b >> 10) & 0x30);
+    }
+    float lo = 0.f, hi = 0.f;
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // opaque: the compiler would otherwise fold each mask into a bit-field
+        // extract per byte instead of one AND and four byte conversions.
+        lo = dot_u8x4(opaque_u32(w[i] & 0x0f0f0f0fu), lx.v[i], lo);
+        hi = dot_u8x4(opaque_u32((w[i] >> 4) & 0x0f0f0f0fu), lx.v[4 + i], hi);
+    }
+    const float A0 = d * static_cast<float>(sc0), B0 = dmin * static_cast<float>(m0);
+    const float A1 = d * static_cast<float>(sc1), B1 = dmin * static_cast<float>(m1);
+    return (A0 * lo - B0 * lx.s[0]) + (A1 * hi - B1 * lx.s[1]);
+}
+
 // Contribution of one block to the lane's partial dot product. `blk` points
 // at the block in LDS.
 template <int TYPE>
 __device__ __forceinline__ float block_dot(const uint8_t* blk, const LaneX<TYPE>& lx, int j) {
     if constexpr (TYPE == kQ4_K) {
-        const uint4 hdr = *reinterpret_cast<const uint4*>(blk);                // d, dmin, scales[12]
-        const uint4 q = *reinterpret_cast<const uint4*>(blk + 16 + 16 * j);   // qs bytes 16j..16j+15
-        const float d = half_bits(hdr.x & 0xffffu);
-        const float dmin = half_bits(hdr.x >> 16);
-        // scale_min_k4 (src/cuda/matmul_q4.cu:18-26) for sub-blocks 2g, 2g+1:
-        // sub < 4 reads bytes sub, sub+4; sub >= 4 combines byte sub+4 with the
-        // top two bits of bytes sub-4 and sub. t = sub % 4 for both pairs.
-        const int g = j >> 1;
-        const int sh = 16 * (g & 1);                 // byte 2g%4 of each scale word
-        const uint32_t a = hdr.y >> sh, b = hdr.z >> sh, c = hdr.w >> sh;
-        uint32_t sc0, m0, sc1, m1;
-        if (g < 2) {
-            sc0 = a & 63;
-            sc1 = (a >> 8) & 63;
-            m0 = b & 63;
-            m1 = (b >> 8) & 63;
-        } else {
-            sc0 = (c & 15) | ((a >> 2) & 0x30);
-            sc1 = ((c >> 8) & 15) | ((a >> 10) & 0x30);
-            m0 = ((c >> 4) & 15) | ((b >> 2) & 0x30);
-            m1 = ((c >> 12) & 15) | ((b >> 10) & 0x30);
-        }
-        float lo = 0.f, hi = 0.f;
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            lo = dot_u8x4(w[i] & 0x0f0f0f0fu, lx.v[i], lo);
-            hi = dot_u8x4((w[i] >> 4) & 0x0f0f0f0fu, lx.v[4 + i], hi);
-        }
-        const float A0 = d * static_cast<float>(sc0), B0 = dmin * static_cast<float>(m0);
-        const float A1 = d * static_cast<float>(sc1), B1 = dmin * static_cast<float>(m1);
-        return (A0 * lo - B0 * lx.s[0]) + (A1 * hi - B1 * lx.s[1]);
+        return block_dot_q4k(*reinterpret_cast<const uint4*>(blk), *reinterpret_cast<const uint4*>(blk + 16 + 16 * j),
+                             lx, j);
     } else {
         const int half = j >> 2, l0 = 8 * (j & 3);
         const uint8_t* qla = blk + 64 * half + l0;         // quarters 0 (low nibble), 2 (high)
@@ -214,6 +240,42 @@ __device__ __forceinline__ int64_t out_index(int64_t m, int M, int split) {
     if (split <= 0) return m;
     const int64_t pair = m / (2 * split), r = m - pair * 2 * split;
     return r < split ? pair * split + r : M / 2 + pair * split + (r - split);
+}
+
+// Q4_K direct form of gemv_kquant_body: NS (1 or 2) consecutive slices s, s+1
+// of R rows from g0 (row = min(g0 + u, groups - 1)), added to acc[u] in slice
+// order. Straight-line code, so the compiler's load counters know how many
+// loads follow each one and a row's decode waits only for what it reads.
+template <int R, int NS>
+__device__ __forceinline__ void q4k_direct_slices(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                  float (&acc)[R], int nb, uint64_t ub0, int g0, int groups,
+                                                  uint64_t tensor_bytes, int s, int b, int j) {
+    constexpr int BB = KQuant<kQ4_K>::kBlockBytes;
+    LaneX<kQ4_K> lx[NS];
+#pragma unroll
+    for (int h = 0; h < NS; ++h) load_lane_x_values(lx[h], x, 8 * (s + h) + b, j);
+    __builtin_amdgcn_sched_barrier(0);   // the x loads first
+    uint4 hd[R][NS], qv[R][NS];
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const int g = min(g0 + u, groups - 1);
+#pragma unroll
+        for (int h = 0; h < NS; ++h) {
+            const uint64_t bh = (ub0 + static_cast<uint64_t>(g) * nb + 8 * (s + h) + b) * BB;
+            // In range whenever the caller validated the shape; a block past the
+            // tensor would read block 0 instead of faulting.
+            const uint64_t bs = bh + BB <= tensor_bytes ? bh : 0;
+            hd[u][h] = ld16_nt(w + bs);
+            qv[u][h] = ld16_nt(w + bs + 16 + 16 * j);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);   // every load issued before the x sums
+#pragma unroll
+    for (int h = 0; h < NS; ++h) lane_x_sums(lx[h]);
+#pragma unroll
+    for (int u = 0; u < R; ++u)
+#pragma unroll
+        for (int h = 0; h < NS; ++h) acc[u] += block_dot_q4k(hd[u][h], qv[u][h], lx[h], j);
 }
 
 // Fast path. Row groups: when 8 | nb, group = one row and unit (row, slice s)
@@ -312,6 +374,51 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant(const uint8_t* __restr
     gemv_kquant_body<TYPE, R>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, blockIdx.y);
 }
 
+// The Q4_K direct form of gemv_kquant_body for rows of whole units (8 | nb):
+// same row groups, expert selection, lane map, block_dot_q4k and summation
+// order (so the same bits), with the lane's quants loaded straight into VGPRs
+// by q4k_direct_slices, NS (1 or 2, NS | nb / 8) slices at a time. Its own
+// kernels, so that the LDS-staged form's registers do not count against it.
+template <int R, int NS>
+__device__ __forceinline__ void q4k_direct_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                float* __restrict__ y, int M, int nb, uint64_t ub0, int groups,
+                                                uint64_t tensor_bytes, const Experts& ex, int sel, int split = 0) {
+    const int lane = threadIdx.x & 63;
+    const int wv = wave_in_block();
+    const int g0 = (blockIdx.x * kGemvWaves + wv) * R;
+    const int b = lane >> 3, j = lane & 7;
+    const int S = nb >> 3;
+    uint64_t eoff = 0;
+    int64_t x_off, y_off;
+    const bool ok_e = select_expert(ex, sel, M, x_off, y_off, eoff);
+    x += x_off;
+    y += y_off;
+    if (!ok_e) {
+        if (lane < R && g0 + lane < M) y[g0 + lane] = __builtin_nanf("");
+        return;
+    }
+    ub0 += eoff / 256;
+    float acc[R];
+#pragma unroll
+    for (int u = 0; u < R; ++u) acc[u] = 0.f;
+    for (int s = 0; s < S; s += NS) q4k_direct_slices<R, NS>(w, x, acc, nb, ub0, g0, groups, tensor_bytes, s, b, j);
+    float out = 0.f;
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const float t = group_sum<64>(acc[u]);
+        if (lane == u) out = t;
+    }
+    if (lane < R && g0 + lane < M) y[out_index(g0 + lane, M, split)] = out;
+}
+
+template <int R, int NS>
+__global__ __launch_bounds__(kGemvBlock) void gemv_q4k_direct(const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ x, float* __restrict__ y,
+                                                              int M, int nb, uint64_t ub0, int groups,
+                                                              uint64_t tensor_bytes, Experts ex) {
+    q4k_direct_body<R, NS>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, blockIdx.y);
+}
+
 // The routed experts' gate and up projections of one token in one launch:
 // launch rows 0 .. n_sel-1 run the gate tensor, n_sel .. 2 n_sel-1 the up
 // tensor, each for selection slot blockIdx.y mod n_sel (uniform per workgroup).
@@ -324,6 +431,18 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant_gate_up(const uint8_t*
     const bool up = static_cast<int>(blockIdx.y) >= n_sel;
     gemv_kquant_body<TYPE, R>(up ? wu : wg, x, up ? yu : yg, M, nb, 0, groups, tensor_bytes, ex,
                               up ? static_cast<int>(blockIdx.y) - n_sel : static_cast<int>(blockIdx.y));
+}
+
+template <int R, int NS>
+__global__ __launch_bounds__(kGemvBlock) void gemv_q4k_direct_gate_up(const uint8_t* __restrict__ wg,
+                                                                      const uint8_t* __restrict__ wu,
+                                                                      const float* __restrict__ x,
+                                                                      float* __restrict__ yg, float* __restrict__ yu,
+                                                                      int M, int nb, int groups,
+                                                                      uint64_t tensor_bytes, Experts ex, int n_sel) {
+    const bool up = static_cast<int>(blockIdx.y) >= n_sel;
+    q4k_direct_body<R, NS>(up ? wu : wg, x, up ? yu : yg, M, nb, 0, groups, tensor_bytes, ex,
+                           up ? static_cast<int>(blockIdx.y) - n_sel : static_cast<int>(blockIdx.y));
 }
 
 // The SwiGLU hidden rows of a MoE layer in one launch: h = SiLU(Wg x) * (Wu x)
@@ -466,6 +585,15 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant_multi(const float* __r
     if (static_cast<int64_t>(blockIdx.x) * kGemvWaves * R >= m.groups) return;   // uniform per workgroup
     gemv_kquant_body<TYPE, R>(m.w, x, m.y, m.M, nb, m.ub0, m.groups, m.tensor_bytes, Experts{nullptr, 0, 0, 0}, 0,
                               m.split);
+}
+
+template <int R, int NS>
+__global__ __launch_bounds__(kGemvBlock) void gemv_q4k_direct_multi(const float* __restrict__ x, int nb,
+                                                                    GemvMulti mu) {
+    const GemvMat& m = mu.d[blockIdx.y];
+    if (static_cast<int64_t>(blockIdx.x) * kGemvWaves * R >= m.groups) return;   // uniform per workgroup
+    q4k_direct_body<R, NS>(m.w, x, m.y, m.M, nb, m.ub0, m.groups, m.tensor_bytes, Experts{nullptr, 0, 0, 0}, 0,
+                           m.split);
 }
 
 // ------------------------------------------------------------ MoE down + combine
@@ -1029,10 +1157,17 @@ template <int TYPE, int R>
 void launch_kquant(const uint8_t* w, const float* x, float* y, int M, int nb, uint64_t ub0, int groups,
                    uint64_t tensor_bytes, const Experts& ex, int n_sel, hipStream_t s) {
     constexpr int CPU = KQuant<TYPE>::kBlockBytes * 8 / 16;
-    const size_t lds = static_cast<size_t>(kGemvWaves) * R * CPU * 16;
     const int waves = (groups + R - 1) / R;
-    gemv_kquant<TYPE, R><<<dim3(blocks_for(waves, kGemvWaves), n_sel), kGemvBlock, lds, s>>>(
-        w, x, y, M, nb, ub0, groups, tensor_bytes, ex);
+    const dim3 grid(blocks_for(waves, kGemvWaves), n_sel);
+    if (TYPE == kQ4_K && nb >= 8) {   // rows of whole units: the direct form
+        if ((nb / 8) % 2 == 0)
+            gemv_q4k_direct<R, 2><<<grid, kGemvBlock, 0, s>>>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex);
+        else
+            gemv_q4k_direct<R, 1><<<grid, kGemvBlock, 0, s>>>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex);
+        return;
+    }
+    const size_t lds = static_cast<size_t>(kGemvWaves) * R * CPU * 16;
+    gemv_kquant<TYPE, R><<<grid, kGemvBlock, lds, s>>>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex);
 }
 
 template <int TYPE>
@@ -1040,10 +1175,14 @@ void dispatch_kquant(const uint8_t* w, const float* x, float* y, int M, int nb, 
                      uint64_t tensor_bytes, const Experts& ex, int n_sel, hipStream_t s) {
     // Units per wave: enough waves to fill 256 CUs several times over. More than
     // 4 units per wave measured slower (fewer waves per SIMD to hide latency).
+    // Q4_K rows of two or more units (K >= 4096) load all of a row's units at
+    // once: 2 rows per wave from 4096 units (measured at 2048 x 4096: 3.8 us
+    // against 4.3 with 1 row per wave).
     const int64_t all = static_cast<int64_t>(groups) * n_sel;
+    const bool multi_unit = TYPE == kQ4_K && nb >= 16;
     if (all >= 4 * 4096)
         launch_kquant<TYPE, 4>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, n_sel, s);
-    else if (all >= 2 * 4096)
+    else if (all >= 2 * 4096 || (multi_unit && all * (nb / 8) >= 4096))
         launch_kquant<TYPE, 2>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, n_sel, s);
     else
         launch_kquant<TYPE, 1>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, n_sel, s);
@@ -1104,10 +1243,18 @@ bool kquant_rowpath(const uint8_t* w, int type, uint64_t num_elements, const flo
 template <int TYPE, int R>
 void launch_multi_r(const GemvMulti& mu, int n, const float* x, int nb, hipStream_t s) {
     constexpr int CPU = KQuant<TYPE>::kBlockBytes * 8 / 16;
-    const size_t lds = static_cast<size_t>(kGemvWaves) * R * CPU * 16;
     int64_t gx = 1;
     for (int j = 0; j < n; ++j) gx = std::max<int64_t>(gx, blocks_for((mu.d[j].groups + R - 1) / R, kGemvWaves));
-    gemv_kquant_multi<TYPE, R><<<dim3(static_cast<unsigned>(gx), n), kGemvBlock, lds, s>>>(x, nb, mu);
+    const dim3 grid(static_cast<unsigned>(gx), n);
+    if (TYPE == kQ4_K && nb >= 8) {   // rows of whole units: the direct form
+        if ((nb / 8) % 2 == 0)
+            gemv_q4k_direct_multi<R, 2><<<grid, kGemvBlock, 0, s>>>(x, nb, mu);
+        else
+            gemv_q4k_direct_multi<R, 1><<<grid, kGemvBlock, 0, s>>>(x, nb, mu);
+        return;
+    }
+    const size_t lds = static_cast<size_t>(kGemvWaves) * R * CPU * 16;
+    gemv_kquant_multi<TYPE, R><<<grid, kGemvBlock, lds, s>>>(x, nb, mu);
 }
 
 // Up to kMultiMax matrices of one K-quant type, each on the per-row path.
@@ -1127,10 +1274,20 @@ template <int TYPE, int R>
 void launch_gate_up_r(const uint8_t* wg, const uint8_t* wu, const float* x, float* yg, float* yu, int M, int nb,
                       int groups, uint64_t tensor_bytes, const Experts& ex, int n_sel, hipStream_t s) {
     constexpr int CPU = KQuant<TYPE>::kBlockBytes * 8 / 16;
-    const size_t lds = static_cast<size_t>(kGemvWaves) * R * CPU * 16;
     const int waves = (groups + R - 1) / R;
-    gemv_kquant_gate_up<TYPE, R><<<dim3(blocks_for(waves, kGemvWaves), 2 * n_sel), kGemvBlock, lds, s>>>(
-        wg, wu, x, yg, yu, M, nb, groups, tensor_bytes, ex, n_sel);
+    const dim3 grid(blocks_for(waves, kGemvWaves), 2 * n_sel);
+    if (TYPE == kQ4_K && nb >= 8) {   // rows of whole units: the direct form
+        if ((nb / 8) % 2 == 0)
+            gemv_q4k_direct_gate_up<R, 2><<<grid, kGemvBlock, 0, s>>>(wg, wu, x, yg, yu, M, nb, groups,
+                                                                       tensor_bytes, ex, n_sel);
+        else
+            gemv_q4k_direct_gate_up<R, 1><<<grid, kGemvBlock, 0, s>>>(wg, wu, x, yg, yu, M, nb, groups,
+                                                                       tensor_bytes, ex, n_sel);
+        return;
+    }
+    const size_t lds = static_cast<size_t>(kGemvWaves) * R * CPU * 16;
+    gemv_kquant_gate_up<TYPE, R><<<grid, kGemvBlock, lds, s>>>(wg, wu, x, yg, yu, M, nb, groups, tensor_bytes, ex,
+                                                              n_sel);
 }
 
 // Units per wave as dispatch_kquant picks them for the 2 n_sel matrices.
