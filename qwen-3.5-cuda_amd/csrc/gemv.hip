@@ -244,16 +244,26 @@ __device__ __forceinline__ int64_t out_index(int64_t m, int M, int split) {
 
 // Q4_K direct form of gemv_kquant_body: NS (1 or 2) consecutive slices s, s+1
 // of R rows from g0 (row = min(g0 + u, groups - 1)), added to acc[u] in slice
-// order. Straight-line code, so the compiler's load counters know how many
-// loads follow each one and a row's decode waits only for what it reads.
+// order. Every thread of the workgroup calls it (one barrier). The slices' x
+// values (NS x 8 KB) are loaded once per workgroup, 2 NS float4 per thread,
+// before the weights, and staged in xs; then each lane loads block L/8's
+// 16-byte header and its own 16 qs bytes of every row straight into VGPRs.
+// Every wave of every workgroup reads the same x, so the lines holding it are
+// the L2's busiest: loaded per wave (8 KB each) x took longer to arrive than
+// the weights (measured at 8192 x 2048: ~2 us into a ~3 us wave), loaded per
+// workgroup the request count is a quarter.
 template <int R, int NS>
 __device__ __forceinline__ void q4k_direct_slices(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                  float (&acc)[R], int nb, uint64_t ub0, int g0, int groups,
-                                                  uint64_t tensor_bytes, int s, int b, int j) {
+                                                  float4* xs, float (&acc)[R], int nb, uint64_t ub0, int g0,
+                                                  int groups, uint64_t tensor_bytes, int s, int b, int j) {
     constexpr int BB = KQuant<kQ4_K>::kBlockBytes;
-    LaneX<kQ4_K> lx[NS];
+    constexpr int NX = NS * 512;                    // float4 of x in the NS slices
+    constexpr int PER = NX / kGemvBlock;
+    static_assert(PER * kGemvBlock == NX, "x staging");
+    float4 xt[PER];
+    const float* xsl = x + static_cast<size_t>(s) * 2048;
 #pragma unroll
-    for (int h = 0; h < NS; ++h) load_lane_x_values(lx[h], x, 8 * (s + h) + b, j);
+    for (int i = 0; i < PER; ++i) xt[i] = ld4(xsl + 4 * (threadIdx.x + i * kGemvBlock));
     __builtin_amdgcn_sched_barrier(0);   // the x loads first
     uint4 hd[R][NS], qv[R][NS];
 #pragma unroll
@@ -269,9 +279,22 @@ __device__ __forceinline__ void q4k_direct_slices(const uint8_t* __restrict__ w,
             qv[u][h] = ld16_nt(w + bs + 16 + 16 * j);
         }
     }
-    __builtin_amdgcn_sched_barrier(0);   // every load issued before the x sums
+    __builtin_amdgcn_sched_barrier(0);   // every load issued before the staging
 #pragma unroll
-    for (int h = 0; h < NS; ++h) lane_x_sums(lx[h]);
+    for (int i = 0; i < PER; ++i) xs[threadIdx.x + i * kGemvBlock] = xt[i];
+    __syncthreads();
+    LaneX<kQ4_K> lx[NS];
+#pragma unroll
+    for (int h = 0; h < NS; ++h) {
+        // load_lane_x_values' elements, from the staged copy
+        const float4* lo = xs + (h * 2048 + b * 256 + 64 * (j >> 1) + 16 * (j & 1)) / 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lx[h].v[i] = lo[i];
+            lx[h].v[4 + i] = lo[8 + i];
+        }
+        lane_x_sums(lx[h]);
+    }
 #pragma unroll
     for (int u = 0; u < R; ++u)
 #pragma unroll
@@ -379,6 +402,8 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant(const uint8_t* __restr
 // order (so the same bits), with the lane's quants loaded straight into VGPRs
 // by q4k_direct_slices, NS (1 or 2, NS | nb / 8) slices at a time. Its own
 // kernels, so that the LDS-staged form's registers do not count against it.
+// Every exit before the slices is uniform per workgroup (the expert slot is
+// blockIdx.y), so every thread that reaches a barrier has company.
 template <int R, int NS>
 __device__ __forceinline__ void q4k_direct_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                 float* __restrict__ y, int M, int nb, uint64_t ub0, int groups,
@@ -398,10 +423,14 @@ __device__ __forceinline__ void q4k_direct_body(const uint8_t* __restrict__ w, c
         return;
     }
     ub0 += eoff / 256;
+    __shared__ float4 xs[NS * 512];
     float acc[R];
 #pragma unroll
     for (int u = 0; u < R; ++u) acc[u] = 0.f;
-    for (int s = 0; s < S; s += NS) q4k_direct_slices<R, NS>(w, x, acc, nb, ub0, g0, groups, tensor_bytes, s, b, j);
+    for (int s = 0; s < S; s += NS) {
+        if (s > 0) __syncthreads();   // every wave is done with the previous slices' x
+        q4k_direct_slices<R, NS>(w, x, xs, acc, nb, ub0, g0, groups, tensor_bytes, s, b, j);
+    }
     float out = 0.f;
 #pragma unroll
     for (int u = 0; u < R; ++u) {
