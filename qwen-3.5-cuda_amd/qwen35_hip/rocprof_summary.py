@@ -49,6 +49,12 @@ NAMES = [
     # next rows (kernel symbols; several bench shapes can share one instantiation)
     ("gemv_mfma<14, 2>", "gemv Q6_K MFMA, 2-block k-slices (LM head)"),
     ("gemv_mfma<12, 2>", "gemv Q4_K MFMA, 2-block k-slices"),
+    ("gemv_q4k_direct_multi", "gemv Q4_K direct, several matrices of one x (matmul_dispatch_multi)"),
+    ("gemv_q4k_direct_gate_up", "gemv Q4_K direct, routed experts' gate + up (moe_expert_gate_up)"),
+    ("gemv_q4k_direct<2, 1>", "gemv Q4_K direct, 2 rows/wave (GDN qkv)"),
+    ("gemv_q4k_direct<2, 2>", "gemv Q4_K direct, 2 rows/wave, 2-unit rows (out proj)"),
+    ("gemv_q4k_direct<1, 1>", "gemv Q4_K direct, 1 row/wave (experts)"),
+    ("gemv_q4k_direct", "gemv Q4_K direct, other shapes"),
     ("gemv_kquant<14, 4>", "gemv Q6_K per-row, 4 units/wave"),
     ("gemv_kquant<12, 2>", "gemv Q4_K per-row, 2 units/wave (GDN qkv)"),
     ("gemv_kquant<12, 1>", "gemv Q4_K per-row, 1 unit/wave (out proj, experts)"),
