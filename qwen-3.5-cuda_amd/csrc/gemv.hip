@@ -252,9 +252,9 @@ __device__ __forceinline__ int64_t out_index(int64_t m, int M, int split) {
 // the L2's busiest: loaded per wave (8 KB each) x took longer to arrive than
 // the weights (measured at 8192 x 2048: ~2 us into a ~3 us wave), loaded per
 // workgroup the request count is a quarter.
-template <int R, int NS>
-__device__ __forceinline__ void q4k_direct_slices(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                  float4* xs, float (&acc)[R], int nb, uint64_t ub0, int g0,
+template <int R, int NS, int MAT = 1>
+__device__ __forceinline__ void q4k_direct_slices(const uint8_t* const (&w)[MAT], const float* __restrict__ x,
+                                                  float4* xs, float (&acc)[MAT][R], int nb, uint64_t ub0, int g0,
                                                   int groups, uint64_t tensor_bytes, int s, int b, int j) {
     constexpr int BB = KQuant<kQ4_K>::kBlockBytes;
     constexpr int NX = NS * 512;                    // float4 of x in the NS slices
@@ -265,20 +265,22 @@ __device__ __forceinline__ void q4k_direct_slices(const uint8_t* __restrict__ w,
 #pragma unroll
     for (int i = 0; i < PER; ++i) xt[i] = ld4(xsl + 4 * (threadIdx.x + i * kGemvBlock));
     __builtin_amdgcn_sched_barrier(0);   // the x loads first
-    uint4 hd[R][NS], qv[R][NS];
+    uint4 hd[MAT][R][NS], qv[MAT][R][NS];
 #pragma unroll
-    for (int u = 0; u < R; ++u) {
-        const int g = min(g0 + u, groups - 1);
+    for (int mt = 0; mt < MAT; ++mt)
 #pragma unroll
-        for (int h = 0; h < NS; ++h) {
-            const uint64_t bh = (ub0 + static_cast<uint64_t>(g) * nb + 8 * (s + h) + b) * BB;
-            // In range whenever the caller validated the shape; a block past the
-            // tensor would read block 0 instead of faulting.
-            const uint64_t bs = bh + BB <= tensor_bytes ? bh : 0;
-            hd[u][h] = ld16_nt(w + bs);
-            qv[u][h] = ld16_nt(w + bs + 16 + 16 * j);
+        for (int u = 0; u < R; ++u) {
+            const int g = min(g0 + u, groups - 1);
+#pragma unroll
+            for (int h = 0; h < NS; ++h) {
+                const uint64_t bh = (ub0 + static_cast<uint64_t>(g) * nb + 8 * (s + h) + b) * BB;
+                // In range whenever the caller validated the shape; a block past
+                // the tensor would read block 0 instead of faulting.
+                const uint64_t bs = bh + BB <= tensor_bytes ? bh : 0;
+                hd[mt][u][h] = ld16_nt(w[mt] + bs);
+                qv[mt][u][h] = ld16_nt(w[mt] + bs + 16 + 16 * j);
+            }
         }
-    }
     __builtin_amdgcn_sched_barrier(0);   // every load issued before the staging
 #pragma unroll
     for (int i = 0; i < PER; ++i) xs[threadIdx.x + i * kGemvBlock] = xt[i];
@@ -296,9 +298,11 @@ __device__ __forceinline__ void q4k_direct_slices(const uint8_t* __restrict__ w,
         lane_x_sums(lx[h]);
     }
 #pragma unroll
-    for (int u = 0; u < R; ++u)
+    for (int mt = 0; mt < MAT; ++mt)
 #pragma unroll
-        for (int h = 0; h < NS; ++h) acc[u] += block_dot_q4k(hd[u][h], qv[u][h], lx[h], j);
+        for (int u = 0; u < R; ++u)
+#pragma unroll
+            for (int h = 0; h < NS; ++h) acc[mt][u] += block_dot_q4k(hd[mt][u][h], qv[mt][u][h], lx[h], j);
 }
 
 // Fast path. Row groups: when 8 | nb, group = one row and unit (row, slice s)
@@ -424,17 +428,18 @@ __device__ __forceinline__ void q4k_direct_body(const uint8_t* __restrict__ w, c
     }
     ub0 += eoff / 256;
     __shared__ float4 xs[NS * 512];
-    float acc[R];
+    float acc[1][R];
 #pragma unroll
-    for (int u = 0; u < R; ++u) acc[u] = 0.f;
+    for (int u = 0; u < R; ++u) acc[0][u] = 0.f;
+    const uint8_t* const wm[1] = {w};
     for (int s = 0; s < S; s += NS) {
         if (s > 0) __syncthreads();   // every wave is done with the previous slices' x
-        q4k_direct_slices<R, NS>(w, x, xs, acc, nb, ub0, g0, groups, tensor_bytes, s, b, j);
+        q4k_direct_slices<R, NS>(wm, x, xs, acc, nb, ub0, g0, groups, tensor_bytes, s, b, j);
     }
     float out = 0.f;
 #pragma unroll
     for (int u = 0; u < R; ++u) {
-        const float t = group_sum<64>(acc[u]);
+        const float t = group_sum<64>(acc[0][u]);
         if (lane == u) out = t;
     }
     if (lane < R && g0 + lane < M) y[out_index(g0 + lane, M, split)] = out;
@@ -500,23 +505,15 @@ struct RouteJob {
     float* w;              // out: their softmax weights
 };
 
-template <int TYPE, int R, int VPL>
-__global__ __launch_bounds__(kGemvBlock) void gemv_kquant_swiglu(const float* __restrict__ x, int nb, PairJob routed,
-                                                                 PairJob shared, int n_sel, RouteJob rt) {
-    constexpr int BB = KQuant<TYPE>::kBlockBytes;
-    constexpr int UB = 8 * BB;
-    constexpr int CPU = UB / 16;
-    constexpr int NC = (2 * R * CPU + kWave - 1) / kWave;
-    extern __shared__ uint4 gemv_stage[];
-    const bool sh = static_cast<int>(blockIdx.y) == n_sel;
-    const PairJob& jb = sh ? shared : routed;
-    if (static_cast<int64_t>(blockIdx.x) * kGemvWaves * R >= jb.M) return;   // uniform per workgroup
-    const int lane = threadIdx.x & 63;
-    const int wv = wave_in_block();
-    uint4* slot = gemv_stage + wv * (2 * R * CPU);
-    const int g0 = (blockIdx.x * kGemvWaves + wv) * R;
-    const int b = lane >> 3, j = lane & 7;
-    const int S = nb >> 3;
+// The part of a SwiGLU launch before its rows: with VPL > 0 the routing (wave 0
+// of every routed workgroup runs the top-k into LDS, workgroup (0, 0) writes the
+// ids and weights out), then the expert selection of the workgroup's launch row.
+// Sets h (the output rows) and ub (the expert's first block); false (after
+// writing NaN rows) when the expert id is invalid. Every decision is uniform per
+// workgroup.
+template <int R, int VPL>
+__device__ __forceinline__ bool swiglu_setup(const PairJob& jb, bool sh, int n_sel, const RouteJob& rt, int lane,
+                                             int wv, int g0, float*& h, uint64_t& ub) {
     Experts ex = jb.ex;
     if constexpr (VPL > 0) {
         __shared__ int32_t sidx[kWave];
@@ -543,12 +540,35 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant_swiglu(const float* __
     uint64_t eoff = 0;
     int64_t x_off, y_off;
     const bool ok_e = select_expert(ex, sh ? 0 : static_cast<int>(blockIdx.y), jb.M, x_off, y_off, eoff);
-    float* h = jb.h + y_off;
+    h = jb.h + y_off;
     if (!ok_e) {
         if (lane < R && g0 + lane < jb.M) h[g0 + lane] = __builtin_nanf("");
-        return;
+        return false;
     }
-    const uint64_t ub = eoff / 256;
+    ub = eoff / 256;
+    return true;
+}
+
+template <int TYPE, int R, int VPL>
+__global__ __launch_bounds__(kGemvBlock) void gemv_kquant_swiglu(const float* __restrict__ x, int nb, PairJob routed,
+                                                                 PairJob shared, int n_sel, RouteJob rt) {
+    constexpr int BB = KQuant<TYPE>::kBlockBytes;
+    constexpr int UB = 8 * BB;
+    constexpr int CPU = UB / 16;
+    constexpr int NC = (2 * R * CPU + kWave - 1) / kWave;
+    extern __shared__ uint4 gemv_stage[];
+    const bool sh = static_cast<int>(blockIdx.y) == n_sel;
+    const PairJob& jb = sh ? shared : routed;
+    if (static_cast<int64_t>(blockIdx.x) * kGemvWaves * R >= jb.M) return;   // uniform per workgroup
+    const int lane = threadIdx.x & 63;
+    const int wv = wave_in_block();
+    uint4* slot = gemv_stage + wv * (2 * R * CPU);
+    const int g0 = (blockIdx.x * kGemvWaves + wv) * R;
+    const int b = lane >> 3, j = lane & 7;
+    const int S = nb >> 3;
+    float* h;
+    uint64_t ub;
+    if (!swiglu_setup<R, VPL>(jb, sh, n_sel, rt, lane, wv, g0, h, ub)) return;   // uniform per workgroup
 
     float ag[R], au[R];
 #pragma unroll
@@ -586,6 +606,43 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant_swiglu(const float* __
     for (int u = 0; u < R; ++u) {
         const float tg = group_sum<64>(ag[u]);
         const float tu = group_sum<64>(au[u]);
+        if (lane == u) out = silu(tg) * tu;
+    }
+    if (lane < R && g0 + lane < jb.M) h[g0 + lane] = out;
+}
+
+// gemv_kquant_swiglu for Q4_K in the direct form (q4k_direct_slices with the
+// gate and up rows of the wave, one staged x for both): same rows, reductions
+// and bits.
+template <int R, int NS, int VPL>
+__global__ __launch_bounds__(kGemvBlock) void gemv_q4k_direct_swiglu(const float* __restrict__ x, int nb,
+                                                                     PairJob routed, PairJob shared, int n_sel,
+                                                                     RouteJob rt) {
+    const bool sh = static_cast<int>(blockIdx.y) == n_sel;
+    const PairJob& jb = sh ? shared : routed;
+    if (static_cast<int64_t>(blockIdx.x) * kGemvWaves * R >= jb.M) return;   // uniform per workgroup
+    const int lane = threadIdx.x & 63;
+    const int wv = wave_in_block();
+    const int g0 = (blockIdx.x * kGemvWaves + wv) * R;
+    const int b = lane >> 3, j = lane & 7;
+    const int S = nb >> 3;
+    float* h;
+    uint64_t ub;
+    if (!swiglu_setup<R, VPL>(jb, sh, n_sel, rt, lane, wv, g0, h, ub)) return;   // uniform per workgroup
+    __shared__ float4 xs[NS * 512];
+    float acc[2][R];
+#pragma unroll
+    for (int u = 0; u < R; ++u) acc[0][u] = acc[1][u] = 0.f;
+    const uint8_t* const wm[2] = {jb.wg, jb.wu};
+    for (int s = 0; s < S; s += NS) {
+        if (s > 0) __syncthreads();   // every wave is done with the previous slices' x
+        q4k_direct_slices<R, NS, 2>(wm, x, xs, acc, nb, ub, g0, jb.M, ~uint64_t{0}, s, b, j);
+    }
+    float out = 0.f;
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const float tg = group_sum<64>(acc[0][u]);
+        const float tu = group_sum<64>(acc[1][u]);
         if (lane == u) out = silu(tg) * tu;
     }
     if (lane < R && g0 + lane < jb.M) h[g0 + lane] = out;
@@ -1373,12 +1430,18 @@ template <int TYPE, int R, int VPL>
 void launch_swiglu_r(const float* x, int nb, const PairJob& routed, const PairJob& shared, int n_sel,
                      const RouteJob& rt, hipStream_t s) {
     constexpr int CPU = KQuant<TYPE>::kBlockBytes * 8 / 16;
-    const size_t lds = static_cast<size_t>(kGemvWaves) * 2 * R * CPU * 16;
     const int rows = std::max(n_sel > 0 ? routed.M : 0, shared.M);
     const int rows_y = n_sel + (shared.M > 0 ? 1 : 0);
-    gemv_kquant_swiglu<TYPE, R, VPL>
-        <<<dim3(blocks_for((rows + R - 1) / R, kGemvWaves), rows_y), kGemvBlock, lds, s>>>(x, nb, routed, shared,
-                                                                                          n_sel, rt);
+    const dim3 grid(blocks_for((rows + R - 1) / R, kGemvWaves), rows_y);
+    if (TYPE == kQ4_K) {   // rows of whole units (8 | nb here): the direct form
+        if ((nb / 8) % 2 == 0)
+            gemv_q4k_direct_swiglu<R, 2, VPL><<<grid, kGemvBlock, 0, s>>>(x, nb, routed, shared, n_sel, rt);
+        else
+            gemv_q4k_direct_swiglu<R, 1, VPL><<<grid, kGemvBlock, 0, s>>>(x, nb, routed, shared, n_sel, rt);
+        return;
+    }
+    const size_t lds = static_cast<size_t>(kGemvWaves) * 2 * R * CPU * 16;
+    gemv_kquant_swiglu<TYPE, R, VPL><<<grid, kGemvBlock, lds, s>>>(x, nb, routed, shared, n_sel, rt);
 }
 
 template <int TYPE, int VPL>
