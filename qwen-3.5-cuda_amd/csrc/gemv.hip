@@ -783,6 +783,112 @@ __global__ __launch_bounds__(kGemvBlock) void moe_down_combine_kernel(
     }
 }
 
+// moe_down_combine_kernel for Q4_K routed and shared tensors: the same rows,
+// lane map, block_dot_q4k, reductions and combine (so the same bits), with
+// every wave's quants loaded straight into VGPRs (144-byte blocks are 16-byte
+// aligned: lane L takes block L/8's header and its own 16 qs bytes) and the
+// hidden rows the workgroup reads -- routed rows 0 .. 4 KT - 1 (row j clamped to
+// k - 1) and the shared row -- loaded once per workgroup, before the weights,
+// and staged in LDS (loaded per wave they were 3x the weight bytes, and every
+// workgroup reads the same rows).
+template <int KT, int SS>
+__global__ __launch_bounds__(kGemvBlock) void moe_down_combine_q4k(
+        const uint8_t* __restrict__ wd, uint64_t expert_blocks, int n_experts, const int32_t* __restrict__ idx,
+        const float* __restrict__ wts, int k, const float* __restrict__ hid, const uint8_t* __restrict__ wsd,
+        const float* __restrict__ shid, const float* __restrict__ slogit, float* __restrict__ out) {
+    constexpr int BB = KQuant<kQ4_K>::kBlockBytes;
+    constexpr int NXR = 4 * KT * (kDcInter / 4);   // float4 of the routed hidden rows
+    constexpr int NXS = SS * 512;                  // float4 of the shared hidden row (2048 SS)
+    constexpr int PR = NXR / kGemvBlock, PS = NXS / kGemvBlock;
+    static_assert(PR * kGemvBlock == NXR && PS * kGemvBlock == NXS, "x staging");
+    __shared__ float4 xr[NXR];
+    __shared__ float4 xsh[NXS];
+    __shared__ float part[4 * KT][4];
+    __shared__ float spart[4];
+    const int lane = threadIdx.x & 63, w = wave_in_block();
+    const int b = lane >> 3, jj = lane & 7;
+    const int q = blockIdx.x;
+
+    float4 tr[PR], ts[PS];
+#pragma unroll
+    for (int i = 0; i < PR; ++i) {
+        const int c = threadIdx.x + i * kGemvBlock;
+        const int jr = min(c / (kDcInter / 4), k - 1);
+        tr[i] = ld4(hid + static_cast<size_t>(jr) * kDcInter + 4 * (c % (kDcInter / 4)));
+    }
+#pragma unroll
+    for (int i = 0; i < PS; ++i) ts[i] = ld4(shid + 4 * (threadIdx.x + i * kGemvBlock));
+    __builtin_amdgcn_sched_barrier(0);   // the hidden rows first
+
+    uint4 he[KT], qe[KT], hs[SS], qs[SS];
+    bool valid[KT];
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+        const int j = w + 4 * t;
+        const int e = j < k ? idx[j] : 0;
+        valid[t] = e >= 0 && e < n_experts;
+        const uint8_t* blk = wd + (static_cast<uint64_t>(valid[t] ? e : 0) * expert_blocks + 8 * q + b) * BB;
+        he[t] = ld16_nt(blk);
+        qe[t] = ld16_nt(blk + 16 + 16 * jj);
+    }
+    const int row = 4 * q + w;
+#pragma unroll
+    for (int s = 0; s < SS; ++s) {
+        const uint8_t* blk = wsd + (static_cast<uint64_t>(row) * 8 * SS + 8 * s + b) * BB;
+        hs[s] = ld16_nt(blk);
+        qs[s] = ld16_nt(blk + 16 + 16 * jj);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // every load issued before the staging
+#pragma unroll
+    for (int i = 0; i < PR; ++i) xr[threadIdx.x + i * kGemvBlock] = tr[i];
+#pragma unroll
+    for (int i = 0; i < PS; ++i) xsh[threadIdx.x + i * kGemvBlock] = ts[i];
+    __syncthreads();
+
+    const int xo = 64 * (jj >> 1) + 16 * (jj & 1);   // load_lane_x_values' offsets in a 256-element block
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+        const int j = w + 4 * t;
+        LaneX<kQ4_K> lx;
+        const float4* lo = xr + (min(j, k - 1) * kDcInter + (b & 1) * 256 + xo) / 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lx.v[i] = lo[i];
+            lx.v[4 + i] = lo[8 + i];
+        }
+        lane_x_sums(lx);
+        float a = 0.f;
+        a += block_dot_q4k(he[t], qe[t], lx, jj);
+        a = group_sum<16>(a);
+        if (j < k && (lane & 15) == 0) part[j][lane >> 4] = valid[t] ? a : __builtin_nanf("");
+    }
+    {
+        float a = 0.f;
+#pragma unroll
+        for (int s = 0; s < SS; ++s) {
+            LaneX<kQ4_K> lx;
+            const float4* lo = xsh + ((8 * s + b) * 256 + xo) / 4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                lx.v[i] = lo[i];
+                lx.v[4 + i] = lo[8 + i];
+            }
+            lane_x_sums(lx);
+            a += block_dot_q4k(hs[s], qs[s], lx, jj);
+        }
+        a = group_sum<64>(a);
+        if (lane == 0) spart[w] = a;
+    }
+    __syncthreads();
+    if (w == 0 && lane < 4) {
+        float acc = 0.f;
+        for (int j = 0; j < k; ++j) acc = __builtin_fmaf(wts[j], part[j][lane], acc);
+        const float sc = sigmoid(slogit[0]);
+        acc += spart[lane] * sc;
+        out[4 * q + lane] = acc;
+    }
+}
+
 __global__ __launch_bounds__(kBlock) void fill_zero(float* __restrict__ p, int n) {
     for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) p[i] = 0.f;
 }
@@ -1405,6 +1511,11 @@ struct DownCombine {
 
 template <int TE, int TS, int KT, int SS>
 void launch_dc(const DownCombine& a, hipStream_t s) {
+    if (TE == kQ4_K && TS == kQ4_K) {
+        moe_down_combine_q4k<KT, SS><<<a.d_model / 4, kGemvBlock, 0, s>>>(
+            a.wd, a.expert_blocks, a.n_experts, a.idx, a.wts, a.k, a.hid, a.wsd, a.shid, a.slogit, a.out);
+        return;
+    }
     moe_down_combine_kernel<TE, TS, KT, SS><<<a.d_model / 4, kGemvBlock, 0, s>>>(
         a.wd, a.expert_blocks, a.n_experts, a.idx, a.wts, a.k, a.hid, a.wsd, a.shid, a.slogit, a.out);
 }

@@ -1042,6 +1042,7 @@ def test_moe_expert_gate_up_equals_two_expert_matmuls(kind, M, K):
 
 @pytest.mark.parametrize("kind,skind,k,inter,S,K", [
     ("Q4_K", "Q4_K", 8, 512, 2048, 2048),    # the model's shapes: one launch
+    ("Q4_K", "Q4_K", 3, 512, 4096, 1020),    # 3 experts (one per wave, one wave idle), 2-slice shared rows
     ("Q6_K", "Q4_K", 8, 512, 2048, 2048),    # shared expert of another type: two launches
     ("Q4_K", "Q4_K", 3, 768, 1024, 4096),    # two 8-block slices per row
     ("Q4_K", "Q4_K", 4, 512, 512, 512),      # K = 512: the separate kernels through the workspace
