@@ -440,7 +440,7 @@ def build_next_rows(torch, ops, synth, host):
             layer = GdnLayerDecode(*ww, conv_w, la, ldt, lnw)
             return (lambda: layer.forward(lx, lout)) if fused else (lambda: layer.forward_reference_launches(lx, lout))
         desc = ("one GDN layer decode step, Q4_K weights, 16/32 heads of 128: " +
-                ("fused entry points, 4 launches" if fused else "the reference's sequence of 10 calls"))
+                ("fused entry points, 3 launches" if fused else "the reference's sequence of 10 calls"))
         k = Kernel(name, desc, nb, nb, mk_l)
         k.layer = True
         k.no_cpu = True

@@ -27,6 +27,13 @@ void matmul_dispatch(const QuantTensor& weight, const float* x, float* y, int M,
 // W[element_offset + m*K + k] * x[t*K + k] (matrix cores for Q4_K / Q6_K at
 // rows >= 16, fp32 accuracy), with a device workspace of
 // matmul_rows_workspace_bytes(rows, K) bytes. Throws as matmul_dispatch.
+// gdn_norm_gate of x, z [heads x dim] into normed, then matmul_dispatch of weight on
+// normed (K = heads * dim): the same bits, one launch for Q4_K weights on the per-row
+// path. Throws as the two calls.  ref: src/layer_gdn.cpp:109-112
+void gdn_norm_gate_matmul(const float* x, const float* z, const float* norm_weight, float* normed, int heads, int dim,
+                          float eps, const QuantTensor& weight, float* y, int M, hipStream_t stream = nullptr,
+                          uint64_t element_offset = 0);
+
 size_t matmul_rows_workspace_bytes(int rows, int K);
 void matmul_rows(const QuantTensor& weight, const float* x, float* y, int rows, int M, int K, void* workspace,
                  size_t workspace_bytes, hipStream_t stream = nullptr, uint64_t element_offset = 0);

@@ -134,6 +134,19 @@ int qwen_gdn_norm_gate(const float* x, const float* z, const float* weight, floa
 int qwen_gdn_norm_gate_rows(const float* x, const float* z, const float* weight, float* out,
                             int rows, int heads, int dim, float eps, void* stream);
 
+/* The gated norm and the output projection of a GDN decode step in one launch:
+ * normed = qwen_gdn_norm_gate(x, z, norm_weight) over heads of dim, then
+ * y = qwen_matmul_dispatch(weight, type, num_elements, normed, M, K = heads * dim,
+ * element_offset). Results are the bits of those two calls (normed included). One
+ * launch for Q4_K weights on the per-row GEMV path, dim 64 / 128 / 256, K a multiple
+ * of 2048 and 16-byte aligned pointers: every workgroup normalises the x it reads;
+ * otherwise the two calls. Statuses as those calls.
+ * ref: src/layer_gdn.cpp:109-112 (gdn_norm_gate, matmul_dispatch) */
+int qwen_gdn_norm_gate_matmul(const float* x, const float* z, const float* norm_weight, float* normed,
+                              int heads, int dim, float eps, const void* weight, int type,
+                              uint64_t num_elements, float* y, int M, uint64_t element_offset,
+                              void* stream);
+
 /* Gates of the delta rule: beta = 1/(1+expf(-beta_raw)),
  * decay = expf(a * softplus(alpha_raw + dt_bias)), softplus(x) = x > 20 ? x : log1p(exp(x)).
  * beta_raw, alpha_raw, beta, decay [heads]; a, dt_bias [heads].

@@ -252,18 +252,34 @@ __device__ __forceinline__ int64_t out_index(int64_t m, int M, int split) {
 // the L2's busiest: loaded per wave (8 KB each) x took longer to arrive than
 // the weights (measured at 8192 x 2048: ~2 us into a ~3 us wave), loaded per
 // workgroup the request count is a quarter.
-template <int R, int NS, int MAT = 1>
+// x of a GEMV produced in its own launch: the gated per-head RMSNorm of the
+// reference's GDN layer, x = ((core * r) * w) * silu(z) per head of 4 LPH
+// values (norm_gate_v4<LPH>'s lane groups and arithmetic, so the same bits).
+// normed (may be null) receives x from workgroup (0, 0).
+struct NormGateX {
+    const float* z;
+    const float* w;
+    float eps;
+    float* normed;
+};
+
+template <int R, int NS, int MAT = 1, int LPH = 0>
 __device__ __forceinline__ void q4k_direct_slices(const uint8_t* const (&w)[MAT], const float* __restrict__ x,
                                                   float4* xs, float (&acc)[MAT][R], int nb, uint64_t ub0, int g0,
-                                                  int groups, uint64_t tensor_bytes, int s, int b, int j) {
+                                                  int groups, uint64_t tensor_bytes, int s, int b, int j,
+                                                  const NormGateX& ng = NormGateX{}) {
     constexpr int BB = KQuant<kQ4_K>::kBlockBytes;
     constexpr int NX = NS * 512;                    // float4 of x in the NS slices
     constexpr int PER = NX / kGemvBlock;
     static_assert(PER * kGemvBlock == NX, "x staging");
-    float4 xt[PER];
+    float4 xt[PER], zt[LPH > 0 ? PER : 1];
     const float* xsl = x + static_cast<size_t>(s) * 2048;
 #pragma unroll
     for (int i = 0; i < PER; ++i) xt[i] = ld4(xsl + 4 * (threadIdx.x + i * kGemvBlock));
+    if constexpr (LPH > 0) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) zt[i] = ld4(ng.z + static_cast<size_t>(s) * 2048 + 4 * (threadIdx.x + i * kGemvBlock));
+    }
     __builtin_amdgcn_sched_barrier(0);   // the x loads first
     uint4 hd[MAT][R][NS], qv[MAT][R][NS];
 #pragma unroll
@@ -282,6 +298,27 @@ __device__ __forceinline__ void q4k_direct_slices(const uint8_t* const (&w)[MAT]
             }
         }
     __builtin_amdgcn_sched_barrier(0);   // every load issued before the staging
+    if constexpr (LPH > 0) {
+        // float4 c of the slices is element group c % LPH of head (s * 512 + c) / LPH
+        // (s * 512 and i * kGemvBlock are multiples of LPH): the LPH lanes of a head
+        // are consecutive lanes of one wave, as in norm_gate_v4.
+        constexpr int D = 4 * LPH;
+        const float4 wv = ld4(ng.w + 4 * (threadIdx.x % LPH));
+        const bool first = blockIdx.x == 0 && blockIdx.y == 0;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const float ss = group_sum<LPH>(sumsq4(xt[i]));
+            const float r = rsqrtf(ss / static_cast<float>(D) + ng.eps);
+            const float4 sz = silu4(zt[i]);
+            float4 o;
+            o.x = xt[i].x * r * wv.x * sz.x;
+            o.y = xt[i].y * r * wv.y * sz.y;
+            o.z = xt[i].z * r * wv.z * sz.z;
+            o.w = xt[i].w * r * wv.w * sz.w;
+            xt[i] = o;
+            if (first && ng.normed) st4(ng.normed + static_cast<size_t>(s) * 2048 + 4 * (threadIdx.x + i * kGemvBlock), o);
+        }
+    }
 #pragma unroll
     for (int i = 0; i < PER; ++i) xs[threadIdx.x + i * kGemvBlock] = xt[i];
     __syncthreads();
@@ -408,10 +445,11 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant(const uint8_t* __restr
 // kernels, so that the LDS-staged form's registers do not count against it.
 // Every exit before the slices is uniform per workgroup (the expert slot is
 // blockIdx.y), so every thread that reaches a barrier has company.
-template <int R, int NS>
+template <int R, int NS, int LPH = 0>
 __device__ __forceinline__ void q4k_direct_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                 float* __restrict__ y, int M, int nb, uint64_t ub0, int groups,
-                                                uint64_t tensor_bytes, const Experts& ex, int sel, int split = 0) {
+                                                uint64_t tensor_bytes, const Experts& ex, int sel, int split = 0,
+                                                const NormGateX& ng = NormGateX{}) {
     const int lane = threadIdx.x & 63;
     const int wv = wave_in_block();
     const int g0 = (blockIdx.x * kGemvWaves + wv) * R;
@@ -434,7 +472,7 @@ __device__ __forceinline__ void q4k_direct_body(const uint8_t* __restrict__ w, c
     const uint8_t* const wm[1] = {w};
     for (int s = 0; s < S; s += NS) {
         if (s > 0) __syncthreads();   // every wave is done with the previous slices' x
-        q4k_direct_slices<R, NS>(wm, x, xs, acc, nb, ub0, g0, groups, tensor_bytes, s, b, j);
+        q4k_direct_slices<R, NS, 1, LPH>(wm, x, xs, acc, nb, ub0, g0, groups, tensor_bytes, s, b, j, ng);
     }
     float out = 0.f;
 #pragma unroll
@@ -451,6 +489,17 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_q4k_direct(const uint8_t* __r
                                                               int M, int nb, uint64_t ub0, int groups,
                                                               uint64_t tensor_bytes, Experts ex) {
     q4k_direct_body<R, NS>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, blockIdx.y);
+}
+
+// The gated per-head RMSNorm of x (core, heads of 4 LPH) followed by the GEMV
+// on its output, one launch: every workgroup normalises the slices of x it
+// stages (q4k_direct_slices with a NormGateX), workgroup 0 also writes them out.
+template <int R, int NS, int LPH>
+__global__ __launch_bounds__(kGemvBlock) void gemv_q4k_norm_gate(const uint8_t* __restrict__ w,
+                                                                 const float* __restrict__ core, NormGateX ng,
+                                                                 float* __restrict__ y, int M, int nb, uint64_t ub0,
+                                                                 uint64_t tensor_bytes) {
+    q4k_direct_body<R, NS, LPH>(w, core, y, M, nb, ub0, M, tensor_bytes, Experts{nullptr, 0, 0, 0}, 0, 0, ng);
 }
 
 // The routed experts' gate and up projections of one token in one launch:
@@ -1597,6 +1646,58 @@ int qwen_matmul_dispatch(const void* weight, int type, uint64_t num_elements, co
     QK_REQUIRE(x && y, "matmul_dispatch: null pointer");
     return launch_gemv(static_cast<const uint8_t*>(weight), type, num_elements, x, y, M, K, element_offset,
                        Experts{nullptr, 0, 0, 0}, 1, as_stream(stream), "matmul_dispatch");
+}
+
+// qwen_gdn_norm_gate + qwen_matmul_dispatch in one launch when the shape allows
+// (see the header); validation as the two calls.
+int qwen_gdn_norm_gate_matmul(const float* x, const float* z, const float* norm_weight, float* normed, int heads,
+                              int dim, float eps, const void* weight, int type, uint64_t num_elements, float* y,
+                              int M, uint64_t element_offset, void* stream) {
+    QK_REQUIRE(heads > 0 && dim > 0, "gdn_norm_gate_matmul: bad heads %d / dim %d", heads, dim);
+    QK_REQUIRE(x && z && norm_weight && normed, "gdn_norm_gate_matmul: null pointer");
+    const int64_t K64 = static_cast<int64_t>(heads) * dim;
+    QK_REQUIRE(K64 <= (int64_t{1} << 30), "gdn_norm_gate_matmul: %lld inputs", static_cast<long long>(K64));
+    const int K = static_cast<int>(K64);
+    if (!weight) return fail(QWEN_STATUS_INVALID_ARGUMENT, "tensor is not loaded");
+    if (!type_supported(type)) return fail(QWEN_STATUS_UNSUPPORTED_TYPE, "unsupported GGML type %d", type);
+    if (M <= 0 || element_offset > num_elements ||
+        static_cast<uint64_t>(M) * static_cast<uint64_t>(K) > num_elements - element_offset)
+        return fail(QWEN_STATUS_OUT_OF_RANGE, "GEMV shape exceeds tensor (M=%d, K=%d)", M, K);
+    QK_REQUIRE(y, "gdn_norm_gate_matmul: null pointer");
+    const auto* w = static_cast<const uint8_t*>(weight);
+    const int lph = dim == 64 ? 16 : dim == 128 ? 32 : dim == 256 ? 64 : 0;
+    const bool one = type == kQ4_K && lph && K % 2048 == 0 && aligned16(z) && aligned16(norm_weight) &&
+                     aligned16(normed) && kquant_rowpath(w, type, num_elements, x, M, K, element_offset);
+    if (!one) {
+        const int rc = qwen_gdn_norm_gate(x, z, norm_weight, normed, heads, dim, eps, stream);
+        return rc ? rc : qwen_matmul_dispatch(weight, type, num_elements, normed, y, M, K, element_offset, stream);
+    }
+    const hipStream_t s = as_stream(stream);
+    const int nb = K / 256;
+    const uint64_t tensor_bytes = (num_elements / 256) * static_cast<uint64_t>(block_bytes(type));
+    const uint64_t ub0 = element_offset / 256;
+    const NormGateX ng{z, norm_weight, eps, normed};
+    // rows per wave as dispatch_kquant picks them for this matrix
+    const int R = M >= 4 * 4096 ? 4 : (M >= 2 * 4096 || (nb >= 16 && static_cast<int64_t>(M) * (nb / 8) >= 4096)) ? 2 : 1;
+    const bool two = (nb / 8) % 2 == 0;
+    auto go = [&](auto r_c, auto ns_c, auto lph_c) {
+        constexpr int RR = decltype(r_c)::value, NS = decltype(ns_c)::value, L = decltype(lph_c)::value;
+        gemv_q4k_norm_gate<RR, NS, L><<<blocks_for((M + RR - 1) / RR, kGemvWaves), kGemvBlock, 0, s>>>(
+            w, x, ng, y, M, nb, ub0, tensor_bytes);
+    };
+    auto by_lph = [&](auto r_c, auto ns_c) {
+        if (lph == 16) go(r_c, ns_c, std::integral_constant<int, 16>{});
+        else if (lph == 32) go(r_c, ns_c, std::integral_constant<int, 32>{});
+        else go(r_c, ns_c, std::integral_constant<int, 64>{});
+    };
+    auto by_ns = [&](auto r_c) {
+        if (two) by_lph(r_c, std::integral_constant<int, 2>{});
+        else by_lph(r_c, std::integral_constant<int, 1>{});
+    };
+    if (R == 4) by_ns(std::integral_constant<int, 4>{});
+    else if (R == 2) by_ns(std::integral_constant<int, 2>{});
+    else by_ns(std::integral_constant<int, 1>{});
+    return check_launch("gdn_norm_gate_matmul");
 }
 
 int qwen_moe_expert_matmul(const void* weight, int type, uint64_t num_elements, uint64_t expert_stride, int n_experts,

@@ -247,6 +247,16 @@ void matmul_dispatch(const QuantTensor& w, const float* x, float* y, int M, int 
     check(status);
 }
 
+void gdn_norm_gate_matmul(const float* x, const float* z, const float* norm_weight, float* normed, int heads, int dim,
+                          float eps, const QuantTensor& w, float* y, int M, hipStream_t stream,
+                          uint64_t element_offset) {
+    const int status = qwen_gdn_norm_gate_matmul(x, z, norm_weight, normed, heads, dim, eps, w.device_ptr,
+                                                 static_cast<int>(w.type), w.num_elements, y, M, element_offset,
+                                                 st(stream));
+    throw_tensor_status(status, w);
+    check(status);
+}
+
 size_t matmul_rows_workspace_bytes(int rows, int K) { return qwen_matmul_rows_workspace_bytes(rows, K); }
 
 void matmul_rows(const QuantTensor& w, const float* x, float* y, int rows, int M, int K, void* workspace,

@@ -51,6 +51,7 @@ SIGNATURES: dict[str, list] = {
     "qwen_gdn_frontend_rows": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P],
     "qwen_gdn_norm_gate": [_P, _P, _P, _P, _I, _I, _F, _P],
     "qwen_gdn_norm_gate_rows": [_P, _P, _P, _P, _I, _I, _I, _F, _P],
+    "qwen_gdn_norm_gate_matmul": [_P, _P, _P, _P, _I, _I, _F, _P, _I, _U64, _P, _I, _U64, _P],
     "qwen_moe_silu_mul": [_P, _P, _P, _I, _P],
     "qwen_moe_shared_add": [_P, _P, _P, _I, _P],
     "qwen_moe_shared_add_rows": [_P, _P, _P, _I, _I, _P],

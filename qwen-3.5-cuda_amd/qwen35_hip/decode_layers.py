@@ -16,7 +16,8 @@ history, recurrent state, per-token buffers; forward src/layer_gdn.cpp:78-113):
 * `forward(x)`: the four projections in one `matmul_dispatch_multi`, conv + SiLU
   + Q/K L2 + gates + recurrence in `gdn_decode_step` (the bits of
   `gdn_frontend_rows` followed by `gdn_gated_recurrent_rows`), then the gated
-  norm and the output projection: four launches.
+  norm and the output projection in `gdn_norm_gate_matmul` (the bits of
+  `gdn_norm_gate_rows` followed by `matmul_dispatch`): three launches.
 
 Both update the layer's conv history and recurrent state (the fused step writes
 the new history into a second buffer and the two are swapped, since the
@@ -94,9 +95,10 @@ class GdnLayerDecode:
                             self.alpha_raw, self.a, self.dt, self.kh, self.vh, self.dk, self.dv, y=self.conv,
                             out=self.core, eps=self.eps)
         self.history, self._history_next = self._history_next, self.history
-        ops.gdn_norm_gate_rows(self.core.view(self.vh, self.dv), self.z.view(self.vh, self.dv), self.norm_w,
-                               out=self.normed.view(self.vh, self.dv), eps=self.eps)
-        self._proj("out", self.normed, out, self.vd)
+        w, M = self.w["out"]
+        ops.gdn_norm_gate_matmul(self.core.view(self.vh, self.dv), self.z.view(self.vh, self.dv), self.norm_w, w,
+                                 self.wtype, M * self.vd, M, normed=self.normed.view(self.vh, self.dv), out=out,
+                                 eps=self.eps)
         return out
 
 

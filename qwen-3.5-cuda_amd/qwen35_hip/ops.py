@@ -211,6 +211,29 @@ def gdn_norm_gate_rows(x, z, weight, out=None, eps=1e-6, stream=None):
     return out
 
 
+def gdn_norm_gate_matmul(x, z, norm_weight, weight, ggml_type, num_elements: int, M: int, element_offset: int = 0,
+                         normed=None, out=None, eps=1e-6, stream=None):
+    """x, z [heads, dim]; norm_weight [dim] -> normed [heads, dim] (the gated norm) and
+    out [M] = W[element_offset ..] @ normed, in one launch where the library can
+    (src/layer_gdn.cpp:109-112)."""
+    _dev(x, z, norm_weight, dtype=torch.float32)
+    _dev(weight, dtype=torch.uint8)
+    heads, dim = _rows(x)
+    _same(x.shape, z)
+    _same((dim,), norm_weight)
+    normed = torch.empty_like(x) if normed is None else normed
+    _dev(normed, dtype=torch.float32)
+    _same(x.shape, normed)
+    t = GGML_TYPES[ggml_type] if isinstance(ggml_type, str) else int(ggml_type)
+    out = torch.empty(M, dtype=torch.float32, device=x.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    if out.numel() < M:
+        raise ValueError(f"out has {out.numel()} elements, M = {M}")
+    check(load().qwen_gdn_norm_gate_matmul(_p(x), _p(z), _p(norm_weight), _p(normed), heads, dim, eps, _p(weight), t,
+                                           num_elements, _p(out), M, element_offset, _stream(stream)))
+    return normed, out
+
+
 def gdn_gate_values_rows(beta_raw, alpha_raw, a, dt_bias, beta=None, decay=None, stream=None):
     """beta_raw, alpha_raw [rows, heads] (or [heads]); a, dt_bias [heads] -> beta, decay."""
     _dev(beta_raw, alpha_raw, a, dt_bias, dtype=torch.float32)

@@ -192,3 +192,20 @@ def test_attn_decode_noalloc_host_validation(lib):
     assert f(NULL, FAKE, FAKE, NULL, FAKE, 16, 2, 256, 3, ST) == INV and "null" in msg(lib)
     assert lib.qwen_attn_decode_workspace_bytes(64, 8, 256, 19999) > 8 << 20
     assert f(FAKE, FAKE, FAKE, NULL, FAKE, 64, 8, 256, 19999, ST) == INV and "scratch" in msg(lib)
+
+
+def test_gdn_norm_gate_matmul_host_validation(lib):
+    """The fused gated norm + output projection rejects what either call would
+    (sizes, null pointers, a shape past the tensor, an unloaded tensor) before any
+    launch."""
+    INV, OOR = _lib.STATUS_INVALID_ARGUMENT, _lib.STATUS_OUT_OF_RANGE
+    p = ctypes.c_void_p(1 << 20)
+    assert lib.qwen_gdn_norm_gate_matmul(p, p, p, p, 0, 128, 1e-6, p, 12, 1 << 20, p, 8, 0, ST) == INV
+    assert "bad heads" in msg(lib)
+    assert lib.qwen_gdn_norm_gate_matmul(p, NULL, p, p, 32, 128, 1e-6, p, 12, 1 << 20, p, 8, 0, ST) == INV
+    assert "null pointer" in msg(lib)
+    assert lib.qwen_gdn_norm_gate_matmul(p, p, p, p, 32, 128, 1e-6, NULL, 12, 1 << 20, p, 8, 0, ST) == INV
+    assert msg(lib) == "tensor is not loaded"
+    # 2048 rows x 4096 inputs need 8 Mi elements
+    assert lib.qwen_gdn_norm_gate_matmul(p, p, p, p, 32, 128, 1e-6, p, 12, 4096 * 2047, p, 2048, 0, ST) == OOR
+    assert "GEMV shape exceeds tensor" in msg(lib)

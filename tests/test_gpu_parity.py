@@ -686,9 +686,34 @@ def test_gdn_gated_recurrent_equals_gates_then_recurrence(rows, kh, vh, dk, dv):
     assert_bits_equal(host(s2), host(s1), "state")
 
 
+@pytest.mark.parametrize("kind,heads,dim,M,off_rows", [("Q4_K", 32, 128, 2048, 0), ("Q4_K", 16, 128, 96, 3),
+                                                        ("Q4_K", 32, 64, 1000, 0), ("Q4_K", 16, 256, 4100, 0),
+                                                        ("Q4_K", 16, 128, 16400, 0),
+                                                        ("Q6_K", 32, 128, 64, 0), ("Q4_K", 3, 128, 40, 0)])
+def test_gdn_norm_gate_matmul_equals_norm_gate_then_matmul(kind, heads, dim, M, off_rows):
+    """The gated norm and output projection in one entry point (src/layer_gdn.cpp:
+    109-112) give the bits of gdn_norm_gate_rows followed by matmul_dispatch, normed
+    included: the one-launch form (Q4_K, K = heads * dim a multiple of 2048, dim 64 /
+    128 / 256, R = 1, 2 and 4 rows per wave, a row offset into the tensor) and the two
+    calls it falls back to (Q6_K; K = 384)."""
+    r = rng(heads * dim + M)
+    K = heads * dim
+    t = ops.GGML_TYPES[kind]
+    w = dev(_gemv_weight(kind, M + off_rows, K, r))
+    n_el = (M + off_rows) * K
+    x = dev(r.standard_normal((heads, dim)).astype(F32))
+    z = dev((2 * r.standard_normal((heads, dim))).astype(F32))
+    nw = dev((1 + 0.1 * r.standard_normal(dim)).astype(F32))
+    ref_n = ops.gdn_norm_gate_rows(x, z, nw)
+    ref_y = ops.matmul_dispatch(w, t, n_el, ref_n.view(-1), M, K, element_offset=off_rows * K)
+    got_n, got_y = ops.gdn_norm_gate_matmul(x, z, nw, w, t, n_el, M, element_offset=off_rows * K)
+    assert_bits_equal(host(got_n), host(ref_n), what=f"{kind} normed")
+    assert_bits_equal(host(got_y), host(ref_y), what=f"{kind} {M}x{K} out")
+
+
 def test_gdn_layer_decode_fused_equals_reference_launches():
     """A GDN layer's decode step (src/layer_gdn.cpp:78-113) through the fused
-    entry points (four launches) against the reference's sequence of calls on the
+    entry points (three launches) against the reference's sequence of calls on the
     same library (ten launches), three tokens in a row with the conv history and
     the recurrent state carried: same outputs, state and history (the fused
     front end's L2 norm sums in another order, so fp32 tolerance)."""
