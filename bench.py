@@ -485,7 +485,7 @@ def build_next_rows(torch, ops, synth, host):
             return ((lambda: layer.forward(lx, apos, lout)) if fused else
                     (lambda: layer.forward_reference_launches(lx, apos, lout)))
         desc = ("one attention layer decode step at position 2047, Q4_K weights, 16 query / 2 KV heads of 256: " +
-                ("fused entry points, 4 launches" if fused else "the reference's sequence of 15 calls"))
+                ("fused entry points, 3 calls" if fused else "the reference's sequence of 15 calls"))
         k = Kernel(name, desc, nb, nb, mk_a)
         k.layer = True
         k.no_cpu = True

@@ -62,6 +62,15 @@ size_t attn_decode_workspace_bytes(int heads, int kv_heads, int dim, int pos);
 void attn_decode(const float* q, const float* k_cache, const float* v_cache, const float* gate, float* out, int heads,
                  int kv_heads, int dim, int pos, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+// The Q/K norm + RoPE of src/layer_attn.cpp:91-96 folded into attn_decode: q_normed
+// receives the normalised queries (q read only; q_normed == q normalises in place),
+// the cache row of pos is normalised in place, then the decode of q_normed. The
+// same bits as those calls; one split pass at the production head shape.
+void attn_decode_norm_rope(const float* q, float* q_normed, float* k_cache, const float* v_cache, const float* gate,
+                           float* out, int heads, int kv_heads, int dim, int pos, const float* q_weight,
+                           const float* k_weight, int rope_dim, float theta, float eps, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream);
+
 // moe_shared_add per row: accum, shared_out [rows x dim], sgate [rows].
 void moe_shared_add_rows(float* accum, const float* shared_out, const float* sgate, int rows, int dim,
                          hipStream_t stream);

@@ -269,6 +269,22 @@ int qwen_attn_decode(const float* q, const float* k_cache, const float* v_cache,
                      float* out, int heads, int kv_heads, int dim, int pos, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* The attention front end folded into the decode: q_normed = q with
+ * qwen_attn_qk_norm_rope_rows applied (q_weight, rope at position pos), the cache
+ * row of pos (k_cache + pos * kv_heads * dim) normalised and rotated in place with
+ * k_weight, then qwen_attn_decode of q_normed. q is read only; q_normed [heads x
+ * dim] receives the normalised queries (q_normed == q normalises in place; any
+ * other overlap is rejected). Outputs are the bits of those calls. One split pass
+ * for head dim 256, rope_dim 64, 8 or 16 query heads per kv head, 16-byte aligned
+ * pointers and q_normed apart from q: every workgroup normalises the query heads it
+ * reads, the one holding key pos that row; otherwise a copy of q and the calls.
+ * Workspace and statuses as qwen_attn_decode, plus the front end's.
+ * ref: src/layer_attn.cpp:91-96 (attn_head_norm, rope_forward) and :103-108 */
+int qwen_attn_decode_norm_rope(const float* q, float* q_normed, float* k_cache, const float* v_cache,
+                               const float* gate, float* out, int heads, int kv_heads, int dim, int pos,
+                               const float* q_weight, const float* k_weight, int rope_dim, float theta,
+                               float eps, void* workspace, size_t workspace_bytes, void* stream);
+
 /* qwen_attn_decode without a workspace argument and without any allocation: the
  * split-K partials live in a fixed device array of
  * qwen_attn_decode_noalloc_max_scratch_bytes() bytes (8 MiB) inside the library,

@@ -22,6 +22,7 @@
 #include <algorithm>
 #include <cmath>
 
+#include "attn_common.hpp"
 #include "capi_common.hpp"
 #include "device_common.hpp"
 
@@ -29,22 +30,6 @@ namespace qk {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kMaxDen = 128;  // pairs per kernel-argument table
-
-struct RopeDen {
-    float den[kMaxDen];
-};
-
-// den[i - lo] = powf(theta, (2i)/rope_dim) for i in [lo, lo + count): the
-// exponent is formed in float as the reference does (src/cuda/rope.cu:19).
-RopeDen make_den(int lo, int count, int rope_dim, float theta) {
-    RopeDen d{};
-    for (int j = 0; j < count; ++j) {
-        const float e = (2.0f * static_cast<float>(lo + j)) / static_cast<float>(rope_dim);
-        d.den[j] = static_cast<float>(std::pow(static_cast<double>(theta), static_cast<double>(e)));
-    }
-    return d;
-}
 
 // ------------------------------------------------------------ vector kernel
 // Any head_dim of 64, 128 or 256 floats (LPH = 16, 32, 64 lanes per head): the
@@ -172,12 +157,6 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_v4(float* __restrict__ q,
 constexpr int kGroupHeads = 3;
 constexpr int kGroupBlock = 192;
 
-__device__ __forceinline__ float pl16_hi(float v) {  // lane m (even row) <- lane m + 16
-    return __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)[1]);
-}
-__device__ __forceinline__ float pl32_hi(float v) {  // lane m (< 32) <- lane m + 32
-    return __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false)[1]);
-}
 
 // POS: positions from the array `pos`, else pos0 + t.
 template <int HPW, bool NORM, bool POS>
@@ -198,7 +177,7 @@ __global__ __launch_bounds__(kGroupBlock) void qk_norm_rope_grouped(float* __res
     // No load sits behind a branch, so the scalar argument loads are not
     // serialised behind waits.
     const float fp = static_cast<float>(POS ? pos[t] : pos0 + t);
-    const float dn0 = den.den[4 * (lane & 7) + (lane >> 4)];  // lane 16r + m: pair 4(m % 8) + r
+    const float dn0 = rope256_den(den, lane);
     float4 v[HPW];
     float* ptr[HPW];
 #pragma unroll
@@ -214,38 +193,13 @@ __global__ __launch_bounds__(kGroupBlock) void qk_norm_rope_grouped(float* __res
         wq = ld4((q_heads > 0 ? qw : kw) + 4 * lane);
         wk = ld4((k_heads > 0 ? kw : qw) + 4 * lane);
     }
-    float s0, c0;
-    sincosf(fp / dn0, &s0, &c0);
-    const float c01 = pl16_hi(c0), s01 = pl16_hi(s0);
-    const float cs[4] = {c0, c01, pl32_hi(c0), pl32_hi(c01)};
-    const float sn[4] = {s0, s01, pl32_hi(s0), pl32_hi(s01)};
-    const bool first = lane < 8, second = lane >= 8 && lane < 16;
+    const Rope256 rp = rope256_angles(fp, dn0);
 #pragma unroll
     for (int j = 0; j < HPW; ++j) {
         const int h = h0 + j;
-        float4 x = v[j];
-        if constexpr (NORM) {
-            const float4 wv = (min(h, hpr - 1) < q_heads) ? wq : wk;
-            const float ss = group_sum<kWave>(sumsq4(x));
-            const float r = rsqrtf(ss / 256.0f + eps);
-            x.x = x.x * (r * wv.x);
-            x.y = x.y * (r * wv.y);
-            x.z = x.z * (r * wv.z);
-            x.w = x.w * (r * wv.w);
-        }
-        const float pv[4] = {dpp_move<0x128>(x.x), dpp_move<0x128>(x.y), dpp_move<0x128>(x.z), dpp_move<0x128>(x.w)};
-        const float a[4] = {x.x, x.y, x.z, x.w};
-        float o[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (first)
-                o[i] = a[i] * cs[i] - pv[i] * sn[i];  // x[i]      = a c - b s
-            else if (second)
-                o[i] = a[i] * cs[i] + pv[i] * sn[i];  // x[i+half] = b c + a s
-            else
-                o[i] = a[i];
-        }
-        if (h < hpr) st4_nt(ptr[j] + 4 * lane, make_float4(o[0], o[1], o[2], o[3]));  // wave-uniform
+        const float4 wv = (min(h, hpr - 1) < q_heads) ? wq : wk;
+        const float4 o = norm_rope256<NORM>(v[j], wv, rp, eps, lane);
+        if (h < hpr) st4_nt(ptr[j] + 4 * lane, o);  // wave-uniform
     }
 }
 

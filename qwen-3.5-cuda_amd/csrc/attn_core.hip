@@ -24,6 +24,7 @@
 #include <cmath>
 #include <mutex>
 
+#include "attn_common.hpp"
 #include "capi_common.hpp"
 #include "device_common.hpp"
 
@@ -152,11 +153,25 @@ __global__ __launch_bounds__(kBlock) void values_kernel(const float* __restrict_
 constexpr int kKeyStride = kMaxDim + 4;
 constexpr int kPairLanes = 1;
 
-template <int G, int L>
+// NR: the attention front end folded in (qwen_attn_decode_norm_rope): q and
+// the cache row of key pos = n_keys - 1 arrive unnormalised; each workgroup
+// applies the per-head RMSNorm and RoPE (head_dim 256, rope_dim 64;
+// norm_rope256, the arithmetic of qk_norm_rope_grouped) to its G query heads in
+// registers, the workgroup whose keys hold pos does the same to that row and
+// writes it back to the cache, and split 0 of each kv head writes its G
+// normalised query heads to q_out (when set).
+struct NormRopeArgs {
+    const float* qw;
+    const float* kw;
+    float* q_out;
+    float eps;
+};
+
+template <int G, int L, bool NR = false>
 __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
     const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
     float* __restrict__ ws_acc, float* __restrict__ ws_m, float* __restrict__ ws_l, int kv_heads, int n_keys,
-    int splits, float scale) {
+    int splits, float scale, NormRopeArgs nr = NormRopeArgs{}, RopeDen den = RopeDen{}) {
     constexpr int D = kMaxDim;                 // this path: head dim 256
     constexpr int D4 = D / 4;
     constexpr int NT = G * L * kPairLanes;
@@ -190,6 +205,31 @@ __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
 #pragma unroll
     for (int k2 = 0; k2 < LH; ++k2)  // rows past the end clamped (weight 0)
         vcol[k2] = vbase[static_cast<size_t>(min(t0 + half * LH + k2, n_keys - 1)) * row_stride + col];
+    if constexpr (NR) {
+        // Thread (wave w, lane) holds float4 `lane` of query head w + 4 i in qr[i]
+        // and of key t0 + w + 4 i in kr[i] (NT = 256, D4 = 64): whole heads per
+        // wave, the layout norm_rope256 takes.
+        static_assert(NT == 4 * kWave && D4 == kWave, "front end layout");
+        const int lane = tid & (kWave - 1), w = wave_in_block();
+        const float dn0 = rope256_den(den, lane);
+        const float4 wq = ld4(nr.qw + 4 * lane), wk = ld4(nr.kw + 4 * lane);
+        const Rope256 rp = rope256_angles(static_cast<float>(n_keys - 1), dn0);
+#pragma unroll
+        for (int i = 0; i < QCH; ++i) {
+            qr[i] = norm_rope256<true>(qr[i], wq, rp, nr.eps, lane);
+            if (split == 0 && nr.q_out) st4(nr.q_out + static_cast<size_t>(kv) * G * D + 4 * (tid + i * NT), qr[i]);
+        }
+        const int kk = n_keys - 1 - t0;   // key pos in this split's tile (wave-uniform)
+        if (kk < L && (kk & 3) == w) {
+#pragma unroll
+            for (int i = 0; i < KCH; ++i) {
+                if (i == kk >> 2) {
+                    kr[i] = norm_rope256<true>(kr[i], wk, rp, nr.eps, lane);
+                    st4(const_cast<float*>(kbase) + static_cast<size_t>(n_keys - 1) * row_stride + 4 * lane, kr[i]);
+                }
+            }
+        }
+    }
 #pragma unroll
     for (int i = 0; i < QCH; ++i) {
         const int c = tid + i * NT;
@@ -478,31 +518,40 @@ size_t qwen_attn_decode_workspace_bytes(int heads, int kv_heads, int dim, int po
 
 namespace {
 
+// The split pass and the combine (fused_ok shapes, 16-byte aligned q and
+// cache); NR: the front end folded into the split pass.
+template <bool NR>
+int split_combine(const float* q, const float* k_cache, const float* v_cache, const float* gate, float* out,
+                  int heads, int kv_heads, int dim, int pos, void* workspace, hipStream_t s,
+                  const NormRopeArgs& nr = NormRopeArgs{}, const RopeDen& den = RopeDen{}) {
+    const int n_keys = pos + 1;
+    const int g = heads / kv_heads;
+    const int splits = fused_splits(heads, kv_heads, n_keys);
+    float* acc = static_cast<float*>(workspace);
+    float* m = acc + static_cast<size_t>(splits) * heads * dim;
+    float* l = m + static_cast<size_t>(splits) * heads;
+    const dim3 grid(splits, kv_heads);
+    const float scale = host_rsqrt(dim);
+    if (g == 8)
+        decode_split<8, 32, NR><<<grid, 8 * 32 * kPairLanes, 0, s>>>(q, k_cache, v_cache, acc, m, l, kv_heads, n_keys,
+                                                                    splits, scale, nr, den);
+    else
+        decode_split<16, 16, NR><<<grid, 16 * 16 * kPairLanes, 0, s>>>(q, k_cache, v_cache, acc, m, l, kv_heads,
+                                                                      n_keys, splits, scale, nr, den);
+    int st = check_launch("attn_decode");
+    if (st) return st;
+    decode_combine<<<dim3(heads, (dim + kCombineCols - 1) / kCombineCols), kBlock, 0, s>>>(acc, m, l, gate, out, g,
+                                                                                        dim, splits);
+    return check_launch("attn_decode");
+}
+
 // qwen_attn_decode on a workspace already checked against the shape.
 int attn_decode_ws(const float* q, const float* k_cache, const float* v_cache, const float* gate, float* out,
                    int heads, int kv_heads, int dim, int pos, void* workspace, void* stream) {
     hipStream_t s = as_stream(stream);
     const int n_keys = pos + 1;
-    if (fused_ok(heads, kv_heads, dim, n_keys) && aligned16(q) && aligned16(k_cache)) {
-        const int g = heads / kv_heads;
-        const int splits = fused_splits(heads, kv_heads, n_keys);
-        float* acc = static_cast<float*>(workspace);
-        float* m = acc + static_cast<size_t>(splits) * heads * dim;
-        float* l = m + static_cast<size_t>(splits) * heads;
-        const dim3 grid(splits, kv_heads);
-        const float scale = host_rsqrt(dim);
-        if (g == 8)
-            decode_split<8, 32><<<grid, 8 * 32 * kPairLanes, 0, s>>>(q, k_cache, v_cache, acc, m, l, kv_heads, n_keys,
-                                                                    splits, scale);
-        else
-            decode_split<16, 16><<<grid, 16 * 16 * kPairLanes, 0, s>>>(q, k_cache, v_cache, acc, m, l, kv_heads,
-                                                                      n_keys, splits, scale);
-        int st = check_launch("attn_decode");
-        if (st) return st;
-        decode_combine<<<dim3(heads, (dim + kCombineCols - 1) / kCombineCols), kBlock, 0, s>>>(acc, m, l, gate, out, g,
-                                                                                            dim, splits);
-        return check_launch("attn_decode");
-    }
+    if (fused_ok(heads, kv_heads, dim, n_keys) && aligned16(q) && aligned16(k_cache))
+        return split_combine<false>(q, k_cache, v_cache, gate, out, heads, kv_heads, dim, pos, workspace, s);
     float* sc = static_cast<float*>(workspace);
     int st = qwen_attn_scores(q, k_cache, sc, heads, kv_heads, dim, pos, stream);
     if (!st) st = qwen_attn_softmax(sc, heads, n_keys, stream);
@@ -523,6 +572,43 @@ int qwen_attn_decode(const float* q, const float* k_cache, const float* v_cache,
     const size_t need = qwen_attn_decode_workspace_bytes(heads, kv_heads, dim, pos);
     QK_REQUIRE(workspace_bytes >= need, "attn_decode: workspace of %zu bytes, need %zu", workspace_bytes, need);
     return attn_decode_ws(q, k_cache, v_cache, gate, out, heads, kv_heads, dim, pos, workspace, stream);
+}
+
+int qwen_attn_decode_norm_rope(const float* q, float* q_normed, float* k_cache, const float* v_cache,
+                               const float* gate, float* out, int heads, int kv_heads, int dim, int pos,
+                               const float* q_weight, const float* k_weight, int rope_dim, float theta, float eps,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+    QK_ATTN_SHAPE("attn_decode_norm_rope");
+    QK_REQUIRE(q && q_normed && k_cache && v_cache && out && workspace && q_weight && k_weight,
+               "attn_decode_norm_rope: null pointer");
+    QK_REQUIRE(rope_dim >= 0 && rope_dim <= dim && (rope_dim & 1) == 0 && rope_dim / 2 <= 1024,
+               "attn_decode_norm_rope: rope_dim %d invalid for head_dim %d", rope_dim, dim);
+    QK_REQUIRE(rope_dim == 0 || theta > 0.0f, "attn_decode_norm_rope: theta must be positive");
+    const size_t need = qwen_attn_decode_workspace_bytes(heads, kv_heads, dim, pos);
+    QK_REQUIRE(workspace_bytes >= need, "attn_decode_norm_rope: workspace of %zu bytes, need %zu", workspace_bytes,
+               need);
+    const size_t qbytes = static_cast<size_t>(heads) * dim * sizeof(float);
+    const auto qa = reinterpret_cast<uintptr_t>(q), na = reinterpret_cast<uintptr_t>(q_normed);
+    const bool disjoint = na + qbytes <= qa || qa + qbytes <= na;
+    QK_REQUIRE(disjoint || q_normed == q, "attn_decode_norm_rope: q_normed overlaps q without being q");
+    hipStream_t s = as_stream(stream);
+    float* krow = k_cache + static_cast<size_t>(pos) * kv_heads * dim;
+    if (disjoint && rope_dim == 64 && fused_ok(heads, kv_heads, dim, pos + 1) && aligned16(q) && aligned16(q_normed) &&
+        aligned16(k_cache) && aligned16(q_weight) && aligned16(k_weight)) {
+        const NormRopeArgs nr{q_weight, k_weight, q_normed, eps};
+        return split_combine<true>(q, k_cache, v_cache, gate, out, heads, kv_heads, dim, pos, workspace, s, nr,
+                                   make_den(0, 32, 64, theta));
+    }
+    // Other shapes: the front end on a copy of q, then the decode.
+    if (q_normed != q) {
+        const hipError_t e = hipMemcpyAsync(q_normed, q, qbytes, hipMemcpyDeviceToDevice, s);
+        if (e != hipSuccess)
+            return fail(QWEN_STATUS_LAUNCH_FAILED, "attn_decode_norm_rope: copy of q failed: %s", hipGetErrorString(e));
+    }
+    int st = qwen_attn_qk_norm_rope_rows(q_normed, krow, q_weight, k_weight, nullptr, pos, 1, heads, kv_heads, dim,
+                                         rope_dim, theta, eps, stream);
+    if (!st) st = attn_decode_ws(q_normed, k_cache, v_cache, gate, out, heads, kv_heads, dim, pos, workspace, stream);
+    return st;
 }
 
 size_t qwen_attn_decode_noalloc_max_scratch_bytes(void) { return kDecodeScratchBytes; }

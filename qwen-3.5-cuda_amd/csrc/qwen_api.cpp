@@ -178,6 +178,14 @@ void attn_decode(const float* q, const float* k_cache, const float* v_cache, con
                            st(stream)));
 }
 
+void attn_decode_norm_rope(const float* q, float* q_normed, float* k_cache, const float* v_cache, const float* gate,
+                           float* out, int heads, int kv_heads, int dim, int pos, const float* q_weight,
+                           const float* k_weight, int rope_dim, float theta, float eps, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
+    check(qwen_attn_decode_norm_rope(q, q_normed, k_cache, v_cache, gate, out, heads, kv_heads, dim, pos, q_weight,
+                                     k_weight, rope_dim, theta, eps, workspace, workspace_bytes, st(stream)));
+}
+
 void moe_topk(const float* router, int* top_idx, float* top_weight, int experts, int k, hipStream_t stream) {
     check(qwen_moe_topk(router, top_idx, top_weight, experts, k, st(stream)));
 }

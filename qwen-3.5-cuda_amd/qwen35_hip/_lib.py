@@ -76,6 +76,7 @@ SIGNATURES: dict[str, list] = {
     "qwen_attn_kv_store": [_P, _P, _P, _P, _I, _I, _I, _P],
     "qwen_attn_decode_workspace_bytes": [_I, _I, _I, _I],
     "qwen_attn_decode": [_P] * 5 + [_I, _I, _I, _I, _P, ctypes.c_size_t, _P],
+    "qwen_attn_decode_norm_rope": [_P] * 6 + [_I, _I, _I, _I, _P, _P, _I, _F, _F, _P, ctypes.c_size_t, _P],
     "qwen_attn_decode_noalloc_max_scratch_bytes": [],
     "qwen_attn_decode_noalloc": [_P] * 5 + [_I, _I, _I, _I, _P],
     "qwen_moe_topk": [_P, _P, _P, _I, _I, _P],

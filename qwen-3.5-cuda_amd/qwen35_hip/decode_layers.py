@@ -142,9 +142,10 @@ class AttnLayerDecode:
     * `forward(x, pos, out)`: the three projections in one `matmul_dispatch_multi`
       whose query | gate output is written already split (q, then the gate) and
       whose K and V outputs are the cache rows at `pos` (no split launch, no cache
-      copies), Q/K head norm + partial RoPE in one `attn_qk_norm_rope_rows` (K
-      normalized in place in the cache row), `attn_decode` (scores, softmax,
-      values and the sigmoid gate), output projection: four launches.
+      copies), Q/K head norm + partial RoPE folded into the decode
+      (`attn_decode_norm_rope`: the bits of `attn_qk_norm_rope_rows`, K normalized
+      in place in the cache row, followed by `attn_decode` with its scores,
+      softmax, values and sigmoid gate), output projection: three calls.
     """
 
     def __init__(self, w_qg, w_k, w_v, w_out, q_norm, k_norm, *, wtype="Q4_K", d_model=2048, heads=16, kv_heads=2,
@@ -204,10 +205,9 @@ class AttnLayerDecode:
                 for n, y, s in (("qg", self.qg, hd), ("k", self.k_cache[pos], 0), ("v", self.v_cache[pos], 0))]
         ops.matmul_dispatch_multi(jobs, x, self.dm)        # qg = [q | gate] (the split layout)
         q, gate = self.qg[:self.qd], self.qg[self.qd:]
-        ops.attn_qk_norm_rope_rows(q.view(1, h, hd), self.k_cache[pos].view(1, kvh, hd), self.q_norm,
-                                   self.k_norm, pos0=pos, rope_dim=self.rope_dim, theta=self.theta, eps=self.eps)
-        ops.attn_decode(q, self.k_cache, self.v_cache, h, kvh, hd, pos, gate=gate, workspace=self.workspace,
-                        out=self.gated)
+        ops.attn_decode_norm_rope(q, self.k_cache, self.v_cache, h, kvh, hd, pos, self.q_norm, self.k_norm,
+                                  self.rope_dim, self.theta, gate=gate, workspace=self.workspace, q_normed=self.q,
+                                  out=self.gated, eps=self.eps)
         self._proj("out", self.gated, out, self.qd)
         return out
 

@@ -452,6 +452,35 @@ def attn_decode(q, k_cache, v_cache, heads, kv_heads, dim, pos, gate=None, works
     return out
 
 
+def attn_decode_norm_rope(q, k_cache, v_cache, heads, kv_heads, dim, pos, q_weight, k_weight, rope_dim, theta,
+                          gate=None, workspace=None, q_normed=None, out=None, eps=1e-6, stream=None):
+    """attn_qk_norm_rope_rows on a copy of q (-> q_normed) and on the cache row of pos
+    (in place), then attn_decode of q_normed, in one split pass where the library can
+    (src/layer_attn.cpp:91-96, 103-108). Returns (out, q_normed)."""
+    _dev(q, k_cache, v_cache, q_weight, k_weight, dtype=torch.float32)
+    _attn_check(q, k_cache, heads, kv_heads, dim, pos)
+    _attn_check(q, v_cache, heads, kv_heads, dim, pos)
+    _same((dim,), q_weight)
+    _same((dim,), k_weight)
+    if gate is not None:
+        _dev(gate, dtype=torch.float32)
+    nbytes = attn_decode_workspace_bytes(heads, kv_heads, dim, pos)
+    if workspace is None:
+        workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+    _dev(workspace)
+    q_normed = torch.empty(heads * dim, dtype=torch.float32, device=q.device) if q_normed is None else q_normed
+    _dev(q_normed, dtype=torch.float32)
+    if q_normed.numel() < heads * dim:
+        raise ValueError(f"q_normed has {q_normed.numel()} elements, need {heads * dim}")
+    out = torch.empty(heads * dim, dtype=torch.float32, device=q.device) if out is None else out
+    _dev(out, dtype=torch.float32)
+    check(load().qwen_attn_decode_norm_rope(_p(q), _p(q_normed), _p(k_cache), _p(v_cache), _p(gate), _p(out), heads,
+                                            kv_heads, dim, pos, _p(q_weight), _p(k_weight), rope_dim, theta, eps,
+                                            _p(workspace), workspace.numel() * workspace.element_size(),
+                                            _stream(stream)))
+    return out, q_normed
+
+
 def attn_decode_noalloc(q, k_cache, v_cache, heads, kv_heads, dim, pos, gate=None, out=None, stream=None):
     """attn_decode with the library's fixed device scratch instead of a workspace
     (no device allocation in the call when `out` is given)."""

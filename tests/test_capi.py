@@ -209,3 +209,24 @@ def test_gdn_norm_gate_matmul_host_validation(lib):
     # 2048 rows x 4096 inputs need 8 Mi elements
     assert lib.qwen_gdn_norm_gate_matmul(p, p, p, p, 32, 128, 1e-6, p, 12, 4096 * 2047, p, 2048, 0, ST) == OOR
     assert "GEMV shape exceeds tensor" in msg(lib)
+
+
+def test_attn_decode_norm_rope_host_validation(lib):
+    """The folded attention decode rejects bad shapes, null pointers, a partly
+    overlapping q_normed and a short workspace before any launch."""
+    INV = _lib.STATUS_INVALID_ARGUMENT
+    p = ctypes.c_void_p(1 << 20)
+    big = 1 << 30
+    assert lib.qwen_attn_decode_norm_rope(p, ctypes.c_void_p((1 << 20) + 4096), p, p, NULL, p, 16, 3, 256, 10, p, p,
+                                          64, 1e7, 1e-6, p, big, ST) == INV
+    assert "not a multiple" in msg(lib)
+    assert lib.qwen_attn_decode_norm_rope(p, ctypes.c_void_p((1 << 20) + 65536), p, p, NULL, p, 16, 2, 256, 10, NULL,
+                                          p, 64, 1e7, 1e-6, p, big, ST) == INV
+    assert "null pointer" in msg(lib)
+    assert lib.qwen_attn_decode_norm_rope(p, ctypes.c_void_p((1 << 20) + 64), p, p, NULL, p, 16, 2, 256, 10, p, p,
+                                          64, 1e7, 1e-6, p, big, ST) == INV
+    assert "overlaps q" in msg(lib)
+    assert lib.qwen_attn_decode_norm_rope(p, p, p, p, NULL, p, 16, 2, 256, 10, p, p, 65, 1e7, 1e-6, p, big, ST) == INV
+    assert "rope_dim" in msg(lib)
+    assert lib.qwen_attn_decode_norm_rope(p, p, p, p, NULL, p, 16, 2, 256, 10, p, p, 64, 1e7, 1e-6, p, 16, ST) == INV
+    assert "workspace" in msg(lib)

@@ -799,9 +799,9 @@ def _attn_layer_pair(r, max_seq_len):
 @pytest.mark.parametrize("start", [0, 700])
 def test_attn_layer_decode_fused_equals_reference_launches(start):
     """A full-attention layer's decode step (src/layer_attn.cpp:63-111) through
-    the fused entry points (four launches: projections with the query | gate
-    rows written split and K, V straight into the cache rows, Q/K norm + RoPE,
-    attention decode, output projection) against the
+    the fused entry points (three calls: projections with the query | gate
+    rows written split and K, V straight into the cache rows, Q/K norm + RoPE
+    folded into the attention decode, output projection) against the
     reference's sequence of fifteen calls on the same library, three tokens in a
     row from position `start` (0, and 700 over a cache whose earlier rows hold the
     same random keys and values in both layers): same output and cache rows
@@ -951,6 +951,38 @@ def test_attn_decode(oracle, heads, kv, dim, pos, gated):
     got = host(ops.attn_decode(dev(q), dev(K), dev(V), heads, kv, dim, pos, gate=None if gate is None else dev(gate)))
     ref = oracle.attn_decode(q, K, V, heads, kv, dim, pos, gate=gate)
     _assert_scaled(got, ref, _attn_scale(oracle, q, K, V, heads, kv, dim, pos, gate), f"decode pos {pos}")
+
+
+@pytest.mark.parametrize("heads,kv,dim,pos,rope,inplace", [(16, 2, 256, 2047, 64, False), (16, 2, 256, 0, 64, False),
+                                                        (16, 2, 256, 31, 64, False), (16, 2, 256, 32, 64, False),
+                                                        (16, 2, 256, 100, 64, False), (16, 1, 256, 47, 64, False),
+                                                        (16, 2, 256, 40, 32, False), (8, 2, 128, 20, 64, False),
+                                                        (16, 2, 256, 60, 64, True)])
+def test_attn_decode_norm_rope_equals_front_end_then_decode(heads, kv, dim, pos, rope, inplace):
+    """The attention front end folded into the decode (src/layer_attn.cpp:91-96 then
+    :103-108) gives the bits of attn_qk_norm_rope_rows on a copy of q and on the
+    cache row of pos followed by attn_decode: output, normalised q and the whole
+    cache, on the one-pass form (8 and 16 query heads per kv head, key pos at the
+    start, end and inside a 32-key split, one key only) and on the calls it falls
+    back to (rope_dim 32, head dim 128, q normalised in place)."""
+    r = rng(heads * 11 + pos + rope)
+    q, K, V, g = _attn_inputs(r, heads, kv, dim, pos + 1)
+    qw = (1 + 0.2 * r.standard_normal(dim)).astype(F32)
+    kw = (1 + 0.2 * r.standard_normal(dim)).astype(F32)
+    theta, eps = 1e7, 1e-6
+    # reference: the front end on copies, then the decode
+    q_ref, K_ref = dev(q), dev(K)
+    ops.attn_qk_norm_rope_rows(q_ref.view(1, heads, dim), K_ref[pos].view(1, kv, dim), dev(qw), dev(kw), pos0=pos,
+                               rope_dim=rope, theta=theta, eps=eps)
+    out_ref = ops.attn_decode(q_ref, K_ref, dev(V), heads, kv, dim, pos, gate=dev(g))
+    dq, dK = dev(q), dev(K)
+    out, qn = ops.attn_decode_norm_rope(dq, dK, dev(V), heads, kv, dim, pos, dev(qw), dev(kw), rope, theta,
+                                        gate=dev(g), q_normed=dq if inplace else None, eps=eps)
+    assert_bits_equal(host(out), host(out_ref), what=f"out pos {pos}")
+    assert_bits_equal(host(qn), host(q_ref), what="normalised q")
+    assert_bits_equal(host(dK), host(K_ref), what="cache")
+    if not inplace:
+        assert_bits_equal(host(dq), q, what="q untouched")
 
 
 def test_attn_decode_rejects_small_workspace():
