@@ -449,10 +449,10 @@ template <int R, int NS, int LPH = 0>
 __device__ __forceinline__ void q4k_direct_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
                                                 float* __restrict__ y, int M, int nb, uint64_t ub0, int groups,
                                                 uint64_t tensor_bytes, const Experts& ex, int sel, int split = 0,
-                                                const NormGateX& ng = NormGateX{}) {
+                                                const NormGateX& ng = NormGateX{}, int bx = -1) {
     const int lane = threadIdx.x & 63;
     const int wv = wave_in_block();
-    const int g0 = (blockIdx.x * kGemvWaves + wv) * R;
+    const int g0 = ((bx < 0 ? static_cast<int>(blockIdx.x) : bx) * kGemvWaves + wv) * R;
     const int b = lane >> 3, j = lane & 7;
     const int S = nb >> 3;
     uint64_t eoff = 0;
@@ -712,6 +712,7 @@ struct GemvMat {
 };
 struct GemvMulti {
     GemvMat d[kMultiMax];
+    int start[kMultiMax + 1];   // direct form: workgroups [start[j], start[j+1]) run matrix j
 };
 
 template <int TYPE, int R>
@@ -722,13 +723,18 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant_multi(const float* __r
                               m.split);
 }
 
+// One flat grid: workgroup b runs block b - start[j] of matrix j, start[j] <= b <
+// start[j+1] (every workgroup has rows; a grid sized for the largest matrix per
+// launch row left most of the small matrices' workgroups with nothing to do).
 template <int R, int NS>
 __global__ __launch_bounds__(kGemvBlock) void gemv_q4k_direct_multi(const float* __restrict__ x, int nb,
-                                                                    GemvMulti mu) {
-    const GemvMat& m = mu.d[blockIdx.y];
-    if (static_cast<int64_t>(blockIdx.x) * kGemvWaves * R >= m.groups) return;   // uniform per workgroup
+                                                                    GemvMulti mu, int n) {
+    const int b = static_cast<int>(blockIdx.x);
+    int j = 0;
+    while (j + 1 < n && mu.start[j + 1] <= b) ++j;   // uniform per workgroup
+    const GemvMat& m = mu.d[j];
     q4k_direct_body<R, NS>(m.w, x, m.y, m.M, nb, m.ub0, m.groups, m.tensor_bytes, Experts{nullptr, 0, 0, 0}, 0,
-                           m.split);
+                           m.split, NormGateX{}, b - mu.start[j]);
 }
 
 // ------------------------------------------------------------ MoE down + combine
@@ -1487,11 +1493,15 @@ void launch_multi_r(const GemvMulti& mu, int n, const float* x, int nb, hipStrea
     int64_t gx = 1;
     for (int j = 0; j < n; ++j) gx = std::max<int64_t>(gx, blocks_for((mu.d[j].groups + R - 1) / R, kGemvWaves));
     const dim3 grid(static_cast<unsigned>(gx), n);
-    if (TYPE == kQ4_K && nb >= 8) {   // rows of whole units: the direct form
+    if (TYPE == kQ4_K && nb >= 8) {   // rows of whole units: the direct form, one flat grid
+        GemvMulti mf = mu;
+        mf.start[0] = 0;
+        for (int j = 0; j < n; ++j)
+            mf.start[j + 1] = mf.start[j] + static_cast<int>(blocks_for((mu.d[j].groups + R - 1) / R, kGemvWaves));
         if ((nb / 8) % 2 == 0)
-            gemv_q4k_direct_multi<R, 2><<<grid, kGemvBlock, 0, s>>>(x, nb, mu);
+            gemv_q4k_direct_multi<R, 2><<<mf.start[n], kGemvBlock, 0, s>>>(x, nb, mf, n);
         else
-            gemv_q4k_direct_multi<R, 1><<<grid, kGemvBlock, 0, s>>>(x, nb, mu);
+            gemv_q4k_direct_multi<R, 1><<<mf.start[n], kGemvBlock, 0, s>>>(x, nb, mf, n);
         return;
     }
     const size_t lds = static_cast<size_t>(kGemvWaves) * R * CPU * 16;
