@@ -562,7 +562,11 @@ struct RouteJob {
 // workgroup.
 template <int R, int VPL>
 __device__ __forceinline__ bool swiglu_setup(const PairJob& jb, bool sh, int n_sel, const RouteJob& rt, int lane,
-                                             int wv, int g0, float*& h, uint64_t& ub) {
+                                             int wv, int g0, float*& h, uint64_t& ub, int by = -1, int bx = -1) {
+    if (by < 0) {
+        by = static_cast<int>(blockIdx.y);
+        bx = static_cast<int>(blockIdx.x);
+    }
     Experts ex = jb.ex;
     if constexpr (VPL > 0) {
         __shared__ int32_t sidx[kWave];
@@ -572,7 +576,7 @@ __device__ __forceinline__ bool swiglu_setup(const PairJob& jb, bool sh, int n_s
                 float pw;
                 const bool fin = topk_row<VPL>(rt.logits, ex.n_experts, n_sel, pi, pw);
                 if (lane < n_sel) sidx[lane] = fin ? pi : -1;
-                if (blockIdx.x == 0 && blockIdx.y == 0) {
+                if (bx == 0 && by == 0) {
                     if (fin && lane < n_sel) {
                         rt.idx[lane] = pi;
                         rt.w[lane] = pw;
@@ -588,7 +592,7 @@ __device__ __forceinline__ bool swiglu_setup(const PairJob& jb, bool sh, int n_s
     }
     uint64_t eoff = 0;
     int64_t x_off, y_off;
-    const bool ok_e = select_expert(ex, sh ? 0 : static_cast<int>(blockIdx.y), jb.M, x_off, y_off, eoff);
+    const bool ok_e = select_expert(ex, sh ? 0 : by, jb.M, x_off, y_off, eoff);
     h = jb.h + y_off;
     if (!ok_e) {
         if (lane < R && g0 + lane < jb.M) h[g0 + lane] = __builtin_nanf("");
@@ -663,21 +667,25 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kquant_swiglu(const float* __
 // gemv_kquant_swiglu for Q4_K in the direct form (q4k_direct_slices with the
 // gate and up rows of the wave, one staged x for both): same rows, reductions
 // and bits.
+// One flat grid: workgroups [0, n_sel nr) take the routed slots (nr each),
+// the ns after them the shared rows.
 template <int R, int NS, int VPL>
 __global__ __launch_bounds__(kGemvBlock) void gemv_q4k_direct_swiglu(const float* __restrict__ x, int nb,
                                                                      PairJob routed, PairJob shared, int n_sel,
-                                                                     RouteJob rt) {
-    const bool sh = static_cast<int>(blockIdx.y) == n_sel;
+                                                                     RouteJob rt, int nr) {
+    const int fb = static_cast<int>(blockIdx.x);
+    const bool sh = fb >= n_sel * nr;
+    const int by = sh ? n_sel : fb / nr;
+    const int bx = sh ? fb - n_sel * nr : fb - by * nr;
     const PairJob& jb = sh ? shared : routed;
-    if (static_cast<int64_t>(blockIdx.x) * kGemvWaves * R >= jb.M) return;   // uniform per workgroup
     const int lane = threadIdx.x & 63;
     const int wv = wave_in_block();
-    const int g0 = (blockIdx.x * kGemvWaves + wv) * R;
+    const int g0 = (bx * kGemvWaves + wv) * R;
     const int b = lane >> 3, j = lane & 7;
     const int S = nb >> 3;
     float* h;
     uint64_t ub;
-    if (!swiglu_setup<R, VPL>(jb, sh, n_sel, rt, lane, wv, g0, h, ub)) return;   // uniform per workgroup
+    if (!swiglu_setup<R, VPL>(jb, sh, n_sel, rt, lane, wv, g0, h, ub, by, bx)) return;   // uniform per workgroup
     __shared__ float4 xs[NS * 512];
     float acc[2][R];
 #pragma unroll
@@ -1603,11 +1611,14 @@ void launch_swiglu_r(const float* x, int nb, const PairJob& routed, const PairJo
     const int rows = std::max(n_sel > 0 ? routed.M : 0, shared.M);
     const int rows_y = n_sel + (shared.M > 0 ? 1 : 0);
     const dim3 grid(blocks_for((rows + R - 1) / R, kGemvWaves), rows_y);
-    if (TYPE == kQ4_K) {   // rows of whole units (8 | nb here): the direct form
+    if (TYPE == kQ4_K) {   // rows of whole units (8 | nb here): the direct form, one flat grid
+        const int nr = n_sel > 0 ? static_cast<int>(blocks_for((routed.M + R - 1) / R, kGemvWaves)) : 0;
+        const int ns = shared.M > 0 ? static_cast<int>(blocks_for((shared.M + R - 1) / R, kGemvWaves)) : 0;
+        const unsigned flat = static_cast<unsigned>(n_sel * nr + ns);
         if ((nb / 8) % 2 == 0)
-            gemv_q4k_direct_swiglu<R, 2, VPL><<<grid, kGemvBlock, 0, s>>>(x, nb, routed, shared, n_sel, rt);
+            gemv_q4k_direct_swiglu<R, 2, VPL><<<flat, kGemvBlock, 0, s>>>(x, nb, routed, shared, n_sel, rt, nr);
         else
-            gemv_q4k_direct_swiglu<R, 1, VPL><<<grid, kGemvBlock, 0, s>>>(x, nb, routed, shared, n_sel, rt);
+            gemv_q4k_direct_swiglu<R, 1, VPL><<<flat, kGemvBlock, 0, s>>>(x, nb, routed, shared, n_sel, rt, nr);
         return;
     }
     const size_t lds = static_cast<size_t>(kGemvWaves) * 2 * R * CPU * 16;
