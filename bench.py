@@ -301,6 +301,25 @@ def build_next_rows(torch, ops, synth, host):
                             nbg, nbg, mk_g)
                 kg.no_cpu = True
                 ks.append(kg)
+            # The whole decode step after the input projections (layer_gdn.cpp:89-106):
+            # conv + SiLU + Q/K L2 norm + gates + recurrence in one launch.
+            C = 2 * kh * dk + vh * dv
+            cw = torch.from_numpy((0.5 * rng.standard_normal((C, 4))).astype(np.float32)).to(dev)
+            hin = torch.from_numpy(rng.standard_normal((C, 3)).astype(np.float32)).to(dev)
+            xin = torch.from_numpy(rng.standard_normal(C).astype(np.float32)).to(dev)
+            ybuf = torch.empty(C, dtype=torch.float32, device=dev)
+            nbd = (2 * st0.numel() + C * 4 + 2 * C * 3 + 2 * C + 4 * vh + vh * dv) * 4
+
+            def mk_d(i, st0=st0, o=o):
+                ss = st0 if i == 0 else st0.clone()
+                hout = torch.empty_like(hin)
+                oo = o if i == 0 else torch.empty_like(o)
+                return lambda: ops.gdn_decode_step(xin, cw, hin, hout, ss, braw.view(-1), araw.view(-1), ag, dtg, kh, vh, dk, dv,
+                                                   y=ybuf, out=oo)
+            kd = Kernel("gdn_decode_step_fused", "one decode step after the input projections: conv + SiLU + Q/K "
+                        "L2 norm + gates + recurrence, one launch (layer_gdn.cpp:89-106)", nbd, nbd, mk_d)
+            kd.no_cpu = True
+            ks.append(kd)
         if rows > 1:
             # The chunked form on the same inputs (its workspace outside the bytes).
             ws = torch.empty(ops.load().qwen_gdn_recurrent_chunked_workspace_bytes(rows, vh), dtype=torch.uint8,

@@ -419,7 +419,7 @@ __global__ __launch_bounds__(kTileBlock) void gdn_step_tile(float* __restrict__ 
 // what they read: the 256 q | k channels of key head h % key_heads in
 // gdn_frontend_k4<32>'s layout (lane L: channels 4L..4L+3 of q for L < 32, of k
 // for L >= 32; a 32-lane sum of squares per head), moved to the recurrence's
-// layout with lane permutes, and each lane its 4 value channels. So every value
+// layout through a per-wave LDS copy, and each lane its 4 value channels. So every value
 // equals what gdn_frontend_rows writes and the recurrence reads, bit for bit.
 // Writes: the front end's output row y and the new history (q | k channels of
 // key head g by wave 0 of the tile h = g, cb = 0; value channels by wave 0 of
@@ -444,18 +444,18 @@ __global__ __launch_bounds__(kTileBlock) void gdn_decode_fused(
     const int j0 = cb * kTileCols + 4 * cg;
     const int r0 = w * (DK / kTileWaves) + rl;
     float* St = S + (static_cast<size_t>(h) * DK + r0) * value_dim + j0;
-    float4 s[RPL];
-#pragma unroll
-    for (int r = 0; r < RPL; ++r) s[r] = ld4_nt(St + static_cast<size_t>(kTileLanes * r) * value_dim);
     const int src = h % key_heads;
     const int kd = key_heads * DK;
     const bool is_q = lane < 32;
     const size_t c = static_cast<size_t>(is_q ? src * DK + 4 * lane : kd + src * DK + 4 * (lane - 32));
     const size_t cv = static_cast<size_t>(2 * kd + h * value_dim + j0);
 
-    // Every load issued before the first use, the state slice's first: taps,
-    // history and input of the lane's q | k channels and of its value
-    // channels, the gates.
+    // Every load issued before the first use: taps, history and input of the
+    // lane's q | k channels and of its value channels, the gates, then the
+    // state slice. Loads return in order, so the front end's inputs come first
+    // and its math runs while the state is still arriving (issued the other
+    // way round, the front end waited for the state: 4.6 us against 4.3 per
+    // step at 32 x 128 x 128).
     const float4 w0 = ld4(cw + 4 * c), w1 = ld4(cw + 4 * c + 4), w2 = ld4(cw + 4 * c + 8), w3 = ld4(cw + 4 * c + 12);
     const float4 ha = ld4(hin + 3 * c), hb = ld4(hin + 3 * c + 4), hd = ld4(hin + 3 * c + 8);
     const float4 xv = ld4(x + c);
@@ -463,6 +463,9 @@ __global__ __launch_bounds__(kTileBlock) void gdn_decode_fused(
     const float4 va = ld4(hin + 3 * cv), vb = ld4(hin + 3 * cv + 4), vd = ld4(hin + 3 * cv + 8);
     const float4 vx = ld4(x + cv);
     const float br = beta_raw[h], ar = alpha_raw[h], ah = a[h], dth = dt[h];
+    float4 s[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) s[r] = ld4_nt(St + static_cast<size_t>(kTileLanes * r) * value_dim);
     __builtin_amdgcn_sched_barrier(0);
 
     // q | k front end (gdn_frontend_k4<32>, one row)
@@ -496,20 +499,19 @@ __global__ __launch_bounds__(kTileBlock) void gdn_decode_fused(
         st4(hout + 3 * cv + 8, make_float4(vx.z, g1.w, g2.w, vx.w));
     }
 
-    // Recurrence layout: lane L needs q, k of rows i = r0 + 8 r -- channel i sits
-    // in lane i / 4 (q) or 32 + i / 4 (k), component i % 4 = L % 4 (r0 - L % 8
-    // and 8 r are multiples of 4).
-    auto pick = [&](int from) {
-        const float px = __shfl(f.x, from), py = __shfl(f.y, from), pz = __shfl(f.z, from), pw = __shfl(f.w, from);
-        const int k4 = lane & 3;
-        return k4 == 0 ? px : k4 == 1 ? py : k4 == 2 ? pz : pw;
-    };
+    // Recurrence layout: lane L needs q, k of rows i = r0 + 16 r. Lane L holds
+    // channels 4L..4L+3 of q (L < 32) or of k (L >= 32) in f, so the wave's f
+    // written to LDS as [lane][4] is the q | k head in channel order: q row i is
+    // float i, k row i float 128 + i. Each wave uses its own copy (no barrier:
+    // a wave's LDS accesses complete in order).
+    __shared__ float qk_lds[kTileWaves][2 * DK];
+    *reinterpret_cast<float4*>(&qk_lds[w][4 * lane]) = f;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     float qr[RPL], kr[RPL];
 #pragma unroll
     for (int r = 0; r < RPL; ++r) {
-        const int from = (r0 + kTileLanes * r) >> 2;
-        qr[r] = pick(from);
-        kr[r] = pick(32 + from);
+        qr[r] = qk_lds[w][r0 + kTileLanes * r];
+        kr[r] = qk_lds[w][DK + r0 + kTileLanes * r];
     }
 
     // gdn_step_tile<128>, gates from the raw projections
