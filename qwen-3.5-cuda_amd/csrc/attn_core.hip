@@ -197,6 +197,17 @@ __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
     float vcol[LH];
 #pragma unroll
     for (int i = 0; i < QCH; ++i) qr[i] = ld4(q + static_cast<size_t>(kv) * G * D + 4 * (tid + i * NT));
+    // NR: the front end's operands right behind q, so that the queries'
+    // norm + rotation runs while the keys and values are still arriving.
+    const int lane = tid & (kWave - 1);
+    float dn0 = 0.f;
+    float4 wq = make_float4(0.f, 0.f, 0.f, 0.f), wk = wq;
+    if constexpr (NR) {
+        dn0 = rope256_den(den, lane);
+        wq = ld4(nr.qw + 4 * lane);
+        wk = ld4(nr.kw + 4 * lane);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
         const int c = tid + i * NT;
@@ -210,9 +221,7 @@ __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
         // and of key t0 + w + 4 i in kr[i] (NT = 256, D4 = 64): whole heads per
         // wave, the layout norm_rope256 takes.
         static_assert(NT == 4 * kWave && D4 == kWave, "front end layout");
-        const int lane = tid & (kWave - 1), w = wave_in_block();
-        const float dn0 = rope256_den(den, lane);
-        const float4 wq = ld4(nr.qw + 4 * lane), wk = ld4(nr.kw + 4 * lane);
+        const int w = wave_in_block();
         const Rope256 rp = rope256_angles(static_cast<float>(n_keys - 1), dn0);
 #pragma unroll
         for (int i = 0; i < QCH; ++i) {
