@@ -138,18 +138,17 @@ __global__ __launch_bounds__(kBlock) void values_kernel(const float* __restrict_
 }
 
 // ---------------------------------------------------------------- fused decode
-// Workgroup (split, kv head): G query heads x L keys; kPairLanes lanes per
-// (head, key) pair take interleaved float4 chunks of the 256-wide dot product.
-// At Qwen3.5's shapes one lane per pair and G * L = 256 threads measured
-// fastest (32 keys per split for 8 heads per kv head, 16 for 16): larger
-// splits halve the partial rows the combine reads, and the scores' LDS reads
-// are broadcasts (a wave reads 2 query rows) or 16-byte rows of distinct keys.
-// All of the split's loads go out before the first wait (a wait on one load
-// waits for all loads issued before it). Keys go through LDS (rows padded to
-// kKeyStride floats so the keys of a wave hit different banks); values stay
-// in VGPRs, thread (group, column) holding its column of one group of keys;
-// groups of P.V (when the workgroup has more threads than columns) meet in
-// LDS. Workspace: acc [Hkv][splits][G][D], then m and l [Hkv][splits][G].
+// Workgroup (split, kv head): G query heads x L keys, G * L = 256 threads,
+// thread (head, key) for the softmax (32 keys per split for 8 heads per kv
+// head, 16 for 16: larger splits halve the partial rows the combine reads).
+// The scores are 16 x 16 fp32 MFMA tiles over the queries and keys staged in
+// LDS (see below). All of the split's loads go out before the first wait (a
+// wait on one load waits for all loads issued before it). Keys go through LDS
+// (rows padded to kKeyStride floats so the 16 rows of a tile hit different
+// banks); values stay in VGPRs, thread (group, column) holding its column of
+// one group of keys; groups of P.V (when the workgroup has more threads than
+// columns) meet in LDS. Workspace: acc [Hkv][splits][G][D], then m and l
+// [Hkv][splits][G].
 constexpr int kKeyStride = kMaxDim + 4;
 constexpr int kPairLanes = 1;
 
@@ -184,6 +183,7 @@ __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
     __shared__ float4 q_lds[G][D4];
     __shared__ __align__(16) float k_lds[L][kKeyStride];
     __shared__ __align__(16) float p_lds[G][L];
+    __shared__ float sc_lds[(NT / kWave) / (L / 16)][L / 16][16][17];   // partial score tiles
     __shared__ float acc_lds[HALVES > 1 ? HALVES - 1 : 1][HALVES > 1 ? G : 1][HALVES > 1 ? D : 1];
     const int split = blockIdx.x, kv = blockIdx.y;
     const int tid = threadIdx.x;
@@ -251,27 +251,45 @@ __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
     }
     __syncthreads();
 
-    // scores: pair (hh, tt) = lanes 4*pair .. +3; lane r takes chunks r, r+4, ...
+    // scores on the matrix cores (v_mfma_f32_16x16x4_f32): 16 keys x 16 heads
+    // tiles (8 query heads: columns 8..15 repeat them and are not read), the
+    // head dim split in P parts over the waves; wave w takes tile w % T, part
+    // w / T. In a 16x16x4 product lane l gives A[key l % 16][k = l / 16] and
+    // B[k][head l % 16]; lane group g = l / 16 runs over dims part DP + g DP/4
+    // + j (j < DP/4), four at a time from one 16-byte LDS read of the key row
+    // and of the query row. The P partial tiles meet in LDS and are added in
+    // part order for thread (head hh, key tt). (Per-thread dot products over
+    // LDS read 2 KB per thread, 512 KB per workgroup: 11.0 against 10.25 us
+    // per decode at 4096 keys.)
     const int pair = tid / kPairLanes, r = tid % kPairLanes;
     const int hh = pair / L, tt = pair % L;
     const bool valid = t0 + tt < n_keys;
-    float a0 = 0.f, a1 = 0.f;
+    {
+        constexpr int T = L / 16, P = (NT / kWave) / T, DP = D / P;
+        static_assert(T * 16 == L && P * T == NT / kWave && G <= 16 && DP % 16 == 0, "score tiles");
+        typedef float v4f_t __attribute__((ext_vector_type(4)));
+        const int w = wave_in_block(), l = tid & (kWave - 1);
+        const int tile = w % T, part = w / T;
+        const int m = l & 15, g = l >> 4;
+        const float* krow = &k_lds[tile * 16 + m][part * DP + g * (DP / 4)];
+        const float4* qrow = &q_lds[m % G][(part * DP + g * (DP / 4)) / 4];
+        v4f_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
-    for (int c = r; c < D4; c += 2 * kPairLanes) {
-        const float4 kk = *reinterpret_cast<const float4*>(&k_lds[tt][4 * c]);
-        const float4 qq = q_lds[hh][c];
-        const float4 k2 = *reinterpret_cast<const float4*>(&k_lds[tt][4 * (c + kPairLanes)]);
-        const float4 q2 = q_lds[hh][c + kPairLanes];
-        a0 = __builtin_fmaf(qq.x, kk.x, a0);
-        a1 = __builtin_fmaf(q2.x, k2.x, a1);
-        a0 = __builtin_fmaf(qq.y, kk.y, a0);
-        a1 = __builtin_fmaf(q2.y, k2.y, a1);
-        a0 = __builtin_fmaf(qq.z, kk.z, a0);
-        a1 = __builtin_fmaf(q2.z, k2.z, a1);
-        a0 = __builtin_fmaf(qq.w, kk.w, a0);
-        a1 = __builtin_fmaf(q2.w, k2.w, a1);
+        for (int s = 0; s < DP / 16; ++s) {
+            const float4 ka = *reinterpret_cast<const float4*>(krow + 4 * s);
+            const float4 qb = qrow[s];
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.x, qb.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.y, qb.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.z, qb.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.w, qb.w, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc_lds[part][tile][4 * g + i][m] = acc[i];   // key 4g + i, head m
+        __syncthreads();
     }
-    const float dot = group_sum<kPairLanes>(a0 + a1);
+    float dot = 0.f;
+#pragma unroll
+    for (int p = 0; p < (NT / kWave) / (L / 16); ++p) dot += sc_lds[p][tt >> 4][tt & 15][hh];
     const float sc = valid ? dot * scale : -INFINITY;
     // max and sum over the L keys of head hh: 4*L consecutive lanes
     constexpr int HL = L * kPairLanes;
