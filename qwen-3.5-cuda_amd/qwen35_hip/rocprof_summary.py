@@ -49,6 +49,9 @@ NAMES = [
     # next rows (kernel symbols; several bench shapes can share one instantiation)
     ("gemv_mfma<14, 2>", "gemv Q6_K MFMA, 2-block k-slices (LM head)"),
     ("gemv_mfma<12, 2>", "gemv Q4_K MFMA, 2-block k-slices"),
+    ("gemv_q4k_direct_swiglu", "gemv Q4_K direct, MoE SwiGLU rows (moe_route_swiglu)"),
+    ("gemv_q4k_norm_gate", "gemv Q4_K direct after the gated norm (gdn_norm_gate_matmul)"),
+    ("moe_down_combine_q4k", "moe_down_combine, Q4_K direct (routed + shared down, combine)"),
     ("gemv_q4k_direct_multi", "gemv Q4_K direct, several matrices of one x (matmul_dispatch_multi)"),
     ("gemv_q4k_direct_gate_up", "gemv Q4_K direct, routed experts' gate + up (moe_expert_gate_up)"),
     ("gemv_q4k_direct<2, 1>", "gemv Q4_K direct, 2 rows/wave (GDN qkv)"),
