@@ -303,7 +303,7 @@ __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
     const float p = valid ? expf(sc - m) : 0.0f;  // every split holds at least one valid key
     const float l = group_sum<HL>(r == 0 ? p : 0.0f);
     if (r == 0) p_lds[hh][tt] = p;
-    const size_t stat = (static_cast<size_t>(kv) * splits + split) * G + hh;
+    const size_t stat = (static_cast<size_t>(kv) * G + hh) * splits + split;
     if (tt == 0 && r == 0) {
         ws_m[stat] = m;
         ws_l[stat] = l;
@@ -339,76 +339,101 @@ __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
         }
     }
 #pragma unroll
-    for (int h2 = 0; h2 < G; ++h2) ws_acc[((static_cast<size_t>(kv) * splits + split) * G + h2) * D + col] = acc[h2];
+    // partials as [head][16-column block][split][16]: the combine's workgroup
+    // (head, column block) then reads one contiguous run
+    for (int h2 = 0; h2 < G; ++h2)
+        ws_acc[((static_cast<size_t>(kv) * G + h2) * (D / 16) + col / 16) * splits * 16 + split * 16 + (col & 15)] =
+            acc[h2];
 }
 
-// Workgroup (query head, 64 columns): wave w folds splits w, w+4, ... for the
-// 64 columns (lane = column) into a running (max, weight, sum) with the usual
-// online rescaling, kCombineBatch splits per memory round trip (the partials
-// were written by workgroups on every XCD, so they come from memory); the four
-// wave states merge in LDS, then divide by the total weight and apply the gate.
-constexpr int kCombineCols = 64;
-constexpr int kCombineBatch = 32;
+// Workgroup (query head, 16 columns), 256 workgroups for 16 heads of 256
+// columns. Every wave first reduces the head's largest split max M over all
+// splits (lane-strided loads, a DPP max); thread (wave w, lane L) then adds
+// exp(m_s - M) times the partial row of splits s = 16 w + L/4, + 64, + 128, ...
+// for columns 4 (L % 4) .. + 3 of the block (one 16-byte load per split), and
+// exp(m_s - M) l_s; the 16 lanes of a column quad add up by lane swaps and the
+// 4 waves through LDS in wave order, then the sum is divided by the total
+// weight and gated. One max and no rescaling chain: the merge of running
+// (max, weight, sum) states split by split costs ~2 us of dependent exp/FMA
+// latency at 128 splits, more than the kernel's loads.
+// The split pass stores the partials as [head][16-column block][split][16],
+// so a workgroup reads one contiguous run of splits x 64 bytes.
+constexpr int kCombineCols = 16;
+constexpr int kCombineBatch = 2;   // splits per thread and memory round trip
 
 __global__ __launch_bounds__(kBlock) void decode_combine(const float* __restrict__ ws_acc,
                                                          const float* __restrict__ ws_m,
                                                          const float* __restrict__ ws_l,
                                                          const float* __restrict__ gate, float* __restrict__ out,
-                                                         int group, int dim, int splits) {
-    constexpr int NW = kBlock / kWave;
-    __shared__ float zpart[NW][kCombineCols];
-    __shared__ float mpart[NW], tpart[NW];
-    const int h = blockIdx.x;
-    const int kv = h / group, hh = h - kv * group;
+                                                         int splits) {
+    constexpr int D = kMaxDim, NCB = D / kCombineCols, NW = kBlock / kWave;
+    constexpr int SPW = kWave / 4;   // splits per wave and round (4 lanes per split)
+    constexpr int STEP = SPW * NW * kCombineBatch;
+    __shared__ float4 zpart[NW][4];
+    __shared__ float tpart[NW][4];
+    const int h = blockIdx.x / NCB, cb = blockIdx.x - h * NCB;
     const int lane = threadIdx.x & 63, w = wave_in_block();
-    const int j = blockIdx.y * kCombineCols + lane;
-    const int jc = min(j, dim - 1);
-    const size_t s0 = static_cast<size_t>(kv) * splits * group + hh;  // stat of split s: s0 + s * group
-    const float* accp = ws_acc + (static_cast<size_t>(kv) * splits * group + hh) * dim + jc;  // split s: + s*group*dim
-    const size_t acc_split = static_cast<size_t>(group) * dim;
-    // Per batch: lane i < kCombineBatch loads the statistics of split
-    // base + i*NW (vector loads; as wave-uniform scalar loads they would queue
-    // behind the scalar cache's small limit of outstanding requests), every
-    // lane loads its column of all kCombineBatch partial rows.
-    float m = -INFINITY, z = 0.f, tot = 0.f;
-    for (int base = w; base < splits; base += NW * kCombineBatch) {
-        const int si = base + min(lane, kCombineBatch - 1) * NW;
-        const bool mine = lane < kCombineBatch && si < splits;
-        const float mi = mine ? ws_m[s0 + static_cast<size_t>(si) * group] : -INFINITY;
-        const float li = mine ? ws_l[s0 + static_cast<size_t>(si) * group] : 0.0f;
-        float a[kCombineBatch];
+    const int cq = lane & 3;
+    const size_t s0 = static_cast<size_t>(h) * splits;   // stat of split s: s0 + s
+    const float* accp = ws_acc + (s0 * NCB + static_cast<size_t>(cb) * splits) * kCombineCols + 4 * cq;  // + 16 s
+    const int first = SPW * w + (lane >> 2);
+    // the first batch's partials and statistics, requested with the max's loads
+    float4 a[kCombineBatch];
+    float mi[kCombineBatch], li[kCombineBatch];
+    auto load_batch = [&](int base) {
 #pragma unroll
-        for (int i = 0; i < kCombineBatch; ++i)
-            a[i] = accp[static_cast<size_t>(min(base + i * NW, splits - 1)) * acc_split];
-        const float mb = fmaxf(m, wave_max(mi));
-        const float r = expf(m - mb);  // 0 on the first batch (m = -inf)
-        const float ei = mine ? expf(mi - mb) : 0.0f;
-        tot = __builtin_fmaf(tot, r, group_sum<64>(ei * li));
-        z *= r;
+        for (int i = 0; i < kCombineBatch; ++i) {
+            const size_t sc = static_cast<size_t>(min(base + i * SPW * NW, splits - 1));
+            a[i] = ld4(accp + sc * kCombineCols);
+            mi[i] = ws_m[s0 + sc];
+            li[i] = ws_l[s0 + sc];
+        }
+    };
+    load_batch(first);
+    float M = -INFINITY;
+    for (int s = lane; s < splits; s += kWave) M = fmaxf(M, ws_m[s0 + s]);
+    M = wave_max(M);
+    float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    float t = 0.f;
+    for (int base = first;;) {
 #pragma unroll
-        for (int i = 0; i < kCombineBatch; ++i)  // weight of split base + i*NW (0 past the end)
-            z = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ei), i)), a[i], z);
-        m = mb;
+        for (int i = 0; i < kCombineBatch; ++i) {
+            const float e = base + i * SPW * NW < splits ? expf(mi[i] - M) : 0.f;
+            t = __builtin_fmaf(e, li[i], t);
+            z = make_float4(__builtin_fmaf(e, a[i].x, z.x), __builtin_fmaf(e, a[i].y, z.y),
+                            __builtin_fmaf(e, a[i].z, z.z), __builtin_fmaf(e, a[i].w, z.w));
+        }
+        base += STEP;
+        if (base >= splits) break;
+        load_batch(base);
     }
-    zpart[w][lane] = z;
-    if (lane == 0) {
-        mpart[w] = m;
-        tpart[w] = tot;
+#pragma unroll
+    for (int o = 4; o < kWave; o <<= 1) {
+        t += __shfl_xor(t, o);
+        z.x += __shfl_xor(z.x, o);
+        z.y += __shfl_xor(z.y, o);
+        z.z += __shfl_xor(z.z, o);
+        z.w += __shfl_xor(z.w, o);
+    }
+    if (lane < 4) {
+        zpart[w][lane] = z;
+        tpart[w][lane] = t;
     }
     __syncthreads();
-    if (w == 0 && j < dim) {
-        const float M = fmaxf(fmaxf(mpart[0], mpart[1]), fmaxf(mpart[2], mpart[3]));
-        float zz = 0.f, tt = 0.f;
+    if (w == 0 && lane < 4) {
+        float4 zz = zpart[0][lane];
+        float tt = tpart[0][lane];
 #pragma unroll
-        for (int v = 0; v < NW; ++v) {
-            if (mpart[v] == -INFINITY) continue;  // a wave with no split (splits < NW)
-            const float e = expf(mpart[v] - M);
-            zz = __builtin_fmaf(e, zpart[v][lane], zz);
-            tt = __builtin_fmaf(e, tpart[v], tt);
+        for (int v = 1; v < NW; ++v) {
+            zz = make_float4(zz.x + zpart[v][lane].x, zz.y + zpart[v][lane].y, zz.z + zpart[v][lane].z,
+                             zz.w + zpart[v][lane].w);
+            tt += tpart[v][lane];
         }
-        float o = zz / tt;
-        if (gate) o = o / (1.0f + expf(-gate[static_cast<size_t>(h) * dim + j]));
-        out[static_cast<size_t>(h) * dim + j] = o;
+        const float o[4] = {zz.x / tt, zz.y / tt, zz.z / tt, zz.w / tt};
+        const size_t j0 = static_cast<size_t>(h) * D + cb * kCombineCols + 4 * lane;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            out[j0 + i] = gate ? o[i] / (1.0f + expf(-gate[j0 + i])) : o[i];
     }
 }
 
@@ -567,8 +592,7 @@ int split_combine(const float* q, const float* k_cache, const float* v_cache, co
                                                                       n_keys, splits, scale, nr, den);
     int st = check_launch("attn_decode");
     if (st) return st;
-    decode_combine<<<dim3(heads, (dim + kCombineCols - 1) / kCombineCols), kBlock, 0, s>>>(acc, m, l, gate, out, g,
-                                                                                        dim, splits);
+    decode_combine<<<heads * (kMaxDim / kCombineCols), kBlock, 0, s>>>(acc, m, l, gate, out, splits);
     return check_launch("attn_decode");
 }
 

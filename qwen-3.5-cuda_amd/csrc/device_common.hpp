@@ -129,6 +129,17 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 }
 
 // ---------------------------------------------------------------- memory
+// Tile of workgroup b in a grid of exactly `tiles` workgroups. Workgroups are
+// dealt to the 8 XCDs round robin (b % 8), so tiles 2 l and 2 l + 1 (two
+// halves of a 128-byte line segment) go to workgroups b and b + 8 of a group
+// of 16, on one XCD, whose L2 then fetches the line once; the last tiles % 16
+// keep their own index. A bijection on [0, tiles).
+__device__ __forceinline__ int tile_of_block(int b, int tiles) {
+    if (b >= (tiles & ~15)) return b;
+    const int idx = b >> 3;
+    return (((idx >> 1) << 3) + (b & 7)) * 2 + (idx & 1);
+}
+
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }

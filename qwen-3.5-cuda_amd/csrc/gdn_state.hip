@@ -285,17 +285,6 @@ constexpr int kTileLanes = 16;                       // lanes per column group
 constexpr int kTileGroups = kWave / kTileLanes;      // column groups per wave
 constexpr int kTileCols = 4 * kTileGroups;           // value columns per workgroup
 
-// Tile of workgroup b in a grid of exactly `tiles` workgroups. Workgroups are
-// dealt to the 8 XCDs round robin (b % 8), so tiles 2 l and 2 l + 1 (the two
-// halves of a 128-byte line segment when value_dim % 32 == 0) go to workgroups
-// b and b + 8 of a group of 16; the last tiles % 16 keep their own index. A
-// bijection on [0, tiles).
-__device__ __forceinline__ int tile_of_block(int b, int tiles) {
-    if (b >= (tiles & ~15)) return b;
-    const int idx = b >> 3;
-    return (((idx >> 1) << 3) + (b & 7)) * 2 + (idx & 1);
-}
-
 // One token on a lane's slice (RPL rows kr / qr of k / q, the state rows s at
 // St + 8 r * value_dim, value columns vv, gates b / d): S *= d; m = k . S;
 // delta = (v - m) b; S += k delta; o = q . S. Stores the state slice and
