@@ -377,6 +377,14 @@ __global__ __launch_bounds__(kBlock) void decode_combine(const float* __restrict
     const size_t s0 = static_cast<size_t>(h) * splits;   // stat of split s: s0 + s
     const float* accp = ws_acc + (s0 * NCB + static_cast<size_t>(cb) * splits) * kCombineCols + 4 * cq;  // + 16 s
     const int first = SPW * w + (lane >> 2);
+    // the gate of the columns this lane stores (lanes 0-3 of wave 0), requested
+    // first: loaded at the end it would add a memory round trip to the tail
+    const size_t j0 = static_cast<size_t>(h) * D + cb * kCombineCols + 4 * cq;
+    float gv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (gate) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) gv[i] = gate[j0 + i];
+    }
     // the first batch's partials and statistics, requested with the max's loads
     float4 a[kCombineBatch];
     float mi[kCombineBatch], li[kCombineBatch];
@@ -430,10 +438,8 @@ __global__ __launch_bounds__(kBlock) void decode_combine(const float* __restrict
             tt += tpart[v][lane];
         }
         const float o[4] = {zz.x / tt, zz.y / tt, zz.z / tt, zz.w / tt};
-        const size_t j0 = static_cast<size_t>(h) * D + cb * kCombineCols + 4 * lane;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            out[j0 + i] = gate ? o[i] / (1.0f + expf(-gate[j0 + i])) : o[i];
+        for (int i = 0; i < 4; ++i) out[j0 + i] = gate ? o[i] / (1.0f + expf(-gv[i])) : o[i];
     }
 }
 
