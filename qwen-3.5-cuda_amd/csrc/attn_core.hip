@@ -147,8 +147,8 @@ __global__ __launch_bounds__(kBlock) void values_kernel(const float* __restrict_
 // (rows padded to kKeyStride floats so the 16 rows of a tile hit different
 // banks); values stay in VGPRs, thread (group, column) holding its column of
 // one group of keys; groups of P.V (when the workgroup has more threads than
-// columns) meet in LDS. Workspace: acc [Hkv][splits][G][D], then m and l
-// [Hkv][splits][G].
+// columns) meet in LDS. Workspace: acc [H][D / 16][splits][16] (query head
+// h = kv G + head of the group), then m and l [H][splits].
 constexpr int kKeyStride = kMaxDim + 4;
 constexpr int kPairLanes = 1;
 
