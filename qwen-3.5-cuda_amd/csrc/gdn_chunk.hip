@@ -18,9 +18,9 @@
 // The decay ratios are running products, never quotients, so decays that
 // underflow give exact zeros rather than 0/0.
 //
-// Kernel A (one workgroup per (chunk, value head), all chunks in parallel):
-// K K^T and Q K^T on fp32 MFMA (v_mfma_f32_16x16x4f32), the ratios, and T as a
-// blocked inverse (16 x 16 diagonal blocks by forward substitution, the others
+// Kernel A (one workgroup per (chunk, key head), all chunks in parallel):
+// K K^T and Q K^T on fp32 MFMA (v_mfma_f32_16x16x4f32) once, then for each value
+// head that reads this key head the ratios and T as a blocked inverse (16 x 16 diagonal blocks by forward substitution, the others
 // as MFMA products) -> T', Bm, gamma, R[C-1][.] to the caller's workspace.
 // Kernel B (one workgroup per (value head, 16 state columns), chunks in order,
 // the workgroups of one head on one XCD):
@@ -76,27 +76,21 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
                                                            const float* __restrict__ decay, float* __restrict__ ws,
                                                            int rows, int key_heads, int value_heads,
                                                            int64_t qkv_stride) {
-    __shared__ __align__(16) float Kl[kC][kDK + 4];   // the chunk's K rows
-    __shared__ __align__(16) float G[kC][kLdA];    // K K^T, then A (strictly lower)
-    __shared__ __align__(16) float Pm[kC][kLdA];   // Q K^T, then T
+    // The chunk's K rows while the products run; after them the same storage
+    // holds A (strictly lower) and T of the value head in hand.
+    __shared__ __align__(16) float kat[2 * kC * kLdA];
+    static_assert(kC * (kDK + 4) <= 2 * kC * kLdA, "K rows fit the A and T storage");
+    __shared__ __align__(16) float G[kC][kLdA];    // K K^T
+    __shared__ __align__(16) float Pm[kC][kLdA];   // Q K^T
     __shared__ __align__(16) float sb[kC], sd[kC];
-    const int c = blockIdx.x, h = blockIdx.y;
+    float(*Kl)[kDK + 4] = reinterpret_cast<float(*)[kDK + 4]>(kat);
+    float(*Ab)[kLdA] = reinterpret_cast<float(*)[kLdA]>(kat);
+    float(*T)[kLdA] = reinterpret_cast<float(*)[kLdA]>(kat + kC * kLdA);
+    const int c = blockIdx.x, src = blockIdx.y;   // chunk, key head
     const int t0 = c * kC;
-    const int src = h % key_heads;
     const int lane = threadIdx.x & 63;
     const int wv = wave_in_block();
     const int g = lane >> 4, n = lane & 15;
-    float* wsc = ws + (static_cast<size_t>(c) * value_heads + h) * kWsFloats;
-    float* Tp = wsc;
-    float* Bm = wsc + kC * kC;
-    float* gam = wsc + 2 * kC * kC;
-    float* rr = gam + kC;
-
-    if (threadIdx.x < kC) {  // padding tokens: beta 0 (no update), decay 1
-        const int t = t0 + threadIdx.x;
-        sb[threadIdx.x] = t < rows ? beta[static_cast<int64_t>(t) * value_heads + h] : 0.0f;
-        sd[threadIdx.x] = t < rows ? decay[static_cast<int64_t>(t) * value_heads + h] : 1.0f;
-    }
 
     // Lower-triangle 16x16 tiles (mt >= nt) of K K^T and Q K^T. Wave w loads
     // the K and Q rows of tokens 16w .. 16w+15 once (lane: token 16w + L%16,
@@ -146,114 +140,129 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
             tile(a, mt, nt, G);
         }
     }
-    __syncthreads();
 
-    // Rows 16wv .. 16wv+15 per wave, lane i = column i: R[t][i] as a running
-    // product (the factor up to the wave's first row rebuilt from the decays,
-    // the same multiplication sequence as one pass over all rows), A and Bm.
-    // The decays are read once into registers (broadcast LDS reads) and the
-    // products run over all 64 positions with the factors outside a lane's
-    // range replaced by 1.0 (exact), so the chains are plain multiplies
-    // without an LDS round trip per step.
-    {
-        const int i = lane;
-        const int ta = 16 * wv;
-        float dall[kC];
-#pragma unroll
-        for (int t = 0; t < kC; t += 4) {
-            const float4 v4 = *reinterpret_cast<const float4*>(&sd[t]);
-            dall[t] = v4.x;
-            dall[t + 1] = v4.y;
-            dall[t + 2] = v4.z;
-            dall[t + 3] = v4.w;
-        }
-        float r = 1.0f;
-#pragma unroll
-        for (int t = 1; t < kC - 16; ++t) r *= (t > i && t < ta) ? dall[t] : 1.0f;
-        float dv16[16], bv16[16], gv[16], pv[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            dv16[u] = sd[ta + u];
-            bv16[u] = sb[ta + u];
-            gv[u] = G[ta + u][i];
-            pv[u] = Pm[ta + u][i];
-        }
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int t = ta + u;
-            if (t > i) r *= dv16[u];
-            G[t][i] = t > i ? (bv16[u] * gv[u]) * r : 0.0f;
-            Bm[t * kC + i] = t >= i ? pv[u] * r : 0.0f;
-        }
-        if (wv == 3) rr[i] = r;  // R[C-1][i]
-        if (wv == 0) {  // gamma_t = d_0 * ... * d_t in order, lane t
-            float gm = 1.0f;
-#pragma unroll
-            for (int t = 0; t < kC; ++t) gm *= t <= lane ? dall[t] : 1.0f;
-            gam[lane] = gm;
-        }
-    }
-    __syncthreads();
-
-    // T = (I + A)^-1 in 16 x 16 blocks (A strictly lower). Diagonal blocks by
-    // forward substitution, lane L = block L/16, column L%16:
-    //   T_II[t][j] = [t == j] - sum_{i<t} A_II[t][i] T_II[i][j];
-    // then block rows I = 1..3, wave J computing
-    //   T_IJ = -T_II (sum_{K=J}^{I-1} A_IK T_KJ)
-    // on MFMA. The 4 k-slots of the MFMAs of one 16-deep product map to
-    // k = 4g + q (q the MFMA's index): A operands are 4 consecutive floats of a
-    // row, and a result in the D layout (lane: rows 4g + r) is directly the B
-    // operand of the next product. T goes to Pm's storage (Pm is consumed).
-    float(*T)[kLdA] = Pm;
-    __syncthreads();  // every wave is done reading Pm
-    if (wv == 0) {
-        const int I = lane >> 4, j = lane & 15;
-        float tc[16];
-#pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            float acc[4] = {t == j ? 1.0f : 0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int i4 = 0; i4 < t; i4 += 4) {
-                const float4 a = *reinterpret_cast<const float4*>(&G[16 * I + t][16 * I + i4]);
-                acc[0] = __builtin_fmaf(-a.x, tc[i4], acc[0]);
-                if (i4 + 1 < t) acc[1] = __builtin_fmaf(-a.y, tc[i4 + 1], acc[1]);
-                if (i4 + 2 < t) acc[2] = __builtin_fmaf(-a.z, tc[i4 + 2], acc[2]);
-                if (i4 + 3 < t) acc[3] = __builtin_fmaf(-a.w, tc[i4 + 3], acc[3]);
-            }
-            tc[t] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-            T[16 * I + t][16 * I + j] = tc[t];
-        }
-    }
-    __syncthreads();
-    // 16 x 16 x 16 product: acc += X[16xa rows][16xa cols] * Y, X rows from LDS at
-    // (xr, xc), Y given as its D-layout registers (rows 4g + q, column n).
-    auto prod_regs = [&](v4f_t acc, const float(*X)[kLdA], int xr, int xc, const v4f_t& y) {
-        const float4 a = *reinterpret_cast<const float4*>(&X[xr + n][xc + 4 * g]);
-        acc = mfma4(a.x, y[0], acc);
-        acc = mfma4(a.y, y[1], acc);
-        acc = mfma4(a.z, y[2], acc);
-        return mfma4(a.w, y[3], acc);
-    };
-    for (int I = 1; I < 4; ++I) {
-        if (wv < I) {
-            const int J = wv;
-            v4f_t m = {0.f, 0.f, 0.f, 0.f};
-            for (int K = J; K < I; ++K) {
-                v4f_t tkj;  // T_KJ rows 4g + q, column n
-#pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4) tkj[q4] = T[16 * K + 4 * g + q4][16 * J + n];
-                m = prod_regs(m, G, 16 * I, 16 * K, tkj);
-            }
-            v4f_t t = prod_regs(v4f_t{0.f, 0.f, 0.f, 0.f}, T, 16 * I, 16 * I, m);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) T[16 * I + 4 * g + r][16 * J + n] = -t[r];
+    // The products depend on the key head only: every value head h with
+    // h % key_heads == src (the heads that read this key head) takes them from
+    // here, so K and Q are read and multiplied once per key head.
+    for (int h = src; h < value_heads; h += key_heads) {
+        float* wsc = ws + (static_cast<size_t>(c) * value_heads + h) * kWsFloats;
+        float* Tp = wsc;
+        float* Bm = wsc + kC * kC;
+        float* gam = wsc + 2 * kC * kC;
+        float* rr = gam + kC;
+        __syncthreads();   // the products are done; the previous head's readers of sb, sd, A, T too
+        if (threadIdx.x < kC) {  // padding tokens: beta 0 (no update), decay 1
+            const int t = t0 + threadIdx.x;
+            sb[threadIdx.x] = t < rows ? beta[static_cast<int64_t>(t) * value_heads + h] : 0.0f;
+            sd[threadIdx.x] = t < rows ? decay[static_cast<int64_t>(t) * value_heads + h] : 1.0f;
         }
         __syncthreads();
-    }
-    // T' = T diag(beta), zeros above the diagonal.
-    for (int e = threadIdx.x; e < kC * kC; e += kThreads) {
-        const int t = e / kC, jj = e % kC;
-        Tp[e] = t >= jj ? T[t][jj] * sb[jj] : 0.0f;
+
+        // Rows 16wv .. 16wv+15 per wave, lane i = column i: R[t][i] as a running
+        // product (the factor up to the wave's first row rebuilt from the decays,
+        // the same multiplication sequence as one pass over all rows), A and Bm.
+        // The decays are read once into registers (broadcast LDS reads) and the
+        // products run over all 64 positions with the factors outside a lane's
+        // range replaced by 1.0 (exact), so the chains are plain multiplies
+        // without an LDS round trip per step.
+        {
+            const int i = lane;
+            const int ta = 16 * wv;
+            float dall[kC];
+#pragma unroll
+            for (int t = 0; t < kC; t += 4) {
+                const float4 v4 = *reinterpret_cast<const float4*>(&sd[t]);
+                dall[t] = v4.x;
+                dall[t + 1] = v4.y;
+                dall[t + 2] = v4.z;
+                dall[t + 3] = v4.w;
+            }
+            float r = 1.0f;
+#pragma unroll
+            for (int t = 1; t < kC - 16; ++t) r *= (t > i && t < ta) ? dall[t] : 1.0f;
+            float dv16[16], bv16[16], gv[16], pv[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                dv16[u] = sd[ta + u];
+                bv16[u] = sb[ta + u];
+                gv[u] = G[ta + u][i];
+                pv[u] = Pm[ta + u][i];
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int t = ta + u;
+                if (t > i) r *= dv16[u];
+                Ab[t][i] = t > i ? (bv16[u] * gv[u]) * r : 0.0f;
+                Bm[t * kC + i] = t >= i ? pv[u] * r : 0.0f;
+            }
+            if (wv == 3) rr[i] = r;  // R[C-1][i]
+            if (wv == 0) {  // gamma_t = d_0 * ... * d_t in order, lane t
+                float gm = 1.0f;
+#pragma unroll
+                for (int t = 0; t < kC; ++t) gm *= t <= lane ? dall[t] : 1.0f;
+                gam[lane] = gm;
+            }
+        }
+        __syncthreads();
+
+        // T = (I + A)^-1 in 16 x 16 blocks (A strictly lower). Diagonal blocks by
+        // forward substitution, lane L = block L/16, column L%16:
+        //   T_II[t][j] = [t == j] - sum_{i<t} A_II[t][i] T_II[i][j];
+        // then block rows I = 1..3, wave J computing
+        //   T_IJ = -T_II (sum_{K=J}^{I-1} A_IK T_KJ)
+        // on MFMA. The 4 k-slots of the MFMAs of one 16-deep product map to
+        // k = 4g + q (q the MFMA's index): A operands are 4 consecutive floats of a
+        // row, and a result in the D layout (lane: rows 4g + r) is directly the B
+        // operand of the next product.
+        if (wv == 0) {
+            const int I = lane >> 4, j = lane & 15;
+            float tc[16];
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                float acc[4] = {t == j ? 1.0f : 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int i4 = 0; i4 < t; i4 += 4) {
+                    const float4 a = *reinterpret_cast<const float4*>(&Ab[16 * I + t][16 * I + i4]);
+                    acc[0] = __builtin_fmaf(-a.x, tc[i4], acc[0]);
+                    if (i4 + 1 < t) acc[1] = __builtin_fmaf(-a.y, tc[i4 + 1], acc[1]);
+                    if (i4 + 2 < t) acc[2] = __builtin_fmaf(-a.z, tc[i4 + 2], acc[2]);
+                    if (i4 + 3 < t) acc[3] = __builtin_fmaf(-a.w, tc[i4 + 3], acc[3]);
+                }
+                tc[t] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+                T[16 * I + t][16 * I + j] = tc[t];
+            }
+        }
+        __syncthreads();
+        // 16 x 16 x 16 product: acc += X[16xa rows][16xa cols] * Y, X rows from LDS at
+        // (xr, xc), Y given as its D-layout registers (rows 4g + q, column n).
+        auto prod_regs = [&](v4f_t acc, const float(*X)[kLdA], int xr, int xc, const v4f_t& y) {
+            const float4 a = *reinterpret_cast<const float4*>(&X[xr + n][xc + 4 * g]);
+            acc = mfma4(a.x, y[0], acc);
+            acc = mfma4(a.y, y[1], acc);
+            acc = mfma4(a.z, y[2], acc);
+            return mfma4(a.w, y[3], acc);
+        };
+        for (int I = 1; I < 4; ++I) {
+            if (wv < I) {
+                const int J = wv;
+                v4f_t m = {0.f, 0.f, 0.f, 0.f};
+                for (int K = J; K < I; ++K) {
+                    v4f_t tkj;  // T_KJ rows 4g + q, column n
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4) tkj[q4] = T[16 * K + 4 * g + q4][16 * J + n];
+                    m = prod_regs(m, Ab, 16 * I, 16 * K, tkj);
+                }
+                v4f_t t = prod_regs(v4f_t{0.f, 0.f, 0.f, 0.f}, T, 16 * I, 16 * I, m);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) T[16 * I + 4 * g + r][16 * J + n] = -t[r];
+            }
+            __syncthreads();
+        }
+        // T' = T diag(beta), zeros above the diagonal.
+        for (int e = threadIdx.x; e < kC * kC; e += kThreads) {
+            const int t = e / kC, jj = e % kC;
+            Tp[e] = t >= jj ? T[t][jj] * sb[jj] : 0.0f;
+        }
     }
 }
 
@@ -521,7 +530,7 @@ int qwen_gdn_recurrent_chunked(float* state, const float* q, const float* k, con
     const hipStream_t s = as_stream(stream);
     const int nchunks = (rows + kC - 1) / kC;
     float* ws = static_cast<float*>(workspace);
-    gdn_chunk_prep<<<dim3(nchunks, value_heads), kThreads, 0, s>>>(q, k, beta, decay, ws, rows, key_heads, value_heads,
+    gdn_chunk_prep<<<dim3(nchunks, std::min(key_heads, value_heads)), kThreads, 0, s>>>(q, k, beta, decay, ws, rows, key_heads, value_heads,
                                                                    qkv_stride);
     gdn_chunk_state<<<(value_dim / kNB) * value_heads, kThreads, 0, s>>>(state, q, k, v, ws, out, rows, key_heads,
                                                                          value_heads, value_dim, qkv_stride,
