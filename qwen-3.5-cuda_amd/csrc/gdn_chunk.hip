@@ -92,6 +92,19 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
     const int wv = wave_in_block();
     const int g = lane >> 4, n = lane & 15;
 
+    // beta and decay of token t0 + threadIdx.x (threads < kC) for value head h,
+    // held in registers: the next head's are requested while this head's work
+    // runs. Padding tokens: beta 0 (no update), decay 1.
+    float bn = 0.0f, dn = 1.0f;
+    auto load_gates = [&](int h) {
+        const int t = t0 + threadIdx.x;
+        if (threadIdx.x < kC && t < rows) {
+            bn = beta[static_cast<int64_t>(t) * value_heads + h];
+            dn = decay[static_cast<int64_t>(t) * value_heads + h];
+        }
+    };
+    load_gates(src);
+
     // Lower-triangle 16x16 tiles (mt >= nt) of K K^T and Q K^T. Wave w loads
     // the K and Q rows of tokens 16w .. 16w+15 once (lane: token 16w + L%16,
     // dims 32(L/16) .. +31, the MFMA k-slot map of both operands) and puts its
@@ -151,11 +164,11 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
         float* gam = wsc + 2 * kC * kC;
         float* rr = gam + kC;
         __syncthreads();   // the products are done; the previous head's readers of sb, sd, A, T too
-        if (threadIdx.x < kC) {  // padding tokens: beta 0 (no update), decay 1
-            const int t = t0 + threadIdx.x;
-            sb[threadIdx.x] = t < rows ? beta[static_cast<int64_t>(t) * value_heads + h] : 0.0f;
-            sd[threadIdx.x] = t < rows ? decay[static_cast<int64_t>(t) * value_heads + h] : 1.0f;
+        if (threadIdx.x < kC) {
+            sb[threadIdx.x] = bn;
+            sd[threadIdx.x] = dn;
         }
+        if (h + key_heads < value_heads) load_gates(h + key_heads);
         __syncthreads();
 
         // Rows 16wv .. 16wv+15 per wave, lane i = column i: R[t][i] as a running
