@@ -942,7 +942,9 @@ def test_attn_stages(oracle, pos):
     (16, 2, 256, 1000, True), (16, 2, 256, 4095, True), (8, 2, 128, 200, True), (32, 2, 64, 77, False),
     (6, 2, 256, 50, True), (16, 2, 100, 45, True), (4, 1, 512, 20, True),
     (32, 2, 256, 15, True), (32, 2, 256, 16, False), (32, 2, 256, 2047, True), (16, 1, 256, 700, True),
-    (8, 1, 256, 63, True)])
+    (8, 1, 256, 63, True),
+    # more splits than one pass of the combine's workgroup takes (128): 282 and 257 splits
+    (16, 2, 256, 9000, True), (32, 2, 256, 4100, False)])
 def test_attn_decode(oracle, heads, kv, dim, pos, gated):
     """Fused decode at the Qwen3.5 attention shape across split boundaries (32 keys per
     split), groups of 4 and 16, and the staged fallback (group 3, dim 100, dim 512)."""
