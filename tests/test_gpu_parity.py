@@ -546,6 +546,21 @@ def test_gdn_recurrent_chunked(oracle, rows, gates):
     _check_gdn_recurrence(oracle, qkv, beta, decay, state, out, host(ds), kh, vh, dk, dv)
 
 
+@pytest.mark.parametrize("kh,vh", [(4, 4), (2, 6), (2, 3), (4, 2)])
+def test_gdn_recurrent_chunked_head_maps(oracle, kh, vh):
+    """Value head h reads key head h % key_heads (src/cuda/gdn.cu:108-151); the
+    chunked prep computes K K^T and Q K^T once per key head for every value head
+    that reads it: one, three, an uneven split (2 key heads, 3 value heads) and
+    more key heads than value heads, over a ragged second chunk."""
+    dk, dv, rows = 128, 32, 100
+    r = rng(kh * 16 + vh)
+    qkv, b, alpha, a, dt, state = _gdn_inputs(r, rows, kh, vh, dk, dv)
+    beta, decay = oracle.gdn_gate_values_rows(b, alpha, a, dt)
+    ds = dev(state)
+    out = host(ops.gdn_recurrent_chunked(ds, dev(qkv), dev(beta), dev(decay), kh, vh, dk, dv))
+    _check_gdn_recurrence(oracle, qkv, beta, decay, state, out, host(ds), kh, vh, dk, dv)
+
+
 def test_gdn_recurrent_chunked_long_and_fallback(oracle):
     """2048 tokens (32 chunks): the chunked form and the token-loop kernel both
     against the oracle's token loop (condition-scale bar: late outputs of strongly
