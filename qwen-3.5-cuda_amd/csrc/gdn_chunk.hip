@@ -324,8 +324,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int nchunks = (rows + kC - 1) / kC;
     const int tok = 16 * wv + n;   // token row of this lane's A operands
     const int tres = 16 * wv + 4 * g;   // first of the 4 token rows of this lane's results
-    float kA[32], qA[32], vv[4], gm[4], glast;
-    float4 tpr[4], bmr[4], rq[4];
+    float kA[32], qA[32], vv[4], gm[4], glast, gm_n[4], glast_n;
+    float4 tpr[4], bmr[4], rq[4], rq_n[4];
     auto chunk_base = [&](int c) { return ws + (static_cast<size_t>(c) * value_heads + h) * kWsFloats; };
     // Padding tokens of the last chunk read the last real row and are not
     // zeroed: the prep kernel gives them beta 0 and decay 1, so their rows and
@@ -360,18 +360,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
             vv[r] = v[static_cast<int64_t>(t) * qkv_stride + static_cast<size_t>(h) * value_dim + j0 + n];
         }
     };
-    auto load_gam = [&](int c) {
+    auto load_gam = [&](int c, float (&g4)[4], float& gl) {
         const float4 gv = ld4(chunk_base(c) + 2 * kC * kC + tres);
-        gm[0] = gv.x;
-        gm[1] = gv.y;
-        gm[2] = gv.z;
-        gm[3] = gv.w;
+        g4[0] = gv.x;
+        g4[1] = gv.y;
+        g4[2] = gv.z;
+        g4[3] = gv.w;
         // gamma_{C-1} through a vector load: its address is wave-uniform, and as
         // a scalar load it would share lgkmcnt with the LDS traffic, so every
         // LDS wait would also wait for it (scalar loads return out of order).
         // lane & (rows >> 31) is 0 (rows > 0) but not known to the compiler to
         // be uniform, which keeps the load on the vector path.
-        glast = chunk_base(c)[2 * kC * kC + kC - 1 + (lane & (rows >> 31))];
+        gl = chunk_base(c)[2 * kC * kC + kC - 1 + (lane & (rows >> 31))];
     };
     // elements 16s + 4g .. 16s + 4g + 3 (s < 4) of a 64-long row: p = row + 4g
     auto load_rows16 = [&](float4 (&dst)[4], const float* p) {
@@ -398,7 +398,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     load_v(0);
     load_rows16(tpr, tp_row(0));
     load_rows16(bmr, bm_row(0));
-    load_gam(0);
+    load_gam(0, gm, glast);
     load_rows16(rq, rr_row(0));
 
     for (int c = 0; c < nchunks; ++c) {
@@ -436,6 +436,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         }
         const v4f_t X = (xa[0] + xa[1]) + (xa[2] + xa[3]);
         const v4f_t Y = (ya[0] + ya[1]) + (ya[2] + ya[3]);
+        // gamma and R[C-1] of the next chunk a whole chunk ahead, into their
+        // own registers (requested at the end of the chunk they came back
+        // ~2000 cycles after the next chunk's Rv needed them)
+        load_gam(cn, gm_n, glast_n);
+        load_rows16(rq_n, rr_row(cn));
         load_kq(cn);
 
         // Result rows: tokens 16wv + 4g + r, column n.
@@ -498,8 +503,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
                             __builtin_fmaf(glast, sC[0].z, A0[2]), __builtin_fmaf(glast, sC[0].w, A0[3]));
         sn[1] = make_float4(__builtin_fmaf(glast, sC[1].x, A1[0]), __builtin_fmaf(glast, sC[1].y, A1[1]),
                             __builtin_fmaf(glast, sC[1].z, A1[2]), __builtin_fmaf(glast, sC[1].w, A1[3]));
-        load_gam(cn);      // gamma and R[C-1] are dead for this chunk from here on
-        load_rows16(rq, rr_row(cn));
+        // gamma and R[C-1] are dead for this chunk from here on
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            gm[r] = gm_n[r];
+            rq[r] = rq_n[r];
+        }
+        glast = glast_n;
         __syncthreads();  // every wave is done reading SlT, KsT, DlT of this chunk
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) *reinterpret_cast<float4*>(&SlT[n][32 * wv + 16 * mt + 4 * g]) = sn[mt];
