@@ -324,7 +324,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int nchunks = (rows + kC - 1) / kC;
     const int tok = 16 * wv + n;   // token row of this lane's A operands
     const int tres = 16 * wv + 4 * g;   // first of the 4 token rows of this lane's results
-    float kA[32], qA[32], vv[4], gm[4], glast, gm_n[4], glast_n;
+    float kA[32], qA[32], kB[32], qB[32], vv[4], gm[4], glast, gm_n[4], glast_n;
     float4 tpr[4], bmr[4], rq[4], rq_n[4];
     auto chunk_base = [&](int c) { return ws + (static_cast<size_t>(c) * value_heads + h) * kWsFloats; };
     // Padding tokens of the last chunk read the last real row and are not
@@ -336,22 +336,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     // k-slot map of every product here: step 4j + c of a 4-wide group g takes
     // element 16j + 4g + c of the contracted dimension (dims of K / Q, tokens
     // of T', Bm and R), so each 4 lanes of a row read 64 contiguous bytes.
-    auto load_kq = [&](int c) {
+    // K and Q rows of chunk c, dims 16j + 4g .. + 3 (one 16-byte load each)
+    auto load_kq_j = [&](int c, int j, float (&kd)[32], float (&qd)[32]) {
         const int t = min(c * kC + tok, rows - 1);
         const float* kr = k + static_cast<int64_t>(t) * qkv_stride + src * kDK + 4 * g;
         const float* qr = q + static_cast<int64_t>(t) * qkv_stride + src * kDK + 4 * g;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float4 a = ld4(kr + 16 * j), b = ld4(qr + 16 * j);
-            kA[4 * j] = a.x;
-            kA[4 * j + 1] = a.y;
-            kA[4 * j + 2] = a.z;
-            kA[4 * j + 3] = a.w;
-            qA[4 * j] = b.x;
-            qA[4 * j + 1] = b.y;
-            qA[4 * j + 2] = b.z;
-            qA[4 * j + 3] = b.w;
-        }
+        const float4 a = ld4(kr + 16 * j), b = ld4(qr + 16 * j);
+        kd[4 * j] = a.x;
+        kd[4 * j + 1] = a.y;
+        kd[4 * j + 2] = a.z;
+        kd[4 * j + 3] = a.w;
+        qd[4 * j] = b.x;
+        qd[4 * j + 1] = b.y;
+        qd[4 * j + 2] = b.z;
+        qd[4 * j + 3] = b.w;
     };
     auto load_v = [&](int c) {
 #pragma unroll
@@ -394,14 +392,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     auto bm_row = [&](int c) { return chunk_base(c) + kC * kC + (16 * wv + n) * kC + 4 * g; };
     auto rr_row = [&](int c) { return chunk_base(c) + 2 * kC * kC + kC + 4 * g; };
     // the loop's load order (the wait counts at its head then line up)
-    load_kq(0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) load_kq_j(0, j, kA, qA);
     load_v(0);
     load_rows16(tpr, tp_row(0));
     load_rows16(bmr, bm_row(0));
     load_gam(0, gm, glast);
     load_rows16(rq, rr_row(0));
 
-    for (int c = 0; c < nchunks; ++c) {
+    // Chunk c with its K and Q rows in kc / qc; chunk c + 1's are loaded into
+    // kn / qn during c's X and Y products (the loop runs two chunks per pass
+    // with the two register sets swapped, so nothing is copied).
+    auto chunk_step = [&](int c, float (&kc)[32], float (&qc)[32], float (&kn)[32], float (&qn)[32])
+                          __attribute__((always_inline)) {
         const int t0 = c * kC;
         // Inputs of chunk cn are prefetched during this chunk (the last chunk
         // reloads its own; unconditional loads keep the wait counts exact).
@@ -425,15 +428,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
         for (int j = 0; j < 8; ++j)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) KsT[16 * j + 4 * g + c][tok] = kA[4 * j + c];
+            for (int c = 0; c < 4; ++c) KsT[16 * j + 4 * g + c][tok] = kc[4 * j + c];
         v4f_t xa[4], ya[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) xa[u] = ya[u] = v4f_t{0.f, 0.f, 0.f, 0.f};
+        // The next chunk's 16 row loads go out between the products, two per 8
+        // MFMAs: issued in one burst they held the wave ~1000 cycles at a point
+        // where the chunk's chain waits on it.
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 32; ++s) {
-            xa[s & 3] = mfma4(kA[s], sB[s], xa[s & 3]);
-            ya[s & 3] = mfma4(qA[s], sB[s], ya[s & 3]);
+            if ((s & 3) == 0) load_kq_j(cn, s >> 2, kn, qn);
+            xa[s & 3] = mfma4(kc[s], sB[s], xa[s & 3]);
+            ya[s & 3] = mfma4(qc[s], sB[s], ya[s & 3]);
         }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);   // 2 VMEM reads
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);   // 8 MFMAs
+        }
+        __builtin_amdgcn_sched_barrier(0);
         const v4f_t X = (xa[0] + xa[1]) + (xa[2] + xa[3]);
         const v4f_t Y = (ya[0] + ya[1]) + (ya[2] + ya[3]);
         // gamma and R[C-1] of the next chunk a whole chunk ahead, into their
@@ -441,7 +455,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         // ~2000 cycles after the next chunk's Rv needed them)
         load_gam(cn, gm_n, glast_n);
         load_rows16(rq_n, rr_row(cn));
-        load_kq(cn);
 
         // Result rows: tokens 16wv + 4g + r, column n.
         *reinterpret_cast<float4*>(&RvT[n][tres]) =
@@ -514,6 +527,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) *reinterpret_cast<float4*>(&SlT[n][32 * wv + 16 * mt + 4 * g]) = sn[mt];
         __syncthreads();
+    };
+    for (int c = 0; c < nchunks; c += 2) {
+        chunk_step(c, kA, qA, kB, qB);
+        if (c + 1 < nchunks) chunk_step(c + 1, kB, qB, kA, qA);
     }
 
     for (int e = threadIdx.x; e < kDK * kNB; e += kThreads)
