@@ -289,7 +289,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     // The tiles a lane reads as MFMA operands along their K dimension are stored
     // transposed ([column][row]), so those operands are consecutive floats: one
     // 16-byte LDS read per 4 operands and one wait before the products.
-    __shared__ __align__(16) float KsT[kDK][kC + 4];  // the chunk's K^T, [key][token]
+    __shared__ __align__(16) float KsT[kDK][kC + 4];  // the chunk's R[C-1][t] k_t, [key][token]
     __shared__ __align__(16) float RvT[kNB][kC + 4];  // V - gamma X, [column][token]
     __shared__ __align__(16) float DlT[kNB][kC + 4];  // Delta, [column][token]
     __shared__ __align__(16) float SlT[kNB][kDK + 4]; // this block's 128 x 16 state, [column][key]
@@ -325,7 +325,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int tok = 16 * wv + n;   // token row of this lane's A operands
     const int tres = 16 * wv + 4 * g;   // first of the 4 token rows of this lane's results
     float kA[32], qA[32], kB[32], qB[32], vv[4], gm[4], glast, gm_n[4], glast_n;
-    float4 tpr[4], bmr[4], rq[4], rq_n[4];
+    float4 tpr[4], bmr[4];
+    float rt, rt_n;   // R[C-1][tok]: the K rows go to LDS already scaled by it
     auto chunk_base = [&](int c) { return ws + (static_cast<size_t>(c) * value_heads + h) * kWsFloats; };
     // Padding tokens of the last chunk read the last real row and are not
     // zeroed: the prep kernel gives them beta 0 and decay 1, so their rows and
@@ -387,10 +388,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
             dst[4 * s + 3] = t.w;
         }
     };
-    // T' and Bm rows 16wv + n and R[C-1], at this lane's k-slot columns.
+    // T' and Bm rows 16wv + n at this lane's k-slot columns; R[C-1] at token tok.
     auto tp_row = [&](int c) { return chunk_base(c) + (16 * wv + n) * kC + 4 * g; };
     auto bm_row = [&](int c) { return chunk_base(c) + kC * kC + (16 * wv + n) * kC + 4 * g; };
-    auto rr_row = [&](int c) { return chunk_base(c) + 2 * kC * kC + kC + 4 * g; };
+    auto rr_tok = [&](int c) { return chunk_base(c)[2 * kC * kC + kC + tok]; };
     // the loop's load order (the wait counts at its head then line up)
 #pragma unroll
     for (int j = 0; j < 8; ++j) load_kq_j(0, j, kA, qA);
@@ -398,7 +399,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     load_rows16(tpr, tp_row(0));
     load_rows16(bmr, bm_row(0));
     load_gam(0, gm, glast);
-    load_rows16(rq, rr_row(0));
+    rt = rr_tok(0);
 
     // Chunk c with its K and Q rows in kc / qc; chunk c + 1's are loaded into
     // kn / qn during c's X and Y products (the loop runs two chunks per pass
@@ -428,7 +429,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
         for (int j = 0; j < 8; ++j)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) KsT[16 * j + 4 * g + c][tok] = kc[4 * j + c];
+            for (int c = 0; c < 4; ++c) KsT[16 * j + 4 * g + c][tok] = kc[4 * j + c] * rt;
         v4f_t xa[4], ya[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) xa[u] = ya[u] = v4f_t{0.f, 0.f, 0.f, 0.f};
@@ -454,7 +455,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         // own registers (requested at the end of the chunk they came back
         // ~2000 cycles after the next chunk's Rv needed them)
         load_gam(cn, gm_n, glast_n);
-        load_rows16(rq_n, rr_row(cn));
+        rt_n = rr_tok(cn);
 
         // Result rows: tokens 16wv + 4g + r, column n.
         *reinterpret_cast<float4*>(&RvT[n][tres]) =
@@ -499,8 +500,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 
         // S rows 32wv + 16mt + (0..15): gamma_{C-1} S0 + sum_t R[C-1][t] k_t Delta_t
         // (step 4s + c: token 16s + 4g + c).
-        const float rk[16] = {rq[0].x, rq[0].y, rq[0].z, rq[0].w, rq[1].x, rq[1].y, rq[1].z, rq[1].w,
-                              rq[2].x, rq[2].y, rq[2].z, rq[2].w, rq[3].x, rq[3].y, rq[3].z, rq[3].w};
         v4f_t A0 = {0.f, 0.f, 0.f, 0.f}, A1 = A0;
         const int m0 = 32 * wv + n;
         float ka[16], kb[16];
@@ -508,8 +507,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         lds16(kb, &KsT[m0 + 16][4 * g]);
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
-            A0 = mfma4(rk[s] * ka[s], db[s], A0);
-            A1 = mfma4(rk[s] * kb[s], db[s], A1);
+            A0 = mfma4(ka[s], db[s], A0);   // KsT holds R[C-1][t] k_t (the same product)
+            A1 = mfma4(kb[s], db[s], A1);
         }
         float4 sn[2];
         sn[0] = make_float4(__builtin_fmaf(glast, sC[0].x, A0[0]), __builtin_fmaf(glast, sC[0].y, A0[1]),
@@ -520,9 +519,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             gm[r] = gm_n[r];
-            rq[r] = rq_n[r];
         }
         glast = glast_n;
+        rt = rt_n;
         __syncthreads();  // every wave is done reading SlT, KsT, DlT of this chunk
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) *reinterpret_cast<float4*>(&SlT[n][32 * wv + 16 * mt + 4 * g]) = sn[mt];
