@@ -70,8 +70,9 @@ __global__ __launch_bounds__(kBlock) void kv_store_kernel(const float* __restric
     }
 }
 
-// ---------------------------------------------------------------- drop-in stages
-// One wave per (head, key): dot over dim, lanes strided.
+// ---------------------------------------------------------------- drop-in stages (other shapes)
+// attn_scores outside the tiled form's shapes (scores_split): one wave per
+// (head, key), dot over dim, lanes strided.
 __global__ __launch_bounds__(kBlock) void scores_kernel(const float* __restrict__ q, const float* __restrict__ kc,
                                                         float* __restrict__ s, int heads, int kv_heads, int dim,
                                                         int n_keys, float scale) {
@@ -98,8 +99,9 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(v, __shfl_xor(v, 32));
 }
 
-// One block per head row of n scores.
-__global__ __launch_bounds__(kBlock) void softmax_kernel(float* __restrict__ s, int n) {
+// Softmax of one head row per workgroup for rows longer than the register
+// form takes (softmax_regs): three passes over the row in global memory.
+__global__ __launch_bounds__(kBlock) void softmax_loop(float* __restrict__ s, int n) {
     __shared__ float red[kBlock / kWave];
     float* r = s + static_cast<size_t>(blockIdx.x) * n;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -123,20 +125,6 @@ __global__ __launch_bounds__(kBlock) void softmax_kernel(float* __restrict__ s, 
     for (int i = threadIdx.x; i < n; i += kBlock) r[i] /= sum;
 }
 
-// out[h][j]: one thread per (head, column), keys in order.
-__global__ __launch_bounds__(kBlock) void values_kernel(const float* __restrict__ s, const float* __restrict__ vc,
-                                                        float* __restrict__ out, int heads, int kv_heads, int dim,
-                                                        int n_keys) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (i >= static_cast<int64_t>(heads) * dim) return;
-    const int h = static_cast<int>(i / dim), j = static_cast<int>(i - static_cast<int64_t>(h) * dim);
-    const int kv = h / (heads / kv_heads);
-    const float* sh = s + static_cast<size_t>(h) * n_keys;
-    float z = 0.f;
-    for (int t = 0; t < n_keys; ++t) z = __builtin_fmaf(sh[t], vc[(static_cast<size_t>(t) * kv_heads + kv) * dim + j], z);
-    out[i] = z;
-}
-
 // ---------------------------------------------------------------- fused decode
 // Workgroup (split, kv head): G query heads x L keys, G * L = 256 threads,
 // thread (head, key) for the softmax (32 keys per split for 8 heads per kv
@@ -151,6 +139,234 @@ __global__ __launch_bounds__(kBlock) void values_kernel(const float* __restrict_
 // h = kv G + head of the group), then m and l [H][splits].
 constexpr int kKeyStride = kMaxDim + 4;
 constexpr int kPairLanes = 1;
+
+// Scores of G query heads x L keys on the matrix cores
+// (v_mfma_f32_16x16x4_f32), from the queries and keys staged in LDS: 16 keys
+// x 16 heads tiles (for 8 query heads, columns 8..15 repeat them and are not
+// read), the head dim split in P parts over the NT / 64 waves; wave w takes
+// tile w % T, part w / T. In a 16x16x4 product lane l gives A[key l % 16][k =
+// l / 16] and B[k][head l % 16]; lane group g = l / 16 runs over dims part DP
+// + g DP/4 + j (j < DP/4), four at a time from one 16-byte LDS read of the key
+// row and of the query row. Partial tile `part` goes to sc[part]; the caller
+// waits at a barrier and adds the P parts in part order for (head, key).
+template <int G, int L, int NT>
+struct ScoreTiles {
+    static constexpr int T = L / 16, P = (NT / kWave) / T, DP = kMaxDim / P;
+    static_assert(T * 16 == L && P * T == NT / kWave && G <= 16 && DP % 16 == 0, "score tiles");
+    typedef float Part[T][16][17];
+
+    static __device__ __forceinline__ void run(const float4 (*q_lds)[kMaxDim / 4], const float (*k_lds)[kKeyStride],
+                                               Part* sc, int tid) {
+        typedef float v4f_t __attribute__((ext_vector_type(4)));
+        const int w = wave_in_block(), l = tid & (kWave - 1);
+        const int tile = w % T, part = w / T;
+        const int m = l & 15, g = l >> 4;
+        const float* krow = &k_lds[tile * 16 + m][part * DP + g * (DP / 4)];
+        const float4* qrow = &q_lds[m % G][(part * DP + g * (DP / 4)) / 4];
+        v4f_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+        for (int s = 0; s < DP / 16; ++s) {
+            const float4 ka = *reinterpret_cast<const float4*>(krow + 4 * s);
+            const float4 qb = qrow[s];
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.x, qb.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.y, qb.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.z, qb.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.w, qb.w, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[part][tile][4 * g + i][m] = acc[i];   // key 4g + i, head m
+    }
+
+    // q . k of (head hh, key tt) from the P partial tiles, in part order.
+    static __device__ __forceinline__ float dot(const Part* sc, int hh, int tt) {
+        float d = 0.f;
+#pragma unroll
+        for (int p = 0; p < P; ++p) d += sc[p][tt >> 4][tt & 15][hh];
+        return d;
+    }
+};
+
+// ---------------------------------------------------------------- drop-in stages
+// The reference's three launches keep their signatures and meaning (scores
+// [H][n] in HBM between them) with bodies shaped for the whole GPU.
+//
+// attn_scores: workgroup (split of L keys, kv head), thread (head, key): the G
+// query heads of the kv head and the split's key rows staged in LDS, the dot
+// products on the matrix cores (ScoreTiles, the tiles of the fused decode), so
+// every key row is read from HBM once per call (256 workgroups at 4096 keys).
+template <int G, int L>
+__global__ __launch_bounds__(G * L) void scores_split(const float* __restrict__ q, const float* __restrict__ kc,
+                                                      float* __restrict__ s, int kv_heads, int n_keys, float scale) {
+    constexpr int D = kMaxDim, D4 = D / 4, NT = G * L;
+    constexpr int QCH = G * D4 / NT, KCH = L * D4 / NT;
+    static_assert((G * D4) % NT == 0 && (L * D4) % NT == 0, "scores_split shape");
+    using Tiles = ScoreTiles<G, L, NT>;
+    __shared__ float4 q_lds[G][D4];
+    __shared__ __align__(16) float k_lds[L][kKeyStride];
+    __shared__ typename Tiles::Part sc_lds[Tiles::P];
+    const int split = blockIdx.x, kv = blockIdx.y, tid = threadIdx.x;
+    const int t0 = split * L;
+    const size_t row_stride = static_cast<size_t>(kv_heads) * D;
+    const float* kbase = kc + static_cast<size_t>(kv) * D;
+    float4 qr[QCH], kr[KCH];
+#pragma unroll
+    for (int i = 0; i < QCH; ++i) qr[i] = ld4(q + static_cast<size_t>(kv) * G * D + 4 * (tid + i * NT));
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {  // rows past the end clamped (their scores are not stored)
+        const int c = tid + i * NT;
+        kr[i] = ld4(kbase + static_cast<size_t>(min(t0 + c / D4, n_keys - 1)) * row_stride + 4 * (c % D4));
+    }
+#pragma unroll
+    for (int i = 0; i < QCH; ++i) {
+        const int c = tid + i * NT;
+        q_lds[c / D4][c % D4] = qr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+        const int c = tid + i * NT;
+        *reinterpret_cast<float4*>(&k_lds[c / D4][4 * (c % D4)]) = kr[i];
+    }
+    __syncthreads();
+    Tiles::run(q_lds, k_lds, sc_lds, tid);
+    __syncthreads();
+    const int hh = tid / L, tt = tid % L;
+    if (t0 + tt < n_keys)
+        s[(static_cast<size_t>(kv) * G + hh) * n_keys + t0 + tt] = Tiles::dot(sc_lds, hh, tt) * scale;
+}
+
+// attn_softmax: one workgroup of 1024 threads per head row, the row held in
+// registers (element tid + 1024 k in value k), so it is read once and written
+// once: row max (DPP within waves, then the 16 wave maxima in LDS), expf(s -
+// max), the sum (each thread over its values in order, then lanes, then waves
+// in wave order), then exp / sum as the reference divides.
+constexpr int kSoftmaxThreads = 1024;
+
+template <int VPT>
+__global__ __launch_bounds__(kSoftmaxThreads) void softmax_regs(float* __restrict__ s, int n) {
+    constexpr int NW = kSoftmaxThreads / kWave;
+    __shared__ float wmax[NW], wsum[NW];
+    float* r = s + static_cast<size_t>(blockIdx.x) * n;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), w = wave_in_block();
+    float v[VPT];
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int i = tid + k * kSoftmaxThreads;
+        v[k] = i < n ? r[i] : -INFINITY;
+    }
+    float m = v[0];
+#pragma unroll
+    for (int k = 1; k < VPT; ++k) m = fmaxf(m, v[k]);
+    m = wave_max(m);
+    if (lane == 0) wmax[w] = m;
+    __syncthreads();
+    m = wmax[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) m = fmaxf(m, wmax[i]);
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        v[k] = tid + k * kSoftmaxThreads < n ? expf(v[k] - m) : 0.f;
+        sum += v[k];
+    }
+    sum = group_sum<64>(sum);
+    if (lane == 0) wsum[w] = sum;
+    __syncthreads();
+    sum = wsum[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) sum += wsum[i];
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int i = tid + k * kSoftmaxThreads;
+        if (i < n) r[i] = v[k] / sum;
+    }
+}
+
+// attn_values: workgroup (query head, 16-column block), the keys split over
+// its threads and the partial sums added in a fixed order (lane swaps within a
+// wave, then the waves in wave order through LDS), so the result does not
+// depend on scheduling. VEC (head dim a multiple of 4, 16-byte aligned
+// cache): thread (key lane kq = tid / 4, column quad tid % 4) adds p[t] v[t]
+// for t = kq, kq + 64, ... (one 16-byte load of 64-byte key segments); else
+// thread (key lane tid / 16, column tid % 16) with scalar loads. Workgroups
+// are mapped so that the G query heads of a kv head and neighbouring column
+// blocks run on one XCD (workgroup b on XCD b % 8), whose L2 then serves the
+// value rows G times from one HBM read.
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void values_cols(const float* __restrict__ s, const float* __restrict__ vc,
+                                                      float* __restrict__ out, int heads, int kv_heads, int dim,
+                                                      int n_keys, int ncb) {
+    constexpr int NW = kBlock / kWave;
+    constexpr int KL = VEC ? kBlock / 4 : kBlock / 16;   // key lanes per workgroup
+    constexpr int CW = VEC ? 4 : 1;                       // columns per thread
+    __shared__ float part[NW][16];
+    const int nblk = gridDim.x, b = blockIdx.x;
+    const int idx = (nblk & 7) ? b : (b & 7) * (nblk >> 3) + (b >> 3);
+    const int G = heads / kv_heads;
+    const int g = idx % G, unit = idx / G;
+    const int cb = unit % ncb, kv = unit / ncb;
+    const int h = kv * G + g;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), w = wave_in_block();
+    const int kq = VEC ? tid >> 2 : tid >> 4;
+    const int cidx = VEC ? tid & 3 : tid & 15;
+    const int col = cb * 16 + CW * cidx;
+    const bool live = col < dim;
+    const float* sh = s + static_cast<size_t>(h) * n_keys;
+    const size_t stride = static_cast<size_t>(kv_heads) * dim;
+    const float* vp = vc + static_cast<size_t>(kv) * dim + (live ? col : 0);
+    float acc[CW];
+#pragma unroll
+    for (int c = 0; c < CW; ++c) acc[c] = 0.f;
+    auto load = [&](int t, float (&vv)[CW]) {
+        if constexpr (VEC) {
+            const float4 x = ld4(vp + static_cast<size_t>(t) * stride);
+            vv[0] = x.x, vv[1] = x.y, vv[2] = x.z, vv[3] = x.w;
+        } else {
+            vv[0] = vp[static_cast<size_t>(t) * stride];
+        }
+    };
+    if (live) {
+        constexpr int U = 4;   // keys in flight per thread
+        int t = kq;
+        for (; t + (U - 1) * KL < n_keys; t += U * KL) {
+            float p[U], vv[U][CW];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                p[u] = sh[t + u * KL];
+                load(t + u * KL, vv[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int c = 0; c < CW; ++c) acc[c] = __builtin_fmaf(p[u], vv[u][c], acc[c]);
+        }
+        for (; t < n_keys; t += KL) {
+            float vv[CW];
+            const float p = sh[t];
+            load(t, vv);
+#pragma unroll
+            for (int c = 0; c < CW; ++c) acc[c] = __builtin_fmaf(p, vv[c], acc[c]);
+        }
+    }
+    // key lanes of one column (lanes cidx + (kWave / KL_w) j) within the wave
+#pragma unroll
+    for (int o = VEC ? 4 : 16; o < kWave; o <<= 1)
+#pragma unroll
+        for (int c = 0; c < CW; ++c) acc[c] += __shfl_xor(acc[c], o);
+    if (lane < 16 / CW) {
+#pragma unroll
+        for (int c = 0; c < CW; ++c) part[w][CW * lane + c] = acc[c];
+    }
+    __syncthreads();
+    if (w == 0 && lane < 16 / CW && live) {
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            float z = part[0][CW * lane + c];
+#pragma unroll
+            for (int i = 1; i < NW; ++i) z += part[i][CW * lane + c];
+            out[static_cast<size_t>(h) * dim + col + c] = z;
+        }
+    }
+}
 
 // NR: the attention front end folded in (qwen_attn_decode_norm_rope): q and
 // the cache row of key pos = n_keys - 1 arrive unnormalised; each workgroup
@@ -183,7 +399,7 @@ __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
     __shared__ float4 q_lds[G][D4];
     __shared__ __align__(16) float k_lds[L][kKeyStride];
     __shared__ __align__(16) float p_lds[G][L];
-    __shared__ float sc_lds[(NT / kWave) / (L / 16)][L / 16][16][17];   // partial score tiles
+    __shared__ typename ScoreTiles<G, L, NT>::Part sc_lds[ScoreTiles<G, L, NT>::P];   // partial score tiles
     __shared__ float acc_lds[HALVES > 1 ? HALVES - 1 : 1][HALVES > 1 ? G : 1][HALVES > 1 ? D : 1];
     const int split = blockIdx.x, kv = blockIdx.y;
     const int tid = threadIdx.x;
@@ -251,45 +467,16 @@ __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
     }
     __syncthreads();
 
-    // scores on the matrix cores (v_mfma_f32_16x16x4_f32): 16 keys x 16 heads
-    // tiles (8 query heads: columns 8..15 repeat them and are not read), the
-    // head dim split in P parts over the waves; wave w takes tile w % T, part
-    // w / T. In a 16x16x4 product lane l gives A[key l % 16][k = l / 16] and
-    // B[k][head l % 16]; lane group g = l / 16 runs over dims part DP + g DP/4
-    // + j (j < DP/4), four at a time from one 16-byte LDS read of the key row
-    // and of the query row. The P partial tiles meet in LDS and are added in
-    // part order for thread (head hh, key tt). (Per-thread dot products over
+    // scores on the matrix cores (ScoreTiles). (Per-thread dot products over
     // LDS read 2 KB per thread, 512 KB per workgroup: 11.0 against 10.25 us
     // per decode at 4096 keys.)
     const int pair = tid / kPairLanes, r = tid % kPairLanes;
     const int hh = pair / L, tt = pair % L;
     const bool valid = t0 + tt < n_keys;
-    {
-        constexpr int T = L / 16, P = (NT / kWave) / T, DP = D / P;
-        static_assert(T * 16 == L && P * T == NT / kWave && G <= 16 && DP % 16 == 0, "score tiles");
-        typedef float v4f_t __attribute__((ext_vector_type(4)));
-        const int w = wave_in_block(), l = tid & (kWave - 1);
-        const int tile = w % T, part = w / T;
-        const int m = l & 15, g = l >> 4;
-        const float* krow = &k_lds[tile * 16 + m][part * DP + g * (DP / 4)];
-        const float4* qrow = &q_lds[m % G][(part * DP + g * (DP / 4)) / 4];
-        v4f_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-        for (int s = 0; s < DP / 16; ++s) {
-            const float4 ka = *reinterpret_cast<const float4*>(krow + 4 * s);
-            const float4 qb = qrow[s];
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.x, qb.x, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.y, qb.y, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.z, qb.z, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.w, qb.w, acc, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sc_lds[part][tile][4 * g + i][m] = acc[i];   // key 4g + i, head m
-        __syncthreads();
-    }
-    float dot = 0.f;
-#pragma unroll
-    for (int p = 0; p < (NT / kWave) / (L / 16); ++p) dot += sc_lds[p][tt >> 4][tt & 15][hh];
+    using Tiles = ScoreTiles<G, L, NT>;
+    Tiles::run(q_lds, k_lds, sc_lds, tid);
+    __syncthreads();
+    const float dot = Tiles::dot(sc_lds, hh, tt);
     const float sc = valid ? dot * scale : -INFINITY;
     // max and sum over the L keys of head hh: 4*L consecutive lanes
     constexpr int HL = L * kPairLanes;
@@ -539,10 +726,20 @@ int qwen_attn_scores(const float* q, const float* k_cache, float* scores, int he
                      void* stream) {
     QK_ATTN_SHAPE("attn_scores");
     QK_REQUIRE(q && k_cache && scores, "attn_scores: null pointer");
-    const int64_t waves = static_cast<int64_t>(heads) * (pos + 1);
-    scores_kernel<<<blocks_for(waves, kBlock / kWave), kBlock, 0, as_stream(stream)>>>(q, k_cache, scores, heads,
-                                                                                      kv_heads, dim, pos + 1,
-                                                                                      host_rsqrt(dim));
+    const int n_keys = pos + 1;
+    hipStream_t s = as_stream(stream);
+    if (fused_ok(heads, kv_heads, dim, n_keys) && aligned16(q) && aligned16(k_cache)) {
+        const int L = split_keys(heads / kv_heads);
+        const dim3 grid((n_keys + L - 1) / L, kv_heads);
+        if (heads / kv_heads == 8)
+            scores_split<8, 32><<<grid, 8 * 32, 0, s>>>(q, k_cache, scores, kv_heads, n_keys, host_rsqrt(dim));
+        else
+            scores_split<16, 16><<<grid, 16 * 16, 0, s>>>(q, k_cache, scores, kv_heads, n_keys, host_rsqrt(dim));
+        return check_launch("attn_scores");
+    }
+    const int64_t waves = static_cast<int64_t>(heads) * n_keys;
+    scores_kernel<<<blocks_for(waves, kBlock / kWave), kBlock, 0, s>>>(q, k_cache, scores, heads, kv_heads, dim,
+                                                                      n_keys, host_rsqrt(dim));
     return check_launch("attn_scores");
 }
 
@@ -550,7 +747,20 @@ int qwen_attn_softmax(float* scores, int heads, int valid_len, void* stream) {
     QK_REQUIRE(heads >= 0 && valid_len >= 0, "attn_softmax: negative size");
     if (heads == 0 || valid_len == 0) return ok();
     QK_REQUIRE(scores, "attn_softmax: null pointer");
-    softmax_kernel<<<heads, kBlock, 0, as_stream(stream)>>>(scores, valid_len);
+    hipStream_t s = as_stream(stream);
+    const int vpt = (valid_len + kSoftmaxThreads - 1) / kSoftmaxThreads;
+    if (vpt <= 1)
+        softmax_regs<1><<<heads, kSoftmaxThreads, 0, s>>>(scores, valid_len);
+    else if (vpt <= 2)
+        softmax_regs<2><<<heads, kSoftmaxThreads, 0, s>>>(scores, valid_len);
+    else if (vpt <= 4)
+        softmax_regs<4><<<heads, kSoftmaxThreads, 0, s>>>(scores, valid_len);
+    else if (vpt <= 8)
+        softmax_regs<8><<<heads, kSoftmaxThreads, 0, s>>>(scores, valid_len);
+    else if (vpt <= 16)
+        softmax_regs<16><<<heads, kSoftmaxThreads, 0, s>>>(scores, valid_len);
+    else
+        softmax_loop<<<heads, kBlock, 0, s>>>(scores, valid_len);
     return check_launch("attn_softmax");
 }
 
@@ -558,9 +768,16 @@ int qwen_attn_values(const float* scores, const float* v_cache, float* out, int 
                      void* stream) {
     QK_ATTN_SHAPE("attn_values");
     QK_REQUIRE(scores && v_cache && out, "attn_values: null pointer");
-    const int64_t n = static_cast<int64_t>(heads) * dim;
-    values_kernel<<<blocks_for(n, kBlock), kBlock, 0, as_stream(stream)>>>(scores, v_cache, out, heads, kv_heads, dim,
-                                                                           pos + 1);
+    const int ncb = (dim + 15) / 16;
+    const int64_t blocks = static_cast<int64_t>(heads) * ncb;
+    QK_REQUIRE(blocks <= INT32_MAX, "attn_values: %d heads x %d columns is too large", heads, dim);
+    hipStream_t s = as_stream(stream);
+    if (dim % 4 == 0 && aligned16(v_cache))
+        values_cols<true><<<static_cast<unsigned>(blocks), kBlock, 0, s>>>(scores, v_cache, out, heads, kv_heads, dim,
+                                                                           pos + 1, ncb);
+    else
+        values_cols<false><<<static_cast<unsigned>(blocks), kBlock, 0, s>>>(scores, v_cache, out, heads, kv_heads,
+                                                                            dim, pos + 1, ncb);
     return check_launch("attn_values");
 }
 

@@ -392,6 +392,8 @@ def attn_scores(q, k_cache, heads, kv_heads, dim, pos, out=None, stream=None):
     _attn_check(q, k_cache, heads, kv_heads, dim, pos)
     out = torch.empty(heads * (pos + 1), dtype=torch.float32, device=q.device) if out is None else out
     _dev(out, dtype=torch.float32)
+    if out.numel() < heads * (pos + 1):
+        raise ValueError("scores output too small for the shape")
     check(load().qwen_attn_scores(_p(q), _p(k_cache), _p(out), heads, kv_heads, dim, pos, _stream(stream)))
     return out
 
@@ -406,9 +408,12 @@ def attn_softmax(scores, heads, valid_len, stream=None):
 
 def attn_values(scores, v_cache, heads, kv_heads, dim, pos, out=None, stream=None):
     _dev(scores, v_cache, dtype=torch.float32)
-    _attn_check(scores, v_cache, heads, kv_heads, 1, pos)
+    if scores.numel() < heads * (pos + 1) or v_cache.numel() < (pos + 1) * kv_heads * dim:
+        raise ValueError("scores or cache too small for the shape")
     out = torch.empty(heads * dim, dtype=torch.float32, device=scores.device) if out is None else out
     _dev(out, dtype=torch.float32)
+    if out.numel() < heads * dim:
+        raise ValueError("values output too small for the shape")
     check(load().qwen_attn_values(_p(scores), _p(v_cache), _p(out), heads, kv_heads, dim, pos, _stream(stream)))
     return out
 

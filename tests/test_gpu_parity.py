@@ -931,18 +931,29 @@ def test_attn_split_qg_gate_and_kv_store(oracle):
             ops.attn_kv_store(dev(k), dev(v), kc, vc, bad, max_len)
 
 
-@pytest.mark.parametrize("pos", [0, 40, 1000])
-def test_attn_stages(oracle, pos):
-    """The reference's three launches: scores, softmax, values (16 query / 2 kv heads of 256)."""
-    heads, kv, dim = 16, 2, 256
-    q, K, V, _ = _attn_inputs(rng(pos + 1), heads, kv, dim, pos + 1)
+# 16 / 2 heads of 256 and 32 / 2: the tiled scores (32 and 16 keys per split),
+# the register softmax (1 to 16 values per thread) and the 16-byte values form;
+# 9001 keys: more than 8 values per softmax thread and a partial last split;
+# 20000: the softmax past the register form; head dims 128 and 100 (scores one
+# wave per head and key; values over 16-column blocks with dead column quads)
+# and 102 (values with scalar loads).
+@pytest.mark.parametrize("heads,kv,dim,pos", [
+    (16, 2, 256, 0), (16, 2, 256, 40), (16, 2, 256, 1000), (16, 2, 256, 4095), (16, 2, 256, 9000),
+    (32, 2, 256, 100), (32, 2, 256, 2047), (16, 1, 256, 517), (16, 2, 256, 19999),
+    (8, 2, 128, 200), (6, 2, 100, 50), (4, 1, 102, 20)])
+def test_attn_stages(oracle, heads, kv, dim, pos):
+    """The reference's three launches (src/layer_attn.cpp:103-105): scores, softmax and
+    values each against the oracle on the oracle's inputs, then the GPU chain of the
+    four calls (with the gate) against the oracle's decode."""
+    q, K, V, g = _attn_inputs(rng(pos + 1 + heads + dim), heads, kv, dim, pos + 1)
     dq, dK, dV = dev(q), dev(K), dev(V)
     s = ops.attn_scores(dq, dK, heads, kv, dim, pos)
     rs = oracle.attn_scores(q, K, heads, kv, dim, pos)
     # a score is a dot product: bound its error by sum |q_i k_i| / sqrt(D)
+    grp = heads // kv
     ks = np.abs(K.reshape(pos + 1, kv, dim).astype(np.float64))
-    sscale = np.stack([ks[:, h // 8] @ np.abs(q.reshape(heads, dim)[h]) for h in range(heads)]).reshape(-1) / 16.0
-    _assert_scaled(host(s), rs, sscale, "scores")
+    sscale = np.stack([ks[:, h // grp] @ np.abs(q.reshape(heads, dim)[h]) for h in range(heads)]).reshape(-1)
+    _assert_scaled(host(s), rs, sscale / np.sqrt(dim), "scores")
     # softmax of the oracle's scores on both sides: probabilities to 1e-5 relative
     p = ops.attn_softmax(dev(rs), heads, pos + 1)
     rp = oracle.attn_softmax(rs, heads, pos + 1)
@@ -950,6 +961,24 @@ def test_attn_stages(oracle, pos):
     out = ops.attn_values(dev(rp), dV, heads, kv, dim, pos)
     _assert_scaled(host(out), oracle.attn_values(rp, V, heads, kv, dim, pos),
                    _attn_scale(oracle, q, K, V, heads, kv, dim, pos), "values")
+    # the chain on the GPU, gated, against the oracle's sequence
+    s = ops.attn_scores(dq, dK, heads, kv, dim, pos)
+    ops.attn_softmax(s, heads, pos + 1)
+    o = ops.attn_values(s, dV, heads, kv, dim, pos)
+    o = ops.attn_sigmoid_gate(o, dev(g), out=o)
+    _assert_scaled(host(o), oracle.attn_decode(q, K, V, heads, kv, dim, pos, gate=g),
+                   _attn_scale(oracle, q, K, V, heads, kv, dim, pos, g), "chain")
+
+
+def test_attn_values_deterministic():
+    """The values sum runs in a fixed order: the same call twice gives the same bits."""
+    heads, kv, dim, pos = 16, 2, 256, 4095
+    _, _, V, _ = _attn_inputs(rng(77), heads, kv, dim, pos + 1)
+    p = rng(78).random(heads * (pos + 1)).astype(F32)
+    dp, dV = dev(p), dev(V)
+    a = host(ops.attn_values(dp, dV, heads, kv, dim, pos))
+    b = host(ops.attn_values(dp, dV, heads, kv, dim, pos))
+    assert_bits_equal(a, b)
 
 
 @pytest.mark.parametrize("heads,kv,dim,pos,gated", [
