@@ -34,6 +34,26 @@ __device__ __forceinline__ void stage_rows_weights(float4* wl, const float* __re
     __syncthreads();
 }
 
+// ss / n, the mean of the squares (src/cuda/ops.cu:56 divides). For n a power of
+// two the quotient equals ss * 2^-log2(n) bit for bit (division and
+// multiplication both round the same real number), one multiply instead of the
+// IEEE division sequence on the row's critical path.
+__device__ __forceinline__ float div_n(float ss, int n) {
+    if ((n & (n - 1)) == 0) return ss * __int_as_float((127 - __builtin_ctz(static_cast<unsigned>(n))) << 23);
+    return ss / static_cast<float>(n);
+}
+
+// Sum-of-squares order shared by every vector row form, so that a row gives the
+// same bits whether it is normalised alone or among many rows (the launch shape
+// depends on the row count): with the row in 16-byte chunks c = 0, 1, ... and
+// chunk c on lane c % 64, lane l adds its chunks in two sets, c / 64 even and
+// c / 64 odd, each in order; each set is summed over the 64 lanes by
+// group_sum<64>, and the odd set's total is added to the even set's. The
+// two-wave form (rmsnorm_rows_split) holds one set per wave.
+__device__ __forceinline__ float row_sumsq(float even, float odd) {
+    return group_sum<kWave>(even) + group_sum<kWave>(odd);
+}
+
 // ------------------------------------------------------------- fp32 rows
 // One wave per row; lane l holds float4 chunks l, l+64, ... (up to MAXC).
 // Lanes past the row end load a clamped in-row address and use zeros, so every
@@ -69,11 +89,16 @@ __global__ __launch_bounds__(STAGE ? kStageWaves * kWave : kWave) void rmsnorm_r
     // Chunks past the row end (clamped loads) are left out of the sum by a
     // select once every load is issued: overwriting a load's destination
     // registers in the load loop would make each load wait for the previous one.
-    float ss = 0.f;
+    float se = 0.f, so = 0.f;
 #pragma unroll
-    for (int c = 0; c < MAXC; ++c) ss += c * kWave + lane < n4 ? sumsq4(v[c]) : 0.f;
-    ss = group_sum<kWave>(ss);
-    const float r = rsqrtf(ss / static_cast<float>(n) + eps);
+    for (int c = 0; c < MAXC; ++c) {
+        const float q = c * kWave + lane < n4 ? sumsq4(v[c]) : 0.f;
+        if (c % 2 == 0)
+            se += q;
+        else
+            so += q;
+    }
+    const float r = rsqrtf(div_n(row_sumsq(se, so), n) + eps);
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
         const int i = c * kWave + lane;
@@ -99,7 +124,7 @@ __global__ __launch_bounds__(STAGE ? kStageWaves * kWave : kWave) void rmsnorm_r
 // order. Twice the waves in flight for the same bytes: at 36 x 2048 it measured
 // 2.16 us against 2.50 us with one wave per row (a plain copy of the same bytes
 // takes 1.87 us).
-constexpr int kSplitWaves = 2;
+constexpr int kSplitWaves = 2;   // the two chunk sets of row_sumsq
 constexpr int kSplitRows = 256;
 
 // FULL: n4 == MAXC * kSplitWaves * 64 (every chunk inside the row: no clamps or
@@ -133,10 +158,8 @@ __global__ __launch_bounds__(kSplitWaves * kWave) void rmsnorm_rows_split(
     ss = group_sum<kWave>(ss);
     if (lane == 0) part[wv] = ss;
     __syncthreads();
-    ss = part[0];
-#pragma unroll
-    for (int k = 1; k < kSplitWaves; ++k) ss += part[k];
-    const float r = rsqrtf(ss / static_cast<float>(n) + eps);
+    ss = part[0] + part[1];   // the set order of row_sumsq: wave 0 holds the even chunk set
+    const float r = rsqrtf(div_n(ss, n) + eps);
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
         float4 o;
@@ -178,7 +201,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_rows_any(const float* __restri
     float ss = 0.f;
     for (int i = threadIdx.x; i < n; i += kBlock) ss += x[base + i] * x[base + i];
     ss = block_sum(ss, lds);
-    const float r = rsqrtf(ss / static_cast<float>(n) + eps);
+    const float r = rsqrtf(div_n(ss, n) + eps);
     for (int i = threadIdx.x; i < n; i += kBlock) {
         float o = x[base + i] * r * w[i];
         if constexpr (GATED) o *= silu(gate[base + i]);
@@ -222,7 +245,7 @@ __global__ __launch_bounds__(STAGE ? kStageWaves * kWave : kWave) void residual_
         }
     }
     ss = group_sum<kWave>(ss);
-    const float r = rsqrtf(ss / static_cast<float>(n) + eps);
+    const float r = rsqrtf(div_n(ss, n) + eps);
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
         const int i = c * kWave + lane;
@@ -246,7 +269,7 @@ __global__ __launch_bounds__(kBlock) void residual_rmsnorm_f32_any(const float* 
         ss += s * s;
     }
     ss = block_sum(ss, lds);
-    const float r = rsqrtf(ss / static_cast<float>(n) + eps);
+    const float r = rsqrtf(div_n(ss, n) + eps);
     // Each thread re-reads only the elements it wrote itself.
     for (int i = threadIdx.x; i < n; i += kBlock) normed[base + i] = resid[base + i] * r * w[i];
 }
@@ -309,7 +332,7 @@ __global__ __launch_bounds__(STAGE ? kStageWaves * kWave : kWave) void residual_
         }
     }
     ss = group_sum<kWave>(ss);
-    const float r = rsqrtf(ss / static_cast<float>(n) + eps);
+    const float r = rsqrtf(div_n(ss, n) + eps);
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
         const int i = c * kWave + lane;
@@ -341,27 +364,32 @@ __global__ __launch_bounds__(kBlock) void residual_rmsnorm_bf16_any(const uint16
         ss += f * f;
     }
     ss = block_sum(ss, lds);
-    const float r = rsqrtf(ss / static_cast<float>(n) + eps);
+    const float r = rsqrtf(div_n(ss, n) + eps);
     for (int i = threadIdx.x; i < n; i += kBlock) normed[base + i] = to_bf16(from_bf16(resid[base + i]) * r * w[i]);
 }
 
 // ------------------------------------------------------------- elementwise
 __global__ __launch_bounds__(kBlock) void add_v4(const float* __restrict__ a, const float* __restrict__ b,
-                                                 float* __restrict__ out, int n4) {
-    for (int i = blockIdx.x * kBlock + threadIdx.x; i < n4; i += gridDim.x * kBlock) {
-        const float4 p = ld4(a + 4 * static_cast<size_t>(i));
-        const float4 q = ld4(b + 4 * static_cast<size_t>(i));
-        st4(out + 4 * static_cast<size_t>(i), make_float4(p.x + q.x, p.y + q.y, p.z + q.z, p.w + q.w));
+                                                 float* __restrict__ out, int64_t n4) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n4;
+         i += static_cast<int64_t>(gridDim.x) * kBlock) {
+        const float4 p = ld4(a + 4 * i);
+        const float4 q = ld4(b + 4 * i);
+        st4(out + 4 * i, make_float4(p.x + q.x, p.y + q.y, p.z + q.z, p.w + q.w));
     }
 }
 
 __global__ __launch_bounds__(kBlock) void add_any(const float* __restrict__ a, const float* __restrict__ b,
-                                                  float* __restrict__ out, int n) {
-    for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) out[i] = a[i] + b[i];
+                                                  float* __restrict__ out, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kBlock)
+        out[i] = a[i] + b[i];
 }
 
-__global__ __launch_bounds__(kBlock) void copy_row(const float* __restrict__ src, float* __restrict__ dst, int n) {
-    for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) dst[i] = src[i];
+__global__ __launch_bounds__(kBlock) void copy_row(const float* __restrict__ src, float* __restrict__ dst, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kBlock)
+        dst[i] = src[i];
 }
 
 // ------------------------------------------------------------- launchers

@@ -81,6 +81,33 @@ def test_rmsnorm_gated(oracle, rows, n):
     assert_f32_close(got, oracle.rmsnorm_gated_rows(x, g, w), what="gated")
 
 
+@pytest.mark.parametrize("n", [2048, 1000, 64, 8192])
+@pytest.mark.parametrize("gated", [False, True])
+def test_rmsnorm_rows_bits_independent_of_row_count(n, gated):
+    """A row normalised alone (the two-wave form below 256 rows) and among 300 or 1100
+    rows (one wave per row; weights staged in LDS from 1024 rows) gives the same bits:
+    every form adds the squares in one order."""
+    r = rng(n + gated)
+    x = r.standard_normal((1100, n)).astype(F32)
+    g = r.standard_normal((1100, n)).astype(F32)
+    w = (1 + 0.1 * r.standard_normal(n)).astype(F32)
+    dx, dg, dw = dev(x), dev(g), dev(w)
+
+    def run(rows):
+        if gated:
+            return host(ops.rmsnorm_gated_rows(dx[:rows].contiguous(), dg[:rows].contiguous(), dw))
+        return host(ops.rmsnorm_rows(dx[:rows].contiguous(), dw))
+    alone = np.concatenate([run(1)] + [host(ops.rmsnorm_gated_rows(dx[i:i + 1].contiguous(), dg[i:i + 1].contiguous(),
+                                                                    dw) if gated else
+                                            ops.rmsnorm_rows(dx[i:i + 1].contiguous(), dw)) for i in (1, 299, 1099)])
+    few, many, most = run(36), run(300), run(1100)
+    for got in (few[:2], many[:2], most[:2]):
+        assert_bits_equal(got, alone[:2], what=f"first rows, n {n}")
+    assert_bits_equal(many[299], alone[2], what="row 299")
+    assert_bits_equal(most[299], alone[2], what="row 299 of 1100")
+    assert_bits_equal(most[1099], alone[3], what="row 1099")
+
+
 @pytest.mark.parametrize("n", [2048, 1001, 1 << 20])
 def test_residual_add(oracle, n):
     r = rng(n)
