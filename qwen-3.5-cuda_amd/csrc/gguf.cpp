@@ -20,6 +20,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <cerrno>
 #include <cstdio>
 #include <cstring>
 #include <iostream>
@@ -60,9 +61,10 @@ public:
         return true;
     }
     void advise_sequential() const {
-        if (data_) madvise(const_cast<uint8_t*>(data_), size_, MADV_SEQUENTIAL);
+        if (fd_ >= 0) (void)posix_fadvise(fd_, 0, 0, POSIX_FADV_SEQUENTIAL);
     }
     const uint8_t* data() const { return data_; }
+    int fd() const { return fd_; }
     size_t size() const { return size_; }
 
 private:
@@ -136,22 +138,39 @@ std::vector<std::string> array_text(Cursor& c) {
 
 uint64_t round_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 
-// memcpy of n bytes split over up to `threads` host threads (the source is the
-// file mapping, so this is where the file is read).
-void parallel_copy(void* dst, const uint8_t* src, size_t n, unsigned threads) {
+// pread of n bytes at file offset `off` into dst, split over up to `threads`
+// host threads (this is where the tensor data is read from the file). Returns
+// false when the file ends before n bytes or a read fails: a file cut short
+// while it is being loaded ends in an error, as the reference's fin.read does
+// (src/loader_gguf.cpp:357-361), never in a read past the end of a mapping.
+bool parallel_read(int fd, void* dst, uint64_t off, size_t n, unsigned threads) {
+    auto read_all = [fd](uint8_t* d, uint64_t o, size_t len) {
+        while (len > 0) {
+            const ssize_t r = ::pread(fd, d, len, static_cast<off_t>(o));
+            if (r < 0 && errno == EINTR) continue;
+            if (r <= 0) return false;
+            d += r;
+            o += static_cast<uint64_t>(r);
+            len -= static_cast<size_t>(r);
+        }
+        return true;
+    };
     constexpr size_t kMinPerThread = size_t{4} << 20;
     const unsigned t = static_cast<unsigned>(std::max<size_t>(1, std::min<size_t>(threads, n / kMinPerThread)));
-    if (t <= 1) {
-        std::memcpy(dst, src, n);
-        return;
-    }
+    uint8_t* d = static_cast<uint8_t*>(dst);
+    if (t <= 1) return read_all(d, off, n);
     std::vector<std::thread> pool;
+    std::vector<char> good(t, 0);
     const size_t part = (n + t - 1) / t;
     for (unsigned i = 0; i < t; ++i) {
         const size_t b = i * part, e = std::min(n, b + part);
-        if (b < e) pool.emplace_back([=] { std::memcpy(static_cast<uint8_t*>(dst) + b, src + b, e - b); });
+        if (b < e)
+            pool.emplace_back([&, i, b, e] { good[i] = read_all(d + b, off + b, e - b); });
+        else
+            good[i] = 1;
     }
     for (auto& th : pool) th.join();
+    return std::all_of(good.begin(), good.end(), [](char g) { return g != 0; });
 }
 
 }  // namespace
@@ -322,9 +341,10 @@ bool GgufLoader::load_tensors_to_gpu(int base_layer_count, hipStream_t stream) {
     }
     std::sort(sel.begin(), sel.end(), [&](size_t a, size_t b) { return tensors_[a].offset < tensors_[b].offset; });
     // The file may have changed since open(): every selected tensor must still
-    // lie inside this mapping, or the copies would read past it (SIGBUS). The
-    // reference's read fails instead ("Error reading binary tensor data",
-    // src/loader_gguf.cpp:355-360); this check runs before any device call.
+    // lie inside it, checked here before any device call; the reference's read
+    // fails instead ("Error reading binary tensor data", src/loader_gguf.cpp:
+    // 355-360). The data itself is read with pread (parallel_read), so a file
+    // cut short after this check still ends in that error.
     const uint64_t avail = m.size() - payload_offset_;
     for (size_t i : sel) {
         const QuantTensor& t = tensors_[i];
@@ -359,6 +379,7 @@ bool GgufLoader::load_tensors_to_gpu(int base_layer_count, hipStream_t stream) {
     void* stage[2] = {nullptr, nullptr};
     hipEvent_t done[2] = {nullptr, nullptr};
     bool ok = true;
+    std::string short_read;   // tensor whose data the file no longer holds
     for (int b = 0; b < 2 && ok; ++b)
         ok = hipHostMalloc(&stage[b], kStageBytes, hipHostMallocDefault) == hipSuccess &&
              hipEventCreateWithFlags(&done[b], hipEventDisableTiming) == hipSuccess;
@@ -372,12 +393,16 @@ bool GgufLoader::load_tensors_to_gpu(int base_layer_count, hipStream_t stream) {
         bool in_flight[2] = {false, false};
         for (size_t k = 0; k < sel.size() && ok; ++k) {
             const QuantTensor& t = tensors_[sel[k]];
-            const uint8_t* src = m.data() + payload_offset_ + t.offset;
+            const uint64_t src = payload_offset_ + t.offset;
             uint64_t done_bytes = 0;
             while (done_bytes < t.size_bytes && ok) {
                 const size_t n = static_cast<size_t>(std::min<uint64_t>(t.size_bytes - done_bytes, kStageBytes - fill));
                 uint8_t* dst = static_cast<uint8_t*>(stage[b]) + fill;
-                parallel_copy(dst, src + done_bytes, n, threads);
+                if (!parallel_read(m.fd(), dst, src + done_bytes, n, threads)) {
+                    short_read = t.name;
+                    ok = false;
+                    break;
+                }
                 ok = hipMemcpyAsync(arena + slot[k] + done_bytes, dst, n, hipMemcpyHostToDevice, s) == hipSuccess;
                 fill += n;
                 done_bytes += n;
@@ -397,15 +422,30 @@ bool GgufLoader::load_tensors_to_gpu(int base_layer_count, hipStream_t stream) {
         const bool synced = hipStreamSynchronize(s) == hipSuccess;
         ok = ok && synced;
     } else {
-        // No pinned staging (pinned memory exhausted): synchronous copies
-        // straight from the mapped file, as the reference uploads.
+        // No pinned staging (pinned memory exhausted): reads into a pageable
+        // buffer and synchronous copies, as the reference uploads.
         (void)hipGetLastError();
-        ok = true;
+        std::vector<uint8_t> bounce;
+        try {
+            bounce.resize(kStageBytes);
+            ok = true;
+        } catch (const std::bad_alloc&) {
+            ok = false;
+        }
         uint8_t* arena = static_cast<uint8_t*>(arena_);
+        const unsigned threads = std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
         for (size_t k = 0; k < sel.size() && ok; ++k) {
             const QuantTensor& t = tensors_[sel[k]];
-            ok = hipMemcpy(arena + slot[k], m.data() + payload_offset_ + t.offset, t.size_bytes,
-                           hipMemcpyHostToDevice) == hipSuccess;
+            for (uint64_t done_bytes = 0; done_bytes < t.size_bytes && ok;) {
+                const size_t n = static_cast<size_t>(std::min<uint64_t>(t.size_bytes - done_bytes, kStageBytes));
+                if (!parallel_read(m.fd(), bounce.data(), payload_offset_ + t.offset + done_bytes, n, threads)) {
+                    short_read = t.name;
+                    ok = false;
+                    break;
+                }
+                ok = hipMemcpy(arena + slot[k] + done_bytes, bounce.data(), n, hipMemcpyHostToDevice) == hipSuccess;
+                done_bytes += n;
+            }
         }
     }
     for (int b = 0; b < 2; ++b) {
@@ -416,6 +456,10 @@ bool GgufLoader::load_tensors_to_gpu(int base_layer_count, hipStream_t stream) {
     if (!ok) {
         const hipError_t err = hipGetLastError();
         unload_gpu();
+        if (!short_read.empty())
+            return fail("cannot re-read GGUF file " + filepath_ + ": error reading binary tensor data for '" +
+                            short_read + "'",
+                        false);
         return fail(std::string("tensor upload failed: ") + hipGetErrorString(err), false);
     }
     for (size_t k = 0; k < sel.size(); ++k) tensors_[sel[k]].device_ptr = static_cast<uint8_t*>(arena_) + slot[k];
