@@ -23,6 +23,7 @@
 #include <algorithm>
 #include <cmath>
 #include <mutex>
+#include <type_traits>
 
 #include "attn_common.hpp"
 #include "capi_common.hpp"
@@ -382,9 +383,20 @@ struct NormRopeArgs {
     float eps;
 };
 
+// The key cache argument: read-only (and __restrict__) for the plain decode; a
+// plain float* for NR, whose kernel also writes the cache row of pos.
+template <bool NR>
+struct KeyCache {
+    typedef const float* __restrict__ type;
+};
+template <>
+struct KeyCache<true> {
+    typedef float* type;
+};
+
 template <int G, int L, bool NR = false>
 __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
-    const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
+    const float* __restrict__ q, typename KeyCache<NR>::type kc, const float* __restrict__ vc,
     float* __restrict__ ws_acc, float* __restrict__ ws_m, float* __restrict__ ws_l, int kv_heads, int n_keys,
     int splits, float scale, NormRopeArgs nr = NormRopeArgs{}, RopeDen den = RopeDen{}) {
     constexpr int D = kMaxDim;                 // this path: head dim 256
@@ -450,7 +462,8 @@ __global__ __launch_bounds__(G * L * kPairLanes) void decode_split(
             for (int i = 0; i < KCH; ++i) {
                 if (i == kk >> 2) {
                     kr[i] = norm_rope256<true>(kr[i], wk, rp, nr.eps, lane);
-                    st4(const_cast<float*>(kbase) + static_cast<size_t>(n_keys - 1) * row_stride + 4 * lane, kr[i]);
+                    st4(kc + static_cast<size_t>(kv) * D + static_cast<size_t>(n_keys - 1) * row_stride + 4 * lane,
+                        kr[i]);
                 }
             }
         }
@@ -796,7 +809,8 @@ namespace {
 // The split pass and the combine (fused_ok shapes, 16-byte aligned q and
 // cache); NR: the front end folded into the split pass.
 template <bool NR>
-int split_combine(const float* q, const float* k_cache, const float* v_cache, const float* gate, float* out,
+int split_combine(const float* q, std::conditional_t<NR, float*, const float*> k_cache, const float* v_cache,
+                  const float* gate, float* out,
                   int heads, int kv_heads, int dim, int pos, void* workspace, hipStream_t s,
                   const NormRopeArgs& nr = NormRopeArgs{}, const RopeDen& den = RopeDen{}) {
     const int n_keys = pos + 1;
