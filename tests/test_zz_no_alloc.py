@@ -77,3 +77,54 @@ def test_noalloc_decode_rejects_shapes_beyond_its_scratch():
     st = lib.qwen_attn_decode_noalloc(px, px, px, px, px, 64, 8, 256, 19999, P(torch.cuda.current_stream().cuda_stream))
     assert st == _lib.STATUS_INVALID_ARGUMENT
     assert b"scratch" in lib.qwen_last_error()
+
+
+_CAPTURE_CHILD = r"""
+import ctypes, sys
+import numpy as np, torch
+from qwen35_hip import _lib
+lib = _lib.load()
+P = ctypes.c_void_p
+torch.cuda.set_device(0)
+H, KV, D, pos = 16, 2, 256, 1000
+r = np.random.default_rng(11)
+q, K, V, g = (torch.from_numpy(a).cuda() for a in (
+    r.standard_normal(H * D).astype(np.float32), r.standard_normal((pos + 1, KV * D)).astype(np.float32),
+    r.standard_normal((pos + 1, KV * D)).astype(np.float32), r.standard_normal(H * D).astype(np.float32)))
+ptrs = [P(t.data_ptr()) for t in (q, K, V, g)]
+out = torch.zeros(H * D, device="cuda")
+ref = torch.zeros(H * D, device="cuda")
+need = lib.qwen_attn_decode_workspace_bytes(H, KV, D, pos)
+ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+torch.cuda.synchronize()
+s = torch.cuda.Stream()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph, stream=s):   # the first noalloc call of this process
+    rc = lib.qwen_attn_decode_noalloc(*ptrs, P(out.data_ptr()), H, KV, D, pos, P(s.cuda_stream))
+assert rc == 0, lib.qwen_last_error()
+cur = P(torch.cuda.current_stream().cuda_stream)
+assert lib.qwen_attn_decode(*ptrs, P(ref.data_ptr()), H, KV, D, pos, P(ws.data_ptr()), need, cur) == 0
+for i in range(3):
+    out.fill_(float(i))                    # eager work between the replays
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), f"replay {i}"
+print("noalloc capture ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """The scratch array's address is looked up at the first call on a device: that
+    first call may itself be under HIP graph capture (a fresh process captures it,
+    replays the graph three times with eager work between, and every replay equals
+    qwen_attn_decode with a workspace bit for bit)."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    pkg = Path(_lib.__file__).resolve().parents[1]
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join([str(pkg), os.environ.get("PYTHONPATH", "")]))
+    res = subprocess.run([sys.executable, "-c", _CAPTURE_CHILD], env=env, capture_output=True, text=True, timeout=110)
+    assert res.returncode == 0 and "noalloc capture ok" in res.stdout, res.stdout + res.stderr
