@@ -12,8 +12,8 @@ inputs resident in HBM:
   C4b GDN gated per-head RMSNorm, fp32 [4096 x 32 x 128]
   C5  Q4_K and Q6_K embedding dequant-gather, 8192 ids from 248320 x 2048
 
-Timed region (the contract): the step captured as one HIP graph (nine launches,
-no host work between them) replayed K times, bracketed by
+Timed region (the contract): the step captured as one HIP graph (eight launches:
+C3b and C3c run as one routed + shared SwiGLU launch; no host work between them) replayed K times, bracketed by
 torch.cuda.synchronize(); value = algorithmic bytes per step / wall time per step.
 One step touches ~830 MB, more than the 256 MB MALL, so every call reads its
 inputs from HBM and pays for writing its outputs back.
@@ -27,10 +27,12 @@ copy of the same byte count (the fastest of three launch shapes, COPY_FORMS) is
 reported beside each kernel as the box's practical ceiling. Algorithmic bytes count every input read once and every
 output written once. The roofline object reports the kernel with the largest
 time per step; its "traffic" comes from the committed rocprofv3 counter runs
-(profiles/traffic.json) when present.
+(profiles/traffic.json), and only while the kernel's source files have the
+digest recorded with those counts ("traffic_source" says which run and whether
+it applies; otherwise traffic is null).
 
-CPU baseline: the oracle (oracle/liboracle.so, a C++ restatement of the
-reference kernels) timed on this host on a bounded sample of each config.
+CPU baseline: the oracle (oracle/liboracle_fp32.so, a C++ restatement of the
+reference kernels) timed on this host's cores over the full configs.
 """
 
 from __future__ import annotations
@@ -1096,13 +1098,26 @@ def main() -> int:
     roofline = None
     if not args.no_per_kernel and kernels:
         dom = max(kernels, key=lambda k: k.us)
-        traffic = None
+        # HBM bytes per launch from the committed counter runs (FETCH_SIZE and
+        # WRITE_SIZE, calibrated on a copy): used only when the kernel's source
+        # files still have the digest recorded with the counts, else null.
+        from qwen35_hip.rocprof_summary import sources_digest
+        traffic, tsrc = None, {"file": "profiles/traffic.json"}
         tf = ROOT / "profiles" / "traffic.json"
         if tf.exists():
-            traffic = json.loads(tf.read_text()).get(dom.name, {}).get("bytes_per_launch")
+            tj = json.loads(tf.read_text())
+            rec = tj.get(dom.name, {})
+            tsrc["measured_at_commit"] = tj.get("_provenance", {}).get("commit")
+            tsrc["sources_sha256"] = rec.get("sources_sha256")
+            tsrc["current_sources_sha256"] = sources_digest(dom.name)
+            if rec.get("sources_sha256") and rec["sources_sha256"] == tsrc["current_sources_sha256"]:
+                traffic = rec.get("bytes_per_launch")
+            else:
+                tsrc["note"] = "counted on other kernel sources: traffic left null"
         roofline = {"kernel": dom.name, "bound": "hbm", "achieved": round(dom.bytes / dom.us / 1e3, 1),
                     "peak": PEAK_GBPS, "unit": "GB/s", "frac": round(dom.bytes / dom.us / 1e3 / PEAK_GBPS, 4),
-                    "traffic": traffic, "algorithmic_bytes": dom.bytes, "us_per_call": round(dom.us, 3),
+                    "traffic": traffic, "traffic_source": tsrc, "algorithmic_bytes": dom.bytes,
+                    "us_per_call": round(dom.us, 3),
                     "copy_same_bytes_gbps": round(dom.bytes / dom.copy_us / 1e3, 1),
                     "copy_1gib_gbps": round(big / copy_big / 1e3, 1)}
 

@@ -24,9 +24,11 @@ from __future__ import annotations
 
 import argparse
 import csv
+import hashlib
 import json
 import sys
 from collections import defaultdict
+from pathlib import Path
 
 # symbol substring -> bench.py kernel name (first match wins)
 NAMES = [
@@ -72,9 +74,11 @@ NAMES = [
     ("gdn_chunk_state", "gdn_recurrent chunked: state walk"),
     ("decode_split", "attn_decode split-K pass"),
     ("decode_combine", "attn_decode combine"),
-    ("scores_kernel", "attn_scores (staged)"),
-    ("softmax_kernel", "attn_softmax (staged)"),
-    ("values_kernel", "attn_values (staged)"),
+    ("scores_split", "attn_scores (drop-in, MFMA tiles)"),
+    ("scores_kernel", "attn_scores (drop-in, other shapes)"),
+    ("softmax_regs", "attn_softmax (drop-in, row in registers)"),
+    ("softmax_loop", "attn_softmax (drop-in, long rows)"),
+    ("values_cols", "attn_values (drop-in)"),
     ("topk_rows_kernel", "moe_topk_rows"),
     ("weighted_sum_v4", "moe_weighted_sum_rows"),
     ("gemm_prep_x", "matmul_rows prep (x to fp16 parts)"),
@@ -90,6 +94,34 @@ ALGORITHMIC = {
     # the LM-head GEMV (bench.py next rows: Q6_K 248320 x 2048, x and y fp32)
     "gemv Q6_K MFMA, 2-block k-slices (LM head)": 418179072,
 }
+
+
+# Source files (qwen-3.5-cuda_amd/csrc) each counted kernel is compiled from,
+# with the headers they include. The traffic summary records their digest, so a
+# counter figure is used (bench.py) only while the kernel source is the one it
+# was measured on.
+CSRC = Path(__file__).resolve().parents[1] / "csrc"
+_COMMON = ["capi_common.hpp", "device_common.hpp", "../../include/qwen35_hip.h"]
+KERNEL_SOURCES = {
+    "rmsnorm": ["norm.hip"], "residual_rmsnorm_bf16": ["norm.hip"], "qk_norm_rope": ["attn.hip", "attn_common.hpp"],
+    "swiglu_bf16": ["moe.hip"], "shared_swiglu_sigmoid_bf16": ["moe.hip"], "swiglu_routed_shared_bf16": ["moe.hip"],
+    "gdn_frontend": ["gdn.hip", "gdn_common.hpp"], "gdn_norm_gate": ["gdn.hip", "gdn_common.hpp"],
+    "dequant_gather_q4_k": ["dequant.hip", "ggml_common.hpp"], "dequant_gather_q6_k": ["dequant.hip", "ggml_common.hpp"],
+    "gemv Q6_K MFMA, 2-block k-slices (LM head)": ["gemv.hip", "ggml_common.hpp", "moe_common.hpp"],
+}
+
+
+def sources_digest(name: str) -> str | None:
+    """sha256 (16 hex digits) over the kernel's source files, or None for a kernel
+    without a source list."""
+    files = KERNEL_SOURCES.get(name)
+    if files is None:
+        return None
+    h = hashlib.sha256()
+    for f in sorted(files + _COMMON):
+        h.update(f.encode())
+        h.update((CSRC / f).read_bytes())
+    return h.hexdigest()[:16]
 
 
 def kernel_name(symbol: str) -> str | None:
@@ -167,7 +199,7 @@ def traffic(fetch_csv: str, write_csv: str, copy_bytes: int) -> dict:
         wb = write[name] * 1024.0 * w_scale
         out[name] = {"fetch_kib": fetch[name], "write_kib": write[name], "fetch_bytes": round(fb),
                      "write_bytes": round(wb), "bytes_per_launch": round(fb + wb), "algorithmic_bytes": alg,
-                     "traffic_over_algorithmic": round((fb + wb) / alg, 4)}
+                     "traffic_over_algorithmic": round((fb + wb) / alg, 4), "sources_sha256": sources_digest(name)}
     return out
 
 
