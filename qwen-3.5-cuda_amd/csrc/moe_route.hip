@@ -10,12 +10,15 @@
 // the stream, and launches k expert GEMV chains with host-side offsets and k
 // moe_add calls with host-side weights.
 //
-// Here top-k is one wave per token row (topk_row, moe_common.hpp). Routing
+// Here top-k runs on 32 lanes per token row, two rows per wave
+// (topk_rows_group, moe_common.hpp; one wave per row for rows past 256 logits
+// or k past 32). Routing
 // stays on the device: qwen_moe_expert_matmul (gemv.hip) reads the expert ids,
 // and qwen_moe_weighted_sum_rows reads the weights, so no host round trip is
 // needed.
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "capi_common.hpp"
 #include "device_common.hpp"
@@ -28,7 +31,7 @@ constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
 constexpr int kMaxExperts = 16 * kWave;  // logits per row held in VGPRs (16 per lane)
 
-template <int VPL>
+template <int VPL, int KC>
 __global__ __launch_bounds__(kBlock) void topk_rows_kernel(const float* __restrict__ x, int32_t* __restrict__ idx,
                                                            float* __restrict__ w, int rows, int n, int k) {
     const int row = blockIdx.x * kWaves + wave_in_block();
@@ -36,7 +39,7 @@ __global__ __launch_bounds__(kBlock) void topk_rows_kernel(const float* __restri
     const int lane = threadIdx.x & 63;
     int pick_i;
     float weight;
-    const bool ok = topk_row<VPL>(x + static_cast<size_t>(row) * n, n, k, pick_i, weight);
+    const bool ok = topk_row<VPL, KC>(x + static_cast<size_t>(row) * n, n, k, pick_i, weight);
     int32_t* ir = idx + static_cast<size_t>(row) * k;
     float* wr = w + static_cast<size_t>(row) * k;
     if (!ok) {   // a non-finite logit: idx[0] = -1, w[0] = NaN, the rest untouched
@@ -49,6 +52,36 @@ __global__ __launch_bounds__(kBlock) void topk_rows_kernel(const float* __restri
     if (lane < k) {
         ir[lane] = pick_i;
         wr[lane] = weight;
+    }
+}
+
+// R = 64 / G rows per wave (topk_rows_group): row R w + r in lane group r.
+// VEC: rows of exactly G x VPL logits, 16-byte aligned.
+template <int G, int VPL, int KC, bool VEC>
+__global__ __launch_bounds__(kBlock) void topk_group_kernel(const float* __restrict__ x, int32_t* __restrict__ idx,
+                                                            float* __restrict__ w, int rows, int n, int k) {
+    constexpr int R = kWave / G;
+    const int row0 = R * (blockIdx.x * kWaves + wave_in_block());
+    if (row0 >= rows) return;  // wave-uniform
+    const int lane = threadIdx.x & 63, grp = lane / G, gl = lane & (G - 1);
+    const int row = row0 + grp;   // a row past the end repeats the last row and writes nothing
+    int pick_i;
+    float weight;
+    const uint32_t ok = topk_rows_group<G, VPL, KC, VEC>(x + static_cast<size_t>(min(row, rows - 1)) * n, n, k,
+                                                         pick_i, weight);
+    if (row >= rows) return;
+    int32_t* ir = idx + static_cast<size_t>(row) * k;
+    float* wr = w + static_cast<size_t>(row) * k;
+    if (!((ok >> grp) & 1)) {   // a non-finite logit: idx[0] = -1, w[0] = NaN, the rest untouched
+        if (gl == 0) {
+            ir[0] = -1;
+            wr[0] = __builtin_nanf("");
+        }
+        return;
+    }
+    if (gl < k) {
+        ir[gl] = pick_i;
+        wr[gl] = weight;
     }
 }
 
@@ -108,18 +141,48 @@ int qwen_moe_topk_rows(const float* logits, int32_t* idx, float* weights, int ro
     if (rows == 0) return ok();
     QK_REQUIRE(logits && idx && weights, "moe_topk: null pointer");
     hipStream_t s = as_stream(stream);
+    // Rows of up to 256 logits and k <= 32: 32 lanes per row (two rows per wave),
+    // 16-byte loads when a row fills the 32 lanes exactly, the rounds unrolled
+    // for k = 8 (Qwen3.5's experts per token).
+    if (n <= 256 && k <= 32) {
+        const unsigned grid2 = blocks_for((rows + 1) / 2, kWaves);
+        const bool vec = aligned16(logits);
+        const auto group = [&](auto vpl_c) {
+            constexpr int V = decltype(vpl_c)::value;
+            if (vec && n == 32 * V && V % 4 == 0) {
+                if (k == 8)
+                    topk_group_kernel<32, V, 8, (V % 4 == 0)><<<grid2, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
+                else
+                    topk_group_kernel<32, V, 0, (V % 4 == 0)><<<grid2, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
+            } else {
+                if (k == 8)
+                    topk_group_kernel<32, V, 8, false><<<grid2, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
+                else
+                    topk_group_kernel<32, V, 0, false><<<grid2, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
+            }
+        };
+        if (n <= 32)
+            group(std::integral_constant<int, 1>{});
+        else if (n <= 64)
+            group(std::integral_constant<int, 2>{});
+        else if (n <= 128)
+            group(std::integral_constant<int, 4>{});
+        else
+            group(std::integral_constant<int, 8>{});
+        return check_launch("moe_topk");
+    }
     const unsigned grid = blocks_for(rows, kWaves);
     const int vpl = (n + kWave - 1) / kWave;
     if (vpl <= 1)
-        topk_rows_kernel<1><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
+        topk_rows_kernel<1, 0><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
     else if (vpl <= 2)
-        topk_rows_kernel<2><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
+        topk_rows_kernel<2, 0><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
     else if (vpl <= 4)
-        topk_rows_kernel<4><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
+        topk_rows_kernel<4, 0><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
     else if (vpl <= 8)
-        topk_rows_kernel<8><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
+        topk_rows_kernel<8, 0><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
     else
-        topk_rows_kernel<16><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
+        topk_rows_kernel<16, 0><<<grid, kBlock, 0, s>>>(logits, idx, weights, rows, n, k);
     return check_launch("moe_topk");
 }
 

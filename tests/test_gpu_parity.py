@@ -1102,6 +1102,13 @@ def test_moe_topk_rows_many_ties(oracle, n, k, offset):
     x = (np.round(r.standard_normal((rows, n)) * 2.0) / 4.0).astype(F32)
     x[0, :] = 1.0                     # every logit tied
     x[1, ::7] = 9.0                   # a tie of many at the top, spread over lanes
+    x[2, :] = -1.0                    # +0 and -0 compare equal (lower index first)
+    x[2, 5::11] = -0.0
+    x[2, 9::13] = 0.0
+    x[3, :] = -3.0                    # negative logits only, ties among them
+    x[3, ::5] = -2.5
+    x[4, :] = np.float32(-3.4028235e38)   # the extremes of the finite range
+    x[4, 3::9] = np.float32(3.4028235e38)
     buf = dev(np.concatenate([np.zeros(offset, F32), x.ravel()]))
     xin = buf[offset:].view(rows, n)
     ri, rw = oracle.moe_topk_rows(x, k)
