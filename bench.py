@@ -230,7 +230,7 @@ def build_next_rows(torch, ops, synth, host):
     add("gemv_out_q4_k", "Q4_K [2048 x 4096] x f32 [4096] (layer_gdn.cpp:112 output projection)", "Q4_K",
         torch.from_numpy(t).to(dev), 2048 * 4096, 2048, 4096, [0], 144, t)
     # A Q6_K projection at the qkv shape (Q4_K_M files hold some projections as
-    # Q6_K): the staged per-row kernel.
+    # Q6_K): the direct per-row kernel.
     t = synth.q6k_table(8192, 2048, seed_tensor=24)
     add("gemv_qkv_q6_k", "Q6_K [8192 x 2048] x f32 [2048] (a Q6_K projection at the qkv shape)", "Q6_K",
         torch.from_numpy(t).to(dev), 8192 * 2048, 8192, 2048, [0], 210, t)

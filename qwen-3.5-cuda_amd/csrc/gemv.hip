@@ -166,6 +166,37 @@ __device__ __forceinline__ float block_dot_q4k(uint4 hdr, uint4 q, const LaneX<k
     return (A0 * lo - B0 * lx.s[0]) + (A1 * hi - B1 * lx.s[1]);
 }
 
+// Contribution of one Q6_K block to lane j's partial dot product from the
+// lane's bytes of it: ql bytes 64 half + l0 .. + 7 (la0, la1: quarters 0 and 2
+// in the low and high nibbles) and 64 half + 32 + l0 .. + 7 (lb0, lb1:
+// quarters 1 and 3), qh bytes 128 + 32 half + l0 .. + 7 (h0, h1: 2 bits per
+// quarter), scale bytes 192 + 8 half .. + 7 (s0, s1) and the block scale d
+// (half = j / 4, l0 = 8 (j % 4)).
+__device__ __forceinline__ float q6k_lane_dot(uint32_t la0, uint32_t la1, uint32_t lb0, uint32_t lb1, uint32_t h0,
+                                              uint32_t h1, uint32_t s0, uint32_t s1, float d,
+                                              const LaneX<kQ6_K>& lx, int j) {
+    // scales[8*half + l0/16 + 2*qq]: bytes (l0/16) + {0, 2} of the first word
+    // (qq 0, 1) and of the second word (qq 2, 3).
+    const int ss = 8 * ((8 * (j & 3)) >> 4);
+    const int8_t sc[4] = {static_cast<int8_t>(s0 >> ss), static_cast<int8_t>(s0 >> (ss + 16)),
+                          static_cast<int8_t>(s1 >> ss), static_cast<int8_t>(s1 >> (ss + 16))};
+    const uint32_t L[4][2] = {{la0 & 0x0f0f0f0fu, la1 & 0x0f0f0f0fu},
+                              {lb0 & 0x0f0f0f0fu, lb1 & 0x0f0f0f0fu},
+                              {(la0 >> 4) & 0x0f0f0f0fu, (la1 >> 4) & 0x0f0f0f0fu},
+                              {(lb0 >> 4) & 0x0f0f0f0fu, (lb1 >> 4) & 0x0f0f0f0fu}};
+    float acc = 0.f;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+        const uint32_t q0 = L[qq][0] | (((h0 >> (2 * qq)) & 0x03030303u) << 4);
+        const uint32_t q1 = L[qq][1] | (((h1 >> (2 * qq)) & 0x03030303u) << 4);
+        float t = dot_u8x4(q0, lx.v[2 * qq], 0.f);
+        t = dot_u8x4(q1, lx.v[2 * qq + 1], t);
+        // sum((q - 32) * x) = sum(q * x) - 32 * sum(x)
+        acc = __builtin_fmaf(d * static_cast<float>(sc[qq]), t - lx.s[qq], acc);
+    }
+    return acc;
+}
+
 // Contribution of one block to the lane's partial dot product. `blk` points
 // at the block in LDS.
 template <int TYPE>
@@ -178,31 +209,10 @@ __device__ __forceinline__ float block_dot(const uint8_t* blk, const LaneX<TYPE>
         const uint8_t* qla = blk + 64 * half + l0;         // quarters 0 (low nibble), 2 (high)
         const uint8_t* qlb = qla + 32;                     // quarters 1, 3
         const uint8_t* qhp = blk + 128 + 32 * half + l0;   // 2 bits per quarter
-        const uint32_t la0 = lds_u32_a2(qla), la1 = lds_u32_a2(qla + 4);
-        const uint32_t lb0 = lds_u32_a2(qlb), lb1 = lds_u32_a2(qlb + 4);
-        const uint32_t h0 = lds_u32_a2(qhp), h1 = lds_u32_a2(qhp + 4);
-        // scales[8*half + l0/16 + 2*qq]: bytes (l0/16) + {0, 2} of the first
-        // word (qq 0, 1) and of the second word (qq 2, 3).
-        const uint32_t s0 = lds_u32_a2(blk + 192 + 8 * half), s1 = lds_u32_a2(blk + 196 + 8 * half);
-        const int ss = 8 * (l0 >> 4);
-        const float d = half_bits(*reinterpret_cast<const uint16_t*>(blk + 208));
-        const int8_t sc[4] = {static_cast<int8_t>(s0 >> ss), static_cast<int8_t>(s0 >> (ss + 16)),
-                              static_cast<int8_t>(s1 >> ss), static_cast<int8_t>(s1 >> (ss + 16))};
-        const uint32_t L[4][2] = {{la0 & 0x0f0f0f0fu, la1 & 0x0f0f0f0fu},
-                                  {lb0 & 0x0f0f0f0fu, lb1 & 0x0f0f0f0fu},
-                                  {(la0 >> 4) & 0x0f0f0f0fu, (la1 >> 4) & 0x0f0f0f0fu},
-                                  {(lb0 >> 4) & 0x0f0f0f0fu, (lb1 >> 4) & 0x0f0f0f0fu}};
-        float acc = 0.f;
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-            const uint32_t q0 = L[qq][0] | (((h0 >> (2 * qq)) & 0x03030303u) << 4);
-            const uint32_t q1 = L[qq][1] | (((h1 >> (2 * qq)) & 0x03030303u) << 4);
-            float t = dot_u8x4(q0, lx.v[2 * qq], 0.f);
-            t = dot_u8x4(q1, lx.v[2 * qq + 1], t);
-            // sum((q - 32) * x) = sum(q * x) - 32 * sum(x)
-            acc = __builtin_fmaf(d * static_cast<float>(sc[qq]), t - lx.s[qq], acc);
-        }
-        return acc;
+        return q6k_lane_dot(lds_u32_a2(qla), lds_u32_a2(qla + 4), lds_u32_a2(qlb), lds_u32_a2(qlb + 4),
+                            lds_u32_a2(qhp), lds_u32_a2(qhp + 4), lds_u32_a2(blk + 192 + 8 * half),
+                            lds_u32_a2(blk + 196 + 8 * half), half_bits(*reinterpret_cast<const uint16_t*>(blk + 208)),
+                            lx, j);
     }
 }
 
@@ -341,6 +351,99 @@ __device__ __forceinline__ void q4k_direct_slices(const uint8_t* const (&w)[MAT]
         for (int u = 0; u < R; ++u)
 #pragma unroll
             for (int h = 0; h < NS; ++h) acc[mt][u] += block_dot_q4k(hd[mt][u][h], qv[mt][u][h], lx[h], j);
+}
+
+// Q6_K direct form (rows of whole units, 8 | nb): the lane map of block_dot
+// (lane j of block L/8 takes ql bytes 64 half + l0 .. +7 and +32, qh bytes 128
+// + 32 half + l0 .. +7, scale bytes 192 + 8 half .. +7 and d) with every piece
+// loaded straight into VGPRs. A 210-byte block starts 2 (b mod 2) bytes past a
+// 4-byte boundary of its 16-byte-aligned unit, so each 8-byte piece lies at
+// byte 0 or 2 of the 4-byte-aligned 12 bytes around it: one 12-byte load
+// (dwordx3, dword alignment) and two v_alignbyte per piece. The 12 bytes stay
+// inside the unit (the last piece, block 7's scales, ends the window at the
+// unit's byte 1680). x is staged once per workgroup as in q4k_direct_slices.
+struct __attribute__((aligned(4))) Q6Piece {
+    uint32_t x, y, z;
+};
+// 8 bytes at byte offset sb (0 or 2) of the 12 bytes w.
+__device__ __forceinline__ uint2 q6_piece(Q6Piece w, uint32_t sb) {
+    return make_uint2(__builtin_amdgcn_alignbyte(w.y, w.x, sb), __builtin_amdgcn_alignbyte(w.z, w.y, sb));
+}
+
+// NS (1 or 2) consecutive slices s, s+1 of R rows from g0 (row = min(g0 + u,
+// groups - 1)), added to acc[u] in slice order; every thread of the workgroup
+// calls it (one barrier).
+template <int R, int NS, int NWV = kGemvWaves>
+__device__ __forceinline__ void q6k_direct_slices(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                  float4* xs, float (&acc)[R], int nb, uint64_t ub0, int g0,
+                                                  int groups, int s, int b, int j) {
+    constexpr int BB = KQuant<kQ6_K>::kBlockBytes;
+    constexpr int NX = NS * 512;
+    constexpr int NTH = NWV * kWave;
+    constexpr int PER = NX / NTH;
+    static_assert(PER * NTH == NX, "x staging");
+    const int half = j >> 2, l0 = 8 * (j & 3);
+    const uint32_t sb = 2 * (b & 1);
+    float4 xt[PER];
+    const float* xsl = x + static_cast<size_t>(s) * 2048;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) xt[i] = ld4(xsl + 4 * (threadIdx.x + i * NTH));
+    __builtin_amdgcn_sched_barrier(0);   // the x loads first
+    Q6Piece pc[R][NS][4];
+    uint32_t dh[R][NS];
+    // The lane's byte offsets inside a unit (the same in every unit): the four
+    // 12-byte windows and d. The unit's address is wave-uniform, so each load is
+    // a scalar base plus a 32-bit lane offset.
+    const uint32_t blk = b * BB;
+    const uint32_t lo[4] = {blk + 64 * half + l0 - sb, blk + 64 * half + 32 + l0 - sb,
+                            blk + 128 + 32 * half + l0 - sb, blk + 192 + 8 * half - sb};
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const int g = min(g0 + u, groups - 1);
+#pragma unroll
+        for (int h = 0; h < NS; ++h) {
+            // Every unit read lies inside the tensor: rows are clamped to groups - 1
+            // and every entry point checks element_offset + M K (or the expert
+            // stride) against num_elements on the host.
+            const uint8_t* unit = w + (ub0 + static_cast<uint64_t>(g) * nb + 8 * (s + h)) * BB;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) pc[u][h][q] = *reinterpret_cast<const Q6Piece*>(unit + lo[q]);
+            dh[u][h] = *reinterpret_cast<const uint16_t*>(unit + blk + 208);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);   // every load issued before the staging
+#pragma unroll
+    for (int i = 0; i < PER; ++i) xs[threadIdx.x + i * NTH] = xt[i];
+    __syncthreads();
+    LaneX<kQ6_K> lx[NS];
+#pragma unroll
+    for (int h = 0; h < NS; ++h) {
+        // load_lane_x<kQ6_K>'s elements, from the staged copy
+        const float4* bx = xs + (h * 2048 + b * 256 + 128 * half + l0) / 4;
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+            lx[h].v[2 * qq] = bx[8 * qq];
+            lx[h].v[2 * qq + 1] = bx[8 * qq + 1];
+        }
+    }
+    // every LDS read issued before the first use (one wait, not one per pair)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int h = 0; h < NS; ++h) {
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+            const float4 a = lx[h].v[2 * qq], c = lx[h].v[2 * qq + 1];
+            lx[h].s[qq] = 32.0f * (((a.x + a.y) + (a.z + a.w)) + ((c.x + c.y) + (c.z + c.w)));
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < R; ++u)
+#pragma unroll
+        for (int h = 0; h < NS; ++h) {
+            const uint2 la = q6_piece(pc[u][h][0], sb), lb = q6_piece(pc[u][h][1], sb);
+            const uint2 qh = q6_piece(pc[u][h][2], sb), sc = q6_piece(pc[u][h][3], sb);
+            acc[u] += q6k_lane_dot(la.x, la.y, lb.x, lb.y, qh.x, qh.y, sc.x, sc.y, half_bits(dh[u][h]), lx[h], j);
+        }
 }
 
 // Fast path. Row groups: when 8 | nb, group = one row and unit (row, slice s)
@@ -482,6 +585,56 @@ __device__ __forceinline__ void q4k_direct_body(const uint8_t* __restrict__ w, c
         if (lane == u) out = t;
     }
     if (lane < R && g0 + lane < M) y[out_index(g0 + lane, M, split)] = out;
+}
+
+// The Q6_K direct form of gemv_kquant_body (rows of whole units): same row
+// groups, expert selection, lane map, lane arithmetic (q6k_lane_dot) and
+// summation order as the LDS-staged form, so the same bits.
+template <int R, int NS>
+__device__ __forceinline__ void q6k_direct_body(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                float* __restrict__ y, int M, int nb, uint64_t ub0, int groups,
+                                                const Experts& ex, int sel, int split = 0, int bx = -1) {
+    const int lane = threadIdx.x & 63;
+    const int wv = wave_in_block();
+    const int g0 = ((bx < 0 ? static_cast<int>(blockIdx.x) : bx) * kGemvWaves + wv) * R;
+    const int b = lane >> 3, j = lane & 7;
+    const int S = nb >> 3;
+    uint64_t eoff = 0;
+    int64_t x_off, y_off;
+    const bool ok_e = select_expert(ex, sel, M, x_off, y_off, eoff);
+    x += x_off;
+    y += y_off;
+    if (!ok_e) {   // uniform per workgroup: no barrier is reached
+        if (lane < R && g0 + lane < M) y[g0 + lane] = __builtin_nanf("");
+        return;
+    }
+    ub0 += eoff / 256;
+    __shared__ float4 xs[NS * 512];
+    float acc[R];
+#pragma unroll
+    for (int u = 0; u < R; ++u) acc[u] = 0.f;
+    q6k_direct_slices<R, NS>(w, x, xs, acc, nb, ub0, g0, groups, 0, b, j);
+    for (int s = NS; s < S; s += NS) {
+        __syncthreads();   // every wave is done with the previous slices' x
+        q6k_direct_slices<R, NS>(w, x, xs, acc, nb, ub0, g0, groups, s, b, j);
+    }
+    float out = 0.f;
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const float t = group_sum<64>(acc[u]);
+        if (lane == u) out = t;
+    }
+    if (lane < R && g0 + lane < M) y[out_index(g0 + lane, M, split)] = out;
+}
+
+// EX: expert selection (ex.idx set); else a plain GEMV, whose kernel has the
+// selection folded away (no scalar loads or branches before the first weight
+// load: 3.1 against 2.9 us at 512 x 2048).
+template <int R, int NS, bool EX>
+__global__ __launch_bounds__(kGemvBlock) void gemv_q6k_direct(const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ x, float* __restrict__ y,
+                                                              int M, int nb, uint64_t ub0, int groups, Experts ex) {
+    q6k_direct_body<R, NS>(w, x, y, M, nb, ub0, groups, EX ? ex : Experts{nullptr, 0, 0, 0}, EX ? blockIdx.y : 0);
 }
 
 template <int R, int NS>
@@ -751,6 +904,17 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_q4k_direct_multi(const float*
     const GemvMat& m = mu.d[j];
     q4k_direct_body<R, NS>(m.w, x, m.y, m.M, nb, m.ub0, m.groups, m.tensor_bytes, Experts{nullptr, 0, 0, 0}, 0,
                            m.split, NormGateX{}, b - mu.start[j]);
+}
+
+template <int R, int NS>
+__global__ __launch_bounds__(kGemvBlock) void gemv_q6k_direct_multi(const float* __restrict__ x, int nb,
+                                                                    GemvMulti mu, int n) {
+    const int b = static_cast<int>(blockIdx.x);
+    int j = 0;
+    while (j + 1 < n && mu.start[j + 1] <= b) ++j;   // uniform per workgroup
+    const GemvMat& m = mu.d[j];
+    q6k_direct_body<R, NS>(m.w, x, m.y, m.M, nb, m.ub0, m.groups, Experts{nullptr, 0, 0, 0}, 0, m.split,
+                           b - mu.start[j]);
 }
 
 // ------------------------------------------------------------ MoE down + combine
@@ -1429,6 +1593,23 @@ void launch_kquant(const uint8_t* w, const float* x, float* y, int M, int nb, ui
             gemv_q4k_direct<R, 1><<<grid, kGemvBlock, 0, s>>>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex);
         return;
     }
+    if (TYPE == kQ6_K && nb >= 8) {
+        if constexpr (R <= 2) {
+            const bool two = (nb / 8) % 2 == 0;
+            if (ex.idx) {
+                if (two)
+                    gemv_q6k_direct<R, 2, true><<<grid, kGemvBlock, 0, s>>>(w, x, y, M, nb, ub0, groups, ex);
+                else
+                    gemv_q6k_direct<R, 1, true><<<grid, kGemvBlock, 0, s>>>(w, x, y, M, nb, ub0, groups, ex);
+            } else {
+                if (two)
+                    gemv_q6k_direct<R, 2, false><<<grid, kGemvBlock, 0, s>>>(w, x, y, M, nb, ub0, groups, ex);
+                else
+                    gemv_q6k_direct<R, 1, false><<<grid, kGemvBlock, 0, s>>>(w, x, y, M, nb, ub0, groups, ex);
+            }
+            return;
+        }
+    }
     const size_t lds = static_cast<size_t>(kGemvWaves) * R * CPU * 16;
     gemv_kquant<TYPE, R><<<grid, kGemvBlock, lds, s>>>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex);
 }
@@ -1443,6 +1624,13 @@ void dispatch_kquant(const uint8_t* w, const float* x, float* y, int M, int nb, 
     // against 4.3 with 1 row per wave).
     const int64_t all = static_cast<int64_t>(groups) * n_sel;
     const bool multi_unit = TYPE == kQ4_K && nb >= 16;
+    if (TYPE == kQ6_K && nb >= 8) {   // the direct form: 2 rows per wave from 8192 rows (measured at 8192 x 2048)
+        if (all >= 2 * 4096)
+            launch_kquant<TYPE, 2>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, n_sel, s);
+        else
+            launch_kquant<TYPE, 1>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, n_sel, s);
+        return;
+    }
     if (all >= 4 * 4096)
         launch_kquant<TYPE, 4>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, n_sel, s);
     else if (all >= 2 * 4096 || (multi_unit && all * (nb / 8) >= 4096))
@@ -1520,6 +1708,20 @@ void launch_multi_r(const GemvMulti& mu, int n, const float* x, int nb, hipStrea
             gemv_q4k_direct_multi<R, 1><<<mf.start[n], kGemvBlock, 0, s>>>(x, nb, mf, n);
         return;
     }
+    if (TYPE == kQ6_K && nb >= 8) {
+        if constexpr (R <= 2) {
+            GemvMulti mf = mu;
+            mf.start[0] = 0;
+            for (int j = 0; j < n; ++j)
+                mf.start[j + 1] =
+                    mf.start[j] + static_cast<int>(blocks_for((mu.d[j].groups + R - 1) / R, kGemvWaves));
+            if ((nb / 8) % 2 == 0)
+                gemv_q6k_direct_multi<R, 2><<<mf.start[n], kGemvBlock, 0, s>>>(x, nb, mf, n);
+            else
+                gemv_q6k_direct_multi<R, 1><<<mf.start[n], kGemvBlock, 0, s>>>(x, nb, mf, n);
+            return;
+        }
+    }
     const size_t lds = static_cast<size_t>(kGemvWaves) * R * CPU * 16;
     gemv_kquant_multi<TYPE, R><<<grid, kGemvBlock, lds, s>>>(x, nb, mu);
 }
@@ -1529,6 +1731,8 @@ template <int TYPE>
 void launch_multi(const GemvMulti& mu, int n, const float* x, int nb, hipStream_t s) {
     int64_t all = 0;   // units per wave as dispatch_kquant picks them, over all matrices
     for (int j = 0; j < n; ++j) all += mu.d[j].groups;
+    if (TYPE == kQ6_K && nb >= 8)   // the direct form: at most 2 rows per wave
+        all = std::min<int64_t>(all, 4 * 4096 - 1);
     if (all >= 4 * 4096)
         launch_multi_r<TYPE, 4>(mu, n, x, nb, s);
     else if (all >= 2 * 4096)

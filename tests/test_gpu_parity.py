@@ -1354,6 +1354,10 @@ GEMV_CASES = [
     ("Q6_K", 16400, 2048, 16397, 0), ("Q6_K", 16420, 4096, 16401, 16), ("Q6_K", 20000, 512, 19999, 0),
     ("Q6_K", 16500, 768, 16500, 0), ("Q4_K", 65600, 2048, 65543, 40), ("Q4_K", 65600, 1024, 65600, 0),
     ("Q4_K", 65536, 3072, 65536, 0),
+    # Q6_K direct form (rows of whole units): 2 rows per wave from 8192 rows, both slices of a
+    # K = 4096 row at once with a row offset, three slices one at a time, a ragged last wave
+    ("Q6_K", 8192, 2048, 8192, 0), ("Q6_K", 1100, 4096, 1000, 77), ("Q6_K", 301, 6144, 299, 1),
+    ("Q6_K", 9001, 2048, 8999, 2),
 ]
 
 
