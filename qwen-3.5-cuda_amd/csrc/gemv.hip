@@ -276,7 +276,7 @@ struct NormGateX {
 template <int R, int NS, int MAT = 1, int LPH = 0, int NWV = kGemvWaves>
 __device__ __forceinline__ void q4k_direct_slices(const uint8_t* const (&w)[MAT], const float* __restrict__ x,
                                                   float4* xs, float (&acc)[MAT][R], int nb, uint64_t ub0, int g0,
-                                                  int groups, uint64_t tensor_bytes, int s, int b, int j,
+                                                  int groups, int s, int b, int j,
                                                   const NormGateX& ng = NormGateX{}) {
     constexpr int BB = KQuant<kQ4_K>::kBlockBytes;
     constexpr int NX = NS * 512;                    // float4 of x in the NS slices
@@ -293,6 +293,13 @@ __device__ __forceinline__ void q4k_direct_slices(const uint8_t* const (&w)[MAT]
     }
     __builtin_amdgcn_sched_barrier(0);   // the x loads first
     uint4 hd[MAT][R][NS], qv[MAT][R][NS];
+    // Lane offsets inside a unit (block b's header, its qs bytes 16j..16j+15),
+    // the same in every unit; the unit's address is wave-uniform. Every unit
+    // read lies inside the tensor: rows are clamped to groups - 1 and every
+    // entry point checks the shape (element_offset + M K, or the expert stride)
+    // against the tensor on the host. (A per-lane range check here held
+    // 64-bit addresses for every row in VGPRs.)
+    const uint32_t ho = b * BB, qo = b * BB + 16 + 16 * j;
 #pragma unroll
     for (int mt = 0; mt < MAT; ++mt)
 #pragma unroll
@@ -300,12 +307,9 @@ __device__ __forceinline__ void q4k_direct_slices(const uint8_t* const (&w)[MAT]
             const int g = min(g0 + u, groups - 1);
 #pragma unroll
             for (int h = 0; h < NS; ++h) {
-                const uint64_t bh = (ub0 + static_cast<uint64_t>(g) * nb + 8 * (s + h) + b) * BB;
-                // In range whenever the caller validated the shape; a block past
-                // the tensor would read block 0 instead of faulting.
-                const uint64_t bs = bh + BB <= tensor_bytes ? bh : 0;
-                hd[mt][u][h] = ld16_nt(w[mt] + bs);
-                qv[mt][u][h] = ld16_nt(w[mt] + bs + 16 + 16 * j);
+                const uint8_t* unit = w[mt] + (ub0 + static_cast<uint64_t>(g) * nb + 8 * (s + h)) * BB;
+                hd[mt][u][h] = ld16_nt(unit + ho);
+                qv[mt][u][h] = ld16_nt(unit + qo);
             }
         }
     __builtin_amdgcn_sched_barrier(0);   // every load issued before the staging
@@ -574,9 +578,11 @@ __device__ __forceinline__ void q4k_direct_body(const uint8_t* __restrict__ w, c
 #pragma unroll
     for (int u = 0; u < R; ++u) acc[0][u] = 0.f;
     const uint8_t* const wm[1] = {w};
-    for (int s = 0; s < S; s += NS) {
-        if (s > 0) __syncthreads();   // every wave is done with the previous slices' x
-        q4k_direct_slices<R, NS, 1, LPH, NWV>(wm, x, xs, acc, nb, ub0, g0, groups, tensor_bytes, s, b, j, ng);
+    (void)tensor_bytes;
+    q4k_direct_slices<R, NS, 1, LPH, NWV>(wm, x, xs, acc, nb, ub0, g0, groups, 0, b, j, ng);
+    for (int s = NS; s < S; s += NS) {
+        __syncthreads();   // every wave is done with the previous slices' x
+        q4k_direct_slices<R, NS, 1, LPH, NWV>(wm, x, xs, acc, nb, ub0, g0, groups, s, b, j, ng);
     }
     float out = 0.f;
 #pragma unroll
@@ -637,12 +643,15 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_q6k_direct(const uint8_t* __r
     q6k_direct_body<R, NS>(w, x, y, M, nb, ub0, groups, EX ? ex : Experts{nullptr, 0, 0, 0}, EX ? blockIdx.y : 0);
 }
 
-template <int R, int NS>
+// EX: expert selection (ex.idx set); else a plain GEMV with the selection
+// folded away (no scalar loads or branches before the first weight load).
+template <int R, int NS, bool EX>
 __global__ __launch_bounds__(kGemvBlock) void gemv_q4k_direct(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x, float* __restrict__ y,
                                                               int M, int nb, uint64_t ub0, int groups,
                                                               uint64_t tensor_bytes, Experts ex) {
-    q4k_direct_body<R, NS>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex, blockIdx.y);
+    q4k_direct_body<R, NS>(w, x, y, M, nb, ub0, groups, tensor_bytes, EX ? ex : Experts{nullptr, 0, 0, 0},
+                           EX ? blockIdx.y : 0);
 }
 
 // The gated per-head RMSNorm of x (core, heads of 4 LPH) followed by the GEMV
@@ -852,9 +861,10 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_q4k_direct_swiglu(const float
 #pragma unroll
     for (int u = 0; u < R; ++u) acc[0][u] = acc[1][u] = 0.f;
     const uint8_t* const wm[2] = {jb.wg, jb.wu};
-    for (int s = 0; s < S; s += NS) {
-        if (s > 0) __syncthreads();   // every wave is done with the previous slices' x
-        q4k_direct_slices<R, NS, 2>(wm, x, xs, acc, nb, ub, g0, jb.M, ~uint64_t{0}, s, b, j);
+    q4k_direct_slices<R, NS, 2>(wm, x, xs, acc, nb, ub, g0, jb.M, 0, b, j);
+    for (int s = NS; s < S; s += NS) {
+        __syncthreads();   // every wave is done with the previous slices' x
+        q4k_direct_slices<R, NS, 2>(wm, x, xs, acc, nb, ub, g0, jb.M, s, b, j);
     }
     float out = 0.f;
 #pragma unroll
@@ -1587,10 +1597,20 @@ void launch_kquant(const uint8_t* w, const float* x, float* y, int M, int nb, ui
     const int waves = (groups + R - 1) / R;
     const dim3 grid(blocks_for(waves, kGemvWaves), n_sel);
     if (TYPE == kQ4_K && nb >= 8) {   // rows of whole units: the direct form
-        if ((nb / 8) % 2 == 0)
-            gemv_q4k_direct<R, 2><<<grid, kGemvBlock, 0, s>>>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex);
-        else
-            gemv_q4k_direct<R, 1><<<grid, kGemvBlock, 0, s>>>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex);
+        const bool two = (nb / 8) % 2 == 0;
+        if (ex.idx) {
+            if (two)
+                gemv_q4k_direct<R, 2, true><<<grid, kGemvBlock, 0, s>>>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex);
+            else
+                gemv_q4k_direct<R, 1, true><<<grid, kGemvBlock, 0, s>>>(w, x, y, M, nb, ub0, groups, tensor_bytes, ex);
+        } else {
+            if (two)
+                gemv_q4k_direct<R, 2, false><<<grid, kGemvBlock, 0, s>>>(w, x, y, M, nb, ub0, groups, tensor_bytes,
+                                                                         ex);
+            else
+                gemv_q4k_direct<R, 1, false><<<grid, kGemvBlock, 0, s>>>(w, x, y, M, nb, ub0, groups, tensor_bytes,
+                                                                         ex);
+        }
         return;
     }
     if (TYPE == kQ6_K && nb >= 8) {
