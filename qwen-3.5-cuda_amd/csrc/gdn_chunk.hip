@@ -40,7 +40,9 @@ namespace {
 constexpr int kC = 64;                        // tokens per chunk
 constexpr int kDK = 128;                      // key dim of the chunked path
 constexpr int kNB = 16;                       // state columns per workgroup (kernel B)
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;                 // prep
+constexpr int kWalkThreads = 512;             // state walk: two waves per SIMD
+constexpr int64_t kMaxWalkStride = 0x7fffffff / (4 * 64);   // floats; 64 rows of 4-byte elements below 2^31 bytes
 constexpr int kXcds = 8;                      // gfx950: 8 XCDs, workgroups dealt round-robin
 constexpr int kLdA = kC + 4;                  // LDS row stride of the C x C matrices (16-byte rows)
 constexpr size_t kWsFloats = 2 * kC * kC + 2 * kC;   // per (chunk, head): T', Bm, gamma, R[C-1][.]
@@ -279,20 +281,61 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
     }
 }
 
-// One workgroup per CU (51 KB of LDS): one wave per SIMD, so the scheduler may
-// keep every operand load of a chunk in flight.
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gdn_chunk_state(float* __restrict__ S, const float* __restrict__ q,
-                                                            const float* __restrict__ k, const float* __restrict__ v,
-                                                            const float* __restrict__ ws, float* __restrict__ out,
-                                                            int rows, int key_heads, int value_heads, int value_dim,
-                                                            int64_t qkv_stride, int64_t out_stride) {
+// ---------------------------------------------------------------- state walk
+// Raw buffer access for the walk: a wave-uniform descriptor (base, byte range)
+// and a loop-invariant 32-bit lane offset, so a load costs no address
+// arithmetic on the vector ALU. Every VALU instruction issued while the
+// SIMD's matrix pipe runs the other wave's MFMAs waits for a pipe slot
+// (~one 16x16x4 f32 MFMA, measured), and per-load 64-bit address arithmetic
+// was most of the walk's VALU work. Loads at or past the range return 0 and
+// stores there are dropped: the padding tokens of a partial last chunk read
+// zeros (finite; their beta 0 and decay 1 give them zero rows and columns of
+// T' and zero rows of Bm, so they add nothing) and their outputs are not written.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const float* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+// The 16-byte load is reinterpreted whole: taking its result apart element by
+// element compiled to a 4-byte load on this compiler.
+__device__ __forceinline__ float4 buf_ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float buf_ld1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ void buf_st1(float x, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, x), r, off, 0, 0);
+}
+
+// Per-chunk inputs a lane holds, loaded one chunk ahead (two sets, swapped by
+// the loop's two chunk steps, so nothing is copied).
+struct ChunkIn {
+    float rows[32];   // K rows (K waves) or Q rows (Q waves): dims 16j + 4g + c of token 16w + n
+    float gm[4];      // gamma at the lane's 4 result tokens
+    float glast;      // gamma_{C-1}
+    float4 rt4;       // R[C-1][t] at the lane's 4 result tokens
+    float o[4];       // this chunk's outputs (Q waves), stored during the next chunk
+};
+
+// One workgroup per (value head, 16 state columns), 8 waves, two per SIMD:
+// wave w < 4 (K wave) computes X = K S0 for tokens 16w..16w+15, V - gamma X,
+// Delta and state rows 32w..32w+31; wave w + 4 (Q wave, the same SIMD) computes
+// Y = Q S0 for the same tokens and O. Each SIMD so runs two instruction streams
+// whose stalls the other fills. The role branches hold no loads that the other
+// role's code reads, and every path back to the loop head issues both chunks'
+// loads, which keeps the compiler's memory-wait counts tight (a branch that
+// skipped the second chunk, or one register set loaded at different points by
+// the two roles, turned them into full drains).
+__global__ __launch_bounds__(kWalkThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_chunk_state(
+    float* __restrict__ S, const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ ws, float* __restrict__ out, int rows, int key_heads, int value_heads, int value_dim,
+    int64_t qkv_stride, int64_t out_stride) {
     // The tiles a lane reads as MFMA operands along their K dimension are stored
-    // transposed ([column][row]), so those operands are consecutive floats: one
-    // 16-byte LDS read per 4 operands and one wait before the products.
-    __shared__ __align__(16) float KsT[kDK][kC + 4];  // the chunk's R[C-1][t] k_t, [key][token]
-    __shared__ __align__(16) float RvT[kNB][kC + 4];  // V - gamma X, [column][token]
-    __shared__ __align__(16) float DlT[kNB][kC + 4];  // Delta, [column][token]
-    __shared__ __align__(16) float SlT[kNB][kDK + 4]; // this block's 128 x 16 state, [column][key]
+    // transposed ([column][row]), so those operands are consecutive floats.
+    __shared__ __align__(16) float KsT[kDK][kC + 4];      // the chunk's k_t, [key][token]
+    __shared__ __align__(16) float RvT[kNB][kC + 4];      // V - gamma X, [column][token]
+    __shared__ __align__(16) float DlT[kNB][kC + 4];      // Delta, [column][token]
+    __shared__ __align__(16) float DsT[kNB][kC + 4];      // R[C-1][t] Delta_t, [column][token]
+    __shared__ __align__(16) float SlT[2][kNB][kDK + 4];  // the 128 x 16 state block, [column][key], by chunk parity
     // Workgroup i runs on XCD i % 8 (round-robin dispatch). With the value
     // heads a multiple of 8, head h's column blocks all get ids i with
     // i % 8 == h % 8, so the chunk data of a head (K, Q, T', Bm, V) is fetched
@@ -310,74 +353,86 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int j0 = cb * kNB;
     const int src = h % key_heads;
     const int lane = threadIdx.x & 63;
-    const int wv = wave_in_block();
+    const int wid = wave_in_block();
+    const int wv = wid & 3;          // token tile (and SIMD)
+    const bool qw = wid >= 4;        // Q wave
     const int g = lane >> 4, n = lane & 15;
     float* Sg = S + static_cast<size_t>(h) * kDK * value_dim + j0;
 
-    for (int e = threadIdx.x; e < kDK * kNB; e += kThreads)
-        SlT[e % kNB][e / kNB] = Sg[static_cast<size_t>(e / kNB) * value_dim + e % kNB];
+    for (int e = threadIdx.x; e < kDK * kNB; e += kWalkThreads)
+        SlT[0][e % kNB][e / kNB] = Sg[static_cast<size_t>(e / kNB) * value_dim + e % kNB];
     __syncthreads();
 
-    // Per-chunk inputs of this lane, each reloaded for the next chunk as soon as
-    // it is dead in the current one (the state-free loads overlap the chain of
-    // MFMAs that the state forces).
     const int nchunks = (rows + kC - 1) / kC;
-    const int tok = 16 * wv + n;   // token row of this lane's A operands
+    const int tok = 16 * wv + n;     // token row of this lane's A operands
     const int tres = 16 * wv + 4 * g;   // first of the 4 token rows of this lane's results
-    float kA[32], qA[32], kB[32], qB[32], vv[4], gm[4], glast, gm_n[4], glast_n;
-    float4 tpr[4], bmr[4];
-    float rt, rt_n;   // R[C-1][tok]: the K rows go to LDS already scaled by it
-    auto chunk_base = [&](int c) { return ws + (static_cast<size_t>(c) * value_heads + h) * kWsFloats; };
-    // Padding tokens of the last chunk read the last real row and are not
-    // zeroed: the prep kernel gives them beta 0 and decay 1, so their rows and
-    // columns of T' are zero, their Delta is exactly 0 (0 times finite values)
-    // and they add nothing to the state; their outputs are not stored. Keeping
-    // the loaded values raw also keeps the prefetches asynchronous (a select on
-    // a loaded value would wait for the load right away).
-    // k-slot map of every product here: step 4j + c of a 4-wide group g takes
-    // element 16j + 4g + c of the contracted dimension (dims of K / Q, tokens
-    // of T', Bm and R), so each 4 lanes of a row read 64 contiguous bytes.
-    // K and Q rows of chunk c, dims 16j + 4g .. + 3 (one 16-byte load each)
-    auto load_kq_j = [&](int c, int j, float (&kd)[32], float (&qd)[32]) {
-        const int t = min(c * kC + tok, rows - 1);
-        const float* kr = k + static_cast<int64_t>(t) * qkv_stride + src * kDK + 4 * g;
-        const float* qr = q + static_cast<int64_t>(t) * qkv_stride + src * kDK + 4 * g;
-        const float4 a = ld4(kr + 16 * j), b = ld4(qr + 16 * j);
-        kd[4 * j] = a.x;
-        kd[4 * j + 1] = a.y;
-        kd[4 * j + 2] = a.z;
-        kd[4 * j + 3] = a.w;
-        qd[4 * j] = b.x;
-        qd[4 * j + 1] = b.y;
-        qd[4 * j + 2] = b.z;
-        qd[4 * j + 3] = b.w;
-    };
-    auto load_v = [&](int c) {
+    const uint32_t stride4 = static_cast<uint32_t>(qkv_stride) * 4u;
+    const uint32_t ostride4 = static_cast<uint32_t>(out_stride) * 4u;
+    // Loop-invariant lane byte offsets. k-slot map of every product: step
+    // 4j + c of a 4-wide lane group g takes element 16j + 4g + c of the
+    // contracted dimension, so the 4 lanes of a row read 64 contiguous bytes.
+    const uint32_t ro = static_cast<uint32_t>(tok) * stride4 + 16u * g;
+    uint32_t vo[4], oo[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = min(c * kC + tres + r, rows - 1);
-            vv[r] = v[static_cast<int64_t>(t) * qkv_stride + static_cast<size_t>(h) * value_dim + j0 + n];
+    for (int r = 0; r < 4; ++r) {
+        vo[r] = static_cast<uint32_t>(tres + r) * stride4 + 4u * n;
+        oo[r] = static_cast<uint32_t>(tres + r) * ostride4 + 4u * n;
+    }
+    // T' (K waves) or Bm (Q waves) rows 16wv + n at this lane's k-slot columns
+    const uint32_t mo = static_cast<uint32_t>((qw ? kC * kC : 0) + (16 * wv + n) * kC + 4 * g) * 4u;
+    const uint32_t go = static_cast<uint32_t>(2 * kC * kC + tres) * 4u;
+    const uint32_t rto = static_cast<uint32_t>(2 * kC * kC + kC + tres) * 4u;
+    // gamma_{C-1}: one address for the wave, through a vector load (a scalar
+    // load shares lgkmcnt with the LDS traffic). lane & (rows >> 31) is 0
+    // (rows > 0) but not known to the compiler to be uniform.
+    const uint32_t glo = static_cast<uint32_t>(2 * kC * kC + kC - 1 + (lane & (rows >> 31))) * 4u;
+    const float* const rsrc = (qw ? q : k) + src * kDK;
+    const float* const vsrc = v + static_cast<size_t>(h) * value_dim + j0;
+    float* const osrc = out + static_cast<size_t>(h) * value_dim + j0;
+    // chunk c's token rows (fewer in a partial last chunk) and workspace block
+    auto rows_rsrc = [&](const float* base, int c, int64_t stride, uint32_t s4) {
+        return buf_rsrc(base + static_cast<int64_t>(c) * kC * stride, static_cast<uint32_t>(min(rows - c * kC, kC)) * s4);
+    };
+    auto ws_rsrc = [&](int c) {
+        return buf_rsrc(ws + (static_cast<size_t>(c) * value_heads + h) * kWsFloats, static_cast<uint32_t>(kWsFloats * 4));
+    };
+    float vv[4];
+    float4 tm[4], bm[4];   // T' rows (K waves), Bm rows (Q waves); each role loads and reads only its own
+    ChunkIn inA, inB;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) inA.o[r] = inB.o[r] = 0.0f;
+    auto load_in = [&](int c, ChunkIn& d, int j) {   // row piece j < 8, or (j == 8) the gates
+        if (j < 8) {
+            const float4 a = buf_ld4(rows_rsrc(rsrc, c, qkv_stride, stride4), ro + 64u * j);
+            d.rows[4 * j] = a.x;
+            d.rows[4 * j + 1] = a.y;
+            d.rows[4 * j + 2] = a.z;
+            d.rows[4 * j + 3] = a.w;
+        } else {
+            const __amdgpu_buffer_rsrc_t w = ws_rsrc(c);
+            const float4 gv = buf_ld4(w, go);
+            d.gm[0] = gv.x;
+            d.gm[1] = gv.y;
+            d.gm[2] = gv.z;
+            d.gm[3] = gv.w;
+            d.glast = buf_ld1(w, glo);
+            d.rt4 = buf_ld4(w, rto);
         }
     };
-    auto load_gam = [&](int c, float (&g4)[4], float& gl) {
-        const float4 gv = ld4(chunk_base(c) + 2 * kC * kC + tres);
-        g4[0] = gv.x;
-        g4[1] = gv.y;
-        g4[2] = gv.z;
-        g4[3] = gv.w;
-        // gamma_{C-1} through a vector load: its address is wave-uniform, and as
-        // a scalar load it would share lgkmcnt with the LDS traffic, so every
-        // LDS wait would also wait for it (scalar loads return out of order).
-        // lane & (rows >> 31) is 0 (rows > 0) but not known to the compiler to
-        // be uniform, which keeps the load on the vector path.
-        gl = chunk_base(c)[2 * kC * kC + kC - 1 + (lane & (rows >> 31))];
-    };
-    // elements 16s + 4g .. 16s + 4g + 3 (s < 4) of a 64-long row: p = row + 4g
-    auto load_rows16 = [&](float4 (&dst)[4], const float* p) {
+    auto load_v = [&](int c) {
+        const __amdgpu_buffer_rsrc_t r = rows_rsrc(vsrc, c, qkv_stride, stride4);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) dst[s] = ld4(p + 16 * s);
+        for (int i = 0; i < 4; ++i) vv[i] = buf_ld1(r, vo[i]);
     };
-    // the same 16 elements of an LDS row (p = row + 4g), as 4 x 16-byte reads
+    // T' and Bm are zero above their 16 x 16 diagonal blocks: block s > wv is
+    // never multiplied, and its load re-reads block wv (the same number of
+    // loads on every wave keeps the wait counts uniform).
+    auto load_m = [&](int c, float4 (&m)[4]) {
+        const __amdgpu_buffer_rsrc_t w = ws_rsrc(c);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) m[s] = buf_ld4(w, mo + 64u * min(s, wv));
+    };
+    // elements 16s + 4g .. 16s + 4g + 3 (s < 4) of a 64-long LDS row (p = row + 4g)
     auto lds16 = [](float (&dst)[16], const float* p) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -388,152 +443,154 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
             dst[4 * s + 3] = t.w;
         }
     };
-    // T' and Bm rows 16wv + n at this lane's k-slot columns; R[C-1] at token tok.
-    auto tp_row = [&](int c) { return chunk_base(c) + (16 * wv + n) * kC + 4 * g; };
-    auto bm_row = [&](int c) { return chunk_base(c) + kC * kC + (16 * wv + n) * kC + 4 * g; };
-    auto rr_tok = [&](int c) { return chunk_base(c)[2 * kC * kC + kC + tok]; };
-    // the loop's load order (the wait counts at its head then line up)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) load_kq_j(0, j, kA, qA);
+    for (int j = 0; j <= 8; ++j) load_in(0, inA, j);
     load_v(0);
-    load_rows16(tpr, tp_row(0));
-    load_rows16(bmr, bm_row(0));
-    load_gam(0, gm, glast);
-    rt = rr_tok(0);
+    if (qw) load_m(0, bm);
+    else load_m(0, tm);
+    // The loop's wait counts are then computed from its own loads only.
+    __builtin_amdgcn_s_waitcnt(0);
 
-    // Chunk c with its K and Q rows in kc / qc; chunk c + 1's are loaded into
-    // kn / qn during c's X and Y products (the loop runs two chunks per pass
-    // with the two register sets swapped, so nothing is copied).
-    auto chunk_step = [&](int c, float (&kc)[32], float (&qc)[32], float (&kn)[32], float (&qn)[32])
+    // Chunk c with its inputs in cur; chunk c + 1's are loaded into nxt (the
+    // last chunk reloads its own: unconditional loads keep the wait counts exact).
+    auto chunk_step = [&](int c, ChunkIn& cur, ChunkIn& nxt, const float (*Sl)[kDK + 4], float (*Sw)[kDK + 4])
                           __attribute__((always_inline)) {
-        const int t0 = c * kC;
-        // Inputs of chunk cn are prefetched during this chunk (the last chunk
-        // reloads its own; unconditional loads keep the wait counts exact).
         const int cn = min(c + 1, nchunks - 1);
-
-        // S0 as the B operand (rows 16j + 4g + c, column n) and at this wave's
-        // rows of the state update's result tiles (32wv + 16mt + 4g + r).
+        // S0 as the B operand (rows 16j + 4g + c, column n)
         float sB[32];
         float4 sC[2];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float4 t = *reinterpret_cast<const float4*>(&SlT[n][16 * j + 4 * g]);
+            const float4 t = *reinterpret_cast<const float4*>(&Sl[n][16 * j + 4 * g]);
             sB[4 * j] = t.x;
             sB[4 * j + 1] = t.y;
             sB[4 * j + 2] = t.z;
             sB[4 * j + 3] = t.w;
         }
+        if (!qw) {
+            // S0 at this wave's state-update rows (32wv + 16mt + 4g + r), and the K rows to LDS
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) sC[mt] = *reinterpret_cast<const float4*>(&SlT[n][32 * wv + 16 * mt + 4 * g]);
-
+            for (int mt = 0; mt < 2; ++mt) sC[mt] = *reinterpret_cast<const float4*>(&Sl[n][32 * wv + 16 * mt + 4 * g]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+            for (int j = 0; j < 8; ++j)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) KsT[16 * j + 4 * g + c][tok] = kc[4 * j + c] * rt;
-        v4f_t xa[4], ya[4];
+                for (int cc = 0; cc < 4; ++cc) KsT[16 * j + 4 * g + cc][tok] = cur.rows[4 * j + cc];
+        }
+        // X = K S0 (K waves) or Y = Q S0 (Q waves); the next chunk's row loads go
+        // out one per 4 MFMAs (issued in one burst they held the wave)
+        v4f_t xa[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) xa[u] = ya[u] = v4f_t{0.f, 0.f, 0.f, 0.f};
-        // The next chunk's 16 row loads go out between the products, two per 8
-        // MFMAs: issued in one burst they held the wave ~1000 cycles at a point
-        // where the chunk's chain waits on it.
+        for (int u = 0; u < 4; ++u) xa[u] = v4f_t{0.f, 0.f, 0.f, 0.f};
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 32; ++s) {
-            if ((s & 3) == 0) load_kq_j(cn, s >> 2, kn, qn);
-            xa[s & 3] = mfma4(kc[s], sB[s], xa[s & 3]);
-            ya[s & 3] = mfma4(qc[s], sB[s], ya[s & 3]);
+            if ((s & 3) == 0) load_in(cn, nxt, s >> 2);
+            xa[s & 3] = mfma4(cur.rows[s], sB[s], xa[s & 3]);
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);   // 2 VMEM reads
-            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);   // 8 MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // 1 VMEM read
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   // 4 MFMAs
         }
         __builtin_amdgcn_sched_barrier(0);
         const v4f_t X = (xa[0] + xa[1]) + (xa[2] + xa[3]);
-        const v4f_t Y = (ya[0] + ya[1]) + (ya[2] + ya[3]);
-        // gamma and R[C-1] of the next chunk a whole chunk ahead, into their
-        // own registers (requested at the end of the chunk they came back
-        // ~2000 cycles after the next chunk's Rv needed them)
-        load_gam(cn, gm_n, glast_n);
-        rt_n = rr_tok(cn);
-
-        // Result rows: tokens 16wv + 4g + r, column n.
-        *reinterpret_cast<float4*>(&RvT[n][tres]) =
-            make_float4(vv[0] - gm[0] * X[0], vv[1] - gm[1] * X[1], vv[2] - gm[2] * X[2], vv[3] - gm[3] * X[3]);
-        load_v(cn);
+        load_in(cn, nxt, 8);
+        if (!qw) {
+            // result rows: tokens 16wv + 4g + r, column n
+            *reinterpret_cast<float4*>(&RvT[n][tres]) =
+                make_float4(__builtin_fmaf(-cur.gm[0], X[0], vv[0]), __builtin_fmaf(-cur.gm[1], X[1], vv[1]),
+                            __builtin_fmaf(-cur.gm[2], X[2], vv[2]), __builtin_fmaf(-cur.gm[3], X[3], vv[3]));
+            load_v(cn);
+        }
         __syncthreads();
-
-        // Delta = T' Rv (this wave's 16 rows; K = the chunk's 64 tokens).
-        float rb[16];
-        lds16(rb, &RvT[n][4 * g]);
-        v4f_t D0 = {0.f, 0.f, 0.f, 0.f}, D1 = D0;
+        if (!qw) {
+            // Delta = T' Rv (this wave's 16 rows; K = the chunk's tokens up to the diagonal block)
+            float rb[16];
+            lds16(rb, &RvT[n][4 * g]);
+            v4f_t D0 = {0.f, 0.f, 0.f, 0.f}, D1 = D0;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            D0 = mfma4(tpr[s].x, rb[4 * s], D0);
-            D1 = mfma4(tpr[s].y, rb[4 * s + 1], D1);
-            D0 = mfma4(tpr[s].z, rb[4 * s + 2], D0);
-            D1 = mfma4(tpr[s].w, rb[4 * s + 3], D1);
+            for (int s = 0; s < 4; ++s) {
+                if (s <= wv) {
+                    D0 = mfma4(tm[s].x, rb[4 * s], D0);
+                    D1 = mfma4(tm[s].y, rb[4 * s + 1], D1);
+                    D0 = mfma4(tm[s].z, rb[4 * s + 2], D0);
+                    D1 = mfma4(tm[s].w, rb[4 * s + 3], D1);
+                }
+            }
+            load_m(cn, tm);
+            const v4f_t D = D0 + D1;
+            *reinterpret_cast<float4*>(&DlT[n][tres]) = make_float4(D[0], D[1], D[2], D[3]);
+            // R[C-1][t] Delta_t: the state update's operand
+            *reinterpret_cast<float4*>(&DsT[n][tres]) =
+                make_float4(D[0] * cur.rt4.x, D[1] * cur.rt4.y, D[2] * cur.rt4.z, D[3] * cur.rt4.w);
         }
-        load_rows16(tpr, tp_row(cn));
-        *reinterpret_cast<float4*>(&DlT[n][tres]) = make_float4(D0[0] + D1[0], D0[1] + D1[1], D0[2] + D1[2],
-                                                                 D0[3] + D1[3]);
         __syncthreads();
-
-        // O = gamma Y + Bm Delta.
-        float db[16];   // Delta rows 16s + 4g + c, column n (also the state update's B operands)
-        lds16(db, &DlT[n][4 * g]);
-        v4f_t O0 = {gm[0] * Y[0], gm[1] * Y[1], gm[2] * Y[2], gm[3] * Y[3]}, O1 = {0.f, 0.f, 0.f, 0.f};
+        if (qw) {
+            // O = gamma Y + Bm Delta, stored during the next chunk
+            float db[16];
+            lds16(db, &DlT[n][4 * g]);
+            v4f_t O0 = {0.f, 0.f, 0.f, 0.f}, O1 = O0;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            O0 = mfma4(bmr[s].x, db[4 * s], O0);
-            O1 = mfma4(bmr[s].y, db[4 * s + 1], O1);
-            O0 = mfma4(bmr[s].z, db[4 * s + 2], O0);
-            O1 = mfma4(bmr[s].w, db[4 * s + 3], O1);
+            for (int s = 0; s < 4; ++s) {
+                if (s <= wv) {
+                    O0 = mfma4(bm[s].x, db[4 * s], O0);
+                    O1 = mfma4(bm[s].y, db[4 * s + 1], O1);
+                    O0 = mfma4(bm[s].z, db[4 * s + 2], O0);
+                    O1 = mfma4(bm[s].w, db[4 * s + 3], O1);
+                }
+            }
+            load_m(cn, bm);
+            const v4f_t O = O0 + O1;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cur.o[r] = __builtin_fmaf(cur.gm[r], X[r], O[r]);
+            // The previous chunk's outputs (none before chunk 0: a zero-range
+            // descriptor drops them). Stored a chunk late, their registers stay
+            // live: the store's data would otherwise be overwritten right after
+            // it by the next chunk's S0 reads, which waits for the store to complete.
+            const __amdgpu_buffer_rsrc_t orr =
+                c > 0 ? rows_rsrc(osrc, c - 1, out_stride, ostride4) : buf_rsrc(osrc, 0u);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) buf_st1(nxt.o[r], orr, oo[r]);
+        } else {
+            // state rows 32wv + 16mt + (0..15): gamma_{C-1} S0 + sum_t k_t (R[C-1][t] Delta_t)
+            // (step 4s + c: token 16s + 4g + c)
+            float db[16];
+            lds16(db, &DsT[n][4 * g]);
+            v4f_t A0 = {0.f, 0.f, 0.f, 0.f}, A1 = A0;
+            const int m0 = 32 * wv + n;
+            float ka[16], kb[16];
+            lds16(ka, &KsT[m0][4 * g]);
+            lds16(kb, &KsT[m0 + 16][4 * g]);
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                A0 = mfma4(ka[s], db[s], A0);
+                A1 = mfma4(kb[s], db[s], A1);
+            }
+            // the new state goes to the other buffer: no barrier between the
+            // readers of this chunk's S0 and these writes
+            *reinterpret_cast<float4*>(&Sw[n][32 * wv + 4 * g]) =
+                make_float4(__builtin_fmaf(cur.glast, sC[0].x, A0[0]), __builtin_fmaf(cur.glast, sC[0].y, A0[1]),
+                            __builtin_fmaf(cur.glast, sC[0].z, A0[2]), __builtin_fmaf(cur.glast, sC[0].w, A0[3]));
+            *reinterpret_cast<float4*>(&Sw[n][32 * wv + 16 + 4 * g]) =
+                make_float4(__builtin_fmaf(cur.glast, sC[1].x, A1[0]), __builtin_fmaf(cur.glast, sC[1].y, A1[1]),
+                            __builtin_fmaf(cur.glast, sC[1].z, A1[2]), __builtin_fmaf(cur.glast, sC[1].w, A1[3]));
         }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = t0 + tres + r;
-            if (t < rows)
-                out[static_cast<int64_t>(t) * out_stride + static_cast<size_t>(h) * value_dim + j0 + n] = O0[r] + O1[r];
-        }
-        load_rows16(bmr, bm_row(cn));
-
-        // S rows 32wv + 16mt + (0..15): gamma_{C-1} S0 + sum_t R[C-1][t] k_t Delta_t
-        // (step 4s + c: token 16s + 4g + c).
-        v4f_t A0 = {0.f, 0.f, 0.f, 0.f}, A1 = A0;
-        const int m0 = 32 * wv + n;
-        float ka[16], kb[16];
-        lds16(ka, &KsT[m0][4 * g]);
-        lds16(kb, &KsT[m0 + 16][4 * g]);
-#pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            A0 = mfma4(ka[s], db[s], A0);   // KsT holds R[C-1][t] k_t (the same product)
-            A1 = mfma4(kb[s], db[s], A1);
-        }
-        float4 sn[2];
-        sn[0] = make_float4(__builtin_fmaf(glast, sC[0].x, A0[0]), __builtin_fmaf(glast, sC[0].y, A0[1]),
-                            __builtin_fmaf(glast, sC[0].z, A0[2]), __builtin_fmaf(glast, sC[0].w, A0[3]));
-        sn[1] = make_float4(__builtin_fmaf(glast, sC[1].x, A1[0]), __builtin_fmaf(glast, sC[1].y, A1[1]),
-                            __builtin_fmaf(glast, sC[1].z, A1[2]), __builtin_fmaf(glast, sC[1].w, A1[3]));
-        // gamma and R[C-1] are dead for this chunk from here on
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            gm[r] = gm_n[r];
-        }
-        glast = glast_n;
-        rt = rt_n;
-        __syncthreads();  // every wave is done reading SlT, KsT, DlT of this chunk
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) *reinterpret_cast<float4*>(&SlT[n][32 * wv + 16 * mt + 4 * g]) = sn[mt];
-        __syncthreads();
+        __syncthreads();   // the new state is visible; KsT, RvT, DlT, DsT are free
     };
-    for (int c = 0; c < nchunks; c += 2) {
-        chunk_step(c, kA, qA, kB, qB);
-        if (c + 1 < nchunks) chunk_step(c + 1, kB, qB, kA, qA);
+    int c = 0;
+    for (; c + 1 < nchunks; c += 2) {
+        chunk_step(c, inA, inB, SlT[0], SlT[1]);
+        chunk_step(c + 1, inB, inA, SlT[1], SlT[0]);
     }
-
-    for (int e = threadIdx.x; e < kDK * kNB; e += kThreads)
-        Sg[static_cast<size_t>(e / kNB) * value_dim + e % kNB] = SlT[e % kNB][e / kNB];
+    if (c < nchunks) chunk_step(c, inA, inB, SlT[0], SlT[1]);
+    if (qw) {   // the last chunk's outputs
+        const __amdgpu_buffer_rsrc_t orr = rows_rsrc(osrc, nchunks - 1, out_stride, ostride4);
+        const ChunkIn& last = (nchunks & 1) ? inA : inB;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) buf_st1(last.o[r], orr, oo[r]);
+    }
+    for (int e = threadIdx.x; e < kDK * kNB; e += kWalkThreads)
+        Sg[static_cast<size_t>(e / kNB) * value_dim + e % kNB] = SlT[nchunks & 1][e % kNB][e / kNB];
 }
 
 }  // namespace
@@ -555,9 +612,11 @@ int qwen_gdn_recurrent_chunked(float* state, const float* q, const float* k, con
     // The same limit as the token loop, checked before the path is chosen, so
     // the status does not depend on which path a call's alignment selects.
     QK_REQUIRE(value_dim <= kMaxValueDim, "GDN value dimension exceeds kernel limit");
+    // The walk addresses a chunk's 64 rows with 32-bit byte offsets and buffer
+    // ranges below 2^31: longer row strides take the token loop.
     const bool chunked = key_dim == kDK && value_dim > 0 && value_dim % kNB == 0 && aligned16(q) && aligned16(k) &&
                          aligned16(workspace) && qkv_stride % 4 == 0 && rows > 0 && key_heads > 0 &&
-                         value_heads > 0;
+                         value_heads > 0 && qkv_stride <= kMaxWalkStride && out_stride <= kMaxWalkStride;
     if (!chunked)  // shapes outside the chunked kernels: the token loop, no workspace
         return qwen_gdn_recurrent_rows(state, q, k, v, beta, decay, out, rows, key_heads, value_heads, key_dim,
                                        value_dim, qkv_stride, out_stride, stream);
@@ -571,9 +630,15 @@ int qwen_gdn_recurrent_chunked(float* state, const float* q, const float* k, con
     float* ws = static_cast<float*>(workspace);
     gdn_chunk_prep<<<dim3(nchunks, std::min(key_heads, value_heads)), kThreads, 0, s>>>(q, k, beta, decay, ws, rows, key_heads, value_heads,
                                                                    qkv_stride);
-    gdn_chunk_state<<<(value_dim / kNB) * value_heads, kThreads, 0, s>>>(state, q, k, v, ws, out, rows, key_heads,
-                                                                         value_heads, value_dim, qkv_stride,
-                                                                         out_stride);
+    // One row: its stride is not used to step between rows, but the walk's
+    // buffer range is one stride long, so it must cover the row's q, k, v and out.
+    const int64_t row_extent = std::max<int64_t>(static_cast<int64_t>(key_heads) * key_dim,
+                                                 static_cast<int64_t>(value_heads) * value_dim);
+    const int64_t qs = rows == 1 ? std::max(qkv_stride, row_extent) : qkv_stride;
+    const int64_t os = rows == 1 ? std::max(out_stride, row_extent) : out_stride;
+    QK_REQUIRE(qs <= kMaxWalkStride && os <= kMaxWalkStride, "gdn_recurrent_chunked: row too long for the chunked walk");
+    gdn_chunk_state<<<(value_dim / kNB) * value_heads, kWalkThreads, 0, s>>>(state, q, k, v, ws, out, rows, key_heads,
+                                                                             value_heads, value_dim, qs, os);
     return check_launch("gdn_recurrent_chunked");
 }
 
