@@ -273,10 +273,16 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
             }
             __syncthreads();
         }
-        // T' = T diag(beta), zeros above the diagonal.
-        for (int e = threadIdx.x; e < kC * kC; e += kThreads) {
-            const int t = e / kC, jj = e % kC;
-            Tp[e] = t >= jj ? T[t][jj] * sb[jj] : 0.0f;
+        // T' = T diag(beta), zeros above the diagonal; 4 columns per thread
+        // (a 16-byte LDS read and store each instead of four 4-byte ones: the
+        // recurrence over 4096 tokens 251 -> 245 us).
+        for (int e = threadIdx.x; e < kC * kC / 4; e += kThreads) {
+            const int t = e / (kC / 4), j4 = 4 * (e % (kC / 4));
+            const float4 tv = *reinterpret_cast<const float4*>(&T[t][j4]);
+            const float4 bv = *reinterpret_cast<const float4*>(&sb[j4]);
+            *reinterpret_cast<float4*>(Tp + t * kC + j4) =
+                make_float4(t >= j4 ? tv.x * bv.x : 0.0f, t >= j4 + 1 ? tv.y * bv.y : 0.0f,
+                            t >= j4 + 2 ? tv.z * bv.z : 0.0f, t >= j4 + 3 ? tv.w * bv.w : 0.0f);
         }
     }
 }
@@ -322,11 +328,11 @@ struct ChunkIn {
 // Y = Q S0 for the same tokens and O. Each SIMD so runs two instruction streams
 // whose stalls the other fills. The older wave of a SIMD wins its issue
 // arbitration: with the Q waves first, their MFMAs cover the K waves' LDS and
-// vector ALU work (the other order measured 5% slower). The role branches hold no loads that the other
-// role's code reads, and every path back to the loop head issues both chunks'
-// loads, which keeps the compiler's memory-wait counts tight (a branch that
-// skipped the second chunk, or one register set loaded at different points by
-// the two roles, turned them into full drains).
+// vector ALU work (the other order measured 5% slower). The role branches hold
+// no loads that the other role's code reads, and every path back to the loop
+// head issues both chunks' loads, which keeps the compiler's memory-wait counts
+// tight (a branch that skipped the second chunk, or one register set loaded at
+// different points by the two roles, turned them into full drains).
 __global__ __launch_bounds__(kWalkThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_chunk_state(
     float* __restrict__ S, const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ ws, float* __restrict__ out, int rows, int key_heads, int value_heads, int value_dim,
