@@ -20,14 +20,16 @@
 //
 // Kernel A (one workgroup per (chunk, key head), all chunks in parallel):
 // K K^T and Q K^T on fp32 MFMA (v_mfma_f32_16x16x4f32) once, then for each value
-// head that reads this key head the ratios and T as a blocked inverse (16 x 16 diagonal blocks by forward substitution, the others
-// as MFMA products) -> T', Bm, gamma, R[C-1][.] to the caller's workspace.
-// Kernel B (one workgroup per (value head, 16 state columns), chunks in order,
-// the workgroups of one head on one XCD):
-// X = K S0 and Y = Q S0 (each wave one 16-token M-tile, K = 128 over 32 MFMA
-// steps), Delta = T' (V - gamma X), O = gamma Y + Bm Delta, then the 128 x 16
-// state block updated from K~^T Delta; the block lives in LDS between chunks
-// and is read from / written to the state once per call.
+// head that reads this key head the ratios and T as a blocked inverse (16 x 16
+// diagonal blocks by forward substitution, the others as MFMA products)
+// -> T', Bm, gamma, R[C-1][.] to the caller's workspace.
+// Kernel B (one 8-wave workgroup per (value head, 16 state columns), chunks in
+// order, the workgroups of one head on one XCD): per SIMD a Q wave computing
+// Y = Q S0 and O = gamma Y + Bm Delta for 16 tokens, and a K wave computing
+// X = K S0, Delta = T' (V - gamma X) for the same tokens and 32 rows of the state
+// update S_C = gamma_{C-1} S0 + K^T (R[C-1] Delta) (each 16-token product K = 128
+// over 32 MFMA steps); the 128 x 16 state block lives in LDS between chunks and
+// is read from / written to the state once per call.
 #include <algorithm>
 
 #include "capi_common.hpp"
