@@ -56,10 +56,14 @@ NAMES = [
     ("moe_down_combine_q4k", "moe_down_combine, Q4_K direct (routed + shared down, combine)"),
     ("gemv_q4k_direct_multi", "gemv Q4_K direct, several matrices of one x (matmul_dispatch_multi)"),
     ("gemv_q4k_direct_gate_up", "gemv Q4_K direct, routed experts' gate + up (moe_expert_gate_up)"),
-    ("gemv_q4k_direct<2, 1>", "gemv Q4_K direct, 2 rows/wave (GDN qkv)"),
-    ("gemv_q4k_direct<2, 2>", "gemv Q4_K direct, 2 rows/wave, 2-unit rows (out proj)"),
-    ("gemv_q4k_direct<1, 1>", "gemv Q4_K direct, 1 row/wave (experts)"),
+    ("gemv_q4k_direct<2, 1,", "gemv Q4_K direct, 2 rows/wave (GDN qkv)"),
+    ("gemv_q4k_direct<2, 2,", "gemv Q4_K direct, 2 rows/wave, 2-unit rows (out proj)"),
+    ("gemv_q4k_direct<1, 1,", "gemv Q4_K direct, 1 row/wave (experts)"),
     ("gemv_q4k_direct", "gemv Q4_K direct, other shapes"),
+    ("gemv_q6k_direct_multi", "gemv Q6_K direct, several matrices of one x (matmul_dispatch_multi)"),
+    ("gemv_q6k_direct<2,", "gemv Q6_K direct, 2 rows/wave (8192-row matrices)"),
+    ("gemv_q6k_direct<1,", "gemv Q6_K direct, 1 row/wave"),
+    ("gemv_q6k_direct", "gemv Q6_K direct, other shapes"),
     ("gemv_kquant<14, 4>", "gemv Q6_K per-row, 4 units/wave"),
     ("gemv_kquant<12, 2>", "gemv Q4_K per-row, 2 units/wave (GDN qkv)"),
     ("gemv_kquant<12, 1>", "gemv Q4_K per-row, 1 unit/wave (out proj, experts)"),
@@ -79,8 +83,11 @@ NAMES = [
     ("softmax_regs", "attn_softmax (drop-in, row in registers)"),
     ("softmax_loop", "attn_softmax (drop-in, long rows)"),
     ("values_cols", "attn_values (drop-in)"),
+    ("topk_group_kernel", "moe_topk, two rows per wave (top-k of <= 256)"),
     ("topk_rows_kernel", "moe_topk_rows"),
     ("weighted_sum_v4", "moe_weighted_sum_rows"),
+    ("gates_kernel", "gdn gates (decode, separate launch)"),
+    ("sigmoid_gate_kernel", "attn sigmoid gate (drop-in)"),
     ("gemm_prep_x", "matmul_rows prep (x to fp16 parts)"),
     ("gemm_q4k", "matmul_rows Q4_K GEMM, fp16 MFMA"),
     ("gemm_q6k", "matmul_rows Q6_K GEMM, fp16 MFMA"),
