@@ -292,10 +292,11 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
 // ---------------------------------------------------------------- state walk
 // Raw buffer access for the walk: a wave-uniform descriptor (base, byte range)
 // and a loop-invariant 32-bit lane offset, so a load costs no address
-// arithmetic on the vector ALU. Every VALU instruction issued while the
-// SIMD's matrix pipe runs the other wave's MFMAs waits for a pipe slot
-// (~one 16x16x4 f32 MFMA, measured), and per-load 64-bit address arithmetic
-// was most of the walk's VALU work. Loads at or past the range return 0 and
+// arithmetic on the vector ALU. A SIMD's vector-ALU and MFMA work do not
+// overlap, even from different waves (one wave streaming fp32 MFMAs beside one
+// running FMAs takes the sum of their times, measured), so every VALU
+// instruction adds to the chunk's time; per-load 64-bit address arithmetic was
+// most of the walk's VALU work. Loads at or past the range return 0 and
 // stores there are dropped: the padding tokens of a partial last chunk read
 // zeros (finite; their beta 0 and decay 1 give them zero rows and columns of
 // T' and zero rows of Bm, so they add nothing) and their outputs are not written.
