@@ -588,6 +588,61 @@ def test_gdn_recurrent_chunked_head_maps(oracle, kh, vh):
     _check_gdn_recurrence(oracle, qkv, beta, decay, state, out, host(ds), kh, vh, dk, dv)
 
 
+def test_gdn_recurrent_chunked_strides(oracle):
+    """Row strides the chunked state walk addresses with 32-bit lane offsets from a
+    per-chunk base: a qkv row padded past q | k | v and an output row padded past its
+    values (the padding stays untouched); one row with strides 0 (the walk reads a
+    range one stride long, so the library widens it to the row); and a qkv stride past
+    the walk's 32-bit limit, which runs the token loop (the same bits as calling it)."""
+    import ctypes
+    from qwen35_hip._lib import check
+
+    lib = ops.load()
+    kh, vh, dk, dv = 4, 8, 128, 32
+    kd = kh * dk
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    def call(fn, state, qkv_t, beta, decay, out_t, rows, qs, os, ws=True):
+        base = qkv_t.data_ptr()
+        args = [vp(state), ctypes.c_void_p(base), ctypes.c_void_p(base + 4 * kd), ctypes.c_void_p(base + 8 * kd),
+                vp(beta), vp(decay), vp(out_t), rows, kh, vh, dk, dv, qs, os]
+        if ws:
+            w = torch.empty(lib.qwen_gdn_recurrent_chunked_workspace_bytes(rows, vh), dtype=torch.uint8, device="cuda")
+            args += [vp(w), w.numel()]
+        check(fn(*args, None))
+        torch.cuda.synchronize()
+
+    r = rng(977)
+    # padded rows: qkv stride 2 kd + vh dv + 12, output stride vh dv + 20 (two chunks, the second ragged)
+    rows = 100
+    qkv, b, alpha, a, dt, state = _gdn_inputs(r, rows, kh, vh, dk, dv, extra=12)
+    beta, decay = oracle.gdn_gate_values_rows(b, alpha, a, dt)
+    ds = dev(state)
+    out = torch.full((rows, vh * dv + 20), 7.0, device="cuda")
+    call(lib.qwen_gdn_recurrent_chunked, ds, dev(qkv), dev(beta), dev(decay), out, rows, qkv.shape[1], out.shape[1])
+    o = host(out)
+    assert (o[:, vh * dv:] == 7.0).all(), "output padding written"
+    _check_gdn_recurrence(oracle, qkv, beta, decay, state, np.ascontiguousarray(o[:, :vh * dv]), host(ds), kh, vh, dk, dv)
+    # one row, strides 0
+    qkv, b, alpha, a, dt, state = _gdn_inputs(r, 1, kh, vh, dk, dv)
+    beta, decay = oracle.gdn_gate_values_rows(b, alpha, a, dt)
+    ds = dev(state)
+    out = torch.empty((1, vh * dv), device="cuda")
+    call(lib.qwen_gdn_recurrent_chunked, ds, dev(qkv), dev(beta), dev(decay), out, 1, 0, 0)
+    _check_gdn_recurrence(oracle, qkv, beta, decay, state, host(out), host(ds), kh, vh, dk, dv)
+    # qkv stride 8,400,000 floats (past 2^31 bytes over 64 rows): the token loop, bit for bit
+    qkv, b, alpha, a, dt, state = _gdn_inputs(r, 2, kh, vh, dk, dv)
+    beta, decay = (dev(x) for x in oracle.gdn_gate_values_rows(b, alpha, a, dt))
+    wide = torch.zeros((2, 8_400_000), device="cuda")
+    wide[:, :qkv.shape[1]] = dev(qkv)
+    s1, s2 = dev(state), dev(state)
+    o1, o2 = torch.empty((2, vh * dv), device="cuda"), torch.empty((2, vh * dv), device="cuda")
+    call(lib.qwen_gdn_recurrent_chunked, s1, wide, beta, decay, o1, 2, wide.shape[1], vh * dv)
+    call(lib.qwen_gdn_recurrent_rows, s2, wide, beta, decay, o2, 2, wide.shape[1], vh * dv, ws=False)
+    assert_bits_equal(host(o1), host(o2), "long-stride fallback outputs")
+    assert_bits_equal(host(s1), host(s2), "long-stride fallback state")
+
+
 def test_gdn_recurrent_chunked_long_and_fallback(oracle):
     """2048 tokens (32 chunks): the chunked form and the token-loop kernel both
     against the oracle's token loop (condition-scale bar: late outputs of strongly
