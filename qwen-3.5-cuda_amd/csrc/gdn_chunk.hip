@@ -330,8 +330,9 @@ struct ChunkIn {
 // V - gamma X, Delta and state rows 32w..32w+31; the Q wave (wave w) computes
 // Y = Q S0 for the same tokens and O. Each SIMD so runs two instruction streams
 // whose stalls the other fills. The older wave of a SIMD wins its issue
-// arbitration: with the Q waves first, their MFMAs cover the K waves' LDS and
-// vector ALU work (the other order measured 5% slower). The role branches hold
+// arbitration: with the Q waves first, the K waves' LDS writes and loads at the
+// start of a chunk run while the Q waves' products hold the matrix pipe (the
+// other order measured 5% slower). The role branches hold
 // no loads that the other role's code reads, and every path back to the loop
 // head issues both chunks' loads, which keeps the compiler's memory-wait counts
 // tight (a branch that skipped the second chunk, or one register set loaded at
