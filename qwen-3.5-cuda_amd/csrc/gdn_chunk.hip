@@ -300,6 +300,8 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
 // stores there are dropped: the padding tokens of a partial last chunk read
 // zeros (finite; their beta 0 and decay 1 give them zero rows and columns of
 // T' and zero rows of Bm, so they add nothing) and their outputs are not written.
+// Descriptor: stride 0 (raw, the range counted in bytes), dword 3 = 0x00020000
+// (gfx9 DATA_FORMAT field = 4, 32-bit elements; no swizzle, no index stride).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const float* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
