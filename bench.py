@@ -338,7 +338,7 @@ def build_next_rows(torch, ops, synth, host):
                 oo = o if i == 0 else torch.empty_like(o)
                 return lambda: ops.gdn_recurrent_chunked(ss, qq, beta, decay, kh, vh, dk, dv, oo, workspace=ws)
             kc = Kernel("gdn_recurrent_chunked_4096", "the same 4096 tokens in the chunked form (64-token chunks, "
-                        "fp32 MFMA, 2 launches)", nb, nb, mk_chunk)
+                        "fp16-pair MFMA for the long products, 2 launches)", nb, nb, mk_chunk)
             kc.gdn = k.gdn
             ks.append(kc)
 

@@ -209,7 +209,9 @@ int qwen_gdn_decode_step(const float* x, const float* conv_weight, const float* 
 /* Chunked form of qwen_gdn_recurrent_rows for many tokens (prefill): the same
  * recurrence re-associated over chunks of 64 tokens (decay ratios as running
  * products, a 64 x 64 triangular solve per chunk and head, the state updated
- * once per chunk on fp32 MFMA); equal to the token loop within fp32 rounding.
+ * once per chunk; the products over 128 keys or 64 tokens on fp16 MFMA with each
+ * fp32 operand held as a scaled pair of fp16 values);
+ * equal to the token loop within fp32 rounding.
  * Arguments as qwen_gdn_recurrent_rows plus a caller-owned device workspace of
  * at least qwen_gdn_recurrent_chunked_workspace_bytes(rows, value_heads)
  * (16-byte aligned; contents scratch). Shapes the chunked kernels do not cover

@@ -22,14 +22,31 @@
 // K K^T and Q K^T on fp32 MFMA (v_mfma_f32_16x16x4f32) once, then for each value
 // head that reads this key head the ratios and T as a blocked inverse (16 x 16
 // diagonal blocks by forward substitution, the others as MFMA products)
-// -> T', Bm, gamma, R[C-1][.] to the caller's workspace.
+// -> T', Bm, gamma, R[C-1][.] to the caller's workspace; and the chunk's K and Q
+// as fp16 pairs (below).
 // Kernel B (one 8-wave workgroup per (value head, 16 state columns), chunks in
 // order, the workgroups of one head on one XCD): per SIMD a Q wave computing
 // Y = Q S0 and O = gamma Y + Bm Delta for 16 tokens, and a K wave computing
 // X = K S0, Delta = T' (V - gamma X) for the same tokens and 32 rows of the state
-// update S_C = gamma_{C-1} S0 + K^T (R[C-1] Delta) (each 16-token product K = 128
-// over 32 MFMA steps); the 128 x 16 state block lives in LDS between chunks and
-// is read from / written to the state once per call.
+// update S_C = gamma_{C-1} S0 + K^T (R[C-1] Delta); the K waves hold the
+// 128 x 16 state block in registers between chunks (read from / written to the
+// state once per call) and publish it to the other waves through LDS.
+//
+// fp16 pairs. The three products with a long sum (X and Y over the 128 key dims,
+// the state update over the chunk's 64 tokens) run on v_mfma_f32_16x16x32_f16:
+// it sums 32 terms per lane group where v_mfma_f32_16x16x4f32 sums 4, in ~22
+// cycles against ~35 (measured on gfx950), and a SIMD's MFMA time is not hidden
+// behind its other work. An fp32 operand x is scaled by 2^e (e chosen per block
+// from the block's largest |x| or a bound on it, so that the largest lands in
+// [2^14, 2^15)) and held as hi = fp16(x 2^e), lo = fp16(x 2^e - hi); a product is
+// hi lo' + lo hi' + hi hi' (fp16 products are exact in fp32), accumulated in
+// fp32 and scaled back exactly by ldexp(., -(e + e')). The dropped lo lo' and
+// the two roundings are below ~2^-21 of each term, under the fp32 token loop's
+// own rounding at these sums; elements below ~2^-38 of their block's scale
+// fall into fp16's subnormals and lose their low bits (a scale multiplier
+// 2^-(e + e') held as a float, e clamped to keep it normal, lost a strongly
+// decayed head's whole state of ~1e-23 this way). The Delta and O products
+// (the triangular 16-token blocks) stay fp32.
 #include <algorithm>
 
 #include "capi_common.hpp"
@@ -47,15 +64,77 @@ constexpr int kWalkThreads = 512;             // state walk: two waves per SIMD
 constexpr int64_t kMaxWalkStride = 0x7fffffff / (4 * 64);   // floats; 64 rows of 4-byte elements below 2^31 bytes
 constexpr int kXcds = 8;                      // gfx950: 8 XCDs, workgroups dealt round-robin
 constexpr int kLdA = kC + 4;                  // LDS row stride of the C x C matrices (16-byte rows)
-constexpr size_t kWsFloats = 2 * kC * kC + 2 * kC;   // per (chunk, head): T', Bm, gamma, R[C-1][.]
+// Per (chunk, value head): T', Bm, gamma, R[C-1][.], then {gamma_{C-1}, eK, eQ, rho}
+// (eK, eQ: int bits)
+// (rho bounds |R[C-1][t] Delta[t][j]| / max_i |(V - gamma X)[i][j]|).
+constexpr int kWsExtra = 2 * kC * kC + 2 * kC;
+constexpr size_t kWsFloats = kWsExtra + 4;
+// Per (chunk, key head), after all the value-head blocks: fp16 pairs of K and
+// Q by token (layout at the prep's stores).
+constexpr uint32_t kKRows = 0, kQRows = kC * kDK * 4;
+constexpr size_t kKqBytes = 2 * kC * kDK * 4;
+constexpr int kKtLd = kDK + 16;               // LDS row of the walk's K copy: 288 bytes (transposed reads without bank conflicts)
 
 typedef float v4f_t __attribute__((ext_vector_type(4)));
+typedef unsigned u4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef float f2_t __attribute__((ext_vector_type(2)));
 
 // D[m][n] += sum over the instruction's 4 k-slots of A[m][k] B[k][n]: lane L
 // supplies A[L%16][L/16] and B[L/16][L%16]; D lane L, element r is
 // D[4(L/16) + r][L%16].
 __device__ __forceinline__ v4f_t mfma4(float a, float b, v4f_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+// The same over 32 k-slots: lane L supplies 8 fp16 values, A[L%16][8(L/16) + s]
+// and B[8(L/16) + s][L%16] (s < 8); D as above. Only the pairing matters here:
+// slot s of lane group g means the same k in both operands.
+__device__ __forceinline__ v4f_t mfma16(u4_t a, u4_t b, v4f_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a), __builtin_bit_cast(h8_t, b), c, 0, 0,
+                                                  0);
+}
+
+// 2^e puts m (>= 0, finite) in [2^14, 2^15): m = f 2^E with f in [0.5, 1),
+// e = 15 - E (fp32 subnormals included); 15 for m = 0.
+__device__ __forceinline__ int scale_exp(float m) { return 15 - __builtin_amdgcn_frexp_expf(m); }
+// (a, b) 2^e as fp16 pairs: hi rounded to nearest, lo the rest rounded to nearest.
+__device__ __forceinline__ void split2(float a, float b, int e, unsigned& hi, unsigned& lo) {
+    const f2_t s = {__builtin_amdgcn_ldexpf(a, e), __builtin_amdgcn_ldexpf(b, e)};
+    const h2_t h = __builtin_convertvector(s, h2_t);
+    const f2_t h32 = __builtin_convertvector(h, f2_t);
+    const f2_t r = {s.x - h32.x, s.y - h32.y};
+    hi = __builtin_bit_cast(unsigned, h);
+    lo = __builtin_bit_cast(unsigned, __builtin_convertvector(r, h2_t));
+}
+__device__ __forceinline__ void split8(const float* x, int e, u4_t& hi, u4_t& lo) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        unsigned h, l;
+        split2(x[2 * p], x[2 * p + 1], e, h, l);
+        hi[p] = h;
+        lo[p] = l;
+    }
+}
+// T' and Bm are stored in the walk's fragment order, each 64 x 64 matrix as 16
+// pieces of 1 KB [row tile][column block s][lane] x 4 floats, lane (n, g)
+// holding row 16 tile + n, columns 16s + 4g .. + 3: one wave instruction reads
+// one piece. Index (in float4 units) of row 16 tile + 0 at column j.
+__host__ __device__ __forceinline__ int frag_index(int tile, int j) {
+    return (tile * 4 + (j >> 4)) * 64 + ((j >> 2) & 3) * 16;
+}
+// max over lanes L, L^16, L^32, L^48 (the four lane groups of a column)
+__device__ __forceinline__ float max_groups(float x) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float m = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+// max over all 64 lanes
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));
+    return max_groups(x);
 }
 
 // The 32 dims of a 128-dim row that lane group g supplies as MFMA k-slots:
@@ -78,8 +157,8 @@ __device__ __forceinline__ void load32(const float* __restrict__ row, int g, boo
 __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restrict__ q, const float* __restrict__ k,
                                                            const float* __restrict__ beta,
                                                            const float* __restrict__ decay, float* __restrict__ ws,
-                                                           int rows, int key_heads, int value_heads,
-                                                           int64_t qkv_stride) {
+                                                           unsigned char* __restrict__ kq, int rows, int key_heads,
+                                                           int value_heads, int64_t qkv_stride) {
     // The chunk's K rows while the products run; after them the same storage
     // holds A (strictly lower) and T of the value head in hand.
     __shared__ __align__(16) float kat[2 * kC * kLdA];
@@ -87,6 +166,10 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
     __shared__ __align__(16) float G[kC][kLdA];    // K K^T
     __shared__ __align__(16) float Pm[kC][kLdA];   // Q K^T
     __shared__ __align__(16) float sb[kC], sd[kC];
+    __shared__ float smax[2][4];                   // per wave: max |K|, max |Q| over its rows
+    __shared__ float stmax[4];                     // per wave: largest |R[C-1][t]| sum_i |T'[t][i]|
+    __shared__ float sR[kC];                       // |R[C-1][t]|
+    __shared__ float sglast;                       // gamma_{C-1}
     float(*Kl)[kDK + 4] = reinterpret_cast<float(*)[kDK + 4]>(kat);
     float(*Ab)[kLdA] = reinterpret_cast<float(*)[kLdA]>(kat);
     float(*T)[kLdA] = reinterpret_cast<float(*)[kLdA]>(kat + kC * kLdA);
@@ -95,6 +178,9 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
     const int lane = threadIdx.x & 63;
     const int wv = wave_in_block();
     const int g = lane >> 4, n = lane & 15;
+    // src < min(key_heads, value_heads): the blocks are sized per value head
+    unsigned char* const kqb = kq + (static_cast<size_t>(c) * value_heads + src) * kKqBytes;
+    int eK, eQ;
 
     // beta and decay of token t0 + threadIdx.x (threads < kC) for value head h,
     // held in registers: the next head's are requested while this head's work
@@ -124,7 +210,41 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
         for (int j = 0; j < 8; ++j)
             *reinterpret_cast<float4*>(&Kl[16 * wv + n][16 * j + 4 * g]) =
                 make_float4(kr[4 * j], kr[4 * j + 1], kr[4 * j + 2], kr[4 * j + 3]);
+        float mk = 0.0f, mq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            mk = fmaxf(mk, fabsf(kr[i]));
+            mq = fmaxf(mq, fabsf(qr[i]));
+        }
+        mk = wave_max(mk);
+        mq = wave_max(mq);
+        if (lane == 0) {
+            smax[0][wv] = mk;
+            smax[1][wv] = mq;
+        }
         __syncthreads();
+        eK = scale_exp(fmaxf(fmaxf(smax[0][0], smax[0][1]), fmaxf(smax[0][2], smax[0][3])));
+        eQ = scale_exp(fmaxf(fmaxf(smax[1][0], smax[1][1]), fmaxf(smax[1][2], smax[1][3])));
+        // K and Q by token (the walk's X and Y operands) in the order the walk's
+        // lanes read them: 1 KB fragments [tile wv][2 kb + (hi, lo)][lane] x 8 fp16,
+        // lane (n, g) = token 16wv + n, slot 4h + c of k-block kb = dim
+        // 32kb + 16h + 4g + c, which is this lane's kr[8kb + 4h + c]. One wave
+        // instruction then reads 1 KB in one piece (16 rows of 64 bytes cost the
+        // CU about twice as long, measured). Padding tokens are zeros.
+        {
+            unsigned char* const rk = kqb + kKRows + (wv * 8 * 64 + lane) * 16;
+            unsigned char* const rq = kqb + kQRows + (wv * 8 * 64 + lane) * 16;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                u4_t hi, lo;
+                split8(kr + 8 * kb, eK, hi, lo);
+                *reinterpret_cast<u4_t*>(rk + 2048 * kb) = hi;
+                *reinterpret_cast<u4_t*>(rk + 2048 * kb + 1024) = lo;
+                split8(qr + 8 * kb, eQ, hi, lo);
+                *reinterpret_cast<u4_t*>(rq + 2048 * kb) = hi;
+                *reinterpret_cast<u4_t*>(rq + 2048 * kb + 1024) = lo;
+            }
+        }
         auto tile = [&](const float (&a)[32], int mt, int nt, float (*D)[kLdA]) {
             v4f_t acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -205,19 +325,25 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
                 gv[u] = G[ta + u][i];
                 pv[u] = Pm[ta + u][i];
             }
+            // Bm[t][i] at the walk's fragment position of row t = 16wv + u, column i
+            float* const bmi = Bm + frag_index(wv, i) * 4 + (i & 3);
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
                 const int t = ta + u;
                 if (t > i) r *= dv16[u];
                 Ab[t][i] = t > i ? (bv16[u] * gv[u]) * r : 0.0f;
-                Bm[t * kC + i] = t >= i ? pv[u] * r : 0.0f;
+                bmi[4 * u] = t >= i ? pv[u] * r : 0.0f;
             }
-            if (wv == 3) rr[i] = r;  // R[C-1][i]
+            if (wv == 3) {  // R[C-1][i]
+                rr[i] = r;
+                sR[i] = fabsf(r);
+            }
             if (wv == 0) {  // gamma_t = d_0 * ... * d_t in order, lane t
                 float gm = 1.0f;
 #pragma unroll
                 for (int t = 0; t < kC; ++t) gm *= t <= lane ? dall[t] : 1.0f;
                 gam[lane] = gm;
+                if (lane == kC - 1) sglast = gm;
             }
         }
         __syncthreads();
@@ -278,14 +404,30 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
         // T' = T diag(beta), zeros above the diagonal; 4 columns per thread
         // (a 16-byte LDS read and store each instead of four 4-byte ones: the
         // recurrence over 4096 tokens 251 -> 245 us).
+        // The 16 threads of a row are 16 consecutive lanes: their |T'| sums add
+        // within the lane group, and each thread keeps the largest row sum times
+        // |R[C-1][t]| it saw (the same token's factors: pairing the largest of each
+        // over different tokens overstated the bound by up to ~1e9 for strongly
+        // decayed heads, whose R[C-1] Delta then fell into fp16's subnormals).
+        float rowmax = 0.0f;
         for (int e = threadIdx.x; e < kC * kC / 4; e += kThreads) {
             const int t = e / (kC / 4), j4 = 4 * (e % (kC / 4));
             const float4 tv = *reinterpret_cast<const float4*>(&T[t][j4]);
             const float4 bv = *reinterpret_cast<const float4*>(&sb[j4]);
-            *reinterpret_cast<float4*>(Tp + t * kC + j4) =
-                make_float4(t >= j4 ? tv.x * bv.x : 0.0f, t >= j4 + 1 ? tv.y * bv.y : 0.0f,
-                            t >= j4 + 2 ? tv.z * bv.z : 0.0f, t >= j4 + 3 ? tv.w * bv.w : 0.0f);
+            const float4 tp = make_float4(t >= j4 ? tv.x * bv.x : 0.0f, t >= j4 + 1 ? tv.y * bv.y : 0.0f,
+                                          t >= j4 + 2 ? tv.z * bv.z : 0.0f, t >= j4 + 3 ? tv.w * bv.w : 0.0f);
+            *reinterpret_cast<float4*>(Tp + (frag_index(t >> 4, j4) + (t & 15)) * 4) = tp;
+            const float part = (fabsf(tp.x) + fabsf(tp.y)) + (fabsf(tp.z) + fabsf(tp.w));
+            rowmax = fmaxf(rowmax, group_sum<16>(part) * sR[t]);
         }
+        rowmax = wave_max(rowmax);
+        if (lane == 0) stmax[wv] = rowmax;
+        __syncthreads();
+        // |R[C-1][t] Delta[t][j]| <= |R[C-1][t]| sum_i |T'[t][i]| max_i |(V - gamma X)[i][j]|
+        if (threadIdx.x == 0)
+            *reinterpret_cast<float4*>(wsc + kWsExtra) =
+                make_float4(sglast, __int_as_float(eK), __int_as_float(eQ),
+                            fmaxf(fmaxf(stmax[0], stmax[1]), fmaxf(stmax[2], stmax[3])));
     }
 }
 
@@ -302,8 +444,11 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
 // T' and zero rows of Bm, so they add nothing) and their outputs are not written.
 // Descriptor: stride 0 (raw, the range counted in bytes), dword 3 = 0x00020000
 // (gfx9 DATA_FORMAT field = 4, 32-bit elements; no swizzle, no index stride).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const float* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, static_cast<int>(bytes), 0x00020000);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ u4_t buf_ld4u(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 // The 16-byte load is reinterpreted whole: taking its result apart element by
 // element compiled to a 4-byte load on this compiler.
@@ -320,10 +465,7 @@ __device__ __forceinline__ void buf_st1(float x, __amdgpu_buffer_rsrc_t r, uint3
 // Per-chunk inputs a lane holds, loaded one chunk ahead (two sets, swapped by
 // the loop's two chunk steps, so nothing is copied).
 struct ChunkIn {
-    float rows[32];   // K rows (K waves) or Q rows (Q waves): dims 16j + 4g + c of token 16w + n
-    float gm[4];      // gamma at the lane's 4 result tokens
-    float glast;      // gamma_{C-1}
-    float4 rt4;       // R[C-1][t] at the lane's 4 result tokens
+    u4_t a[8];        // K (K waves) or Q (Q waves) by token as fp16 pairs: a[2 kb + (0 hi, 1 lo)]
     float o[4];       // this chunk's outputs (Q waves), stored during the next chunk
 };
 
@@ -339,17 +481,35 @@ struct ChunkIn {
 // head issues both chunks' loads, which keeps the compiler's memory-wait counts
 // tight (a branch that skipped the second chunk, or one register set loaded at
 // different points by the two roles, turned them into full drains).
+//
+// Operand pairing of the fp16 products (slot s = 4h + r of lane group g):
+//   X, Y: k-block kb (32 key dims, the state rows of K wave kb), slot -> key
+//         32kb + 16h + 4g + r; the state's fp16 pairs for kb are exactly what
+//         lane (n, g) of K wave kb holds (rows 32kb + 16mt + 4g + r, mt = h).
+//   state update: k-block kb (32 tokens), slot -> token 32kb + 16h + 4g + r;
+//         the R[C-1] Delta pairs are what lane (n, g) of K wave 2kb + h holds.
+// So the fp16 pairs of the state and of R[C-1] Delta move through LDS lane to
+// same lane. The state update's other operand, K by key, is the K waves' own
+// K by token copied to LDS and read back with ds_read_b64_tr_b16 (gfx950's
+// transposing LDS read): in each 16-lane group lane j points at 4 consecutive
+// key dims of token t_{j/4}, and lane i receives key dim d0 + i of the four
+// tokens. A vector-memory instruction costs the CU ~30-60 cycles beside the
+// others' (measured; the walk's time follows its count of them), an LDS one ~15.
+//
+// The gates of a chunk (gamma, R[C-1], the scales) are loaded once per Q wave
+// a chunk ahead and shared through LDS.
 __global__ __launch_bounds__(kWalkThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gdn_chunk_state(
-    float* __restrict__ S, const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    const float* __restrict__ ws, float* __restrict__ out, int rows, int key_heads, int value_heads, int value_dim,
-    int64_t qkv_stride, int64_t out_stride) {
-    // The tiles a lane reads as MFMA operands along their K dimension are stored
-    // transposed ([column][row]), so those operands are consecutive floats.
-    __shared__ __align__(16) float KsT[kDK][kC + 4];      // the chunk's k_t, [key][token]
+    float* __restrict__ S, const float* __restrict__ v, const float* __restrict__ ws,
+    const unsigned char* __restrict__ kq, float* __restrict__ out, int rows, int key_heads, int value_heads,
+    int value_dim, int64_t qkv_stride, int64_t out_stride) {
+    __shared__ __align__(16) u4_t SH[4][2][64];           // S0 as fp16 pairs: [32-row slab][hi, lo][lane]
+    __shared__ __align__(16) int SE[kNB][4];              // scale exponent e of each (column, slab)
     __shared__ __align__(16) float RvT[kNB][kC + 4];      // V - gamma X, [column][token]
+    __shared__ __align__(16) float RvM[kNB][4];           // max |V - gamma X| of each (column, 16-token tile)
     __shared__ __align__(16) float DlT[kNB][kC + 4];      // Delta, [column][token]
-    __shared__ __align__(16) float DsT[kNB][kC + 4];      // R[C-1][t] Delta_t, [column][token]
-    __shared__ __align__(16) float SlT[2][kNB][kDK + 4];  // the 128 x 16 state block, [column][key], by chunk parity
+    __shared__ __align__(16) u4_t DsH[2][2][64];          // R[C-1] Delta as fp16 pairs: [32-token block][hi, lo][lane]
+    __shared__ __align__(16) _Float16 KT[2][kC][kKtLd];   // the chunk's K as fp16 pairs: [hi, lo][token][key]
+    __shared__ __align__(16) float GT[2][256];            // by chunk parity: gamma [64], R[C-1] [64], gamma_{C-1}, eK, eQ, rho
     // Workgroup i runs on XCD i % 8 (round-robin dispatch). With the value
     // heads a multiple of 8, head h's column blocks all get ids i with
     // i % 8 == h % 8, so the chunk data of a head (K, Q, T', Bm, V) is fetched
@@ -373,65 +533,61 @@ __global__ __launch_bounds__(kWalkThreads) __attribute__((amdgpu_waves_per_eu(2,
     const int g = lane >> 4, n = lane & 15;
     float* Sg = S + static_cast<size_t>(h) * kDK * value_dim + j0;
 
-    for (int e = threadIdx.x; e < kDK * kNB; e += kWalkThreads)
-        SlT[0][e % kNB][e / kNB] = Sg[static_cast<size_t>(e / kNB) * value_dim + e % kNB];
-    __syncthreads();
-
     const int nchunks = (rows + kC - 1) / kC;
-    const int tok = 16 * wv + n;     // token row of this lane's A operands
     const int tres = 16 * wv + 4 * g;   // first of the 4 token rows of this lane's results
     const uint32_t stride4 = static_cast<uint32_t>(qkv_stride) * 4u;
     const uint32_t ostride4 = static_cast<uint32_t>(out_stride) * 4u;
-    // Loop-invariant lane byte offsets. k-slot map of every product: step
-    // 4j + c of a 4-wide lane group g takes element 16j + 4g + c of the
-    // contracted dimension, so the 4 lanes of a row read 64 contiguous bytes.
-    const uint32_t ro = static_cast<uint32_t>(tok) * stride4 + 16u * g;
+    // Loop-invariant lane byte offsets into the chunk's fp16 block: K or Q by
+    // token, this wave's 8 fragments of 1 KB.
+    const uint32_t ao = (qw ? kQRows : kKRows) + static_cast<uint32_t>(wv * 8 * 64 + lane) * 16u;
     uint32_t vo[4], oo[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         vo[r] = static_cast<uint32_t>(tres + r) * stride4 + 4u * n;
         oo[r] = static_cast<uint32_t>(tres + r) * ostride4 + 4u * n;
     }
-    // T' (K waves) or Bm (Q waves) rows 16wv + n at this lane's k-slot columns
-    const uint32_t mo = static_cast<uint32_t>((qw ? kC * kC : 0) + (16 * wv + n) * kC + 4 * g) * 4u;
-    const uint32_t go = static_cast<uint32_t>(2 * kC * kC + tres) * 4u;
-    const uint32_t rto = static_cast<uint32_t>(2 * kC * kC + kC + tres) * 4u;
-    // gamma_{C-1}: one address for the wave, through a vector load (a scalar
-    // load shares lgkmcnt with the LDS traffic). lane & (rows >> 31) is 0
-    // (rows > 0) but not known to the compiler to be uniform.
-    const uint32_t glo = static_cast<uint32_t>(2 * kC * kC + kC - 1 + (lane & (rows >> 31))) * 4u;
-    const float* const rsrc = (qw ? q : k) + src * kDK;
+    // T' (K waves) or Bm (Q waves): this wave's row tile, one 1 KB piece per column block
+    const uint32_t mo = static_cast<uint32_t>((qw ? kC * kC : 0) + (frag_index(wv, 0) + lane) * 4) * 4u;
+    // the gates block, 16 bytes per lane (lanes past its 132 floats read zeros)
+    const uint32_t go = static_cast<uint32_t>(2 * kC * kC + 4 * lane) * 4u;
     const float* const vsrc = v + static_cast<size_t>(h) * value_dim + j0;
     float* const osrc = out + static_cast<size_t>(h) * value_dim + j0;
-    // chunk c's token rows (fewer in a partial last chunk) and workspace block
+    // chunk c's token rows (fewer in a partial last chunk), workspace block and fp16 block
     auto rows_rsrc = [&](const float* base, int c, int64_t stride, uint32_t s4) {
         return buf_rsrc(base + static_cast<int64_t>(c) * kC * stride, static_cast<uint32_t>(min(rows - c * kC, kC)) * s4);
     };
     auto ws_rsrc = [&](int c) {
         return buf_rsrc(ws + (static_cast<size_t>(c) * value_heads + h) * kWsFloats, static_cast<uint32_t>(kWsFloats * 4));
     };
+    auto kq_rsrc = [&](int c) {
+        return buf_rsrc(kq + (static_cast<size_t>(c) * value_heads + src) * kKqBytes, static_cast<uint32_t>(kKqBytes));
+    };
     float vv[4];
     float4 tm[4], bm[4];   // T' rows (K waves), Bm rows (Q waves); each role loads and reads only its own
+    float4 gq;             // Q waves: the next chunk's gates, 16 bytes per lane
+    float s0[8];           // K waves: the state at rows 32wv + 16mt + 4g + r (s0[4 mt + r]), column n
     ChunkIn inA, inB;
 #pragma unroll
     for (int r = 0; r < 4; ++r) inA.o[r] = inB.o[r] = 0.0f;
-    auto load_in = [&](int c, ChunkIn& d, int j) {   // row piece j < 8, or (j == 8) the gates
-        if (j < 8) {
-            const float4 a = buf_ld4(rows_rsrc(rsrc, c, qkv_stride, stride4), ro + 64u * j);
-            d.rows[4 * j] = a.x;
-            d.rows[4 * j + 1] = a.y;
-            d.rows[4 * j + 2] = a.z;
-            d.rows[4 * j + 3] = a.w;
-        } else {
-            const __amdgpu_buffer_rsrc_t w = ws_rsrc(c);
-            const float4 gv = buf_ld4(w, go);
-            d.gm[0] = gv.x;
-            d.gm[1] = gv.y;
-            d.gm[2] = gv.z;
-            d.gm[3] = gv.w;
-            d.glast = buf_ld1(w, glo);
-            d.rt4 = buf_ld4(w, rto);
-        }
+    auto load_in = [&](int c, ChunkIn& d, int j) {   // operand piece j < 8
+        d.a[j] = buf_ld4u(kq_rsrc(c), ao + 1024u * j);
+    };
+    // Q wave wv publishes lanes 16wv .. 16wv + 15 of the gates it loaded
+    auto put_gates = [&](int c) {
+        if (g == wv) *reinterpret_cast<float4*>(&GT[c & 1][4 * lane]) = gq;
+    };
+    // The K wave's state as fp16 pairs for the next products, scaled per
+    // (slab, column) by its largest |value| over the slab's 32 rows.
+    auto put_state = [&]() {
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(s0[i]));
+        const int e = scale_exp(max_groups(m));
+        u4_t hi, lo;
+        split8(s0, e, hi, lo);
+        SH[wv][0][lane] = hi;
+        SH[wv][1][lane] = lo;
+        SE[n][wv] = e;   // the 4 lanes of a column write the same value
     };
     auto load_v = [&](int c) {
         const __amdgpu_buffer_rsrc_t r = rows_rsrc(vsrc, c, qkv_stride, stride4);
@@ -444,7 +600,7 @@ __global__ __launch_bounds__(kWalkThreads) __attribute__((amdgpu_waves_per_eu(2,
     auto load_m = [&](int c, float4 (&m)[4]) {
         const __amdgpu_buffer_rsrc_t w = ws_rsrc(c);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) m[s] = buf_ld4(w, mo + 64u * min(s, wv));
+        for (int s = 0; s < 4; ++s) m[s] = buf_ld4(w, mo + 1024u * min(s, wv));
     };
     // elements 16s + 4g .. 16s + 4g + 3 (s < 4) of a 64-long LDS row (p = row + 4g)
     auto lds16 = [](float (&dst)[16], const float* p) {
@@ -457,66 +613,97 @@ __global__ __launch_bounds__(kWalkThreads) __attribute__((amdgpu_waves_per_eu(2,
             dst[4 * s + 3] = t.w;
         }
     };
+    if (!qw) {
 #pragma unroll
-    for (int j = 0; j <= 8; ++j) load_in(0, inA, j);
-    load_v(0);
-    if (qw) load_m(0, bm);
-    else load_m(0, tm);
+        for (int i = 0; i < 8; ++i) s0[i] = Sg[static_cast<size_t>(32 * wv + 16 * (i >> 2) + 4 * g + (i & 3)) * value_dim + n];
+        put_state();
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) load_in(0, inA, j);
+    if (qw) {
+        gq = buf_ld4(ws_rsrc(0), go);
+        load_m(0, bm);
+    } else {
+        load_v(0);
+        load_m(0, tm);
+    }
     // The loop's wait counts are then computed from its own loads only.
     __builtin_amdgcn_s_waitcnt(0);
+    if (qw) put_gates(0);
+    __syncthreads();   // the state's fp16 pairs, chunk 0's gates
 
     // Chunk c with its inputs in cur; chunk c + 1's are loaded into nxt (the
     // last chunk reloads its own: unconditional loads keep the wait counts exact).
-    auto chunk_step = [&](int c, ChunkIn& cur, ChunkIn& nxt, const float (*Sl)[kDK + 4], float (*Sw)[kDK + 4])
-                          __attribute__((always_inline)) {
+    auto chunk_step = [&](int c, ChunkIn& cur, ChunkIn& nxt) __attribute__((always_inline)) {
         const int cn = min(c + 1, nchunks - 1);
-        // S0 as the B operand (rows 16j + 4g + c, column n)
-        float sB[32];
-        float4 sC[2];
+        // this chunk's gates: gamma and R[C-1] at the lane's 4 result tokens, the scalars
+        const float* const gt = GT[c & 1];
+        const float4 gm = *reinterpret_cast<const float4*>(gt + tres);
+        const float4 rt4 = *reinterpret_cast<const float4*>(gt + kC + tres);
+        const float4 ex = *reinterpret_cast<const float4*>(gt + 2 * kC);   // gamma_{C-1}, eK, eQ (int bits), rho
+        // S0 as fp16 pairs (the B operand of k-block kb) and its (column, slab) scales
+        u4_t bh[4], bl[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float4 t = *reinterpret_cast<const float4*>(&Sl[n][16 * j + 4 * g]);
-            sB[4 * j] = t.x;
-            sB[4 * j + 1] = t.y;
-            sB[4 * j + 2] = t.z;
-            sB[4 * j + 3] = t.w;
+        for (int kb = 0; kb < 4; ++kb) {
+            bh[kb] = SH[kb][0][lane];
+            bl[kb] = SH[kb][1][lane];
         }
-        if (!qw) {
-            // S0 at this wave's state-update rows (32wv + 16mt + 4g + r), and the K rows to LDS
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) sC[mt] = *reinterpret_cast<const float4*>(&Sl[n][32 * wv + 16 * mt + 4 * g]);
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-                for (int cc = 0; cc < 4; ++cc) KsT[16 * j + 4 * g + cc][tok] = cur.rows[4 * j + cc];
-        }
-        // X = K S0 (K waves) or Y = Q S0 (Q waves); the next chunk's row loads go
-        // out one per 4 MFMAs (issued in one burst they held the wave)
+        const int4 se = *reinterpret_cast<const int4*>(&SE[n][0]);
+        // X = K S0 (K waves) or Y = Q S0 (Q waves): per slab hi lo' + lo hi' + hi hi',
+        // four independent chains; the next chunk's operand loads go out between
+        // the products (issued in one burst they held the wave)
         v4f_t xa[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) xa[u] = v4f_t{0.f, 0.f, 0.f, 0.f};
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < 32; ++s) {
-            if ((s & 3) == 0) load_in(cn, nxt, s >> 2);
-            xa[s & 3] = mfma4(cur.rows[s], sB[s], xa[s & 3]);
+        for (int s = 0; s < 12; ++s) {
+            const int kb = s & 3, p = s >> 2;
+            if (s < 8) load_in(cn, nxt, s);
+            xa[kb] = mfma16(p == 1 ? cur.a[2 * kb + 1] : cur.a[2 * kb], p == 0 ? bl[kb] : bh[kb], xa[kb]);
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // 1 VMEM read
-            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   // 4 MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
         }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
         __builtin_amdgcn_sched_barrier(0);
-        const v4f_t X = (xa[0] + xa[1]) + (xa[2] + xa[3]);
-        load_in(cn, nxt, 8);
-        if (!qw) {
+        // Loads stay where they are issued: without this compiler fence the
+        // loads of the loop's first chunk step were sunk below its products to
+        // the barrier, and V then counted as the newest load (a full wait).
+        asm volatile("" ::: "memory");
+        const int ea = __float_as_int(qw ? ex.z : ex.y);   // eQ or eK
+        const int s0e = -(ea + se.x), s1e = -(ea + se.y), s2e = -(ea + se.z), s3e = -(ea + se.w);
+        v4f_t X;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            X[r] = (__builtin_amdgcn_ldexpf(xa[0][r], s0e) + __builtin_amdgcn_ldexpf(xa[1][r], s1e)) +
+                   (__builtin_amdgcn_ldexpf(xa[2][r], s2e) + __builtin_amdgcn_ldexpf(xa[3][r], s3e));
+        if (qw) {
+            gq = buf_ld4(ws_rsrc(cn), go);
+        } else {
             // result rows: tokens 16wv + 4g + r, column n
-            *reinterpret_cast<float4*>(&RvT[n][tres]) =
-                make_float4(__builtin_fmaf(-cur.gm[0], X[0], vv[0]), __builtin_fmaf(-cur.gm[1], X[1], vv[1]),
-                            __builtin_fmaf(-cur.gm[2], X[2], vv[2]), __builtin_fmaf(-cur.gm[3], X[3], vv[3]));
+            float rv[4];
+            rv[0] = __builtin_fmaf(-gm.x, X[0], vv[0]);
+            rv[1] = __builtin_fmaf(-gm.y, X[1], vv[1]);
+            rv[2] = __builtin_fmaf(-gm.z, X[2], vv[2]);
+            rv[3] = __builtin_fmaf(-gm.w, X[3], vv[3]);
+            *reinterpret_cast<float4*>(&RvT[n][tres]) = make_float4(rv[0], rv[1], rv[2], rv[3]);
+            RvM[n][wv] = max_groups(fmaxf(fmaxf(fabsf(rv[0]), fabsf(rv[1])), fmaxf(fabsf(rv[2]), fabsf(rv[3]))));
             load_v(cn);
+            // this wave's 16 tokens of K to LDS by token (slot 4h + c of (kb, g) is
+            // key 32kb + 16h + 4g + c), for the state update's transposed reads
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int kb = j >> 1, pl = j & 1;
+                _Float16* const row = &KT[pl][16 * wv + n][32 * kb + 4 * g];
+                *reinterpret_cast<uint2*>(row) = make_uint2(cur.a[j][0], cur.a[j][1]);
+                *reinterpret_cast<uint2*>(row + 16) = make_uint2(cur.a[j][2], cur.a[j][3]);
+            }
         }
         __syncthreads();
+        int eS = 0;   // K waves: eK + eD, the state update's scale exponent
         if (!qw) {
             // Delta = T' Rv (this wave's 16 rows; K = the chunk's tokens up to the diagonal block)
             float rb[16];
@@ -534,9 +721,18 @@ __global__ __launch_bounds__(kWalkThreads) __attribute__((amdgpu_waves_per_eu(2,
             load_m(cn, tm);
             const v4f_t D = D0 + D1;
             *reinterpret_cast<float4*>(&DlT[n][tres]) = make_float4(D[0], D[1], D[2], D[3]);
-            // R[C-1][t] Delta_t: the state update's operand
-            *reinterpret_cast<float4*>(&DsT[n][tres]) =
-                make_float4(D[0] * cur.rt4.x, D[1] * cur.rt4.y, D[2] * cur.rt4.z, D[3] * cur.rt4.w);
+            // R[C-1][t] Delta_t, the state update's operand, as fp16 pairs. Its
+            // column scale comes from rho max_i |Rv[i][n]| >= max_t |R[C-1][t] Delta[t][n]|,
+            // which every K wave computes alike from the four tiles' maxima.
+            const float4 rm = *reinterpret_cast<const float4*>(&RvM[n][0]);
+            const int eD = scale_exp(ex.w * fmaxf(fmaxf(rm.x, rm.y), fmaxf(rm.z, rm.w)));
+            eS = __float_as_int(ex.y) + eD;
+            unsigned h01, l01, h23, l23;
+            split2(D[0] * rt4.x, D[1] * rt4.y, eD, h01, l01);
+            split2(D[2] * rt4.z, D[3] * rt4.w, eD, h23, l23);
+            // tokens 16wv + 4g + r: k-block wv / 2, slots 4 (wv & 1) + r
+            reinterpret_cast<uint2*>(&DsH[wv >> 1][0][lane])[wv & 1] = make_uint2(h01, h23);
+            reinterpret_cast<uint2*>(&DsH[wv >> 1][1][lane])[wv & 1] = make_uint2(l01, l23);
         }
         __syncthreads();
         if (qw) {
@@ -554,9 +750,12 @@ __global__ __launch_bounds__(kWalkThreads) __attribute__((amdgpu_waves_per_eu(2,
                 }
             }
             load_m(cn, bm);
+            put_gates(cn);   // every wave read this chunk's gates before the last two barriers
             const v4f_t O = O0 + O1;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) cur.o[r] = __builtin_fmaf(cur.gm[r], X[r], O[r]);
+            cur.o[0] = __builtin_fmaf(gm.x, X[0], O[0]);
+            cur.o[1] = __builtin_fmaf(gm.y, X[1], O[1]);
+            cur.o[2] = __builtin_fmaf(gm.z, X[2], O[2]);
+            cur.o[3] = __builtin_fmaf(gm.w, X[3], O[3]);
             // The previous chunk's outputs (none before chunk 0: a zero-range
             // descriptor drops them). Stored a chunk late, their registers stay
             // live: the store's data would otherwise be overwritten right after
@@ -566,45 +765,66 @@ __global__ __launch_bounds__(kWalkThreads) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
             for (int r = 0; r < 4; ++r) buf_st1(nxt.o[r], orr, oo[r]);
         } else {
-            // state rows 32wv + 16mt + (0..15): gamma_{C-1} S0 + sum_t k_t (R[C-1][t] Delta_t)
-            // (step 4s + c: token 16s + 4g + c)
-            float db[16];
-            lds16(db, &DsT[n][4 * g]);
-            v4f_t A0 = {0.f, 0.f, 0.f, 0.f}, A1 = A0;
-            const int m0 = 32 * wv + n;
-            float ka[16], kb[16];
-            lds16(ka, &KsT[m0][4 * g]);
-            lds16(kb, &KsT[m0 + 16][4 * g]);
+            // state rows 32wv + 16mt + 4g + r: gamma_{C-1} S0 + sum_t k_t (R[C-1][t] Delta_t),
+            // per (mt, 32-token block) hi lo' + lo hi' + hi hi' (four chains)
+            u4_t dh[2], dl[2];
 #pragma unroll
-            for (int s = 0; s < 16; ++s) {
-                A0 = mfma4(ka[s], db[s], A0);
-                A1 = mfma4(kb[s], db[s], A1);
+            for (int kb = 0; kb < 2; ++kb) {
+                dh[kb] = DsH[kb][0][lane];
+                dl[kb] = DsH[kb][1][lane];
             }
-            // the new state goes to the other buffer: no barrier between the
-            // readers of this chunk's S0 and these writes
-            *reinterpret_cast<float4*>(&Sw[n][32 * wv + 4 * g]) =
-                make_float4(__builtin_fmaf(cur.glast, sC[0].x, A0[0]), __builtin_fmaf(cur.glast, sC[0].y, A0[1]),
-                            __builtin_fmaf(cur.glast, sC[0].z, A0[2]), __builtin_fmaf(cur.glast, sC[0].w, A0[3]));
-            *reinterpret_cast<float4*>(&Sw[n][32 * wv + 16 + 4 * g]) =
-                make_float4(__builtin_fmaf(cur.glast, sC[1].x, A1[0]), __builtin_fmaf(cur.glast, sC[1].y, A1[1]),
-                            __builtin_fmaf(cur.glast, sC[1].z, A1[2]), __builtin_fmaf(cur.glast, sC[1].w, A1[3]));
+            // K by key, kt[4 mt + 2 kb + plane]: rows 32wv + 16mt + n, slots 4h + r =
+            // tokens 32kb + 16h + 4g + r. Lane j = n of group g points at keys
+            // 32wv + 16mt + 4 (j & 3) .. + 3 of token 32kb + 16h + 4g + (j >> 2).
+            u4_t kt[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int mt = j >> 2, kb = (j >> 1) & 1, pl = j & 1;
+                const _Float16* const p = &KT[pl][32 * kb + 4 * g + (n >> 2)][32 * wv + 16 * mt + 4 * (n & 3)];
+                typedef short s4_t __attribute__((ext_vector_type(4)));
+                typedef __attribute__((address_space(3))) s4_t* lds_s4_t;
+                const s4_t t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t)(p));
+                const s4_t t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t)(p + 16 * kKtLd));
+                const uint2 a0 = __builtin_bit_cast(uint2, t0), a1 = __builtin_bit_cast(uint2, t1);
+                kt[j] = u4_t{a0.x, a0.y, a1.x, a1.y};
+            }
+            v4f_t sa[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) sa[u] = v4f_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {   // u = 2 mt + kb
+                    const int kb = u & 1;
+                    sa[u] = mfma16(p == 1 ? kt[2 * u + 1] : kt[2 * u], p == 0 ? dl[kb] : dh[kb], sa[u]);
+                }
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    s0[4 * mt + r] = __builtin_fmaf(ex.x, s0[4 * mt + r],
+                                                    __builtin_amdgcn_ldexpf(sa[2 * mt][r] + sa[2 * mt + 1][r], -eS));
+            // every wave read this chunk's pairs before the last two barriers
+            put_state();
         }
-        __syncthreads();   // the new state is visible; KsT, RvT, DlT, DsT are free
+        __syncthreads();   // the new state's pairs are visible; RvT, RvM, DlT, DsH are free
     };
     int c = 0;
     for (; c + 1 < nchunks; c += 2) {
-        chunk_step(c, inA, inB, SlT[0], SlT[1]);
-        chunk_step(c + 1, inB, inA, SlT[1], SlT[0]);
+        chunk_step(c, inA, inB);
+        chunk_step(c + 1, inB, inA);
     }
-    if (c < nchunks) chunk_step(c, inA, inB, SlT[0], SlT[1]);
+    if (c < nchunks) chunk_step(c, inA, inB);
     if (qw) {   // the last chunk's outputs
         const __amdgpu_buffer_rsrc_t orr = rows_rsrc(osrc, nchunks - 1, out_stride, ostride4);
         const ChunkIn& last = (nchunks & 1) ? inA : inB;
 #pragma unroll
         for (int r = 0; r < 4; ++r) buf_st1(last.o[r], orr, oo[r]);
     }
-    for (int e = threadIdx.x; e < kDK * kNB; e += kWalkThreads)
-        Sg[static_cast<size_t>(e / kNB) * value_dim + e % kNB] = SlT[nchunks & 1][e % kNB][e / kNB];
+    if (!qw) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) Sg[static_cast<size_t>(32 * wv + 16 * (i >> 2) + 4 * g + (i & 3)) * value_dim + n] = s0[i];
+    }
 }
 
 }  // namespace
@@ -616,7 +836,9 @@ extern "C" {
 
 size_t qwen_gdn_recurrent_chunked_workspace_bytes(int rows, int value_heads) {
     if (rows <= 0 || value_heads <= 0) return 0;
-    return static_cast<size_t>((rows + kC - 1) / kC) * value_heads * kWsFloats * sizeof(float);
+    // per (chunk, value head) the matrices and gates, then per (chunk, key head
+    // read by some value head: fewer than value_heads) the fp16 pairs of K and Q
+    return static_cast<size_t>((rows + kC - 1) / kC) * value_heads * (kWsFloats * sizeof(float) + kKqBytes);
 }
 
 int qwen_gdn_recurrent_chunked(float* state, const float* q, const float* k, const float* v, const float* beta,
@@ -642,8 +864,9 @@ int qwen_gdn_recurrent_chunked(float* state, const float* q, const float* k, con
     const hipStream_t s = as_stream(stream);
     const int nchunks = (rows + kC - 1) / kC;
     float* ws = static_cast<float*>(workspace);
-    gdn_chunk_prep<<<dim3(nchunks, std::min(key_heads, value_heads)), kThreads, 0, s>>>(q, k, beta, decay, ws, rows, key_heads, value_heads,
-                                                                   qkv_stride);
+    unsigned char* kq = static_cast<unsigned char*>(workspace) + static_cast<size_t>(nchunks) * value_heads * kWsFloats * sizeof(float);
+    gdn_chunk_prep<<<dim3(nchunks, std::min(key_heads, value_heads)), kThreads, 0, s>>>(
+        q, k, beta, decay, ws, kq, rows, key_heads, value_heads, qkv_stride);
     // One row: its stride is not used to step between rows, but the walk's
     // buffer range is one stride long, so it must cover the row's q, k, v and out.
     const int64_t row_extent = std::max<int64_t>(static_cast<int64_t>(key_heads) * key_dim,
@@ -651,7 +874,7 @@ int qwen_gdn_recurrent_chunked(float* state, const float* q, const float* k, con
     const int64_t qs = rows == 1 ? std::max(qkv_stride, row_extent) : qkv_stride;
     const int64_t os = rows == 1 ? std::max(out_stride, row_extent) : out_stride;
     QK_REQUIRE(qs <= kMaxWalkStride && os <= kMaxWalkStride, "gdn_recurrent_chunked: row too long for the chunked walk");
-    gdn_chunk_state<<<(value_dim / kNB) * value_heads, kWalkThreads, 0, s>>>(state, q, k, v, ws, out, rows, key_heads,
+    gdn_chunk_state<<<(value_dim / kNB) * value_heads, kWalkThreads, 0, s>>>(state, v, ws, kq, out, rows, key_heads,
                                                                              value_heads, value_dim, qs, os);
     return check_launch("gdn_recurrent_chunked");
 }

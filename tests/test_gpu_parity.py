@@ -550,19 +550,28 @@ def _check_gdn_recurrence(oracle, qkv, beta, decay, state, out, new_state, kh, v
 
 
 @pytest.mark.parametrize("rows,gates", [(1, "normal"), (63, "normal"), (64, "normal"), (200, "normal"),
-                                        (700, "normal"), (150, "fast_decay"), (150, "beta_one")])
+                                        (700, "normal"), (150, "fast_decay"), (150, "beta_one"),
+                                        (128, "tiny_late_beta")])
 def test_gdn_recurrent_chunked(oracle, rows, gates):
     """The chunked prefill form against the oracle's token loop at the Qwen3.5 GDN shape:
     partial last chunks, several chunks, decays that underflow to zero inside a chunk
-    (the ratios are running products), and beta near 1 (the triangular solve's
-    largest off-diagonal terms)."""
+    (the ratios are running products), beta near 1 (the triangular solve's
+    largest off-diagonal terms), and fast decay with beta ~1e-17 on the second half of
+    each chunk, ending in that half: the final state (~1e-23 for some heads) is then
+    R[C-1] Delta of the last tokens alone, whose fp16 scale must come from a bound
+    that pairs each token's factors (pairing the largest of each overstated it by
+    ~1e17) and be undone exactly at any magnitude (a float multiplier clamped to stay
+    normal lost those heads; both flushed the state to zeros in a CPU emulation)."""
     kh, vh, dk, dv = 16, 32, 128, 128
     r = rng(rows * 3 + len(gates))
     qkv, b, alpha, a, dt, state = _gdn_inputs(r, rows, kh, vh, dk, dv)
-    if gates == "fast_decay":
+    if gates in ("fast_decay", "tiny_late_beta"):
         alpha = (alpha + 60.0).astype(F32)      # softplus ~ 60: decay exp(a * 60) underflows for a < -1.6
-    elif gates == "beta_one":
+    if gates == "beta_one":
         b = (b + 12.0).astype(F32)
+    elif gates == "tiny_late_beta":
+        late = (np.arange(rows) % 64) >= 32
+        b = np.where(late[:, None], b - 40.0, b).astype(F32)
     beta, decay = oracle.gdn_gate_values_rows(b, alpha, a, dt)
     if gates == "fast_decay":
         assert (decay == 0).any() and (decay > 0).any()
