@@ -18,12 +18,12 @@
 // The decay ratios are running products, never quotients, so decays that
 // underflow give exact zeros rather than 0/0.
 //
-// Kernel A (one workgroup per (chunk, key head), all chunks in parallel):
-// K K^T and Q K^T on fp32 MFMA (v_mfma_f32_16x16x4f32) once, then for each value
-// head that reads this key head the ratios and T as a blocked inverse (16 x 16
-// diagonal blocks by forward substitution, the others as MFMA products)
-// -> T', Bm, gamma, R[C-1][.] to the caller's workspace; and the chunk's K and Q
-// as fp16 pairs (below).
+// Kernel A (one workgroup per (chunk, key head), all chunks in parallel): the
+// chunk's K and Q as fp16 pairs (below), K K^T and Q K^T from them once, then
+// for each value head that reads this key head the ratios and T as a blocked
+// inverse (16 x 16 diagonal blocks by forward substitution, the others as fp32
+// MFMA products) -> T', Bm, gamma, R[C-1][.] and the K / Q pairs to the
+// caller's workspace.
 // Kernel B (one 8-wave workgroup per (value head, 16 state columns), chunks in
 // order, the workgroups of one head on one XCD): per SIMD a Q wave computing
 // Y = Q S0 and O = gamma Y + Bm Delta for 16 tokens, and a K wave computing
@@ -32,8 +32,8 @@
 // 128 x 16 state block in registers between chunks (read from / written to the
 // state once per call) and publish it to the other waves through LDS.
 //
-// fp16 pairs. The three products with a long sum (X and Y over the 128 key dims,
-// the state update over the chunk's 64 tokens) run on v_mfma_f32_16x16x32_f16:
+// fp16 pairs. The products with a long sum (K K^T, Q K^T, X and Y over the 128
+// key dims, the state update over the chunk's 64 tokens) run on v_mfma_f32_16x16x32_f16:
 // it sums 32 terms per lane group where v_mfma_f32_16x16x4f32 sums 4, in ~22
 // cycles against ~35 (measured on gfx950), and a SIMD's MFMA time is not hidden
 // behind its other work. An fp32 operand x is scaled by 2^e (e chosen per block
@@ -159,10 +159,9 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
                                                            const float* __restrict__ decay, float* __restrict__ ws,
                                                            unsigned char* __restrict__ kq, int rows, int key_heads,
                                                            int value_heads, int64_t qkv_stride) {
-    // The chunk's K rows while the products run; after them the same storage
-    // holds A (strictly lower) and T of the value head in hand.
+    // The chunk's K as fp16 pairs while the products run; after them the same
+    // storage holds A (strictly lower) and T of the value head in hand.
     __shared__ __align__(16) float kat[2 * kC * kLdA];
-    static_assert(kC * (kDK + 4) <= 2 * kC * kLdA, "K rows fit the A and T storage");
     __shared__ __align__(16) float G[kC][kLdA];    // K K^T
     __shared__ __align__(16) float Pm[kC][kLdA];   // Q K^T
     __shared__ __align__(16) float sb[kC], sd[kC];
@@ -170,7 +169,6 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
     __shared__ float stmax[4];                     // per wave: largest |R[C-1][t]| sum_i |T'[t][i]|
     __shared__ float sR[kC];                       // |R[C-1][t]|
     __shared__ float sglast;                       // gamma_{C-1}
-    float(*Kl)[kDK + 4] = reinterpret_cast<float(*)[kDK + 4]>(kat);
     float(*Ab)[kLdA] = reinterpret_cast<float(*)[kLdA]>(kat);
     float(*T)[kLdA] = reinterpret_cast<float(*)[kLdA]>(kat + kC * kLdA);
     const int c = blockIdx.x, src = blockIdx.y;   // chunk, key head
@@ -197,8 +195,11 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
 
     // Lower-triangle 16x16 tiles (mt >= nt) of K K^T and Q K^T. Wave w loads
     // the K and Q rows of tokens 16w .. 16w+15 once (lane: token 16w + L%16,
-    // dims 32(L/16) .. +31, the MFMA k-slot map of both operands) and puts its
-    // K rows in LDS; Q K^T tiles (w, nt <= w) stay with wave w (its Q rows in
+    // dims 32(L/16) .. +31), splits them into fp16 pairs (one scale exponent per
+    // chunk tile, from the tile's largest |K| or |Q|) and puts its K pairs in
+    // LDS; the products run on v_mfma_f32_16x16x32_f16, hi lo' + lo hi' + hi hi'
+    // per k-block of 32 dims (a quarter of the fp32 MFMA time: they were a third
+    // of the kernel's). Q K^T tiles (w, nt <= w) stay with wave w (its Q pairs in
     // VGPRs), the K K^T tiles are dealt so that every wave has five tiles.
     {
         const int tok = t0 + 16 * wv + n;
@@ -206,10 +207,6 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
         float kr[32], qr[32];
         load32(k + row, g, tok < rows, kr);
         load32(q + row, g, tok < rows, qr);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            *reinterpret_cast<float4*>(&Kl[16 * wv + n][16 * j + 4 * g]) =
-                make_float4(kr[4 * j], kr[4 * j + 1], kr[4 * j + 2], kr[4 * j + 3]);
         float mk = 0.0f, mq = 0.0f;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
@@ -225,12 +222,15 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
         __syncthreads();
         eK = scale_exp(fmaxf(fmaxf(smax[0][0], smax[0][1]), fmaxf(smax[0][2], smax[0][3])));
         eQ = scale_exp(fmaxf(fmaxf(smax[1][0], smax[1][1]), fmaxf(smax[1][2], smax[1][3])));
-        // K and Q by token (the walk's X and Y operands) in the order the walk's
-        // lanes read them: 1 KB fragments [tile wv][2 kb + (hi, lo)][lane] x 8 fp16,
-        // lane (n, g) = token 16wv + n, slot 4h + c of k-block kb = dim
-        // 32kb + 16h + 4g + c, which is this lane's kr[8kb + 4h + c]. One wave
+        // K and Q by token (the walk's X and Y operands, and this kernel's) in the
+        // order the walk's lanes read them: 1 KB fragments [tile wv][2 kb + (hi, lo)]
+        // [lane] x 8 fp16, lane (n, g) = token 16wv + n, slot 4h + c of k-block kb =
+        // dim 32kb + 16h + 4g + c, which is this lane's kr[8kb + 4h + c]. One wave
         // instruction then reads 1 KB in one piece (16 rows of 64 bytes cost the
         // CU about twice as long, measured). Padding tokens are zeros.
+        u4_t* const KF = reinterpret_cast<u4_t*>(kat);   // [tile][2 kb + (hi, lo)][lane]
+        static_assert(4 * 8 * 64 * sizeof(u4_t) <= sizeof(kat), "K pairs fit the A and T storage");
+        u4_t qf[8];
         {
             unsigned char* const rk = kqb + kKRows + (wv * 8 * 64 + lane) * 16;
             unsigned char* const rq = kqb + kQRows + (wv * 8 * 64 + lane) * 16;
@@ -240,41 +240,40 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
                 split8(kr + 8 * kb, eK, hi, lo);
                 *reinterpret_cast<u4_t*>(rk + 2048 * kb) = hi;
                 *reinterpret_cast<u4_t*>(rk + 2048 * kb + 1024) = lo;
-                split8(qr + 8 * kb, eQ, hi, lo);
-                *reinterpret_cast<u4_t*>(rq + 2048 * kb) = hi;
-                *reinterpret_cast<u4_t*>(rq + 2048 * kb + 1024) = lo;
+                KF[(wv * 8 + 2 * kb) * 64 + lane] = hi;
+                KF[(wv * 8 + 2 * kb + 1) * 64 + lane] = lo;
+                split8(qr + 8 * kb, eQ, qf[2 * kb], qf[2 * kb + 1]);
+                *reinterpret_cast<u4_t*>(rq + 2048 * kb) = qf[2 * kb];
+                *reinterpret_cast<u4_t*>(rq + 2048 * kb + 1024) = qf[2 * kb + 1];
             }
         }
-        auto tile = [&](const float (&a)[32], int mt, int nt, float (*D)[kLdA]) {
+        __syncthreads();   // every tile's K pairs in LDS
+        // The B operand of a tile with column tile nt is K's fragments of that tile
+        // (B[k][n] = K[16nt + n][k]: the same lane map as the A fragments).
+        auto tile = [&](const u4_t (&a)[8], int mt, int nt, int e, float (*D)[kLdA]) {
             v4f_t acc[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float4 b = *reinterpret_cast<const float4*>(&Kl[16 * nt + n][16 * j + 4 * g]);
-                acc[0] = mfma4(a[4 * j], b.x, acc[0]);
-                acc[1] = mfma4(a[4 * j + 1], b.y, acc[1]);
-                acc[2] = mfma4(a[4 * j + 2], b.z, acc[2]);
-                acc[3] = mfma4(a[4 * j + 3], b.w, acc[3]);
+            for (int kb = 0; kb < 4; ++kb) {
+                const u4_t bh = KF[(nt * 8 + 2 * kb) * 64 + lane], bl = KF[(nt * 8 + 2 * kb + 1) * 64 + lane];
+                acc[kb] = mfma16(a[2 * kb], bl, acc[kb]);
+                acc[kb] = mfma16(a[2 * kb + 1], bh, acc[kb]);
+                acc[kb] = mfma16(a[2 * kb], bh, acc[kb]);
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                D[16 * mt + 4 * g + r][16 * nt + n] = (acc[0][r] + acc[1][r]) + (acc[2][r] + acc[3][r]);
+                D[16 * mt + 4 * g + r][16 * nt + n] =
+                    __builtin_amdgcn_ldexpf((acc[0][r] + acc[1][r]) + (acc[2][r] + acc[3][r]), -e);
         };
-        for (int nt = 0; nt <= wv; ++nt) tile(qr, wv, nt, Pm);
-        // K K^T tiles (mt, nt), mt >= nt: wave w takes 4 - w of them, A rows from LDS.
+        for (int nt = 0; nt <= wv; ++nt) tile(qf, wv, nt, eQ + eK, Pm);
+        // K K^T tiles (mt, nt), mt >= nt: wave w takes 4 - w of them, A pairs from LDS.
         static constexpr int kTiles[10][2] = {{3, 0}, {3, 1}, {3, 2}, {3, 3}, {2, 0}, {2, 1}, {2, 2}, {1, 0}, {1, 1}, {0, 0}};
         const int first = wv == 0 ? 0 : wv == 1 ? 4 : wv == 2 ? 7 : 9;
         for (int i = first; i < first + 4 - wv; ++i) {
             const int mt = kTiles[i][0], nt = kTiles[i][1];
-            float a[32];
+            u4_t af[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float4 v = *reinterpret_cast<const float4*>(&Kl[16 * mt + n][16 * j + 4 * g]);
-                a[4 * j] = v.x;
-                a[4 * j + 1] = v.y;
-                a[4 * j + 2] = v.z;
-                a[4 * j + 3] = v.w;
-            }
-            tile(a, mt, nt, G);
+            for (int j = 0; j < 8; ++j) af[j] = KF[(mt * 8 + j) * 64 + lane];
+            tile(af, mt, nt, 2 * eK, G);
         }
     }
 
