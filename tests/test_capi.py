@@ -159,6 +159,20 @@ def test_matmul_rows_host_validation(lib):
     assert lib.qwen_matmul_rows_multi(NULL, 0, NULL, 32, 256, NULL, 0, ST) == OK
 
 
+def test_gdn_chunked_workspace_bytes(lib):
+    """Per 64-token chunk and value head: T' and Bm (64 x 64 fp32 each), gamma and
+    R[C-1][.] (64 fp32 each) and 4 scalars; then the chunk's K and Q of one key head
+    as fp16 pairs (64 tokens x 128 dims x hi/lo x 2 bytes each), sized per value
+    head (key heads read by some value head are at most the value heads)."""
+    per_head = (2 * 64 * 64 + 2 * 64 + 4) * 4 + 2 * 64 * 128 * 2 * 2
+    f = lib.qwen_gdn_recurrent_chunked_workspace_bytes
+    assert f(0, 32) == 0 and f(16, 0) == 0 and f(-1, 32) == 0
+    assert f(1, 32) == 32 * per_head
+    assert f(64, 2) == 2 * per_head and f(65, 2) == 2 * 2 * per_head
+    assert f(4096, 32) == 64 * 32 * per_head   # 202 MB at the Qwen3.5 GDN shape
+    assert f(4096, 32) % 16 == 0 and (2 * 64 * 64 + 2 * 64 + 4) * 4 % 16 == 0   # the pairs region stays 16-byte aligned
+
+
 def test_gdn_value_dim_limit_on_every_recurrent_path(lib):
     """value_dim above 256 is rejected with the reference's message
     (src/cuda/gdn.cu:167-169) by the token loop and by the chunked entry point
