@@ -303,10 +303,11 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
         // chain, with its 47 lane masks spilled from SGPRs into VGPR lanes, the
         // prep took 4.6% longer.)
         {
-            // The lane index is made opaque per value head so the row loop's lane
-            // masks (t > i, t >= i) are compared where they are used: hoisted out of
-            // the value-head loop they were kept in SGPRs spilled to VGPR lanes, a
-            // reload per use (2.6% of the prep).
+            // The lane index is made opaque per value head so the lane masks of the
+            // row loop (t > i, t >= i) and of gamma's unrolled chain (t <= i) are
+            // compared where they are used: hoisted out of the value-head loop they
+            // were kept in SGPRs spilled to VGPR lanes, a reload per use (4.4% of the
+            // prep, no SGPR spills left).
             int i = lane;
             asm volatile("" : "+v"(i));
             const int ta = 16 * wv;
@@ -344,10 +345,10 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_prep(const float* __restri
                 float gm = 1.0f;
                 for (int t4 = 0; t4 < kC; t4 += 4) {
                     const float4 d4 = *reinterpret_cast<const float4*>(&sd[t4]);
-                    gm *= t4 <= lane ? d4.x : 1.0f;
-                    gm *= t4 + 1 <= lane ? d4.y : 1.0f;
-                    gm *= t4 + 2 <= lane ? d4.z : 1.0f;
-                    gm *= t4 + 3 <= lane ? d4.w : 1.0f;
+                    gm *= t4 <= i ? d4.x : 1.0f;
+                    gm *= t4 + 1 <= i ? d4.y : 1.0f;
+                    gm *= t4 + 2 <= i ? d4.z : 1.0f;
+                    gm *= t4 + 3 <= i ? d4.w : 1.0f;
                 }
                 gam[lane] = gm;
                 if (lane == kC - 1) sglast = gm;
