@@ -13,7 +13,8 @@
       kernel's algorithmic bytes
   python -m qwen35_hip.rocprof_summary counters COUNTERS.csv [...] [--match SYM] [--stages N]
       mean per dispatch of every counter of the --pmc runs for the kernels whose
-      symbol contains SYM; per wave and K stage with SQ_WAVES; the MFMA-busy
+      symbol contains SYM; per wave and stage (N stages per wave: K / 32 of the
+      prefill GEMM, the chunks of the chunked GDN state walk) with SQ_WAVES; the MFMA-busy
       share (SQ_VALU_MFMA_BUSY_CYCLES over 1024 SIMDs x SQ_BUSY_CYCLES / 32 SEs)
 
 Kernel symbols are mapped to the bench.py kernel names; the reference copies are
@@ -236,6 +237,7 @@ def counters(paths: list[str], match: str, stages: int) -> dict:
         waves = m.get("SQ_WAVES")
         if waves:
             d["per_wave_stage"] = {c: m[c] / waves / stages for c in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS",
+                                                                      "SQ_INSTS_SALU", "SQ_INSTS_VMEM",
                                                                       "SQ_VALU_MFMA_BUSY_CYCLES") if c in m}
         if "SQ_VALU_MFMA_BUSY_CYCLES" in m and "SQ_BUSY_CYCLES" in m:
             cycles = m["SQ_BUSY_CYCLES"] / MI355X_SES
@@ -263,7 +265,8 @@ def main(argv=None) -> int:
     k = sub.add_parser("counters")
     k.add_argument("csv", nargs="+")
     k.add_argument("--match", default="gemm_")
-    k.add_argument("--stages", type=int, default=64, help="K stages per wave (K / 32)")
+    k.add_argument("--stages", type=int, default=64,
+                   help="stages per wave: K / 32 for the prefill GEMM, chunks for the chunked GDN state walk")
     args = ap.parse_args(argv)
     if args.cmd == "counters":
         for name, d in counters(args.csv, args.match, args.stages).items():
